@@ -1,0 +1,136 @@
+/* voyager_hip.h -- C ABI of the MI355X (gfx950) quantized-operator library.
+ *
+ * The library executes the reference's `quantized_ops` operator path
+ * (src/voyager_compiler/ops/quantized.py, ops/layout.py) on the GPU.  The
+ * Python package `voyager_amd` registers torch.library kernels under the same
+ * operator names and schemas and calls these entry points through ctypes.
+ *
+ * Conventions
+ *  - Every entry point returns 0 (VH_OK) or a nonzero status; the message of
+ *    the last failure on the calling thread is returned by vh_last_error().
+ *  - Pointers are device pointers; sizes are element counts; every launch is
+ *    asynchronous on the caller's stream and the library never allocates,
+ *    frees or synchronises (safe under stream capture).
+ *  - "Reference form" (ref-form) outputs are what the reference schema
+ *    returns: codes and scales as floating tensors of the input's dtype.
+ *    "Packed" outputs hold one byte per code (and per block scale).
+ */
+#ifndef VOYAGER_HIP_H
+#define VOYAGER_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* vh_stream_t; /* == hipStream_t */
+
+/* status */
+#define VH_OK 0
+#define VH_EINVAL 1
+#define VH_ELAUNCH 2
+
+/* element dtypes of tensors crossing the boundary */
+#define VH_BF16 0
+#define VH_F32 1
+#define VH_F16 2
+#define VH_U8 3
+#define VH_I64 4
+
+/* format kinds (what a 65,536-entry quantization map computes) */
+#define VH_FMT_IDENTITY 0 /* entry i == pattern i (get_quantization_map(None)) */
+#define VH_FMT_INT 1      /* clamp(round(v), p0, p1) */
+#define VH_FMT_MINIFLOAT 2 /* p0 exponent bits, p1 mantissa bits */
+#define VH_FMT_POSIT 3    /* posit<p0, es=p1> */
+#define VH_FMT_STEPS 4    /* non-decreasing step function, <= 64 levels */
+#define VH_FMT_LUT 5      /* anything else: gathered from `lut` */
+
+#define VH_FMT_SIGNED 1
+
+#define VH_MAX_STEPS 64
+
+/* A quantization map in closed form.  Filled by the host after verifying,
+ * with vh_build_table, that the closed form reproduces the caller's table on
+ * all 65,536 inputs. */
+typedef struct vh_format {
+  int32_t kind;
+  int32_t p0, p1;   /* INT: lo, hi | MINIFLOAT: ebits, mbits | POSIT: nbits, es */
+  int32_t flags;    /* VH_FMT_SIGNED */
+  int32_t emin;     /* MINIFLOAT: smallest normal exponent, 2 - 2**(ebits-1) */
+  float max_norm;   /* MINIFLOAT: largest finite magnitude */
+  float clamp_bf16; /* MINIFLOAT: max_norm rounded to bfloat16 (the table's clamp) */
+  float thresh;     /* POSIT: magnitudes below this flush to zero */
+  int32_t nsteps;   /* STEPS: number of thresholds (levels - 1) */
+  uint16_t nan_out; /* STEPS: bfloat16 bits of the entry every NaN input takes */
+  uint16_t nan_level;
+  uint16_t thr_key[VH_MAX_STEPS]; /* STEPS: order key of each level's first input */
+  uint16_t val[VH_MAX_STEPS];     /* STEPS: bfloat16 bits of each level's entry */
+  const void* lut;  /* LUT: 65,536 bfloat16 entries in device memory */
+} vh_format;
+
+const char* vh_last_error(void);
+int vh_abi_version(void);
+
+/* Rebuild a format's 65,536-entry table (bfloat16 bits, entry i for input
+ * pattern i).  Replaces get_quantization_map's table construction
+ * (quantization/fake_quantize.py:68-122) and verifies a classification. */
+int vh_build_table(const vh_format* fmt, uint16_t* out, vh_stream_t stream);
+
+/* Broadcast/block indexing of a per-element parameter (scale, zero point)
+ * against a contiguous tensor of up to VH_MAX_DIMS dims: element (i_0..i_n)
+ * reads param[sum_d (i_d / div[d]) * stride[d]].  div[d] is 1 or the block
+ * size; stride[d] is 0 along broadcast dims.  This is repeat_per_block
+ * (ops/quantized.py:124-144) and torch broadcasting in one rule. */
+#define VH_MAX_DIMS 6
+typedef struct vh_param {
+  const void* ptr; /* NULL: absent */
+  int32_t dtype;
+  int32_t scalar;  /* 1: one value for every element */
+  int64_t div[VH_MAX_DIMS];
+  int64_t stride[VH_MAX_DIMS];
+} vh_param;
+
+/* quantize: out = F(round_c(round_c(x / scale) + zp)), F the map (or none),
+ * round_c the rounding to the compute dtype.  Replaces
+ * quantized_ops.quantize (ops/quantized.py:449-515) and, with no scale,
+ * quantized_ops.vmap (ops/quantized.py:147-184).  out_dtype VH_U8 writes
+ * packed codes. */
+int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
+                const vh_format* fmt, void* out, int32_t out_dtype, vh_stream_t stream);
+
+/* dequantize: out = G((Fin(x) - zp) * scale).  Replaces
+ * quantized_ops.dequantize (ops/quantized.py:518-571).  x_dtype VH_U8 reads
+ * packed codes of fmt_in. */
+int vh_dequantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                  const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
+                  const vh_format* fmt_in, const vh_format* fmt_out, void* out,
+                  int32_t out_dtype, vh_stream_t stream);
+
+/* quantize_mx: block scales over `block` elements along the middle axis of a
+ * contiguous [outer, L, inner] tensor, then codes.  Replaces
+ * quantized_ops.quantize_mx (ops/quantized.py:1070-1115) and
+ * calculate_mx_qparam (ops/quantized.py:958-1031; codes_out NULL).
+ * pot != 0: scale = 2**(floor(log2 amax) - floor(log2 quant_max)); else
+ * scale = scale_fmt(amax / quant_max [/ global_scale]).  Zero/NaN scales
+ * become 1.  scale_dtype / codes_dtype VH_U8 write packed bytes (pot scales
+ * as biased exponents: byte = e + pot_bias, 255 = inf). */
+int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                   int64_t block, float quant_max, int32_t pot, const vh_format* scale_fmt,
+                   const void* global_scale, int32_t gs_dtype, const vh_format* fmt,
+                   void* scale_out, int32_t scale_dtype, int32_t pot_bias,
+                   void* codes_out, int32_t codes_dtype, vh_stream_t stream);
+
+/* quantize_affine: per block min/max -> (scale, zero_point, codes).
+ * Replaces quantized_ops.quantize_affine (ops/quantized.py:1218-1283). */
+int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                       int64_t block, float quant_min, float quant_max,
+                       const vh_format* scale_fmt, const vh_format* fmt, void* scale_out,
+                       void* zp_out, void* codes_out, int32_t codes_dtype, vh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOYAGER_HIP_H */

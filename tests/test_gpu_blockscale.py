@@ -1,0 +1,151 @@
+"""quantize_mx / calculate_mx_qparam / dequantize_mx / quantize_affine on the
+GPU against the oracle, at the configs' shapes and on edge blocks."""
+
+import pytest
+import torch
+
+from helpers import assert_same_bits
+from oracle import ops as O
+from oracle import tables as T
+
+pytestmark = pytest.mark.gpu
+
+
+def cfg1_x():
+    """Config 1's activations: seed 0, N(0,1) [256,4096], 0.1% outliers x20."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(256, 4096, generator=g)
+    out = torch.rand(256, 4096, generator=g) < 0.001
+    return torch.where(out, x * 20, x).bfloat16(), g
+
+
+def test_mxint8_cfg1_activation():
+    x, _ = cfg1_x()
+    tab = T.quantization_map("int8")
+    es, ec = O.quantize_mx(x, tab, [-1], 16, 127.0, True)
+    gs, gc = torch.ops.quantized_ops.quantize_mx(x.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    assert_same_bits(gs, es, "scale")
+    assert_same_bits(gc, ec, "codes")
+    assert_same_bits(torch.ops.quantized_ops.calculate_mx_qparam(x.cuda(), [-1], 16, 127.0, True), es, "qparam")
+
+
+def test_mxint8_packed_matches_ref_form():
+    from voyager_amd import packed
+
+    x, _ = cfg1_x()
+    tab = T.quantization_map("int8")
+    es, ec = O.quantize_mx(x, tab, [-1], 16, 127.0, True)
+    p = packed.quantize_mx_packed(x.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    assert_same_bits(packed.unpack_mx_scale(p), es, "packed scale")
+    assert_same_bits(packed.unpack_codes(p.codes, tab.cuda()), ec, "packed codes")
+
+
+def _edge_blocks(block):
+    rows = [
+        [0.0] * block,
+        [float("nan")] + [1.0] * (block - 1),
+        [float("inf")] + [1.0] * (block - 1),
+        [-float("inf")] + [2.0] * (block - 1),
+        [2.0**-127] + [0.0] * (block - 1),
+        [2.0**-128] + [2.0**-130] * (block - 1),
+        [3e38] + [1.0] * (block - 1),
+        [127.5, -127.5] + [0.25] * (block - 2),
+        [-0.0] * block,
+        [1e-40, -2e-40] + [0.0] * (block - 2),
+    ]
+    return torch.tensor(rows, dtype=torch.float32).bfloat16()
+
+
+@pytest.mark.parametrize("block", [16, 32, 64])
+def test_mx_edge_blocks(block):
+    x = _edge_blocks(block)
+    for dtype, qmax in [("int8", 127.0), ("fp8_e4m3", 448.0)]:
+        tab = T.quantization_map(dtype)
+        es, ec = O.quantize_mx(x, tab, [-1], block, qmax, True)
+        gs, gc = torch.ops.quantized_ops.quantize_mx(x.cuda(), tab.cuda(), [-1], block, qmax, True)
+        assert_same_bits(gs, es, f"{dtype} scale")
+        assert_same_bits(gc, ec, f"{dtype} codes")
+
+
+def test_mxnf4_cfg3_shapes():
+    vt = T.quantization_map("lut4_to_int6")
+    index, entries, mid = T.codebook_index_table(vt)
+    stab = T.quantization_map("fp8_e5m3")
+    g = torch.Generator().manual_seed(1)
+    for shape, sc in [((1, 4096), 1.0), ((16, 14336), 1.0), ((1024, 4096), 0.02)]:
+        x = (torch.randn(*shape, generator=g) * sc).bfloat16()
+        es, ec = O.quantize_mx(x, index, [-1], 64, 31.0, False, stab, mid)
+        gs, gc = torch.ops.quantized_ops.quantize_mx(x.cuda(), index.cuda(), [-1], 64, 31.0, False, stab.cuda(),
+                                                     mid.cuda())
+        assert_same_bits(gs, es, f"scale {shape}")
+        assert_same_bits(gc, ec, f"codes {shape}")
+        # decode and scale, as linear_mx does
+        exp = O.dequantize_mx(ec, es, 64, entries)
+        got = torch.ops.quantized_ops.dequantize_mx(gc, gs, 64, entries.cuda())
+        assert_same_bits(got, exp, f"dequantize_mx {shape}")
+
+
+def test_mx_generic_paths():
+    """Column blocks (axis 0), partial blocks, odd lengths, fp32 input."""
+    g = torch.Generator().manual_seed(6)
+    tab = T.quantization_map("int8")
+    x = (torch.randn(50, 37, generator=g) * 3).bfloat16()
+    for axes in ([0], [-1], [1]):
+        es, ec = O.quantize_mx(x, tab, axes, 16, 127.0, True)
+        gs, gc = torch.ops.quantized_ops.quantize_mx(x.cuda(), tab.cuda(), axes, 16, 127.0, True)
+        assert_same_bits(gs, es, f"scale axes={axes}")
+        assert_same_bits(gc, ec, f"codes axes={axes}")
+    xf = (torch.randn(8, 96, generator=g) * 5).float()
+    es, ec = O.quantize_mx(xf, tab, [-1], 32, 127.0, True)
+    gs, gc = torch.ops.quantized_ops.quantize_mx(xf.cuda(), tab.cuda(), [-1], 32, 127.0, True)
+    assert_same_bits(gs, es, "fp32 scale")
+    assert_same_bits(gc, ec, "fp32 codes")
+    # partial last block on the row path (L % 8 == 0, L % block != 0)
+    x2 = (torch.randn(7, 40, generator=g)).bfloat16()
+    es, ec = O.quantize_mx(x2, tab, [-1], 16, 127.0, True)
+    gs, gc = torch.ops.quantized_ops.quantize_mx(x2.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    assert_same_bits(gs, es, "partial scale")
+    assert_same_bits(gc, ec, "partial codes")
+
+
+def test_mx_nonpot_without_scale_map():
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(32, 256, generator=g)).bfloat16()
+    tab = T.quantization_map("fp8_e4m3")
+    es, ec = O.quantize_mx(x, tab, [-1], 32, 448.0, False)
+    gs, gc = torch.ops.quantized_ops.quantize_mx(x.cuda(), tab.cuda(), [-1], 32, 448.0, False)
+    assert_same_bits(gs, es, "scale")
+    assert_same_bits(gc, ec, "codes")
+
+
+@pytest.mark.parametrize("axis", [-2, -1])
+def test_quantize_affine_kivi(axis):
+    """KIVI 2-bit: keys grouped along tokens (axis -2), values along channels
+    (axis -1), group 32, fp16_e5m10 scale/zero-point map."""
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(2, 8, 256, 128, generator=g).bfloat16()
+    x[0, 0, :3, :5] = torch.tensor(float("nan"))
+    x[1, 2, 5, :] = 7.0  # constant rows / columns
+    qtab = T.quantization_map("uint2")
+    stab = T.quantization_map("fp16_e5m10")
+    es, ez, ev = O.quantize_affine(x, qtab, [axis], 32, 0.0, 3.0, stab)
+    gs, gz, gv = torch.ops.quantized_ops.quantize_affine(x.cuda(), qtab.cuda(), [axis], 32, 0.0, 3.0, stab.cuda())
+    assert_same_bits(gs, es, "scale")
+    assert_same_bits(gz, ez, "zero point")
+    assert_same_bits(gv, ev, "codes")
+    # read back (dequantize with the group zero point)
+    exp = O.dequantize(ev, es, ez, [axis], 32)
+    got = torch.ops.quantized_ops.dequantize(gv, gs, gz, [axis], 32)
+    assert_same_bits(got, exp, "dequantize")
+
+
+def test_quantize_affine_partial_blocks():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(3, 50, 24, generator=g).bfloat16()
+    qtab = T.quantization_map("uint2")
+    for axis in (-2, -1):
+        es, ez, ev = O.quantize_affine(x, qtab, [axis], 32, 0.0, 3.0)
+        gs, gz, gv = torch.ops.quantized_ops.quantize_affine(x.cuda(), qtab.cuda(), [axis], 32, 0.0, 3.0)
+        assert_same_bits(gs, es, f"scale {axis}")
+        assert_same_bits(gz, ez, f"zp {axis}")
+        assert_same_bits(gv, ev, f"codes {axis}")

@@ -1,0 +1,64 @@
+"""Device closed forms of every format against the oracle's tables, over all
+65,536 bfloat16 inputs, through classification and through vmap."""
+
+import pytest
+import torch
+
+from helpers import assert_same_bits
+from oracle import tables as T
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = ["int8", "uint2", "int6", "uint8", "int4", "fp8_e4m3", "fp8_e5m3", "fp16_e5m10", "fp8_e5m2",
+          "fp6_e2m3", "fp4_e2m1", "fp8_e4m3_ieee", "posit8_1", "posit8_0", "posit16_1", "lut4_to_int6", None]
+KIND = {"int8": "int", "uint2": "int", "int6": "int", "uint8": "int", "int4": "int", "fp8_e4m3": "minifloat",
+        "fp8_e5m3": "minifloat", "fp16_e5m10": "minifloat", "fp8_e5m2": "minifloat", "fp6_e2m3": "minifloat",
+        "fp4_e2m1": "minifloat", "fp8_e4m3_ieee": "minifloat", "posit8_1": "posit", "posit8_0": "posit",
+        "posit16_1": "posit", "lut4_to_int6": "steps", None: "identity"}
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_closed_form_reproduces_table(dtype):
+    from voyager_amd import formats
+
+    ref = T.quantization_map(dtype)
+    dev = ref.cuda()
+    c = formats.classify(dev)
+    assert formats.describe(c.fmt).startswith(KIND[dtype]), formats.describe(c.fmt)
+    assert_same_bits(formats.build_table(c.fmt, "cuda"), ref, f"table {dtype}")
+    # vmap over every pattern
+    got = torch.ops.quantized_ops.vmap(T.all_bf16().cuda(), dev)
+    assert_same_bits(got, ref, f"vmap {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["int8", "fp8_e4m3", "fp8_e5m3", "posit8_1", "uint2", "fp16_e5m10"])
+def test_product_table_builder_matches_oracle(dtype):
+    from voyager_amd import formats
+
+    assert_same_bits(formats.quantization_map(dtype, "cuda"), T.quantization_map(dtype), dtype)
+
+
+def test_codebook_tables_match_oracle():
+    from voyager_amd import formats
+
+    idx, ent, mid = formats.codebook_tables("lut4_to_int6", "cuda")
+    oi, oe, om = T.codebook_index_table(T.quantization_map("lut4_to_int6"))
+    assert torch.equal(idx.cpu(), oi) and torch.equal(ent.cpu(), oe) and torch.equal(mid.cpu(), om)
+    c = formats.classify(idx)
+    assert c.index_table and formats.describe(c.fmt).startswith("steps")
+    got = torch.ops.quantized_ops.vmap(T.all_bf16().cuda(), idx)
+    exp = torch.empty(65536, dtype=torch.bfloat16)
+    exp.copy_(oi)
+    assert_same_bits(got, exp, "index vmap")
+
+
+def test_unrecognised_table_uses_lut():
+    from voyager_amd import formats
+
+    g = torch.Generator().manual_seed(5)
+    tab = torch.randn(65536, generator=g).bfloat16()
+    c = formats.classify(tab.cuda())
+    assert formats.describe(c.fmt).startswith("lut")
+    x = (torch.randn(1000, generator=g) * 3).bfloat16()
+    got = torch.ops.quantized_ops.vmap(x.cuda(), tab.cuda())
+    assert_same_bits(got, tab[x.view(torch.int16).long() & 0xFFFF], "lut vmap")

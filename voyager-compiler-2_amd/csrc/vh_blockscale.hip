@@ -1,0 +1,400 @@
+// Block-scaled quantization: quantize_mx / calculate_mx_qparam
+// (ops/quantized.py:958-1115) and quantize_affine (ops/quantized.py:1218-1283).
+//
+// A tensor is seen as contiguous [outer, L, inner] with blocks of `block`
+// elements along L (the reference's _reshape_to_blocks, mx_utils.py:66-125:
+// a partial last block is zero-padded for the reduction).
+//
+// Row path (inner == 1, L % 8 == 0, block % 8 == 0, block <= 512): each
+// thread holds 8 consecutive elements (one 16-byte bf16 load); the block's
+// reduction is a butterfly over block/8 lanes of the wavefront (no LDS), so
+// every element is read from HBM exactly once and codes + scales are written
+// once.  Column path (everything else): one thread per (outer, block, inner)
+// column, consecutive threads on consecutive `inner` for coalescing.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "vh_device.h"
+#include "vh_host.h"
+
+namespace {
+
+enum Mode { MX_POT = 0, MX_SCALED = 1, AFFINE = 2 };
+
+struct Params {
+  int mode;
+  int cdt;            // compute dtype: the input's
+  float quant_max;    // MX: element max; AFFINE: quant_max
+  float quant_min;    // AFFINE
+  int shift;          // MX_POT: floor(log2(quant_max))
+  int has_sfmt;       // scale map present
+  vh_format sfmt;     // scale map
+  const void* gs;     // MX_SCALED: 0-d global scale (device), or null
+  int gs_dtype;
+  int has_fmt;        // element map present (calculate_mx_qparam has none)
+  vh_format fmt;      // element map
+  int scale_dtype;    // cdt or VH_U8
+  int pot_bias;       // packed pot scale byte = e + pot_bias
+  int codes_dtype;    // cdt or VH_U8
+};
+
+// NaN-propagating max/min, as torch.amax / torch.amin.
+VH_DEV float nmax(float a, float b) { return isnan_f(a) ? a : (isnan_f(b) ? b : fmaxf(a, b)); }
+VH_DEV float nmin(float a, float b) { return isnan_f(a) ? a : (isnan_f(b) ? b : fminf(a, b)); }
+
+VH_DEV float load_x(const void* p, int dt, int64_t i) {
+  if (dt == VH_BF16) return bf2f(((const uint16_t*)p)[i]);
+  if (dt == VH_F16) return __half2float(((const __half*)p)[i]);
+  return ((const float*)p)[i];
+}
+
+VH_DEV void store_f(void* p, int dt, int64_t i, float v) {
+  if (dt == VH_BF16) ((uint16_t*)p)[i] = (uint16_t)f2bf(v);
+  else if (dt == VH_F16) ((__half*)p)[i] = __float2half_rn(v);
+  else ((float*)p)[i] = v;
+}
+
+// vmap of a value in the compute dtype through a map, result in cdt.
+VH_DEV float vmap1(float v, const vh_format& f, const uint16_t* lds, int cdt) {
+  uint32_t b = f2bf(v);
+  return round_to(fmt_value(b, f, lds), cdt);
+}
+
+struct BlockScale {
+  float scale;      // the returned scale (cdt value)
+  float el_scale;   // what the elements are divided by
+  float zp;         // AFFINE zero point
+  uint32_t packed;  // packed scale byte
+};
+
+// Scale of one block from its reductions (hi = amax for MX, max for AFFINE;
+// lo = min for AFFINE).
+VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_t* slds) {
+  BlockScale r;
+  r.zp = 0.0f;
+  r.packed = 0;
+  const int cdt = P.cdt;
+  if (P.mode == MX_POT) {
+    // floor(log2(fp32(amax) + 2**-126 * (amax == 0))), mx_utils.py:47-51;
+    // then 2**(e - shift) in the compute dtype (ops/quantized.py:995-1015).
+    float s;
+    int e = 0;
+    bool inf = false;
+    if (isnan_f(hi)) {
+      s = 1.0f;  // NaN > 0 is false
+    } else if (hi == __builtin_inff()) {
+      s = __builtin_inff();
+      inf = true;
+    } else {
+      int E = hi == 0.0f ? -126 : floor_log2(hi);
+      e = E - P.shift;
+      s = round_to(ldexpf(1.0f, e), cdt);
+      if (s == __builtin_inff()) inf = true;
+      if (!(s > 0.0f)) { s = 1.0f; e = 0; }
+    }
+    r.scale = s;
+    r.el_scale = s;
+    int byte = inf ? 255 : e + P.pot_bias;
+    r.packed = (uint32_t)(byte < 0 ? 0 : (byte > 254 && !inf ? 254 : byte));
+    return r;
+  }
+  if (P.mode == MX_SCALED) {
+    float s = round_to(hi / P.quant_max, cdt);
+    const float gs = P.gs ? round_to(load_x(P.gs, P.gs_dtype, 0), cdt) : 1.0f;
+    if (P.gs) s = round_to(s / gs, cdt);
+    uint32_t sb = 0;
+    if (P.has_sfmt) {
+      sb = f2bf(s);
+      s = round_to(fmt_value(sb, P.sfmt, slds), cdt);
+    }
+    if (!(s > 0.0f)) s = 1.0f;
+    r.scale = s;
+    r.el_scale = P.gs ? round_to(s * gs, cdt) : s;
+    if (P.has_sfmt) {
+      uint32_t b = f2bf(s);
+      r.packed = fmt_code(b, bf2f(b), P.sfmt, slds);
+    }
+    return r;
+  }
+  // AFFINE (ops/quantized.py:1262-1281)
+  float s = round_to(round_to(hi - lo, cdt) / (P.quant_max - P.quant_min), cdt);
+  if (!(s > 0.0f)) s = 1.0f;
+  if (P.has_sfmt) {
+    s = vmap1(s, P.sfmt, slds, cdt);
+    if (!(s > 0.0f)) s = 1.0f;
+  }
+  float zp = round_to(round_to(-lo / s, cdt) + P.quant_min, cdt);
+  if (P.has_sfmt) zp = vmap1(zp, P.sfmt, slds, cdt);
+  r.scale = s;
+  r.el_scale = s;
+  r.zp = zp;
+  return r;
+}
+
+// One element's reference-form code value and packed byte.
+VH_DEV void element_code(float x, const BlockScale& bs, const Params& P, const uint16_t* lds, float* v,
+                         uint32_t* code) {
+  float q = round_to(x / bs.el_scale, P.cdt);
+  if (P.mode == AFFINE) q = round_to(q + bs.zp, P.cdt);
+  uint32_t b = f2bf(q);
+  if (P.cdt == VH_BF16 && !isnan_f(q)) b = __float_as_uint(q) >> 16;
+  float val = fmt_value(b, P.fmt, lds);
+  *v = round_to(val, P.cdt);
+  if (P.codes_dtype == VH_U8) *code = fmt_code(b, val, P.fmt, lds);
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256)
+k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, Params P,
+       void* __restrict__ scale_out, void* __restrict__ zp_out, void* __restrict__ codes_out) {
+  __shared__ uint16_t lds[2 * VH_MAX_STEPS];
+  __shared__ uint16_t slds[2 * VH_MAX_STEPS];
+  if (P.has_fmt) stage_steps(P.fmt, lds);
+  if (P.has_sfmt) stage_steps(P.sfmt, slds);
+  const int64_t tpr = nblk * g;  // threads per row
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = t / tpr;
+  const int64_t v = t % tpr;
+  const bool live = row < rows && v * VEC < L;
+  const int64_t base = row * L + v * VEC;
+  float xv[VEC];
+  if (live) {
+    if (P.cdt == VH_BF16) {
+      uint4 raw = *(const uint4*)((const uint16_t*)x + base);
+      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xv[2 * j] = bf2f(w[j] & 0xffffu);
+        xv[2 * j + 1] = bf2f(w[j] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) xv[j] = load_x(x, P.cdt, base + j);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) xv[j] = 0.0f;  // zero padding of a partial block
+  }
+  float hi, lo;
+  if (P.mode == AFFINE) {
+    hi = xv[0];
+    lo = xv[0];
+#pragma unroll
+    for (int j = 1; j < VEC; ++j) {
+      hi = nmax(hi, xv[j]);
+      lo = nmin(lo, xv[j]);
+    }
+  } else {
+    hi = fabsf(xv[0]);
+#pragma unroll
+    for (int j = 1; j < VEC; ++j) hi = nmax(hi, fabsf(xv[j]));
+  }
+  // butterfly over the g lanes of this block (g is a power of two <= 64)
+  for (int off = 1; off < g; off <<= 1) {
+    hi = nmax(hi, __shfl_xor(hi, off));
+    if (P.mode == AFFINE) lo = nmin(lo, __shfl_xor(lo, off));
+  }
+  if (row >= rows) return;
+  BlockScale bs = block_scale(hi, lo, P, slds);
+  const int64_t blk = v / g;
+  if ((v % g) == 0 && blk < nblk) {
+    const int64_t si = row * nblk + blk;
+    if (P.scale_dtype == VH_U8) ((uint8_t*)scale_out)[si] = (uint8_t)bs.packed;
+    else store_f(scale_out, P.cdt, si, bs.scale);
+    if (P.mode == AFFINE) store_f(zp_out, P.cdt, si, bs.zp);
+  }
+  if (!live || !codes_out) return;
+  float cv[VEC];
+  uint32_t cc[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) element_code(xv[j], bs, P, lds, &cv[j], &cc[j]);
+  if (P.codes_dtype == VH_U8) {
+    uint2 pk;
+    pk.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
+    pk.y = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
+    *(uint2*)((uint8_t*)codes_out + base) = pk;
+  } else if (P.cdt == VH_BF16) {
+    uint4 pk;
+    pk.x = f2bf(cv[0]) | (f2bf(cv[1]) << 16);
+    pk.y = f2bf(cv[2]) | (f2bf(cv[3]) << 16);
+    pk.z = f2bf(cv[4]) | (f2bf(cv[5]) << 16);
+    pk.w = f2bf(cv[6]) | (f2bf(cv[7]) << 16);
+    *(uint4*)((uint16_t*)codes_out + base) = pk;
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) store_f(codes_out, P.cdt, base + j, cv[j]);
+  }
+}
+
+// One thread per (outer, block, inner) column.
+__global__ void __launch_bounds__(256)
+k_cols(const void* __restrict__ x, int64_t outer, int64_t L, int64_t inner, int64_t block, int64_t nblk, Params P,
+       void* __restrict__ scale_out, void* __restrict__ zp_out, void* __restrict__ codes_out) {
+  __shared__ uint16_t lds[2 * VH_MAX_STEPS];
+  __shared__ uint16_t slds[2 * VH_MAX_STEPS];
+  if (P.has_fmt) stage_steps(P.fmt, lds);
+  if (P.has_sfmt) stage_steps(P.sfmt, slds);
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = outer * nblk * inner;
+  if (t >= total) return;
+  const int64_t in = t % inner;
+  const int64_t blk = (t / inner) % nblk;
+  const int64_t o = t / (inner * nblk);
+  const int64_t l0 = blk * block;
+  const int64_t l1 = l0 + block < L ? l0 + block : L;
+  const int64_t base = o * L * inner + in;
+  float hi, lo;
+  if (P.mode == AFFINE) {
+    hi = load_x(x, P.cdt, base + l0 * inner);
+    lo = hi;
+  } else {
+    hi = 0.0f;
+    lo = 0.0f;
+  }
+  for (int64_t l = l0; l < l1; ++l) {
+    float xv = load_x(x, P.cdt, base + l * inner);
+    if (P.mode == AFFINE) {
+      hi = nmax(hi, xv);
+      lo = nmin(lo, xv);
+    } else {
+      hi = nmax(hi, fabsf(xv));
+    }
+  }
+  if (P.mode == AFFINE && l1 - l0 < block) {  // zero padding joins min and max
+    hi = nmax(hi, 0.0f);
+    lo = nmin(lo, 0.0f);
+  }
+  BlockScale bs = block_scale(hi, lo, P, slds);
+  const int64_t si = (o * nblk + blk) * inner + in;
+  if (P.scale_dtype == VH_U8) ((uint8_t*)scale_out)[si] = (uint8_t)bs.packed;
+  else store_f(scale_out, P.cdt, si, bs.scale);
+  if (P.mode == AFFINE) store_f(zp_out, P.cdt, si, bs.zp);
+  if (!codes_out) return;
+  for (int64_t l = l0; l < l1; ++l) {
+    int64_t i = base + l * inner;
+    float cv;
+    uint32_t cc;
+    element_code(load_x(x, P.cdt, i), bs, P, lds, &cv, &cc);
+    if (P.codes_dtype == VH_U8) ((uint8_t*)codes_out)[i] = (uint8_t)cc;
+    else store_f(codes_out, P.cdt, i, cv);
+  }
+}
+
+int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block, const Params& P,
+           void* scale_out, void* zp_out, void* codes_out, hipStream_t stream, const char* what) {
+  const int64_t nblk = (L + block - 1) / block;
+  const bool rows_ok = inner == 1 && L % 8 == 0 && block % 8 == 0 && block <= 512 &&
+                       ((block / 8) & (block / 8 - 1)) == 0;
+  if (rows_ok) {
+    const int g = (int)(block / 8);
+    const int64_t threads = outer * nblk * g;
+    const int64_t blocks = (threads + 255) / 256;
+    VH_REQUIRE(blocks < (1ll << 31), "%s: tensor too large", what);
+    hipLaunchKernelGGL(k_rows<8>, dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P, scale_out,
+                       zp_out, codes_out);
+  } else {
+    const int64_t threads = outer * nblk * inner;
+    const int64_t blocks = (threads + 255) / 256;
+    VH_REQUIRE(blocks < (1ll << 31), "%s: tensor too large", what);
+    hipLaunchKernelGGL(k_cols, dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, inner, block, nblk, P,
+                       scale_out, zp_out, codes_out);
+  }
+  return vh::check_launch(what);
+}
+
+int check_common(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner, int64_t block,
+                 const char* what) {
+  VH_REQUIRE(x, "%s: null input", what);
+  VH_REQUIRE(vh::is_float_dtype(x_dtype), "%s: input dtype %d unsupported", what, x_dtype);
+  VH_REQUIRE(outer >= 0 && L >= 0 && inner >= 0, "%s: negative size", what);
+  VH_REQUIRE(block > 0, "%s: block_size must be > 0", what);
+  return VH_OK;
+}
+
+bool packable(const vh_format& f) {
+  switch (f.kind) {
+    case VH_FMT_INT: return (f.p0 >= -128 && f.p1 <= 127) || (f.p0 >= 0 && f.p1 <= 255);
+    case VH_FMT_MINIFLOAT: return f.p0 + f.p1 + ((f.flags & VH_FMT_SIGNED) ? 1 : 0) <= 8;
+    case VH_FMT_POSIT: return f.p0 <= 8;
+    case VH_FMT_STEPS: return true;
+    default: return false;
+  }
+}
+
+}  // namespace
+
+extern "C" int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                              int64_t block, float quant_max, int32_t pot, const vh_format* scale_fmt,
+                              const void* global_scale, int32_t gs_dtype, const vh_format* fmt, void* scale_out,
+                              int32_t scale_dtype, int32_t pot_bias, void* codes_out, int32_t codes_dtype,
+                              vh_stream_t stream) {
+  int rc;
+  if ((rc = check_common(x, x_dtype, outer, L, inner, block, "vh_quantize_mx"))) return rc;
+  VH_REQUIRE(scale_out, "vh_quantize_mx: null scale output");
+  VH_REQUIRE(!codes_out || fmt, "vh_quantize_mx: codes need an element map");
+  VH_REQUIRE(scale_dtype == x_dtype || scale_dtype == VH_U8, "vh_quantize_mx: scale dtype must be the input's or u8");
+  VH_REQUIRE(!codes_out || codes_dtype == x_dtype || codes_dtype == VH_U8,
+             "vh_quantize_mx: codes dtype must be the input's or u8");
+  VH_REQUIRE(!(codes_out && codes_dtype == VH_U8) || packable(*fmt), "vh_quantize_mx: element map has no packed form");
+  VH_REQUIRE(!(scale_dtype == VH_U8 && !pot) || (scale_fmt && packable(*scale_fmt)),
+             "vh_quantize_mx: packed scales need pot or a packable scale map");
+  VH_REQUIRE(pot || quant_max != 0.0f, "vh_quantize_mx: quant_max must be nonzero");
+  Params P;
+  memset(&P, 0, sizeof(P));
+  P.mode = pot ? MX_POT : MX_SCALED;
+  P.cdt = x_dtype;
+  P.quant_max = quant_max;
+  if (pot) {
+    VH_REQUIRE(quant_max > 0.0f, "vh_quantize_mx: quant_max must be positive for power-of-two scales");
+    P.shift = (int)floorf(log2f(quant_max));
+  }
+  if (scale_fmt) {
+    P.has_sfmt = 1;
+    P.sfmt = *scale_fmt;
+  }
+  if (global_scale) {
+    VH_REQUIRE(!pot, "vh_quantize_mx: a global scale needs non-power-of-two scales");
+    VH_REQUIRE(vh::is_float_dtype(gs_dtype), "vh_quantize_mx: global scale dtype unsupported");
+    P.gs = global_scale;
+    P.gs_dtype = gs_dtype;
+  }
+  if (fmt) {
+    P.has_fmt = 1;
+    P.fmt = *fmt;
+  }
+  P.scale_dtype = scale_dtype;
+  P.pot_bias = pot_bias;
+  P.codes_dtype = codes_dtype;
+  if (outer * L * inner == 0) return VH_OK;
+  return launch(x, outer, L, inner, block, P, scale_out, nullptr, codes_out, vh::as_stream(stream),
+                "vh_quantize_mx");
+}
+
+extern "C" int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                                  int64_t block, float quant_min, float quant_max, const vh_format* scale_fmt,
+                                  const vh_format* fmt, void* scale_out, void* zp_out, void* codes_out,
+                                  int32_t codes_dtype, vh_stream_t stream) {
+  int rc;
+  if ((rc = check_common(x, x_dtype, outer, L, inner, block, "vh_quantize_affine"))) return rc;
+  VH_REQUIRE(scale_out && zp_out && fmt, "vh_quantize_affine: null output or map");
+  VH_REQUIRE(codes_dtype == x_dtype || codes_dtype == VH_U8, "vh_quantize_affine: bad codes dtype");
+  VH_REQUIRE(codes_dtype != VH_U8 || packable(*fmt), "vh_quantize_affine: element map has no packed form");
+  Params P;
+  memset(&P, 0, sizeof(P));
+  P.mode = AFFINE;
+  P.cdt = x_dtype;
+  P.quant_max = quant_max;
+  P.quant_min = quant_min;
+  if (scale_fmt) {
+    P.has_sfmt = 1;
+    P.sfmt = *scale_fmt;
+  }
+  P.has_fmt = 1;
+  P.fmt = *fmt;
+  P.scale_dtype = x_dtype;
+  P.codes_dtype = codes_dtype;
+  if (outer * L * inner == 0) return VH_OK;
+  return launch(x, outer, L, inner, block, P, scale_out, zp_out, codes_out, vh::as_stream(stream),
+                "vh_quantize_affine");
+}

@@ -1,0 +1,303 @@
+// Device-side numeric formats of the quantized-operator path (gfx950).
+//
+// Every quantization map of the reference is a 65,536-entry table indexed by
+// a bfloat16 bit pattern (ops/quantized.py:147-190, fake_quantize.py:68-122).
+// Here each table family is a closed form evaluated in registers; the host
+// only selects a closed form after a device kernel has rebuilt the caller's
+// table from it and found every entry equal, so "closed form == table" holds
+// by construction.  Unrecognised tables are gathered from memory (VH_FMT_LUT).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/voyager_hip.h"
+
+#define VH_DEV static __device__ __forceinline__
+
+// ---------------------------------------------------------------- bf16 bits
+VH_DEV float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even float32 -> bfloat16 bits; NaN -> canonical 0x7FC0.
+VH_DEV uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// The float32 value rounded to bfloat16 and back (an eager bf16 op result).
+VH_DEV float rbf(float f) { return bf2f(f2bf(f)); }
+
+// float32 -> float16 -> float32 with round-to-nearest-even (an fp16 op result).
+VH_DEV float rhf(float f) { return __half2float(__float2half_rn(f)); }
+
+// Round a float32 value to the storage dtype of an eager op's result.
+VH_DEV float round_to(float f, int dtype) {
+  if (dtype == VH_BF16) return rbf(f);
+  if (dtype == VH_F16) return rhf(f);
+  return f;
+}
+
+VH_DEV bool isnan_f(float f) { return f != f; }
+
+// floor(log2(|a|)) of a finite nonzero float32, subnormals included.
+VH_DEV int floor_log2(float a) {
+  uint32_t u = __float_as_uint(a) & 0x7fffffffu;
+  int ef = (int)(u >> 23);
+  if (ef) return ef - 127;
+  uint32_t m = u & 0x7fffffu;
+  return (31 - (int)__clz(m)) - 149;
+}
+
+// Order-preserving key of a bfloat16 pattern: -NaN < -inf < ... < -0 < +0 <
+// ... < +inf < +NaN as unsigned 16-bit integers.
+VH_DEV uint32_t bf_key(uint32_t b) {
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+
+// ---------------------------------------------------------------- formats
+// INT: clamp(round_half_even(v), lo, hi); NaN stays NaN; -0 is kept
+// (fake_quantize.py:95-96).
+VH_DEV float fmt_int(float x, const vh_format& f) {
+  float r = rintf(x);
+  float lo = (float)f.p0, hi = (float)f.p1;
+  return r < lo ? lo : (r > hi ? hi : r);
+}
+
+// MINIFLOAT: saturate to the bfloat16-rounded max, then round half-even to a
+// grid of p1 mantissa bits with subnormals below exponent emin, then clamp to
+// max_norm (fake_quantize.py:98-111 with dtypes/fp8.py:69-135).  A zero
+// input gives +0; a nonzero input that rounds to zero keeps its sign.
+VH_DEV float fmt_minifloat(float x, const vh_format& f) {
+  if (isnan_f(x)) return x;
+  if (!(f.flags & VH_FMT_SIGNED)) x = fabsf(x);
+  float cm = f.clamp_bf16;
+  x = x < -cm ? -cm : (x > cm ? cm : x);
+  if (x == 0.0f) return 0.0f;
+  float a = fabsf(x);
+  int e = floor_log2(a);
+  if (e < f.emin) e = f.emin;
+  float r = rintf(ldexpf(a, f.p1 - e));
+  float out = ldexpf(r, e - f.p1);
+  if (out > f.max_norm) out = f.max_norm;
+  return copysignf(out, x);
+}
+
+// POSIT<p0, es=p1>: rounding by manipulation of the float32 encoding, the
+// same steps as dtypes/posit.py:8-73 (round_to_even=True): regime/exponent/
+// fraction assembled into one bit string, rounded at the posit's last bit
+// with guard and sticky bits, saturating at maxpos, and with magnitudes below
+// 2**floor(-(n-1)*2**es + 2**(es-1)) flushed to zero.  Inf/NaN -> NaN.
+VH_DEV float fmt_posit(float x, const vh_format& f) {
+  const int nbits = f.p0, es = f.p1;
+  if (!(fabsf(x) <= 3.4028235e38f)) return __uint_as_float(0x7fc00000u);
+  if (x == 0.0f) return 0.0f;
+  int32_t raw = (int32_t)__float_as_uint(x);
+  int32_t scale = ((raw & 0x7F800000) >> 23) - 127;
+  int32_t frac = raw & 0x7FFFFF;
+  const int32_t max_scale = (nbits - 2) * (1 << es);
+  bool pos = scale >= 0;
+  bool dominated = pos ? (scale > max_scale) : (scale < -max_scale);
+  bool up = false;
+  int32_t ecut = es, fcut = 23;
+  if (!dominated) {
+    // Here |scale| <= max_scale, so every shift below stays within 64 bits.
+    int32_t run = pos ? 1 + (scale >> es) : -(scale >> es);
+    int64_t regime = (pos ? (int64_t)((1ull << (run + 1)) - 1ull) : 0) ^ 1;
+    int64_t expo = scale & ((1 << es) - 1);
+    int64_t pbits = (regime << (23 + es)) | (expo << 23) | frac;
+    int32_t len = 2 + run + es + 23;
+    int64_t last = (int64_t)1 << (len - nbits);
+    int64_t guard = last >> 1;
+    int64_t sticky = guard - 1;
+    bool lb = (pbits & last) != 0;
+    bool gb = (pbits & guard) != 0;
+    bool sb = (pbits & sticky) != 0;
+    up = (lb && gb) || (gb && sb);
+    ecut = 2 + run + es - nbits;
+    ecut = ecut < 0 ? 0 : (ecut > es ? es : ecut);
+    fcut = len - nbits;
+    fcut = fcut < 0 ? 0 : (fcut > 23 ? 23 : fcut);
+  }
+  // A dominated regime truncates every exponent and fraction bit and never
+  // rounds up: 2 + run + es - nbits >= es + 1 and len - nbits >= 24 there.
+  scale &= (int32_t)(0xffffffffu << ecut);
+  scale = scale < -max_scale ? -max_scale : (scale > max_scale ? max_scale : scale);
+  frac &= (int32_t)(0xffffffffu << fcut);
+  int32_t out = ((scale + 127) << 23) | frac;
+  if (up) out += 1 << (fcut + ecut);
+  float v = __int_as_float(out);
+  v = x < 0.0f ? -v : v;
+  if (fabsf(x) < f.thresh) v = 0.0f;
+  return v;
+}
+
+// STEPS: a table that is a non-decreasing step function of the value.  The
+// level is the number of thresholds whose key is <= the input's key (keys are
+// staged in LDS by the kernel: `keys` holds f.thr_key).  NaN inputs are
+// handled by the caller (they take nan_out / nan_level).
+VH_DEV uint32_t steps_level(uint32_t b, int nsteps, const uint16_t* keys) {
+  uint32_t k = bf_key(b);
+  int lo = 0, hi = nsteps;  // first threshold whose key exceeds k
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if ((uint32_t)keys[mid] <= k) lo = mid + 1; else hi = mid;
+  }
+  return (uint32_t)lo;
+}
+
+// Stage a STEPS format's keys and entries in LDS (2 * VH_MAX_STEPS halves).
+// Every thread of the block must call it.
+VH_DEV void stage_steps(const vh_format& f, uint16_t* lds) {
+  if (f.kind == VH_FMT_STEPS) {
+    for (int i = threadIdx.x; i < VH_MAX_STEPS; i += blockDim.x) {
+      lds[i] = f.thr_key[i];
+      lds[VH_MAX_STEPS + i] = f.val[i];
+    }
+  }
+  __syncthreads();
+}
+
+VH_DEV bool bf_isnan_bits(uint32_t b) { return (b & 0x7fffu) > 0x7f80u; }
+
+// Apply a format to a bfloat16 input; returns the table entry's value as
+// float32 (bfloat16 entries are exact in float32; index tables are small
+// integers).  VH_FMT_LUT tables are gathered from device memory.
+VH_DEV float fmt_value(uint32_t b, const vh_format& f, const uint16_t* lds) {
+  float x = bf2f(b);
+  switch (f.kind) {
+    case VH_FMT_IDENTITY: return x;
+    case VH_FMT_INT: return fmt_int(x, f);
+    case VH_FMT_MINIFLOAT: return rbf(fmt_minifloat(x, f));
+    case VH_FMT_POSIT: return rbf(fmt_posit(x, f));
+    case VH_FMT_STEPS:
+      if (bf_isnan_bits(b)) return bf2f(f.nan_out);
+      return bf2f(lds[VH_MAX_STEPS + steps_level(b, f.nsteps, lds)]);
+    default: {  // VH_FMT_LUT: bf16 bit table
+      const uint16_t* t = (const uint16_t*)f.lut;
+      return bf2f(t[b & 0xffffu]);
+    }
+  }
+}
+
+// ------------------------------------------------------------ packed codes
+// One byte per element: INT two's complement; MINIFLOAT sign|exponent|
+// mantissa fields (fp8_e4m3 is the OCP E4M3 byte the fp8 MFMA reads);
+// POSIT the posit bit string; STEPS the level index.  Packed int8 cannot
+// hold NaN: a NaN element packs as 0.
+
+VH_DEV uint32_t mini_code(float v, const vh_format& f) {
+  const int mb = f.p1;
+  uint32_t sign = 0;
+  if ((f.flags & VH_FMT_SIGNED) && (__float_as_uint(v) >> 31)) sign = 1u << (f.p0 + mb);
+  if (isnan_f(v)) return sign | (((1u << f.p0) - 1u) << mb) | ((1u << mb) - 1u);
+  float a = fabsf(v);
+  if (a == 0.0f) return sign;
+  int e = floor_log2(a);
+  uint32_t ef, m;
+  if (e < f.emin) {  // subnormal
+    ef = 0;
+    m = (uint32_t)ldexpf(a, mb - f.emin);
+  } else {
+    ef = (uint32_t)(e - f.emin + 1);
+    m = (uint32_t)ldexpf(a, mb - e) - (1u << mb);
+  }
+  return sign | (ef << mb) | m;
+}
+
+VH_DEV float mini_decode(uint32_t c, const vh_format& f) {
+  const int mb = f.p1;
+  uint32_t m = c & ((1u << mb) - 1u);
+  uint32_t ef = (c >> mb) & ((1u << f.p0) - 1u);
+  float a = ef ? ldexpf((float)(m + (1u << mb)), (int)ef - 1 + f.emin - mb)
+               : ldexpf((float)m, f.emin - mb);
+  if ((f.flags & VH_FMT_SIGNED) && ((c >> (f.p0 + mb)) & 1u)) a = -a;
+  return a;
+}
+
+// Posit bit string of an exactly representable posit value.
+VH_DEV uint32_t posit_code(float v, const vh_format& f) {
+  const int n = f.p0, es = f.p1;
+  if (isnan_f(v)) return 1u << (n - 1);  // NaR
+  if (v == 0.0f) return 0;
+  float a = fabsf(v);
+  int s = floor_log2(a);
+  int k = s >> es;               // regime value (floor)
+  int ex = s - (k << es);        // exponent bits
+  uint32_t fr = __float_as_uint(a) & 0x7fffffu;  // fraction (23 bits)
+  // Assemble regime | exponent | fraction into a long bit string.
+  uint64_t body;
+  int blen;
+  if (k >= 0) {
+    body = ((1ull << (k + 1)) - 1ull) << 1;  // k+1 ones then a zero
+    blen = k + 2;
+  } else {
+    body = 1ull;                              // -k zeros then a one
+    blen = -k + 1;
+  }
+  body = (body << es) | (uint64_t)ex;
+  blen += es;
+  body = (body << 23) | fr;
+  blen += 23;
+  int avail = n - 1;
+  uint32_t bits = blen > avail ? (uint32_t)(body >> (blen - avail))
+                               : (uint32_t)(body << (avail - blen));
+  bits &= (1u << avail) - 1u;
+  if (v < 0.0f) bits = ((~bits) + 1u) & ((1u << n) - 1u);
+  return bits;
+}
+
+VH_DEV float posit_decode(uint32_t c, const vh_format& f) {
+  const int n = f.p0, es = f.p1;
+  c &= (1u << n) - 1u;
+  if (c == 0) return 0.0f;
+  if (c == (1u << (n - 1))) return __uint_as_float(0x7fc00000u);
+  bool neg = (c >> (n - 1)) & 1u;
+  if (neg) c = ((~c) + 1u) & ((1u << n) - 1u);
+  int i = n - 2;
+  uint32_t first = (c >> i) & 1u;
+  int run = 0;
+  while (i >= 0 && ((c >> i) & 1u) == first) { run++; i--; }
+  i--;  // skip the terminating bit
+  int k = first ? run - 1 : -run;
+  int ex = 0, ebits = 0;
+  while (ebits < es) {
+    ex <<= 1;
+    if (i >= 0) { ex |= (c >> i) & 1u; i--; }
+    ebits++;
+  }
+  int fbits = i + 1;
+  uint32_t fr = fbits > 0 ? (c & ((1u << fbits) - 1u)) : 0u;
+  float val = ldexpf(1.0f + ldexpf((float)fr, -fbits), k * (1 << es) + ex);
+  return neg ? -val : val;
+}
+
+// Packed code of an element whose table value is v (bits b of the input).
+VH_DEV uint32_t fmt_code(uint32_t b, float v, const vh_format& f, const uint16_t* lds) {
+  switch (f.kind) {
+    case VH_FMT_INT: return isnan_f(v) ? 0u : ((uint32_t)(int32_t)v & 0xffu);
+    case VH_FMT_MINIFLOAT: return mini_code(v, f) & 0xffu;
+    case VH_FMT_POSIT: return posit_code(v, f) & 0xffu;
+    case VH_FMT_STEPS:
+      if (bf_isnan_bits(b)) return (uint32_t)f.nan_level;
+      return steps_level(b, f.nsteps, lds);
+    default: return 0u;
+  }
+}
+
+// The reference-form value of a packed code (the table entry, as float32).
+VH_DEV float fmt_decode(uint32_t c, const vh_format& f, const uint16_t* lds) {
+  switch (f.kind) {
+    case VH_FMT_INT:
+      return (f.p0 < 0) ? (float)(int8_t)(uint8_t)c : (float)(uint8_t)c;
+    case VH_FMT_MINIFLOAT: {
+      float v = mini_decode(c, f);
+      return rbf(v > f.max_norm ? f.max_norm : v);
+    }
+    case VH_FMT_POSIT: return rbf(posit_decode(c, f));
+    case VH_FMT_STEPS: return bf2f(lds[VH_MAX_STEPS + (c < VH_MAX_STEPS ? c : VH_MAX_STEPS - 1)]);
+    default: return 0.0f;
+  }
+}

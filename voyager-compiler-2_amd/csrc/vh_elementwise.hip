@@ -1,0 +1,329 @@
+// Elementwise quantized ops: table rebuild, quantize (+ vmap) and dequantize.
+//
+// quantize   (ops/quantized.py:449-515):  out = F(rc(rc(x / s) + zp))
+// dequantize (ops/quantized.py:518-571):  out = G(rc((Fin(x) - zp) * s))
+// vmap       (ops/quantized.py:147-184):  out = F(x)
+// where rc rounds to the compute dtype (each eager op's result dtype) and the
+// maps F, Fin, G are closed forms of the caller's 65,536-entry tables.
+//
+// HBM-bound: every thread moves 8 consecutive elements with 16-byte loads
+// (bf16) and stores, so a wavefront touches 1 KiB contiguous per access.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+
+#include "vh_device.h"
+#include "vh_host.h"
+
+namespace vh {
+
+static thread_local std::string g_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return VH_ELAUNCH;
+  }
+  return VH_OK;
+}
+
+}  // namespace vh
+
+extern "C" const char* vh_last_error(void) { return vh::g_error.c_str(); }
+extern "C" int vh_abi_version(void) { return 1; }
+
+// ------------------------------------------------------------ table rebuild
+__global__ void __launch_bounds__(256) k_build_table(vh_format f, uint16_t* out) {
+  __shared__ uint16_t lds[2 * VH_MAX_STEPS];
+  stage_steps(f, lds);
+  uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= 65536u) return;
+  float v = fmt_value(b, f, lds);
+  if (f.kind == VH_FMT_IDENTITY || f.kind == VH_FMT_LUT) {
+    // Entries that are not values of a closed form are copied bit for bit.
+    out[b] = f.kind == VH_FMT_IDENTITY ? (uint16_t)b : ((const uint16_t*)f.lut)[b];
+    return;
+  }
+  out[b] = (uint16_t)f2bf(v);
+}
+
+extern "C" int vh_build_table(const vh_format* fmt, uint16_t* out, vh_stream_t stream) {
+  VH_REQUIRE(fmt && out, "vh_build_table: null argument");
+  VH_REQUIRE(fmt->kind >= VH_FMT_IDENTITY && fmt->kind <= VH_FMT_LUT, "vh_build_table: bad kind %d", fmt->kind);
+  VH_REQUIRE(fmt->kind != VH_FMT_STEPS || (fmt->nsteps >= 0 && fmt->nsteps < VH_MAX_STEPS),
+             "vh_build_table: nsteps %d out of range", fmt->nsteps);
+  hipLaunchKernelGGL(k_build_table, dim3(256), dim3(256), 0, vh::as_stream(stream), *fmt, out);
+  return vh::check_launch("vh_build_table");
+}
+
+// ------------------------------------------------------------ param access
+struct Shape {
+  int64_t dim[VH_MAX_DIMS];  // sizes, innermost last
+  int32_t ndim;
+};
+
+VH_DEV float load_any(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case VH_BF16: return bf2f(((const uint16_t*)p)[i]);
+    case VH_F16: return __half2float(((const __half*)p)[i]);
+    case VH_F32: return ((const float*)p)[i];
+    default: return 0.0f;
+  }
+}
+
+VH_DEV void store_any(void* p, int dtype, int64_t i, float v) {
+  switch (dtype) {
+    case VH_BF16: ((uint16_t*)p)[i] = (uint16_t)f2bf(v); break;
+    case VH_F16: ((__half*)p)[i] = __float2half_rn(v); break;
+    case VH_F32: ((float*)p)[i] = v; break;
+    default: break;
+  }
+}
+
+// Offset of element `flat`'s parameter.
+VH_DEV int64_t param_offset(const vh_param& p, const Shape& s, int64_t flat) {
+  int64_t off = 0;
+  for (int d = s.ndim - 1; d >= 0; --d) {
+    int64_t n = s.dim[d];
+    int64_t i = flat % n;
+    flat /= n;
+    off += (i / p.div[d]) * p.stride[d];
+  }
+  return off;
+}
+
+// Value of bfloat16 pattern `b` under format f as the compute dtype sees it.
+// vmap casts a non-bf16 input to bfloat16 for the index and its result back.
+
+// ------------------------------------------------------------ quantize
+// One thread: VEC consecutive elements.
+constexpr int VEC = 8;
+
+__global__ void __launch_bounds__(256)
+k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_param sp, vh_param zp,
+           int cdt, int has_fmt, vh_format f, void* __restrict__ out, int out_dtype) {
+  __shared__ uint16_t lds[2 * VH_MAX_STEPS];
+  if (has_fmt) stage_steps(f, lds);
+  int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (base >= n) return;
+  const bool full = base + VEC <= n;
+  float xv[VEC];
+  if (x_dtype == VH_BF16 && full) {
+    uint4 raw = *(const uint4*)((const uint16_t*)x + base);
+    uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xv[2 * j] = bf2f(w[j] & 0xffffu);
+      xv[2 * j + 1] = bf2f(w[j] >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) xv[j] = (base + j < n) ? load_any(x, x_dtype, base + j) : 0.0f;
+  }
+  float sv = 1.0f, zv = 0.0f;
+  if (sp.ptr && sp.scalar) sv = load_any(sp.ptr, sp.dtype, 0);
+  if (zp.ptr && zp.scalar) zv = load_any(zp.ptr, zp.dtype, 0);
+  uint32_t res[VEC];
+  float outv[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    float s = sv, z = zv;
+    if (sp.ptr && !sp.scalar) s = load_any(sp.ptr, sp.dtype, param_offset(sp, shape, base + j));
+    if (zp.ptr && !zp.scalar) z = load_any(zp.ptr, zp.dtype, param_offset(zp, shape, base + j));
+    float q = xv[j];
+    if (sp.ptr) q = round_to(q / s, cdt);
+    if (zp.ptr) q = round_to(q + z, cdt);
+    if (has_fmt) {
+      uint32_t b = f2bf(q);  // vmap indexes by the bfloat16 pattern
+      if (cdt == VH_BF16) b = __float_as_uint(q) >> 16;  // exact, keeps NaN bits
+      float v = fmt_value(b, f, lds);
+      if (out_dtype == VH_U8) res[j] = fmt_code(b, v, f, lds);
+      outv[j] = v;
+    } else {
+      outv[j] = q;
+    }
+  }
+  if (out_dtype == VH_U8) {
+    uint8_t* o = (uint8_t*)out;
+    if (full) {
+      uint2 pk;
+      pk.x = res[0] | (res[1] << 8) | (res[2] << 16) | (res[3] << 24);
+      pk.y = res[4] | (res[5] << 8) | (res[6] << 16) | (res[7] << 24);
+      *(uint2*)(o + base) = pk;
+    } else {
+      for (int j = 0; j < VEC; ++j)
+        if (base + j < n) o[base + j] = (uint8_t)res[j];
+    }
+  } else if (out_dtype == VH_BF16 && full) {
+    uint4 pk;
+    pk.x = f2bf(outv[0]) | (f2bf(outv[1]) << 16);
+    pk.y = f2bf(outv[2]) | (f2bf(outv[3]) << 16);
+    pk.z = f2bf(outv[4]) | (f2bf(outv[5]) << 16);
+    pk.w = f2bf(outv[6]) | (f2bf(outv[7]) << 16);
+    *(uint4*)((uint16_t*)out + base) = pk;
+  } else {
+    for (int j = 0; j < VEC; ++j)
+      if (base + j < n) store_any(out, out_dtype, base + j, outv[j]);
+  }
+}
+
+static int check_shape(const int64_t* shape, int32_t ndim, Shape* s, int64_t* n) {
+  VH_REQUIRE(ndim >= 0 && ndim <= VH_MAX_DIMS, "tensor rank %d exceeds %d", ndim, VH_MAX_DIMS);
+  int64_t total = 1;
+  s->ndim = ndim > 0 ? ndim : 1;
+  for (int d = 0; d < VH_MAX_DIMS; ++d) s->dim[d] = 1;
+  for (int d = 0; d < ndim; ++d) {
+    VH_REQUIRE(shape[d] >= 0, "negative size");
+    s->dim[d] = shape[d];
+    total *= shape[d];
+  }
+  *n = total;
+  return VH_OK;
+}
+
+static int check_param(const vh_param* p, const Shape& s, const char* name) {
+  if (!p || !p->ptr) return VH_OK;
+  VH_REQUIRE(vh::is_float_dtype(p->dtype), "%s: dtype %d is not a float dtype", name, p->dtype);
+  if (p->scalar) return VH_OK;
+  for (int d = 0; d < s.ndim; ++d) {
+    VH_REQUIRE(p->div[d] >= 1, "%s: divisor of dim %d must be >= 1", name, d);
+    VH_REQUIRE(p->stride[d] >= 0, "%s: negative stride", name);
+  }
+  return VH_OK;
+}
+
+static int check_fmt(const vh_format* f, const char* name) {
+  if (!f) return VH_OK;
+  VH_REQUIRE(f->kind >= VH_FMT_IDENTITY && f->kind <= VH_FMT_LUT, "%s: bad format kind %d", name, f->kind);
+  VH_REQUIRE(f->kind != VH_FMT_STEPS || (f->nsteps >= 0 && f->nsteps < VH_MAX_STEPS),
+             "%s: nsteps out of range", name);
+  VH_REQUIRE(f->kind != VH_FMT_LUT || f->lut, "%s: LUT format without a table", name);
+  return VH_OK;
+}
+
+static vh_param null_param() {
+  vh_param p;
+  memset(&p, 0, sizeof(p));
+  return p;
+}
+
+static bool packable(const vh_format* f) {
+  if (!f) return false;
+  switch (f->kind) {
+    case VH_FMT_INT: return (f->p0 >= -128 && f->p1 <= 127) || (f->p0 >= 0 && f->p1 <= 255);
+    case VH_FMT_MINIFLOAT: return f->p0 + f->p1 + ((f->flags & VH_FMT_SIGNED) ? 1 : 0) <= 8;
+    case VH_FMT_POSIT: return f->p0 <= 8;
+    case VH_FMT_STEPS: return true;
+    default: return false;
+  }
+}
+
+extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                           const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
+                           const vh_format* fmt, void* out, int32_t out_dtype, vh_stream_t stream) {
+  Shape s;
+  int64_t n;
+  int rc;
+  if ((rc = check_shape(shape, ndim, &s, &n))) return rc;
+  VH_REQUIRE(x && out, "vh_quantize: null tensor");
+  VH_REQUIRE(vh::is_float_dtype(x_dtype), "vh_quantize: input dtype %d unsupported", x_dtype);
+  VH_REQUIRE(vh::is_float_dtype(compute_dtype), "vh_quantize: compute dtype %d unsupported", compute_dtype);
+  if ((rc = check_param(scale, s, "scale"))) return rc;
+  if ((rc = check_param(zero_point, s, "zero_point"))) return rc;
+  if ((rc = check_fmt(fmt, "qmap"))) return rc;
+  VH_REQUIRE(out_dtype != VH_U8 || packable(fmt), "vh_quantize: this map has no packed form");
+  VH_REQUIRE(out_dtype == VH_U8 || vh::is_float_dtype(out_dtype), "vh_quantize: bad output dtype");
+  if (n == 0) return VH_OK;
+  vh_param sp = scale ? *scale : null_param();
+  vh_param zp = zero_point ? *zero_point : null_param();
+  vh_format f;
+  memset(&f, 0, sizeof(f));
+  if (fmt) f = *fmt;
+  int64_t threads = (n + VEC - 1) / VEC;
+  int64_t blocks = (threads + 255) / 256;
+  VH_REQUIRE(blocks < (1ll << 31), "vh_quantize: tensor too large");
+  hipLaunchKernelGGL(k_quantize, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), x, x_dtype, n, s, sp,
+                     zp, compute_dtype, fmt ? 1 : 0, f, out, out_dtype);
+  return vh::check_launch("vh_quantize");
+}
+
+// ------------------------------------------------------------ dequantize
+__global__ void __launch_bounds__(256)
+k_dequantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_param sp, vh_param zp, int cdt,
+             int has_in, vh_format fin, int has_out, vh_format fout, void* __restrict__ out, int out_dtype) {
+  __shared__ uint16_t lds_in[2 * VH_MAX_STEPS];
+  __shared__ uint16_t lds_out[2 * VH_MAX_STEPS];
+  if (has_in) stage_steps(fin, lds_in);
+  if (has_out) stage_steps(fout, lds_out);
+  int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (base >= n) return;
+  float sv = 1.0f, zv = 0.0f;
+  if (sp.ptr && sp.scalar) sv = load_any(sp.ptr, sp.dtype, 0);
+  if (zp.ptr && zp.scalar) zv = load_any(zp.ptr, zp.dtype, 0);
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    int64_t i = base + j;
+    if (i >= n) break;
+    float v;
+    if (x_dtype == VH_U8) {
+      v = fmt_decode(((const uint8_t*)x)[i], fin, lds_in);
+    } else {
+      v = load_any(x, x_dtype, i);
+      if (has_in) {
+        uint32_t b = x_dtype == VH_BF16 ? (uint32_t)((const uint16_t*)x)[i] : f2bf(v);
+        v = round_to(fmt_value(b, fin, lds_in), x_dtype);
+      }
+    }
+    float s = sv, z = zv;
+    if (sp.ptr && !sp.scalar) s = load_any(sp.ptr, sp.dtype, param_offset(sp, shape, i));
+    if (zp.ptr && !zp.scalar) z = load_any(zp.ptr, zp.dtype, param_offset(zp, shape, i));
+    if (zp.ptr) v = round_to(v - z, cdt);
+    if (sp.ptr) v = round_to(v * s, cdt);
+    if (has_out) v = round_to(fmt_value(f2bf(v), fout, lds_out), cdt);
+    store_any(out, out_dtype, i, v);
+  }
+}
+
+extern "C" int vh_dequantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                             const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
+                             const vh_format* fmt_in, const vh_format* fmt_out, void* out, int32_t out_dtype,
+                             vh_stream_t stream) {
+  Shape s;
+  int64_t n;
+  int rc;
+  if ((rc = check_shape(shape, ndim, &s, &n))) return rc;
+  VH_REQUIRE(x && out, "vh_dequantize: null tensor");
+  VH_REQUIRE(vh::is_float_dtype(x_dtype) || x_dtype == VH_U8, "vh_dequantize: input dtype %d unsupported",
+             x_dtype);
+  VH_REQUIRE(x_dtype != VH_U8 || packable(fmt_in), "vh_dequantize: packed input needs a packable input map");
+  VH_REQUIRE(vh::is_float_dtype(compute_dtype) && vh::is_float_dtype(out_dtype), "vh_dequantize: bad dtype");
+  if ((rc = check_param(scale, s, "scale"))) return rc;
+  if ((rc = check_param(zero_point, s, "zero_point"))) return rc;
+  if ((rc = check_fmt(fmt_in, "input_qmap"))) return rc;
+  if ((rc = check_fmt(fmt_out, "output_qmap"))) return rc;
+  if (n == 0) return VH_OK;
+  vh_param sp = scale ? *scale : null_param();
+  vh_param zp = zero_point ? *zero_point : null_param();
+  vh_format fi, fo;
+  memset(&fi, 0, sizeof(fi));
+  memset(&fo, 0, sizeof(fo));
+  if (fmt_in) fi = *fmt_in;
+  if (fmt_out) fo = *fmt_out;
+  int64_t threads = (n + VEC - 1) / VEC;
+  int64_t blocks = (threads + 255) / 256;
+  VH_REQUIRE(blocks < (1ll << 31), "vh_dequantize: tensor too large");
+  hipLaunchKernelGGL(k_dequantize, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), x, x_dtype, n, s,
+                     sp, zp, compute_dtype, fmt_in ? 1 : 0, fi, fmt_out ? 1 : 0, fo, out, out_dtype);
+  return vh::check_launch("vh_dequantize");
+}

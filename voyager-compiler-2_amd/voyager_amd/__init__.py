@@ -1,0 +1,10 @@
+"""MI355X-native (gfx950) execution of Voyager's quantized-operator path.
+
+Importing the package registers the ``quantized_ops`` torch.library namespace
+(``voyager_amd.ops``) whose CUDA-key kernels launch the HIP library
+``_lib/libvoyager_hip.so`` through its C ABI (``include/voyager_hip.h``).
+"""
+
+from . import _lib, formats, ops  # noqa: F401  (ops registers the library)
+
+__all__ = ["formats", "ops"]
