@@ -1,0 +1,246 @@
+"""Benchmark of the quantized-operator hot path on one MI355X.
+
+Workload: FP8 E4M3 per-tensor symmetric
+quantization + GEMM at Llama-3.1-8B prefill projection shapes, M = 2048 tokens
+and (K, N) in {(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)}.
+One step runs, for every shape, what a lowered graph runs
+(quantization/quantize_pt2e.py:538-600): quantize the bf16 activations with
+their calibrated scale to E4M3 bytes, then the FP8 GEMM whose epilogue applies
+the dequantize by the bf16 scale product.  Weights are quantized once before
+timing (the reference bakes them at convert).  Inputs are synthetic (seeded
+N(0,1) activations, N(0,0.02) weights) and resident in HBM.
+
+Prints ONE JSON line.  `value` = GEMM TFLOP/s over the whole step (the four
+GEMMs' 2*M*N*K, divided by the step time, which includes the quantize
+kernels).  `roofline` is for the dominant kernel (the fp8 GEMM), timed with
+HIP events on the launch stream; `cpu_baseline` times the CPU oracle (the
+reference's op sequence in eager PyTorch) on a bounded sample.
+
+Options: --gpus N (1 only), --steps K, --warmup W, --no-cpu (skip the CPU
+baseline), --copy-calibration BYTES (run only a plain device copy, for
+rocprofv3 counter calibration).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "voyager-compiler-2_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+M = 2048
+SHAPES = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+METRIC = "quantized GEMM TFLOPS + quantize GB/s, % of MI355X roofline, 1 GPU"
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "fp8_gemm_cfg2_traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(device):
+    """Seeded synthetic inputs generated on the CPU, then copied (so the CPU
+    baseline sees the same values)."""
+    data = []
+    for i, (K, N) in enumerate(SHAPES):
+        g = torch.Generator().manual_seed(100 + i)
+        x = torch.randn(M, K, generator=g).bfloat16()
+        w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+        data.append((x, w))
+    return data
+
+
+def amax_scale(t: torch.Tensor) -> torch.Tensor:
+    """bf16(amax / 448) as the amax observer computes a calibrated scale."""
+    a = torch.amax(torch.abs(t))
+    return (a / 448.0).to(t.dtype) if a > 0 else torch.ones((), dtype=t.dtype, device=t.device)
+
+
+def gpu_bench(args):
+    import voyager_amd  # noqa: F401
+    from voyager_amd import formats, gemm, packed
+
+    dev = torch.device("cuda:0")
+    tab = formats.quantization_map("fp8_e4m3", dev)
+    cpu_data = make_inputs(dev)
+    layers = []
+    for x, w in cpu_data:
+        xd, wd = x.to(dev), w.to(dev)
+        sx, sw = amax_scale(xd), amax_scale(wd)
+        s = (sx * sw).contiguous()
+        wq = packed.quantize_packed(wd, sw, tab)  # baked once
+        xq = torch.empty(xd.shape, dtype=torch.uint8, device=dev)
+        y = torch.empty(M, wd.shape[0], dtype=torch.bfloat16, device=dev)
+        layers.append(dict(x=xd, sx=sx, s=s, wq=wq, xq=xq, y=y, K=xd.shape[1], N=wd.shape[0]))
+        del wd
+    torch.cuda.synchronize()
+
+    from voyager_amd.ops import _elementwise
+    fmt = formats.classify(tab).fmt
+
+    def quantize(L):
+        # quantize(x, s, qmap=e4m3) with one-byte codes, written in place
+        out = _elementwise("quantize", L["x"], L["sx"], None, None, torch.bfloat16, fmt, None, torch.uint8)
+        L["xq"] = out
+
+    def step(timers=None):
+        for i, L in enumerate(layers):
+            if timers is not None:
+                timers[i][0].record()
+            quantize(L)
+            if timers is not None:
+                timers[i][1].record()
+            gemm.linear_fp8(L["xq"], L["wq"], L["s"], out=L["y"])
+            if timers is not None:
+                timers[i][2].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: K whole steps, no per-kernel events (clean wall time).
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    # Per-kernel durations with HIP events on the launch stream.
+    q_ms = [0.0] * len(layers)
+    g_ms = [0.0] * len(layers)
+    reps = max(3, min(args.steps, 20))
+    for _ in range(reps):
+        timers = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in layers]
+        step(timers)
+        torch.cuda.synchronize()
+        for i, t in enumerate(timers):
+            q_ms[i] += t[0].elapsed_time(t[1]) / reps
+            g_ms[i] += t[1].elapsed_time(t[2]) / reps
+
+    flops = [2.0 * M * L["N"] * L["K"] for L in layers]
+    qbytes = [M * L["K"] * 3.0 for L in layers]  # bf16 in + 1-byte codes out
+    total_flops = sum(flops)
+    value = total_flops / (ms_per_step * 1e-3) / 1e12
+    gemm_tflops = total_flops / (sum(g_ms) * 1e-3) / 1e12
+    q_gbs = sum(qbytes) / (sum(q_ms) * 1e-3) / 1e9
+    per_shape = []
+    for i, L in enumerate(layers):
+        per_shape.append({
+            "K": L["K"], "N": L["N"],
+            "gemm_us": round(g_ms[i] * 1e3, 2), "gemm_tflops": round(flops[i] / (g_ms[i] * 1e-3) / 1e12, 1),
+            "quantize_us": round(q_ms[i] * 1e3, 2),
+            "quantize_gbs": round(qbytes[i] / (q_ms[i] * 1e-3) / 1e9, 1),
+        })
+    traffic = None
+    if os.path.exists(PROFILE_TRAFFIC):
+        with open(PROFILE_TRAFFIC) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    res = {
+        "value": value, "ms_per_step": ms_per_step,
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4), "traffic": traffic},
+        "quantize": {"achieved": round(q_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(q_gbs / HBM_PEAK_GBS, 4)},
+        "per_shape": per_shape,
+    }
+    return res, cpu_data
+
+
+def cpu_baseline(cpu_data, budget_s=8.0):
+    """The reference's CPU op sequence (the oracle) on a bounded sample: the
+    (4096, 4096) projection with the first 256 token rows, all host threads."""
+    from oracle import ops as O
+    from oracle import tables as T
+
+    tab = T.quantization_map("fp8_e4m3")
+    ident = T.quantization_map(None)
+    x, w = cpu_data[0]
+    x = x[:256].contiguous()
+    sx = O.per_tensor_scale(x, 448.0)
+    sw = O.per_tensor_scale(w, 448.0)
+    wq = O.quantize(w, sw, qmap=tab)
+    s = sx * sw
+    threads = torch.get_num_threads()
+
+    def run():
+        xq = O.quantize(x, sx, qmap=tab)
+        return O.dequantize(O.linear(xq, wq), s, input_qmap=ident)
+
+    run()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    flops = 2.0 * x.shape[0] * w.shape[0] * w.shape[1]
+    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"oracle quantize+linear+dequantize, M=256 of 2048, K=N=4096, median of {len(times)} runs "
+                      f"({med * 1e3:.1f} ms each), torch CPU threads={threads}"}
+
+
+def copy_calibration(nbytes: int):
+    """A plain device copy of known size, for scaling rocprofv3 byte counters."""
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0").fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "launches": 5}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU design is described in DESIGN.md but not run)", file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
+    res, cpu_data = gpu_bench(args)
+    cpu = None if args.no_cpu else cpu_baseline(cpu_data)
+    line = {
+        "metric": METRIC,
+        "value": round(res["value"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: fp8_e4m3 per-tensor quantize + linear, M=2048, (K,N) in "
+                               "{(4096,4096),(4096,1024),(4096,14336),(14336,4096)}",
+                   "tokens": M, "shapes": SHAPES, "parallelism": "none (1 GPU)"},
+        "roofline": res["roofline"],
+        "quantize": res["quantize"],
+        "per_shape": res["per_shape"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -129,6 +129,54 @@ int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer, int64_t L,
                        const vh_format* scale_fmt, const vh_format* fmt, void* scale_out,
                        void* zp_out, void* codes_out, int32_t codes_dtype, vh_stream_t stream);
 
+
+/* ------------------------------------------------------------------ GEMM
+ * C[M, N] = epilogue(A[M, K] . B[N, K]^T), operands K-contiguous ("xc,kc"),
+ * fp32 accumulation on MFMA.  Replaces the GEMM inside quantized_ops.linear
+ * / matmul (ops/layout.py:231-275) and the decode + GEMM of linear_mx /
+ * matmul_mx (ops/quantized.py:651-805): decoded operands are formed in
+ * registers while tiles are staged, never in HBM. */
+#define OP_BF16 0 /* bfloat16 elements */
+#define OP_FP8 1  /* OCP E4M3 bytes (fp8 MFMA); both operands or neither */
+#define OP_MXI8 2 /* int8 codes * 2**(scale_byte - bias) per `block` elements */
+#define OP_P8 3   /* posit8 codes, decoded through `lut` (256 bf16 entries) */
+
+#define EPI_PLAIN 0       /* v = acc [* scale] [+ bias[n]] rounded to out_dtype */
+#define EPI_ROUND_SCALE 1 /* v = bf16(bf16(acc) * scale): linear then dequantize */
+
+typedef struct vh_epilogue {
+  int32_t mode;
+  int32_t out_dtype;    /* VH_BF16 or VH_F32 */
+  const void* scale;    /* 0-d device scalar (alpha / dequantize scale) or NULL */
+  int32_t scale_dtype;
+  const void* bias;     /* [N] device vector or NULL */
+  int32_t bias_dtype;
+} vh_epilogue;
+
+typedef struct vh_gemm_desc {
+  const void* A;
+  const void* B;
+  void* C;
+  int64_t M, N, K;
+  int64_t lda, ldb; /* row pitch of A / B in bytes */
+  int64_t ldc;      /* row pitch of C in elements */
+  int32_t a_fmt, b_fmt;
+  const void* a_scale; /* OP_MXI8: [M, a_scale_ld] bytes */
+  const void* b_scale; /* OP_MXI8: [N, b_scale_ld] bytes */
+  int64_t a_scale_ld, b_scale_ld;
+  int32_t a_block, b_block;
+  int32_t a_bias, b_bias;
+  const void* lut;     /* OP_P8 decode table */
+  int32_t tile_hint;   /* 0: automatic; 2: 256x128, 3: 128x128, 4: 128x64 */
+  int64_t batch;       /* independent GEMMs (<= 1: one) */
+  int64_t batch_stride_a, batch_stride_b; /* bytes (0: broadcast) */
+  int64_t batch_stride_c;                 /* elements */
+  int64_t batch_stride_a_scale, batch_stride_b_scale; /* bytes */
+  vh_epilogue epi;
+} vh_gemm_desc;
+
+int vh_gemm(const vh_gemm_desc* desc, vh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

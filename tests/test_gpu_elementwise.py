@@ -3,6 +3,7 @@
 import pytest
 import torch
 
+import voyager_amd  # noqa: F401  (registers quantized_ops)
 from helpers import assert_same_bits
 from oracle import ops as O
 from oracle import tables as T
@@ -108,8 +109,8 @@ def test_packed_codes_roundtrip(dtype):
     codes = packed.quantize_packed(x.cuda(), s.cuda(), tab.cuda())
     assert codes.dtype == torch.uint8
     back = packed.unpack_codes(codes, tab.cuda())
-    if dtype == "int8":  # packed int8 holds no NaN: NaN packs as code 0
-        exp = torch.where(torch.isnan(exp), torch.zeros_like(exp), exp)
+    if dtype == "int8":  # packed int8 holds neither NaN nor -0: both pack as code 0
+        exp = torch.where(torch.isnan(exp) | (exp == 0), torch.zeros_like(exp), exp)
     assert_same_bits(back, exp, dtype)
     if dtype == "fp8_e4m3":  # the bytes are OCP E4M3
         ref = exp.float().to(torch.float8_e4m3fn).view(torch.uint8)

@@ -1,0 +1,153 @@
+"""GEMM ops on the GPU against the oracle (1e-2 max-abs-normalized, bf16
+out, fp32 accumulation) and, where cheap, a float64 matmul."""
+
+import pytest
+import torch
+
+import voyager_amd  # noqa: F401  (registers quantized_ops)
+from helpers import assert_same_bits, max_rel_err
+from oracle import ops as O
+from oracle import tables as T
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).bfloat16()
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (100, 70, 136), (256, 512, 1024), (1, 4096, 4096), (333, 129, 72)])
+def test_linear_bf16(M, N, K):
+    x, w = _rand((M, K), 1), _rand((N, K), 2, 0.05)
+    exp = O.linear(x, w)
+    got = torch.ops.quantized_ops.linear(x.cuda(), w.cuda())
+    assert got.dtype == torch.bfloat16
+    assert max_rel_err(got, exp) < TOL
+    ref64 = x.double() @ w.double().T
+    assert max_rel_err(got, ref64) < TOL
+
+
+def test_linear_layouts_bias_and_out_dtype():
+    x, w, b = _rand((48, 96), 3), _rand((80, 96), 4), _rand((80,), 5)
+    for layout, xs, ws in [("xc,kc->xk", x, w), ("xc,ck->xk", x, w.T.contiguous()),
+                           ("cx,ck->xk", x.T.contiguous(), w.T.contiguous()), ("xc,kc->kx", x, w)]:
+        exp = O.linear(xs, ws, b, layout=layout, out_dtype=torch.float32)
+        got = torch.ops.quantized_ops.linear(xs.cuda(), ws.cuda(), b.cuda(), layout=layout, out_dtype=torch.float32)
+        assert got.dtype == torch.float32 and list(got.shape) == list(exp.shape)
+        assert max_rel_err(got, exp) < 1e-5, layout
+
+
+def test_matmul_batched():
+    a, b = _rand((2, 3, 40, 64), 6), _rand((2, 3, 64, 24), 7)
+    exp = O.matmul(a, b)
+    got = torch.ops.quantized_ops.matmul(a.cuda(), b.cuda())
+    assert list(got.shape) == [2, 3, 40, 24]
+    assert max_rel_err(got, exp) < TOL
+    exp = O.matmul(a, b, out_dtype=torch.float32)
+    got = torch.ops.quantized_ops.matmul(a.cuda(), b.cuda(), out_dtype=torch.float32)
+    assert max_rel_err(got, exp) < 1e-5
+
+
+def _cfg1():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(256, 4096, generator=g)
+    x = torch.where(torch.rand(256, 4096, generator=g) < 0.001, x * 20, x).bfloat16()
+    w = (torch.randn(4096, 4096, generator=g) * 0.02).bfloat16()
+    return x, w
+
+
+def test_linear_mx_mxint8_cfg1():
+    """Config 1 end to end through the reference op sequence:
+    quantize_mx(X), quantize_mx(W), linear_mx."""
+    x, w = _cfg1()
+    tab = T.quantization_map("int8")
+    sx, cx = O.quantize_mx(x, tab, [-1], 16, 127.0, True)
+    sw, cw = O.quantize_mx(w, tab, [-1], 16, 127.0, True)
+    exp = O.linear_mx(cx, cw, input_scale=sx, weight_scale=sw, block_size=16)
+    gsx, gcx = torch.ops.quantized_ops.quantize_mx(x.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    gsw, gcw = torch.ops.quantized_ops.quantize_mx(w.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    assert_same_bits(gsx, sx, "x scale")
+    assert_same_bits(gcw, cw, "w codes")
+    got = torch.ops.quantized_ops.linear_mx(gcx, gcw, input_scale=gsx, weight_scale=gsw, block_size=16)
+    assert got.dtype == torch.bfloat16
+    assert max_rel_err(got, exp) < TOL
+    # the packed MX-int8 GEMM (codes + scale bytes decoded in the GEMM)
+    from voyager_amd import gemm, packed
+
+    px = packed.quantize_mx_packed(x.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    pw = packed.quantize_mx_packed(w.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    got2 = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias)
+    assert max_rel_err(got2, exp) < TOL
+    # both GPU paths compute the same exact products; only summation order differs
+    assert max_rel_err(got2, got) < 1e-2
+
+
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("K,N", [(4096, 1024), (14336, 4096)])
+def test_linear_mx_mxnf4_cfg3(M, K, N):
+    vt = T.quantization_map("lut4_to_int6")
+    index, entries, mid = T.codebook_index_table(vt)
+    stab = T.quantization_map("fp8_e5m3")
+    x, w = _rand((M, K), 10), _rand((N, K), 11, 0.02)
+    sx, cx = O.quantize_mx(x, index, [-1], 64, 31.0, False, stab, mid)
+    sw, cw = O.quantize_mx(w, index, [-1], 64, 31.0, False, stab)
+    exp = O.linear_mx(cx, cw, input_scale=sx, weight_scale=sw, block_size=64, input_code=entries,
+                      weight_code=entries)
+    d = "cuda"
+    gsx, gcx = torch.ops.quantized_ops.quantize_mx(x.to(d), index.to(d), [-1], 64, 31.0, False, stab.to(d), mid.to(d))
+    gsw, gcw = torch.ops.quantized_ops.quantize_mx(w.to(d), index.to(d), [-1], 64, 31.0, False, stab.to(d))
+    assert_same_bits(gcw, cw, "w codes")
+    got = torch.ops.quantized_ops.linear_mx(gcx, gcw, input_scale=gsx, weight_scale=gsw, block_size=64,
+                                            input_code=entries.to(d), weight_code=entries.to(d))
+    assert max_rel_err(got, exp) < TOL
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 1024), (2048, 4096, 1024), (130, 384, 200)])
+def test_linear_fp8_per_tensor(M, K, N):
+    """Config 2's path: quantize X and W to E4M3 with amax scales,
+    linear(xq, wq) in bf16, then dequantize by the bf16 scale product."""
+    x, w = _rand((M, K), 20), _rand((N, K), 21, 0.02)
+    tab = T.quantization_map("fp8_e4m3")
+    sx = O.per_tensor_scale(x, 448.0)
+    sw = O.per_tensor_scale(w, 448.0)
+    s = sx * sw  # the scale product is formed in bf16 at convert
+    xq = O.quantize(x, sx, qmap=tab)
+    wq = O.quantize(w, sw, qmap=tab)
+    ident = T.quantization_map(None)
+    exp = O.dequantize(O.linear(xq, wq), s, input_qmap=ident)
+    from voyager_amd import gemm, packed
+
+    d = "cuda"
+    cx = packed.quantize_packed(x.to(d), sx.to(d), tab.to(d))
+    cw = packed.quantize_packed(w.to(d), sw.to(d), tab.to(d))
+    assert torch.equal(cx.cpu(), xq.float().to(torch.float8_e4m3fn).view(torch.uint8))
+    got = gemm.linear_fp8(cx, cw, s.to(d))
+    assert max_rel_err(got, exp) < TOL
+    ref64 = (xq.double() @ wq.double().T) * s.double()
+    assert max_rel_err(got, ref64) < TOL
+    # the reference-form ops give the same answer
+    gq = torch.ops.quantized_ops.quantize(x.to(d), sx.to(d), qmap=tab.to(d))
+    gw = torch.ops.quantized_ops.quantize(w.to(d), sw.to(d), qmap=tab.to(d))
+    got2 = torch.ops.quantized_ops.dequantize(torch.ops.quantized_ops.linear(gq, gw), s.to(d),
+                                              input_qmap=ident.to(d))
+    assert max_rel_err(got2, exp) < TOL
+
+
+def test_linear_posit8():
+    """Config 4's GEMM at a reduced M: posit8-cast operands, bf16 GEMM."""
+    x, w = _rand((256, 4096), 30), _rand((512, 4096), 31, 0.02)
+    tab = T.quantization_map("posit8_1")
+    one = torch.tensor(1.0, dtype=torch.bfloat16)
+    xq, wq = O.quantize(x, one, qmap=tab), O.quantize(w, one, qmap=tab)
+    exp = O.linear(xq, wq)
+    from voyager_amd import gemm, packed
+
+    d = "cuda"
+    cx = packed.quantize_packed(x.to(d), one.to(d), tab.to(d))
+    cw = packed.quantize_packed(w.to(d), one.to(d), tab.to(d))
+    lut = gemm.posit8_lut(tab.to(d))
+    got = gemm.linear_posit8(cx, cw, lut)
+    assert max_rel_err(got, exp) < TOL

@@ -185,8 +185,8 @@ VH_DEV float fmt_value(uint32_t b, const vh_format& f, const uint16_t* lds) {
 // ------------------------------------------------------------ packed codes
 // One byte per element: INT two's complement; MINIFLOAT sign|exponent|
 // mantissa fields (fp8_e4m3 is the OCP E4M3 byte the fp8 MFMA reads);
-// POSIT the posit bit string; STEPS the level index.  Packed int8 cannot
-// hold NaN: a NaN element packs as 0.
+// POSIT the posit bit string; STEPS the level index.  Packed int8 holds
+// neither NaN nor -0: a NaN element packs as 0 and -0 as +0.
 
 VH_DEV uint32_t mini_code(float v, const vh_format& f) {
   const int mb = f.p1;
@@ -293,8 +293,10 @@ VH_DEV float fmt_decode(uint32_t c, const vh_format& f, const uint16_t* lds) {
     case VH_FMT_INT:
       return (f.p0 < 0) ? (float)(int8_t)(uint8_t)c : (float)(uint8_t)c;
     case VH_FMT_MINIFLOAT: {
+      // Codes beyond max_norm are the format's NaN (the map never emits
+      // them for a finite input).
       float v = mini_decode(c, f);
-      return rbf(v > f.max_norm ? f.max_norm : v);
+      return fabsf(v) > f.max_norm ? __uint_as_float(0x7fc00000u) : rbf(v);
     }
     case VH_FMT_POSIT: return rbf(posit_decode(c, f));
     case VH_FMT_STEPS: return bf2f(lds[VH_MAX_STEPS + (c < VH_MAX_STEPS ? c : VH_MAX_STEPS - 1)]);

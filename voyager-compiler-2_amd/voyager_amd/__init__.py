@@ -6,5 +6,6 @@ Importing the package registers the ``quantized_ops`` torch.library namespace
 """
 
 from . import _lib, formats, ops  # noqa: F401  (ops registers the library)
+from . import gemm, packed  # noqa: F401  (gemm registers the GEMM ops)
 
-__all__ = ["formats", "ops"]
+__all__ = ["formats", "gemm", "ops", "packed"]

@@ -103,6 +103,8 @@ _SIGNATURES = {
          _P, _P, _P, _I32, _P],
         _I32,
     ),
+    # vh_gemm takes a vh_gemm_desc*; voyager_amd.gemm.GemmDesc mirrors it.
+    "vh_gemm": ([_P, _P], _I32),
 }
 
 #: Every symbol ``include/voyager_hip.h`` declares.

@@ -1,0 +1,314 @@
+"""GEMM ops: ``quantized_ops.linear`` / ``matmul`` (``ops/layout.py:216-284``)
+and ``linear_mx`` / ``matmul_mx`` (``ops/quantized.py:651-819``) on the HIP
+GEMM core (``vh_gemm``), plus the packed fp8 / MX-int8 / posit8 GEMMs a
+lowered graph runs.
+
+The reference computes every GEMM as an fp32 (or bf16) ``aten`` product of
+decoded operands, rounded once to the output dtype.  Here the product is an
+MFMA GEMM with fp32 accumulation; the epilogue applies ``alpha``, the bias and
+the one rounding.  Results agree with the reference to the accumulation
+order (the parity bar is 1e-2 max-abs-normalized error).
+"""
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib, formats
+from ._lib import VH_BF16, VH_F32, dtype_code, load, stream_of
+from .ops import LINEAR_LAYOUT, MATMUL_LAYOUT, _require_gpu, decode_table, lib
+
+OP_BF16, OP_FP8, OP_MXI8, OP_P8 = 0, 1, 2, 3
+EPI_PLAIN, EPI_ROUND_SCALE = 0, 1
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [
+        ("mode", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+        ("scale", ctypes.c_void_p),
+        ("scale_dtype", ctypes.c_int32),
+        ("bias", ctypes.c_void_p),
+        ("bias_dtype", ctypes.c_int32),
+    ]
+
+
+class GemmDesc(ctypes.Structure):
+    _fields_ = [
+        ("A", ctypes.c_void_p), ("B", ctypes.c_void_p), ("C", ctypes.c_void_p),
+        ("M", ctypes.c_int64), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+        ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
+        ("a_fmt", ctypes.c_int32), ("b_fmt", ctypes.c_int32),
+        ("a_scale", ctypes.c_void_p), ("b_scale", ctypes.c_void_p),
+        ("a_scale_ld", ctypes.c_int64), ("b_scale_ld", ctypes.c_int64),
+        ("a_block", ctypes.c_int32), ("b_block", ctypes.c_int32),
+        ("a_bias", ctypes.c_int32), ("b_bias", ctypes.c_int32),
+        ("lut", ctypes.c_void_p),
+        ("tile_hint", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("batch_stride_a", ctypes.c_int64), ("batch_stride_b", ctypes.c_int64),
+        ("batch_stride_c", ctypes.c_int64),
+        ("batch_stride_a_scale", ctypes.c_int64), ("batch_stride_b_scale", ctypes.c_int64),
+        ("epi", Epilogue),
+    ]
+
+
+def run(desc: GemmDesc, device) -> None:
+    st = load().vh_gemm(ctypes.c_void_p(ctypes.addressof(desc)),
+                        ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+    _lib.check(st, "vh_gemm")
+
+
+def _epilogue(mode, out_dtype, scale=None, bias=None) -> Epilogue:
+    e = Epilogue()
+    e.mode = mode
+    e.out_dtype = dtype_code(out_dtype)
+    if scale is not None:
+        e.scale = scale.data_ptr()
+        e.scale_dtype = dtype_code(scale.dtype)
+    if bias is not None:
+        e.bias = bias.data_ptr()
+        e.bias_dtype = dtype_code(bias.dtype)
+    return e
+
+
+def gemm_bf16(a: torch.Tensor, b: torch.Tensor, out_dtype, bias=None, alpha=None) -> torch.Tensor:
+    """``a[..., M, K] . b[..., N, K]^T`` (bf16 operands, fp32 accumulation),
+    ``* alpha + bias`` in fp32, one rounding to ``out_dtype``."""
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise NotImplementedError(f"GEMM operands must be bfloat16 on the GPU (got {a.dtype}, {b.dtype})")
+    K = a.shape[-1]
+    if b.shape[-1] != K:
+        raise RuntimeError(f"GEMM contraction mismatch: {list(a.shape)} vs {list(b.shape)}")
+    if b.dim() == 2 and a.dim() > 2:  # one GEMM over all leading dims
+        lead = a.shape[:-1]
+        return gemm_bf16(a.reshape(-1, K), b, out_dtype, bias, alpha).view(*lead, b.shape[0])
+    batch_shape = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    M, N = a.shape[-2], b.shape[-2]
+    a3 = a.expand(*batch_shape, M, K).reshape(-1, M, K).contiguous() if a.dim() > 2 else a.contiguous()
+    bb = b.expand(*batch_shape, N, K) if b.dim() > 2 else b
+    b3 = bb.reshape(-1, N, K).contiguous() if bb.dim() > 2 else bb.contiguous()
+    nbat = 1
+    for n in batch_shape:
+        nbat *= n
+    out = torch.empty(*batch_shape, M, N, dtype=out_dtype, device=a.device)
+    if alpha is not None:
+        alpha = alpha.reshape(()).to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+    d = GemmDesc()
+    d.A, d.B, d.C = a3.data_ptr(), b3.data_ptr(), out.data_ptr()
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb, d.ldc = K * 2, K * 2, N
+    d.a_fmt = d.b_fmt = OP_BF16
+    d.batch = nbat
+    d.batch_stride_a = M * K * 2 if a.dim() > 2 else 0
+    d.batch_stride_b = N * K * 2 if bb.dim() > 2 else 0
+    d.batch_stride_c = M * N
+    d.epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
+    run(d, a.device)
+    return out
+
+
+def _parse_layout(layout: str):
+    ops_, out = layout.split("->")
+    act, w = ops_.split(",")
+    if act not in ("xc", "cx") or w not in ("kc", "ck") or out not in ("xk", "kx"):
+        raise AssertionError(layout)
+    return act, w, out
+
+
+def _to_kc(act, w, a, b, native_w):
+    """Operands as [.., M, K] and [.., N, K] from their stored layouts."""
+    if act == "cx":
+        a = a.mT
+    # linear's native weight is kc ([N, K]); matmul's is ck ([K, N])
+    if w == "ck":
+        b = b.mT
+    return a, b
+
+
+def _gemm_in_layout(a, b, layout, out_dtype, bias, native, alpha=None):
+    act, w, out_l = _parse_layout(layout)
+    a, b = _to_kc(act, w, a, b, native)
+    dtype = a.dtype if out_dtype is None else out_dtype
+    if out_dtype is None and bias is not None and bias.dtype != a.dtype:
+        dtype = torch.promote_types(a.dtype, bias.dtype)
+    y = gemm_bf16(a, b, dtype, bias, alpha)
+    return y.mT.contiguous() if out_l != "xk" else y
+
+
+def _linear_cuda(input, weight, bias=None, *, layout=LINEAR_LAYOUT, out_dtype=None):
+    _require_gpu(input, weight, bias)
+    return _gemm_in_layout(input, weight, layout, out_dtype, bias, LINEAR_LAYOUT)
+
+
+def _matmul_cuda(input, other, *, layout=MATMUL_LAYOUT, out_dtype=None):
+    _require_gpu(input, other)
+    return _gemm_in_layout(input, other, layout, out_dtype, None, MATMUL_LAYOUT)
+
+
+lib.impl("linear", _linear_cuda, "CUDA")
+lib.impl("matmul", _matmul_cuda, "CUDA")
+
+
+def _gemm_shape(a, b, layout, bias, out_dtype):
+    act, w, out_l = _parse_layout(layout)
+    if act == "cx":
+        a = a.mT
+    if w == "ck":
+        b = b.mT
+    batch = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2]) if (a.dim() > 2 or b.dim() > 2) else ()
+    shape = [*batch, a.shape[-2], b.shape[-2]]
+    if out_l == "kx":
+        shape[-2], shape[-1] = shape[-1], shape[-2]
+    dtype = a.dtype if out_dtype is None else out_dtype
+    return shape, dtype
+
+
+@torch.library.register_fake("quantized_ops::linear")
+def _linear_fake(input, weight, bias=None, *, layout=LINEAR_LAYOUT, out_dtype=None):
+    shape, dtype = _gemm_shape(input, weight, layout, bias, out_dtype)
+    return input.new_empty(shape, dtype=dtype)
+
+
+@torch.library.register_fake("quantized_ops::matmul")
+def _matmul_fake(input, other, *, layout=MATMUL_LAYOUT, out_dtype=None):
+    shape, dtype = _gemm_shape(input, other, layout, None, out_dtype)
+    return input.new_empty(shape, dtype=dtype)
+
+
+# ----------------------------------------------------------------- *_mx
+def _decode(x, scale, code, block_size):
+    """``_dequantize_mx`` (``ops/quantized.py:574-591``) on the GPU."""
+    if code is None and scale is None:
+        return x
+    if scale is None:
+        return torch.ops.quantized_ops.vmap(x, decode_table(code)) if code is not None else x
+    return torch.ops.quantized_ops.dequantize_mx(x, scale, block_size, code)
+
+
+def _mx_common(kind, x, w, bias, input_scale, weight_scale, block_size, input_code, weight_code, alpha, A_data,
+               layout, out_dtype):
+    _require_gpu(x, w, bias, input_scale, weight_scale, input_code, weight_code, alpha)
+    if A_data is not None:
+        raise NotImplementedError(f"quantized_ops.{kind}: the outlier (CSR) term is not supported on the GPU yet")
+    xd = _decode(x, input_scale, input_code, block_size)
+    wd = _decode(w, weight_scale, weight_code, block_size)
+    dtype = xd.dtype if out_dtype is None else out_dtype
+    act, wl, out_l = _parse_layout(layout)
+    a, b = _to_kc(act, wl, xd, wd, None)
+    acc_bias = bias if kind == "linear_mx" else None
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise NotImplementedError(f"quantized_ops.{kind}: decoded operands must be bfloat16 on the GPU")
+    y = gemm_bf16(a, b, dtype, acc_bias, alpha)
+    return y.mT.contiguous() if out_l != "xk" else y
+
+
+def _linear_mx_cuda(input, weight, bias=None, *, input_scale=None, weight_scale=None, block_size=None,
+                    input_code=None, weight_code=None, alpha=None, A_data=None, A_indices=None, A_indptr=None,
+                    layout=LINEAR_LAYOUT, out_dtype=None):
+    return _mx_common("linear_mx", input, weight, bias, input_scale, weight_scale, block_size, input_code,
+                      weight_code, alpha, A_data, layout, out_dtype)
+
+
+def _matmul_mx_cuda(self, other, *, input_scale=None, weight_scale=None, block_size=None, input_code=None,
+                    weight_code=None, alpha=None, A_data=None, A_indices=None, A_indptr=None,
+                    layout=MATMUL_LAYOUT, out_dtype=None):
+    return _mx_common("matmul_mx", self, other, None, input_scale, weight_scale, block_size, input_code,
+                      weight_code, alpha, A_data, layout, out_dtype)
+
+
+lib.impl("linear_mx", _linear_mx_cuda, "CUDA")
+lib.impl("matmul_mx", _matmul_mx_cuda, "CUDA")
+
+
+@torch.library.register_fake("quantized_ops::linear_mx")
+def _linear_mx_fake(input, weight, bias=None, **kwargs):
+    shape, dtype = _gemm_shape(input, weight, kwargs.get("layout", LINEAR_LAYOUT), bias, kwargs.get("out_dtype"))
+    return input.new_empty(shape, dtype=dtype)
+
+
+@torch.library.register_fake("quantized_ops::matmul_mx")
+def _matmul_mx_fake(self, other, **kwargs):
+    shape, dtype = _gemm_shape(self, other, kwargs.get("layout", MATMUL_LAYOUT), None, kwargs.get("out_dtype"))
+    return self.new_empty(shape, dtype=dtype)
+
+
+# ----------------------------------------------------------------- packed GEMMs
+def linear_fp8(xq: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor, out: Optional[torch.Tensor] = None,
+               tile_hint: int = 0) -> torch.Tensor:
+    """Per-tensor FP8 linear as a lowered graph runs it: ``dequantize(linear(
+    xq, wq), s)`` (``quantization/quantize_pt2e.py:538-600``) with E4M3 bytes
+    ``xq`` [M, K] and ``wq`` [N, K] and the bf16 scale product ``s``: the fp32
+    accumulator is rounded to bf16, multiplied by ``s`` and rounded again."""
+    M, K = xq.shape
+    N = wq.shape[0]
+    if wq.shape[1] != K:
+        raise RuntimeError("linear_fp8: contraction mismatch")
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=xq.device)
+    d = GemmDesc()
+    d.A, d.B, d.C = xq.data_ptr(), wq.data_ptr(), out.data_ptr()
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb, d.ldc = xq.stride(0), wq.stride(0), out.stride(0)
+    d.a_fmt = d.b_fmt = OP_FP8
+    d.tile_hint = tile_hint
+    d.epi = _epilogue(EPI_ROUND_SCALE, torch.bfloat16, scale)
+    run(d, xq.device)
+    return out
+
+
+def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: int, bias_w: int,
+                  out_dtype=torch.bfloat16, bias=None, alpha=None, tile_hint: int = 0) -> torch.Tensor:
+    """MX-int8 ``linear_mx`` on packed operands: int8 codes with biased
+    power-of-two scale bytes, decoded exactly to bf16 in the GEMM's staging."""
+    M, K = x_codes.shape
+    N = w_codes.shape[0]
+    out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
+    if alpha is not None:
+        alpha = alpha.reshape(()).to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+    d = GemmDesc()
+    d.A, d.B, d.C = x_codes.data_ptr(), w_codes.data_ptr(), out.data_ptr()
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb, d.ldc = x_codes.stride(0), w_codes.stride(0), N
+    d.a_fmt = d.b_fmt = OP_MXI8
+    d.a_scale, d.b_scale = x_scale.data_ptr(), w_scale.data_ptr()
+    d.a_scale_ld, d.b_scale_ld = x_scale.stride(0), w_scale.stride(0)
+    d.a_block = d.b_block = block_size
+    d.a_bias, d.b_bias = bias_x, bias_w
+    d.tile_hint = tile_hint
+    d.epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
+    run(d, x_codes.device)
+    return out
+
+
+def posit8_lut(qmap: torch.Tensor) -> torch.Tensor:
+    """256-entry bf16 decode table of posit8 packed codes (code -> entry)."""
+    c = formats.classify(qmap)
+    codes = torch.arange(256, dtype=torch.uint8, device=qmap.device)
+    from .ops import _elementwise
+
+    return _elementwise("dequantize", codes, None, None, None, torch.bfloat16, c.fmt, None, torch.bfloat16)
+
+
+def linear_posit8(x_codes, w_codes, lut: torch.Tensor, out_dtype=torch.bfloat16, tile_hint: int = 0):
+    """Posit8 ``linear`` on packed codes (``quantize_pt2e.py:557-561``: a
+    direct cast, the GEMM reads posit values as bf16): each code is decoded
+    through ``lut`` while staging, then bf16 MFMA, one rounding at the end."""
+    M, K = x_codes.shape
+    N = w_codes.shape[0]
+    out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
+    d = GemmDesc()
+    d.A, d.B, d.C = x_codes.data_ptr(), w_codes.data_ptr(), out.data_ptr()
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb, d.ldc = x_codes.stride(0), w_codes.stride(0), N
+    d.a_fmt = d.b_fmt = OP_P8
+    d.lut = lut.data_ptr()
+    d.tile_hint = tile_hint
+    d.epi = _epilogue(EPI_PLAIN, out_dtype)
+    run(d, x_codes.device)
+    return out
