@@ -47,6 +47,7 @@ typedef struct ihipStream_t* vh_stream_t; /* == hipStream_t */
 #define VH_FMT_LUT 5      /* anything else: gathered from `lut` */
 
 #define VH_FMT_SIGNED 1
+#define VH_FMT_HW_E4M3 2 /* MINIFLOAT e4m3 (max 448) on the OCP fp8 converter */
 
 #define VH_MAX_STEPS 64
 

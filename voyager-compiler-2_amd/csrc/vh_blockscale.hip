@@ -100,9 +100,9 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
     return r;
   }
   if (P.mode == MX_SCALED) {
-    float s = round_to(hi / P.quant_max, cdt);
+    float s = div_round(hi, P.quant_max, cdt);
     const float gs = P.gs ? round_to(load_x(P.gs, P.gs_dtype, 0), cdt) : 1.0f;
-    if (P.gs) s = round_to(s / gs, cdt);
+    if (P.gs) s = div_round(s, gs, cdt);
     uint32_t sb = 0;
     if (P.has_sfmt) {
       sb = f2bf(s);
@@ -118,13 +118,13 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
     return r;
   }
   // AFFINE (ops/quantized.py:1262-1281)
-  float s = round_to(round_to(hi - lo, cdt) / (P.quant_max - P.quant_min), cdt);
+  float s = div_round(round_to(hi - lo, cdt), P.quant_max - P.quant_min, cdt);
   if (!(s > 0.0f)) s = 1.0f;
   if (P.has_sfmt) {
     s = vmap1(s, P.sfmt, slds, cdt);
     if (!(s > 0.0f)) s = 1.0f;
   }
-  float zp = round_to(round_to(-lo / s, cdt) + P.quant_min, cdt);
+  float zp = round_to(div_round(-lo, s, cdt) + P.quant_min, cdt);
   if (P.has_sfmt) zp = vmap1(zp, P.sfmt, slds, cdt);
   r.scale = s;
   r.el_scale = s;
@@ -133,24 +133,24 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
 }
 
 // One element's reference-form code value and packed byte.
+template <int KIND>
 VH_DEV void element_code(float x, const BlockScale& bs, const Params& P, const uint16_t* lds, float* v,
                          uint32_t* code) {
-  float q = round_to(x / bs.el_scale, P.cdt);
+  float q = div_round(x, bs.el_scale, P.cdt);
   if (P.mode == AFFINE) q = round_to(q + bs.zp, P.cdt);
-  uint32_t b = f2bf(q);
-  if (P.cdt == VH_BF16 && !isnan_f(q)) b = __float_as_uint(q) >> 16;
-  float val = fmt_value(b, P.fmt, lds);
+  const uint32_t b = (P.cdt == VH_BF16 && !isnan_f(q)) ? (__float_as_uint(q) >> 16) : f2bf(q);
+  const float val = fmt_value_k<KIND>(b, P.fmt, lds);
   *v = round_to(val, P.cdt);
-  if (P.codes_dtype == VH_U8) *code = fmt_code(b, val, P.fmt, lds);
+  *code = fmt_code_k<KIND>(b, val, P.fmt, lds);
 }
 
-template <int VEC>
+template <int VEC, int KIND>
 __global__ void __launch_bounds__(256)
 k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, Params P,
        void* __restrict__ scale_out, void* __restrict__ zp_out, void* __restrict__ codes_out) {
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
   __shared__ uint16_t slds[2 * VH_MAX_STEPS];
-  if (P.has_fmt) stage_steps(P.fmt, lds);
+  if constexpr (KIND == K_STEPS) stage_steps(P.fmt, lds);
   if (P.has_sfmt) stage_steps(P.sfmt, slds);
   const int64_t tpr = nblk * g;  // threads per row
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -204,11 +204,12 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
     else store_f(scale_out, P.cdt, si, bs.scale);
     if (P.mode == AFFINE) store_f(zp_out, P.cdt, si, bs.zp);
   }
+  if constexpr (KIND == K_NONE) return;
   if (!live || !codes_out) return;
   float cv[VEC];
   uint32_t cc[VEC];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) element_code(xv[j], bs, P, lds, &cv[j], &cc[j]);
+  for (int j = 0; j < VEC; ++j) element_code<KIND>(xv[j], bs, P, lds, &cv[j], &cc[j]);
   if (P.codes_dtype == VH_U8) {
     uint2 pk;
     pk.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
@@ -228,12 +229,13 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
 }
 
 // One thread per (outer, block, inner) column.
+template <int KIND>
 __global__ void __launch_bounds__(256)
 k_cols(const void* __restrict__ x, int64_t outer, int64_t L, int64_t inner, int64_t block, int64_t nblk, Params P,
        void* __restrict__ scale_out, void* __restrict__ zp_out, void* __restrict__ codes_out) {
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
   __shared__ uint16_t slds[2 * VH_MAX_STEPS];
-  if (P.has_fmt) stage_steps(P.fmt, lds);
+  if constexpr (KIND == K_STEPS) stage_steps(P.fmt, lds);
   if (P.has_sfmt) stage_steps(P.sfmt, slds);
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = outer * nblk * inner;
@@ -270,12 +272,13 @@ k_cols(const void* __restrict__ x, int64_t outer, int64_t L, int64_t inner, int6
   if (P.scale_dtype == VH_U8) ((uint8_t*)scale_out)[si] = (uint8_t)bs.packed;
   else store_f(scale_out, P.cdt, si, bs.scale);
   if (P.mode == AFFINE) store_f(zp_out, P.cdt, si, bs.zp);
+  if constexpr (KIND == K_NONE) return;
   if (!codes_out) return;
   for (int64_t l = l0; l < l1; ++l) {
     int64_t i = base + l * inner;
     float cv;
     uint32_t cc;
-    element_code(load_x(x, P.cdt, i), bs, P, lds, &cv, &cc);
+    element_code<KIND>(load_x(x, P.cdt, i), bs, P, lds, &cv, &cc);
     if (P.codes_dtype == VH_U8) ((uint8_t*)codes_out)[i] = (uint8_t)cc;
     else store_f(codes_out, P.cdt, i, cv);
   }
@@ -291,14 +294,22 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
     const int64_t threads = outer * nblk * g;
     const int64_t blocks = (threads + 255) / 256;
     VH_REQUIRE(blocks < (1ll << 31), "%s: tensor too large", what);
-    hipLaunchKernelGGL(k_rows<8>, dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P, scale_out,
-                       zp_out, codes_out);
+    dispatch_kind(P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE, [&](auto kind) {
+      constexpr int K = decltype(kind)::value;
+      hipLaunchKernelGGL((k_rows<8, K>), dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P,
+                         scale_out, zp_out, codes_out);
+      return 0;
+    });
   } else {
     const int64_t threads = outer * nblk * inner;
     const int64_t blocks = (threads + 255) / 256;
     VH_REQUIRE(blocks < (1ll << 31), "%s: tensor too large", what);
-    hipLaunchKernelGGL(k_cols, dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, inner, block, nblk, P,
-                       scale_out, zp_out, codes_out);
+    dispatch_kind(P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE, [&](auto kind) {
+      constexpr int K = decltype(kind)::value;
+      hipLaunchKernelGGL(k_cols<K>, dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, inner, block, nblk, P,
+                         scale_out, zp_out, codes_out);
+      return 0;
+    });
   }
   return vh::check_launch(what);
 }

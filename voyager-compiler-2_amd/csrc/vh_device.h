@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/voyager_hip.h"
 
 #define VH_DEV static __device__ __forceinline__
@@ -42,6 +44,28 @@ VH_DEV float round_to(float f, int dtype) {
 
 VH_DEV bool isnan_f(float f) { return f != f; }
 
+// RNE_bf16(RN_f32(x / s)), the result of an eager bfloat16 division.
+// x * rcp(s) is within 3 float32 ulps of RN_f32(x / s) when s and 1/s are
+// normal (rcp is accurate to 1 ulp), so unless that product lies within 4
+// ulps of a bfloat16 rounding midpoint (low 16 bits near 0x8000) both round
+// to the same bfloat16; the rare remainder takes the correctly rounded
+// division.  Zeros, infinities and NaNs take the fast path and agree.
+VH_DEV float div_bf16(float x, float s) {
+  const float as = fabsf(s);
+  if (as >= 0x1p-126f && as <= 0x1p126f) {
+    const float q = x * __builtin_amdgcn_rcpf(s);
+    const uint32_t u = __float_as_uint(q);
+    if (((u - 0x7FFCu) & 0xFFFFu) > 8u) return bf2f(f2bf(q));
+  }
+  return bf2f(f2bf(x / s));
+}
+
+// The eager result dtype's rounding of x / s.
+VH_DEV float div_round(float x, float s, int dtype) {
+  if (dtype == VH_BF16) return div_bf16(x, s);
+  return round_to(x / s, dtype);
+}
+
 // floor(log2(|a|)) of a finite nonzero float32, subnormals included.
 VH_DEV int floor_log2(float a) {
   uint32_t u = __float_as_uint(a) & 0x7fffffffu;
@@ -70,8 +94,28 @@ VH_DEV float fmt_int(float x, const vh_format& f) {
 // grid of p1 mantissa bits with subnormals below exponent emin, then clamp to
 // max_norm (fake_quantize.py:98-111 with dtypes/fp8.py:69-135).  A zero
 // input gives +0; a nonzero input that rounds to zero keeps its sign.
+// OCP E4M3 (max 448) on the hardware converter, which rounds half to even
+// with subnormals; zero maps to +0 like the table.  Returns the fp8 byte.
+VH_DEV uint32_t e4m3_hw_code(float x) {
+  if (x == 0.0f) return 0u;
+  const float c = isnan_f(x) ? x : fminf(fmaxf(x, -448.0f), 448.0f);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, c, 0, false) & 0xffu;
+}
+
+VH_DEV float e4m3_hw_value(float x) {
+  if (isnan_f(x)) return x;
+  return __builtin_amdgcn_cvt_f32_fp8((int)e4m3_hw_code(x), 0);
+}
+
+// The E4M3 byte of a value already on the grid (a table entry): exact, with
+// the sign of zero kept.
+VH_DEV uint32_t e4m3_encode(float v) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xffu;
+}
+
 VH_DEV float fmt_minifloat(float x, const vh_format& f) {
   if (isnan_f(x)) return x;
+  if (f.flags & VH_FMT_HW_E4M3) return e4m3_hw_value(x);
   if (!(f.flags & VH_FMT_SIGNED)) x = fabsf(x);
   float cm = f.clamp_bf16;
   x = x < -cm ? -cm : (x > cm ? cm : x);
@@ -162,23 +206,58 @@ VH_DEV void stage_steps(const vh_format& f, uint16_t* lds) {
 
 VH_DEV bool bf_isnan_bits(uint32_t b) { return (b & 0x7fffu) > 0x7f80u; }
 
+// Kernels are specialised on the format kind (K_* below) so each instance
+// holds only its own closed form; the runtime-dispatch versions serve the
+// per-block scale maps.
+enum {
+  K_IDENTITY = VH_FMT_IDENTITY,
+  K_INT = VH_FMT_INT,
+  K_MINI = VH_FMT_MINIFLOAT,
+  K_POSIT = VH_FMT_POSIT,
+  K_STEPS = VH_FMT_STEPS,
+  K_LUT = VH_FMT_LUT,
+  K_E4M3 = 6,  // VH_FMT_MINIFLOAT with VH_FMT_HW_E4M3
+  K_NONE = 7,  // no map
+};
+
+static inline int kernel_kind(const vh_format* f) {
+  if (!f) return K_NONE;
+  if (f->kind == VH_FMT_MINIFLOAT && (f->flags & VH_FMT_HW_E4M3)) return K_E4M3;
+  return f->kind;
+}
+
 // Apply a format to a bfloat16 input; returns the table entry's value as
 // float32 (bfloat16 entries are exact in float32; index tables are small
-// integers).  VH_FMT_LUT tables are gathered from device memory.
+// integers).  K_LUT tables are gathered from device memory.
+template <int KIND>
+VH_DEV float fmt_value_k(uint32_t b, const vh_format& f, const uint16_t* lds) {
+  const float x = bf2f(b);
+  if constexpr (KIND == K_IDENTITY || KIND == K_NONE) {
+    return x;
+  } else if constexpr (KIND == K_INT) {
+    return fmt_int(x, f);
+  } else if constexpr (KIND == K_E4M3) {
+    return e4m3_hw_value(x);
+  } else if constexpr (KIND == K_MINI) {
+    return rbf(fmt_minifloat(x, f));
+  } else if constexpr (KIND == K_POSIT) {
+    return rbf(fmt_posit(x, f));
+  } else if constexpr (KIND == K_STEPS) {
+    if (bf_isnan_bits(b)) return bf2f(f.nan_out);
+    return bf2f(lds[VH_MAX_STEPS + steps_level(b, f.nsteps, lds)]);
+  } else {
+    return bf2f(((const uint16_t*)f.lut)[b & 0xffffu]);
+  }
+}
+
 VH_DEV float fmt_value(uint32_t b, const vh_format& f, const uint16_t* lds) {
-  float x = bf2f(b);
   switch (f.kind) {
-    case VH_FMT_IDENTITY: return x;
-    case VH_FMT_INT: return fmt_int(x, f);
-    case VH_FMT_MINIFLOAT: return rbf(fmt_minifloat(x, f));
-    case VH_FMT_POSIT: return rbf(fmt_posit(x, f));
-    case VH_FMT_STEPS:
-      if (bf_isnan_bits(b)) return bf2f(f.nan_out);
-      return bf2f(lds[VH_MAX_STEPS + steps_level(b, f.nsteps, lds)]);
-    default: {  // VH_FMT_LUT: bf16 bit table
-      const uint16_t* t = (const uint16_t*)f.lut;
-      return bf2f(t[b & 0xffffu]);
-    }
+    case VH_FMT_IDENTITY: return fmt_value_k<K_IDENTITY>(b, f, lds);
+    case VH_FMT_INT: return fmt_value_k<K_INT>(b, f, lds);
+    case VH_FMT_MINIFLOAT: return fmt_value_k<K_MINI>(b, f, lds);
+    case VH_FMT_POSIT: return fmt_value_k<K_POSIT>(b, f, lds);
+    case VH_FMT_STEPS: return fmt_value_k<K_STEPS>(b, f, lds);
+    default: return fmt_value_k<K_LUT>(b, f, lds);
   }
 }
 
@@ -189,6 +268,7 @@ VH_DEV float fmt_value(uint32_t b, const vh_format& f, const uint16_t* lds) {
 // neither NaN nor -0: a NaN element packs as 0 and -0 as +0.
 
 VH_DEV uint32_t mini_code(float v, const vh_format& f) {
+  if (f.flags & VH_FMT_HW_E4M3) return e4m3_encode(v);
   const int mb = f.p1;
   uint32_t sign = 0;
   if ((f.flags & VH_FMT_SIGNED) && (__float_as_uint(v) >> 31)) sign = 1u << (f.p0 + mb);
@@ -275,31 +355,79 @@ VH_DEV float posit_decode(uint32_t c, const vh_format& f) {
 }
 
 // Packed code of an element whose table value is v (bits b of the input).
+template <int KIND>
+VH_DEV uint32_t fmt_code_k(uint32_t b, float v, const vh_format& f, const uint16_t* lds) {
+  if constexpr (KIND == K_INT) {
+    return isnan_f(v) ? 0u : ((uint32_t)(int32_t)v & 0xffu);
+  } else if constexpr (KIND == K_E4M3) {
+    return e4m3_encode(v);
+  } else if constexpr (KIND == K_MINI) {
+    return mini_code(v, f) & 0xffu;
+  } else if constexpr (KIND == K_POSIT) {
+    return posit_code(v, f) & 0xffu;
+  } else if constexpr (KIND == K_STEPS) {
+    if (bf_isnan_bits(b)) return (uint32_t)f.nan_level;
+    return steps_level(b, f.nsteps, lds);
+  } else {
+    return 0u;
+  }
+}
+
 VH_DEV uint32_t fmt_code(uint32_t b, float v, const vh_format& f, const uint16_t* lds) {
   switch (f.kind) {
-    case VH_FMT_INT: return isnan_f(v) ? 0u : ((uint32_t)(int32_t)v & 0xffu);
-    case VH_FMT_MINIFLOAT: return mini_code(v, f) & 0xffu;
-    case VH_FMT_POSIT: return posit_code(v, f) & 0xffu;
-    case VH_FMT_STEPS:
-      if (bf_isnan_bits(b)) return (uint32_t)f.nan_level;
-      return steps_level(b, f.nsteps, lds);
+    case VH_FMT_INT: return fmt_code_k<K_INT>(b, v, f, lds);
+    case VH_FMT_MINIFLOAT: return fmt_code_k<K_MINI>(b, v, f, lds);
+    case VH_FMT_POSIT: return fmt_code_k<K_POSIT>(b, v, f, lds);
+    case VH_FMT_STEPS: return fmt_code_k<K_STEPS>(b, v, f, lds);
     default: return 0u;
   }
 }
 
 // The reference-form value of a packed code (the table entry, as float32).
+template <int KIND>
+VH_DEV float fmt_decode_k(uint32_t c, const vh_format& f, const uint16_t* lds) {
+  if constexpr (KIND == K_INT) {
+    return (f.p0 < 0) ? (float)(int8_t)(uint8_t)c : (float)(uint8_t)c;
+  } else if constexpr (KIND == K_E4M3) {
+    return rbf(__builtin_amdgcn_cvt_f32_fp8((int)c, 0));
+  } else if constexpr (KIND == K_MINI) {
+    // Codes beyond max_norm are the format's NaN (the map never emits
+    // them for a finite input).
+    float v = mini_decode(c, f);
+    return fabsf(v) > f.max_norm ? __uint_as_float(0x7fc00000u) : rbf(v);
+  } else if constexpr (KIND == K_POSIT) {
+    return rbf(posit_decode(c, f));
+  } else if constexpr (KIND == K_STEPS) {
+    return bf2f(lds[VH_MAX_STEPS + (c < VH_MAX_STEPS ? c : VH_MAX_STEPS - 1)]);
+  } else {
+    return 0.0f;
+  }
+}
+
 VH_DEV float fmt_decode(uint32_t c, const vh_format& f, const uint16_t* lds) {
   switch (f.kind) {
-    case VH_FMT_INT:
-      return (f.p0 < 0) ? (float)(int8_t)(uint8_t)c : (float)(uint8_t)c;
-    case VH_FMT_MINIFLOAT: {
-      // Codes beyond max_norm are the format's NaN (the map never emits
-      // them for a finite input).
-      float v = mini_decode(c, f);
-      return fabsf(v) > f.max_norm ? __uint_as_float(0x7fc00000u) : rbf(v);
-    }
-    case VH_FMT_POSIT: return rbf(posit_decode(c, f));
-    case VH_FMT_STEPS: return bf2f(lds[VH_MAX_STEPS + (c < VH_MAX_STEPS ? c : VH_MAX_STEPS - 1)]);
+    case VH_FMT_INT: return fmt_decode_k<K_INT>(c, f, lds);
+    case VH_FMT_MINIFLOAT:
+      if (f.flags & VH_FMT_HW_E4M3) return fmt_decode_k<K_E4M3>(c, f, lds);
+      return fmt_decode_k<K_MINI>(c, f, lds);
+    case VH_FMT_POSIT: return fmt_decode_k<K_POSIT>(c, f, lds);
+    case VH_FMT_STEPS: return fmt_decode_k<K_STEPS>(c, f, lds);
     default: return 0.0f;
+  }
+}
+
+// Dispatch a kernel template on a format's kind: F is called with an
+// integral-constant kind.
+template <typename F>
+static inline int dispatch_kind(int kind, F&& fn) {
+  switch (kind) {
+    case K_IDENTITY: return fn(std::integral_constant<int, K_IDENTITY>{});
+    case K_INT: return fn(std::integral_constant<int, K_INT>{});
+    case K_MINI: return fn(std::integral_constant<int, K_MINI>{});
+    case K_POSIT: return fn(std::integral_constant<int, K_POSIT>{});
+    case K_STEPS: return fn(std::integral_constant<int, K_STEPS>{});
+    case K_LUT: return fn(std::integral_constant<int, K_LUT>{});
+    case K_E4M3: return fn(std::integral_constant<int, K_E4M3>{});
+    default: return fn(std::integral_constant<int, K_NONE>{});
   }
 }

@@ -44,18 +44,21 @@ extern "C" const char* vh_last_error(void) { return vh::g_error.c_str(); }
 extern "C" int vh_abi_version(void) { return 1; }
 
 // ------------------------------------------------------------ table rebuild
+// Rebuilds a table with the same specialised closed form the quantize
+// kernels run, so a table that passes verification is what they compute.
+template <int KIND>
 __global__ void __launch_bounds__(256) k_build_table(vh_format f, uint16_t* out) {
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
   stage_steps(f, lds);
   uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= 65536u) return;
-  float v = fmt_value(b, f, lds);
-  if (f.kind == VH_FMT_IDENTITY || f.kind == VH_FMT_LUT) {
-    // Entries that are not values of a closed form are copied bit for bit.
-    out[b] = f.kind == VH_FMT_IDENTITY ? (uint16_t)b : ((const uint16_t*)f.lut)[b];
-    return;
+  if constexpr (KIND == K_IDENTITY) {
+    out[b] = (uint16_t)b;  // bit for bit, NaN payloads included
+  } else if constexpr (KIND == K_LUT) {
+    out[b] = ((const uint16_t*)f.lut)[b];
+  } else {
+    out[b] = (uint16_t)f2bf(fmt_value_k<KIND>(b, f, lds));
   }
-  out[b] = (uint16_t)f2bf(v);
 }
 
 extern "C" int vh_build_table(const vh_format* fmt, uint16_t* out, vh_stream_t stream) {
@@ -63,8 +66,16 @@ extern "C" int vh_build_table(const vh_format* fmt, uint16_t* out, vh_stream_t s
   VH_REQUIRE(fmt->kind >= VH_FMT_IDENTITY && fmt->kind <= VH_FMT_LUT, "vh_build_table: bad kind %d", fmt->kind);
   VH_REQUIRE(fmt->kind != VH_FMT_STEPS || (fmt->nsteps >= 0 && fmt->nsteps < VH_MAX_STEPS),
              "vh_build_table: nsteps %d out of range", fmt->nsteps);
-  hipLaunchKernelGGL(k_build_table, dim3(256), dim3(256), 0, vh::as_stream(stream), *fmt, out);
-  return vh::check_launch("vh_build_table");
+  hipStream_t st = vh::as_stream(stream);
+  return dispatch_kind(kernel_kind(fmt), [&](auto kind) {
+    constexpr int K = decltype(kind)::value;
+    if constexpr (K == K_NONE) {
+      return (int)VH_EINVAL;
+    } else {
+      hipLaunchKernelGGL(k_build_table<K>, dim3(256), dim3(256), 0, st, *fmt, out);
+      return vh::check_launch("vh_build_table");
+    }
+  });
 }
 
 // ------------------------------------------------------------ param access
@@ -110,11 +121,12 @@ VH_DEV int64_t param_offset(const vh_param& p, const Shape& s, int64_t flat) {
 // One thread: VEC consecutive elements.
 constexpr int VEC = 8;
 
+template <int KIND>
 __global__ void __launch_bounds__(256)
 k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_param sp, vh_param zp,
-           int cdt, int has_fmt, vh_format f, void* __restrict__ out, int out_dtype) {
+           int cdt, vh_format f, void* __restrict__ out, int out_dtype) {
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
-  if (has_fmt) stage_steps(f, lds);
+  if constexpr (KIND == K_STEPS) stage_steps(f, lds);
   int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
   if (base >= n) return;
   const bool full = base + VEC <= n;
@@ -128,29 +140,40 @@ k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_p
       xv[2 * j + 1] = bf2f(w[j] >> 16);
     }
   } else {
-#pragma unroll
     for (int j = 0; j < VEC; ++j) xv[j] = (base + j < n) ? load_any(x, x_dtype, base + j) : 0.0f;
   }
-  float sv = 1.0f, zv = 0.0f;
-  if (sp.ptr && sp.scalar) sv = load_any(sp.ptr, sp.dtype, 0);
-  if (zp.ptr && zp.scalar) zv = load_any(zp.ptr, zp.dtype, 0);
+  // Per-element parameters: one value, or indexed (a loop, kept out of the
+  // unrolled element code).
+  float sv[VEC], zv[VEC];
+  const float s0 = (sp.ptr && sp.scalar) ? load_any(sp.ptr, sp.dtype, 0) : 1.0f;
+  const float z0 = (zp.ptr && zp.scalar) ? load_any(zp.ptr, zp.dtype, 0) : 0.0f;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    sv[j] = s0;
+    zv[j] = z0;
+  }
+  if (sp.ptr && !sp.scalar)
+    for (int j = 0; j < VEC; ++j)
+      if (base + j < n) sv[j] = load_any(sp.ptr, sp.dtype, param_offset(sp, shape, base + j));
+  if (zp.ptr && !zp.scalar)
+    for (int j = 0; j < VEC; ++j)
+      if (base + j < n) zv[j] = load_any(zp.ptr, zp.dtype, param_offset(zp, shape, base + j));
+  const bool has_s = sp.ptr != nullptr, has_z = zp.ptr != nullptr;
   uint32_t res[VEC];
   float outv[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
-    float s = sv, z = zv;
-    if (sp.ptr && !sp.scalar) s = load_any(sp.ptr, sp.dtype, param_offset(sp, shape, base + j));
-    if (zp.ptr && !zp.scalar) z = load_any(zp.ptr, zp.dtype, param_offset(zp, shape, base + j));
     float q = xv[j];
-    if (sp.ptr) q = round_to(q / s, cdt);
-    if (zp.ptr) q = round_to(q + z, cdt);
-    if (has_fmt) {
-      uint32_t b = f2bf(q);  // vmap indexes by the bfloat16 pattern
-      if (cdt == VH_BF16) b = __float_as_uint(q) >> 16;  // exact, keeps NaN bits
-      float v = fmt_value(b, f, lds);
-      if (out_dtype == VH_U8) res[j] = fmt_code(b, v, f, lds);
+    if (has_s) q = div_round(q, sv[j], cdt);
+    if (has_z) q = round_to(q + zv[j], cdt);
+    if constexpr (KIND != K_NONE) {
+      // vmap indexes by the bfloat16 pattern (exact when cdt is bf16)
+      const uint32_t b = (cdt == VH_BF16 && !isnan_f(q)) ? (__float_as_uint(q) >> 16) : f2bf(q);
+      const float v = fmt_value_k<KIND>(b, f, lds);
+      res[j] = fmt_code_k<KIND>(b, v, f, lds);
       outv[j] = v;
     } else {
+      res[j] = 0;
       outv[j] = q;
     }
   }
@@ -253,18 +276,23 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
   int64_t threads = (n + VEC - 1) / VEC;
   int64_t blocks = (threads + 255) / 256;
   VH_REQUIRE(blocks < (1ll << 31), "vh_quantize: tensor too large");
-  hipLaunchKernelGGL(k_quantize, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), x, x_dtype, n, s, sp,
-                     zp, compute_dtype, fmt ? 1 : 0, f, out, out_dtype);
-  return vh::check_launch("vh_quantize");
+  hipStream_t st = vh::as_stream(stream);
+  return dispatch_kind(kernel_kind(fmt), [&](auto kind) {
+    constexpr int K = decltype(kind)::value;
+    hipLaunchKernelGGL(k_quantize<K>, dim3((unsigned)blocks), dim3(256), 0, st, x, x_dtype, n, s, sp, zp,
+                       compute_dtype, f, out, out_dtype);
+    return vh::check_launch("vh_quantize");
+  });
 }
 
 // ------------------------------------------------------------ dequantize
+template <int KIN>
 __global__ void __launch_bounds__(256)
 k_dequantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_param sp, vh_param zp, int cdt,
-             int has_in, vh_format fin, int has_out, vh_format fout, void* __restrict__ out, int out_dtype) {
+             vh_format fin, int has_out, vh_format fout, void* __restrict__ out, int out_dtype) {
   __shared__ uint16_t lds_in[2 * VH_MAX_STEPS];
   __shared__ uint16_t lds_out[2 * VH_MAX_STEPS];
-  if (has_in) stage_steps(fin, lds_in);
+  if constexpr (KIN == K_STEPS) stage_steps(fin, lds_in);
   if (has_out) stage_steps(fout, lds_out);
   int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
   if (base >= n) return;
@@ -277,12 +305,12 @@ k_dequantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh
     if (i >= n) break;
     float v;
     if (x_dtype == VH_U8) {
-      v = fmt_decode(((const uint8_t*)x)[i], fin, lds_in);
+      v = fmt_decode_k<KIN>(((const uint8_t*)x)[i], fin, lds_in);
     } else {
       v = load_any(x, x_dtype, i);
-      if (has_in) {
+      if constexpr (KIN != K_NONE) {
         uint32_t b = x_dtype == VH_BF16 ? (uint32_t)((const uint16_t*)x)[i] : f2bf(v);
-        v = round_to(fmt_value(b, fin, lds_in), x_dtype);
+        v = round_to(fmt_value_k<KIN>(b, fin, lds_in), x_dtype);
       }
     }
     float s = sv, z = zv;
@@ -323,7 +351,11 @@ extern "C" int vh_dequantize(const void* x, int32_t x_dtype, const int64_t* shap
   int64_t threads = (n + VEC - 1) / VEC;
   int64_t blocks = (threads + 255) / 256;
   VH_REQUIRE(blocks < (1ll << 31), "vh_dequantize: tensor too large");
-  hipLaunchKernelGGL(k_dequantize, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), x, x_dtype, n, s,
-                     sp, zp, compute_dtype, fmt_in ? 1 : 0, fi, fmt_out ? 1 : 0, fo, out, out_dtype);
-  return vh::check_launch("vh_dequantize");
+  hipStream_t st = vh::as_stream(stream);
+  return dispatch_kind(kernel_kind(fmt_in), [&](auto kind) {
+    constexpr int K = decltype(kind)::value;
+    hipLaunchKernelGGL(k_dequantize<K>, dim3((unsigned)blocks), dim3(256), 0, st, x, x_dtype, n, s, sp, zp,
+                       compute_dtype, fi, fmt_out ? 1 : 0, fo, out, out_dtype);
+    return vh::check_launch("vh_dequantize");
+  });
 }

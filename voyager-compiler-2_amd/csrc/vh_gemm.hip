@@ -52,38 +52,43 @@ struct GemmArgs {
 };
 
 // ------------------------------------------------------------ staging
-// Bytes of one row of a stage that a thread loads with one 16-byte access:
-// for fp8/bf16 the stored bytes are the LDS bytes; for decoded formats a
-// 16-byte LDS chunk (8 bf16) comes from 8 code bytes.
-__device__ __forceinline__ uint4 load16(const uint8_t* p, bool ok) {
-  if (!ok) return make_uint4(0, 0, 0, 0);
-  return *(const uint4*)p;
+// Global loads go through buffer resources: an access past the resource's
+// end returns zero, so tile edges in M / N need no branches.  Rows shorter
+// than a stage (the last K step) are masked with a select.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, RSRC_WORD3);
 }
 
-__device__ __forceinline__ uint2 load8(const uint8_t* p, bool ok) {
-  if (!ok) return make_uint2(0, 0);
-  return *(const uint2*)p;
+__device__ __forceinline__ uint4 bload16(rsrc_t r, int off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// bf16 bits of int8 code c times 2**e (exact: |c| < 2**8 and 2**e >= 2**-133
-// whenever a code is nonzero in a block that scale could round).
+__device__ __forceinline__ uint2 bload8(rsrc_t r, int off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
+
+__device__ __forceinline__ uint32_t bload1(rsrc_t r, int off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
+// bf16 bits of int8 code c times 2**e.  Exact: |c| <= 128 needs 8
+// significant bits and the block's nonzero codes come with 2**e >= 2**-133.
 __device__ __forceinline__ uint32_t mxi8_bf16(int c, int e) {
-  float v = ldexpf((float)c, e);
-  return __float_as_uint(v) >> 16;
+  return __float_as_uint(ldexpf((float)c, e)) >> 16;
 }
 
 __device__ __forceinline__ uint4 decode_mxi8(uint2 raw, int e) {
-  uint32_t b[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    b[j] = (raw.x >> (8 * j)) & 0xffu;
-    b[4 + j] = (raw.y >> (8 * j)) & 0xffu;
-  }
   uint4 o;
-  o.x = mxi8_bf16((int8_t)b[0], e) | (mxi8_bf16((int8_t)b[1], e) << 16);
-  o.y = mxi8_bf16((int8_t)b[2], e) | (mxi8_bf16((int8_t)b[3], e) << 16);
-  o.z = mxi8_bf16((int8_t)b[4], e) | (mxi8_bf16((int8_t)b[5], e) << 16);
-  o.w = mxi8_bf16((int8_t)b[6], e) | (mxi8_bf16((int8_t)b[7], e) << 16);
+  o.x = mxi8_bf16((int8_t)(raw.x & 0xff), e) | (mxi8_bf16((int8_t)((raw.x >> 8) & 0xff), e) << 16);
+  o.y = mxi8_bf16((int8_t)((raw.x >> 16) & 0xff), e) | (mxi8_bf16((int8_t)(raw.x >> 24), e) << 16);
+  o.z = mxi8_bf16((int8_t)(raw.y & 0xff), e) | (mxi8_bf16((int8_t)((raw.y >> 8) & 0xff), e) << 16);
+  o.w = mxi8_bf16((int8_t)((raw.y >> 16) & 0xff), e) | (mxi8_bf16((int8_t)(raw.y >> 24), e) << 16);
   return o;
 }
 
@@ -97,41 +102,62 @@ __device__ __forceinline__ uint4 decode_p8(uint2 raw, const uint16_t* lut) {
   return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
 }
 
-// The 16-byte LDS chunk `c` (0..7) of row `r` of stage starting at element
-// k0, for an operand in format fmt.
+// One operand of the block: its rows as a buffer resource.
 struct Operand {
-  const uint8_t* p;
-  int64_t rows, ld, K;
-  int fmt;
-  const uint8_t* scale;
-  int64_t lds;
-  int block, bias;
+  rsrc_t data;
+  rsrc_t scale;
+  int ld;       // row pitch (bytes)
+  int sld;      // scale row pitch (bytes)
+  int64_t K;    // elements
+  int block_shift;
+  int bias;
 };
 
-__device__ __forceinline__ uint4 fetch_chunk(const Operand& o, int64_t r, int c, int64_t k0, const uint16_t* lut) {
-  const bool rok = r < o.rows;
-  if (o.fmt == OP_FP8) {
-    int64_t k = k0 + c * 16;
-    return load16(o.p + r * o.ld + k, rok && k < o.K);
+// Raw bytes of one 16-byte LDS chunk, as loaded.  Masking and decoding wait
+// for the LDS store (after the stage's MFMAs), so the loads stay in flight
+// while the MFMAs run.
+struct Raw {
+  uint4 v;      // fp8 / bf16: the chunk; decoded formats: 8 code bytes in v.x, v.y
+  uint32_t s;   // MX int8: the block's scale byte
+  bool live;    // the chunk lies before K
+};
+
+template <int FMT>
+__device__ __forceinline__ Raw fetch_raw(const Operand& o, int r, int c, int64_t k0) {
+  Raw w;
+  if constexpr (FMT == OP_FP8) {
+    const int64_t k = k0 + c * 16;
+    w.v = bload16(o.data, r * o.ld + (int)k);
+    w.live = k < o.K;
+  } else if constexpr (FMT == OP_BF16) {
+    const int64_t k = k0 + c * 8;
+    w.v = bload16(o.data, r * o.ld + (int)k * 2);
+    w.live = k < o.K;
+  } else {
+    const int64_t k = k0 + c * 8;
+    uint2 raw = bload8(o.data, r * o.ld + (int)k);
+    w.v = make_uint4(raw.x, raw.y, 0, 0);
+    w.live = k < o.K;
+    if constexpr (FMT == OP_MXI8) w.s = bload1(o.scale, r * o.sld + (int)(k >> o.block_shift));
   }
-  if (o.fmt == OP_BF16) {
-    int64_t k = k0 + c * 8;
-    return load16(o.p + r * o.ld + k * 2, rok && k < o.K);
-  }
-  // decoded formats: 8 elements from 8 code bytes
-  int64_t k = k0 + c * 8;
-  bool ok = rok && k < o.K;
-  uint2 raw = load8(o.p + r * o.ld + k, ok);
-  if (o.fmt == OP_MXI8) {
-    int e = 0;
-    if (ok) e = (int)o.scale[r * o.lds + k / o.block] - o.bias;
-    return decode_mxi8(raw, e);
-  }
-  return decode_p8(raw, lut);
+  return w;
 }
 
-template <int BM, int BN, bool FP8>
+template <int FMT>
+__device__ __forceinline__ uint4 finish_raw(const Raw& w, const Operand& o, const uint16_t* lut) {
+  const uint32_t m = w.live ? 0xffffffffu : 0u;
+  if constexpr (FMT == OP_FP8 || FMT == OP_BF16) {
+    return make_uint4(w.v.x & m, w.v.y & m, w.v.z & m, w.v.w & m);
+  } else {
+    uint2 raw = make_uint2(w.v.x & m, w.v.y & m);
+    if constexpr (FMT == OP_MXI8) return decode_mxi8(raw, (int)w.s - o.bias);
+    else return decode_p8(raw, lut);
+  }
+}
+
+template <int BM, int BN, int AF, int BF>
 __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
+  constexpr bool FP8 = AF == OP_FP8;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* As = smem;                          // [2][BM][ROWP]
   uint8_t* Bs = smem + 2 * BM * ROWP;          // [2][BN][ROWP]
@@ -142,7 +168,7 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  if (g.a_fmt == OP_P8 || g.b_fmt == OP_P8) {
+  if constexpr (AF == OP_P8 || BF == OP_P8) {
     for (int i = tid; i < 256; i += NT) lut[i] = g.lut[i];
     __syncthreads();
   }
@@ -168,27 +194,43 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
   if (g.a_scale) g.a_scale += bat * g.ssa;
   if (g.b_scale) g.b_scale += bat * g.ssb;
 
-  Operand oa{g.A + m0 * g.lda, g.M - m0, g.lda, g.K, g.a_fmt, g.a_scale ? g.a_scale + m0 * g.lds_a : nullptr,
-             g.lds_a, g.a_block, g.a_bias};
-  Operand ob{g.B + n0 * g.ldb, g.N - n0, g.ldb, g.K, g.b_fmt, g.b_scale ? g.b_scale + n0 * g.lds_b : nullptr,
-             g.lds_b, g.b_block, g.b_bias};
+  const int64_t rows_a = (g.M - m0) < BM ? (g.M - m0) : BM;
+  const int64_t rows_b = (g.N - n0) < BN ? (g.N - n0) : BN;
+  Operand oa, ob;
+  oa.data = make_rsrc(g.A + m0 * g.lda, rows_a * g.lda);
+  ob.data = make_rsrc(g.B + n0 * g.ldb, rows_b * g.ldb);
+  oa.ld = (int)g.lda;
+  ob.ld = (int)g.ldb;
+  oa.K = ob.K = g.K;
+  if constexpr (AF == OP_MXI8) {
+    oa.scale = make_rsrc(g.a_scale + m0 * g.lds_a, rows_a * g.lds_a);
+    oa.sld = (int)g.lds_a;
+    oa.block_shift = __builtin_ctz(g.a_block);
+    oa.bias = g.a_bias;
+  }
+  if constexpr (BF == OP_MXI8) {
+    ob.scale = make_rsrc(g.b_scale + n0 * g.lds_b, rows_b * g.lds_b);
+    ob.sld = (int)g.lds_b;
+    ob.block_shift = __builtin_ctz(g.b_block);
+    ob.bias = g.b_bias;
+  }
 
   constexpr int KE = FP8 ? 128 : 64;      // K elements per stage
   constexpr int CA = BM * 8 / NT;         // 16-byte chunks per thread (A)
   constexpr int CB = BN * 8 / NT;
   static_assert(CA >= 1 && CB >= 1, "tile too small");
 
-  uint4 ra[CA], rb[CB];
+  Raw ra[CA], rb[CB];
   auto fetch = [&](int64_t k0) {
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
       int ch = tid + i * NT;
-      ra[i] = fetch_chunk(oa, ch >> 3, ch & 7, k0, lut);
+      ra[i] = fetch_raw<AF>(oa, ch >> 3, ch & 7, k0);
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
       int ch = tid + i * NT;
-      rb[i] = fetch_chunk(ob, ch >> 3, ch & 7, k0, lut);
+      rb[i] = fetch_raw<BF>(ob, ch >> 3, ch & 7, k0);
     }
   };
   auto stash = [&](int s) {
@@ -197,12 +239,12 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
       int ch = tid + i * NT;
-      *(uint4*)(a + (ch >> 3) * ROWP + (ch & 7) * 16) = ra[i];
+      *(uint4*)(a + (ch >> 3) * ROWP + (ch & 7) * 16) = finish_raw<AF>(ra[i], oa, lut);
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
       int ch = tid + i * NT;
-      *(uint4*)(b + (ch >> 3) * ROWP + (ch & 7) * 16) = rb[i];
+      *(uint4*)(b + (ch >> 3) * ROWP + (ch & 7) * 16) = finish_raw<BF>(rb[i], ob, lut);
     }
   };
 
@@ -225,7 +267,12 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
   const int lhalf = lane >> 5;
   for (int64_t ks = 0; ks < nk; ++ks) {
     const int s = ks & 1;
-    if (ks + 1 < nk) fetch((ks + 1) * KE);
+    // Unconditional prefetch: past the end of K every chunk is masked to
+    // zero and the stage is never read, and keeping the loop body one basic
+    // block lets the scheduler order the stores after the MFMAs.
+    fetch((ks + 1) * KE);
+    // Issue the prefetch before the stage's LDS reads and MFMAs.
+    __builtin_amdgcn_sched_barrier(0);
     const uint8_t* a = As + s * BM * ROWP + (wm * (BM / 2) + lrow) * ROWP;
     const uint8_t* b = Bs + s * BN * ROWP + (wn * (BN / 2) + lrow) * ROWP;
     if constexpr (FP8) {
@@ -268,9 +315,9 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
       }
     }
-    if (ks + 1 < nk) {
-      stash(s ^ 1);
-    }
+    // Keep the LDS stores (which wait for the prefetch) after the MFMAs.
+    __builtin_amdgcn_sched_barrier(0);
+    stash(s ^ 1);
     __syncthreads();
   }
 
@@ -307,22 +354,27 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, bool FP8>
+template <int BM, int BN, int AF, int BF>
 int launch_tile(const GemmArgs& g, int64_t batch, hipStream_t stream) {
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   const size_t smem = 2 * (BM + BN) * ROWP + 512;
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)k_gemm<BM, BN, FP8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void*)k_gemm<BM, BN, AF, BF>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)smem) != hipSuccess) {
       vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
       return VH_ELAUNCH;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm<BM, BN, FP8>), dim3((unsigned)tiles, (unsigned)batch), dim3(NT), smem, stream, g);
+  hipLaunchKernelGGL((k_gemm<BM, BN, AF, BF>), dim3((unsigned)tiles, (unsigned)batch), dim3(NT), smem, stream, g);
   return vh::check_launch("vh_gemm");
 }
+
+template <int A, int B>
+struct Fmts {
+  static constexpr int a = A, b = B;
+};
 
 }  // namespace
 
@@ -346,10 +398,11 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
     if (fmt == OP_MXI8) {
       const void* sp = s ? d->b_scale : d->a_scale;
       int blk = s ? d->b_block : d->a_block;
-      VH_REQUIRE(sp && blk >= 8 && blk % 8 == 0, "vh_gemm: MX int8 operand needs scales with block %% 8 == 0");
+      VH_REQUIRE(sp && blk >= 8 && (blk & (blk - 1)) == 0, "vh_gemm: MX int8 operand needs a power-of-two block >= 8");
     }
     if (fmt == OP_P8) VH_REQUIRE(d->lut, "vh_gemm: posit8 operand needs its decode table");
   }
+  VH_REQUIRE(d->lda * 256 < (1ll << 31) && d->ldb * 256 < (1ll << 31), "vh_gemm: rows too long for 32-bit offsets");
   if (d->M == 0 || d->N == 0) return VH_OK;
   GemmArgs g;
   memset(&g, 0, sizeof(g));
@@ -390,16 +443,20 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
     else if (tiles(128, 128) * batch >= 256) cfg = 3;
     else cfg = 4;
   }
-  if (fp8) {
+  auto pick = [&](auto tag) -> int {
+    constexpr int AF = decltype(tag)::a, BF = decltype(tag)::b;
     switch (cfg) {
-      case 2: return launch_tile<256, 128, true>(g, batch, st);
-      case 3: return launch_tile<128, 128, true>(g, batch, st);
-      default: return launch_tile<128, 64, true>(g, batch, st);
+      case 2: return launch_tile<256, 128, AF, BF>(g, batch, st);
+      case 3: return launch_tile<128, 128, AF, BF>(g, batch, st);
+      default: return launch_tile<128, 64, AF, BF>(g, batch, st);
     }
-  }
-  switch (cfg) {
-    case 2: return launch_tile<256, 128, false>(g, batch, st);
-    case 3: return launch_tile<128, 128, false>(g, batch, st);
-    default: return launch_tile<128, 64, false>(g, batch, st);
-  }
+  };
+  if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16) return pick(Fmts<OP_BF16, OP_BF16>{});
+  if (d->a_fmt == OP_MXI8 && d->b_fmt == OP_MXI8) return pick(Fmts<OP_MXI8, OP_MXI8>{});
+  if (d->a_fmt == OP_P8 && d->b_fmt == OP_P8) return pick(Fmts<OP_P8, OP_P8>{});
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_MXI8) return pick(Fmts<OP_BF16, OP_MXI8>{});
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_P8) return pick(Fmts<OP_BF16, OP_P8>{});
+  vh::set_error("vh_gemm: operand format pair (%d, %d) is not built", d->a_fmt, d->b_fmt);
+  return VH_EINVAL;
 }

@@ -20,6 +20,7 @@ VH_BF16, VH_F32, VH_F16, VH_U8, VH_I64 = 0, 1, 2, 3, 4
 
 FMT_IDENTITY, FMT_INT, FMT_MINIFLOAT, FMT_POSIT, FMT_STEPS, FMT_LUT = range(6)
 FMT_SIGNED = 1
+FMT_HW_E4M3 = 2
 MAX_STEPS = 64
 MAX_DIMS = 6
 

@@ -21,8 +21,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import (FMT_IDENTITY, FMT_INT, FMT_LUT, FMT_MINIFLOAT, FMT_POSIT, FMT_SIGNED, FMT_STEPS,
-                   MAX_STEPS, Format)
+from ._lib import (FMT_HW_E4M3, FMT_IDENTITY, FMT_INT, FMT_LUT, FMT_MINIFLOAT, FMT_POSIT, FMT_SIGNED,
+                   FMT_STEPS, MAX_STEPS, Format)
 
 QMAP_SIZE = 2**16
 
@@ -178,6 +178,8 @@ def minifloat_format(ebits: int, mbits: int, signed: bool, max_norm: float) -> F
     f.emin = 2 - 2 ** (ebits - 1)
     f.max_norm = max_norm
     f.clamp_bf16 = _bf16(max_norm)
+    if (ebits, mbits, signed, max_norm) == (4, 3, True, 448.0):
+        f.flags |= FMT_HW_E4M3  # OCP E4M3: the hardware converter (verified like any closed form)
     return f
 
 
