@@ -29,6 +29,16 @@ VH_DEV uint32_t f2bf(float f) {
   return u >> 16;
 }
 
+// Two float32 values to packed bfloat16 bits (lo, hi) with the gfx950
+// converter (v_cvt_pk_bf16_f32: round half to even, denormals kept).
+typedef __bf16 vh_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float vh_f32x2 __attribute__((ext_vector_type(2)));
+VH_DEV uint32_t f2bf2_hw(float lo, float hi) {
+  vh_f32x2 v = {lo, hi};
+  vh_bf16x2 h = __builtin_convertvector(v, vh_bf16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
 // The float32 value rounded to bfloat16 and back (an eager bf16 op result).
 VH_DEV float rbf(float f) { return bf2f(f2bf(f)); }
 

@@ -201,6 +201,83 @@ k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_p
   }
 }
 
+// Per-tensor fast path: contiguous bfloat16 input, one scale, no zero point,
+// bfloat16 compute.  Each thread keeps UNROLL 16-byte loads in flight; the
+// reciprocal of the scale is taken once; the bf16 rounding of x/s uses the
+// same midpoint test as div_bf16 with the hardware bf16 converter.
+constexpr int UNROLL = 4;
+
+template <int KIND, bool PACKED>
+__global__ void __launch_bounds__(256)
+k_quantize_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int sdt, vh_format f,
+              void* __restrict__ out) {
+  __shared__ uint16_t lds[2 * VH_MAX_STEPS];
+  if constexpr (KIND == K_STEPS) stage_steps(f, lds);
+  const float s = load_any(sp, sdt, 0);
+  const float as = fabsf(s);
+  const bool fast = as >= 0x1p-126f && as <= 0x1p126f;
+  const float r = __builtin_amdgcn_rcpf(s);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t v0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v0 < nvec; v0 += stride * UNROLL) {
+    uint4 raw[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t v = v0 + u * stride;
+      raw[u] = v < nvec ? *(const uint4*)(x + v * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t v = v0 + u * stride;
+      if (v >= nvec) break;
+      const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+      float q[8];
+      bool slow = !fast;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv = bf2f(j & 1 ? w[j >> 1] >> 16 : w[j >> 1] & 0xffffu);
+        q[j] = xv * r;
+        const uint32_t ub = __float_as_uint(q[j]);
+        slow |= ((ub - 0x7FFCu) & 0xFFFFu) <= 8u;
+      }
+      uint32_t qb[4];
+      if (!slow) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qb[j] = f2bf2_hw(q[2 * j], q[2 * j + 1]);
+      } else {  // near a bf16 midpoint: correctly rounded division
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x0 = bf2f(w[j] & 0xffffu), x1 = bf2f(w[j] >> 16);
+          qb[j] = f2bf(x0 / s) | (f2bf(x1 / s) << 16);
+        }
+      }
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t c[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t b = (qb[j] >> (16 * h)) & 0xffffu;
+          if constexpr (KIND == K_E4M3) {
+            c[h] = e4m3_hw_code(bf2f(b));
+            if constexpr (!PACKED) c[h] = f2bf(__builtin_amdgcn_cvt_f32_fp8((int)c[h], 0));
+          } else if constexpr (KIND == K_NONE) {
+            c[h] = b;
+          } else {
+            const float val = fmt_value_k<KIND>(b, f, lds);
+            c[h] = PACKED ? fmt_code_k<KIND>(b, val, f, lds) : f2bf(val);
+          }
+        }
+        o[j] = PACKED ? (c[0] | (c[1] << 8)) : (c[0] | (c[1] << 16));
+      }
+      if constexpr (PACKED) {
+        *(uint2*)((uint8_t*)out + v * 8) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+      } else {
+        *(uint4*)((uint16_t*)out + v * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+}
+
 static int check_shape(const int64_t* shape, int32_t ndim, Shape* s, int64_t* n) {
   VH_REQUIRE(ndim >= 0 && ndim <= VH_MAX_DIMS, "tensor rank %d exceeds %d", ndim, VH_MAX_DIMS);
   int64_t total = 1;
@@ -273,10 +350,32 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
   vh_format f;
   memset(&f, 0, sizeof(f));
   if (fmt) f = *fmt;
+  hipStream_t st = vh::as_stream(stream);
+  const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  if (x_dtype == VH_BF16 && compute_dtype == VH_BF16 && sp.ptr && sp.scalar && !zp.ptr && n % 8 == 0 && aligned &&
+      (out_dtype == VH_U8 || out_dtype == VH_BF16)) {
+    const int64_t nvec = n / 8;
+    int64_t blocks = (nvec + 256 * UNROLL - 1) / (256 * UNROLL);
+    if (blocks > 8192) blocks = 8192;
+    return dispatch_kind(kernel_kind(fmt), [&](auto kind) {
+      constexpr int K = decltype(kind)::value;
+      if (out_dtype == VH_U8) {
+        if constexpr (K == K_NONE || K == K_IDENTITY || K == K_LUT) {
+          return (int)VH_EINVAL;  // unreachable: checked by packable()
+        } else {
+          hipLaunchKernelGGL((k_quantize_pt<K, true>), dim3((unsigned)blocks), dim3(256), 0, st,
+                             (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, out);
+        }
+      } else {
+        hipLaunchKernelGGL((k_quantize_pt<K, false>), dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, out);
+      }
+      return vh::check_launch("vh_quantize");
+    });
+  }
   int64_t threads = (n + VEC - 1) / VEC;
   int64_t blocks = (threads + 255) / 256;
   VH_REQUIRE(blocks < (1ll << 31), "vh_quantize: tensor too large");
-  hipStream_t st = vh::as_stream(stream);
   return dispatch_kind(kernel_kind(fmt), [&](auto kind) {
     constexpr int K = decltype(kind)::value;
     hipLaunchKernelGGL(k_quantize<K>, dim3((unsigned)blocks), dim3(256), 0, st, x, x_dtype, n, s, sp, zp,

@@ -30,7 +30,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int ROWB = 128;   // bytes of K per row per stage
 constexpr int ROWP = 144;   // padded LDS row pitch
-constexpr int NT = 256;     // threads per block
 
 struct GemmArgs {
   const uint8_t* A;
@@ -155,9 +154,11 @@ __device__ __forceinline__ uint4 finish_raw(const Raw& w, const Operand& o, cons
   }
 }
 
-template <int BM, int BN, int AF, int BF>
-__global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
+// BM x BN block tile computed by WM x WN waves; MINB blocks per CU.
+template <int BM, int BN, int WM, int WN, int MINB, int AF, int BF>
+__global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   constexpr bool FP8 = AF == OP_FP8;
+  constexpr int NT = WM * WN * 64;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* As = smem;                          // [2][BM][ROWP]
   uint8_t* Bs = smem + 2 * BM * ROWP;          // [2][BN][ROWP]
@@ -166,7 +167,7 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
 
   if constexpr (AF == OP_P8 || BF == OP_P8) {
     for (int i = tid; i < 256; i += NT) lut[i] = g.lut[i];
@@ -248,8 +249,10 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
     }
   };
 
-  constexpr int TM = BM / 64;  // 32-row MFMA tiles per wave
-  constexpr int TN = BN / 64;
+  constexpr int TM = BM / WM / 32;  // 32-row MFMA tiles per wave
+  constexpr int TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1 && BM % (WM * 32) == 0 && BN % (WN * 32) == 0, "bad wave layout");
+  static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "stage chunks must divide among threads");
   f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -273,8 +276,8 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
     fetch((ks + 1) * KE);
     // Issue the prefetch before the stage's LDS reads and MFMAs.
     __builtin_amdgcn_sched_barrier(0);
-    const uint8_t* a = As + s * BM * ROWP + (wm * (BM / 2) + lrow) * ROWP;
-    const uint8_t* b = Bs + s * BN * ROWP + (wn * (BN / 2) + lrow) * ROWP;
+    const uint8_t* a = As + s * BM * ROWP + (wm * (BM / WM) + lrow) * ROWP;
+    const uint8_t* b = Bs + s * BN * ROWP + (wn * (BN / WN) + lrow) * ROWP;
     if constexpr (FP8) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
@@ -330,13 +333,13 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * (BN / 2) + j * 32 + lrow;
+      const int64_t col = n0 + wn * (BN / WN) + j * 32 + lrow;
       if (col >= g.N) continue;
       float bias = 0.0f;
       if (e.bias) bias = e.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)e.bias)[col]) : ((const float*)e.bias)[col];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+        const int64_t row = m0 + wm * (BM / WM) + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
         if (row >= g.M) continue;
         float v = acc[i][j][r];
         if (e.mode == EPI_ROUND_SCALE) {
@@ -354,20 +357,21 @@ __global__ void __launch_bounds__(NT, 1) k_gemm(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, int AF, int BF>
+template <int BM, int BN, int WM, int WN, int MINB, int AF, int BF>
 int launch_tile(const GemmArgs& g, int64_t batch, hipStream_t stream) {
+  constexpr int NT = WM * WN * 64;
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   const size_t smem = 2 * (BM + BN) * ROWP + 512;
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)k_gemm<BM, BN, AF, BF>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void*)k_gemm<BM, BN, WM, WN, MINB, AF, BF>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)smem) != hipSuccess) {
       vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
       return VH_ELAUNCH;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm<BM, BN, AF, BF>), dim3((unsigned)tiles, (unsigned)batch), dim3(NT), smem, stream, g);
+  hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, MINB, AF, BF>), dim3((unsigned)tiles, (unsigned)batch), dim3(NT), smem, stream, g);
   return vh::check_launch("vh_gemm");
 }
 
@@ -439,16 +443,26 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
   auto tiles = [&](int bm, int bn) { return ((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn); };
   int cfg = d->tile_hint;
   if (cfg == 0) {
-    if (tiles(256, 128) * batch >= 256) cfg = 2;
-    else if (tiles(128, 128) * batch >= 256) cfg = 3;
+    // Measured on MI355X at M = 2048 (fp8, K in {4096, 14336}): 8-wave
+    // blocks (two waves per SIMD) hide the operand loads best; the largest
+    // tile that still gives every CU work wins, and long K favours 256x128.
+    const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
+    const int64_t t128 = tiles(128, 128) * batch;
+    if (t256 >= 384) cfg = 6;
+    else if (t2561 >= 256 && d->K >= 8192) cfg = 5;
+    else if (t128 >= 256) cfg = 8;
     else cfg = 4;
   }
   auto pick = [&](auto tag) -> int {
     constexpr int AF = decltype(tag)::a, BF = decltype(tag)::b;
     switch (cfg) {
-      case 2: return launch_tile<256, 128, AF, BF>(g, batch, st);
-      case 3: return launch_tile<128, 128, AF, BF>(g, batch, st);
-      default: return launch_tile<128, 64, AF, BF>(g, batch, st);
+      case 2: return launch_tile<256, 128, 2, 2, 1, AF, BF>(g, batch, st);
+      case 3: return launch_tile<128, 128, 2, 2, 2, AF, BF>(g, batch, st);
+      case 5: return launch_tile<256, 128, 4, 2, 1, AF, BF>(g, batch, st);
+      case 6: return launch_tile<256, 256, 4, 2, 1, AF, BF>(g, batch, st);
+      case 7: return launch_tile<128, 256, 2, 4, 1, AF, BF>(g, batch, st);
+      case 8: return launch_tile<128, 128, 4, 2, 1, AF, BF>(g, batch, st);
+      default: return launch_tile<128, 64, 2, 2, 2, AF, BF>(g, batch, st);
     }
   };
   if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
