@@ -181,6 +181,123 @@ def gpu_bench(args):
     return res, cpu_data
 
 
+def bench_config1(args):
+    """Config 1: MXINT8 linear, X [256,4096] (0.1% outliers x20, seed 0), W
+    [4096,4096] N(0,0.02); int8 bs=16 pot scales.  Step = quantize_mx(X) to
+    packed codes + scale bytes, then the packed MX-int8 GEMM."""
+    import voyager_amd  # noqa: F401
+    from voyager_amd import formats, gemm, packed
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(256, 4096, generator=g)
+    x = torch.where(torch.rand(256, 4096, generator=g) < 0.001, x * 20, x).bfloat16()
+    w = (torch.randn(4096, 4096, generator=g) * 0.02).bfloat16()
+    tab = formats.quantization_map("int8", dev)
+    xd, wd = x.to(dev), w.to(dev)
+    pw = packed.quantize_mx_packed(wd, tab, [-1], 16, 127.0, True)
+    st = {}
+
+    def quant():
+        st["px"] = packed.quantize_mx_packed(xd, tab, [-1], 16, 127.0, True)
+
+    def mm():
+        px = st["px"]
+        st["y"] = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias)
+
+    def step():
+        quant()
+        mm()
+
+    gs = capture(step)
+    ms = time_graph(gs, max(args.steps, 20))
+    gq = capture(lambda: [quant() for _ in range(20)])
+    q_ms = time_graph(gq, 5) / 20
+    gm = capture(lambda: [mm() for _ in range(20)])
+    g_ms = time_graph(gm, 5) / 20
+    flops = 2.0 * 256 * 4096 * 4096
+    qbytes = 256 * 4096 * 3 + 256 * 256  # bf16 in, int8 codes + scale bytes out
+    gbytes = 256 * 4096 + 256 * 256 + 4096 * 4096 + 4096 * 256 + 256 * 4096 * 2
+    return {"metric": "MXINT8 linear TFLOP/s (config 1)", "value": round(flops / (ms * 1e-3) / 1e12, 2),
+            "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "gemm": {"us": round(g_ms * 1e3, 2), "TFLOP/s": round(flops / (g_ms * 1e-3) / 1e12, 1),
+                     "GB/s": round(gbytes / (g_ms * 1e-3) / 1e9, 1),
+                     "roofline_us": round(max(flops / 2.5e15, gbytes / 8e12) * 1e6, 2),
+                     "note": "MX-int8 decoded to bf16 while staging; bf16 MFMA (2.5 PF) bound"},
+            "quantize_mx": {"us": round(q_ms * 1e3, 2), "GB/s": round(qbytes / (q_ms * 1e-3) / 1e9, 1)},
+            "config": {"workload": "cfg1: MXINT8 bs=16 pot, X[256,4096] . W[4096,4096]^T"}}
+
+
+def bench_config3(args):
+    """Config 3: MXNF4 decode linear at M in {1, 16} over the four Llama-3.1-8B
+    projections; weights baked once, rotated over > 256 MB."""
+    import voyager_amd  # noqa: F401
+    from voyager_amd import formats, gemm
+
+    dev = torch.device("cuda:0")
+    index, entries, mid = formats.codebook_tables("lut4_to_int6", dev)
+    stab = formats.quantization_map("fp8_e5m3", dev)
+    res = {}
+    tot_b, tot_t = 0.0, 0.0
+    for i, (K, N) in enumerate(SHAPES):
+        g = torch.Generator().manual_seed(1)
+        w = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev)
+        wb = gemm.bake_nf4_weight(w, index, stab, entries)
+        del w
+        wbytes = N * K // 2 + N * K // 64
+        nw = max(2, -(-2 * MALL_BYTES // wbytes))
+        ws = [gemm.NF4Weight(wb.packed.clone(), wb.scale.clone(), wb.scale_fmt, wb.levels, N, K)
+              for _ in range(nw)]
+        for M in (1, 16):
+            x = torch.randn(M, K, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
+            gg = capture(lambda: [gemm.linear_nf4(x, wi, index, stab) for wi in ws])
+            ms = time_graph(gg, 5) / nw
+            b = wbytes + M * K * 2 + M * N * 2
+            res[f"M{M}_K{K}_N{N}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                                      "roofline_us": round(b / 8e12 * 1e6, 2)}
+            tot_b += b
+            tot_t += ms
+        del ws
+    return {"metric": "MXNF4 decode linear GB/s (config 3)", "value": round(tot_b / (tot_t * 1e-3) / 1e9, 1),
+            "unit": "GB/s", "frac_of_hbm": round(tot_b / (tot_t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "per_shape": res, "config": {"workload": "cfg3: lut4_to_int6 bs=64 fp8_e5m3 scales, M in {1,16}"}}
+
+
+def bench_config4(args):
+    """Config 4: posit8 (es=1) quantize / dequantize of a 64M-element bf16
+    tensor N(0,4), and the posit8 GEMM 2048x4096x4096."""
+    import voyager_amd  # noqa: F401
+    from voyager_amd import formats, gemm, packed
+
+    dev = torch.device("cuda:0")
+    tab = formats.quantization_map("posit8_1", dev)
+    one = torch.ones((), dtype=torch.bfloat16, device=dev)
+    g = torch.Generator().manual_seed(0)
+    n = 1 << 26
+    t = (torch.randn(n, generator=g) * 2).bfloat16().to(dev)
+    st = {}
+    gq = capture(lambda: st.__setitem__("c", packed.quantize_packed(t, one, tab)))
+    q_ms = time_graph(gq, 10)
+    gr = capture(lambda: st.__setitem__("r", torch.ops.quantized_ops.quantize(t, one, qmap=tab)))
+    r_ms = time_graph(gr, 10)
+    gd = capture(lambda: st.__setitem__("d", packed.unpack_codes(st["c"], tab)))
+    d_ms = time_graph(gd, 10)
+    x = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(1)).bfloat16().to(dev)
+    w = (torch.randn(4096, 4096, generator=torch.Generator().manual_seed(2)) * 0.02).bfloat16().to(dev)
+    cx, cw = packed.quantize_packed(x, one, tab), packed.quantize_packed(w, one, tab)
+    lut = gemm.posit8_lut(tab)
+    gm = capture(lambda: [gemm.linear_posit8(cx, cw, lut) for _ in range(10)])
+    g_ms = time_graph(gm, 5) / 10
+    flops = 2.0 * 2048 * 4096 * 4096
+    return {"metric": "posit8 quantize GB/s + posit8 GEMM TFLOP/s (config 4)",
+            "quantize_packed": {"us": round(q_ms * 1e3, 2), "GB/s": round(n * 3 / (q_ms * 1e-3) / 1e9, 1)},
+            "quantize_ref_form": {"us": round(r_ms * 1e3, 2), "GB/s": round(n * 4 / (r_ms * 1e-3) / 1e9, 1)},
+            "dequantize_packed": {"us": round(d_ms * 1e3, 2), "GB/s": round(n * 3 / (d_ms * 1e-3) / 1e9, 1)},
+            "gemm": {"us": round(g_ms * 1e3, 2), "TFLOP/s": round(flops / (g_ms * 1e-3) / 1e12, 1),
+                     "peak_TFLOP/s": 2500.0, "note": "posit bytes decoded via LDS table to bf16; bf16 MFMA"},
+            "config": {"workload": "cfg4: posit8_1, 64M-element tensor; GEMM M=2048 K=N=4096"}}
+
+
 def cpu_baseline(cpu_data, budget_s=8.0):
     """The reference's CPU op sequence (the oracle) on a bounded sample: the
     (4096, 4096) projection with the first 256 token rows, all host threads."""
@@ -234,6 +351,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0)
+    ap.add_argument("--config", type=int, default=2,
+                    help="2 (default): the headline line; 1, 3, 4: that config's measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -241,6 +360,10 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.config in (1, 3, 4):
+        fn = {1: bench_config1, 3: bench_config3, 4: bench_config4}[args.config]
+        print(json.dumps(fn(args)), flush=True)
         return
     res, cpu_data = gpu_bench(args)
     cpu = None if args.no_cpu else cpu_baseline(cpu_data)

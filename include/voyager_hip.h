@@ -116,12 +116,14 @@ int vh_dequantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t 
  * pot != 0: scale = 2**(floor(log2 amax) - floor(log2 quant_max)); else
  * scale = scale_fmt(amax / quant_max [/ global_scale]).  Zero/NaN scales
  * become 1.  scale_dtype / codes_dtype VH_U8 write packed bytes (pot scales
- * as biased exponents: byte = e + pot_bias, 255 = inf). */
+ * as biased exponents: byte = e + pot_bias, 255 = inf); scale_dtype VH_F32
+ * writes the scale values as float32.  code_lut (256 bytes, or NULL) remaps
+ * packed codes, e.g. codebook indices to their int8 levels. */
 int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
                    int64_t block, float quant_max, int32_t pot, const vh_format* scale_fmt,
                    const void* global_scale, int32_t gs_dtype, const vh_format* fmt,
                    void* scale_out, int32_t scale_dtype, int32_t pot_bias,
-                   void* codes_out, int32_t codes_dtype, vh_stream_t stream);
+                   void* codes_out, int32_t codes_dtype, const uint8_t* code_lut, vh_stream_t stream);
 
 /* quantize_affine: per block min/max -> (scale, zero_point, codes).
  * Replaces quantized_ops.quantize_affine (ops/quantized.py:1218-1283). */
@@ -178,6 +180,27 @@ typedef struct vh_gemm_desc {
 } vh_gemm_desc;
 
 int vh_gemm(const vh_gemm_desc* desc, vh_stream_t stream);
+
+/* ------------------------------------------------------------ MXNF4 GEMV
+ * Decode-shape linear_mx (ops/quantized.py:651-723) for codebook weights
+ * with 64-element blocks (lut4_to_int6 + fp8_e5m3 scales), M <= 16.
+ *
+ * vh_pack_nf4 bakes [N, K] level indices (0..15, one per byte) into the
+ * GEMV's layout: for each 16-row x 64-column block, 64 lanes x 8 bytes, lane
+ * l holding row l % 16, columns (l / 16) * 16 + [0, 16) as nibbles (column j
+ * in the low nibble of byte j, column j + 8 in its high nibble).  Needs
+ * N % 16 == 0 and K % 64 == 0.  Replaces the weight baking of
+ * quantization/quantize_pt2e.py:819-828 for this format. */
+int vh_pack_nf4(const uint8_t* codes, int64_t N, int64_t K, uint8_t* out, vh_stream_t stream);
+
+/* y[M, N] = sum over blocks b of s_x[m, b] * s_w[n, b] * sum_k Lx[m, k] Lw[n, k]
+ * with Lx the activations' int8 levels [M, K], s_x float32 [M, K/64],
+ * Lw = levels16[index] of the packed weights (levels16: 16 int8 values in
+ * host memory, passed by value), s_w = w_scale_fmt(byte) [N, K/64]; int8
+ * MFMA per block, float32 accumulation, epilogue as vh_gemm (EPI_PLAIN). */
+int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t M, const uint8_t* w_packed,
+                const uint8_t* w_scale, const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N,
+                int64_t K, const vh_epilogue* epi, void* y, vh_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -151,3 +151,27 @@ def test_linear_posit8():
     lut = gemm.posit8_lut(tab.to(d))
     got = gemm.linear_posit8(cx, cw, lut)
     assert max_rel_err(got, exp) < TOL
+
+
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)])
+def test_linear_nf4_gemv_cfg3(M, K, N):
+    """Config 3's decode GEMV on baked 4-bit weights against the oracle's
+    linear_mx of the same quantized operands."""
+    from voyager_amd import gemm
+
+    vt = T.quantization_map("lut4_to_int6")
+    index, entries, mid = T.codebook_index_table(vt)
+    stab = T.quantization_map("fp8_e5m3")
+    g = torch.Generator().manual_seed(40)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    sx, cx = O.quantize_mx(x, index, [-1], 64, 31.0, False, stab, mid)
+    sw, cw = O.quantize_mx(w, index, [-1], 64, 31.0, False, stab)
+    exp = O.linear_mx(cx, cw, input_scale=sx, weight_scale=sw, block_size=64, input_code=entries,
+                      weight_code=entries)
+    d = "cuda"
+    wb = gemm.bake_nf4_weight(w.to(d), index.to(d), stab.to(d), entries.to(d))
+    got = gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d))
+    assert got.dtype == torch.bfloat16 and list(got.shape) == [M, N]
+    assert max_rel_err(got, exp) < TOL

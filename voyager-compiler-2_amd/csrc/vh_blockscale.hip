@@ -37,6 +37,7 @@ struct Params {
   int scale_dtype;    // cdt or VH_U8
   int pot_bias;       // packed pot scale byte = e + pot_bias
   int codes_dtype;    // cdt or VH_U8
+  const uint8_t* code_lut;  // packed codes are remapped through this (or null)
 };
 
 // NaN-propagating max/min, as torch.amax / torch.amin.
@@ -68,8 +69,25 @@ struct BlockScale {
   uint32_t packed;  // packed scale byte
 };
 
+// The scale map applied to a value (SKIND = K_NONE: no map; a specialised
+// kind, or K_LUT + 1 for the runtime switch).
+constexpr int K_RUNTIME = 8;
+
+template <int SKIND>
+VH_DEV float smap_value(uint32_t b, const vh_format& f, const uint16_t* slds) {
+  if constexpr (SKIND == K_RUNTIME) return fmt_value(b, f, slds);
+  else return fmt_value_k<SKIND>(b, f, slds);
+}
+
+template <int SKIND>
+VH_DEV uint32_t smap_code(uint32_t b, float v, const vh_format& f, const uint16_t* slds) {
+  if constexpr (SKIND == K_RUNTIME) return fmt_code(b, v, f, slds);
+  else return fmt_code_k<SKIND>(b, v, f, slds);
+}
+
 // Scale of one block from its reductions (hi = amax for MX, max for AFFINE;
 // lo = min for AFFINE).
+template <int SKIND>
 VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_t* slds) {
   BlockScale r;
   r.zp = 0.0f;
@@ -103,29 +121,28 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
     float s = div_round(hi, P.quant_max, cdt);
     const float gs = P.gs ? round_to(load_x(P.gs, P.gs_dtype, 0), cdt) : 1.0f;
     if (P.gs) s = div_round(s, gs, cdt);
-    uint32_t sb = 0;
-    if (P.has_sfmt) {
-      sb = f2bf(s);
-      s = round_to(fmt_value(sb, P.sfmt, slds), cdt);
+    if constexpr (SKIND != K_NONE) {
+      const uint32_t sb = f2bf(s);
+      s = round_to(smap_value<SKIND>(sb, P.sfmt, slds), cdt);
     }
     if (!(s > 0.0f)) s = 1.0f;
     r.scale = s;
     r.el_scale = P.gs ? round_to(s * gs, cdt) : s;
-    if (P.has_sfmt) {
+    if constexpr (SKIND != K_NONE) {
       uint32_t b = f2bf(s);
-      r.packed = fmt_code(b, bf2f(b), P.sfmt, slds);
+      r.packed = smap_code<SKIND>(b, bf2f(b), P.sfmt, slds);
     }
     return r;
   }
   // AFFINE (ops/quantized.py:1262-1281)
   float s = div_round(round_to(hi - lo, cdt), P.quant_max - P.quant_min, cdt);
   if (!(s > 0.0f)) s = 1.0f;
-  if (P.has_sfmt) {
-    s = vmap1(s, P.sfmt, slds, cdt);
+  if constexpr (SKIND != K_NONE) {
+    s = round_to(smap_value<SKIND>(f2bf(s), P.sfmt, slds), cdt);
     if (!(s > 0.0f)) s = 1.0f;
   }
   float zp = round_to(div_round(-lo, s, cdt) + P.quant_min, cdt);
-  if (P.has_sfmt) zp = vmap1(zp, P.sfmt, slds, cdt);
+  if constexpr (SKIND != K_NONE) zp = round_to(smap_value<SKIND>(f2bf(zp), P.sfmt, slds), cdt);
   r.scale = s;
   r.el_scale = s;
   r.zp = zp;
@@ -134,24 +151,42 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
 
 // One element's reference-form code value and packed byte.
 template <int KIND>
-VH_DEV void element_code(float x, const BlockScale& bs, const Params& P, const uint16_t* lds, float* v,
-                         uint32_t* code) {
+VH_DEV void element_code(float x, const BlockScale& bs, const Params& P, const uint16_t* lds, const uint8_t* clut,
+                         float* v, uint32_t* code) {
   float q = div_round(x, bs.el_scale, P.cdt);
   if (P.mode == AFFINE) q = round_to(q + bs.zp, P.cdt);
   const uint32_t b = (P.cdt == VH_BF16 && !isnan_f(q)) ? (__float_as_uint(q) >> 16) : f2bf(q);
-  const float val = fmt_value_k<KIND>(b, P.fmt, lds);
-  *v = round_to(val, P.cdt);
-  *code = fmt_code_k<KIND>(b, val, P.fmt, lds);
+  if constexpr (KIND == K_STEPS) {
+    const bool nan = bf_isnan_bits(b);
+    const uint32_t lvl = nan ? (uint32_t)P.fmt.nan_level : steps_level(b, P.fmt.nsteps, lds);
+    *v = round_to(nan ? bf2f(P.fmt.nan_out) : bf2f(lds[VH_MAX_STEPS + lvl]), P.cdt);
+    *code = lvl;
+  } else {
+    const float val = fmt_value_k<KIND>(b, P.fmt, lds);
+    *v = round_to(val, P.cdt);
+    *code = fmt_code_k<KIND>(b, val, P.fmt, lds);
+  }
+  if (P.code_lut) *code = clut[*code & 0xffu];
 }
 
-template <int VEC, int KIND>
+// Stage the code remap table in LDS (256 bytes); every thread must call it.
+VH_DEV void stage_code_lut(const Params& P, uint8_t* clut) {
+  if (P.code_lut) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) clut[i] = P.code_lut[i];
+    __syncthreads();
+  }
+}
+
+template <int VEC, int KIND, int SKIND>
 __global__ void __launch_bounds__(256)
 k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, Params P,
        void* __restrict__ scale_out, void* __restrict__ zp_out, void* __restrict__ codes_out) {
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
   __shared__ uint16_t slds[2 * VH_MAX_STEPS];
+  __shared__ uint8_t clut[256];
   if constexpr (KIND == K_STEPS) stage_steps(P.fmt, lds);
-  if (P.has_sfmt) stage_steps(P.sfmt, slds);
+  if constexpr (SKIND == K_STEPS || SKIND == K_RUNTIME) stage_steps(P.sfmt, slds);
+  stage_code_lut(P, clut);
   const int64_t tpr = nblk * g;  // threads per row
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = t / tpr;
@@ -196,12 +231,12 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
     if (P.mode == AFFINE) lo = nmin(lo, __shfl_xor(lo, off));
   }
   if (row >= rows) return;
-  BlockScale bs = block_scale(hi, lo, P, slds);
+  BlockScale bs = block_scale<SKIND>(hi, lo, P, slds);
   const int64_t blk = v / g;
   if ((v % g) == 0 && blk < nblk) {
     const int64_t si = row * nblk + blk;
     if (P.scale_dtype == VH_U8) ((uint8_t*)scale_out)[si] = (uint8_t)bs.packed;
-    else store_f(scale_out, P.cdt, si, bs.scale);
+    else store_f(scale_out, P.scale_dtype, si, bs.scale);
     if (P.mode == AFFINE) store_f(zp_out, P.cdt, si, bs.zp);
   }
   if constexpr (KIND == K_NONE) return;
@@ -209,7 +244,7 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
   float cv[VEC];
   uint32_t cc[VEC];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) element_code<KIND>(xv[j], bs, P, lds, &cv[j], &cc[j]);
+  for (int j = 0; j < VEC; ++j) element_code<KIND>(xv[j], bs, P, lds, clut, &cv[j], &cc[j]);
   if (P.codes_dtype == VH_U8) {
     uint2 pk;
     pk.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
@@ -229,14 +264,16 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
 }
 
 // One thread per (outer, block, inner) column.
-template <int KIND>
+template <int KIND, int SKIND>
 __global__ void __launch_bounds__(256)
 k_cols(const void* __restrict__ x, int64_t outer, int64_t L, int64_t inner, int64_t block, int64_t nblk, Params P,
        void* __restrict__ scale_out, void* __restrict__ zp_out, void* __restrict__ codes_out) {
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
   __shared__ uint16_t slds[2 * VH_MAX_STEPS];
+  __shared__ uint8_t clut[256];
   if constexpr (KIND == K_STEPS) stage_steps(P.fmt, lds);
-  if (P.has_sfmt) stage_steps(P.sfmt, slds);
+  if constexpr (SKIND == K_STEPS || SKIND == K_RUNTIME) stage_steps(P.sfmt, slds);
+  stage_code_lut(P, clut);
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = outer * nblk * inner;
   if (t >= total) return;
@@ -267,10 +304,10 @@ k_cols(const void* __restrict__ x, int64_t outer, int64_t L, int64_t inner, int6
     hi = nmax(hi, 0.0f);
     lo = nmin(lo, 0.0f);
   }
-  BlockScale bs = block_scale(hi, lo, P, slds);
+  BlockScale bs = block_scale<SKIND>(hi, lo, P, slds);
   const int64_t si = (o * nblk + blk) * inner + in;
   if (P.scale_dtype == VH_U8) ((uint8_t*)scale_out)[si] = (uint8_t)bs.packed;
-  else store_f(scale_out, P.cdt, si, bs.scale);
+  else store_f(scale_out, P.scale_dtype, si, bs.scale);
   if (P.mode == AFFINE) store_f(zp_out, P.cdt, si, bs.zp);
   if constexpr (KIND == K_NONE) return;
   if (!codes_out) return;
@@ -278,10 +315,20 @@ k_cols(const void* __restrict__ x, int64_t outer, int64_t L, int64_t inner, int6
     int64_t i = base + l * inner;
     float cv;
     uint32_t cc;
-    element_code<KIND>(load_x(x, P.cdt, i), bs, P, lds, &cv, &cc);
+    element_code<KIND>(load_x(x, P.cdt, i), bs, P, lds, clut, &cv, &cc);
     if (P.codes_dtype == VH_U8) ((uint8_t*)codes_out)[i] = (uint8_t)cc;
     else store_f(codes_out, P.cdt, i, cv);
   }
+}
+
+// Scale maps the configs use get their own kernels; any other map runs the
+// runtime switch.
+template <typename F>
+int dispatch_scale(const Params& P, F&& fn) {
+  if (!P.has_sfmt) return fn(std::integral_constant<int, K_NONE>{});
+  const int k = kernel_kind(&P.sfmt);
+  if (k == K_MINI) return fn(std::integral_constant<int, K_MINI>{});
+  return fn(std::integral_constant<int, K_RUNTIME>{});
 }
 
 int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block, const Params& P,
@@ -296,9 +343,12 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
     VH_REQUIRE(blocks < (1ll << 31), "%s: tensor too large", what);
     dispatch_kind(P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE, [&](auto kind) {
       constexpr int K = decltype(kind)::value;
-      hipLaunchKernelGGL((k_rows<8, K>), dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P,
-                         scale_out, zp_out, codes_out);
-      return 0;
+      return dispatch_scale(P, [&](auto skind) {
+        constexpr int S = decltype(skind)::value;
+        hipLaunchKernelGGL((k_rows<8, K, S>), dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P,
+                           scale_out, zp_out, codes_out);
+        return 0;
+      });
     });
   } else {
     const int64_t threads = outer * nblk * inner;
@@ -306,9 +356,12 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
     VH_REQUIRE(blocks < (1ll << 31), "%s: tensor too large", what);
     dispatch_kind(P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE, [&](auto kind) {
       constexpr int K = decltype(kind)::value;
-      hipLaunchKernelGGL(k_cols<K>, dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, inner, block, nblk, P,
-                         scale_out, zp_out, codes_out);
-      return 0;
+      return dispatch_scale(P, [&](auto skind) {
+        constexpr int S = decltype(skind)::value;
+        hipLaunchKernelGGL((k_cols<K, S>), dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, inner, block,
+                           nblk, P, scale_out, zp_out, codes_out);
+        return 0;
+      });
     });
   }
   return vh::check_launch(what);
@@ -339,12 +392,14 @@ extern "C" int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int
                               int64_t block, float quant_max, int32_t pot, const vh_format* scale_fmt,
                               const void* global_scale, int32_t gs_dtype, const vh_format* fmt, void* scale_out,
                               int32_t scale_dtype, int32_t pot_bias, void* codes_out, int32_t codes_dtype,
-                              vh_stream_t stream) {
+                              const uint8_t* code_lut, vh_stream_t stream) {
   int rc;
   if ((rc = check_common(x, x_dtype, outer, L, inner, block, "vh_quantize_mx"))) return rc;
   VH_REQUIRE(scale_out, "vh_quantize_mx: null scale output");
   VH_REQUIRE(!codes_out || fmt, "vh_quantize_mx: codes need an element map");
-  VH_REQUIRE(scale_dtype == x_dtype || scale_dtype == VH_U8, "vh_quantize_mx: scale dtype must be the input's or u8");
+  VH_REQUIRE(scale_dtype == x_dtype || scale_dtype == VH_U8 || scale_dtype == VH_F32,
+             "vh_quantize_mx: scale dtype must be the input's, f32 or u8");
+  VH_REQUIRE(!code_lut || codes_dtype == VH_U8, "vh_quantize_mx: a code remap needs packed codes");
   VH_REQUIRE(!codes_out || codes_dtype == x_dtype || codes_dtype == VH_U8,
              "vh_quantize_mx: codes dtype must be the input's or u8");
   VH_REQUIRE(!(codes_out && codes_dtype == VH_U8) || packable(*fmt), "vh_quantize_mx: element map has no packed form");
@@ -377,6 +432,7 @@ extern "C" int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int
   P.scale_dtype = scale_dtype;
   P.pot_bias = pot_bias;
   P.codes_dtype = codes_dtype;
+  P.code_lut = code_lut;
   if (outer * L * inner == 0) return VH_OK;
   return launch(x, outer, L, inner, block, P, scale_out, nullptr, codes_out, vh::as_stream(stream),
                 "vh_quantize_mx");

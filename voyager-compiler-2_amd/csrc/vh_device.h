@@ -193,13 +193,17 @@ VH_DEV float fmt_posit(float x, const vh_format& f) {
 // staged in LDS by the kernel: `keys` holds f.thr_key).  NaN inputs are
 // handled by the caller (they take nan_out / nan_level).
 VH_DEV uint32_t steps_level(uint32_t b, int nsteps, const uint16_t* keys) {
-  uint32_t k = bf_key(b);
-  int lo = 0, hi = nsteps;  // first threshold whose key exceeds k
-  while (lo < hi) {
-    int mid = (lo + hi) >> 1;
-    if ((uint32_t)keys[mid] <= k) lo = mid + 1; else hi = mid;
+  // Branch-free search: six halvings cover up to 63 thresholds, so the
+  // lookups of a thread's elements can overlap.
+  const uint32_t k = bf_key(b);
+  int pos = 0;
+#pragma unroll
+  for (int step = 32; step >= 1; step >>= 1) {
+    const int nxt = pos + step;
+    const bool ok = nxt <= nsteps && (uint32_t)keys[nxt <= nsteps ? nxt - 1 : 0] <= k;
+    pos = ok ? nxt : pos;
   }
-  return (uint32_t)lo;
+  return (uint32_t)pos;
 }
 
 // Stage a STEPS format's keys and entries in LDS (2 * VH_MAX_STEPS halves).

@@ -96,7 +96,7 @@ _SIGNATURES = {
     ),
     "vh_quantize_mx": (
         [_P, _I32, _I64, _I64, _I64, _I64, _F32, _I32, ctypes.POINTER(Format), _P, _I32,
-         ctypes.POINTER(Format), _P, _I32, _I32, _P, _I32, _P],
+         ctypes.POINTER(Format), _P, _I32, _I32, _P, _I32, _P, _P],
         _I32,
     ),
     "vh_quantize_affine": (
@@ -106,6 +106,9 @@ _SIGNATURES = {
     ),
     # vh_gemm takes a vh_gemm_desc*; voyager_amd.gemm.GemmDesc mirrors it.
     "vh_gemm": ([_P, _P], _I32),
+    "vh_pack_nf4": ([_P, _I64, _I64, _P, _P], _I32),
+    # x_levels, x_scale, M, w_packed, w_scale, w_scale_fmt, levels16 (host), N, K, epilogue*, y, stream
+    "vh_gemv_nf4": ([_P, _P, _I64, _P, _P, ctypes.POINTER(Format), _P, _I64, _I64, _P, _P, _P], _I32),
 }
 
 #: Every symbol ``include/voyager_hip.h`` declares.

@@ -11,7 +11,7 @@ order (the parity bar is 1e-2 max-abs-normalized error).
 """
 
 import ctypes
-from typing import Optional
+from typing import NamedTuple, Optional
 
 import torch
 
@@ -312,3 +312,89 @@ def linear_posit8(x_codes, w_codes, lut: torch.Tensor, out_dtype=torch.bfloat16,
     d.epi = _epilogue(EPI_PLAIN, out_dtype)
     run(d, x_codes.device)
     return out
+
+
+# ----------------------------------------------------------------- MXNF4 GEMV
+class NF4Weight(NamedTuple):
+    """Weights baked for ``linear_nf4``: level indices packed two per byte in
+    the GEMV's MFMA lane order, plus one scale-map code per 64-block."""
+
+    packed: torch.Tensor      # uint8, N * K / 2
+    scale: torch.Tensor       # uint8 [N, K / 64]
+    scale_fmt: "formats.Classified"
+    levels: bytes             # the 16 int8 codebook levels
+    N: int
+    K: int
+
+
+def _levels_of(entries: torch.Tensor) -> bytes:
+    lv = entries.detach().float().cpu()
+    if lv.numel() != 16 or not torch.equal(lv, lv.round()) or lv.abs().max() > 127:
+        raise ValueError("linear_nf4 needs a 16-entry codebook of integer levels in [-127, 127]")
+    return bytes(int(v) & 0xFF for v in lv.tolist())
+
+
+def bake_nf4_weight(w: torch.Tensor, index_table: torch.Tensor, scale_qmap: torch.Tensor,
+                    entries: torch.Tensor) -> NF4Weight:
+    """``quantize_mx(w, index_table, [-1], 64, 31, scale_qmap=...)`` once (as
+    convert bakes weights, ``quantization/quantize_pt2e.py:819-828``), then
+    packed for the GEMV."""
+    from . import packed as _packed
+
+    N, K = w.shape
+    p = _packed.quantize_mx_packed(w, index_table, [-1], 64, 31.0, False, scale_qmap)
+    out = torch.empty(N * K // 2, dtype=torch.uint8, device=w.device)
+    st = load().vh_pack_nf4(ctypes.c_void_p(p.codes.data_ptr()), N, K, ctypes.c_void_p(out.data_ptr()),
+                            ctypes.c_void_p(stream_of(w)))
+    _lib.check(st, "vh_pack_nf4")
+    return NF4Weight(out, p.scale.contiguous(), p.scale_fmt, _levels_of(entries), N, K)
+
+
+_level_lut_cache = {}
+
+
+def _level_lut(levels: bytes, device) -> torch.Tensor:
+    key = (levels, str(device))
+    t = _level_lut_cache.get(key)
+    if t is None:
+        lut = list(levels) + [0] * (256 - len(levels))
+        t = torch.tensor(lut, dtype=torch.uint8, device=device)
+        _level_lut_cache[key] = t
+    return t
+
+
+def linear_nf4(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, scale_qmap: torch.Tensor,
+               out_dtype=torch.bfloat16, bias=None, alpha=None) -> torch.Tensor:
+    """MXNF4 ``linear_mx`` at decode shapes (M <= 16): the activations are
+    quantized like the reference's in-graph ``quantize_mx`` (one launch that
+    emits their int8 levels and float32 block scales), then the weight-
+    streaming GEMV."""
+    M, K = x.shape
+    if K != weight.K:
+        raise RuntimeError("linear_nf4: contraction mismatch")
+    xc = x.contiguous()
+    ec = formats.classify(index_table)
+    sc = formats.classify(scale_qmap)
+    xl = torch.empty(M, K, dtype=torch.uint8, device=x.device)
+    xs = torch.empty(M, K // 64, dtype=torch.float32, device=x.device)
+    lut = _level_lut(weight.levels, x.device)
+    lib_ = load()
+    st = lib_.vh_quantize_mx(ctypes.c_void_p(xc.data_ptr()), dtype_code(xc.dtype), M, K, 1, 64, 31.0, 0,
+                             ctypes.byref(sc.fmt), None, 0, ctypes.byref(ec.fmt), ctypes.c_void_p(xs.data_ptr()),
+                             VH_F32, 0, ctypes.c_void_p(xl.data_ptr()), dtype_code(torch.uint8),
+                             ctypes.c_void_p(lut.data_ptr()), ctypes.c_void_p(stream_of(x)))
+    _lib.check(st, "vh_quantize_mx")
+    y = torch.empty(M, weight.N, dtype=out_dtype, device=x.device)
+    if alpha is not None:
+        alpha = alpha.reshape(()).to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+    epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
+    lv = ctypes.create_string_buffer(weight.levels, 16)
+    st = lib_.vh_gemv_nf4(ctypes.c_void_p(xl.data_ptr()), ctypes.c_void_p(xs.data_ptr()), M,
+                          ctypes.c_void_p(weight.packed.data_ptr()), ctypes.c_void_p(weight.scale.data_ptr()),
+                          ctypes.byref(weight.scale_fmt.fmt), lv, weight.N, weight.K,
+                          ctypes.c_void_p(ctypes.addressof(epi)), ctypes.c_void_p(y.data_ptr()),
+                          ctypes.c_void_p(stream_of(x)))
+    _lib.check(st, "vh_gemv_nf4")
+    return y

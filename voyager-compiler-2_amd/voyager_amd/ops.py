@@ -311,7 +311,7 @@ def _mx_launch(x, axes, block_size, quant_max, pot, scale_qmap, global_scale, qm
     st = load().vh_quantize_mx(
         ptr(xc), dtype_code(cdt), outer, L, inner, block_size, float(quant_max), 1 if pot else 0, _fmt_ref(sc),
         ptr(gs), dtype_code(gs.dtype) if gs is not None else 0, _fmt_ref(ec), ptr(scale), dtype_code(cdt), 0,
-        ptr(codes), dtype_code(cdt), ctypes.c_void_p(stream_of(x)))
+        ptr(codes), dtype_code(cdt), None, ctypes.c_void_p(stream_of(x)))
     _lib.check(st, "vh_quantize_mx")
     return scale, codes
 

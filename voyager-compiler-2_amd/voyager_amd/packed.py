@@ -68,7 +68,7 @@ def quantize_mx_packed(x: torch.Tensor, qmap: torch.Tensor, axes, block_size: in
     st = load().vh_quantize_mx(
         ptr(xc), dtype_code(xc.dtype), outer, L, inner, block_size, float(quant_max),
         1 if force_scale_power_of_two else 0, ctypes.byref(sc.fmt) if sc else None, None, 0,
-        ctypes.byref(ec.fmt), ptr(scale), VH_U8, bias, ptr(codes), VH_U8, ctypes.c_void_p(stream_of(x)))
+        ctypes.byref(ec.fmt), ptr(scale), VH_U8, bias, ptr(codes), VH_U8, None, ctypes.c_void_p(stream_of(x)))
     _lib.check(st, "vh_quantize_mx")
     return PackedMX(codes, scale, ec, sc, bool(force_scale_power_of_two), bias, block_size, ax)
 
