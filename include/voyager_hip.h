@@ -171,7 +171,8 @@ typedef struct vh_gemm_desc {
   int32_t a_bias, b_bias;
   const void* lut;     /* OP_P8 decode table */
   int32_t tile_hint;   /* 0: automatic; 2: 256x128/4 waves, 3: 128x128/4, 4: 128x64/4,
-                          5: 256x128/8 waves, 6: 256x256/8, 7: 128x256/8, 8: 128x128/8 */
+                          5: 256x128/8 waves, 6: 256x256/8, 7: 128x256/8, 8: 128x128/8,
+                          9: 256x128/8 (one-step prefetch), 10: 128x128/8 (one-step) */
   int64_t batch;       /* independent GEMMs (<= 1: one) */
   int64_t batch_stride_a, batch_stride_b; /* bytes (0: broadcast) */
   int64_t batch_stride_c;                 /* elements */

@@ -112,50 +112,42 @@ struct Operand {
   int bias;
 };
 
-// Raw bytes of one 16-byte LDS chunk, as loaded.  Masking and decoding wait
-// for the LDS store (after the stage's MFMAs), so the loads stay in flight
-// while the MFMAs run.
-struct Raw {
-  uint4 v;      // fp8 / bf16: the chunk; decoded formats: 8 code bytes in v.x, v.y
-  uint32_t s;   // MX int8: the block's scale byte
-  bool live;    // the chunk lies before K
-};
-
+// Raw bytes of one 16-byte LDS chunk, as loaded: the chunk itself for fp8 /
+// bf16; for decoded formats 8 code bytes in x, y and the block's scale byte
+// in z.  Masking (past K) and decoding wait for the LDS store, after the
+// stage's MFMAs, so the loads stay in flight while the MFMAs run.
 template <int FMT>
-__device__ __forceinline__ Raw fetch_raw(const Operand& o, int r, int c, int64_t k0) {
-  Raw w;
+__device__ __forceinline__ uint4 fetch_raw(const Operand& o, int r, int c, int64_t k0) {
   if constexpr (FMT == OP_FP8) {
-    const int64_t k = k0 + c * 16;
-    w.v = bload16(o.data, r * o.ld + (int)k);
-    w.live = k < o.K;
+    return bload16(o.data, r * o.ld + (int)(k0 + c * 16));
   } else if constexpr (FMT == OP_BF16) {
-    const int64_t k = k0 + c * 8;
-    w.v = bload16(o.data, r * o.ld + (int)k * 2);
-    w.live = k < o.K;
+    return bload16(o.data, r * o.ld + (int)(k0 + c * 8) * 2);
   } else {
     const int64_t k = k0 + c * 8;
-    uint2 raw = bload8(o.data, r * o.ld + (int)k);
-    w.v = make_uint4(raw.x, raw.y, 0, 0);
-    w.live = k < o.K;
-    if constexpr (FMT == OP_MXI8) w.s = bload1(o.scale, r * o.sld + (int)(k >> o.block_shift));
+    const uint2 raw = bload8(o.data, r * o.ld + (int)k);
+    uint32_t sc = 0;
+    if constexpr (FMT == OP_MXI8) sc = bload1(o.scale, r * o.sld + (int)(k >> o.block_shift));
+    return make_uint4(raw.x, raw.y, sc, 0);
   }
-  return w;
 }
 
 template <int FMT>
-__device__ __forceinline__ uint4 finish_raw(const Raw& w, const Operand& o, const uint16_t* lut) {
-  const uint32_t m = w.live ? 0xffffffffu : 0u;
+__device__ __forceinline__ uint4 finish_raw(const uint4& w, int c, int64_t k0, const Operand& o,
+                                            const uint16_t* lut) {
+  const int64_t k = k0 + c * (FMT == OP_FP8 ? 16 : 8);
+  const uint32_t m = k < o.K ? 0xffffffffu : 0u;
   if constexpr (FMT == OP_FP8 || FMT == OP_BF16) {
-    return make_uint4(w.v.x & m, w.v.y & m, w.v.z & m, w.v.w & m);
+    return make_uint4(w.x & m, w.y & m, w.z & m, w.w & m);
   } else {
-    uint2 raw = make_uint2(w.v.x & m, w.v.y & m);
-    if constexpr (FMT == OP_MXI8) return decode_mxi8(raw, (int)w.s - o.bias);
+    const uint2 raw = make_uint2(w.x & m, w.y & m);
+    if constexpr (FMT == OP_MXI8) return decode_mxi8(raw, (int)w.z - o.bias);
     else return decode_p8(raw, lut);
   }
 }
 
-// BM x BN block tile computed by WM x WN waves; MINB blocks per CU.
-template <int BM, int BN, int WM, int WN, int MINB, int AF, int BF>
+// BM x BN block tile computed by WM x WN waves; MINB blocks per CU; PF
+// register sets of prefetched chunks (2: loads run two steps ahead).
+template <int BM, int BN, int WM, int WN, int MINB, int PF, int AF, int BF>
 __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   constexpr bool FP8 = AF == OP_FP8;
   constexpr int NT = WM * WN * 64;
@@ -221,8 +213,11 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   constexpr int CB = BN * 8 / NT;
   static_assert(CA >= 1 && CB >= 1, "tile too small");
 
-  Raw ra[CA], rb[CB];
-  auto fetch = [&](int64_t k0) {
+  // Two register sets of prefetched chunks: the loads for step k+2 are
+  // issued while step k computes, so each has a whole step to land before
+  // its LDS store.
+  uint4 ra0[CA], rb0[CB], ra1[PF == 2 ? CA : 1], rb1[PF == 2 ? CB : 1];
+  auto fetch = [&](uint4* ra, uint4* rb, int64_t k0) {
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
       int ch = tid + i * NT;
@@ -234,18 +229,18 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
       rb[i] = fetch_raw<BF>(ob, ch >> 3, ch & 7, k0);
     }
   };
-  auto stash = [&](int s) {
+  auto stash = [&](const uint4* ra, const uint4* rb, int s, int64_t k0) {
     uint8_t* a = As + s * BM * ROWP;
     uint8_t* b = Bs + s * BN * ROWP;
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
       int ch = tid + i * NT;
-      *(uint4*)(a + (ch >> 3) * ROWP + (ch & 7) * 16) = finish_raw<AF>(ra[i], oa, lut);
+      *(uint4*)(a + (ch >> 3) * ROWP + (ch & 7) * 16) = finish_raw<AF>(ra[i], ch & 7, k0, oa, lut);
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
       int ch = tid + i * NT;
-      *(uint4*)(b + (ch >> 3) * ROWP + (ch & 7) * 16) = finish_raw<BF>(rb[i], ob, lut);
+      *(uint4*)(b + (ch >> 3) * ROWP + (ch & 7) * 16) = finish_raw<BF>(rb[i], ch & 7, k0, ob, lut);
     }
   };
 
@@ -261,21 +256,9 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int64_t nk = (g.K + KE - 1) / KE;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-
   const int lrow = lane & 31;
   const int lhalf = lane >> 5;
-  for (int64_t ks = 0; ks < nk; ++ks) {
-    const int s = ks & 1;
-    // Unconditional prefetch: past the end of K every chunk is masked to
-    // zero and the stage is never read, and keeping the loop body one basic
-    // block lets the scheduler order the stores after the MFMAs.
-    fetch((ks + 1) * KE);
-    // Issue the prefetch before the stage's LDS reads and MFMAs.
-    __builtin_amdgcn_sched_barrier(0);
+  auto compute = [&](int s) {
     const uint8_t* a = As + s * BM * ROWP + (wm * (BM / WM) + lrow) * ROWP;
     const uint8_t* b = Bs + s * BN * ROWP + (wn * (BN / WN) + lrow) * ROWP;
     if constexpr (FP8) {
@@ -318,10 +301,45 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
       }
     }
-    // Keep the LDS stores (which wait for the prefetch) after the MFMAs.
-    __builtin_amdgcn_sched_barrier(0);
-    stash(s ^ 1);
+  };
+
+  // Steps are taken in pairs so the two register sets have fixed names.
+  // Past the end of K every chunk is masked to zero, so an odd last step
+  // adds nothing.
+  const int64_t nk = (g.K + KE - 1) / KE;
+  if constexpr (PF == 1) {
+    fetch(ra0, rb0, 0);
+    stash(ra0, rb0, 0, 0);
     __syncthreads();
+    for (int64_t ks = 0; ks < nk; ++ks) {
+      const int st = ks & 1;
+      fetch(ra0, rb0, (ks + 1) * KE);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(st);
+      __builtin_amdgcn_sched_barrier(0);
+      stash(ra0, rb0, st ^ 1, (ks + 1) * KE);
+      __syncthreads();
+    }
+  } else {
+  fetch(ra0, rb0, 0);
+  fetch(ra1, rb1, KE);
+  stash(ra0, rb0, 0, 0);
+  __syncthreads();
+  for (int64_t ks = 0; ks < nk; ks += 2) {
+    fetch(ra0, rb0, (ks + 2) * KE);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    __builtin_amdgcn_sched_barrier(0);
+    stash(ra1, rb1, 1, (ks + 1) * KE);
+    __syncthreads();
+    if (ks + 1 >= nk) break;
+    fetch(ra1, rb1, (ks + 3) * KE);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+    __builtin_amdgcn_sched_barrier(0);
+    stash(ra0, rb0, 0, (ks + 2) * KE);
+    __syncthreads();
+  }
   }
 
   // ---- epilogue: lane holds column lrow of each 32x32 tile, rows
@@ -357,21 +375,21 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, int MINB, int AF, int BF>
+template <int BM, int BN, int WM, int WN, int MINB, int PF, int AF, int BF>
 int launch_tile(const GemmArgs& g, int64_t batch, hipStream_t stream) {
   constexpr int NT = WM * WN * 64;
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   const size_t smem = 2 * (BM + BN) * ROWP + 512;
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)k_gemm<BM, BN, WM, WN, MINB, AF, BF>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void*)k_gemm<BM, BN, WM, WN, MINB, PF, AF, BF>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)smem) != hipSuccess) {
       vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
       return VH_ELAUNCH;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, MINB, AF, BF>), dim3((unsigned)tiles, (unsigned)batch), dim3(NT), smem, stream, g);
+  hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, MINB, PF, AF, BF>), dim3((unsigned)tiles, (unsigned)batch), dim3(NT), smem, stream, g);
   return vh::check_launch("vh_gemm");
 }
 
@@ -443,26 +461,30 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
   auto tiles = [&](int bm, int bn) { return ((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn); };
   int cfg = d->tile_hint;
   if (cfg == 0) {
-    // Measured on MI355X at M = 2048 (fp8, K in {4096, 14336}): 8-wave
-    // blocks (two waves per SIMD) hide the operand loads best; the largest
-    // tile that still gives every CU work wins, and long K favours 256x128.
+    // Measured on MI355X at M = 2048 with amax-scaled fp8 data (K in {4096,
+    // 14336}, N in {1024, 4096, 14336}): 8-wave blocks (two waves per SIMD)
+    // cover the operand loads; the largest tile that still fills the GPU
+    // wins (less LDS and L2 traffic per MFMA); a grid too small for 256 CUs
+    // takes 128 x 64.
     const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
     const int64_t t128 = tiles(128, 128) * batch;
     if (t256 >= 384) cfg = 6;
-    else if (t2561 >= 256 && d->K >= 8192) cfg = 5;
-    else if (t128 >= 256) cfg = 8;
+    else if (t2561 >= 256 && d->K >= 8192) cfg = 9;
+    else if (t128 >= 256) cfg = 10;
     else cfg = 4;
   }
   auto pick = [&](auto tag) -> int {
     constexpr int AF = decltype(tag)::a, BF = decltype(tag)::b;
     switch (cfg) {
-      case 2: return launch_tile<256, 128, 2, 2, 1, AF, BF>(g, batch, st);
-      case 3: return launch_tile<128, 128, 2, 2, 2, AF, BF>(g, batch, st);
-      case 5: return launch_tile<256, 128, 4, 2, 1, AF, BF>(g, batch, st);
-      case 6: return launch_tile<256, 256, 4, 2, 1, AF, BF>(g, batch, st);
-      case 7: return launch_tile<128, 256, 2, 4, 1, AF, BF>(g, batch, st);
-      case 8: return launch_tile<128, 128, 4, 2, 1, AF, BF>(g, batch, st);
-      default: return launch_tile<128, 64, 2, 2, 2, AF, BF>(g, batch, st);
+      case 2: return launch_tile<256, 128, 2, 2, 1, 1, AF, BF>(g, batch, st);
+      case 3: return launch_tile<128, 128, 2, 2, 2, 2, AF, BF>(g, batch, st);
+      case 5: return launch_tile<256, 128, 4, 2, 1, 2, AF, BF>(g, batch, st);
+      case 6: return launch_tile<256, 256, 4, 2, 1, 1, AF, BF>(g, batch, st);
+      case 7: return launch_tile<128, 256, 2, 4, 1, 2, AF, BF>(g, batch, st);
+      case 8: return launch_tile<128, 128, 4, 2, 1, 2, AF, BF>(g, batch, st);
+      case 9: return launch_tile<256, 128, 4, 2, 1, 1, AF, BF>(g, batch, st);
+      case 10: return launch_tile<128, 128, 4, 2, 1, 1, AF, BF>(g, batch, st);
+      default: return launch_tile<128, 64, 2, 2, 2, 2, AF, BF>(g, batch, st);
     }
   };
   if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
