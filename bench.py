@@ -298,6 +298,90 @@ def bench_config4(args):
             "config": {"workload": "cfg4: posit8_1, 64M-element tensor; GEMM M=2048 K=N=4096"}}
 
 
+def bench_config5(args):
+    """Config 5: one random-init Llama-3.1-8B-architecture decoder layer, decode
+    step at batch 8 over a 4096-token context (3968 KIVI 2-bit tokens, 127
+    residual, this step's).  Two such layers (and caches) alternate in the
+    graph, as consecutive layers of a model do, so neither fits the 256 MB
+    Infinity Cache; the time of one layer step is half a replay."""
+    import voyager_amd  # noqa: F401
+    from oracle import decode as D
+    from voyager_amd import decode
+
+    dev = torch.device("cuda:0")
+    cfg = D.Config()
+    B, n_main, n_res = 8, 3968, 127
+    pos = n_main + n_res
+    layers, caches, xs, cpu_data = [], [], [], None
+    for li in range(2):
+        w = D.random_layer(cfg, seed=li)
+        g = torch.Generator().manual_seed(100 + li)
+        kv = [torch.randn(B, cfg.n_kv_heads, n, 128, generator=g).bfloat16() for n in (n_main, n_main, n_res, n_res)]
+        x = torch.randn(B, cfg.hidden, generator=g).bfloat16()
+        wd = {k: v.to(dev) for k, v in w.items()}
+        layer = decode.DecoderLayer(wd, cfg.n_heads, cfg.n_kv_heads, cfg.eps, cfg.rope_theta, max_batch=B,
+                                    max_pos=pos + 1)
+        cache, kq, vq = decode.KiviCache.from_bf16(*[t.to(dev) for t in kv])
+        if li == 0 and not args.no_cpu:
+            tab = voyager_amd.formats.quantization_map("int8", dev)
+            mx = {}
+            for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
+                sc, cd = torch.ops.quantized_ops.quantize_mx(wd[k], tab, [-1], 16, 127.0, True)
+                mx[k] = (cd.cpu(), sc.cpu())
+            k_past = torch.cat((D.kivi_dequantize(kq[2].cpu(), kq[0].cpu(), kq[1].cpu(), -2), kv[2]), dim=2)
+            v_past = torch.cat((D.kivi_dequantize(vq[2].cpu(), vq[0].cpu(), vq[1].cpu(), -1), kv[3]), dim=2)
+            cpu_data = (x, w, k_past, v_past, mx)
+        del wd, kq, vq
+        layers.append(layer)
+        caches.append(cache)
+        xs.append(x.to(dev))
+    torch.cuda.synchronize()
+    stage_lists = [l.stages(x, c, pos) for l, c, x in zip(layers, caches, xs)]
+    names = [n for n, _ in stage_lists[0]]
+    reps = 10
+    step_g = capture(lambda: [fn() for _ in range(reps) for st in stage_lists for _, fn in st])
+    for _ in range(max(1, args.warmup // 10)):
+        step_g.replay()
+    torch.cuda.synchronize()
+    step_ms = time_graph(step_g, max(1, args.steps // 10)) / (2 * reps)
+    layers[0].flag.check()
+    per = {}
+    sbytes = layers[0].stage_bytes(B, caches[0])
+    for i, name in enumerate(names):
+        gi = capture(lambda: [st[i][1]() for _ in range(reps) for st in stage_lists])
+        ms = time_graph(gi, 5) / (2 * reps)
+        per[name] = {"us": round(ms * 1e3, 2), "GB/s": round(sbytes[name] / (ms * 1e-3) / 1e9, 1)}
+    total_b = sum(sbytes.values())
+    gbs = total_b / (step_ms * 1e-3) / 1e9
+    dom = max(("gate_up_proj", "down_proj", "qkv_proj", "o_proj", "attention"), key=lambda n: sbytes[n])
+    d_gbs = per[dom]["GB/s"]
+    cpu = None
+    if cpu_data is not None:
+        x, w, k_past, v_past, mx = cpu_data
+        cos, sin = D.rope_cos_sin(torch.tensor([pos]), 128, cfg.rope_theta)
+        torch.set_num_threads(os.cpu_count() or 1)
+        D.decode_layer(x, w, k_past, v_past, cos, sin, cfg, mx=mx)
+        t0 = time.perf_counter()
+        n = 0
+        while n < 2 or time.perf_counter() - t0 < 10.0:
+            D.decode_layer(x, w, k_past, v_past, cos, sin, cfg, mx=mx)
+            n += 1
+        cs = (time.perf_counter() - t0) / n
+        cpu = {"value": round(total_b / cs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+               "kind": "port", "ms_per_step": round(cs * 1e3, 1),
+               "sample": f"{n} full decode steps of the oracle layer (eager torch, reference op sequence)"}
+    return {"metric": "MX-int8 / KIVI decoder-layer decode step, HBM GB/s (config 5)",
+            "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+            "us_per_step": round(step_ms * 1e3, 2), "roofline_us": round(total_b / 8e12 * 1e6, 2),
+            "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": total_b,
+            "dtype": "int8 codes / 2-bit KIVI, fp32 accumulate", "data": "synthetic",
+            "roofline": {"bound": "hbm", "kernel": dom, "achieved": d_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(d_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+            "per_stage": per, "stage_bytes": sbytes, "cpu_baseline": cpu,
+            "config": {"workload": "cfg5: Llama-3.1-8B-arch decoder layer, decode, batch 8, ctx 4096, MXINT8 bs=16 "
+                                   "linears, KIVI 2-bit K/V (group 32, fp16 scale/zero), 128-token residual"}}
+
+
 def cpu_baseline(cpu_data, budget_s=8.0):
     """The reference's CPU op sequence (the oracle) on a bounded sample: the
     (4096, 4096) projection with the first 256 token rows, all host threads."""
@@ -352,7 +436,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0)
     ap.add_argument("--config", type=int, default=2,
-                    help="2 (default): the headline line; 1, 3, 4: that config's measurements")
+                    help="2 (default): the headline line; 1, 3, 4, 5: that config's measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -361,8 +445,8 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
-    if args.config in (1, 3, 4):
-        fn = {1: bench_config1, 3: bench_config3, 4: bench_config4}[args.config]
+    if args.config in (1, 3, 4, 5):
+        fn = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config]
         print(json.dumps(fn(args)), flush=True)
         return
     res, cpu_data = gpu_bench(args)

@@ -203,6 +203,99 @@ int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t M, const u
                 const uint8_t* w_scale, const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N,
                 int64_t K, const vh_epilogue* epi, void* y, vh_stream_t stream);
 
+/* ------------------------------------------------- decoder-layer decode step
+ * One decode step (a batch of single tokens, M <= 16) of a Llama-style layer
+ * whose linears are MX-int8 (int8 codes, block 16 along K, power-of-two
+ * scales: quantize_mx + linear_mx, ops/quantized.py:1122-1216 / :651-723)
+ * and whose KV cache is KIVI: 2-bit group-wise affine codes
+ * (quantize_affine / dequantize, ops/quantized.py:1218-1283 / :518-571; keys
+ * grouped along tokens, values along channels, group 32) plus a
+ * full-precision residual window (quant_folding.py:1025-1120).
+ *
+ * Each linear's input is handed over as its MX-int8 fake quantization
+ * (code x 2**e, exact) in fp16, produced by the kernel that computes it.
+ * Kernels report data they cannot represent by OR-ing VH_DECODE_ERR_* bits
+ * into a caller-owned device int32 (`flag`); the caller checks it. */
+#define VH_DECODE_ERR_FP16_RANGE 1   /* an activation block exceeds fp16 (|x| > 65504) */
+#define VH_DECODE_ERR_WEIGHT_RANGE 2 /* a weight block exponent outside [-24, 5] */
+#define VH_KIVI_RES_CAP 128          /* residual window slots */
+
+#define VH_GEMV_STORE 0    /* y = bf16(x W^T) */
+#define VH_GEMV_RESIDUAL 1 /* y = bf16(bf16(x W^T) + residual) */
+#define VH_GEMV_SWIGLU 2   /* y = bf16(silu(bf16(x Wg^T)) * bf16(x Wu^T)), fq_out = its fake quantization */
+
+/* LlamaRMSNorm of each row of x [M, H] (bf16) with weight w [H]: h_out
+ * (bf16, optional) and its MX-int8 fake quantization fq [M, H] (fp16 bits).
+ * Replaces the rmsnorm + quantize_mx pair of a converted decoder layer. */
+int vh_rmsnorm_mx8(const uint16_t* x, const uint16_t* w, int64_t M, int64_t H, float eps, uint16_t* h_out,
+                   uint16_t* fq, int32_t* flag, vh_stream_t stream);
+
+/* Bake MX-int8 weights [N, K] -- codes one int8 per byte and block scales as
+ * biased exponent bytes 2**(byte - scale_bias), as vh_quantize_mx packs
+ * them -- into the GEMV layout: w_codes N*K bytes, w_hb N*K/16 bytes.
+ * paired != 0 interleaves rows [0, N/2) and [N/2, N) tile by tile (gate / up
+ * projections for VH_GEMV_SWIGLU).  Blocks whose exponent is outside
+ * [-24, 5] (and not all-zero) set VH_DECODE_ERR_WEIGHT_RANGE.  Needs
+ * N % 16 == 0 (32 when paired) and K % 256 == 0.  Replaces the weight baking
+ * of quantization/quantize_pt2e.py:819-828 for this format. */
+int vh_mx8_bake(const uint8_t* codes, const uint8_t* scale, int32_t scale_bias, int64_t N, int64_t K,
+                int32_t paired, uint8_t* w_codes, uint8_t* w_hb, int32_t* flag, vh_stream_t stream);
+
+/* linear_mx of fake-quantized activations x_fq [M, K] (fp16 bits) and baked
+ * MX-int8 weights with N output columns (2N baked rows for VH_GEMV_SWIGLU);
+ * exact products, fp32 accumulation, bf16 output y [M, N] (optional for
+ * SWIGLU), residual [M, N] for VH_GEMV_RESIDUAL, fq_out [M, N] (fp16 bits)
+ * for SWIGLU.  tiles_per_block 1 or 2 (16 or 32 columns per workgroup,
+ * STORE / RESIDUAL).  M <= 16, K % 256 == 0, N % 16 == 0. */
+int vh_gemv_mx8(const uint16_t* x_fq, int64_t M, int64_t K, const uint8_t* w_codes, const uint8_t* w_hb, int64_t N,
+                int32_t mode, int32_t tiles_per_block, const uint16_t* residual, uint16_t* y, uint16_t* fq_out,
+                int32_t* flag, vh_stream_t stream);
+
+/* Bake a KIVI main cache of P = batch x kv-heads sequences of T tokens
+ * (T % 32 == 0, head_dim 128): codes (0..3, one per byte) [P, T, 128] and
+ * bf16 scale / zero point as quantize_affine returns them -- keys
+ * [P, T/32, 128] (grouped along tokens), values [P, T, 4] (grouped along
+ * channels) -- into the attention layout: kc P*T*32 bytes, ks / kz fp16
+ * [P, T/32, 128], vc P*T*32 bytes, vsz fp16 P*T*8. */
+int vh_kivi_bake(const uint8_t* k_codes, const uint16_t* k_scale, const uint16_t* k_zp, const uint8_t* v_codes,
+                 const uint16_t* v_scale, const uint16_t* v_zp, int64_t P, int64_t T, uint8_t* kc, uint16_t* ks,
+                 uint16_t* kz, uint8_t* vc, uint16_t* vsz, vh_stream_t stream);
+
+/* Fill the first n residual slots from k, v [P, n, 128] (bf16): kr
+ * [P, 128 slots, 128] and vr [P, 128 channels, 128 slots] (slot-permuted). */
+int vh_kivi_bake_residual(const uint16_t* k, const uint16_t* v, int64_t P, int64_t n, uint16_t* kr, uint16_t* vr,
+                          vh_stream_t stream);
+
+typedef struct vh_kivi_desc {
+  const uint16_t* qkv;     /* [batch, qkv_ld] bf16: nq query heads, nkv key heads, nkv value heads (pre-RoPE) */
+  int64_t qkv_ld;
+  const uint16_t* cos;     /* [128] bf16 RoPE tables at this step's position */
+  const uint16_t* sin;
+  const uint8_t* kc;       /* main cache (vh_kivi_bake); unused when n_main == 0 */
+  const uint16_t* ks;
+  const uint16_t* kz;
+  const uint8_t* vc;
+  const uint16_t* vsz;
+  uint16_t* kr;            /* residual window (this step's key and value are written to slot n_res) */
+  uint16_t* vr;
+  int64_t batch, nkv, nq, head_dim; /* nq == 4 nkv, head_dim == 128 */
+  int64_t n_main;          /* main-cache tokens (multiple of 32) */
+  int64_t n_res;           /* residual slots filled before this step (< 128) */
+  float softmax_scale;     /* 1 / sqrt(head_dim) */
+  float* part;             /* workspace of part_floats floats */
+  int64_t part_floats;     /* >= batch * nkv * (ceil(n_main / 512) + 1) * 4 * 130 */
+  uint16_t* attn;          /* [batch, nq * 128] bf16 attention output (optional) */
+  uint16_t* attn_fq;       /* [batch, nq * 128] fp16 bits: its MX-int8 fake quantization */
+  int32_t* flag;
+} vh_kivi_desc;
+
+/* Decode attention over main + residual: RoPE on this step's query and key,
+ * the key / value appended at residual slot n_res, then softmax(q K^T *
+ * softmax_scale) V over the n_main + n_res + 1 positions (GQA, 4 query heads
+ * per kv head).  Replaces the split-cache attention of a converted decode
+ * graph (quant_folding.py:2391-2547 read path, eager attention). */
+int vh_kivi_attention(const vh_kivi_desc* desc, vh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

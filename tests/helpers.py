@@ -28,3 +28,16 @@ def max_rel_err(got: torch.Tensor, ref: torch.Tensor) -> float:
     g = got.detach().double().cpu()
     r = ref.detach().double().cpu()
     return float((g - r).abs().max() / r.abs().max().clamp_min(1e-30))
+
+
+def assert_within_bf16_ulps(got, ref64, ulps=1.0, atol=None, what=""):
+    """Each bf16 element of ``got`` within ``ulps`` bf16 ulps of the float64
+    reference ``ref64`` (the ulp of |ref| in bf16), plus ``atol`` (a tensor or
+    scalar: the float32 accumulation error allowance where terms cancel)."""
+    g = got.detach().cpu().double()
+    r = ref64.detach().cpu().double()
+    mag = r.abs().clamp_min(2.0**-126)
+    ulp = torch.pow(2.0, torch.floor(torch.log2(mag)) - 7)
+    lim = ulps * ulp + (0.0 if atol is None else atol)
+    bad = (g - r).abs() > lim
+    assert not bool(bad.any()), f"{what}: {int(bad.sum())} elements beyond {ulps} bf16 ulp(s)"

@@ -1,0 +1,253 @@
+"""The decoder-layer decode step (config 5) on the GPU against the oracle:
+MX-int8 GEMV (exact products, fp32 accumulation), RMSNorm + MX-int8 fake
+quantization, KIVI attention and the whole layer."""
+
+import pytest
+import torch
+
+import voyager_amd  # noqa: F401
+from helpers import assert_within_bf16_ulps, max_rel_err
+from oracle import decode as D
+from voyager_amd import _lib, decode
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _mx_ref(w_gpu):
+    """Reference-form MX-int8 (scale, codes) of a GPU weight, by the
+    parity-tested GPU quantize_mx, on the CPU."""
+    tab = decode.formats.quantization_map("int8", DEV)
+    s, c = torch.ops.quantized_ops.quantize_mx(w_gpu, tab, [-1], 16, 127.0, True)
+    return c.cpu(), s.cpu()
+
+
+@pytest.mark.parametrize("M", [1, 8, 16])
+@pytest.mark.parametrize("K,N", [(4096, 6144), (14336, 4096), (256, 48), (768, 4096)])
+def test_gemv_mx8_store(M, K, N):
+    g = _gen(K + N + M)
+    x = (torch.randn(M, K, generator=g) * 2).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    wg = w.to(DEV)
+    cw, sw = _mx_ref(wg)
+    if N * K <= 4096 * 4096:
+        sw0, cw0 = D.mx8_quantize(w)
+        assert torch.equal(cw0, cw) and torch.equal(sw0, sw)
+    exp = D.mx8_linear(x, cw, sw)
+    flag = decode.ErrorFlag(DEV)
+    wt = decode.quantize_mx8_weight(wg)
+    xq = D.mx8_fake_quant(x)
+    fq = xq.half().to(DEV)
+    ref64, abs64 = _ref64(xq, cw, sw)
+    for tpb in (1, 2) if (N // 16) % 2 == 0 else (1,):
+        got = decode.gemv_mx8(fq, wt, flag, tiles_per_block=tpb)
+        assert got.dtype == torch.bfloat16 and list(got.shape) == [M, N]
+        assert max_rel_err(got, exp) < 1e-2, tpb
+        # exact products and float32 accumulation: the bf16 rounding of the exact sum
+        assert_within_bf16_ulps(got, ref64, 1.0, 2.0**-14 * abs64, f"tiles_per_block={tpb}")
+    flag.check()
+
+
+def _ref64(xq, cw, sw):
+    """float64 x_fq @ (codes * scale)^T and the sum of |terms| per output."""
+    wd = D.O.dequantize_mx_parts(cw, sw, None, 16).double()
+    x64 = xq.double()
+    return x64 @ wd.T, x64.abs() @ wd.abs().T
+
+
+def test_gemv_mx8_residual_and_zero_blocks():
+    g = _gen(7)
+    M, K, N = 8, 1024, 512
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    w[3, 64:128] = 0  # all-zero blocks bake with any exponent
+    w[:, 512:528] = 0
+    r = torch.randn(M, N, generator=g).bfloat16()
+    cw, sw = _mx_ref(w.to(DEV))
+    exp = (D.mx8_linear(x, cw, sw) + r)
+    flag = decode.ErrorFlag(DEV)
+    wt = decode.quantize_mx8_weight(w.to(DEV))
+    xq = D.mx8_fake_quant(x)
+    got = decode.gemv_mx8(xq.half().to(DEV), wt, flag, _lib.GEMV_RESIDUAL, residual=r.to(DEV))
+    assert max_rel_err(got, exp) < 1e-2
+    # bf16(bf16(exact sum) + r): within one ulp of each rounding
+    ref64, abs64 = _ref64(xq, cw, sw)
+    lin = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    lin = decode.gemv_mx8(xq.half().to(DEV), wt, flag, y=lin)
+    assert_within_bf16_ulps(lin, ref64, 1.0, 2.0**-14 * abs64, "linear part")
+    assert torch.equal(got.cpu(), (lin.cpu() + r))
+    flag.check()
+
+
+def test_gemv_mx8_weight_range_error():
+    w = torch.zeros(16, 256, dtype=torch.bfloat16, device=DEV)
+    w[0, 0] = 2.0**-40  # block exponent -46: not representable in the fp16 operand
+    with pytest.raises(RuntimeError, match="weight block exponent"):
+        decode.quantize_mx8_weight(w)
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_gemv_mx8_swiglu(M):
+    g = _gen(11 + M)
+    K, F = 1024, 768
+    x = torch.randn(M, K, generator=g).bfloat16()
+    wg_, wu_ = (torch.randn(F, K, generator=g) * 0.05).bfloat16(), (torch.randn(F, K, generator=g) * 0.05).bfloat16()
+    cg, sg = _mx_ref(wg_.to(DEV))
+    cu, su = _mx_ref(wu_.to(DEV))
+    act = torch.nn.functional.silu(D.mx8_linear(x, cg, sg)) * D.mx8_linear(x, cu, su)
+    flag = decode.ErrorFlag(DEV)
+    wt = decode.quantize_mx8_weight(torch.cat((wg_, wu_)).to(DEV), paired=True)
+    y = torch.empty(M, F, dtype=torch.bfloat16, device=DEV)
+    fq = decode.gemv_mx8(D.mx8_fake_quant(x).half().to(DEV), wt, flag, _lib.GEMV_SWIGLU, y=y)
+    assert max_rel_err(y, act) < 1e-2
+    # the fake quantization is the oracle's quantize_mx of the kernel's own product, bit for bit
+    assert torch.equal(fq.cpu(), D.mx8_fake_quant(y.cpu()).half())
+    flag.check()
+
+
+@pytest.mark.parametrize("M,H", [(8, 4096), (3, 14336), (1, 256)])
+def test_rmsnorm_mx8(M, H):
+    g = _gen(H + M)
+    x = (torch.randn(M, H, generator=g) * 3).bfloat16()
+    w = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16()
+    exp = D.rms_norm(x, w, 1e-5)
+    flag = decode.ErrorFlag(DEV)
+    h = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    fq = decode.rmsnorm_mx8(x.to(DEV), w.to(DEV), 1e-5, flag, h_out=h)
+    hc = h.cpu()
+    # the row sum of squares is accumulated in another order: at most one bf16 ulp apart
+    diff = (hc.view(torch.int16).int() - exp.view(torch.int16).int()).abs()
+    assert int(diff.max()) <= 1 and float((diff > 0).float().mean()) < 0.01
+    assert torch.equal(fq.cpu(), D.mx8_fake_quant(hc).half())
+    flag.check()
+
+
+def test_fq_range_flag():
+    # one nonzero element: rsqrt(mean(x**2)) = 16, so the normed value is
+    # 16 * 8192 = 2**17 and its block's fake-quantized values exceed fp16
+    x = torch.zeros(1, 256, dtype=torch.bfloat16)
+    x[0, 0] = 1.0
+    flag = decode.ErrorFlag(DEV)
+    decode.rmsnorm_mx8(x.to(DEV), torch.full((256,), 8192.0, dtype=torch.bfloat16, device=DEV), 1e-5, flag)
+    with pytest.raises(RuntimeError, match="fp16 range"):
+        flag.check()
+
+
+def _attention_case(B, nkv, n_main, n_res, seed):
+    g = _gen(seed)
+    nq = 4 * nkv
+    qkv = torch.randn(B, (nq + 2 * nkv) * 128, generator=g).bfloat16()
+    k_main = torch.randn(B, nkv, n_main, 128, generator=g).bfloat16()
+    v_main = torch.randn(B, nkv, n_main, 128, generator=g).bfloat16()
+    k_res = torch.randn(B, nkv, n_res, 128, generator=g).bfloat16()
+    v_res = torch.randn(B, nkv, n_res, 128, generator=g).bfloat16()
+    return nq, qkv, k_main, v_main, k_res, v_res
+
+
+def _expected_attention(nq, nkv, qkv, k_deq, v_deq, k_res, v_res, cos, sin):
+    B = qkv.shape[0]
+    q = qkv[:, : nq * 128].view(B, 1, nq, 128).transpose(1, 2)
+    k = qkv[:, nq * 128:(nq + nkv) * 128].view(B, 1, nkv, 128).transpose(1, 2)
+    v = qkv[:, (nq + nkv) * 128:].view(B, 1, nkv, 128).transpose(1, 2)
+    c, s = cos[:, None, None, :], sin[:, None, None, :]
+    q, k = D.apply_rope(q, c, s), D.apply_rope(k, c, s)
+    keys = torch.cat((k_deq, k_res, k), dim=2)
+    values = torch.cat((v_deq, v_res, v), dim=2)
+    exp = D.eager_attention(q, keys, values, 128 ** -0.5).reshape(B, nq * 128)
+    # the same attention in float64 (no bf16 rounding after the dequantize)
+    grp = nq // nkv
+    K64, V64 = keys.double().repeat_interleave(grp, 1), values.double().repeat_interleave(grp, 1)
+    w64 = torch.softmax((q.double() @ K64.transpose(2, 3)) * 128 ** -0.5, dim=-1)
+    exp64 = (w64 @ V64).transpose(1, 2).reshape(B, nq * 128)
+    return exp, exp64, k, v
+
+
+@pytest.mark.parametrize("B,nkv,n_main,n_res", [(2, 2, 96, 5), (1, 1, 0, 0), (2, 1, 544, 127), (1, 2, 512, 31),
+                                                (8, 8, 3968, 127)])
+def test_kivi_attention(B, nkv, n_main, n_res):
+    nq, qkv, k_main, v_main, k_res, v_res = _attention_case(B, nkv, n_main, n_res, 100 + n_main + n_res)
+    cache, kq, vq = decode.KiviCache.from_bf16(k_main.to(DEV), v_main.to(DEV), k_res.to(DEV), v_res.to(DEV))
+    if n_main:
+        if B * nkv * n_main <= 64 * 1024:
+            ks, kz, kc = D.kivi_quantize(k_main, -2)
+            assert torch.equal(kc, kq[2].cpu()) and torch.equal(ks, kq[0].cpu()) and torch.equal(kz, kq[1].cpu())
+        k_deq = D.kivi_dequantize(kq[2].cpu(), kq[0].cpu(), kq[1].cpu(), -2)
+        v_deq = D.kivi_dequantize(vq[2].cpu(), vq[0].cpu(), vq[1].cpu(), -1)
+    else:
+        k_deq = v_deq = torch.zeros(B, nkv, 0, 128, dtype=torch.bfloat16)
+    pos = n_main + n_res
+    cos, sin = D.rope_cos_sin(torch.tensor([pos]), 128, 5e5)
+    exp, exp64, k_new, v_new = _expected_attention(nq, nkv, qkv, k_deq, v_deq, k_res, v_res, cos, sin)
+    flag = decode.ErrorFlag(DEV)
+    attn = torch.empty(B, nq * 128, dtype=torch.bfloat16, device=DEV)
+    fq = decode.kivi_attention(qkv.to(DEV), cache, cos[0].to(DEV), sin[0].to(DEV), nq, flag, attn=attn)
+    assert cache.n_res == n_res + 1
+    # The reference's eager bf16 chain (scores, scaled scores and probabilities
+    # each rounded to bf16) is itself up to ~1% (max-abs-normalized) away from
+    # float64 at these lengths; the kernel keeps float32 and fp16 operands:
+    # bf16 output rounding alone is up to 2**-9 of each element
+    assert max_rel_err(attn, exp64) < 5e-3
+    assert max_rel_err(attn, exp) < max_rel_err(exp, exp64) + 1e-2
+    assert torch.equal(fq.cpu(), D.mx8_fake_quant(attn.cpu()).half())
+    # the step's key (after RoPE) and value landed in the residual window
+    kr, vr = cache.residual_tokens(n_res + 1)
+    assert torch.equal(kr[:, :, :n_res].cpu(), k_res) and torch.equal(vr[:, :, :n_res].cpu(), v_res)
+    assert torch.equal(kr[:, :, n_res:].cpu(), k_new) and torch.equal(vr[:, :, n_res:].cpu(), v_new)
+    flag.check()
+
+
+def test_decode_layer_cfg5():
+    """Config 5: one random-init Llama-3.1-8B-architecture layer, decode at
+    batch 8 over a 4096-token context (3968 KIVI tokens + 127 residual +
+    this step's), every linear MX-int8 bs=16, against the oracle layer on the
+    same quantized weights and cache."""
+    cfg = D.Config()
+    w = D.random_layer(cfg, seed=0)
+    wd = {k: v.to(DEV) for k, v in w.items()}
+    mx = {k: _mx_ref(wd[k]) for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")}
+    layer = decode.DecoderLayer(wd, cfg.n_heads, cfg.n_kv_heads, cfg.eps, cfg.rope_theta, max_batch=8, max_pos=4096)
+    g = _gen(1)
+    B, n_main, n_res = 8, 3968, 127
+    k_main = torch.randn(B, 8, n_main, 128, generator=g).bfloat16()
+    v_main = torch.randn(B, 8, n_main, 128, generator=g).bfloat16()
+    k_res = torch.randn(B, 8, n_res, 128, generator=g).bfloat16()
+    v_res = torch.randn(B, 8, n_res, 128, generator=g).bfloat16()
+    x = torch.randn(B, cfg.hidden, generator=g).bfloat16()
+    cache, kq, vq = decode.KiviCache.from_bf16(k_main.to(DEV), v_main.to(DEV), k_res.to(DEV), v_res.to(DEV))
+    k_past = torch.cat((D.kivi_dequantize(kq[2].cpu(), kq[0].cpu(), kq[1].cpu(), -2), k_res), dim=2)
+    v_past = torch.cat((D.kivi_dequantize(vq[2].cpu(), vq[0].cpu(), vq[1].cpu(), -1), v_res), dim=2)
+    pos = n_main + n_res
+    cos, sin = D.rope_cos_sin(torch.tensor([pos]), 128, cfg.rope_theta)
+    assert torch.equal(layer.rope[0, pos].cpu(), cos[0]) and torch.equal(layer.rope[1, pos].cpu(), sin[0])
+    exp = D.decode_layer(x, w, k_past, v_past, cos, sin, cfg, mx=mx)
+    out = layer.step(x.to(DEV), cache, pos)
+    torch.cuda.synchronize()
+    layer.flag.check()
+    b = {k: v[:B] for k, v in layer.buf.items()}
+    # Every quantized stage is the reference op sequence bit for bit when fed
+    # the oracle's own inputs (isolating it from upstream differences):
+    assert torch.equal(b["qkv"].cpu(), torch.cat([D.mx8_linear(exp["h1"], *mx[k]) for k in ("wq", "wk", "wv")], -1))
+    f = decode.ErrorFlag(DEV)
+    o = decode.gemv_mx8(D.mx8_fake_quant(exp["attn"]).half().to(DEV), layer.o, f, _lib.GEMV_RESIDUAL,
+                        residual=x.to(DEV))
+    assert torch.equal(o.cpu(), exp["x1"])
+    act = torch.empty(B, cfg.intermediate, dtype=torch.bfloat16, device=DEV)
+    decode.gemv_mx8(D.mx8_fake_quant(exp["h2"]).half().to(DEV), layer.gate_up, f, _lib.GEMV_SWIGLU, y=act)
+    assert torch.equal(act.cpu(), exp["act"])
+    d = decode.gemv_mx8(D.mx8_fake_quant(exp["act"]).half().to(DEV), layer.down, f, _lib.GEMV_RESIDUAL,
+                        residual=exp["x1"].to(DEV))
+    assert torch.equal(d.cpu(), exp["out"])
+    f.check()
+    # End to end the layer differs only through attention, whose float32 /
+    # fp16-operand result (checked against float64 in test_kivi_attention) is
+    # ~1.5% (max-abs-normalized) from the reference's bf16 eager chain; the
+    # MX re-quantization of x1 / act carries that into a few bf16 ulps of out.
+    assert max_rel_err(b["attn"], exp["attn"]) < 2e-2
+    assert max_rel_err(b["x1"], exp["x1"]) < 1e-2
+    assert max_rel_err(b["act"], exp["act"]) < 2e-2
+    assert max_rel_err(out, exp["out"]) < 2e-2

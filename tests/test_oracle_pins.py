@@ -359,3 +359,90 @@ def test_linear_mx_against_float64_matmul():
     ref = xd @ wd.T
     err = np.abs(y.double().numpy() - ref).max() / np.abs(ref).max()
     assert y.dtype == torch.bfloat16 and err < 1e-2
+
+
+# ------------------------------------------------------------ decoder layer
+def _hf_layer(cfg, weights):
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaDecoderLayer, LlamaRotaryEmbedding
+
+    hc = LlamaConfig(hidden_size=cfg.hidden, num_attention_heads=cfg.n_heads, num_key_value_heads=cfg.n_kv_heads,
+                     head_dim=cfg.head_dim, intermediate_size=cfg.intermediate, rope_theta=cfg.rope_theta,
+                     rms_norm_eps=cfg.eps, max_position_embeddings=4096)
+    hc._attn_implementation = "eager"
+    layer = LlamaDecoderLayer(hc, layer_idx=0).to(torch.bfloat16).eval()
+    names = {"input_layernorm.weight": "ln1", "post_attention_layernorm.weight": "ln2",
+             "self_attn.q_proj.weight": "wq", "self_attn.k_proj.weight": "wk", "self_attn.v_proj.weight": "wv",
+             "self_attn.o_proj.weight": "wo", "mlp.gate_proj.weight": "wg", "mlp.up_proj.weight": "wu",
+             "mlp.down_proj.weight": "wd"}
+    state = {k: weights[v] for k, v in names.items()}
+    layer.load_state_dict(state, strict=True)
+    return layer, LlamaRotaryEmbedding(hc)
+
+
+def test_decode_layer_matches_transformers():
+    """With plain bf16 linears and an unquantized cache, the oracle's decode
+    step is transformers' LlamaDecoderLayer (eager attention, default RoPE)
+    bit for bit -- the reference's pinned dependency (pyproject.toml:37)."""
+    from transformers.cache_utils import DynamicCache
+
+    from oracle import decode as D
+
+    cfg = D.Config(hidden=256, n_heads=8, n_kv_heads=2, head_dim=32, intermediate=512)
+    w = D.random_layer(cfg, seed=3)
+    layer, rotary = _hf_layer(cfg, w)
+    g = torch.Generator().manual_seed(4)
+    B, T = 3, 45
+    x = torch.randn(B, cfg.hidden, generator=g).bfloat16()
+    k_past = torch.randn(B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).bfloat16()
+    v_past = torch.randn(B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).bfloat16()
+    cos, sin = D.rope_cos_sin(torch.tensor([T]), cfg.head_dim, cfg.rope_theta)
+    ours = D.decode_layer(x, w, k_past, v_past, cos, sin, cfg)["out"]
+    pos = torch.full((B, 1), T, dtype=torch.long)
+    pe = rotary(x[:, None, :], pos)
+    assert torch.equal(pe[0][0, 0], cos[0]) and torch.equal(pe[1][0, 0], sin[0])
+    cache = DynamicCache()
+    cache.update(k_past.clone(), v_past.clone(), 0)
+    with torch.no_grad():
+        ref = layer(x[:, None, :], attention_mask=None, position_ids=pos, past_key_values=cache, use_cache=True,
+                    position_embeddings=pe)
+    ref = ref[0] if isinstance(ref, tuple) else ref
+    assert torch.equal(ours, ref.reshape(B, cfg.hidden))
+
+
+def test_kivi_round_trip_float64():
+    """quantize_affine + dequantize with the KIVI spec (uint2, group 32,
+    fp16 scale / zero point) against the affine formula in float64: codes are
+    round-half-even((x - min) / s) clamped to [0, 3] with s = fp16((max - min) / 3)
+    and zp = fp16(-min / s), and the round trip is (code - zp) * s."""
+    import numpy as np
+
+    from oracle import decode as D
+
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(2, 3, 64, 64, generator=g) * 2).bfloat16()
+    for axis in (-2, -1):
+        s, z, c = D.kivi_quantize(x, axis)
+        xr = x.float().numpy()
+        if axis == -2:
+            blk = xr.reshape(2, 3, 2, 32, 64)
+            lo, hi = blk.min(axis=3), blk.max(axis=3)
+            rep = lambda a: np.repeat(a, 32, axis=2)
+        else:
+            blk = xr.reshape(2, 3, 64, 2, 32)
+            lo, hi = blk.min(axis=4), blk.max(axis=4)
+            rep = lambda a: np.repeat(a, 32, axis=3)
+        bf = lambda a: torch.from_numpy(np.asarray(a, dtype=np.float32)).bfloat16().float().numpy()
+        sc = bf(bf(hi - lo) / 3.0)
+        sc = np.where(sc > 0, sc, 1.0).astype(np.float32)
+        sc = bf(sc.astype(np.float16).astype(np.float32))
+        zp = bf(bf(bf(-lo) / sc))
+        zp = bf(zp.astype(np.float16).astype(np.float32))
+        assert np.array_equal(s.float().numpy(), sc)
+        assert np.array_equal(z.float().numpy(), zp)
+        q = bf(bf(xr / rep(sc)) + rep(zp))
+        codes = np.clip(np.round(q), 0, 3)
+        assert np.array_equal(c.float().numpy(), codes)
+        deq = D.kivi_dequantize(c, s, z, axis).double().numpy()
+        ref = bf(bf(codes - rep(zp)) * rep(sc))
+        assert np.allclose(deq, ref, rtol=0, atol=0)

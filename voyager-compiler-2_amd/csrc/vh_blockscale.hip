@@ -40,10 +40,6 @@ struct Params {
   const uint8_t* code_lut;  // packed codes are remapped through this (or null)
 };
 
-// NaN-propagating max/min, as torch.amax / torch.amin.
-VH_DEV float nmax(float a, float b) { return isnan_f(a) ? a : (isnan_f(b) ? b : fmaxf(a, b)); }
-VH_DEV float nmin(float a, float b) { return isnan_f(a) ? a : (isnan_f(b) ? b : fminf(a, b)); }
-
 VH_DEV float load_x(const void* p, int dt, int64_t i) {
   if (dt == VH_BF16) return bf2f(((const uint16_t*)p)[i]);
   if (dt == VH_F16) return __half2float(((const __half*)p)[i]);

@@ -109,7 +109,20 @@ _SIGNATURES = {
     "vh_pack_nf4": ([_P, _I64, _I64, _P, _P], _I32),
     # x_levels, x_scale, M, w_packed, w_scale, w_scale_fmt, levels16 (host), N, K, epilogue*, y, stream
     "vh_gemv_nf4": ([_P, _P, _I64, _P, _P, ctypes.POINTER(Format), _P, _I64, _I64, _P, _P, _P], _I32),
+    # decoder-layer decode step
+    "vh_rmsnorm_mx8": ([_P, _P, _I64, _I64, _F32, _P, _P, _P, _P], _I32),
+    "vh_mx8_bake": ([_P, _P, _I32, _I64, _I64, _I32, _P, _P, _P, _P], _I32),
+    "vh_gemv_mx8": ([_P, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P], _I32),
+    "vh_kivi_bake": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P], _I32),
+    "vh_kivi_bake_residual": ([_P, _P, _I64, _I64, _P, _P, _P], _I32),
+    # vh_kivi_attention takes a vh_kivi_desc*; voyager_amd.decode.KiviDesc mirrors it.
+    "vh_kivi_attention": ([_P, _P], _I32),
 }
+
+DECODE_ERR_FP16_RANGE = 1
+DECODE_ERR_WEIGHT_RANGE = 2
+KIVI_RES_CAP = 128
+GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
 
 #: Every symbol ``include/voyager_hip.h`` declares.
 EXPORTED = tuple(_SIGNATURES)
