@@ -255,14 +255,15 @@ int vh_gemv_mx8(const uint16_t* x_fq, int64_t M, int64_t K, const uint8_t* w_cod
  * (T % 32 == 0, head_dim 128): codes (0..3, one per byte) [P, T, 128] and
  * bf16 scale / zero point as quantize_affine returns them -- keys
  * [P, T/32, 128] (grouped along tokens), values [P, T, 4] (grouped along
- * channels) -- into the attention layout: kc P*T*32 bytes, ks / kz fp16
- * [P, T/32, 128], vc P*T*32 bytes, vsz fp16 P*T*8. */
+ * channels) -- into the attention layout: one 3072-byte block per 32 tokens
+ * (key codes, value codes, key and value scale / zero point as fp16),
+ * main_out P*T*96 bytes. */
 int vh_kivi_bake(const uint8_t* k_codes, const uint16_t* k_scale, const uint16_t* k_zp, const uint8_t* v_codes,
-                 const uint16_t* v_scale, const uint16_t* v_zp, int64_t P, int64_t T, uint8_t* kc, uint16_t* ks,
-                 uint16_t* kz, uint8_t* vc, uint16_t* vsz, vh_stream_t stream);
+                 const uint16_t* v_scale, const uint16_t* v_zp, int64_t P, int64_t T, uint8_t* main_out,
+                 vh_stream_t stream);
 
-/* Fill the first n residual slots from k, v [P, n, 128] (bf16): kr
- * [P, 128 slots, 128] and vr [P, 128 channels, 128 slots] (slot-permuted). */
+/* Fill the first n residual slots from k, v [P, n, 128] (bf16): kr and vr
+ * are [P, 128 slots, 128] bf16. */
 int vh_kivi_bake_residual(const uint16_t* k, const uint16_t* v, int64_t P, int64_t n, uint16_t* kr, uint16_t* vr,
                           vh_stream_t stream);
 
@@ -271,11 +272,7 @@ typedef struct vh_kivi_desc {
   int64_t qkv_ld;
   const uint16_t* cos;     /* [128] bf16 RoPE tables at this step's position */
   const uint16_t* sin;
-  const uint8_t* kc;       /* main cache (vh_kivi_bake); unused when n_main == 0 */
-  const uint16_t* ks;
-  const uint16_t* kz;
-  const uint8_t* vc;
-  const uint16_t* vsz;
+  const uint8_t* main;     /* main cache (vh_kivi_bake); unused when n_main == 0 */
   uint16_t* kr;            /* residual window (this step's key and value are written to slot n_res) */
   uint16_t* vr;
   int64_t batch, nkv, nq, head_dim; /* nq == 4 nkv, head_dim == 128 */
@@ -283,7 +280,7 @@ typedef struct vh_kivi_desc {
   int64_t n_res;           /* residual slots filled before this step (< 128) */
   float softmax_scale;     /* 1 / sqrt(head_dim) */
   float* part;             /* workspace of part_floats floats */
-  int64_t part_floats;     /* >= batch * nkv * (ceil(n_main / 512) + 1) * 4 * 130 */
+  int64_t part_floats;     /* >= batch * nkv * ceil(n_main / 512) * 4 * 130 */
   uint16_t* attn;          /* [batch, nq * 128] bf16 attention output (optional) */
   uint16_t* attn_fq;       /* [batch, nq * 128] fp16 bits: its MX-int8 fake quantization */
   int32_t* flag;

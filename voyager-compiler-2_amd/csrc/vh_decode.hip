@@ -38,8 +38,8 @@ constexpr int HEAD_DIM = 128;
 constexpr int GQA = 4;        // query heads per kv head
 constexpr int KV_GROUP = 32;  // KIVI group: tokens per key group, channels per value group
 constexpr int ATT_WAVES = 4;
-constexpr int STEPS_PER_WAVE = 4;
-constexpr int STEPS_PER_SPLIT = ATT_WAVES * STEPS_PER_WAVE;
+constexpr int GROUPS_PER_WAVE = 4;  // one super-step of 128 tokens per wave
+constexpr int STEPS_PER_SPLIT = ATT_WAVES * GROUPS_PER_WAVE;
 constexpr int RES_CAP = VH_KIVI_RES_CAP;
 constexpr int PART = HEAD_DIM + 2;  // m, l, o[128]
 
@@ -337,30 +337,31 @@ __global__ void __launch_bounds__(256) k_bake_mx8_scales(const uint8_t* __restri
 }
 
 // ------------------------------------------------------------ KIVI attention
-// Cache layouts (P = batch x kv heads, G = main groups of 32 tokens):
-//   keys:   codes [P][G][2 tiles][64 lanes][8 B]; lane l of tile t holds
-//           token 32 g + 16 t + l % 16, channels 32 cs + 8 (l / 16) + j as
-//           2-bit fields (dword cs / 2; pair (cs % 2) 4 + p at bits 2k and
-//           16 + 2k for j = 2p, 2p + 1); scale, zp fp16 [P][G][128].
-//   values: codes [P][G][64 lanes][16 B]; lane l dword d holds tiles 2d, 2d+1:
-//           channel 16 r8 + l % 16 at tokens tok(l / 16, j), pair hh 4 + p for
-//           j = 2p, 2p + 1; scale/zp fp16 [P][G][4][8][4 groups][2] for
-//           tokens tok(q, j).  tok(q, j) = 16 (j / 4) + 4 q + j % 4 is the
-//           token the score MFMA leaves in lane group q, register j % 4 of
-//           tile j / 4.
-//   residual: keys bf16 [P][RES_CAP][128]; values bf16 [P][128][RES_CAP]
-//           with the slots of each 32-block permuted so tok(q, j) sits at
-//           8 q + j.
+// Main-cache layout (P = batch x kv heads, G = groups of 32 tokens): one
+// 3 KB block per (P, g), read by one wave with three 16-byte loads per lane
+// and staged through LDS:
+//   [0, 1024)     key codes [2 tiles][64 lanes][8 B]: lane l of tile t holds
+//                 token 32 g + 16 t + l % 16, channels 32 cs + 8 (l / 16) + j
+//                 as 2-bit fields (dword cs / 2; pair (cs % 2) 4 + p at bits
+//                 2k and 16 + 2k for j = 2p, 2p + 1).
+//   [1024, 2048)  value codes [64 lanes][16 B]: lane l dword d holds tiles
+//                 2d, 2d + 1 (channel 16 r8 + l % 16) at tokens tok(l / 16, j),
+//                 pair hh 4 + p for j = 2p, 2p + 1.
+//   [2048, 2560)  key scale / zero point fp16 [4 cs][4 q][8 scale, 8 zp] for
+//                 channels 32 cs + 8 q + j (the group's per-channel affine).
+//   [2560, 3072)  value scale / zero point fp16 [4 q][8 j][4 groups][2] of
+//                 token tok(q, j) (per-token affine of each 32 channels).
+// tok(q, j) = 16 (j / 4) + 4 q + j % 4 is the token the score MFMA leaves in
+// lane group q, register j % 4 of tile j / 4.
+// Residual window: keys and values bf16 [P][RES_CAP][128].
+constexpr int GROUP_BYTES = 3072;
+
 struct KiviArgs {
   const uint16_t* qkv;
   int64_t qkv_ld;
   const uint16_t* cos;
   const uint16_t* sin;
-  const uint8_t* kc;
-  const _Float16* ks;
-  const _Float16* kz;
-  const uint8_t* vc;
-  const _Float16* vsz;
+  const uint8_t* main;
   uint16_t* kr;
   uint16_t* vr;
   int32_t n_groups, n_res, nkv, nq, splits;
@@ -368,7 +369,6 @@ struct KiviArgs {
   float* part;
 };
 
-VH_DEV int res_phys(int slot) { return (slot & ~31) | (((slot >> 2) & 3) << 3) | (((slot >> 4) & 1) << 2) | (slot & 3); }
 
 VH_DEV uint16_t rope1(const uint16_t* base, const uint16_t* cs, const uint16_t* sn, int c) {
   const float x = bf2f(base[c]);
@@ -376,191 +376,251 @@ VH_DEV uint16_t rope1(const uint16_t* base, const uint16_t* cs, const uint16_t* 
   return (uint16_t)f2bf(rbf(x * bf2f(cs[c])) + rbf(xr * bf2f(sn[c])));
 }
 
-// Two 2-bit fields (bits 2k and 16 + 2k) as an exact fp16 pair.
-VH_DEV uint32_t code_pair(uint32_t w, int k) {
-  const uint32_t v = ((w >> (2 * k)) & 0x00030003u) | 0x64006400u;  // 1024 + c
-  const f16x2 h = __builtin_bit_cast(f16x2, v) - (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
-  return __builtin_bit_cast(uint32_t, h);
-}
-
 VH_DEV uint32_t pack_h2(float a, float b) {
   const f16x2 h = {(_Float16)a, (_Float16)b};
   return __builtin_bit_cast(uint32_t, h);
 }
 
-template <bool RESID>
-__device__ __forceinline__ void kivi_split(const KiviArgs& a, uint16_t (*s_q)[HEAD_DIM], float (*s_part)[GQA][PART]) {
+// Cross-lane reductions: DPP row rotations (row_ror:4 / :8, lane i reads
+// lane (i - 4) / (i - 8) mod 16 of its row) combine the four group columns of
+// a head (lanes n, n + 4, n + 8, n + 12 of a 16-lane row).
+VH_DEV float ror4(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+}
+VH_DEV float ror8(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+}
+// lane l and lane l ^ 16 (l ^ 32)
+VH_DEV float sum_x16(float v) { return v + __shfl_xor(v, 16); }
+VH_DEV float sum_x32(float v) { return v + __shfl_xor(v, 32); }
+VH_DEV float max_x16(float v) { return fmaxf(v, __shfl_xor(v, 16)); }
+VH_DEV float max_x32(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
+
+// Code operands: the pair of 2-bit fields at bits 2p and 16 + 2p of W
+// becomes the fp16 pair (1024 + c * 4**p), one v_and_or_b32 with a mask
+// held in a VGPR; the 4**-p goes into the other operand.  mk[p] =
+// 0x00030003 << 2p.
+struct CodeMasks {
+  uint32_t mk[4];
+};
+
+VH_DEV CodeMasks code_masks() {
+  CodeMasks m;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) asm volatile("v_mov_b32 %0, %1" : "=v"(m.mk[p]) : "i"(0x00030003u << (2 * p)));
+  return m;
+}
+
+// The four operand dwords of pairs kb .. kb + 3 (kb = 0 or 4) of W.
+VH_DEV f16x8 code_operand(uint32_t W, int kb, const CodeMasks& m) {
+  const uint32_t w = kb ? (W >> 8) : W;
+  return __builtin_bit_cast(f16x8, make_uint4((w & m.mk[0]) | 0x64006400u, (w & m.mk[1]) | 0x64006400u,
+                                              (w & m.mk[2]) | 0x64006400u, (w & m.mk[3]) | 0x64006400u));
+}
+
+VH_DEV uint4 sel4(bool c, const uint4& v) { return c ? v : make_uint4(0u, 0u, 0u, 0u); }
+
+constexpr float V_SCALE = 256.0f;  // value operands carry 2**8 (kept clear of fp16 subnormals)
+
+// One super-step (ng of 4 consecutive 32-token groups staged at blk0) for one
+// wave, from a fresh softmax state.  MFMA column n = lane % 16 is (group
+// gq = n / 4, head h = n % 4): the lane's B operands (q * s for keys, p * s
+// for values) are built once, for its own group.  Scores come from per-group
+// accumulators (each column reads its own group's); the value MFMAs take the
+// operand masked to the group.  The +1024 offset of the code operands is one
+// MFMA against a constant operand.  Outputs: the head's max m (all lanes of
+// the head), the lane's partial sum, acc (o^T, scaled by V_SCALE, column n)
+// and zt (the zero-point and offset terms of column n, per channel group,
+// partial over the lane group q).
+VH_DEV void main_superstep(const uint8_t* blk0, int ng, const uint4 (&qh)[4], int lane, float scale_log2, float& m,
+                           float& lsum, f32x4 (&acc)[8], float (&zt)[4]) {
+  const int n = lane & 15, q = lane >> 4, gq = n >> 2;
+  const bool own_live = gq < ng;
+  const uint8_t* own = blk0 + gq * GROUP_BYTES;
+  const CodeMasks cm = code_masks();
+  const f16x8 ONE = __builtin_bit_cast(f16x8, make_uint4(0x64006400u, 0x64006400u, 0x64006400u, 0x64006400u));
+  // keys: (q * s) * 4**-p of the own group (fp16) and the zero-point term
+  f16x8 Bk[4];
+  float bias = 0.0f;
+#pragma unroll
+  for (int cs = 0; cs < 4; ++cs) {
+    const f16x8 sv = *(const f16x8*)(own + 2048 + (cs * 4 + q) * 32);
+    const f16x8 zv = *(const f16x8*)(own + 2048 + (cs * 4 + q) * 32 + 16);
+    const uint32_t qw[4] = {qh[cs].x, qh[cs].y, qh[cs].z, qh[cs].w};
+    uint32_t bq[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float q0 = bf2f(qw[p] & 0xffffu) * (float)sv[2 * p];
+      const float q1 = bf2f(qw[p] >> 16) * (float)sv[2 * p + 1];
+      bias = fmaf(q0, (float)zv[2 * p], bias);
+      bias = fmaf(q1, (float)zv[2 * p + 1], bias);
+      const float f = 1.0f / (float)(1 << (2 * p));
+      bq[p] = pack_h2(q0 * f, q1 * f);
+    }
+    Bk[cs] = __builtin_bit_cast(f16x8, make_uint4(bq[0], bq[1], bq[2], bq[3]));
+  }
+  f32x4 Sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int cs = 0; cs < 4; ++cs) Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ONE, Bk[cs], Sc, 0, 0, 0);
+  f32x4 S[4][2];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    S[g][0] = {0.0f, 0.0f, 0.0f, 0.0f};
+    S[g][1] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (g >= ng) continue;
+    const uint8_t* blk = blk0 + g * GROUP_BYTES;
+    const uint2 kc0 = *(const uint2*)(blk + lane * 8);
+    const uint2 kc1 = *(const uint2*)(blk + 512 + lane * 8);
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs) {
+      const int kb = (cs & 1) * 4;
+      S[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(cs < 2 ? kc0.x : kc0.y, kb, cm), Bk[cs], S[g][0],
+                                                      0, 0, 0);
+      S[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(cs < 2 ? kc1.x : kc1.y, kb, cm), Bk[cs], S[g][1],
+                                                      0, 0, 0);
+    }
+  }
+  bias = sum_x32(sum_x16(bias));
+  const float off = Sc[0] + bias;
+  float sc[2][4];
+  float mloc = -__builtin_inff();
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = gq == 0 ? S[0][t][r] : gq == 1 ? S[1][t][r] : gq == 2 ? S[2][t][r] : S[3][t][r];
+      sc[t][r] = own_live ? (v - off) * scale_log2 : -__builtin_inff();
+      mloc = fmaxf(mloc, sc[t][r]);
+    }
+  mloc = fmaxf(mloc, ror4(mloc));
+  mloc = fmaxf(mloc, ror8(mloc));
+  m = max_x32(max_x16(mloc));
+  float p[8];
+  lsum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p[j] = exp2f(sc[j >> 2][j & 3] - m);
+    lsum += p[j];
+  }
+  // values: (p * s) * 2**8 * 4**-pp of the own group per channel group
+  f16x8 Bv[4];
+#pragma unroll
+  for (int gc = 0; gc < 4; ++gc) {
+    uint32_t pw[4];
+    zt[gc] = 0.0f;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const f16x8 e0 = *(const f16x8*)(own + 2560 + (q * 8 + 2 * pp) * 16);
+      const f16x8 e1 = *(const f16x8*)(own + 2560 + (q * 8 + 2 * pp + 1) * 16);
+      // (an absent group's block is a staged copy of a present one: finite, and its p are 0)
+      const float p0 = p[2 * pp] * (float)e0[2 * gc], p1 = p[2 * pp + 1] * (float)e1[2 * gc];
+      zt[gc] = fmaf(p0, (float)e0[2 * gc + 1], zt[gc]);
+      zt[gc] = fmaf(p1, (float)e1[2 * gc + 1], zt[gc]);
+      const float f = V_SCALE / (float)(1 << (2 * pp));
+      pw[pp] = pack_h2(p0 * f, p1 * f);
+    }
+    Bv[gc] = __builtin_bit_cast(f16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    // the +1024 offset of the value codes, for this column (lane group 0 only)
+    f32x4 vc = {0.0f, 0.0f, 0.0f, 0.0f};
+    vc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ONE, Bv[gc], vc, 0, 0, 0);
+    if (q == 0) zt[gc] += vc[0] * (1.0f / V_SCALE);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    if (g >= ng) break;
+    const uint4 vcode = *(const uint4*)(blk0 + g * GROUP_BYTES + 1024 + lane * 16);
+    const uint32_t vw[4] = {vcode.x, vcode.y, vcode.z, vcode.w};
+    f16x8 Bm[4];
+#pragma unroll
+    for (int gc = 0; gc < 4; ++gc) Bm[gc] = __builtin_bit_cast(f16x8, sel4(gq == g, __builtin_bit_cast(uint4, Bv[gc])));
+#pragma unroll
+    for (int r8 = 0; r8 < 8; ++r8)
+      acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(vw[r8 >> 1], (r8 & 1) * 4, cm), Bm[r8 >> 1],
+                                                      acc[r8], 0, 0, 0);
+  }
+}
+
+// Workgroups (split, P) stream the main cache: each wave stages one
+// super-step (GROUPS_PER_WAVE groups, 12 KB) in LDS and computes it.
+__global__ void __launch_bounds__(ATT_WAVES * 64) k_kivi_split(KiviArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
+  __shared__ __attribute__((aligned(16))) uint4 s_stage[ATT_WAVES][GROUPS_PER_WAVE * GROUP_BYTES / 16];
+  float (*s_part)[GQA][PART] = (float (*)[GQA][PART])&s_stage[0][0];  // reused once the waves are done
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int P = blockIdx.y, split = blockIdx.x;
   const int b = P / a.nkv, kvh = P % a.nkv;
+  const int n = lane & 15, q = lane >> 4;
   const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
-  for (int i = tid; i < 16 * HEAD_DIM; i += ATT_WAVES * 64) {
-    const int h = i / HEAD_DIM, c = i % HEAD_DIM;
-    s_q[h][c] = h < GQA ? rope1(qrow + (kvh * GQA + h) * HEAD_DIM, a.cos, a.sin, c) : (uint16_t)0;
+
+  // this wave's blocks go out before anything else
+  // (a partial super-step re-reads its last group for the absent ones; they are masked)
+  const int g0 = split * STEPS_PER_SPLIT + wave * GROUPS_PER_WAVE;
+  const int ng = max(0, min(GROUPS_PER_WAVE, a.n_groups - g0));
+  static_assert(GROUPS_PER_WAVE == 4, "the prefetch registers below are spelled out for 4 groups");
+  uint4 pa0, pa1, pa2, pb0, pb1, pb2, pc0, pc1, pc2, pd0, pd1, pd2;  // [group][third of the block]
+  const uint4* gsrc = (const uint4*)(a.main + ((int64_t)P * a.n_groups + g0) * GROUP_BYTES) + lane;
+  if (ng > 0) {
+    const uint4* ga = gsrc;
+    const uint4* gb = gsrc + min(1, ng - 1) * (GROUP_BYTES / 16);
+    const uint4* gc = gsrc + min(2, ng - 1) * (GROUP_BYTES / 16);
+    const uint4* gd = gsrc + min(3, ng - 1) * (GROUP_BYTES / 16);
+    pa0 = ga[0]; pa1 = ga[64]; pa2 = ga[128];
+    pb0 = gb[0]; pb1 = gb[64]; pb2 = gb[128];
+    pc0 = gc[0]; pc1 = gc[64]; pc2 = gc[128];
+    pd0 = gd[0]; pd1 = gd[64]; pd2 = gd[128];
   }
-  if constexpr (RESID) {
-    // this step's key (after RoPE) and value enter residual slot n_res
-    if (tid < HEAD_DIM) {
-      const uint16_t* kb = qrow + (a.nq + kvh) * HEAD_DIM;
-      a.kr[((int64_t)P * RES_CAP + a.n_res) * HEAD_DIM + tid] = rope1(kb, a.cos, a.sin, tid);
-      a.vr[((int64_t)P * HEAD_DIM + tid) * RES_CAP + res_phys(a.n_res)] =
-          qrow[(a.nq + a.nkv + kvh) * HEAD_DIM + tid];
-    }
+  for (int i = tid; i < GQA * HEAD_DIM; i += ATT_WAVES * 64) {
+    const int h = i / HEAD_DIM, c = i % HEAD_DIM;
+    s_q[h][c] = rope1(qrow + (kvh * GQA + h) * HEAD_DIM, a.cos, a.sin, c);
+  }
+  if (ng > 0) {
+    uint4* sa = s_stage[wave] + lane;
+    uint4* sb = sa + GROUP_BYTES / 16;
+    uint4* sc = sb + GROUP_BYTES / 16;
+    uint4* sd = sc + GROUP_BYTES / 16;
+    sa[0] = pa0; sa[64] = pa1; sa[128] = pa2;
+    sb[0] = pb0; sb[64] = pb1; sb[128] = pb2;
+    sc[0] = pc0; sc[64] = pc1; sc[128] = pc2;
+    sd[0] = pd0; sd[64] = pd1; sd[128] = pd2;
   }
   __syncthreads();
 
-  const int n = lane & 15, q = lane >> 4;
   float m = -__builtin_inff(), lsum = 0.0f;
   f32x4 acc[8];
+  float zt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float zt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-
-  int st0, st1;
-  const int n_valid = a.n_res + 1;
-  if constexpr (RESID) {
-    st0 = wave;
-    st1 = (wave * KV_GROUP < n_valid) ? wave + 1 : wave;
-  } else {
-    st0 = split * STEPS_PER_SPLIT + wave * STEPS_PER_WAVE;
-    st1 = min(st0 + STEPS_PER_WAVE, a.n_groups);
+  if (ng > 0) {
+    uint4 qh[4];
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs) qh[cs] = *(const uint4*)&s_q[n & 3][cs * 32 + q * 8];
+    main_superstep((const uint8_t*)s_stage[wave], ng, qh, lane, a.scale_log2, m, lsum, acc, zt);
   }
-
-  // the query side of the score MFMA: head n, channels 32 cs + 8 q + j
-  uint4 qb[4];
+  // columns -> heads: o = acc / V_SCALE - zt summed over the four group
+  // columns of the head (and zt over the lane groups)
 #pragma unroll
-  for (int cs = 0; cs < 4; ++cs) qb[cs] = *(const uint4*)&s_q[n][cs * 32 + q * 8];
-
-  for (int st = st0; st < st1; ++st) {
-    f32x4 S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-    float bias = 0.0f;
-    uint4 vcode;
-    uint4 vsz[8];
-    if constexpr (RESID) {
+  for (int gc = 0; gc < 4; ++gc) zt[gc] = sum_x32(sum_x16(zt[gc]));
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint16_t* kp = a.kr + ((int64_t)P * RES_CAP + st * 32 + t * 16 + n) * HEAD_DIM + q * 8;
+  for (int r8 = 0; r8 < 8; ++r8)
 #pragma unroll
-        for (int cs = 0; cs < 4; ++cs) {
-          const uint4 kv = *(const uint4*)(kp + cs * 32);
-          S[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kv),
-                                                        __builtin_bit_cast(bf16x8, qb[cs]), S[t], 0, 0, 0);
-        }
-      }
-    } else {
-      const int64_t pg = (int64_t)P * a.n_groups + st;
-      const uint2 kc0 = *(const uint2*)(a.kc + (pg * 2 * 64 + lane) * 8);
-      const uint2 kc1 = *(const uint2*)(a.kc + (pg * 2 * 64 + 64 + lane) * 8);
-      vcode = *(const uint4*)(a.vc + (pg * 64 + lane) * 16);
-      const _Float16* vz = a.vsz + (pg * 4 + q) * 8 * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vsz[j] = *(const uint4*)(vz + j * 8);
-#pragma unroll
-      for (int cs = 0; cs < 4; ++cs) {
-        const f16x8 sv = *(const f16x8*)(a.ks + pg * HEAD_DIM + cs * 32 + q * 8);
-        const f16x8 zv = *(const f16x8*)(a.kz + pg * HEAD_DIM + cs * 32 + q * 8);
-        const uint32_t qw[4] = {qb[cs].x, qb[cs].y, qb[cs].z, qb[cs].w};
-        uint32_t bq[4];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const float q0 = bf2f(qw[p] & 0xffffu) * (float)sv[2 * p];
-          const float q1 = bf2f(qw[p] >> 16) * (float)sv[2 * p + 1];
-          bias = fmaf(q0, (float)zv[2 * p], bias);
-          bias = fmaf(q1, (float)zv[2 * p + 1], bias);
-          bq[p] = pack_h2(q0, q1);
-        }
-        const f16x8 B = __builtin_bit_cast(f16x8, make_uint4(bq[0], bq[1], bq[2], bq[3]));
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const uint32_t W = (cs < 2) ? (t ? kc1.x : kc0.x) : (t ? kc1.y : kc0.y);
-          const int kb = (cs & 1) * 4;
-          const uint4 A = make_uint4(code_pair(W, kb), code_pair(W, kb + 1), code_pair(W, kb + 2), code_pair(W, kb + 3));
-          S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, A), B, S[t], 0, 0, 0);
-        }
-      }
-      bias += __shfl_xor(bias, 16);
-      bias += __shfl_xor(bias, 32);
+    for (int r = 0; r < 4; ++r) {
+      float v = acc[r8][r] * (1.0f / V_SCALE) - zt[r8 >> 1];
+      v += ror4(v);
+      v += ror8(v);
+      acc[r8][r] = v;
     }
-    // scores of head n at tokens 16 t + 4 q + r of this step
-    float sc[2][4];
-    float mloc = -__builtin_inff();
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s = (S[t][r] - bias) * a.scale_log2;
-        if constexpr (RESID) {
-          if (st * 32 + t * 16 + q * 4 + r >= n_valid) s = -__builtin_inff();
-        }
-        sc[t][r] = s;
-        mloc = fmaxf(mloc, s);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float mnew = fmaxf(m, mloc);
-    const float alpha = exp2f(m - mnew);
-    m = mnew;
-    float p[8];
-    float psum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p[j] = exp2f(sc[j >> 2][j & 3] - mnew);
-      psum += p[j];
-    }
-    lsum = lsum * alpha + psum;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-
-    if constexpr (RESID) {
-      const uint32_t pb[4] = {f2bf2_hw(p[0], p[1]), f2bf2_hw(p[2], p[3]), f2bf2_hw(p[4], p[5]), f2bf2_hw(p[6], p[7])};
-      const bf16x8 B = __builtin_bit_cast(bf16x8, make_uint4(pb[0], pb[1], pb[2], pb[3]));
-#pragma unroll
-      for (int r8 = 0; r8 < 8; ++r8) {
-        const uint4 vv = *(const uint4*)(a.vr + ((int64_t)P * HEAD_DIM + r8 * 16 + n) * RES_CAP + st * 32 + q * 8);
-        acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), B, acc[r8], 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int gc = 0; gc < 4; ++gc) zt[gc] *= alpha;
-      f16x8 Bv[4];
-#pragma unroll
-      for (int gc = 0; gc < 4; ++gc) {
-        uint32_t pw[4];
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-          const f16x8 e0 = __builtin_bit_cast(f16x8, vsz[2 * pp]);
-          const f16x8 e1 = __builtin_bit_cast(f16x8, vsz[2 * pp + 1]);
-          const float p0 = p[2 * pp] * (float)e0[2 * gc];
-          const float p1 = p[2 * pp + 1] * (float)e1[2 * gc];
-          zt[gc] = fmaf(p0, (float)e0[2 * gc + 1], zt[gc]);
-          zt[gc] = fmaf(p1, (float)e1[2 * gc + 1], zt[gc]);
-          pw[pp] = pack_h2(p0, p1);
-        }
-        Bv[gc] = __builtin_bit_cast(f16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-      }
-      const uint32_t vw[4] = {vcode.x, vcode.y, vcode.z, vcode.w};
-#pragma unroll
-      for (int r8 = 0; r8 < 8; ++r8) {
-        const uint32_t W = vw[r8 >> 1];
-        const int kb = (r8 & 1) * 4;
-        const uint4 A = make_uint4(code_pair(W, kb), code_pair(W, kb + 1), code_pair(W, kb + 2), code_pair(W, kb + 3));
-        acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, A), Bv[r8 >> 1], acc[r8], 0, 0, 0);
-      }
-    }
-  }
-  // wave result: o[ch][n] = acc - zero-point term, ch = 16 r8 + 4 q + r
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
-#pragma unroll
-  for (int gc = 0; gc < 4; ++gc) {
-    zt[gc] += __shfl_xor(zt[gc], 16);
-    zt[gc] += __shfl_xor(zt[gc], 32);
-  }
+  lsum += ror4(lsum);
+  lsum += ror8(lsum);
+  lsum = sum_x32(sum_x16(lsum));
+  __syncthreads();  // the stage area becomes s_part
+  // wave result in lanes n < 4 (head n): o[ch] for ch = 16 r8 + 4 q + r
   if (n < GQA) {
 #pragma unroll
     for (int r8 = 0; r8 < 8; ++r8)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_part[wave][n][2 + r8 * 16 + q * 4 + r] = acc[r8][r] - zt[r8 >> 1];
+      for (int r = 0; r < 4; ++r) s_part[wave][n][2 + r8 * 16 + q * 4 + r] = acc[r8][r];
     if (q == 0) {
       s_part[wave][n][0] = m;
       s_part[wave][n][1] = lsum;
@@ -581,7 +641,7 @@ __device__ __forceinline__ void kivi_split(const KiviArgs& a, uint16_t (*s_q)[HE
     o0 = fmaf(f, s_part[w][h][2 + c2], o0);
     o1 = fmaf(f, s_part[w][h][3 + c2], o1);
   }
-  float* out = a.part + (((int64_t)P * (a.splits + 1) + split) * GQA + h) * PART;
+  float* out = a.part + (((int64_t)P * a.splits + split) * GQA + h) * PART;
   if ((tid & 63) == 0) {
     out[0] = M;
     out[1] = L;
@@ -590,99 +650,183 @@ __device__ __forceinline__ void kivi_split(const KiviArgs& a, uint16_t (*s_q)[HE
   out[3 + c2] = o1;
 }
 
-// One launch: workgroups (split < splits, P) read the main cache, (splits, P)
-// the residual window.
-__global__ void __launch_bounds__(ATT_WAVES * 64) k_kivi_split(KiviArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[16][HEAD_DIM];
-  __shared__ float s_part[ATT_WAVES][GQA][PART];
-  if ((int)blockIdx.x == a.splits) kivi_split<true>(a, s_q, s_part);
-  else kivi_split<false>(a, s_q, s_part);
+VH_DEV float block_max128(float v, float* s_red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = fmaxf(s_red[0], s_red[1]);
+  __syncthreads();
+  return r;
 }
 
-// Merge the splits of each (batch, query head); write the attention output
-// (bf16) and its MX-int8 fake quantization for the output projection.
-__global__ void __launch_bounds__(HEAD_DIM) k_kivi_combine(const float* __restrict__ part, int nsplit, int nkv, int nq,
-                                                           uint16_t* __restrict__ attn, _Float16* __restrict__ fq,
-                                                           int* __restrict__ flag) {
-  const int bh = blockIdx.x, b = bh / nq, H = bh % nq;
-  const int P = b * nkv + H / GQA, h = H % GQA, c = threadIdx.x;
-  const float* base = part + ((int64_t)P * nsplit * GQA + h) * PART;
-  float M = -__builtin_inff();
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, base[(int64_t)s * GQA * PART]);
-  float L = 0.0f, O = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
+VH_DEV float block_sum128(float v, float* s_red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = s_red[0] + s_red[1];
+  __syncthreads();
+  return r;
+}
+
+// Per (batch, query head): attention over the residual window (its n_res
+// cached tokens and this step's key / value, taken from the qkv row), merged
+// with the main-cache splits; writes the attention output (bf16) and its
+// MX-int8 fake quantization.  The workgroup of head 0 of each kv head
+// appends this step's key (after RoPE) and value at residual slot n_res.
+// One thread per channel / residual slot.
+__global__ void __launch_bounds__(HEAD_DIM) k_kivi_combine(KiviArgs a, uint16_t* __restrict__ attn,
+                                                           _Float16* __restrict__ fq, int* __restrict__ flag) {
+  __shared__ float s_q[HEAD_DIM];
+  __shared__ float s_kn[HEAD_DIM];
+  __shared__ float s_p[RES_CAP];
+  __shared__ float s_o[8][HEAD_DIM];
+  __shared__ float s_red[2];
+  const int bh = blockIdx.x, b = bh / a.nq, H = bh % a.nq, kvh = H / GQA, h = H % GQA;
+  const int P = b * a.nkv + kvh, c = threadIdx.x;
+  const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
+  s_q[c] = bf2f(rope1(qrow + H * HEAD_DIM, a.cos, a.sin, c));
+  const uint16_t kn = rope1(qrow + (a.nq + kvh) * HEAD_DIM, a.cos, a.sin, c);
+  const uint16_t vn = qrow[(a.nq + a.nkv + kvh) * HEAD_DIM + c];
+  s_kn[c] = bf2f(kn);
+  if (h == 0) {
+    a.kr[((int64_t)P * RES_CAP + a.n_res) * HEAD_DIM + c] = kn;
+    a.vr[((int64_t)P * RES_CAP + a.n_res) * HEAD_DIM + c] = vn;
+  }
+  __syncthreads();
+  // score of residual slot t = c: its 256-byte key row in one round trip
+  float sc = -__builtin_inff();
+  if (c < a.n_res) {
+    const uint4* kp = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + c) * HEAD_DIM);
+    uint4 kw[HEAD_DIM / 8];
+#pragma unroll
+    for (int i = 0; i < HEAD_DIM / 8; ++i) kw[i] = kp[i];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < HEAD_DIM / 8; ++i) {
+      const uint32_t ww[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc = fmaf(s_q[8 * i + 2 * j], bf2f(ww[j] & 0xffffu), acc);
+        acc = fmaf(s_q[8 * i + 2 * j + 1], bf2f(ww[j] >> 16), acc);
+      }
+    }
+    sc = acc * a.scale_log2;
+  } else if (c == a.n_res) {
+    float acc = 0.0f;
+    for (int j = 0; j < HEAD_DIM; ++j) acc = fmaf(s_q[j], s_kn[j], acc);
+    sc = acc * a.scale_log2;
+  }
+  const float mr = block_max128(sc, s_red);
+  const float p = c <= a.n_res ? exp2f(sc - mr) : 0.0f;
+  s_p[c] = p;
+  const float lr = block_sum128(p, s_red);
+  // values: thread (token subset ts, channel octet co) sums tokens ts + 8u
+  {
+    const int co = c & 15, ts = c >> 4;
+    const uint4* vp = (const uint4*)(a.vr + (int64_t)P * RES_CAP * HEAD_DIM) + co;
+    float o8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    uint4 vw[RES_CAP / 8];
+#pragma unroll
+    for (int u = 0; u < RES_CAP / 8; ++u) {
+      const int t = ts + 8 * u;
+      vw[u] = t < a.n_res ? vp[(int64_t)t * (HEAD_DIM / 8)] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < RES_CAP / 8; ++u) {
+      const float pt = s_p[ts + 8 * u];
+      const uint32_t ww[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o8[2 * j] = fmaf(pt, bf2f(ww[j] & 0xffffu), o8[2 * j]);
+        o8[2 * j + 1] = fmaf(pt, bf2f(ww[j] >> 16), o8[2 * j + 1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_o[ts][co * 8 + j] = o8[j];
+  }
+  __syncthreads();
+  float orr = fmaf(s_p[a.n_res], bf2f(vn), 0.0f);
+#pragma unroll
+  for (int ts = 0; ts < 8; ++ts) orr += s_o[ts][c];
+  // merge with the main-cache splits
+  const float* base = a.part + ((int64_t)P * a.splits * GQA + h) * PART;
+  float M = mr;
+  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, base[(int64_t)s * GQA * PART]);
+  const float fr = exp2f(mr - M);
+  float L = lr * fr, O = orr * fr;
+  for (int s = 0; s < a.splits; ++s) {
     const float* ps = base + (int64_t)s * GQA * PART;
     const float f = ps[0] == -__builtin_inff() ? 0.0f : exp2f(ps[0] - M);
     L = fmaf(f, ps[1], L);
     O = fmaf(f, ps[2 + c], O);
   }
   const float o = rbf(O / L);
-  const int64_t idx = (int64_t)b * nq * HEAD_DIM + H * HEAD_DIM + c;
+  const int64_t idx = (int64_t)b * a.nq * HEAD_DIM + H * HEAD_DIM + c;
   if (attn) attn[idx] = (uint16_t)f2bf(o);
-  const Mx8Scale sc = mx8_scale(max16(fabsf(o)));
-  fq[idx] = fq_half(mx8_fq(o, sc), flag);
+  const Mx8Scale scl = mx8_scale(max16(fabsf(o)));
+  fq[idx] = fq_half(mx8_fq(o, scl), flag);
 }
 
-// Bake: keys.  One thread per (P, g, tile, lane) -> 8 bytes; scale / zp to fp16.
-__global__ void __launch_bounds__(256) k_bake_kivi_keys(const uint8_t* __restrict__ codes, int64_t P, int64_t T,
-                                                        uint8_t* __restrict__ out) {
-  const int64_t G = T / KV_GROUP;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= P * G * 2 * 64) return;
-  const int lane = (int)(t % 64), tile = (int)((t / 64) % 2);
-  const int64_t g = (t / 128) % G, p = t / (128 * G);
-  const int64_t tok = g * KV_GROUP + tile * 16 + (lane & 15);
-  const uint8_t* src = codes + (p * T + tok) * HEAD_DIM;
-  uint32_t w[2] = {0u, 0u};
-#pragma unroll
-  for (int cs = 0; cs < 4; ++cs)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t c = src[cs * 32 + (lane >> 4) * 8 + j] & 3u;
-      const int k = (cs & 1) * 4 + j / 2;
-      w[cs >> 1] |= c << ((j & 1) * 16 + 2 * k);
-    }
-  *(uint2*)(out + t * 8) = make_uint2(w[0], w[1]);
-}
-
-// Bake: values.  One thread per (P, g, lane) -> 16 code bytes, plus the
-// (scale, zp) of the lane-group's 8 tokens when lane % 16 == 0.
-__global__ void __launch_bounds__(256) k_bake_kivi_values(const uint8_t* __restrict__ codes,
-                                                          const uint16_t* __restrict__ scale,
-                                                          const uint16_t* __restrict__ zp, int64_t P, int64_t T,
-                                                          uint8_t* __restrict__ out, _Float16* __restrict__ sz) {
+// Bake the main cache: one thread per (P, g, lane) writes its key codes
+// (2 x 8 B), value codes (16 B) and one 16-byte piece of the scale / zero
+// point quarter (lanes 0-31 keys, 32-63 values).
+__global__ void __launch_bounds__(256) k_bake_kivi(const uint8_t* __restrict__ kcode, const uint16_t* __restrict__ ks,
+                                                   const uint16_t* __restrict__ kz, const uint8_t* __restrict__ vcode,
+                                                   const uint16_t* __restrict__ vs, const uint16_t* __restrict__ vz,
+                                                   int64_t P, int64_t T, uint8_t* __restrict__ out) {
   const int64_t G = T / KV_GROUP;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= P * G * 64) return;
   const int lane = (int)(t % 64), q = lane >> 4;
   const int64_t g = (t / 64) % G, p = t / (64 * G);
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  uint8_t* blk = out + (p * G + g) * GROUP_BYTES;
+  // keys: tile tt, token 32 g + 16 tt + lane % 16
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const uint8_t* src = kcode + (p * T + g * KV_GROUP + tt * 16 + (lane & 15)) * HEAD_DIM;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t c = src[cs * 32 + q * 8 + j] & 3u;
+        const int k = (cs & 1) * 4 + j / 2;
+        w[cs >> 1] |= c << ((j & 1) * 16 + 2 * k);
+      }
+    *(uint2*)(blk + tt * 512 + lane * 8) = make_uint2(w[0], w[1]);
+  }
+  // values: tile r8 (channel 16 r8 + lane % 16), tokens tok(q, j)
+  uint32_t v[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int r8 = 0; r8 < 8; ++r8)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int64_t tok = g * KV_GROUP + 16 * (j / 4) + 4 * q + (j % 4);
-      const uint32_t c = codes[(p * T + tok) * HEAD_DIM + r8 * 16 + (lane & 15)] & 3u;
+      const uint32_t c = vcode[(p * T + tok) * HEAD_DIM + r8 * 16 + (lane & 15)] & 3u;
       const int k = (r8 & 1) * 4 + j / 2;
-      w[r8 >> 1] |= c << ((j & 1) * 16 + 2 * k);
+      v[r8 >> 1] |= c << ((j & 1) * 16 + 2 * k);
     }
-  *(uint4*)(out + t * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-  if ((lane & 15) == 0) {
-    _Float16* d = sz + ((p * G + g) * 4 + q) * 64;
-    for (int j = 0; j < 8; ++j) {
-      const int64_t tok = g * KV_GROUP + 16 * (j / 4) + 4 * q + (j % 4);
-      for (int gc = 0; gc < 4; ++gc) {
-        d[j * 8 + gc * 2] = (_Float16)bf2f(scale[(p * T + tok) * 4 + gc]);
-        d[j * 8 + gc * 2 + 1] = (_Float16)bf2f(zp[(p * T + tok) * 4 + gc]);
-      }
+  *(uint4*)(blk + 1024 + lane * 16) = make_uint4(v[0], v[1], v[2], v[3]);
+  _Float16 piece[8];
+  if (lane < 32) {
+    // key piece: slot (cs, qq) = lane / 2, half 0 scale / 1 zp
+    const int slot = lane >> 1, cs = slot >> 2, qq = slot & 3;
+    const uint16_t* src = ((lane & 1) ? kz : ks) + (p * G + g) * HEAD_DIM + cs * 32 + qq * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) piece[j] = (_Float16)bf2f(src[j]);
+    *(f16x8*)(blk + 2048 + lane * 16) = *(const f16x8*)piece;
+  } else {
+    // value piece: (qq, j) = (lane - 32) / 8, % 8 -> 4 groups x (scale, zp)
+    const int i = lane - 32, qq = i >> 3, j = i & 7;
+    const int64_t tok = g * KV_GROUP + 16 * (j / 4) + 4 * qq + (j % 4);
+#pragma unroll
+    for (int gc = 0; gc < 4; ++gc) {
+      piece[2 * gc] = (_Float16)bf2f(vs[(p * T + tok) * 4 + gc]);
+      piece[2 * gc + 1] = (_Float16)bf2f(vz[(p * T + tok) * 4 + gc]);
     }
+    *(f16x8*)(blk + 2560 + i * 16) = *(const f16x8*)piece;
   }
-}
-
-__global__ void __launch_bounds__(256) k_bf16_to_f16(const uint16_t* __restrict__ in, int64_t n,
-                                                     _Float16* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = (_Float16)bf2f(in[i]);
 }
 
 __global__ void __launch_bounds__(256) k_bake_kivi_residual(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -694,7 +838,7 @@ __global__ void __launch_bounds__(256) k_bake_kivi_residual(const uint16_t* __re
   const int s = (int)((i / HEAD_DIM) % n);
   const int64_t p = i / (HEAD_DIM * n);
   kr[(p * RES_CAP + s) * HEAD_DIM + c] = k[i];
-  vr[(p * HEAD_DIM + c) * RES_CAP + res_phys(s)] = v[i];
+  vr[(p * RES_CAP + s) * HEAD_DIM + c] = v[i];
 }
 
 inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
@@ -754,20 +898,12 @@ extern "C" int vh_gemv_mx8(const uint16_t* x_fq, int64_t M, int64_t K, const uin
 
 extern "C" int vh_kivi_bake(const uint8_t* k_codes, const uint16_t* k_scale, const uint16_t* k_zp,
                             const uint8_t* v_codes, const uint16_t* v_scale, const uint16_t* v_zp, int64_t P,
-                            int64_t T, uint8_t* kc, uint16_t* ks, uint16_t* kz, uint8_t* vc, uint16_t* vsz,
-                            vh_stream_t stream) {
-  VH_REQUIRE(k_codes && k_scale && k_zp && v_codes && v_scale && v_zp && kc && ks && kz && vc && vsz,
-             "vh_kivi_bake: null argument");
+                            int64_t T, uint8_t* main_out, vh_stream_t stream) {
+  VH_REQUIRE(k_codes && k_scale && k_zp && v_codes && v_scale && v_zp && main_out, "vh_kivi_bake: null argument");
   VH_REQUIRE(P > 0 && T > 0 && T % KV_GROUP == 0, "vh_kivi_bake: needs T %% 32 == 0");
-  hipStream_t s = vh::as_stream(stream);
   const int64_t G = T / KV_GROUP;
-  hipLaunchKernelGGL(k_bake_kivi_keys, dim3(blocks_for(P * G * 128, 256)), dim3(256), 0, s, k_codes, P, T, kc);
-  hipLaunchKernelGGL(k_bf16_to_f16, dim3(blocks_for(P * G * HEAD_DIM, 256)), dim3(256), 0, s, k_scale,
-                     P * G * HEAD_DIM, (_Float16*)ks);
-  hipLaunchKernelGGL(k_bf16_to_f16, dim3(blocks_for(P * G * HEAD_DIM, 256)), dim3(256), 0, s, k_zp,
-                     P * G * HEAD_DIM, (_Float16*)kz);
-  hipLaunchKernelGGL(k_bake_kivi_values, dim3(blocks_for(P * G * 64, 256)), dim3(256), 0, s, v_codes, v_scale, v_zp,
-                     P, T, vc, (_Float16*)vsz);
+  hipLaunchKernelGGL(k_bake_kivi, dim3(blocks_for(P * G * 64, 256)), dim3(256), 0, vh::as_stream(stream), k_codes,
+                     k_scale, k_zp, v_codes, v_scale, v_zp, P, T, main_out);
   return vh::check_launch("vh_kivi_bake");
 }
 
@@ -782,26 +918,26 @@ extern "C" int vh_kivi_bake_residual(const uint16_t* k, const uint16_t* v, int64
 }
 
 extern "C" int vh_kivi_attention(const vh_kivi_desc* d, vh_stream_t stream) {
-  VH_REQUIRE(d && d->qkv && d->cos && d->sin && d->kr && d->vr && d->part && d->attn_fq && d->flag,
+  VH_REQUIRE(d && d->qkv && d->cos && d->sin && d->kr && d->vr && d->attn_fq && d->flag,
              "vh_kivi_attention: null argument");
   VH_REQUIRE(d->batch >= 1 && d->nkv >= 1 && d->nq == GQA * d->nkv, "vh_kivi_attention: needs nq == 4 nkv");
   VH_REQUIRE(d->head_dim == HEAD_DIM, "vh_kivi_attention: head_dim must be %d", HEAD_DIM);
   VH_REQUIRE(d->n_main >= 0 && d->n_main % KV_GROUP == 0, "vh_kivi_attention: n_main must be a multiple of 32");
-  VH_REQUIRE(d->n_main == 0 || (d->kc && d->ks && d->kz && d->vc && d->vsz), "vh_kivi_attention: missing main cache");
+  VH_REQUIRE(d->n_main == 0 || d->main, "vh_kivi_attention: missing main cache");
   VH_REQUIRE(d->n_res >= 0 && d->n_res < RES_CAP, "vh_kivi_attention: n_res must be in [0, %d)", RES_CAP);
   VH_REQUIRE(d->qkv_ld >= (int64_t)(d->nq + 2 * d->nkv) * HEAD_DIM, "vh_kivi_attention: qkv_ld too small");
   const int G = (int)(d->n_main / KV_GROUP);
   const int splits = (G + STEPS_PER_SPLIT - 1) / STEPS_PER_SPLIT;
-  VH_REQUIRE(d->part_floats >= (int64_t)d->batch * d->nkv * (splits + 1) * GQA * PART,
+  VH_REQUIRE(d->part_floats >= (int64_t)d->batch * d->nkv * splits * GQA * PART,
              "vh_kivi_attention: workspace too small (needs %lld floats)",
-             (long long)d->batch * d->nkv * (splits + 1) * GQA * PART);
-  KiviArgs a{d->qkv, d->qkv_ld, d->cos, d->sin, d->kc, (const _Float16*)d->ks, (const _Float16*)d->kz, d->vc,
-             (const _Float16*)d->vsz, d->kr, d->vr, G, (int32_t)d->n_res, (int32_t)d->nkv, (int32_t)d->nq, splits,
-             d->softmax_scale * 1.4426950408889634f, d->part};
+             (long long)d->batch * d->nkv * splits * GQA * PART);
+  VH_REQUIRE(splits == 0 || d->part, "vh_kivi_attention: missing workspace");
+  KiviArgs a{d->qkv, d->qkv_ld, d->cos, d->sin, d->main, d->kr, d->vr, G, (int32_t)d->n_res, (int32_t)d->nkv,
+             (int32_t)d->nq, splits, d->softmax_scale * 1.4426950408889634f, d->part};
   hipStream_t s = vh::as_stream(stream);
   const unsigned P = (unsigned)(d->batch * d->nkv);
-  hipLaunchKernelGGL(k_kivi_split, dim3((unsigned)(splits + 1), P), dim3(ATT_WAVES * 64), 0, s, a);
-  hipLaunchKernelGGL(k_kivi_combine, dim3((unsigned)(d->batch * d->nq)), dim3(HEAD_DIM), 0, s, d->part, splits + 1,
-                     (int)d->nkv, (int)d->nq, d->attn, (_Float16*)d->attn_fq, (int*)d->flag);
+  if (splits > 0) hipLaunchKernelGGL(k_kivi_split, dim3((unsigned)splits, P), dim3(ATT_WAVES * 64), 0, s, a);
+  hipLaunchKernelGGL(k_kivi_combine, dim3((unsigned)(d->batch * d->nq)), dim3(HEAD_DIM), 0, s, a, d->attn,
+                     (_Float16*)d->attn_fq, (int*)d->flag);
   return vh::check_launch("vh_kivi_attention");
 }

@@ -113,7 +113,7 @@ _SIGNATURES = {
     "vh_rmsnorm_mx8": ([_P, _P, _I64, _I64, _F32, _P, _P, _P, _P], _I32),
     "vh_mx8_bake": ([_P, _P, _I32, _I64, _I64, _I32, _P, _P, _P, _P], _I32),
     "vh_gemv_mx8": ([_P, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P], _I32),
-    "vh_kivi_bake": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P], _I32),
+    "vh_kivi_bake": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P], _I32),
     "vh_kivi_bake_residual": ([_P, _P, _I64, _I64, _P, _P, _P], _I32),
     # vh_kivi_attention takes a vh_kivi_desc*; voyager_amd.decode.KiviDesc mirrors it.
     "vh_kivi_attention": ([_P, _P], _I32),

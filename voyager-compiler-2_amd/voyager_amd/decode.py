@@ -125,8 +125,7 @@ class KiviDesc(ctypes.Structure):
     _fields_ = [
         ("qkv", ctypes.c_void_p), ("qkv_ld", ctypes.c_int64),
         ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
-        ("kc", ctypes.c_void_p), ("ks", ctypes.c_void_p), ("kz", ctypes.c_void_p),
-        ("vc", ctypes.c_void_p), ("vsz", ctypes.c_void_p),
+        ("main", ctypes.c_void_p),
         ("kr", ctypes.c_void_p), ("vr", ctypes.c_void_p),
         ("batch", ctypes.c_int64), ("nkv", ctypes.c_int64), ("nq", ctypes.c_int64), ("head_dim", ctypes.c_int64),
         ("n_main", ctypes.c_int64), ("n_res", ctypes.c_int64),
@@ -153,15 +152,12 @@ class KiviCache:
         P = batch * nkv
         self.P = P
         G = n_main // KIVI_GROUP
-        u8, f16, bf = torch.uint8, torch.float16, torch.bfloat16
-        self.kc = torch.zeros(P * n_main * 32, dtype=u8, device=device)
-        self.ks = torch.zeros(P, G, HEAD_DIM, dtype=f16, device=device)
-        self.kz = torch.zeros(P, G, HEAD_DIM, dtype=f16, device=device)
-        self.vc = torch.zeros(P * n_main * 32, dtype=u8, device=device)
-        self.vsz = torch.zeros(P * n_main * 8, dtype=f16, device=device)
+        bf = torch.bfloat16
+        # one 3072-byte block per 32 tokens: key / value codes, key / value scale + zero point
+        self.main = torch.zeros(P * G * 3072, dtype=torch.uint8, device=device)
         cap = _lib.KIVI_RES_CAP
         self.kr = torch.zeros(P, cap, HEAD_DIM, dtype=bf, device=device)
-        self.vr = torch.zeros(P, HEAD_DIM, cap, dtype=bf, device=device)
+        self.vr = torch.zeros(P, cap, HEAD_DIM, dtype=bf, device=device)
 
     @classmethod
     def from_bf16(cls, k_main: torch.Tensor, v_main: torch.Tensor, k_res: torch.Tensor, v_res: torch.Tensor):
@@ -199,8 +195,8 @@ class KiviCache:
         for t in (ks_, kz_, vs_, vz_):
             if t.dtype != torch.bfloat16:
                 raise TypeError("KiviCache: scales / zero points must be bfloat16")
-        st = load().vh_kivi_bake(ptr(kc8), ptr(ks_), ptr(kz_), ptr(vc8), ptr(vs_), ptr(vz_), P, T, ptr(self.kc),
-                                 ptr(self.ks), ptr(self.kz), ptr(self.vc), ptr(self.vsz), _stream(kc8))
+        st = load().vh_kivi_bake(ptr(kc8), ptr(ks_), ptr(kz_), ptr(vc8), ptr(vs_), ptr(vz_), P, T, ptr(self.main),
+                                 _stream(kc8))
         check(st, "vh_kivi_bake")
 
     def load_residual(self, k_res: torch.Tensor, v_res: torch.Tensor) -> None:
@@ -217,16 +213,14 @@ class KiviCache:
 
     def residual_tokens(self, n: int):
         """The first n residual keys / values as ``[batch, nkv, n, 128]`` bf16."""
-        idx = torch.arange(n, device=self.kr.device)
-        phys = (idx & ~31) | (((idx >> 2) & 3) << 3) | (((idx >> 4) & 1) << 2) | (idx & 3)
         k = self.kr[:, :n].reshape(self.batch, self.nkv, n, HEAD_DIM)
-        v = self.vr[:, :, phys].transpose(1, 2).reshape(self.batch, self.nkv, n, HEAD_DIM)
+        v = self.vr[:, :n].reshape(self.batch, self.nkv, n, HEAD_DIM)
         return k, v
 
 
 def part_floats(batch: int, nkv: int, n_main: int) -> int:
     splits = -(-(n_main // KIVI_GROUP) // 16)
-    return batch * nkv * (splits + 1) * GQA * (HEAD_DIM + 2)
+    return max(1, batch * nkv * splits * GQA * (HEAD_DIM + 2))
 
 
 def kivi_attention(qkv: torch.Tensor, cache: KiviCache, cos: torch.Tensor, sin: torch.Tensor, nq: int,
@@ -243,8 +237,7 @@ def kivi_attention(qkv: torch.Tensor, cache: KiviCache, cos: torch.Tensor, sin: 
     if attn_fq is None:
         attn_fq = torch.empty(B, nq * HEAD_DIM, dtype=torch.float16, device=dev)
     d = KiviDesc(qkv=qkv.data_ptr(), qkv_ld=qkv.stride(0), cos=cos.data_ptr(), sin=sin.data_ptr(),
-                 kc=_vp(cache.kc), ks=_vp(cache.ks), kz=_vp(cache.kz), vc=_vp(cache.vc), vsz=_vp(cache.vsz),
-                 kr=_vp(cache.kr), vr=_vp(cache.vr), batch=B, nkv=cache.nkv, nq=nq, head_dim=HEAD_DIM,
+                 main=_vp(cache.main) if cache.n_main else None, kr=_vp(cache.kr), vr=_vp(cache.vr), batch=B, nkv=cache.nkv, nq=nq, head_dim=HEAD_DIM,
                  n_main=cache.n_main, n_res=cache.n_res, softmax_scale=HEAD_DIM ** -0.5, part=part.data_ptr(),
                  part_floats=part.numel(), attn=_vp(attn), attn_fq=attn_fq.data_ptr(), flag=flag.t.data_ptr())
     st = load().vh_kivi_attention(ctypes.byref(d), _stream(qkv))
