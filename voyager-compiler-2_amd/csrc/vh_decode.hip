@@ -33,7 +33,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int MX_SHIFT = 6;  // floor(log2(127)): pot scale 2**(floor(log2(amax)) - 6)
-constexpr int GEMV_WAVES = 16;
+constexpr int GEMV_WAVES = 8;  // two workgroups per CU: one streams while the other reduces
 constexpr int HEAD_DIM = 128;
 constexpr int GQA = 4;        // query heads per kv head
 constexpr int KV_GROUP = 32;  // KIVI group: tokens per key group, channels per value group
@@ -187,7 +187,7 @@ struct GemvArgs {
 };
 
 template <int NT>
-__global__ void __launch_bounds__(GEMV_WAVES * 64) k_gemv_mx8(GemvArgs a) {
+__global__ void __launch_bounds__(GEMV_WAVES * 64, 2) k_gemv_mx8(GemvArgs a) {
   __shared__ float s_red[GEMV_WAVES][NT][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t nsp = a.K / 64, ngr = a.K / 256;
@@ -650,91 +650,111 @@ __global__ void __launch_bounds__(ATT_WAVES * 64) k_kivi_split(KiviArgs a) {
   out[3 + c2] = o1;
 }
 
-VH_DEV float block_max128(float v, float* s_red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  const float r = fmaxf(s_red[0], s_red[1]);
-  __syncthreads();
-  return r;
-}
-
-VH_DEV float block_sum128(float v, float* s_red) {
-  v = wave_sum(v);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  const float r = s_red[0] + s_red[1];
-  __syncthreads();
-  return r;
-}
-
 // Per (batch, query head): attention over the residual window (its n_res
 // cached tokens and this step's key / value, taken from the qkv row), merged
 // with the main-cache splits; writes the attention output (bf16) and its
 // MX-int8 fake quantization.  The workgroup of head 0 of each kv head
 // appends this step's key (after RoPE) and value at residual slot n_res.
-// One thread per channel / residual slot.
-__global__ void __launch_bounds__(HEAD_DIM) k_kivi_combine(KiviArgs a, uint16_t* __restrict__ attn,
-                                                           _Float16* __restrict__ fq, int* __restrict__ flag) {
-  __shared__ float s_q[HEAD_DIM];
-  __shared__ float s_kn[HEAD_DIM];
+// 256 threads: two per residual key row, 16 token subsets for the values;
+// the first 128 (one per channel) merge and write.
+constexpr int COMBINE_PRELOAD = 16;  // splits whose partials are loaded up front
+constexpr int COMBINE_THREADS = 2 * HEAD_DIM;
+
+VH_DEV float block_max256(float v, float* s_red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+  return r;
+}
+
+VH_DEV float block_sum256(float v, float* s_red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  __syncthreads();
+  return r;
+}
+
+__global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, uint16_t* __restrict__ attn,
+                                                                  _Float16* __restrict__ fq, int* __restrict__ flag) {
+  __shared__ __attribute__((aligned(16))) float s_q[HEAD_DIM];
   __shared__ float s_p[RES_CAP];
-  __shared__ float s_o[8][HEAD_DIM];
-  __shared__ float s_red[2];
+  __shared__ float s_o[16][HEAD_DIM];
+  __shared__ float s_red[4];
   const int bh = blockIdx.x, b = bh / a.nq, H = bh % a.nq, kvh = H / GQA, h = H % GQA;
-  const int P = b * a.nkv + kvh, c = threadIdx.x;
+  const int P = b * a.nkv + kvh, tid = threadIdx.x;
+  const int c = tid & (HEAD_DIM - 1);              // channel (first half of the block: merge / output)
+  const int tk = tid >> 1, kh = tid & 1;           // key row tk, channel half kh
+  const int co = tid & 15, ts = tid >> 4;          // value octet co, token subset ts (slots ts + 16u)
   const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
-  s_q[c] = bf2f(rope1(qrow + H * HEAD_DIM, a.cos, a.sin, c));
+  // every independent load goes out first (one round trip)
+  uint4 kw[HEAD_DIM / 16], vw[RES_CAP / 16];
+  const uint4* kp = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + tk) * HEAD_DIM + kh * (HEAD_DIM / 2));
+  const uint4* vp = (const uint4*)(a.vr + (int64_t)P * RES_CAP * HEAD_DIM) + co;
+#pragma unroll
+  for (int i = 0; i < HEAD_DIM / 16; ++i) kw[i] = tk < a.n_res ? kp[i] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int u = 0; u < RES_CAP / 16; ++u)
+    vw[u] = ts + 16 * u < a.n_res ? vp[(int64_t)(ts + 16 * u) * (HEAD_DIM / 8)] : make_uint4(0u, 0u, 0u, 0u);
+  const float* base = a.part + ((int64_t)P * a.splits * GQA + h) * PART;
+  float pm[COMBINE_PRELOAD], pl[COMBINE_PRELOAD], po[COMBINE_PRELOAD];
+  const bool merger = tid < HEAD_DIM;
+#pragma unroll
+  for (int s = 0; s < COMBINE_PRELOAD; ++s) {
+    const bool ok = merger && s < a.splits;
+    const float* ps = base + (int64_t)s * GQA * PART;
+    pm[s] = ok ? ps[0] : -__builtin_inff();
+    pl[s] = ok ? ps[1] : 0.0f;
+    po[s] = ok ? ps[2 + c] : 0.0f;
+  }
+  // RoPE of this step's query / key (channel c; the second half of the block duplicates)
+  const float qc = bf2f(rope1(qrow + H * HEAD_DIM, a.cos, a.sin, c));
   const uint16_t kn = rope1(qrow + (a.nq + kvh) * HEAD_DIM, a.cos, a.sin, c);
   const uint16_t vn = qrow[(a.nq + a.nkv + kvh) * HEAD_DIM + c];
-  s_kn[c] = bf2f(kn);
-  if (h == 0) {
+  if (merger) s_q[c] = qc;
+  // this step's own score, q . k_new
+  const float s_new = block_sum256(merger ? qc * bf2f(kn) : 0.0f, s_red) * a.scale_log2;
+  if (h == 0 && merger) {
+    // this step's key (after RoPE) and value enter residual slot n_res (read
+    // by later steps only: this step takes them from the qkv row)
     a.kr[((int64_t)P * RES_CAP + a.n_res) * HEAD_DIM + c] = kn;
     a.vr[((int64_t)P * RES_CAP + a.n_res) * HEAD_DIM + c] = vn;
   }
-  __syncthreads();
-  // score of residual slot t = c: its 256-byte key row in one round trip
-  float sc = -__builtin_inff();
-  if (c < a.n_res) {
-    const uint4* kp = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + c) * HEAD_DIM);
-    uint4 kw[HEAD_DIM / 8];
-#pragma unroll
-    for (int i = 0; i < HEAD_DIM / 8; ++i) kw[i] = kp[i];
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < HEAD_DIM / 8; ++i) {
-      const uint32_t ww[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc = fmaf(s_q[8 * i + 2 * j], bf2f(ww[j] & 0xffffu), acc);
-        acc = fmaf(s_q[8 * i + 2 * j + 1], bf2f(ww[j] >> 16), acc);
-      }
-    }
-    sc = acc * a.scale_log2;
-  } else if (c == a.n_res) {
-    float acc = 0.0f;
-    for (int j = 0; j < HEAD_DIM; ++j) acc = fmaf(s_q[j], s_kn[j], acc);
-    sc = acc * a.scale_log2;
-  }
-  const float mr = block_max128(sc, s_red);
-  const float p = c <= a.n_res ? exp2f(sc - mr) : 0.0f;
-  s_p[c] = p;
-  const float lr = block_sum128(p, s_red);
-  // values: thread (token subset ts, channel octet co) sums tokens ts + 8u
+  // score of residual slot tk: two threads, 64 channels each
+  float acc = 0.0f;
   {
-    const int co = c & 15, ts = c >> 4;
-    const uint4* vp = (const uint4*)(a.vr + (int64_t)P * RES_CAP * HEAD_DIM) + co;
-    float o8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    uint4 vw[RES_CAP / 8];
+    const float4* q4 = (const float4*)(s_q + kh * (HEAD_DIM / 2));
 #pragma unroll
-    for (int u = 0; u < RES_CAP / 8; ++u) {
-      const int t = ts + 8 * u;
-      vw[u] = t < a.n_res ? vp[(int64_t)t * (HEAD_DIM / 8)] : make_uint4(0u, 0u, 0u, 0u);
+    for (int i = 0; i < HEAD_DIM / 16; ++i) {
+      const float4 qa = q4[2 * i], qb = q4[2 * i + 1];
+      const uint32_t ww[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+      acc = fmaf(qa.x, bf2f(ww[0] & 0xffffu), acc);
+      acc = fmaf(qa.y, bf2f(ww[0] >> 16), acc);
+      acc = fmaf(qa.z, bf2f(ww[1] & 0xffffu), acc);
+      acc = fmaf(qa.w, bf2f(ww[1] >> 16), acc);
+      acc = fmaf(qb.x, bf2f(ww[2] & 0xffffu), acc);
+      acc = fmaf(qb.y, bf2f(ww[2] >> 16), acc);
+      acc = fmaf(qb.z, bf2f(ww[3] & 0xffffu), acc);
+      acc = fmaf(qb.w, bf2f(ww[3] >> 16), acc);
     }
+  }
+  acc += __shfl_xor(acc, 1);
+  float sc = -__builtin_inff();
+  if (tk < a.n_res) sc = acc * a.scale_log2;
+  else if (tk == a.n_res) sc = s_new;
+  const float mr = block_max256(kh == 0 ? sc : -__builtin_inff(), s_red);
+  const float p = tk <= a.n_res ? exp2f(sc - mr) : 0.0f;
+  if (kh == 0) s_p[tk] = p;
+  const float lr = block_sum256(kh == 0 ? p : 0.0f, s_red);
+  {
+    float o8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int u = 0; u < RES_CAP / 8; ++u) {
-      const float pt = s_p[ts + 8 * u];
+    for (int u = 0; u < RES_CAP / 16; ++u) {
+      const float pt = s_p[ts + 16 * u];
       const uint32_t ww[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -746,16 +766,24 @@ __global__ void __launch_bounds__(HEAD_DIM) k_kivi_combine(KiviArgs a, uint16_t*
     for (int j = 0; j < 8; ++j) s_o[ts][co * 8 + j] = o8[j];
   }
   __syncthreads();
-  float orr = fmaf(s_p[a.n_res], bf2f(vn), 0.0f);
+  if (!merger) return;
+  float orr = s_p[a.n_res] * bf2f(vn);
 #pragma unroll
-  for (int ts = 0; ts < 8; ++ts) orr += s_o[ts][c];
+  for (int t16 = 0; t16 < 16; ++t16) orr += s_o[t16][c];
   // merge with the main-cache splits
-  const float* base = a.part + ((int64_t)P * a.splits * GQA + h) * PART;
   float M = mr;
-  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, base[(int64_t)s * GQA * PART]);
+#pragma unroll
+  for (int s = 0; s < COMBINE_PRELOAD; ++s) M = fmaxf(M, pm[s]);
+  for (int s = COMBINE_PRELOAD; s < a.splits; ++s) M = fmaxf(M, base[(int64_t)s * GQA * PART]);
   const float fr = exp2f(mr - M);
   float L = lr * fr, O = orr * fr;
-  for (int s = 0; s < a.splits; ++s) {
+#pragma unroll
+  for (int s = 0; s < COMBINE_PRELOAD; ++s) {
+    const float f = pm[s] == -__builtin_inff() ? 0.0f : exp2f(pm[s] - M);
+    L = fmaf(f, pl[s], L);
+    O = fmaf(f, po[s], O);
+  }
+  for (int s = COMBINE_PRELOAD; s < a.splits; ++s) {
     const float* ps = base + (int64_t)s * GQA * PART;
     const float f = ps[0] == -__builtin_inff() ? 0.0f : exp2f(ps[0] - M);
     L = fmaf(f, ps[1], L);
@@ -937,7 +965,7 @@ extern "C" int vh_kivi_attention(const vh_kivi_desc* d, vh_stream_t stream) {
   hipStream_t s = vh::as_stream(stream);
   const unsigned P = (unsigned)(d->batch * d->nkv);
   if (splits > 0) hipLaunchKernelGGL(k_kivi_split, dim3((unsigned)splits, P), dim3(ATT_WAVES * 64), 0, s, a);
-  hipLaunchKernelGGL(k_kivi_combine, dim3((unsigned)(d->batch * d->nq)), dim3(HEAD_DIM), 0, s, a, d->attn,
+  hipLaunchKernelGGL(k_kivi_combine, dim3((unsigned)(d->batch * d->nq)), dim3(COMBINE_THREADS), 0, s, a, d->attn,
                      (_Float16*)d->attn_fq, (int*)d->flag);
   return vh::check_launch("vh_kivi_attention");
 }
