@@ -347,6 +347,65 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   const vh_epilogue& e = g.epi;
   float sc = 1.0f;
   if (e.scale) sc = e.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)e.scale) : *(const float*)e.scale;
+
+  // bf16 output through LDS: each wave rounds its sub-tile (hardware
+  // converter, round half to even), writes it row-major to LDS (the stage
+  // buffers are free after the loop's last barrier), and stores whole
+  // 16-byte row chunks.
+  constexpr int SUBM = BM / WM, SUBN = BN / WN, PITCH = SUBN + 8;  // bf16 elements
+  static_assert(WM * WN * SUBM * PITCH * 2 <= 2 * (BM + BN) * ROWP, "epilogue tile does not fit the stage LDS");
+  if (e.out_dtype == VH_BF16 && ((uintptr_t)g.C % 16) == 0 && (g.ldc % 8) == 0 && (g.N % 8) == 0) {
+    uint16_t* ct = (uint16_t*)smem + wave * SUBM * PITCH;
+    const bool round_scale = e.mode == EPI_ROUND_SCALE;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * SUBN + j * 32 + lrow;
+      float bias = 0.0f;
+      if (e.bias && col < g.N)
+        bias = e.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)e.bias)[col]) : ((const float*)e.bias)[col];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
+          if (round_scale) {
+            // dequantize(linear(xq, wq), s): round to bf16, times s, round again
+            const uint32_t b = f2bf2_hw(v0, v1);
+            v0 = bf2f(b & 0xffffu) * sc;
+            v1 = bf2f(b >> 16) * sc;
+          } else {
+            if (e.scale) {
+              v0 *= sc;
+              v1 *= sc;
+            }
+            if (e.bias) {
+              v0 += bias;
+              v1 += bias;
+            }
+          }
+          const uint32_t o = f2bf2_hw(v0, v1);
+          const int row = i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+          ct[row * PITCH + j * 32 + lrow] = (uint16_t)(o & 0xffffu);
+          ct[(row + 1) * PITCH + j * 32 + lrow] = (uint16_t)(o >> 16);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    constexpr int CPR = SUBN / 8;  // 16-byte chunks per row
+    static_assert((SUBM * CPR) % 64 == 0, "chunks must divide among the wave");
+#pragma unroll
+    for (int it = 0; it < SUBM * CPR / 64; ++it) {
+      const int q = lane + 64 * it;
+      const int row = q / CPR, ch = q % CPR;
+      const int64_t grow = m0 + wm * SUBM + row;
+      const int64_t gcol = n0 + wn * SUBN + ch * 8;
+      const uint4 v = *(const uint4*)(ct + row * PITCH + ch * 8);
+      if (grow < g.M && gcol < g.N) *(uint4*)((uint16_t*)g.C + grow * g.ldc + gcol) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
