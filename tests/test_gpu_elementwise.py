@@ -122,3 +122,24 @@ def test_cpu_tensor_fails_loudly():
     x = torch.randn(16).bfloat16()
     with pytest.raises((RuntimeError, NotImplementedError)):
         torch.ops.quantized_ops.quantize(x, torch.tensor(1.0, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.0173, 3.5, 0.0078125, 2.0**-130, 1.5e38])
+def test_quantize_packed_e4m3_every_bf16_pattern(scale):
+    """The per-tensor E4M3 fast path (packed bytes for the FP8 GEMM): all
+    65,536 bf16 patterns against the oracle's quantize, read back through the
+    table entry's E4M3 byte.  A subnormal and a huge scale force the exact
+    fallback; 0.0173 puts many quotients next to bf16 rounding midpoints."""
+    from voyager_amd import packed
+
+    x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    s = torch.tensor(scale, dtype=torch.bfloat16)
+    tab = T.quantization_map("fp8_e4m3")
+    exp = O.quantize(x, s, qmap=tab)  # table values (bf16)
+    got = packed.quantize_packed(x.cuda(), s.cuda(), tab.cuda()).cpu()
+    back = packed.unpack_codes(got.cuda(), tab.cuda()).cpu()
+    assert_same_bits(back, exp, f"scale {scale}")
+    # the packed byte is the OCP E4M3 encoding of the table value, sign of zero included
+    ref = exp.float().to(torch.float8_e4m3fn).view(torch.uint8)
+    fin = ~torch.isnan(exp)
+    assert torch.equal(got[fin], ref[fin])

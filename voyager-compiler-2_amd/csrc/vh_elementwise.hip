@@ -207,6 +207,89 @@ k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_p
 // same midpoint test as div_bf16 with the hardware bf16 converter.
 constexpr int UNROLL = 4;
 
+typedef unsigned short vh_u16x2 __attribute__((ext_vector_type(2)));
+
+VH_DEV uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(vh_u16x2, a) - __builtin_bit_cast(vh_u16x2, b));
+}
+VH_DEV uint32_t pk_min_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_min(__builtin_bit_cast(vh_u16x2, a), __builtin_bit_cast(vh_u16x2, b)));
+}
+VH_DEV uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(vh_u16x2, a), __builtin_bit_cast(vh_u16x2, b)));
+}
+
+// Per-tensor quantize to packed OCP E4M3 bytes (the FP8 GEMM operand):
+// code = E4M3(bf16(x / s)) with saturation at 448, as the table does.  Per
+// pair of elements: x * rcp(s), the hardware bf16 rounding, the 448 clamp as
+// a packed integer min on the bf16 magnitude, the hardware fp8 converter
+// (+0.0 first: an exact zero takes code 0 whatever its sign).  Two running
+// packed 16-bit extremes flag the rare cases this shortcut cannot decide --
+// a product within 4 fp32 ulps of a bf16 rounding midpoint, a NaN -- and the
+// thread then redoes its elements with the correctly rounded division.
+__global__ void __launch_bounds__(256)
+k_quantize_e4m3_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int sdt, uint8_t* __restrict__ out) {
+  const float s = load_any(sp, sdt, 0);
+  const float as = fabsf(s);
+  const bool fast_scale = as >= 0x1p-126f && as <= 0x1p126f;
+  const float r = __builtin_amdgcn_rcpf(s);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t v0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v0 < nvec; v0 += stride * UNROLL) {
+    uint4 raw[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t v = v0 + u * stride;
+      raw[u] = v < nvec ? *(const uint4*)(x + v * 8) : make_uint4(0, 0, 0, 0);
+    }
+    uint2 res[UNROLL];
+    uint32_t mn = 0xffffffffu, mx = 0u;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+      uint32_t o[2] = {0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float q0 = __uint_as_float(w[j] << 16) * r;
+        const float q1 = __uint_as_float(w[j] & 0xffff0000u) * r;
+        const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(q1), __float_as_uint(q0), 0x05040100u);
+        mn = pk_min_u16(mn, pk_sub_u16(lo, 0x7ffc7ffcu));
+        uint32_t b = f2bf2_hw(q0, q1);
+        const uint32_t m = b & 0x7fff7fffu;
+        mx = pk_max_u16(mx, m);
+        b = pk_min_u16(m, 0x43e043e0u) | (b & 0x80008000u);
+        const float f0 = __uint_as_float(b << 16) + 0.0f;
+        const float f1 = __uint_as_float(b & 0xffff0000u) + 0.0f;
+        if (j & 1) o[j >> 1] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f0, f1, (int)o[j >> 1], true);
+        else o[j >> 1] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f0, f1, (int)o[j >> 1], false);
+      }
+      res[u] = make_uint2(o[0], o[1]);
+    }
+    const bool exact_needed = !fast_scale || (mn & 0xffffu) <= 8u || (mn >> 16) <= 8u || (mx & 0xffffu) > 0x7f80u ||
+                              (mx >> 16) > 0x7f80u;
+    if (exact_needed) {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+        uint32_t o[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xv = bf2f(j & 1 ? w[j >> 1] >> 16 : w[j >> 1] & 0xffffu);
+          const uint32_t c = e4m3_hw_code(bf2f(f2bf(xv / s)));
+          o[j >> 2] |= c << (8 * (j & 3));
+        }
+        res[u] = make_uint2(o[0], o[1]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t v = v0 + u * stride;
+      if (v < nvec) *(uint2*)(out + v * 8) = res[u];
+    }
+  }
+}
+
 template <int KIND, bool PACKED>
 __global__ void __launch_bounds__(256)
 k_quantize_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int sdt, vh_format f,
@@ -362,6 +445,9 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
       if (out_dtype == VH_U8) {
         if constexpr (K == K_NONE || K == K_IDENTITY || K == K_LUT) {
           return (int)VH_EINVAL;  // unreachable: checked by packable()
+        } else if constexpr (K == K_E4M3) {
+          hipLaunchKernelGGL(k_quantize_e4m3_pt, dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)x, nvec,
+                             sp.ptr, sp.dtype, (uint8_t*)out);
         } else {
           hipLaunchKernelGGL((k_quantize_pt<K, true>), dim3((unsigned)blocks), dim3(256), 0, st,
                              (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, out);
