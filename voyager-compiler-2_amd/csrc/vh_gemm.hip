@@ -145,6 +145,227 @@ __device__ __forceinline__ uint4 finish_raw(const uint4& w, int c, int64_t k0, c
   }
 }
 
+// ------------------------------------------------------------ epilogue
+// Wave (wm, wn) holds TM x TN 32x32 accumulator tiles of its (32 TM) x
+// (32 TN) sub-tile: lane holds column lane % 32 of each tile, rows
+// (r/4)*8 + (lane/32)*4 + r%4 of accumulator element r.  The caller has
+// finished with the LDS stage buffers (all waves past a barrier) when the
+// bf16 path reuses them.
+// True when the bf16 LDS-staged epilogue applies: bf16 output whose rows
+// start 16-byte aligned and hold whole 8-element chunks.
+__host__ __device__ inline bool lds_epilogue_ok(const void* C, int out_dtype, int64_t ldc, int64_t N) {
+  return out_dtype == VH_BF16 && ((uintptr_t)C % 16) == 0 && (ldc % 8) == 0 && (N % 8) == 0;
+}
+
+__device__ __forceinline__ float epi_scale(const vh_epilogue& e) {
+  if (!e.scale) return 1.0f;
+  return e.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)e.scale) : *(const float*)e.scale;
+}
+
+// bf16 output through LDS: each wave rounds its sub-tile (hardware
+// converter, round half to even), writes it row-major to LDS (padded rows,
+// WM * WN * 32 TM * (32 TN + 8) bf16 in all), and stores whole 16-byte row
+// chunks.  Needs lds_epilogue_ok.
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_tile_lds(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint8_t* smem, int64_t m0,
+                                               int64_t n0, int wave, int wm, int wn, int lane) {
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  const vh_epilogue& e = g.epi;
+  const float sc = epi_scale(e);
+  constexpr int SUBM = TM * 32, SUBN = TN * 32, PITCH = SUBN + 8;  // bf16 elements
+  uint16_t* ct = (uint16_t*)smem + wave * SUBM * PITCH;
+  const bool round_scale = e.mode == EPI_ROUND_SCALE;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = n0 + wn * SUBN + j * 32 + lrow;
+    float bias = 0.0f;
+    if (e.bias && col < g.N)
+      bias = e.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)e.bias)[col]) : ((const float*)e.bias)[col];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
+        if (round_scale) {
+          // dequantize(linear(xq, wq), s): round to bf16, times s, round again
+          const uint32_t b = f2bf2_hw(v0, v1);
+          v0 = bf2f(b & 0xffffu) * sc;
+          v1 = bf2f(b >> 16) * sc;
+        } else {
+          if (e.scale) {
+            v0 *= sc;
+            v1 *= sc;
+          }
+          if (e.bias) {
+            v0 += bias;
+            v1 += bias;
+          }
+        }
+        const uint32_t o = f2bf2_hw(v0, v1);
+        const int row = i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+        ct[row * PITCH + j * 32 + lrow] = (uint16_t)(o & 0xffffu);
+        ct[(row + 1) * PITCH + j * 32 + lrow] = (uint16_t)(o >> 16);
+      }
+      // one accumulator tile at a time keeps the register demand at 16
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  constexpr int CPR = SUBN / 8;  // 16-byte chunks per row
+  static_assert((SUBM * CPR) % 64 == 0, "chunks must divide among the wave");
+#pragma unroll
+  for (int it = 0; it < SUBM * CPR / 64; ++it) {
+    const int q = lane + 64 * it;
+    const int row = q / CPR, ch = q % CPR;
+    const int64_t grow = m0 + wm * SUBM + row;
+    const int64_t gcol = n0 + wn * SUBN + ch * 8;
+    const uint4 v = *(const uint4*)(ct + row * PITCH + ch * 8);
+    if (grow < g.M && gcol < g.N) *(uint4*)((uint16_t*)g.C + grow * g.ldc + gcol) = v;
+  }
+}
+
+// store_tile_lds for transposed accumulators: tile (i, j) holds rows n of
+// B tile j by columns m of A tile i, so lane holds output row m = lane % 32
+// and, per group q of four accumulator elements, four consecutive output
+// columns n = 8 q + 4 (lane / 32) + {0..3}: one 8-byte LDS write each.
+// MODE: 0 round-scale (dequantize(linear(xq, wq), s): round to bf16, times
+// s, round again), 1 scale only, 2 scale and bias.
+template <int TM, int TN, int MODE>
+__device__ __forceinline__ void stage_tile_t(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint16_t* ct, int64_t n0,
+                                             int wn, int lane) {
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  const vh_epilogue& e = g.epi;
+  const float sc = epi_scale(e);
+  constexpr int SUBN = TN * 32, PITCH = SUBN + 8;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = j * 32 + q * 8 + lhalf * 4;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          v[u] = acc[i][j][4 * q + u];
+          if constexpr (MODE == 0) {
+            v[u] = rbf(v[u]) * sc;
+          } else {
+            v[u] *= sc;
+            if constexpr (MODE == 2) {
+              const int64_t col = n0 + wn * SUBN + nl + u;
+              if (col < g.N)
+                v[u] += e.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)e.bias)[col]) : ((const float*)e.bias)[col];
+            }
+          }
+        }
+        *(uint2*)(ct + (i * 32 + lrow) * PITCH + nl) = make_uint2(f2bf2_hw(v[0], v[1]), f2bf2_hw(v[2], v[3]));
+      }
+      // one accumulator tile at a time keeps the register demand at 16
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void store_tile_lds_t(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint8_t* smem, int64_t m0,
+                                                 int64_t n0, int wave, int wm, int wn, int lane) {
+  constexpr int SUBM = TM * 32, SUBN = TN * 32, PITCH = SUBN + 8;  // bf16 elements
+  uint16_t* ct = (uint16_t*)smem + wave * SUBM * PITCH;
+  if (g.epi.mode == EPI_ROUND_SCALE) stage_tile_t<TM, TN, 0>(g, acc, ct, n0, wn, lane);
+  else if (!g.epi.bias) stage_tile_t<TM, TN, 1>(g, acc, ct, n0, wn, lane);
+  else stage_tile_t<TM, TN, 2>(g, acc, ct, n0, wn, lane);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  constexpr int CPR = SUBN / 8;  // 16-byte chunks per row
+  static_assert((SUBM * CPR) % 64 == 0, "chunks must divide among the wave");
+#pragma unroll
+  for (int it = 0; it < SUBM * CPR / 64; ++it) {
+    const int q = lane + 64 * it;
+    const int row = q / CPR, ch = q % CPR;
+    const int64_t grow = m0 + wm * SUBM + row;
+    const int64_t gcol = n0 + wn * SUBN + ch * 8;
+    const uint4 v = *(const uint4*)(ct + row * PITCH + ch * 8);
+    if (grow < g.M && gcol < g.N) *(uint4*)((uint16_t*)g.C + grow * g.ldc + gcol) = v;
+  }
+}
+
+// Element-wise stores (f32 output, or bf16 rows the LDS path cannot take).
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_tile_direct(const GemmArgs& g, f32x16 (&acc)[TM][TN], int64_t m0, int64_t n0,
+                                                  int wm, int wn, int lane) {
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  const vh_epilogue& e = g.epi;
+  const float sc = epi_scale(e);
+  constexpr int SUBM = TM * 32, SUBN = TN * 32;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * SUBN + j * 32 + lrow;
+      if (col >= g.N) continue;
+      float bias = 0.0f;
+      if (e.bias) bias = e.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)e.bias)[col]) : ((const float*)e.bias)[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * SUBM + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+        if (row >= g.M) continue;
+        float v = acc[i][j][r];
+        if (e.mode == EPI_ROUND_SCALE) {
+          // dequantize(linear(xq, wq), s): the GEMM rounds to bf16, then the
+          // bf16 product with the scale rounds again.
+          v = rbf(rbf(v) * sc);
+        } else {
+          if (e.scale) v = v * sc;
+          if (e.bias) v = v + bias;
+        }
+        if (e.out_dtype == VH_BF16) ((uint16_t*)g.C)[row * g.ldc + col] = (uint16_t)f2bf(v);
+        else ((float*)g.C)[row * g.ldc + col] = v;
+      }
+    }
+  }
+}
+
+// Epilogue of a block tile: wave (wm, wn) holds TM x TN 32x32 accumulator
+// tiles of its (32 TM) x (32 TN) sub-tile; lane holds column lane % 32 of
+// each tile, rows (r/4)*8 + (lane/32)*4 + r%4 of accumulator element r.  The
+// caller has finished with the LDS stage buffers (all waves past a barrier).
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint8_t* smem, int64_t m0,
+                                           int64_t n0, int wave, int wm, int wn, int lane) {
+  if (lds_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N))
+    store_tile_lds<TM, TN, WM, WN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+  else
+    store_tile_direct<TM, TN, WM, WN>(g, acc, m0, n0, wm, wn, lane);
+}
+
+// Block tile id -> (m0, n0).  Blocks are dealt to the 8 XCDs round robin;
+// when the tile count is a multiple of 8, consecutive tile ids are
+// renumbered so that each XCD gets a contiguous range of them, and groups of
+// GM tile-rows are walked column by column so an XCD's blocks share operand
+// panels in its L2.
+__device__ __forceinline__ void tile_origin(int64_t M, int64_t N, int BM, int BN, int64_t& m0, int64_t& n0) {
+  const int64_t tiles_m = (M + BM - 1) / BM;
+  const int64_t tiles_n = (N + BN - 1) / BN;
+  const int64_t ntiles = tiles_m * tiles_n;
+  int64_t pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  constexpr int GM = 8;
+  const int64_t group = pid / (GM * tiles_n);
+  const int64_t first_m = group * GM;
+  const int64_t gsize = (tiles_m - first_m) < GM ? (tiles_m - first_m) : GM;
+  const int64_t tm = first_m + (pid % (GM * tiles_n)) % gsize;
+  const int64_t tn = (pid % (GM * tiles_n)) / gsize;
+  m0 = tm * BM;
+  n0 = tn * BN;
+}
+
 // BM x BN block tile computed by WM x WN waves; MINB blocks per CU; PF
 // register sets of prefetched chunks (2: loads run two steps ahead).
 template <int BM, int BN, int WM, int WN, int MINB, int PF, int AF, int BF>
@@ -166,20 +387,8 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
     __syncthreads();
   }
 
-  // ---- tile id with XCD grouping
-  const int64_t tiles_m = (g.M + BM - 1) / BM;
-  const int64_t tiles_n = (g.N + BN - 1) / BN;
-  const int64_t ntiles = tiles_m * tiles_n;
-  int64_t pid = blockIdx.x;
-  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-  // group GM tile-rows so consecutive ids walk down a column band
-  constexpr int GM = 8;
-  const int64_t group = pid / (GM * tiles_n);
-  const int64_t first_m = group * GM;
-  const int64_t gsize = (tiles_m - first_m) < GM ? (tiles_m - first_m) : GM;
-  const int64_t tm = first_m + (pid % (GM * tiles_n)) % gsize;
-  const int64_t tn = (pid % (GM * tiles_n)) / gsize;
-  const int64_t m0 = tm * BM, n0 = tn * BN;
+  int64_t m0, n0;
+  tile_origin(g.M, g.N, BM, BN, m0, n0);
   const int64_t bat = blockIdx.y;
   g.A += bat * g.sa;
   g.B += bat * g.sb;
@@ -248,6 +457,7 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   constexpr int TN = BN / WN / 32;
   static_assert(TM >= 1 && TN >= 1 && BM % (WM * 32) == 0 && BN % (WN * 32) == 0, "bad wave layout");
   static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "stage chunks must divide among threads");
+  static_assert(WN * BM * (BN / WN + 8) * 2 <= 2 * (BM + BN) * ROWP, "epilogue tile does not fit the stage LDS");
   f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -342,96 +552,247 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   }
   }
 
-  // ---- epilogue: lane holds column lrow of each 32x32 tile, rows
-  // (r/4)*8 + lhalf*4 + r%4.
-  const vh_epilogue& e = g.epi;
-  float sc = 1.0f;
-  if (e.scale) sc = e.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)e.scale) : *(const float*)e.scale;
+  store_tile<TM, TN, WM, WN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+}
 
-  // bf16 output through LDS: each wave rounds its sub-tile (hardware
-  // converter, round half to even), writes it row-major to LDS (the stage
-  // buffers are free after the loop's last barrier), and stores whole
-  // 16-byte row chunks.
-  constexpr int SUBM = BM / WM, SUBN = BN / WN, PITCH = SUBN + 8;  // bf16 elements
-  static_assert(WM * WN * SUBM * PITCH * 2 <= 2 * (BM + BN) * ROWP, "epilogue tile does not fit the stage LDS");
-  if (e.out_dtype == VH_BF16 && ((uintptr_t)g.C % 16) == 0 && (g.ldc % 8) == 0 && (g.N % 8) == 0) {
-    uint16_t* ct = (uint16_t*)smem + wave * SUBM * PITCH;
-    const bool round_scale = e.mode == EPI_ROUND_SCALE;
+// ------------------------------------------------------------ fp8 x fp8
+// E4M3 x E4M3 with the stage loads going straight from global memory into
+// LDS (buffer_load_dwordx4 ... lds): no staging registers, so NS stages of
+// KS K-bytes per row stay in flight in LDS while four waves (2 x 2, one per
+// SIMD) each run a (BM/2) x (BN/2) sub-tile of 32x32x64 MFMAs, KS / 64
+// steps per stage.
+//
+// Stage layout: A rows then B rows, KS bytes each, the row's 16-byte chunks
+// stored at chunk ^ swz(row % 16).  A DMA instruction writes 1 KB of LDS
+// contiguously (1024 / KS rows), lane l to byte 16 l, so the swizzle is
+// applied by choosing which global chunk each lane fetches; with KS = 128
+// every instruction reads whole 128-byte lines.  swz keeps the fragment
+// reads (lane l: row l % 32, chunks 4 t + 2 (l / 32) + {0, 1} of step t) on
+// distinct 16-byte bank groups for every aligned group of 8 lanes within
+// 128 bytes and of 16 lanes within 256 bytes.
+//
+// Stage s: its fragments for step 0 are in registers; each step runs its
+// MFMAs with the next step's fragment reads interleaved.  The DMA of stage
+// s + NS - 1 (into the buffer stage s - 1 used) is spread over the MFMAs up
+// to the middle of the last step, where the wave waits for its own DMA of
+// stage s + 1, waits for its LDS reads, and meets the other waves at a
+// barrier; after it, the reads of stage s + 1's first fragments.  Buffer
+// reuse is safe: every read of stage s - 1's buffer precedes the barrier of
+// stage s - 1 in its wave, and the DMA into it follows that barrier.
+template <int KS>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (KS == 64) return ((r >> 1) & 3) ^ ((r >> 3) & 1);
+  else return (r & 7) ^ ((r >> 3) & 1);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int NST>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(NST >= 0 && NST < 64, "vmcnt range");
+  // s_waitcnt vmcnt(NST), expcnt / lgkmcnt left at their maxima
+  __builtin_amdgcn_s_waitcnt((NST & 15) | (7 << 4) | (15 << 8) | ((NST >> 4) << 14));
+}
+
+// Waits for this wave's outstanding LDS reads, then meets the workgroup.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor words of a raw (unswizzled) resource over [p, p + bytes).
+__device__ __forceinline__ i32x4 raw_desc(const void* p, int64_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+  return i32x4{(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xffffu), n, RSRC_WORD3};
+}
+
+// 16 bytes per lane from rsrc + voff straight into LDS at lds + 16 lane.
+// Written as inline asm so the compiler adds no wait of its own for it: the
+// stage protocol orders these writes (vmcnt waits and barriers).  An offset
+// past the resource reads zero.  m0 carries the LDS address (one wait state
+// before the load uses it: the s_nop).
+__device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t lds, int voff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
+
+template <int BM, int BN, int NS, int KS>
+__global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) k_gemm_f8dl(GemmArgs g) {
+  constexpr int P = KS / 64;                 // MFMA steps per stage
+  constexpr int CPR = KS / 16;               // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;              // rows per DMA instruction
+  constexpr int STAGE = (BM + BN) * KS;      // bytes per stage buffer
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 tiles per wave
+  constexpr int LA = BM / RPI / 4, LB = BN / RPI / 4;  // DMA instructions per wave and stage
+  constexpr int L = LA + LB;
+  static_assert((KS == 64 || KS == 128) && BM % 64 == 0 && BN % 64 == 0 && NS >= 2 && (NS * P) % 2 == 0,
+                "bad fp8 tile");
+  static_assert(BM % (4 * RPI) == 0 && BN % (4 * RPI) == 0, "DMA blocks must divide among the waves");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int64_t m0, n0;
+  tile_origin(g.M, g.N, BM, BN, m0, n0);
+  const int64_t bat = blockIdx.y;
+  g.A += bat * g.sa;
+  g.B += bat * g.sb;
+  g.C = (uint8_t*)g.C + bat * g.sc * 2;
+  const int64_t rows_a = (g.M - m0) < BM ? (g.M - m0) : BM;
+  const int64_t rows_b = (g.N - n0) < BN ? (g.N - n0) : BN;
+  const i32x4 ra = raw_desc(g.A + m0 * g.lda, rows_a * g.lda);
+  const i32x4 rb = raw_desc(g.B + n0 * g.ldb, rows_b * g.ldb);
+  const int K = (int)g.K;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+
+  // DMA: block q of RPI rows (A blocks, then B blocks) is fetched by wave
+  // q % 4; lane l takes row q RPI + l / CPR, LDS chunk l % CPR.  Row % 16 is
+  // the same for all of a wave's blocks (4 RPI is a multiple of 16 or RPI is).
+  const int drow = lane / CPR;
+  const int dchunk = ((lane % CPR) ^ swz<KS>(((wave * RPI) & 15) + drow)) * 16;
+  int voa[LA], vob[LB];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * SUBN + j * 32 + lrow;
-      float bias = 0.0f;
-      if (e.bias && col < g.N)
-        bias = e.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)e.bias)[col]) : ((const float*)e.bias)[col];
+  for (int i = 0; i < LA; ++i) voa[i] = ((wave + 4 * i) * RPI + drow) * (int)g.lda + dchunk;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
+  for (int i = 0; i < LB; ++i) vob[i] = ((wave + 4 * i) * RPI + drow) * (int)g.ldb + dchunk;
+
+  // DMA d of stage ks (0 <= d < L).  Branch-free: a chunk at or past K (the
+  // K tail, the stages padded past the end) gets an offset past the
+  // resource and reads as zero; rows past M / N are past the resource.
+  auto dma = [&](int64_t ks, int d) {
+    const int k0 = (int)(ks * KS);
+    const bool live = k0 + dchunk < K;
+    const uint32_t base = lds0 + (uint32_t)((ks % NS) * STAGE) + wave * 1024;
+    if (d < LA) dma16(ra, base + d * 4096, live ? voa[d] + k0 : (int)0x80000000);
+    else dma16(rb, base + BM * KS + (d - LA) * 4096, live ? vob[d - LA] + k0 : (int)0x80000000);
+  };
+
+  // Fragment read r of step t (0 <= r < 2 (TM + TN)), in the order the
+  // MFMAs (i outer, j inner) first need them: A tile 0, the B tiles, A
+  // tiles 1 ..; r % 2 is the half.
+  const int fsw = swz<KS>(lane & 15);
+  const int arow = (wm * (BM / 2) + (lane & 31)) * KS;
+  const int brow = BM * KS + (wn * (BN / 2) + (lane & 31)) * KS;
+  i32x8 f0a[TM], f0b[TN], f1a[TM], f1b[TN];
+  auto read_one = [&](i32x8* fa, i32x8* fb, int buf, int t, int r) {
+    const uint8_t* base = smem + buf * STAGE;
+    const bool isb = r >= 2 && r < 2 + 2 * TN;
+    const int ti = r < 2 ? 0 : isb ? (r - 2) >> 1 : 1 + ((r - 2 - 2 * TN) >> 1);
+    const int chunk = (4 * t + 2 * (lane >> 5) + (r & 1)) ^ fsw;
+    const uint4 v = *(const uint4*)(base + (isb ? brow : arow) + ti * 32 * KS + chunk * 16);
+    i32x8& f = isb ? fb[ti] : fa[ti];
+    if (r & 1) f.hi = i32x4{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+    else f.lo = i32x4{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+  };
+
+  f32x16 acc[TM][TN];
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
-          if (round_scale) {
-            // dequantize(linear(xq, wq), s): round to bf16, times s, round again
-            const uint32_t b = f2bf2_hw(v0, v1);
-            v0 = bf2f(b & 0xffffu) * sc;
-            v1 = bf2f(b >> 16) * sc;
-          } else {
-            if (e.scale) {
-              v0 *= sc;
-              v1 *= sc;
-            }
-            if (e.bias) {
-              v0 += bias;
-              v1 += bias;
-            }
-          }
-          const uint32_t o = f2bf2_hw(v0, v1);
-          const int row = i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-          ct[row * PITCH + j * 32 + lrow] = (uint16_t)(o & 0xffffu);
-          ct[(row + 1) * PITCH + j * 32 + lrow] = (uint16_t)(o >> 16);
-        }
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto mfma = [&](const i32x8* fa, const i32x8* fb, int q) {
+    const int i = q / TN, j = q % TN;
+    // B as the row operand: accumulators come out transposed (store_tile_lds_t)
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+  };
+
+  constexpr int Q = TM * TN;           // MFMAs per step
+  constexpr int H1 = TM / 2 * TN;      // MFMAs of the last step before the barrier
+  constexpr int NR = 2 * (TM + TN);    // fragment reads per step
+  constexpr int PRE = (P - 1) * Q + H1;  // MFMAs of a stage before its barrier
+
+  // The stage count is padded to a multiple of NS (padded stages are zero)
+  // so the loop body has no exits between stages.
+  const int64_t nk = ((g.K + KS - 1) / KS + NS - 1) / NS * NS;
+  // prologue: stages 0 .. NS-2 in flight, stage 0's first fragments read
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+#pragma unroll
+    for (int d = 0; d < L; ++d) dma(s, d);
+  wait_vmcnt<(NS - 2) * L>();
+  lds_barrier();
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read_one(f0a, f0b, 0, 0, r);
+
+  // Step t of stage ks on fragments F, reading the next step's into G.
+  auto step = [&](int64_t ks, int t, i32x8* fa, i32x8* fb, i32x8* ga, i32x8* gb) {
+    const int buf = (int)(ks % NS);
+    if (t < P - 1) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+#pragma unroll
+        for (int r = q * NR / Q; r < (q + 1) * NR / Q; ++r) read_one(ga, gb, buf, t + 1, r);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma(fa, fb, q);
+        __builtin_amdgcn_sched_barrier(0);
+        const int m = t * Q + q;
+#pragma unroll
+        for (int d = m * L / PRE; d < (m + 1) * L / PRE; ++d) dma(ks + NS - 1, d);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < H1; ++q) {
+        mfma(fa, fb, q);
+        __builtin_amdgcn_sched_barrier(0);
+        const int m = t * Q + q;
+#pragma unroll
+        for (int d = m * L / PRE; d < (m + 1) * L / PRE; ++d) dma(ks + NS - 1, d);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_vmcnt<(NS - 2) * L>();
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = H1; q < Q; ++q) {
+#pragma unroll
+        for (int r = (q - H1) * NR / (Q - H1); r < (q - H1 + 1) * NR / (Q - H1); ++r)
+          read_one(ga, gb, (buf + 1) % NS, 0, r);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma(fa, fb, q);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    constexpr int CPR = SUBN / 8;  // 16-byte chunks per row
-    static_assert((SUBM * CPR) % 64 == 0, "chunks must divide among the wave");
+  };
+  for (int64_t ks = 0; ks < nk; ks += NS) {
 #pragma unroll
-    for (int it = 0; it < SUBM * CPR / 64; ++it) {
-      const int q = lane + 64 * it;
-      const int row = q / CPR, ch = q % CPR;
-      const int64_t grow = m0 + wm * SUBM + row;
-      const int64_t gcol = n0 + wn * SUBN + ch * 8;
-      const uint4 v = *(const uint4*)(ct + row * PITCH + ch * 8);
-      if (grow < g.M && gcol < g.N) *(uint4*)((uint16_t*)g.C + grow * g.ldc + gcol) = v;
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * (BN / WN) + j * 32 + lrow;
-      if (col >= g.N) continue;
-      float bias = 0.0f;
-      if (e.bias) bias = e.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)e.bias)[col]) : ((const float*)e.bias)[col];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * (BM / WM) + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-        if (row >= g.M) continue;
-        float v = acc[i][j][r];
-        if (e.mode == EPI_ROUND_SCALE) {
-          // dequantize(linear(xq, wq), s): the GEMM rounds to bf16, then the
-          // bf16 product with the scale rounds again.
-          v = rbf(rbf(v) * sc);
-        } else {
-          if (e.scale) v = v * sc;
-          if (e.bias) v = v + bias;
-        }
-        if (e.out_dtype == VH_BF16) ((uint16_t*)g.C)[row * g.ldc + col] = (uint16_t)f2bf(v);
-        else ((float*)g.C)[row * g.ldc + col] = v;
-      }
+    for (int u = 0; u < NS * P; u += 2) {
+      step(ks + u / P, u % P, f0a, f0b, f1a, f1b);
+      step(ks + (u + 1) / P, (u + 1) % P, f1a, f1b, f0a, f0b);
     }
   }
+  // every DMA has landed and every wave is done with the stage buffers
+  wait_vmcnt<0>();
+  __syncthreads();
+  store_tile_lds_t<TM, TN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+}
+
+template <int BM, int BN, int NS, int KS>
+int launch_f8dl(const GemmArgs& g, int64_t batch, hipStream_t stream) {
+  constexpr size_t stages = (size_t)NS * (BM + BN) * KS;
+  constexpr size_t epi = (size_t)4 * (BM / 2) * (BN / 2 + 8) * 2;  // store_tile_lds_t: 4 waves, bf16, padded rows
+  constexpr size_t smem = stages > epi ? stages : epi;
+  static_assert(smem <= 160 * 1024, "LDS");
+  const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)k_gemm_f8dl<BM, BN, NS, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)smem) != hipSuccess) {
+      vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
+      return VH_ELAUNCH;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_gemm_f8dl<BM, BN, NS, KS>), dim3((unsigned)tiles, (unsigned)batch), dim3(256), smem, stream, g);
+  return vh::check_launch("vh_gemm");
 }
 
 template <int BM, int BN, int WM, int WN, int MINB, int PF, int AF, int BF>
@@ -520,11 +881,12 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
   auto tiles = [&](int bm, int bn) { return ((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn); };
   int cfg = d->tile_hint;
   if (cfg == 0) {
-    // Measured on MI355X at M = 2048 with amax-scaled fp8 data (K in {4096,
-    // 14336}, N in {1024, 4096, 14336}): 8-wave blocks (two waves per SIMD)
-    // cover the operand loads; the largest tile that still fills the GPU
-    // wins (less LDS and L2 traffic per MFMA); a grid too small for 256 CUs
-    // takes 128 x 64.
+    // Register-staged kernel (bf16, MX-int8 and posit8 operands; fp8 when
+    // the LDS epilogue does not apply).  Measured on MI355X at M = 2048 with
+    // fp8 data (K in {4096, 14336}, N in {1024, 4096, 14336}): 8-wave
+    // blocks (two waves per SIMD) cover the operand loads; the largest tile
+    // that still fills the GPU wins (less LDS and L2 traffic per MFMA); a
+    // grid too small for 256 CUs takes 128 x 64.
     const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
     const int64_t t128 = tiles(128, 128) * batch;
     if (t256 >= 384) cfg = 6;
@@ -546,6 +908,29 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       default: return launch_tile<128, 64, 2, 2, 2, 2, AF, BF>(g, batch, st);
     }
   };
+  if (fp8 && lds_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N)) {
+    if (d->tile_hint == 0) {
+      // Direct-to-LDS kernels with 128-byte stages.  Measured on MI355X at
+      // M = 2048 (K in {4096, 14336}, N in {1024, 4096, 14336}): the
+      // largest tile that still gives every CU a block wins, since each
+      // CU's operand stream from L2 is the limit; 256 x 256 only pays when
+      // the grid covers the GPU well over once.
+      const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
+      cfg = t256 >= 384 ? 30 : t2561 >= 224 ? 31 : 33;
+    }
+    switch (cfg) {
+      case 20: return launch_f8dl<256, 256, 4, 64>(g, batch, st);
+      case 21: return launch_f8dl<256, 128, 4, 64>(g, batch, st);
+      case 23: return launch_f8dl<128, 128, 8, 64>(g, batch, st);
+      case 24: return launch_f8dl<128, 256, 4, 64>(g, batch, st);
+      case 30: return launch_f8dl<256, 256, 2, 128>(g, batch, st);
+      case 31: return launch_f8dl<256, 128, 3, 128>(g, batch, st);
+      case 32: return launch_f8dl<128, 256, 3, 128>(g, batch, st);
+      case 33: return launch_f8dl<128, 128, 4, 128>(g, batch, st);
+      case 34: return launch_f8dl<256, 128, 2, 128>(g, batch, st);
+      default: break;
+    }
+  }
   if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
   if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16) return pick(Fmts<OP_BF16, OP_BF16>{});
   if (d->a_fmt == OP_MXI8 && d->b_fmt == OP_MXI8) return pick(Fmts<OP_MXI8, OP_MXI8>{});
