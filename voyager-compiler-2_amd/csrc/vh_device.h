@@ -39,6 +39,18 @@ VH_DEV uint32_t f2bf2_hw(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// Streaming accesses that bypass cache residency (the nt bit): each element
+// of a large elementwise op is touched once, so its lines should not evict
+// data that is reused.  16-byte loads, 8- and 16-byte stores.
+typedef unsigned int vh_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int vh_u32x2 __attribute__((ext_vector_type(2)));
+VH_DEV uint4 ld_stream16(const void* p) {
+  const vh_u32x4 v = __builtin_nontemporal_load((const vh_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+VH_DEV void st_stream8(void* p, uint2 v) { __builtin_nontemporal_store(vh_u32x2{v.x, v.y}, (vh_u32x2*)p); }
+VH_DEV void st_stream16(void* p, uint4 v) { __builtin_nontemporal_store(vh_u32x4{v.x, v.y, v.z, v.w}, (vh_u32x4*)p); }
+
 // The float32 value rounded to bfloat16 and back (an eager bf16 op result).
 VH_DEV float rbf(float f) { return bf2f(f2bf(f)); }
 

@@ -132,7 +132,7 @@ k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_p
   const bool full = base + VEC <= n;
   float xv[VEC];
   if (x_dtype == VH_BF16 && full) {
-    uint4 raw = *(const uint4*)((const uint16_t*)x + base);
+    uint4 raw = ld_stream16((const uint16_t*)x + base);
     uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -183,7 +183,7 @@ k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_p
       uint2 pk;
       pk.x = res[0] | (res[1] << 8) | (res[2] << 16) | (res[3] << 24);
       pk.y = res[4] | (res[5] << 8) | (res[6] << 16) | (res[7] << 24);
-      *(uint2*)(o + base) = pk;
+      st_stream8(o + base, pk);
     } else {
       for (int j = 0; j < VEC; ++j)
         if (base + j < n) o[base + j] = (uint8_t)res[j];
@@ -194,7 +194,7 @@ k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_p
     pk.y = f2bf(outv[2]) | (f2bf(outv[3]) << 16);
     pk.z = f2bf(outv[4]) | (f2bf(outv[5]) << 16);
     pk.w = f2bf(outv[6]) | (f2bf(outv[7]) << 16);
-    *(uint4*)((uint16_t*)out + base) = pk;
+    st_stream16((uint16_t*)out + base, pk);
   } else {
     for (int j = 0; j < VEC; ++j)
       if (base + j < n) store_any(out, out_dtype, base + j, outv[j]);
@@ -241,7 +241,7 @@ k_quantize_e4m3_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp,
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int64_t v = v0 + u * stride;
-      raw[u] = v < nvec ? *(const uint4*)(x + v * 8) : make_uint4(0, 0, 0, 0);
+      raw[u] = v < nvec ? ld_stream16(x + v * 8) : make_uint4(0, 0, 0, 0);
     }
     uint2 res[UNROLL];
     uint32_t mn = 0xffffffffu, mx = 0u;
@@ -285,7 +285,7 @@ k_quantize_e4m3_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp,
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int64_t v = v0 + u * stride;
-      if (v < nvec) *(uint2*)(out + v * 8) = res[u];
+      if (v < nvec) st_stream8(out + v * 8, res[u]);
     }
   }
 }
@@ -306,7 +306,7 @@ k_quantize_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int 
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int64_t v = v0 + u * stride;
-      raw[u] = v < nvec ? *(const uint4*)(x + v * 8) : make_uint4(0, 0, 0, 0);
+      raw[u] = v < nvec ? ld_stream16(x + v * 8) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -353,9 +353,9 @@ k_quantize_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int 
         o[j] = PACKED ? (c[0] | (c[1] << 8)) : (c[0] | (c[1] << 16));
       }
       if constexpr (PACKED) {
-        *(uint2*)((uint8_t*)out + v * 8) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+        st_stream8((uint8_t*)out + v * 8, make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16)));
       } else {
-        *(uint4*)((uint16_t*)out + v * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+        st_stream16((uint16_t*)out + v * 8, make_uint4(o[0], o[1], o[2], o[3]));
       }
     }
   }

@@ -47,6 +47,7 @@ struct GemmArgs {
   const uint16_t* lut;       // OP_P8: 256 bfloat16 entries (device)
   int64_t sa, sb, sc;        // batch strides: bytes of A / B, elements of C
   int64_t ssa, ssb;          // batch strides of the scale bytes
+  int group_m;               // tile-rows per column walk (tile_origin)
   vh_epilogue epi;
 };
 
@@ -349,14 +350,13 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[TM][
 // when the tile count is a multiple of 8, consecutive tile ids are
 // renumbered so that each XCD gets a contiguous range of them, and groups of
 // GM tile-rows are walked column by column so an XCD's blocks share operand
-// panels in its L2.
-__device__ __forceinline__ void tile_origin(int64_t M, int64_t N, int BM, int BN, int64_t& m0, int64_t& n0) {
+// panels in its L2 (group_rows picks GM).
+__device__ __forceinline__ void tile_origin(int64_t M, int64_t N, int BM, int BN, int GM, int64_t& m0, int64_t& n0) {
   const int64_t tiles_m = (M + BM - 1) / BM;
   const int64_t tiles_n = (N + BN - 1) / BN;
   const int64_t ntiles = tiles_m * tiles_n;
   int64_t pid = blockIdx.x;
   if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-  constexpr int GM = 8;
   const int64_t group = pid / (GM * tiles_n);
   const int64_t first_m = group * GM;
   const int64_t gsize = (tiles_m - first_m) < GM ? (tiles_m - first_m) : GM;
@@ -388,7 +388,7 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
   }
 
   int64_t m0, n0;
-  tile_origin(g.M, g.N, BM, BN, m0, n0);
+  tile_origin(g.M, g.N, BM, BN, g.group_m, m0, n0);
   const int64_t bat = blockIdx.y;
   g.A += bat * g.sa;
   g.B += bat * g.sb;
@@ -619,26 +619,29 @@ __device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t lds, int voff)
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 
-template <int BM, int BN, int NS, int KS>
-__global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) k_gemm_f8dl(GemmArgs g) {
+template <int BM, int BN, int NS, int KS, int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
+    __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) k_gemm_f8dl(GemmArgs g) {
   constexpr int P = KS / 64;                 // MFMA steps per stage
   constexpr int CPR = KS / 16;               // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;              // rows per DMA instruction
   constexpr int STAGE = (BM + BN) * KS;      // bytes per stage buffer
-  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 tiles per wave
-  constexpr int LA = BM / RPI / 4, LB = BN / RPI / 4;  // DMA instructions per wave and stage
+  constexpr int NW = WM * WN;                // waves
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // 32x32 tiles per wave
+  constexpr int LA = BM / RPI / NW, LB = BN / RPI / NW;  // DMA instructions per wave and stage
   constexpr int L = LA + LB;
   static_assert((KS == 64 || KS == 128) && BM % 64 == 0 && BN % 64 == 0 && NS >= 2 && (NS * P) % 2 == 0,
                 "bad fp8 tile");
-  static_assert(BM % (4 * RPI) == 0 && BN % (4 * RPI) == 0, "DMA blocks must divide among the waves");
+  static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0 && TM >= 2 && TM % 2 == 0 && TN >= 1,
+                "DMA blocks must divide among the waves");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
 
   int64_t m0, n0;
-  tile_origin(g.M, g.N, BM, BN, m0, n0);
+  tile_origin(g.M, g.N, BM, BN, g.group_m, m0, n0);
   const int64_t bat = blockIdx.y;
   g.A += bat * g.sa;
   g.B += bat * g.sb;
@@ -651,15 +654,15 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
 
   // DMA: block q of RPI rows (A blocks, then B blocks) is fetched by wave
-  // q % 4; lane l takes row q RPI + l / CPR, LDS chunk l % CPR.  Row % 16 is
-  // the same for all of a wave's blocks (4 RPI is a multiple of 16 or RPI is).
+  // q % NW; lane l takes row q RPI + l / CPR, LDS chunk l % CPR.  Row % 16
+  // is the same for all of a wave's blocks (NW RPI is a multiple of 16).
   const int drow = lane / CPR;
   const int dchunk = ((lane % CPR) ^ swz<KS>(((wave * RPI) & 15) + drow)) * 16;
   int voa[LA], vob[LB];
 #pragma unroll
-  for (int i = 0; i < LA; ++i) voa[i] = ((wave + 4 * i) * RPI + drow) * (int)g.lda + dchunk;
+  for (int i = 0; i < LA; ++i) voa[i] = ((wave + NW * i) * RPI + drow) * (int)g.lda + dchunk;
 #pragma unroll
-  for (int i = 0; i < LB; ++i) vob[i] = ((wave + 4 * i) * RPI + drow) * (int)g.ldb + dchunk;
+  for (int i = 0; i < LB; ++i) vob[i] = ((wave + NW * i) * RPI + drow) * (int)g.ldb + dchunk;
 
   // DMA d of stage ks (0 <= d < L).  Branch-free: a chunk at or past K (the
   // K tail, the stages padded past the end) gets an offset past the
@@ -668,16 +671,16 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     const int k0 = (int)(ks * KS);
     const bool live = k0 + dchunk < K;
     const uint32_t base = lds0 + (uint32_t)((ks % NS) * STAGE) + wave * 1024;
-    if (d < LA) dma16(ra, base + d * 4096, live ? voa[d] + k0 : (int)0x80000000);
-    else dma16(rb, base + BM * KS + (d - LA) * 4096, live ? vob[d - LA] + k0 : (int)0x80000000);
+    if (d < LA) dma16(ra, base + d * NW * 1024, live ? voa[d] + k0 : (int)0x80000000);
+    else dma16(rb, base + BM * KS + (d - LA) * NW * 1024, live ? vob[d - LA] + k0 : (int)0x80000000);
   };
 
   // Fragment read r of step t (0 <= r < 2 (TM + TN)), in the order the
   // MFMAs (i outer, j inner) first need them: A tile 0, the B tiles, A
   // tiles 1 ..; r % 2 is the half.
   const int fsw = swz<KS>(lane & 15);
-  const int arow = (wm * (BM / 2) + (lane & 31)) * KS;
-  const int brow = BM * KS + (wn * (BN / 2) + (lane & 31)) * KS;
+  const int arow = (wm * (BM / WM) + (lane & 31)) * KS;
+  const int brow = BM * KS + (wn * (BN / WN) + (lane & 31)) * KS;
   i32x8 f0a[TM], f0b[TN], f1a[TM], f1b[TN];
   auto read_one = [&](i32x8* fa, i32x8* fb, int buf, int t, int r) {
     const uint8_t* base = smem + buf * STAGE;
@@ -775,28 +778,46 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   store_tile_lds_t<TM, TN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
 }
 
-template <int BM, int BN, int NS, int KS>
-int launch_f8dl(const GemmArgs& g, int64_t batch, hipStream_t stream) {
+// Tile-rows per column walk for a BM x BN grid: the group whose per-XCD
+// block of tiles (the XCD's share of the grid) streams the fewest operand
+// rows, GM BM of A plus (tiles per XCD / GM) BN of B.
+int group_rows(int64_t M, int64_t N, int BM, int BN) {
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t per_xcd = (tiles_m * tiles_n + 7) / 8;
+  int best = 1;
+  int64_t best_rows = -1;
+  for (int gm = 1; gm <= 16 && gm <= tiles_m; gm *= 2) {
+    const int64_t rows = gm * (int64_t)BM + (per_xcd + gm - 1) / gm * BN;
+    if (best_rows < 0 || rows <= best_rows) best = gm, best_rows = rows;
+  }
+  return best;
+}
+
+template <int BM, int BN, int NS, int KS, int WM = 2, int WN = 2>
+int launch_f8dl(GemmArgs g, int64_t batch, hipStream_t stream) {
+  g.group_m = group_rows(g.M, g.N, BM, BN);
   constexpr size_t stages = (size_t)NS * (BM + BN) * KS;
-  constexpr size_t epi = (size_t)4 * (BM / 2) * (BN / 2 + 8) * 2;  // store_tile_lds_t: 4 waves, bf16, padded rows
+  constexpr size_t epi = (size_t)WM * WN * (BM / WM) * (BN / WN + 8) * 2;  // store_tile_lds_t: bf16, padded rows
   constexpr size_t smem = stages > epi ? stages : epi;
   static_assert(smem <= 160 * 1024, "LDS");
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)k_gemm_f8dl<BM, BN, NS, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void*)k_gemm_f8dl<BM, BN, NS, KS, WM, WN>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)smem) != hipSuccess) {
       vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
       return VH_ELAUNCH;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_f8dl<BM, BN, NS, KS>), dim3((unsigned)tiles, (unsigned)batch), dim3(256), smem, stream, g);
+  hipLaunchKernelGGL((k_gemm_f8dl<BM, BN, NS, KS, WM, WN>), dim3((unsigned)tiles, (unsigned)batch), dim3(WM * WN * 64),
+                     smem, stream, g);
   return vh::check_launch("vh_gemm");
 }
 
 template <int BM, int BN, int WM, int WN, int MINB, int PF, int AF, int BF>
-int launch_tile(const GemmArgs& g, int64_t batch, hipStream_t stream) {
+int launch_tile(GemmArgs g, int64_t batch, hipStream_t stream) {
+  g.group_m = 8;
   constexpr int NT = WM * WN * 64;
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   const size_t smem = 2 * (BM + BN) * ROWP + 512;
@@ -916,7 +937,7 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       // CU's operand stream from L2 is the limit; 256 x 256 only pays when
       // the grid covers the GPU well over once.
       const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
-      cfg = t256 >= 384 ? 30 : t2561 >= 224 ? 31 : 33;
+      cfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : 33;
     }
     switch (cfg) {
       case 20: return launch_f8dl<256, 256, 4, 64>(g, batch, st);
@@ -928,6 +949,10 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       case 32: return launch_f8dl<128, 256, 3, 128>(g, batch, st);
       case 33: return launch_f8dl<128, 128, 4, 128>(g, batch, st);
       case 34: return launch_f8dl<256, 128, 2, 128>(g, batch, st);
+      case 40: return launch_f8dl<256, 256, 2, 128, 2, 4>(g, batch, st);
+      case 41: return launch_f8dl<256, 256, 2, 128, 4, 2>(g, batch, st);
+      case 42: return launch_f8dl<256, 128, 3, 128, 2, 4>(g, batch, st);
+      case 43: return launch_f8dl<256, 128, 3, 128, 4, 2>(g, batch, st);
       default: break;
     }
   }
