@@ -18,7 +18,9 @@ reference's op sequence in eager PyTorch) on a bounded sample.
 
 Options: --gpus N (1 only), --steps K, --warmup W, --no-cpu (skip the CPU
 baseline), --copy-calibration BYTES (run only a plain device copy, for
-rocprofv3 counter calibration).
+rocprofv3 counter calibration), --profile-shapes R (run only, shape by shape
+in SHAPES order, R quantize launches then R GEMM launches, eagerly: dispatch
+order names the shape in a rocprofv3 counter run).
 """
 
 import argparse
@@ -431,6 +433,31 @@ def copy_calibration(nbytes: int):
     print(json.dumps({"copy_bytes": nbytes, "launches": 5}))
 
 
+def profile_shapes(reps: int):
+    """The config-2 kernels shape by shape, for rocprofv3 counter runs."""
+    import voyager_amd  # noqa: F401
+    from voyager_amd import formats, gemm, packed
+    from voyager_amd.ops import _elementwise
+
+    dev = torch.device("cuda:0")
+    tab = formats.quantization_map("fp8_e4m3", dev)
+    fmt = formats.classify(tab).fmt
+    for i, (x, w) in enumerate(make_inputs(dev)):
+        xd, wd = x.to(dev), w.to(dev)
+        sx, sw = amax_scale(xd), amax_scale(wd)
+        s = (sx * sw).contiguous()
+        wq = packed.quantize_packed(wd, sw, tab)
+        y = torch.empty(M, wd.shape[0], dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(reps):
+            xq = _elementwise("quantize", xd, sx, None, None, torch.bfloat16, fmt, None, torch.uint8)
+        for _ in range(reps):
+            gemm.linear_fp8(xq, wq, s, out=y)
+        torch.cuda.synchronize()
+        log(f"profile-shapes: shape {i} (K, N) = {SHAPES[i]} done")
+    print(json.dumps({"profile_shapes": SHAPES, "reps": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -438,6 +465,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0)
+    ap.add_argument("--profile-shapes", type=int, default=0)
     ap.add_argument("--config", type=int, default=2,
                     help="2 (default): the headline line; 1, 3, 4, 5: that config's measurements")
     args = ap.parse_args()
@@ -447,6 +475,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.profile_shapes:
+        profile_shapes(args.profile_shapes)
         return
     if args.config in (1, 3, 4, 5):
         fn = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config]

@@ -9,11 +9,14 @@
 //                power-of-two `block`) K elements; decoded exactly to
 //                bfloat16 (code * 2**e) while staging, then bf16 MFMA;
 //   * OP_P8   -- posit8 codes; decoded through a 256-entry table in LDS.
-// The block tile is BM x BN with a 128-byte K stage per row, double buffered
-// in LDS (rows padded to 144 bytes so a wave's 16-byte fragment reads hit
-// distinct banks); 4 waves (2 x 2), each owning a (BM/2) x (BN/2) sub-tile of
-// 32 x 32 MFMA tiles.  Tiles are ordered so that blocks that share operand
-// rows run on the same XCD (blocks are dealt to the 8 XCDs round robin).
+// Two kernels.  k_gemm_f8dl (FP8 x FP8 with bf16 output) loads its stages
+// straight into LDS; it is described where it is defined.  k_gemm (every
+// format pair) stages through registers: the block tile is BM x BN with a
+// 128-byte K stage per row, double buffered in LDS (rows padded to 144 bytes
+// so a wave's 16-byte fragment reads hit distinct banks); WM x WN waves, each
+// owning a (BM/WM) x (BN/WN) sub-tile of 32 x 32 MFMA tiles.  In both, tiles
+// are ordered so that blocks that share operand rows run on the same XCD
+// (blocks are dealt to the 8 XCDs round robin).
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -558,9 +561,10 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) k_gemm(GemmArgs g) {
 // ------------------------------------------------------------ fp8 x fp8
 // E4M3 x E4M3 with the stage loads going straight from global memory into
 // LDS (buffer_load_dwordx4 ... lds): no staging registers, so NS stages of
-// KS K-bytes per row stay in flight in LDS while four waves (2 x 2, one per
-// SIMD) each run a (BM/2) x (BN/2) sub-tile of 32x32x64 MFMAs, KS / 64
-// steps per stage.
+// KS K-bytes per row stay in flight in LDS while WM x WN waves (4: one per
+// SIMD, accumulators in AGPRs; 8: two per SIMD, so one issues MFMAs while
+// the other waits on a load) each run a (BM/WM) x (BN/WN) sub-tile of
+// 32x32x64 MFMAs, KS / 64 steps per stage.
 //
 // Stage layout: A rows then B rows, KS bytes each, the row's 16-byte chunks
 // stored at chunk ^ swz(row % 16).  A DMA instruction writes 1 KB of LDS
