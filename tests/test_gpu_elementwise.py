@@ -143,3 +143,56 @@ def test_quantize_packed_e4m3_every_bf16_pattern(scale):
     ref = exp.float().to(torch.float8_e4m3fn).view(torch.uint8)
     fin = ~torch.isnan(exp)
     assert torch.equal(got[fin], ref[fin])
+
+
+@pytest.mark.parametrize("dtype", ["posit8_1", "posit8_0", "posit8_2", "posit16_1"])
+@pytest.mark.parametrize("scale", [1.0, 0.0173, 3.5, 2.0**-130, 1.5e38])
+def test_quantize_posit_every_bf16_pattern(dtype, scale):
+    """The posit table path (per-tensor scale, whole 16-byte rows): all
+    65,536 bf16 patterns, reference form and (8-bit posits) packed codes read
+    back through the code table, against the oracle's closed-form posit
+    rounding.  The patterns cover zero, the flush region below the threshold,
+    the saturating region above maxpos and the non-finite inputs; the
+    subnormal and huge scales force the exact-division fallback."""
+    from voyager_amd import packed
+
+    x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    s = torch.tensor(scale, dtype=torch.bfloat16)
+    tab = T.quantization_map(dtype)
+    exp = O.quantize(x, s, qmap=tab)
+    got = torch.ops.quantized_ops.quantize(x.cuda(), s.cuda(), qmap=tab.cuda()).cpu()
+    assert_same_bits(got, exp, f"{dtype} reference form, scale {scale}")
+    if dtype.startswith("posit8"):
+        codes = packed.quantize_packed(x.cuda(), s.cuda(), tab.cuda())
+        back = packed.unpack_codes(codes, tab.cuda()).cpu()
+        assert_same_bits(back, exp, f"{dtype} packed, scale {scale}")
+
+
+@pytest.mark.parametrize("dtype", ["posit8_1", "int8", "fp8_e4m3", "fp8_e5m3", "uint2"])
+@pytest.mark.parametrize("scale", [None, 0.0173, 3.5])
+def test_dequantize_packed_table(dtype, scale):
+    """dequantize of packed codes to bf16 (the per-workgroup 256-entry table
+    path, taken for whole 16-code rows): every code, with and without a
+    scalar scale, against the oracle's dequantize of the reference-form
+    values.  A 40-code tail that takes the generic kernel must agree too."""
+    from voyager_amd import formats, packed
+    from voyager_amd.ops import _elementwise
+
+    tab = T.quantization_map(dtype)
+    g = torch.Generator().manual_seed(21)
+    x = _specials(4096 * 16, g)
+    codes = packed.quantize_packed(x.cuda(), torch.tensor(1.0, dtype=torch.bfloat16).cuda(), tab.cuda())
+    vals = O.quantize(x, torch.tensor(1.0, dtype=torch.bfloat16), qmap=tab)
+    if "int" in dtype:  # an integer code has no negative zero or NaN: both pack as code 0
+        vals = torch.where((vals == 0) | torch.isnan(vals), torch.zeros_like(vals), vals)
+    fmt = formats.classify(tab.cuda()).fmt
+    for n in (codes.numel(), 40):
+        c, v = codes[:n], vals[:n]
+        if scale is None:
+            got = _elementwise("dequantize", c, None, None, None, torch.bfloat16, fmt, None, torch.bfloat16).cpu()
+            assert_same_bits(got, v, f"{dtype} n={n}")
+        else:
+            sv = torch.tensor(scale, dtype=torch.bfloat16)
+            got = _elementwise("dequantize", c, sv.cuda(), None, None, torch.bfloat16, fmt, None,
+                               torch.bfloat16).cpu()
+            assert_same_bits(got, O.dequantize(v, sv), f"{dtype} n={n} scale {scale}")

@@ -10,6 +10,8 @@
 // (bf16) and stores, so a wavefront touches 1 KiB contiguous per access.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+
 #include <cstring>
 #include <string>
 
@@ -290,6 +292,154 @@ k_quantize_e4m3_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp,
   }
 }
 
+// ------------------------------------------------------------ posit tables
+// A posit's code (or reference-form value) as a function of the bfloat16
+// pattern q = bf16(x / s) only changes for magnitudes between the flush
+// threshold and maxpos.  Each workgroup evaluates the closed form once per
+// pattern of [lo, hi] (host-chosen bf16 magnitude bits, one binade beyond
+// both ends) and per sign, plus four slots per sign: zero, every magnitude
+// below lo (flushed), every finite magnitude above hi (saturated) and the
+// non-finite ones; the elements then cost one LDS lookup instead of ~50 VALU
+// ops of the closed form.
+constexpr int TAB_SPECIAL = 4;
+constexpr int TAB_MAX_SPAN = 8192;  // table entries per sign
+
+template <bool PACKED>
+__device__ __forceinline__ void build_posit_table(const vh_format& f, int lo, int hi, uint16_t* tab) {
+  const int per = TAB_SPECIAL + hi - lo + 1;
+  for (int i = threadIdx.x; i < 2 * per; i += blockDim.x) {
+    const int sgn = i / per, j = i % per;
+    const uint32_t mag = j == 0 ? 0u : j == 1 ? 1u : j == 2 ? 0x7f7fu : j == 3 ? 0x7fc0u : (uint32_t)(lo + j - TAB_SPECIAL);
+    const uint32_t b = mag | ((uint32_t)sgn << 15);
+    const float v = fmt_value_k<K_POSIT>(b, f, nullptr);
+    tab[i] = (uint16_t)(PACKED ? fmt_code_k<K_POSIT>(b, v, f, nullptr) : f2bf(v));
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t posit_lookup(uint32_t b, int lo, int hi, int per, const uint16_t* tab) {
+  const uint32_t m = b & 0x7fffu;
+  const int j = m == 0 ? 0 : m >= 0x7f80u ? 3 : (int)m < lo ? 1 : (int)m > hi ? 2 : TAB_SPECIAL + (int)m - lo;
+  return tab[(b >> 15) * per + j];
+}
+
+// quantize(x, s, qmap=posit) per tensor: q = bf16(x / s) as in k_quantize_pt,
+// then the table.  One 1024-thread workgroup per CU builds the table once;
+// its first loads are issued before the build and every later batch is
+// loaded while the previous one converts.
+constexpr int TAB_THREADS = 1024;
+
+template <bool PACKED>
+__global__ void __launch_bounds__(TAB_THREADS)
+k_quantize_posit_tab(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int sdt, vh_format f, int lo, int hi,
+                     void* __restrict__ out) {
+  extern __shared__ uint16_t tab[];
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t step = stride * UNROLL;
+  auto load = [&](uint4* raw, int64_t v0) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t v = v0 + u * stride;
+      raw[u] = v < nvec ? ld_stream16(x + v * 8) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  int64_t v0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint4 raw[UNROLL];
+  load(raw, v0);
+  build_posit_table<PACKED>(f, lo, hi, tab);
+  const int per = TAB_SPECIAL + hi - lo + 1;
+  const float s = load_any(sp, sdt, 0);
+  const float as = fabsf(s);
+  const bool fast = as >= 0x1p-126f && as <= 0x1p126f;
+  const float r = __builtin_amdgcn_rcpf(s);
+  for (; v0 < nvec; v0 += step) {
+    uint4 nraw[UNROLL];
+    load(nraw, v0 + step);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t v = v0 + u * stride;
+      if (v >= nvec) break;
+      const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+      float q[8];
+      bool slow = !fast;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        q[j] = bf2f(j & 1 ? w[j >> 1] >> 16 : w[j >> 1] & 0xffffu) * r;
+        slow |= ((__float_as_uint(q[j]) - 0x7FFCu) & 0xFFFFu) <= 8u;
+      }
+      uint32_t qb[4];
+      if (!slow) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qb[j] = f2bf2_hw(q[2 * j], q[2 * j + 1]);
+      } else {  // near a bf16 midpoint: correctly rounded division
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qb[j] = f2bf(bf2f(w[j] & 0xffffu) / s) | (f2bf(bf2f(w[j] >> 16) / s) << 16);
+      }
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t c0 = posit_lookup(qb[j] & 0xffffu, lo, hi, per, tab);
+        const uint32_t c1 = posit_lookup(qb[j] >> 16, lo, hi, per, tab);
+        o[j] = PACKED ? (c0 | (c1 << 8)) : (c0 | (c1 << 16));
+      }
+      if constexpr (PACKED) st_stream8((uint8_t*)out + v * 8, make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16)));
+      else st_stream16((uint16_t*)out + v * 8, make_uint4(o[0], o[1], o[2], o[3]));
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) raw[u] = nraw[u];
+  }
+}
+
+// Host: the table's magnitude range for a posit map, or false when it is
+// wider than TAB_MAX_SPAN.  Below 2**(floor(-(n-1) 2**es + 2**(es-1)) - 1)
+// every magnitude flushes to zero; above 2**((n-2) 2**es + 1) every finite
+// one saturates at maxpos.
+bool posit_table_range(const vh_format& f, int* lo, int* hi, size_t* lds_bytes) {
+  const int n = f.p0, es = f.p1;
+  if (f.kind != VH_FMT_POSIT || n < 2 || es < 0 || es > 4) return false;
+  const double e_lo = std::floor(-(n - 1) * std::ldexp(1.0, es) + std::ldexp(1.0, es - 1)) - 1.0;
+  const double e_hi = (n - 2) * std::ldexp(1.0, es) + 1.0;
+  if (e_lo < -126 || e_hi > 127) return false;
+  *lo = (int)(e_lo + 127) << 7;
+  *hi = (int)(e_hi + 127) << 7;
+  if (*hi - *lo + 1 > TAB_MAX_SPAN) return false;
+  *lds_bytes = (size_t)2 * (TAB_SPECIAL + *hi - *lo + 1) * sizeof(uint16_t);
+  return true;
+}
+
+// dequantize of packed codes to bfloat16 (optionally times a scalar scale,
+// rounded to bf16 as the reference's eager product): a 256-entry table of
+// the reference-form values, built per workgroup; 16 codes per thread.
+template <int KIN>
+__global__ void __launch_bounds__(256)
+k_dequantize_tab(const uint8_t* __restrict__ x, int64_t n16, const void* sp, int sdt, vh_format fin,
+                 uint16_t* __restrict__ out) {
+  __shared__ uint16_t lds_in[2 * VH_MAX_STEPS];
+  __shared__ uint32_t tab[256];
+  if constexpr (KIN == K_STEPS) stage_steps(fin, lds_in);
+  const bool has_s = sp != nullptr;
+  const float s = has_s ? load_any(sp, sdt, 0) : 1.0f;
+  for (int c = threadIdx.x; c < 256; c += blockDim.x) {
+    float v = fmt_decode_k<KIN>((uint32_t)c, fin, lds_in);
+    if (has_s) v = rbf(v * s);
+    tab[c] = f2bf(v);
+  }
+  __syncthreads();
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const uint4 c = ld_stream16(x + i * 16);
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[2 * j] = tab[w[j] & 0xffu] | (tab[(w[j] >> 8) & 0xffu] << 16);
+      o[2 * j + 1] = tab[(w[j] >> 16) & 0xffu] | (tab[w[j] >> 24] << 16);
+    }
+    st_stream16(out + i * 16, make_uint4(o[0], o[1], o[2], o[3]));
+    st_stream16(out + i * 16 + 8, make_uint4(o[4], o[5], o[6], o[7]));
+  }
+}
+
 template <int KIND, bool PACKED>
 __global__ void __launch_bounds__(256)
 k_quantize_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int sdt, vh_format f,
@@ -440,6 +590,12 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
     const int64_t nvec = n / 8;
     int64_t blocks = (nvec + 256 * UNROLL - 1) / (256 * UNROLL);
     if (blocks > 8192) blocks = 8192;
+    int lo = 0, hi = 0;
+    size_t tab_bytes = 0;
+    // the posit table costs a few thousand closed-form evaluations per
+    // workgroup: one 1024-thread workgroup per CU, each over a long range
+    int64_t tab_blocks = (nvec + TAB_THREADS * UNROLL - 1) / (TAB_THREADS * UNROLL);
+    if (tab_blocks > 256) tab_blocks = 256;
     return dispatch_kind(kernel_kind(fmt), [&](auto kind) {
       constexpr int K = decltype(kind)::value;
       if (out_dtype == VH_U8) {
@@ -448,10 +604,16 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
         } else if constexpr (K == K_E4M3) {
           hipLaunchKernelGGL(k_quantize_e4m3_pt, dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)x, nvec,
                              sp.ptr, sp.dtype, (uint8_t*)out);
+        } else if (K == K_POSIT && posit_table_range(f, &lo, &hi, &tab_bytes)) {
+          hipLaunchKernelGGL(k_quantize_posit_tab<true>, dim3((unsigned)tab_blocks), dim3(TAB_THREADS), tab_bytes, st,
+                             (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, lo, hi, out);
         } else {
           hipLaunchKernelGGL((k_quantize_pt<K, true>), dim3((unsigned)blocks), dim3(256), 0, st,
                              (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, out);
         }
+      } else if (K == K_POSIT && posit_table_range(f, &lo, &hi, &tab_bytes)) {
+        hipLaunchKernelGGL(k_quantize_posit_tab<false>, dim3((unsigned)tab_blocks), dim3(TAB_THREADS), tab_bytes, st,
+                           (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, lo, hi, out);
       } else {
         hipLaunchKernelGGL((k_quantize_pt<K, false>), dim3((unsigned)blocks), dim3(256), 0, st,
                            (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, out);
@@ -533,10 +695,27 @@ extern "C" int vh_dequantize(const void* x, int32_t x_dtype, const int64_t* shap
   memset(&fo, 0, sizeof(fo));
   if (fmt_in) fi = *fmt_in;
   if (fmt_out) fo = *fmt_out;
+  hipStream_t st = vh::as_stream(stream);
+  if (x_dtype == VH_U8 && out_dtype == VH_BF16 && compute_dtype == VH_BF16 && !fmt_out && !zp.ptr &&
+      (!sp.ptr || sp.scalar) && n % 16 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 16) == 0) {
+    // packed codes -> bf16: a 256-entry table per workgroup
+    const int64_t n16 = n / 16;
+    int64_t blocks = (n16 + 1023) / 1024;
+    if (blocks > 4096) blocks = 4096;
+    return dispatch_kind(kernel_kind(fmt_in), [&](auto kind) {
+      constexpr int K = decltype(kind)::value;
+      if constexpr (K == K_NONE || K == K_IDENTITY || K == K_LUT) {
+        return (int)VH_EINVAL;  // unreachable: checked by packable()
+      } else {
+        hipLaunchKernelGGL(k_dequantize_tab<K>, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t*)x, n16,
+                           sp.ptr, sp.dtype, fi, (uint16_t*)out);
+        return vh::check_launch("vh_dequantize");
+      }
+    });
+  }
   int64_t threads = (n + VEC - 1) / VEC;
   int64_t blocks = (threads + 255) / 256;
   VH_REQUIRE(blocks < (1ll << 31), "vh_dequantize: tensor too large");
-  hipStream_t st = vh::as_stream(stream);
   return dispatch_kind(kernel_kind(fmt_in), [&](auto kind) {
     constexpr int K = decltype(kind)::value;
     hipLaunchKernelGGL(k_dequantize<K>, dim3((unsigned)blocks), dim3(256), 0, st, x, x_dtype, n, s, sp, zp,
