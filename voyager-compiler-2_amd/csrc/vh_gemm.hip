@@ -623,7 +623,7 @@ __device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t lds, int voff)
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 
-template <int BM, int BN, int NS, int KS, int WM, int WN>
+template <int BM, int BN, int NS, int KS, int WM, int WN, int OP>
 __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
     __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) k_gemm_f8dl(GemmArgs g) {
   constexpr int P = KS / 64;                 // MFMA steps per stage
@@ -636,6 +636,8 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   constexpr int L = LA + LB;
   static_assert((KS == 64 || KS == 128) && BM % 64 == 0 && BN % 64 == 0 && NS >= 2 && (NS * P) % 2 == 0,
                 "bad fp8 tile");
+  static_assert(OP == OP_FP8 || OP == OP_BF16, "fp8 or bf16 operands");
+  constexpr bool BF = OP == OP_BF16;  // a 64-byte step is 32 bf16: two 32x32x16 MFMAs
   static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0 && TM >= 2 && TM % 2 == 0 && TN >= 1,
                 "DMA blocks must divide among the waves");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -654,7 +656,7 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   const int64_t rows_b = (g.N - n0) < BN ? (g.N - n0) : BN;
   const i32x4 ra = raw_desc(g.A + m0 * g.lda, rows_a * g.lda);
   const i32x4 rb = raw_desc(g.B + n0 * g.ldb, rows_b * g.ldb);
-  const int K = (int)g.K;
+  const int K = (int)g.K * (BF ? 2 : 1);  // bytes of a row
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
 
   // DMA: block q of RPI rows (A blocks, then B blocks) is fetched by wave
@@ -705,20 +707,29 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  constexpr int Q = BF ? 2 * TM * TN : TM * TN;  // MFMAs per step
+  // B as the row operand: accumulators come out transposed (store_tile_lds_t).
+  // bf16: MFMA q < TM TN takes the first 16 bytes of its fragments, the
+  // others the second; both halves of a pair cover distinct K of the step.
   auto mfma = [&](const i32x8* fa, const i32x8* fb, int q) {
-    const int i = q / TN, j = q % TN;
-    // B as the row operand: accumulators come out transposed (store_tile_lds_t)
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+    if constexpr (BF) {
+      const int p = q % (TM * TN), i = p / TN, j = p % TN;
+      const i32x4 a = q < TM * TN ? fa[i].lo : fa[i].hi, b = q < TM * TN ? fb[j].lo : fb[j].hi;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b), __builtin_bit_cast(bf16x8, a),
+                                                         acc[i][j], 0, 0, 0);
+    } else {
+      const int i = q / TN, j = q % TN;
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+    }
   };
 
-  constexpr int Q = TM * TN;           // MFMAs per step
-  constexpr int H1 = TM / 2 * TN;      // MFMAs of the last step before the barrier
+  constexpr int H1 = BF ? TM * TN : TM / 2 * TN;  // MFMAs of the last step before the barrier
   constexpr int NR = 2 * (TM + TN);    // fragment reads per step
   constexpr int PRE = (P - 1) * Q + H1;  // MFMAs of a stage before its barrier
 
   // The stage count is padded to a multiple of NS (padded stages are zero)
   // so the loop body has no exits between stages.
-  const int64_t nk = ((g.K + KS - 1) / KS + NS - 1) / NS * NS;
+  const int64_t nk = (((int64_t)K + KS - 1) / KS + NS - 1) / NS * NS;
   // prologue: stages 0 .. NS-2 in flight, stage 0's first fragments read
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
@@ -797,7 +808,7 @@ int group_rows(int64_t M, int64_t N, int BM, int BN) {
   return best;
 }
 
-template <int BM, int BN, int NS, int KS, int WM = 2, int WN = 2>
+template <int BM, int BN, int NS, int KS, int WM = 2, int WN = 2, int OP = OP_FP8>
 int launch_f8dl(GemmArgs g, int64_t batch, hipStream_t stream) {
   g.group_m = group_rows(g.M, g.N, BM, BN);
   constexpr size_t stages = (size_t)NS * (BM + BN) * KS;
@@ -807,14 +818,15 @@ int launch_f8dl(GemmArgs g, int64_t batch, hipStream_t stream) {
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)k_gemm_f8dl<BM, BN, NS, KS, WM, WN>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void*)k_gemm_f8dl<BM, BN, NS, KS, WM, WN, OP>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)smem) != hipSuccess) {
       vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
       return VH_ELAUNCH;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_f8dl<BM, BN, NS, KS, WM, WN>), dim3((unsigned)tiles, (unsigned)batch), dim3(WM * WN * 64),
+  hipLaunchKernelGGL((k_gemm_f8dl<BM, BN, NS, KS, WM, WN, OP>), dim3((unsigned)tiles, (unsigned)batch), dim3(WM * WN * 64),
                      smem, stream, g);
   return vh::check_launch("vh_gemm");
 }
@@ -961,6 +973,20 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
     }
   }
   if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16 && lds_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N) &&
+      (d->tile_hint == 0 || d->tile_hint >= 20)) {
+    int bcfg = d->tile_hint;
+    if (bcfg == 0) {
+      const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
+      bcfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : 33;
+    }
+    switch (bcfg) {
+      case 41: return launch_f8dl<256, 256, 2, 128, 4, 2, OP_BF16>(g, batch, st);
+      case 31: return launch_f8dl<256, 128, 3, 128, 2, 2, OP_BF16>(g, batch, st);
+      case 33: return launch_f8dl<128, 128, 4, 128, 2, 2, OP_BF16>(g, batch, st);
+      default: break;
+    }
+  }
   if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16) return pick(Fmts<OP_BF16, OP_BF16>{});
   if (d->a_fmt == OP_MXI8 && d->b_fmt == OP_MXI8) return pick(Fmts<OP_MXI8, OP_MXI8>{});
   if (d->a_fmt == OP_P8 && d->b_fmt == OP_P8) return pick(Fmts<OP_P8, OP_P8>{});
