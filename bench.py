@@ -296,7 +296,9 @@ def bench_config4(args):
             "quantize_ref_form": {"us": round(r_ms * 1e3, 2), "GB/s": round(n * 4 / (r_ms * 1e-3) / 1e9, 1)},
             "dequantize_packed": {"us": round(d_ms * 1e3, 2), "GB/s": round(n * 3 / (d_ms * 1e-3) / 1e9, 1)},
             "gemm": {"us": round(g_ms * 1e3, 2), "TFLOP/s": round(flops / (g_ms * 1e-3) / 1e12, 1),
-                     "peak_TFLOP/s": 2500.0, "note": "posit bytes decoded via LDS table to bf16; bf16 MFMA"},
+                     "peak_TFLOP/s": 2500.0,
+                     "note": "both operands' posit bytes decoded to bf16 through a 256-entry table each call, then the "
+                             "bf16 direct-to-LDS GEMM (decode included in the time)"},
             "config": {"workload": "cfg4: posit8_1, 64M-element tensor; GEMM M=2048 K=N=4096"}}
 
 

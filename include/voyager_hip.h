@@ -109,6 +109,13 @@ int vh_dequantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t 
                   const vh_format* fmt_in, const vh_format* fmt_out, void* out,
                   int32_t out_dtype, vh_stream_t stream);
 
+/* Packed one-byte codes -> bfloat16 through a 256-entry bf16 table in device
+ * memory: out[i] = lut[codes[i]], i < n.  The decode half of the posit8 GEMM
+ * (`gemm.linear_posit8`: the lowered graph's direct cast of posit codes to
+ * bf16, quantization/quantize_pt2e.py:557-561, before the bf16 GEMM).
+ * codes and out 16-byte aligned. */
+int vh_decode_bytes(const void* codes, int64_t n, const void* lut, void* out, vh_stream_t stream);
+
 /* quantize_mx: block scales over `block` elements along the middle axis of a
  * contiguous [outer, L, inner] tensor, then codes.  Replaces
  * quantized_ops.quantize_mx (ops/quantized.py:1070-1115) and

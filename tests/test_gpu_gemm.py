@@ -151,6 +151,23 @@ def test_linear_posit8():
     lut = gemm.posit8_lut(tab.to(d))
     got = gemm.linear_posit8(cx, cw, lut)
     assert max_rel_err(got, exp) < TOL
+    # the in-staging decode (taken with a tile hint) agrees as well
+    assert max_rel_err(gemm.linear_posit8(cx, cw, lut, tile_hint=10), exp) < TOL
+
+
+@pytest.mark.parametrize("n", [16 * 1024, 1000, 15, 16 * 4096 + 7])
+def test_decode_bytes(n):
+    """vh_decode_bytes: every byte through the posit8 table, whole 16-byte
+    rows and a ragged tail, against the oracle's values of the codes."""
+    from voyager_amd import gemm, packed
+
+    tab = T.quantization_map("posit8_1")
+    g = torch.Generator().manual_seed(33)
+    x = (torch.randn(n, generator=g) * 3).bfloat16()
+    one = torch.tensor(1.0, dtype=torch.bfloat16)
+    codes = packed.quantize_packed(x.cuda(), one.cuda(), tab.cuda())
+    got = gemm.decode_bytes(codes, gemm.posit8_lut(tab.cuda())).cpu()
+    assert_same_bits(got, O.quantize(x, one, qmap=tab), f"n={n}")
 
 
 @pytest.mark.parametrize("M", [1, 16])

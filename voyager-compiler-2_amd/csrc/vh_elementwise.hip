@@ -407,6 +407,24 @@ bool posit_table_range(const vh_format& f, int* lo, int* hi, size_t* lds_bytes) 
   return true;
 }
 
+// 16 codes per thread per step: out[i] = tab[x[i]] (low 16 bits), i < 16 n16.
+__device__ __forceinline__ void gather16(const uint8_t* __restrict__ x, int64_t n16, const uint32_t* tab,
+                                         uint16_t* __restrict__ out) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const uint4 c = ld_stream16(x + i * 16);
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[2 * j] = tab[w[j] & 0xffu] | (tab[(w[j] >> 8) & 0xffu] << 16);
+      o[2 * j + 1] = tab[(w[j] >> 16) & 0xffu] | (tab[w[j] >> 24] << 16);
+    }
+    st_stream16(out + i * 16, make_uint4(o[0], o[1], o[2], o[3]));
+    st_stream16(out + i * 16 + 8, make_uint4(o[4], o[5], o[6], o[7]));
+  }
+}
+
 // dequantize of packed codes to bfloat16 (optionally times a scalar scale,
 // rounded to bf16 as the reference's eager product): a 256-entry table of
 // the reference-form values, built per workgroup; 16 codes per thread.
@@ -425,18 +443,21 @@ k_dequantize_tab(const uint8_t* __restrict__ x, int64_t n16, const void* sp, int
     tab[c] = f2bf(v);
   }
   __syncthreads();
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
-    const uint4 c = ld_stream16(x + i * 16);
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    uint32_t o[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[2 * j] = tab[w[j] & 0xffu] | (tab[(w[j] >> 8) & 0xffu] << 16);
-      o[2 * j + 1] = tab[(w[j] >> 16) & 0xffu] | (tab[w[j] >> 24] << 16);
-    }
-    st_stream16(out + i * 16, make_uint4(o[0], o[1], o[2], o[3]));
-    st_stream16(out + i * 16 + 8, make_uint4(o[4], o[5], o[6], o[7]));
+  gather16(x, n16, tab, out);
+}
+
+// Packed bytes -> bf16 through a 256-entry table held in device memory.
+__global__ void __launch_bounds__(256)
+k_decode_bytes(const uint8_t* __restrict__ x, int64_t n, const uint16_t* __restrict__ lut, uint16_t* __restrict__ out) {
+  __shared__ uint32_t tab[256];
+  for (int c = threadIdx.x; c < 256; c += blockDim.x) tab[c] = lut[c];
+  __syncthreads();
+  const int64_t n16 = n / 16;
+  gather16(x, n16, tab, out);
+  // the last n % 16 bytes, one per thread of the first workgroup
+  if (blockIdx.x == 0 && threadIdx.x < (int)(n - n16 * 16)) {
+    const int64_t i = n16 * 16 + threadIdx.x;
+    out[i] = (uint16_t)tab[x[i]];
   }
 }
 
@@ -722,4 +743,17 @@ extern "C" int vh_dequantize(const void* x, int32_t x_dtype, const int64_t* shap
                        compute_dtype, fi, fmt_out ? 1 : 0, fo, out, out_dtype);
     return vh::check_launch("vh_dequantize");
   });
+}
+
+extern "C" int vh_decode_bytes(const void* codes, int64_t n, const void* lut, void* out, vh_stream_t stream) {
+  VH_REQUIRE(codes && lut && out, "vh_decode_bytes: null pointer");
+  VH_REQUIRE(n >= 0, "vh_decode_bytes: negative size");
+  VH_REQUIRE(((uintptr_t)codes % 16) == 0 && ((uintptr_t)out % 16) == 0, "vh_decode_bytes: pointers must be 16-byte aligned");
+  if (n == 0) return VH_OK;
+  int64_t blocks = (n / 16 + 1023) / 1024;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_decode_bytes, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), (const uint8_t*)codes, n,
+                     (const uint16_t*)lut, (uint16_t*)out);
+  return vh::check_launch("vh_decode_bytes");
 }

@@ -104,6 +104,7 @@ _SIGNATURES = {
          _P, _P, _P, _I32, _P],
         _I32,
     ),
+    "vh_decode_bytes": ([_P, _I64, _P, _P, _P], _I32),
     # vh_gemm takes a vh_gemm_desc*; voyager_amd.gemm.GemmDesc mirrors it.
     "vh_gemm": ([_P, _P], _I32),
     "vh_pack_nf4": ([_P, _I64, _I64, _P, _P], _I32),

@@ -16,7 +16,7 @@ from typing import NamedTuple, Optional
 import torch
 
 from . import _lib, formats
-from ._lib import VH_BF16, VH_F32, dtype_code, load, stream_of
+from ._lib import VH_BF16, VH_F32, dtype_code, load, ptr, stream_of
 from .ops import LINEAR_LAYOUT, MATMUL_LAYOUT, _require_gpu, decode_table, lib
 
 OP_BF16, OP_FP8, OP_MXI8, OP_P8 = 0, 1, 2, 3
@@ -295,12 +295,27 @@ def posit8_lut(qmap: torch.Tensor) -> torch.Tensor:
     return _elementwise("dequantize", codes, None, None, None, torch.bfloat16, c.fmt, None, torch.bfloat16)
 
 
+def decode_bytes(codes: torch.Tensor, lut: torch.Tensor) -> torch.Tensor:
+    """bf16 ``lut[codes]`` for one-byte codes (``vh_decode_bytes``)."""
+    c = codes.contiguous()
+    if c.data_ptr() % 16:
+        c = c.clone()
+    out = torch.empty(c.shape, dtype=torch.bfloat16, device=c.device)
+    st = load().vh_decode_bytes(ptr(c), c.numel(), ptr(lut.contiguous()), ptr(out), ctypes.c_void_p(stream_of(c)))
+    _lib.check(st, "vh_decode_bytes")
+    return out
+
+
 def linear_posit8(x_codes, w_codes, lut: torch.Tensor, out_dtype=torch.bfloat16, tile_hint: int = 0):
     """Posit8 ``linear`` on packed codes (``quantize_pt2e.py:557-561``: a
-    direct cast, the GEMM reads posit values as bf16): each code is decoded
-    through ``lut`` while staging, then bf16 MFMA, one rounding at the end."""
+    direct cast, the GEMM reads posit values as bf16), one rounding at the
+    end.  Both operands are decoded through ``lut`` to bf16 (exact) and run
+    through the bf16 GEMM; with a ``tile_hint`` the codes are decoded while
+    the GEMM stages them instead."""
     M, K = x_codes.shape
     N = w_codes.shape[0]
+    if tile_hint == 0 and K % 8 == 0:
+        return gemm_bf16(decode_bytes(x_codes, lut), decode_bytes(w_codes, lut), out_dtype)
     out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
     d = GemmDesc()
     d.A, d.B, d.C = x_codes.data_ptr(), w_codes.data_ptr(), out.data_ptr()
