@@ -9,7 +9,8 @@
 // thread holds 8 consecutive elements (one 16-byte bf16 load); the block's
 // reduction is a butterfly over block/8 lanes of the wavefront (no LDS), so
 // every element is read from HBM exactly once and codes + scales are written
-// once.  Column path (everything else): one thread per (outer, block, inner)
+// once.  Up to 2**16 elements with blocks of at most 64, one element per
+// lane instead (the block's butterfly spans block lanes).  Column path (everything else): one thread per (outer, block, inner)
 // column, consecutive threads on consecutive `inner` for coalescing.
 #include <hip/hip_runtime.h>
 
@@ -191,7 +192,7 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
   const int64_t base = row * L + v * VEC;
   float xv[VEC];
   if (live) {
-    if (P.cdt == VH_BF16) {
+    if (VEC == 8 && P.cdt == VH_BF16) {
       uint4 raw = *(const uint4*)((const uint16_t*)x + base);
       uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -242,11 +243,16 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
 #pragma unroll
   for (int j = 0; j < VEC; ++j) element_code<KIND>(xv[j], bs, P, lds, clut, &cv[j], &cc[j]);
   if (P.codes_dtype == VH_U8) {
-    uint2 pk;
-    pk.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
-    pk.y = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
-    *(uint2*)((uint8_t*)codes_out + base) = pk;
-  } else if (P.cdt == VH_BF16) {
+    if constexpr (VEC == 8) {
+      uint2 pk;
+      pk.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
+      pk.y = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
+      *(uint2*)((uint8_t*)codes_out + base) = pk;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) ((uint8_t*)codes_out)[base + j] = (uint8_t)cc[j];
+    }
+  } else if (VEC == 8 && P.cdt == VH_BF16) {
     uint4 pk;
     pk.x = f2bf(cv[0]) | (f2bf(cv[1]) << 16);
     pk.y = f2bf(cv[2]) | (f2bf(cv[3]) << 16);
@@ -332,7 +338,25 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
   const int64_t nblk = (L + block - 1) / block;
   const bool rows_ok = inner == 1 && L % 8 == 0 && block % 8 == 0 && block <= 512 &&
                        ((block / 8) & (block / 8 - 1)) == 0;
-  if (rows_ok) {
+  // Small tensors (decode-size activations): one element per lane, so each
+  // lane's dependent chain (scale map, element map) is an eighth as long and
+  // there are eight times as many waves.
+  const bool lanes_ok = inner == 1 && block <= 64 && (block & (block - 1)) == 0 && L % block == 0 &&
+                        outer * L <= (1 << 16);
+  if (lanes_ok) {
+    const int g = (int)block;
+    const int64_t threads = outer * nblk * g;
+    const int64_t blocks = (threads + 255) / 256;
+    dispatch_kind(P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE, [&](auto kind) {
+      constexpr int K = decltype(kind)::value;
+      return dispatch_scale(P, [&](auto skind) {
+        constexpr int S = decltype(skind)::value;
+        hipLaunchKernelGGL((k_rows<1, K, S>), dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P,
+                           scale_out, zp_out, codes_out);
+        return 0;
+      });
+    });
+  } else if (rows_ok) {
     const int g = (int)(block / 8);
     const int64_t threads = outer * nblk * g;
     const int64_t blocks = (threads + 255) / 256;

@@ -8,9 +8,11 @@
 // the reference only by its bf16 rounding of each decoded operand (at most
 // 2**-9 relative per element), well inside the 1e-2 GEMM tolerance.
 //
-// Layout: one workgroup (16 waves) per 16 output columns; the waves split K
-// into 16 contiguous ranges, keep 8 blocks of loads in flight each, and
-// reduce through LDS.  Activation scales are staged in LDS block-major.  Weight nibbles are baked
+// Layout: one workgroup per 16 output columns; its WAVES waves split K into
+// contiguous ranges, keep 4 or 8 blocks of loads in flight each, and reduce
+// through LDS.  WAVES = 4 when there are at least 512 column tiles (long
+// per-wave streams, 8+ waves per CU), 16 otherwise (fill the CUs by
+// splitting K further).  Activation scales are staged in LDS block-major.  Weight nibbles are baked
 // in MFMA lane order so every lane's 8-byte load is one coalesced 512-byte
 // wave access per block; nibbles become int8 levels with two v_perm_b32 table
 // lookups per 4 values.
@@ -25,8 +27,6 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int WAVES = 16;
-constexpr int UNROLL = 8;
 constexpr int MAX_BLOCKS = 256;  // K <= 16384 (activation scales staged in LDS)
 
 // Bake: one thread per (tile, block, lane) -> 8 bytes.
@@ -62,6 +62,7 @@ __device__ __forceinline__ uint32_t lut16(uint32_t idx, uint32_t t0, uint32_t t1
   return (hi & mask) | (lo & ~mask);
 }
 
+template <int WAVES>
 __global__ void __launch_bounds__(WAVES * 64)
 k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, const uint8_t* __restrict__ wp,
            const uint8_t* __restrict__ ws, vh_format sfmt, uint4 lv, int64_t N, int64_t K, vh_epilogue epi,
@@ -69,15 +70,10 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
   __shared__ float s_wscale[256];
   __shared__ __attribute__((aligned(16))) float s_xs[MAX_BLOCKS][16];  // activation scales, block-major
   __shared__ float s_red[WAVES][4][64];
+  // blocks per round: 16 waves fit 128 VGPRs (and see short K ranges)
+  constexpr int UNROLL = WAVES == 16 ? 4 : 8;
   const int tid = threadIdx.x;
   const int64_t nb = K / 64;
-  if (tid < 256) s_wscale[tid] = fmt_decode(tid, sfmt, nullptr);
-  for (int i = tid; i < nb * 16; i += WAVES * 64) {
-    const int b = i / 16, m = i % 16;
-    s_xs[b][m] = m < M ? xs[(int64_t)m * nb + b] : 0.0f;
-  }
-  __syncthreads();
-
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t tile = blockIdx.x;
   const int64_t b0 = wave * nb / WAVES, b1 = (wave + 1) * nb / WAVES;
@@ -91,20 +87,37 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
   const uint8_t* wsrow = ws + n * nb;
   const int8_t* xrow = xl + (int64_t)(a_live ? ma : 0) * K + kl;
 
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int64_t b = b0; b < b1; b += UNROLL) {
-    uint2 w[UNROLL];
-    uint4 x[UNROLL];
-    uint32_t sb[UNROLL];
-    // every load of the round is issued before any is used
+  // One round: UNROLL blocks' weights, activations and weight-scale codes.
+  // Every round is loaded one round ahead; the first before the tables are
+  // staged, so the memory latency overlaps the set-up.
+  uint2 w[UNROLL];
+  uint4 x[UNROLL];
+  uint32_t sb[UNROLL];
+  auto load = [&](int64_t b, uint2* wv, uint4* xv, uint32_t* sv) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int64_t bb = b + u;
       const bool ok = bb < b1;
-      w[u] = ok ? *(const uint2*)(wtile + bb * 512) : make_uint2(0, 0);
-      x[u] = (ok && a_live) ? *(const uint4*)(xrow + bb * 64) : make_uint4(0, 0, 0, 0);
-      sb[u] = ok ? wsrow[bb] : 0u;
+      wv[u] = ok ? *(const uint2*)(wtile + bb * 512) : make_uint2(0, 0);
+      xv[u] = (ok && a_live) ? *(const uint4*)(xrow + bb * 64) : make_uint4(0, 0, 0, 0);
+      sv[u] = ok ? wsrow[bb] : 0u;
     }
+  };
+  load(b0, w, x, sb);
+
+  for (int i = tid; i < 256; i += WAVES * 64) s_wscale[i] = fmt_decode(i, sfmt, nullptr);
+  for (int i = tid; i < nb * 16; i += WAVES * 64) {
+    const int bq = i / 16, m = i % 16;
+    s_xs[bq][m] = m < M ? xs[(int64_t)m * nb + bq] : 0.0f;
+  }
+  __syncthreads();
+
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t b = b0; b < b1; b += UNROLL) {
+    uint2 nw[UNROLL];
+    uint4 nx[UNROLL];
+    uint32_t nsb[UNROLL];
+    if (b + UNROLL < b1) load(b + UNROLL, nw, nx, nsb);
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int64_t bb = b + u;
@@ -123,6 +136,12 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
       acc[1] = fmaf((float)d[1], sx.y * swv, acc[1]);
       acc[2] = fmaf((float)d[2], sx.z * swv, acc[2]);
       acc[3] = fmaf((float)d[3], sx.w * swv, acc[3]);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      w[u] = nw[u];
+      x[u] = nx[u];
+      sb[u] = nsb[u];
     }
   }
 #pragma unroll
@@ -175,7 +194,11 @@ extern "C" int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t
   uint32_t t[4];
   memcpy(t, levels16, 16);
   const uint4 lv = make_uint4(t[0], t[1], t[2], t[3]);
-  hipLaunchKernelGGL(k_gemv_nf4, dim3((unsigned)(N / 16)), dim3(WAVES * 64), 0, vh::as_stream(stream), x_levels,
-                     x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
+  if (N / 16 >= 512)
+    hipLaunchKernelGGL(k_gemv_nf4<4>, dim3((unsigned)(N / 16)), dim3(4 * 64), 0, vh::as_stream(stream), x_levels,
+                       x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
+  else
+    hipLaunchKernelGGL(k_gemv_nf4<16>, dim3((unsigned)(N / 16)), dim3(16 * 64), 0, vh::as_stream(stream), x_levels,
+                       x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
   return vh::check_launch("vh_gemv_nf4");
 }
