@@ -951,9 +951,11 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       // M = 2048 (K in {4096, 14336}, N in {1024, 4096, 14336}): the
       // largest tile that still gives every CU a block wins, since each
       // CU's operand stream from L2 is the limit; 256 x 256 only pays when
-      // the grid covers the GPU well over once.
+      // the grid covers the GPU well over once; a grid too small even for
+      // 128 x 128 takes 64 x 128 (1 x 4 waves).
       const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
-      cfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : 33;
+      const int64_t t128 = tiles(128, 128) * batch;
+      cfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : t128 >= 224 ? 33 : 37;
     }
     switch (cfg) {
       case 20: return launch_f8dl<256, 256, 4, 64>(g, batch, st);
@@ -969,6 +971,9 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       case 41: return launch_f8dl<256, 256, 2, 128, 4, 2>(g, batch, st);
       case 42: return launch_f8dl<256, 128, 3, 128, 2, 4>(g, batch, st);
       case 43: return launch_f8dl<256, 128, 3, 128, 4, 2>(g, batch, st);
+      case 35: return launch_f8dl<128, 64, 4, 128, 2, 2>(g, batch, st);
+      case 36: return launch_f8dl<128, 64, 6, 128, 2, 2>(g, batch, st);
+      case 37: return launch_f8dl<64, 128, 4, 128, 1, 4>(g, batch, st);
       default: break;
     }
   }
