@@ -12,10 +12,11 @@
 // contiguous ranges, keep 4 or 8 blocks of loads in flight each, and reduce
 // through LDS.  WAVES = 4 when there are at least 512 column tiles (long
 // per-wave streams, 8+ waves per CU), 16 otherwise (fill the CUs by
-// splitting K further).  Activation scales are staged in LDS block-major.  Weight nibbles are baked
-// in MFMA lane order so every lane's 8-byte load is one coalesced 512-byte
-// wave access per block; nibbles become int8 levels with two v_perm_b32 table
-// lookups per 4 values.
+// splitting K further).  The tile's activation and weight scales are staged
+// in LDS once (decoded to fp32, block-major), so the block loop issues only
+// the weight and activation loads.  Weight nibbles are baked in MFMA lane
+// order so every lane's 8-byte load is one coalesced 512-byte wave access per
+// block; nibbles become int8 levels with three v_perm_b32 per 4 values.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -54,12 +55,15 @@ __global__ void __launch_bounds__(256) k_pack_nf4(const uint8_t* __restrict__ co
 
 // Four byte indices (0..15) -> four int8 levels from a 16-entry table held in
 // four dwords (t0 = levels 0..3, ... t3 = levels 12..15).
+// The third v_perm picks, per byte i, byte i of the low-half lookup (selector
+// i) or of the high-half one (i + 4) by bit 3 of the index: six full-rate
+// ops, no per-byte multiply.
 __device__ __forceinline__ uint32_t lut16(uint32_t idx, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
   const uint32_t sel = idx & 0x07070707u;
   const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
   const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-  const uint32_t mask = ((idx >> 3) & 0x01010101u) * 0xffu;
-  return (hi & mask) | (lo & ~mask);
+  const uint32_t pick = ((idx >> 1) & 0x04040404u) | 0x03020100u;
+  return __builtin_amdgcn_perm(hi, lo, pick);
 }
 
 template <int WAVES>
@@ -67,45 +71,50 @@ __global__ void __launch_bounds__(WAVES * 64)
 k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, const uint8_t* __restrict__ wp,
            const uint8_t* __restrict__ ws, vh_format sfmt, uint4 lv, int64_t N, int64_t K, vh_epilogue epi,
            void* __restrict__ y) {
-  __shared__ float s_wscale[256];
-  __shared__ __attribute__((aligned(16))) float s_xs[MAX_BLOCKS][16];  // activation scales, block-major
+  // activation and weight scales of this tile, block-major: a lane reads
+  // its row's / column's scale of block b at [b][.], no bank conflicts
+  __shared__ __attribute__((aligned(16))) float s_xs[MAX_BLOCKS][16];
+  __shared__ float s_ws[MAX_BLOCKS][16];
   __shared__ float s_red[WAVES][4][64];
   // blocks per round: 16 waves fit 128 VGPRs (and see short K ranges)
   constexpr int UNROLL = WAVES == 16 ? 4 : 8;
   const int tid = threadIdx.x;
-  const int64_t nb = K / 64;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int nb = (int)(K / 64);
+  // wave-uniform block range, kept in scalar registers
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t tile = blockIdx.x;
-  const int64_t b0 = wave * nb / WAVES, b1 = (wave + 1) * nb / WAVES;
+  const int b0 = wave * nb / WAVES, b1 = (wave + 1) * nb / WAVES;
   const int64_t n = tile * 16 + (lane & 15);
   const int ma = lane & 15;         // activation row this lane feeds to the MFMA
   const int mrow = (lane >> 4) * 4; // output rows this lane accumulates
   const bool a_live = ma < M;
-  const int64_t kl = (lane >> 4) * 16;
 
-  const uint8_t* wtile = wp + (tile * nb) * 512 + lane * 8;
-  const uint8_t* wsrow = ws + n * nb;
-  const int8_t* xrow = xl + (int64_t)(a_live ? ma : 0) * K + kl;
-
-  // One round: UNROLL blocks' weights, activations and weight-scale codes.
-  // Every round is loaded one round ahead; the first before the tables are
-  // staged, so the memory latency overlaps the set-up.
-  uint2 w[UNROLL];
-  uint4 x[UNROLL];
-  uint32_t sb[UNROLL];
-  auto load = [&](int64_t b, uint2* wv, uint4* xv, uint32_t* sv) {
+  // Buffer loads: a lane whose row is past M, or a block past this wave's
+  // range, reads out of range and gets zeros without a memory access, so
+  // it adds nothing to the dot products.  Each wave access is then one
+  // 512-byte weight run and at most 64 bytes per live activation row.
+  constexpr uint32_t OOB = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(wp + tile * nb * 512), (short)0, nb * 512, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xl, (short)0, M * (int)K, 0x00020000);
+  const uint32_t woff = (uint32_t)lane * 8u;
+  const uint32_t xoff = a_live ? (uint32_t)(ma * K + (lane >> 4) * 16) : OOB;
+  auto load = [&](int b, vh_u32x2* wv, vh_u32x4* xv) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      const int64_t bb = b + u;
-      const bool ok = bb < b1;
-      wv[u] = ok ? *(const uint2*)(wtile + bb * 512) : make_uint2(0, 0);
-      xv[u] = (ok && a_live) ? *(const uint4*)(xrow + bb * 64) : make_uint4(0, 0, 0, 0);
-      sv[u] = ok ? wsrow[bb] : 0u;
+      const bool ok = b + u < b1;
+      wv[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, ok ? woff + (uint32_t)(b + u) * 512u : OOB, 0, 0);
+      xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + (uint32_t)(b + u) * 64u : OOB, 0, 0);
     }
   };
-  load(b0, w, x, sb);
+  // Rounds alternate between two register sets; the first is loaded before
+  // the scales are staged, so the memory latency overlaps the set-up.
+  vh_u32x2 w0[UNROLL], w1[UNROLL];
+  vh_u32x4 x0[UNROLL], x1[UNROLL];
+  if (b1 > b0) load(b0, w0, x0);
 
-  for (int i = tid; i < 256; i += WAVES * 64) s_wscale[i] = fmt_decode(i, sfmt, nullptr);
+  const uint8_t* wst = ws + tile * 16 * nb;  // the tile's 16 scale rows are contiguous
+  for (int i = tid; i < 16 * nb; i += WAVES * 64) s_ws[i % nb][i / nb] = fmt_decode(wst[i], sfmt, nullptr);
   for (int i = tid; i < nb * 16; i += WAVES * 64) {
     const int bq = i / 16, m = i % 16;
     s_xs[bq][m] = m < M ? xs[(int64_t)m * nb + bq] : 0.0f;
@@ -113,15 +122,11 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
   __syncthreads();
 
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int64_t b = b0; b < b1; b += UNROLL) {
-    uint2 nw[UNROLL];
-    uint4 nx[UNROLL];
-    uint32_t nsb[UNROLL];
-    if (b + UNROLL < b1) load(b + UNROLL, nw, nx, nsb);
+  const int blast = b1 > b0 ? b1 - 1 : b0;
+  auto round = [&](int b, const vh_u32x2* w, const vh_u32x4* x) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      const int64_t bb = b + u;
-      if (bb >= b1) break;
+      const int bb = b + u < b1 ? b + u : blast;  // past the range: zero activations, any finite scale
       i32x4 wl;
       wl[0] = (int)lut16(w[u].x & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
       wl[1] = (int)lut16(w[u].y & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
@@ -130,19 +135,20 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
       i32x4 xa = {(int)x[u].x, (int)x[u].y, (int)x[u].z, (int)x[u].w};
       i32x4 d = {0, 0, 0, 0};
       d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
-      const float swv = s_wscale[sb[u] & 0xffu];
+      const float swv = s_ws[bb][lane & 15];
       const float4 sx = *(const float4*)&s_xs[bb][mrow];
       acc[0] = fmaf((float)d[0], sx.x * swv, acc[0]);
       acc[1] = fmaf((float)d[1], sx.y * swv, acc[1]);
       acc[2] = fmaf((float)d[2], sx.z * swv, acc[2]);
       acc[3] = fmaf((float)d[3], sx.w * swv, acc[3]);
     }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      w[u] = nw[u];
-      x[u] = nx[u];
-      sb[u] = nsb[u];
-    }
+  };
+  for (int b = b0; b < b1; b += 2 * UNROLL) {
+    if (b + UNROLL < b1) load(b + UNROLL, w1, x1);
+    round(b, w0, x0);
+    if (b + UNROLL >= b1) break;
+    if (b + 2 * UNROLL < b1) load(b + 2 * UNROLL, w0, x0);
+    round(b + UNROLL, w1, x1);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) s_red[wave][r][lane] = acc[r];
