@@ -9,9 +9,10 @@
 // thread holds 8 consecutive elements (one 16-byte bf16 load); the block's
 // reduction is a butterfly over block/8 lanes of the wavefront (no LDS), so
 // every element is read from HBM exactly once and codes + scales are written
-// once.  Up to 2**16 elements with blocks of at most 64, one element per
-// lane instead (the block's butterfly spans block lanes).  Column path (everything else): one thread per (outer, block, inner)
-// column, consecutive threads on consecutive `inner` for coalescing.
+// once.  Up to 2**18 elements with blocks of at most 64, one element per
+// lane instead (the block's butterfly spans block lanes).  Column path
+// (everything else): one thread per (outer, block, inner) column,
+// consecutive threads on consecutive `inner` for coalescing.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -181,15 +182,13 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
   __shared__ uint16_t slds[2 * VH_MAX_STEPS];
   __shared__ uint8_t clut[256];
-  if constexpr (KIND == K_STEPS) stage_steps(P.fmt, lds);
-  if constexpr (SKIND == K_STEPS || SKIND == K_RUNTIME) stage_steps(P.sfmt, slds);
-  stage_code_lut(P, clut);
   const int64_t tpr = nblk * g;  // threads per row
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = t / tpr;
   const int64_t v = t % tpr;
   const bool live = row < rows && v * VEC < L;
   const int64_t base = row * L + v * VEC;
+  // the element loads go out first; the table staging runs under their latency
   float xv[VEC];
   if (live) {
     if (VEC == 8 && P.cdt == VH_BF16) {
@@ -208,6 +207,9 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
 #pragma unroll
     for (int j = 0; j < VEC; ++j) xv[j] = 0.0f;  // zero padding of a partial block
   }
+  if constexpr (KIND == K_STEPS) stage_steps(P.fmt, lds);
+  if constexpr (SKIND == K_STEPS || SKIND == K_RUNTIME) stage_steps(P.sfmt, slds);
+  stage_code_lut(P, clut);
   float hi, lo;
   if (P.mode == AFFINE) {
     hi = xv[0];
@@ -342,7 +344,7 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
   // lane's dependent chain (scale map, element map) is an eighth as long and
   // there are eight times as many waves.
   const bool lanes_ok = inner == 1 && block <= 64 && (block & (block - 1)) == 0 && L % block == 0 &&
-                        outer * L <= (1 << 16);
+                        outer * L <= (1 << 18);
   if (lanes_ok) {
     const int g = (int)block;
     const int64_t threads = outer * nblk * g;

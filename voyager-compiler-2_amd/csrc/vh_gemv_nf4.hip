@@ -107,11 +107,15 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
       xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + (uint32_t)(b + u) * 64u : OOB, 0, 0);
     }
   };
-  // Rounds alternate between two register sets; the first is loaded before
-  // the scales are staged, so the memory latency overlaps the set-up.
+  // Rounds alternate between two register sets.  With 16 waves (4-block
+  // rounds) two rounds are always in flight, the first two loaded before the
+  // scales are staged; with 4 waves the second set is loaded once the first
+  // is being consumed (two 8-block rounds in flight would not fit 128 VGPRs).
+  constexpr bool DEEP = WAVES == 16;
   vh_u32x2 w0[UNROLL], w1[UNROLL];
   vh_u32x4 x0[UNROLL], x1[UNROLL];
-  if (b1 > b0) load(b0, w0, x0);
+  if (b0 < b1) load(b0, w0, x0);
+  if (DEEP && b0 + UNROLL < b1) load(b0 + UNROLL, w1, x1);
 
   const uint8_t* wst = ws + tile * 16 * nb;  // the tile's 16 scale rows are contiguous
   for (int i = tid; i < 16 * nb; i += WAVES * 64) s_ws[i % nb][i / nb] = fmt_decode(wst[i], sfmt, nullptr);
@@ -143,12 +147,22 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
       acc[3] = fmaf((float)d[3], sx.w * swv, acc[3]);
     }
   };
-  for (int b = b0; b < b1; b += 2 * UNROLL) {
-    if (b + UNROLL < b1) load(b + UNROLL, w1, x1);
-    round(b, w0, x0);
-    if (b + UNROLL >= b1) break;
-    if (b + 2 * UNROLL < b1) load(b + 2 * UNROLL, w0, x0);
-    round(b + UNROLL, w1, x1);
+  if constexpr (DEEP) {
+    for (int b = b0; b < b1; b += 2 * UNROLL) {
+      round(b, w0, x0);
+      if (b + 2 * UNROLL < b1) load(b + 2 * UNROLL, w0, x0);
+      if (b + UNROLL >= b1) break;
+      round(b + UNROLL, w1, x1);
+      if (b + 3 * UNROLL < b1) load(b + 3 * UNROLL, w1, x1);
+    }
+  } else {
+    for (int b = b0; b < b1; b += 2 * UNROLL) {
+      if (b + UNROLL < b1) load(b + UNROLL, w1, x1);
+      round(b, w0, x0);
+      if (b + UNROLL >= b1) break;
+      if (b + 2 * UNROLL < b1) load(b + 2 * UNROLL, w0, x0);
+      round(b + UNROLL, w1, x1);
+    }
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) s_red[wave][r][lane] = acc[r];
