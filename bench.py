@@ -225,7 +225,7 @@ def bench_config1(args):
             "gemm": {"us": round(g_ms * 1e3, 2), "TFLOP/s": round(flops / (g_ms * 1e-3) / 1e12, 1),
                      "GB/s": round(gbytes / (g_ms * 1e-3) / 1e9, 1),
                      "roofline_us": round(max(flops / 2.5e15, gbytes / 8e12) * 1e6, 2),
-                     "note": "MX-int8 decoded to bf16 while staging; bf16 MFMA (2.5 PF) bound"},
+                     "note": "k_gemm_mxi8: codes decoded to bf16 once per block tile, bf16 MFMA (2.5 PF); K split 4 ways + k_split_reduce"},
             "quantize_mx": {"us": round(q_ms * 1e3, 2), "GB/s": round(qbytes / (q_ms * 1e-3) / 1e9, 1)},
             "config": {"workload": "cfg1: MXINT8 bs=16 pot, X[256,4096] . W[4096,4096]^T"}}
 

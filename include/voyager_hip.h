@@ -179,15 +179,30 @@ typedef struct vh_gemm_desc {
   const void* lut;     /* OP_P8 decode table */
   int32_t tile_hint;   /* 0: automatic; 2: 256x128/4 waves, 3: 128x128/4, 4: 128x64/4,
                           5: 256x128/8 waves, 6: 256x256/8, 7: 128x256/8, 8: 128x128/8,
-                          9: 256x128/8 (one-step prefetch), 10: 128x128/8 (one-step) */
+                          9: 256x128/8 (one-step prefetch), 10: 128x128/8 (one-step);
+                          MX-int8 pairs: 50: 128x128/4 waves, 51: 128x128/8,
+                          52: 128x64/4, 53: 256x128/8, 54: 64x128/4 */
   int64_t batch;       /* independent GEMMs (<= 1: one) */
   int64_t batch_stride_a, batch_stride_b; /* bytes (0: broadcast) */
   int64_t batch_stride_c;                 /* elements */
   int64_t batch_stride_a_scale, batch_stride_b_scale; /* bytes */
   vh_epilogue epi;
+  /* Split of K across workgroups (MX-int8 pairs with batch <= 1, K % 64 ==
+   * 0, N % 4 == 0 and blocks >= 16): each split leaves an fp32 partial in
+   * `workspace` and a second kernel adds them in split order (deterministic)
+   * and applies the epilogue.  split_k 0: automatic; the split needs
+   * vh_gemm_workspace_bytes(desc) bytes of device memory at `workspace`
+   * (16-byte aligned), else the GEMM runs unsplit. */
+  int32_t split_k;
+  void* workspace;
+  int64_t workspace_bytes;
 } vh_gemm_desc;
 
 int vh_gemm(const vh_gemm_desc* desc, vh_stream_t stream);
+
+/* Device bytes vh_gemm would use as split-K workspace for `desc` (0: none).
+ * No counterpart in the reference, whose CPU GEMM needs no workspace. */
+int64_t vh_gemm_workspace_bytes(const vh_gemm_desc* desc);
 
 /* ------------------------------------------------------------ MXNF4 GEMV
  * Decode-shape linear_mx (ops/quantized.py:651-723) for codebook weights

@@ -85,6 +85,76 @@ def test_linear_mx_mxint8_cfg1():
     assert max_rel_err(got2, got) < 1e-2
 
 
+def _deq_mxint8(p):
+    """Exact float64 values of packed MX-int8 operands: code * 2**(byte - bias)."""
+    c = p.codes.cpu().view(torch.int8).double()
+    e = p.scale.cpu().long() - p.bias
+    e = e.repeat_interleave(p.block_size, dim=1)[:, : c.shape[1]]
+    return c * torch.pow(2.0, e.double())
+
+
+@pytest.mark.parametrize("M,N,K,block,hint,split", [
+    (256, 4096, 4096, 16, 0, 0),     # config 1: automatic tile and split
+    (256, 4096, 4096, 16, 50, 1),    # same tile unsplit
+    (130, 200, 1024, 16, 50, 3),     # ragged M / N; 16 stages in splits of 6, 6, 4
+    (130, 200, 1024, 32, 51, 2),
+    (64, 128, 64, 16, 52, 0),        # a single K stage
+    (300, 520, 640, 16, 53, 5),
+    (70, 260, 1152, 32, 54, 4),
+])
+def test_linear_mxint8_split_k(M, N, K, block, hint, split):
+    """The MX-int8 kernel (tiles 50..54, K split across workgroups with fp32
+    partials added in split order) against the exact float64 product of the
+    decoded operands, and against the register-staged kernel (tile 4).  The
+    split adds the same exact products in another order, so the two GPU
+    results agree to fp32 rounding."""
+    from voyager_amd import gemm, packed
+
+    tab = T.quantization_map("int8").cuda()
+    x = _rand((M, K), 30).cuda()
+    w = _rand((N, K), 31, 0.02).cuda()
+    px = packed.quantize_mx_packed(x, tab, [-1], block, 127.0, True)
+    pw = packed.quantize_mx_packed(w, tab, [-1], block, 127.0, True)
+    ref = _deq_mxint8(px) @ _deq_mxint8(pw).T
+    got = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, block, px.bias, pw.bias, tile_hint=hint,
+                             split_k=split)
+    assert max_rel_err(got, ref) < TOL
+    old = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, block, px.bias, pw.bias, tile_hint=4)
+    assert max_rel_err(got, old) < 1e-2
+    # fp32 output with alpha and bias: the reduce kernel's epilogue
+    alpha = torch.tensor(0.75, device="cuda")
+    bias = _rand((N,), 32).cuda()
+    got32 = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, block, px.bias, pw.bias,
+                               out_dtype=torch.float32, bias=bias, alpha=alpha, tile_hint=hint, split_k=split)
+    ref32 = ref * 0.75 + bias.cpu().double()
+    assert got32.dtype == torch.float32
+    assert max_rel_err(got32, ref32) < 1e-5
+
+
+def test_gemm_workspace_query():
+    """vh_gemm_workspace_bytes: split partials for small MX-int8 grids, none
+    for grids that fill the GPU or for other formats."""
+    import ctypes
+
+    from voyager_amd import gemm
+    from voyager_amd._lib import load
+
+    def q(M, N, K, a_fmt=2, split=0):
+        d = gemm.GemmDesc()
+        d.M, d.N, d.K = M, N, K
+        d.lda, d.ldb = K, K
+        d.a_fmt = d.b_fmt = a_fmt
+        d.a_block = d.b_block = 16
+        d.split_k = split
+        return load().vh_gemm_workspace_bytes(ctypes.c_void_p(ctypes.addressof(d)))
+
+    assert q(256, 4096, 4096) == 4 * 256 * 4096 * 4
+    assert q(4096, 4096, 4096) == 0
+    assert q(256, 4096, 4096, a_fmt=0) == 0
+    assert q(256, 4096, 4096, split=1) == 0
+    assert q(130, 200, 1024, split=3) == 3 * 130 * 200 * 4
+
+
 @pytest.mark.parametrize("M", [1, 16])
 @pytest.mark.parametrize("K,N", [(4096, 1024), (14336, 4096)])
 def test_linear_mx_mxnf4_cfg3(M, K, N):

@@ -51,6 +51,8 @@ class GemmDesc(ctypes.Structure):
         ("batch_stride_c", ctypes.c_int64),
         ("batch_stride_a_scale", ctypes.c_int64), ("batch_stride_b_scale", ctypes.c_int64),
         ("epi", Epilogue),
+        ("split_k", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -261,9 +263,12 @@ def linear_fp8(xq: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor, out: Opt
 
 
 def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: int, bias_w: int,
-                  out_dtype=torch.bfloat16, bias=None, alpha=None, tile_hint: int = 0) -> torch.Tensor:
+                  out_dtype=torch.bfloat16, bias=None, alpha=None, tile_hint: int = 0,
+                  split_k: int = 0) -> torch.Tensor:
     """MX-int8 ``linear_mx`` on packed operands: int8 codes with biased
-    power-of-two scale bytes, decoded exactly to bf16 in the GEMM's staging."""
+    power-of-two scale bytes, decoded exactly to bf16 in the GEMM's staging.
+    Grids too small for the GPU split K (``split_k`` 0: automatic); the
+    partials live in a workspace from torch's allocator."""
     M, K = x_codes.shape
     N = w_codes.shape[0]
     out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
@@ -281,7 +286,13 @@ def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: i
     d.a_block = d.b_block = block_size
     d.a_bias, d.b_bias = bias_x, bias_w
     d.tile_hint = tile_hint
+    d.split_k = split_k
     d.epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
+    nbytes = load().vh_gemm_workspace_bytes(ctypes.c_void_p(ctypes.addressof(d)))
+    ws = None
+    if nbytes > 0:  # split-K partials (fp32), from torch's caching allocator
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x_codes.device)
+        d.workspace, d.workspace_bytes = ws.data_ptr(), nbytes
     run(d, x_codes.device)
     return out
 
