@@ -181,7 +181,9 @@ typedef struct vh_gemm_desc {
                           5: 256x128/8 waves, 6: 256x256/8, 7: 128x256/8, 8: 128x128/8,
                           9: 256x128/8 (one-step prefetch), 10: 128x128/8 (one-step);
                           MX-int8 pairs: 50: 128x128/4 waves, 51: 128x128/8,
-                          52: 128x64/4, 53: 256x128/8, 54: 64x128/4 */
+                          52: 128x64/4, 53: 256x128/8, 54: 64x128/4,
+                          55: 128x128 and 56: 256x128 with 4 decoding +
+                          4 multiplying waves */
   int64_t batch;       /* independent GEMMs (<= 1: one) */
   int64_t batch_stride_a, batch_stride_b; /* bytes (0: broadcast) */
   int64_t batch_stride_c;                 /* elements */

@@ -101,9 +101,14 @@ def _deq_mxint8(p):
     (64, 128, 64, 16, 52, 0),        # a single K stage
     (300, 520, 640, 16, 53, 5),
     (70, 260, 1152, 32, 54, 4),
+    (256, 4096, 4096, 16, 55, 4),    # producer / consumer waves
+    (130, 200, 1024, 16, 55, 3),
+    (300, 520, 640, 32, 56, 1),
+    (64, 128, 64, 16, 55, 0),
+    (2048, 4096, 256, 16, 0, 0),     # a grid that fills the GPU: automatic 56, unsplit
 ])
 def test_linear_mxint8_split_k(M, N, K, block, hint, split):
-    """The MX-int8 kernel (tiles 50..54, K split across workgroups with fp32
+    """The MX-int8 kernels (tiles 50..56, K split across workgroups with fp32
     partials added in split order) against the exact float64 product of the
     decoded operands, and against the register-staged kernel (tile 4).  The
     split adds the same exact products in another order, so the two GPU

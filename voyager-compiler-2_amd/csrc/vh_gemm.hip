@@ -754,6 +754,169 @@ done:
   }
 }
 
+// The same computation with the roles split between waves: 4 consumer
+// waves (2 x 2, each a (BM/2) x (BN/2) sub-tile) run the MFMAs of stage s
+// from one LDS buffer while 4 producer waves decode stage s + 1 into the
+// other and have stage s + 2's loads in flight; one barrier per stage.  On a
+// SIMD the consumer's matrix ops and the producer's VALU decode overlap,
+// where the uniform kernel's waves all decode, then all multiply.
+template <int BM, int BN>
+__global__ void __launch_bounds__(512) k_gemm_mxi8_ws(GemmArgs g, int64_t kc, float* __restrict__ part) {
+  constexpr int NP = 256;                            // producer threads
+  constexpr int CA = BM * 4 / NP, CB = BN * 4 / NP;  // 16-code chunks per producer thread and stage
+  static_assert(CA >= 1 && CB >= 1 && (BM * 4) % NP == 0 && (BN * 4) % NP == 0, "stage chunks must divide");
+  constexpr int WM = 2, WN = 2;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1, "bad wave layout");
+  static_assert(WN * BM * (BN / WN + 8) * 2 <= 2 * (BM + BN) * ROWP, "epilogue tile does not fit the stage LDS");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* As = smem;
+  uint8_t* Bs = smem + 2 * BM * ROWP;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool consumer = wave < 4;
+  int64_t m0, n0;
+  tile_origin(g.M, g.N, BM, BN, g.group_m, m0, n0);
+  const int64_t k_lo = (int64_t)blockIdx.y * kc;
+  const int64_t k_hi = (k_lo + kc) < g.K ? (k_lo + kc) : g.K;
+  const int nk = (int)((k_hi - k_lo) / MX_KE);
+
+  // ---- producer state (unused by consumer waves)
+  const int pt = tid - 256;
+  const int64_t rows_a = (g.M - m0) < BM ? (g.M - m0) : BM;
+  const int64_t rows_b = (g.N - n0) < BN ? (g.N - n0) : BN;
+  const rsrc_t ad = make_rsrc(g.A + m0 * g.lda, rows_a * g.lda);
+  const rsrc_t bd = make_rsrc(g.B + n0 * g.ldb, rows_b * g.ldb);
+  const rsrc_t as = make_rsrc(g.a_scale + m0 * g.lds_a, rows_a * g.lds_a);
+  const rsrc_t bs = make_rsrc(g.b_scale + n0 * g.lds_b, rows_b * g.lds_b);
+  const int ash = __builtin_ctz(g.a_block), bsh = __builtin_ctz(g.b_block);
+  int aoff[CA], asrow[CA], ak[CA], boff[CB], bsrow[CB], bk[CB];
+#pragma unroll
+  for (int i = 0; i < CA; ++i) {
+    const int ch = pt + i * NP, r = ch >> 2;
+    ak[i] = (int)k_lo + (ch & 3) * 16;
+    aoff[i] = r * (int)g.lda + ak[i];
+    asrow[i] = r * (int)g.lds_a;
+  }
+#pragma unroll
+  for (int i = 0; i < CB; ++i) {
+    const int ch = pt + i * NP, r = ch >> 2;
+    bk[i] = (int)k_lo + (ch & 3) * 16;
+    boff[i] = r * (int)g.ldb + bk[i];
+    bsrow[i] = r * (int)g.lds_b;
+  }
+  uint4 ra[2][CA], rb[2][CB];
+  uint32_t sa[2][CA], sb[2][CB];
+  auto fetch = [&](int j, int s) {
+    const int kr = (s < nk ? s : nk - 1) * MX_KE;
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      ra[j][i] = bload16(ad, aoff[i] + kr);
+      sa[j][i] = bload1(as, asrow[i] + ((ak[i] + kr) >> ash));
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      rb[j][i] = bload16(bd, boff[i] + kr);
+      sb[j][i] = bload1(bs, bsrow[i] + ((bk[i] + kr) >> bsh));
+    }
+  };
+  auto stash = [&](int j, int st) {
+    uint8_t* a = As + st * BM * ROWP;
+    uint8_t* b = Bs + st * BN * ROWP;
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      const int ch = pt + i * NP;
+      uint4 lo, hi;
+      decode16_mxi8(ra[j][i], (int)sa[j][i] - g.a_bias, lo, hi);
+      uint8_t* d = a + (ch >> 2) * ROWP + (ch & 3) * 32;
+      *(uint4*)d = lo;
+      *(uint4*)(d + 16) = hi;
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int ch = pt + i * NP;
+      uint4 lo, hi;
+      decode16_mxi8(rb[j][i], (int)sb[j][i] - g.b_bias, lo, hi);
+      uint8_t* d = b + (ch >> 2) * ROWP + (ch & 3) * 32;
+      *(uint4*)d = lo;
+      *(uint4*)(d + 16) = hi;
+    }
+  };
+
+  // ---- consumer state
+  const int wm = (wave & 3) / WN, wn = (wave & 3) % WN;
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  auto compute = [&](int st) {
+    const uint8_t* a = As + st * BM * ROWP + (wm * (BM / WM) + lrow) * ROWP;
+    const uint8_t* b = Bs + st * BN * ROWP + (wn * (BN / WN) + lrow) * ROWP;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int off = kk * 32 + lhalf * 16;
+      bf16x8 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = *(const bf16x8*)(a + i * 32 * ROWP + off);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = *(const bf16x8*)(b + j * 32 * ROWP + off);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // Iteration k: consumers multiply stage k (buffer k % 2); producers issue
+  // stage k + 2's loads into the register set stage k used, then decode
+  // stage k + 1 into buffer (k + 1) % 2.  Both buffers are safe: buffer
+  // (k + 1) % 2 was last read in iteration k - 1, before its barrier.
+  if (!consumer) {
+    fetch(0, 0);
+    fetch(1, 1);
+    stash(0, 0);
+  }
+  __syncthreads();
+  for (int k = 0; k < nk; k += 2) {
+    if (consumer) {
+      compute(0);
+    } else {
+      fetch(0, k + 2);
+      if (k + 1 < nk) stash(1, 1);
+    }
+    __syncthreads();
+    if (k + 1 >= nk) break;
+    if (consumer) {
+      compute(1);
+    } else {
+      fetch(1, k + 3);
+      if (k + 2 < nk) stash(0, 0);
+    }
+    __syncthreads();
+  }
+  if (!consumer) return;  // no barrier follows: the epilogue syncs within each wave
+  if (gridDim.y == 1) {
+    store_tile<TM, TN, WM, WN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+  } else {
+    GemmArgs p = g;
+    p.C = part + (int64_t)blockIdx.y * g.M * g.N;
+    p.ldc = g.N;
+    p.epi.mode = EPI_PLAIN;
+    p.epi.out_dtype = VH_F32;
+    p.epi.scale = nullptr;
+    p.epi.bias = nullptr;
+    store_tile_direct<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane);
+  }
+}
+
 // C = epilogue(sum over z of part[z]) for split-K partials [S][M][N] (fp32),
 // summed in split order; four consecutive elements of a row per thread
 // (N % 4 == 0).
@@ -1083,10 +1246,10 @@ int launch_tile(GemmArgs g, int64_t batch, hipStream_t stream) {
   return vh::check_launch("vh_gemm");
 }
 
-template <int BM, int BN, int WM, int WN, int P = 2>
+template <int BM, int BN, int WM, int WN, int P = 2, bool WS = false>
 int launch_mxi8(GemmArgs g, int splits, float* part, hipStream_t stream) {
   g.group_m = 8;
-  constexpr int NT = WM * WN * 64;
+  constexpr int NT = WS ? 512 : WM * WN * 64;
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   const int64_t stages = g.K / MX_KE;
   const int64_t kc = (stages + splits - 1) / splits * MX_KE;
@@ -1094,15 +1257,21 @@ int launch_mxi8(GemmArgs g, int splits, float* part, hipStream_t stream) {
   const size_t smem = 2 * (BM + BN) * ROWP;
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)k_gemm_mxi8<BM, BN, WM, WN, P>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)smem) != hipSuccess) {
+    const void* fn;
+    if constexpr (WS) fn = (const void*)k_gemm_mxi8_ws<BM, BN>;
+    else fn = (const void*)k_gemm_mxi8<BM, BN, WM, WN, P>;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess) {
       vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
       return VH_ELAUNCH;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_mxi8<BM, BN, WM, WN, P>), dim3((unsigned)tiles, (unsigned)sp), dim3(NT), smem, stream, g,
-                     kc, sp > 1 ? part : nullptr);
+  if constexpr (WS)
+    hipLaunchKernelGGL((k_gemm_mxi8_ws<BM, BN>), dim3((unsigned)tiles, (unsigned)sp), dim3(NT), smem, stream, g, kc,
+                       sp > 1 ? part : nullptr);
+  else
+    hipLaunchKernelGGL((k_gemm_mxi8<BM, BN, WM, WN, P>), dim3((unsigned)tiles, (unsigned)sp), dim3(NT), smem, stream,
+                       g, kc, sp > 1 ? part : nullptr);
   if (sp > 1) {
     const int64_t quads = g.M * g.N / 4;
     hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, part, (int)sp,
@@ -1125,15 +1294,19 @@ void mxi8_plan(const vh_gemm_desc* d, int& cfg, int& splits) {
   cfg = d->tile_hint;
   // Measured on MI355X (N = K = 4096): at M = 256, 128 x 128 tiles with 8
   // waves split 4 ways take 25.8 us (4 waves: 30.3 us; 128 x 64 split 4:
-  // 28.6 us; split 8 pays twice the partial traffic); at M = 2048, 256 x 128
-  // unsplit takes 101.7 us (676 TFLOP/s; the register-staged k_gemm 154 us).
-  if (cfg == 0) cfg = tiles(256, 128) >= 256 ? 53 : 51;
+  // 28.6 us; producer / consumer waves 27.5 us; split 8 pays twice the
+  // partial traffic); at M = 2048, 256 x 128 with producer / consumer waves
+  // takes 95.1 us (722 TFLOP/s; uniform waves 101.7 us, the register-staged
+  // k_gemm 154 us).
+  if (cfg == 0) cfg = tiles(256, 128) >= 256 ? 56 : 51;
   int64_t bm = 128, bn = 128;
   switch (cfg) {
     case 50: case 51: break;
     case 52: bn = 64; break;
     case 53: bm = 256; break;
     case 54: bm = 64; break;
+    case 55: break;
+    case 56: bm = 256; break;
     default: cfg = 0; return;
   }
   const int64_t t = tiles(bm, bn);
@@ -1305,6 +1478,8 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
         case 52: return launch_mxi8<128, 64, 2, 2>(g, splits, part, st);
         case 53: return launch_mxi8<256, 128, 4, 2>(g, splits, part, st);
         case 54: return launch_mxi8<64, 128, 1, 4>(g, splits, part, st);
+        case 55: return launch_mxi8<128, 128, 2, 2, 2, true>(g, splits, part, st);
+        case 56: return launch_mxi8<256, 128, 2, 2, 2, true>(g, splits, part, st);
         default: break;
       }
     }
