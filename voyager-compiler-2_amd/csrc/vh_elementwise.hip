@@ -295,106 +295,160 @@ k_quantize_e4m3_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp,
 // ------------------------------------------------------------ posit tables
 // A posit's code (or reference-form value) as a function of the bfloat16
 // pattern q = bf16(x / s) only changes for magnitudes between the flush
-// threshold and maxpos.  Each workgroup evaluates the closed form once per
-// pattern of [lo, hi] (host-chosen bf16 magnitude bits, one binade beyond
-// both ends) and per sign, plus four slots per sign: zero, every magnitude
-// below lo (flushed), every finite magnitude above hi (saturated) and the
-// non-finite ones; the elements then cost one LDS lookup instead of ~50 VALU
-// ops of the closed form.
-constexpr int TAB_SPECIAL = 4;
-constexpr int TAB_MAX_SPAN = 8192;  // table entries per sign
+// threshold and maxpos.  Each workgroup builds an LDS table indexed by
+//   key(q) = min(max(q & 0x7fff, lo1), hi1) - lo1 + (q & 0x8000 ? PLANE : 0)
+// with lo1 = lo - 1 below the flush threshold (every smaller magnitude, zero
+// included, shares its entry) and hi1 = hi + 1 above maxpos (every larger
+// finite magnitude saturates there); lo .. hi (host-chosen, one binade
+// beyond both ends) get the closed form.  Non-finite q, which the clamp
+// would send to the saturated entry, are caught per batch and take NaR.  The
+// closed form runs once per positive magnitude; its negative twin is the
+// posit negation (two's complement of the code; the value with its sign
+// flipped, zero staying +0).  Two keys cost six packed 16-bit ops.
+constexpr int TAB_THREADS = 1024;
+constexpr int TAB_UNROLL = 4;
+constexpr uint32_t TAB_PLANE = 0x2000;  // entries per sign plane (max)
 
 template <bool PACKED>
-__device__ __forceinline__ void build_posit_table(const vh_format& f, int lo, int hi, uint16_t* tab) {
-  const int per = TAB_SPECIAL + hi - lo + 1;
-  for (int i = threadIdx.x; i < 2 * per; i += blockDim.x) {
-    const int sgn = i / per, j = i % per;
-    const uint32_t mag = j == 0 ? 0u : j == 1 ? 1u : j == 2 ? 0x7f7fu : j == 3 ? 0x7fc0u : (uint32_t)(lo + j - TAB_SPECIAL);
-    const uint32_t b = mag | ((uint32_t)sgn << 15);
-    const float v = fmt_value_k<K_POSIT>(b, f, nullptr);
-    tab[i] = (uint16_t)(PACKED ? fmt_code_k<K_POSIT>(b, v, f, nullptr) : f2bf(v));
+__device__ __forceinline__ uint32_t posit_entry(uint32_t b, const vh_format& f) {
+  const float v = fmt_value_k<K_POSIT>(b, f, nullptr);
+  return PACKED ? fmt_code_k<K_POSIT>(b, v, f, nullptr) : f2bf(v);
+}
+
+template <bool PACKED>
+__device__ __forceinline__ uint32_t posit_negate(uint32_t c, const vh_format& f) {
+  if constexpr (PACKED) return (0u - c) & ((1u << f.p0) - 1u);
+  else return (c & 0x7fffu) ? (c ^ 0x8000u) : c;
+}
+
+template <bool PACKED>
+__device__ __forceinline__ void build_posit_table(const vh_format& f, int lo1, int hi1, void* tab) {
+  uint8_t* tb = (uint8_t*)tab;
+  uint16_t* th = (uint16_t*)tab;
+  for (int m = lo1 + (int)threadIdx.x; m <= hi1; m += blockDim.x) {
+    const uint32_t b = m == lo1 ? 1u : m == hi1 ? 0x7f7fu : (uint32_t)m;
+    const uint32_t c = posit_entry<PACKED>(b, f);
+    const uint32_t n = posit_negate<PACKED>(c, f);
+    const int i = m - lo1;
+    if constexpr (PACKED) {
+      tb[i] = (uint8_t)c;
+      tb[i + TAB_PLANE] = (uint8_t)n;
+    } else {
+      th[i] = (uint16_t)c;
+      th[i + TAB_PLANE] = (uint16_t)n;
+    }
   }
   __syncthreads();
 }
 
-__device__ __forceinline__ uint32_t posit_lookup(uint32_t b, int lo, int hi, int per, const uint16_t* tab) {
-  const uint32_t m = b & 0x7fffu;
-  const int j = m == 0 ? 0 : m >= 0x7f80u ? 3 : (int)m < lo ? 1 : (int)m > hi ? 2 : TAB_SPECIAL + (int)m - lo;
-  return tab[(b >> 15) * per + j];
+// Table offsets of the two bf16 patterns in q, one per half.
+VH_DEV uint32_t posit_keys(uint32_t q, uint32_t lo1x2, uint32_t hi1x2) {
+  const uint32_t c = pk_min_u16(pk_max_u16(q & 0x7fff7fffu, lo1x2), hi1x2);
+  return pk_sub_u16(c, lo1x2) | ((q >> 2) & 0x20002000u);
 }
 
 // quantize(x, s, qmap=posit) per tensor: q = bf16(x / s) as in k_quantize_pt,
 // then the table.  One 1024-thread workgroup per CU builds the table once;
-// its first loads are issued before the build and every later batch is
-// loaded while the previous one converts.
-constexpr int TAB_THREADS = 1024;
-
+// its first loads are issued before the build and each later batch is
+// loaded while the previous one converts.  q is formed from x * rcp(s) with the hardware
+// bf16 converter; a thread whose batch holds a product within 4 fp32 ulps of
+// a bf16 rounding midpoint (or a scale outside the normal range) redoes the
+// batch with the correctly rounded division, and a batch holding a
+// non-finite q looks each element's NaR case up separately.
 template <bool PACKED>
 __global__ void __launch_bounds__(TAB_THREADS)
 k_quantize_posit_tab(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int sdt, vh_format f, int lo, int hi,
                      void* __restrict__ out) {
-  extern __shared__ uint16_t tab[];
+  extern __shared__ uint32_t tab[];
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t step = stride * UNROLL;
+  const int64_t step = stride * TAB_UNROLL;
   auto load = [&](uint4* raw, int64_t v0) {
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
+    for (int u = 0; u < TAB_UNROLL; ++u) {
       const int64_t v = v0 + u * stride;
       raw[u] = v < nvec ? ld_stream16(x + v * 8) : make_uint4(0, 0, 0, 0);
     }
   };
   int64_t v0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  uint4 raw[UNROLL];
-  load(raw, v0);
-  build_posit_table<PACKED>(f, lo, hi, tab);
-  const int per = TAB_SPECIAL + hi - lo + 1;
+  uint4 r0[TAB_UNROLL], r1[TAB_UNROLL];
+  load(r0, v0);
+  const int lo1 = lo - 1, hi1 = hi + 1;
+  build_posit_table<PACKED>(f, lo1, hi1, tab);
+  const uint32_t nar[2] = {posit_entry<PACKED>(0x7fc0u, f), posit_entry<PACKED>(0xffc0u, f)};
+  const uint32_t lo1x2 = (uint32_t)lo1 | ((uint32_t)lo1 << 16);
+  const uint32_t hi1x2 = (uint32_t)hi1 | ((uint32_t)hi1 << 16);
+  const uint8_t* tb = (const uint8_t*)tab;
+  const uint16_t* th = (const uint16_t*)tab;
   const float s = load_any(sp, sdt, 0);
   const float as = fabsf(s);
   const bool fast = as >= 0x1p-126f && as <= 0x1p126f;
   const float r = __builtin_amdgcn_rcpf(s);
-  for (; v0 < nvec; v0 += step) {
-    uint4 nraw[UNROLL];
-    load(nraw, v0 + step);
+  // both entries of q, packed; with `special` a non-finite half takes NaR
+  auto lookup = [&](uint32_t q, bool special) -> uint32_t {
+    const uint32_t k = posit_keys(q, lo1x2, hi1x2);
+    uint32_t c0 = PACKED ? (uint32_t)tb[k & 0xffffu] : (uint32_t)th[k & 0xffffu];
+    uint32_t c1 = PACKED ? (uint32_t)tb[k >> 16] : (uint32_t)th[k >> 16];
+    if (special) {
+      if ((q & 0x7fffu) >= 0x7f80u) c0 = nar[(q >> 15) & 1u];
+      if (((q >> 16) & 0x7fffu) >= 0x7f80u) c1 = nar[q >> 31];
+    }
+    return PACKED ? (c0 | (c1 << 8)) : (c0 | (c1 << 16));
+  };
+  auto convert = [&](const uint4* raw, int64_t vb) {
+    uint32_t qb[TAB_UNROLL][4];
+    uint32_t mn = 0xffffffffu, mx = 0u;
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int64_t v = v0 + u * stride;
-      if (v >= nvec) break;
+    for (int u = 0; u < TAB_UNROLL; ++u) {
       const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-      float q[8];
-      bool slow = !fast;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        q[j] = bf2f(j & 1 ? w[j >> 1] >> 16 : w[j >> 1] & 0xffffu) * r;
-        slow |= ((__float_as_uint(q[j]) - 0x7FFCu) & 0xFFFFu) <= 8u;
-      }
-      uint32_t qb[4];
-      if (!slow) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qb[j] = f2bf2_hw(q[2 * j], q[2 * j + 1]);
-      } else {  // near a bf16 midpoint: correctly rounded division
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qb[j] = f2bf(bf2f(w[j] & 0xffffu) / s) | (f2bf(bf2f(w[j] >> 16) / s) << 16);
-      }
-      uint32_t o[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t c0 = posit_lookup(qb[j] & 0xffffu, lo, hi, per, tab);
-        const uint32_t c1 = posit_lookup(qb[j] >> 16, lo, hi, per, tab);
-        o[j] = PACKED ? (c0 | (c1 << 8)) : (c0 | (c1 << 16));
+        const float q0 = __uint_as_float(w[j] << 16) * r;
+        const float q1 = __uint_as_float(w[j] & 0xffff0000u) * r;
+        const uint32_t low = __builtin_amdgcn_perm(__float_as_uint(q1), __float_as_uint(q0), 0x05040100u);
+        mn = pk_min_u16(mn, pk_sub_u16(low, 0x7ffc7ffcu));
+        qb[u][j] = f2bf2_hw(q0, q1);
+        mx = pk_max_u16(mx, qb[u][j] & 0x7fff7fffu);
       }
-      if constexpr (PACKED) st_stream8((uint8_t*)out + v * 8, make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16)));
-      else st_stream16((uint16_t*)out + v * 8, make_uint4(o[0], o[1], o[2], o[3]));
     }
+    const bool exact = !fast || (mn & 0xffffu) <= 8u || (mn >> 16) <= 8u;
+    if (exact) {  // rare: correctly rounded division
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) raw[u] = nraw[u];
+      for (int u = 0; u < TAB_UNROLL; ++u) {
+        const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qb[u][j] = f2bf(bf2f(w[j] & 0xffffu) / s) | (f2bf(bf2f(w[j] >> 16) / s) << 16);
+      }
+    }
+    const bool special = exact || (mx & 0xffffu) >= 0x7f80u || (mx >> 16) >= 0x7f80u;
+#pragma unroll
+    for (int u = 0; u < TAB_UNROLL; ++u) {
+      const int64_t v = vb + u * stride;
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = lookup(qb[u][j], special);
+      if (v < nvec) {
+        if constexpr (PACKED) st_stream8((uint8_t*)out + v * 8, make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16)));
+        else st_stream16((uint16_t*)out + v * 8, make_uint4(o[0], o[1], o[2], o[3]));
+      }
+    }
+  };
+  for (;;) {
+    if (v0 >= nvec) break;
+    load(r1, v0 + step);
+    convert(r0, v0);
+    v0 += step;
+    if (v0 >= nvec) break;
+    load(r0, v0 + step);
+    convert(r1, v0);
+    v0 += step;
   }
 }
 
-// Host: the table's magnitude range for a posit map, or false when it is
-// wider than TAB_MAX_SPAN.  Below 2**(floor(-(n-1) 2**es + 2**(es-1)) - 1)
-// every magnitude flushes to zero; above 2**((n-2) 2**es + 1) every finite
-// one saturates at maxpos.
-bool posit_table_range(const vh_format& f, int* lo, int* hi, size_t* lds_bytes) {
+// Host: the table's magnitude range for a posit map and its LDS bytes, or
+// false for a map it does not cover.  Below 2**(floor(-(n-1) 2**es +
+// 2**(es-1)) - 1) every magnitude flushes to zero; above 2**((n-2) 2**es +
+// 1) every finite one saturates at maxpos.
+bool posit_table_range(const vh_format& f, bool packed, int* lo, int* hi, size_t* lds_bytes) {
   const int n = f.p0, es = f.p1;
   if (f.kind != VH_FMT_POSIT || n < 2 || es < 0 || es > 4) return false;
   const double e_lo = std::floor(-(n - 1) * std::ldexp(1.0, es) + std::ldexp(1.0, es - 1)) - 1.0;
@@ -402,26 +456,40 @@ bool posit_table_range(const vh_format& f, int* lo, int* hi, size_t* lds_bytes) 
   if (e_lo < -126 || e_hi > 127) return false;
   *lo = (int)(e_lo + 127) << 7;
   *hi = (int)(e_hi + 127) << 7;
-  if (*hi - *lo + 1 > TAB_MAX_SPAN) return false;
-  *lds_bytes = (size_t)2 * (TAB_SPECIAL + *hi - *lo + 1) * sizeof(uint16_t);
+  if (*lo < 1 || *hi + 1 >= 0x7f80 || *hi - *lo + 3 > (int)TAB_PLANE) return false;
+  *lds_bytes = (size_t)2 * TAB_PLANE * (packed ? 1 : 2);
   return true;
 }
 
-// 16 codes per thread per step: out[i] = tab[x[i]] (low 16 bits), i < 16 n16.
+// out[i] = tab[x[i]] (low 16 bits) for i < 16 n16: 16 codes per thread per
+// load, GATHER_UNROLL loads in flight per thread.
+constexpr int GATHER_UNROLL = 4;
+
 __device__ __forceinline__ void gather16(const uint8_t* __restrict__ x, int64_t n16, const uint32_t* tab,
                                          uint16_t* __restrict__ out) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
-    const uint4 c = ld_stream16(x + i * 16);
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    uint32_t o[8];
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n16; i0 += stride * GATHER_UNROLL) {
+    uint4 c[GATHER_UNROLL];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[2 * j] = tab[w[j] & 0xffu] | (tab[(w[j] >> 8) & 0xffu] << 16);
-      o[2 * j + 1] = tab[(w[j] >> 16) & 0xffu] | (tab[w[j] >> 24] << 16);
+    for (int u = 0; u < GATHER_UNROLL; ++u) {
+      const int64_t i = i0 + u * stride;
+      c[u] = i < n16 ? ld_stream16(x + i * 16) : make_uint4(0, 0, 0, 0);
     }
-    st_stream16(out + i * 16, make_uint4(o[0], o[1], o[2], o[3]));
-    st_stream16(out + i * 16 + 8, make_uint4(o[4], o[5], o[6], o[7]));
+#pragma unroll
+    for (int u = 0; u < GATHER_UNROLL; ++u) {
+      const int64_t i = i0 + u * stride;
+      const uint32_t w[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
+      uint32_t o[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[2 * j] = tab[w[j] & 0xffu] | (tab[(w[j] >> 8) & 0xffu] << 16);
+        o[2 * j + 1] = tab[(w[j] >> 16) & 0xffu] | (tab[w[j] >> 24] << 16);
+      }
+      if (i < n16) {
+        st_stream16(out + i * 16, make_uint4(o[0], o[1], o[2], o[3]));
+        st_stream16(out + i * 16 + 8, make_uint4(o[4], o[5], o[6], o[7]));
+      }
+    }
   }
 }
 
@@ -615,7 +683,7 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
     size_t tab_bytes = 0;
     // the posit table costs a few thousand closed-form evaluations per
     // workgroup: one 1024-thread workgroup per CU, each over a long range
-    int64_t tab_blocks = (nvec + TAB_THREADS * UNROLL - 1) / (TAB_THREADS * UNROLL);
+    int64_t tab_blocks = (nvec + TAB_THREADS * TAB_UNROLL - 1) / (TAB_THREADS * TAB_UNROLL);
     if (tab_blocks > 256) tab_blocks = 256;
     return dispatch_kind(kernel_kind(fmt), [&](auto kind) {
       constexpr int K = decltype(kind)::value;
@@ -625,14 +693,14 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
         } else if constexpr (K == K_E4M3) {
           hipLaunchKernelGGL(k_quantize_e4m3_pt, dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)x, nvec,
                              sp.ptr, sp.dtype, (uint8_t*)out);
-        } else if (K == K_POSIT && posit_table_range(f, &lo, &hi, &tab_bytes)) {
+        } else if (K == K_POSIT && posit_table_range(f, true, &lo, &hi, &tab_bytes)) {
           hipLaunchKernelGGL(k_quantize_posit_tab<true>, dim3((unsigned)tab_blocks), dim3(TAB_THREADS), tab_bytes, st,
                              (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, lo, hi, out);
         } else {
           hipLaunchKernelGGL((k_quantize_pt<K, true>), dim3((unsigned)blocks), dim3(256), 0, st,
                              (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, out);
         }
-      } else if (K == K_POSIT && posit_table_range(f, &lo, &hi, &tab_bytes)) {
+      } else if (K == K_POSIT && posit_table_range(f, false, &lo, &hi, &tab_bytes)) {
         hipLaunchKernelGGL(k_quantize_posit_tab<false>, dim3((unsigned)tab_blocks), dim3(TAB_THREADS), tab_bytes, st,
                            (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, lo, hi, out);
       } else {
