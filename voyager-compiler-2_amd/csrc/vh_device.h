@@ -41,12 +41,19 @@ VH_DEV uint32_t f2bf2_hw(float lo, float hi) {
 
 // Streaming accesses that bypass cache residency (the nt bit): each element
 // of a large elementwise op is touched once, so its lines should not evict
-// data that is reused.  16-byte loads, 8- and 16-byte stores.
+// data that is reused.  Measured from HBM (inputs rotated through more than
+// the 256 MB Infinity Cache), the hint makes 8M-64M-element quantize streams
+// 5-10% faster than plain accesses; with cache-resident inputs it is the
+// other way round.  8- and 16-byte loads and stores.
 typedef unsigned int vh_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int vh_u32x2 __attribute__((ext_vector_type(2)));
 VH_DEV uint4 ld_stream16(const void* p) {
   const vh_u32x4 v = __builtin_nontemporal_load((const vh_u32x4*)p);
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+VH_DEV uint2 ld_stream8(const void* p) {
+  const vh_u32x2 v = __builtin_nontemporal_load((const vh_u32x2*)p);
+  return make_uint2(v.x, v.y);
 }
 VH_DEV void st_stream8(void* p, uint2 v) { __builtin_nontemporal_store(vh_u32x2{v.x, v.y}, (vh_u32x2*)p); }
 VH_DEV void st_stream16(void* p, uint4 v) { __builtin_nontemporal_store(vh_u32x4{v.x, v.y, v.z, v.w}, (vh_u32x4*)p); }

@@ -461,35 +461,48 @@ bool posit_table_range(const vh_format& f, bool packed, int* lo, int* hi, size_t
   return true;
 }
 
-// out[i] = tab[x[i]] (low 16 bits) for i < 16 n16: 16 codes per thread per
-// load, GATHER_UNROLL loads in flight per thread.
+// out[i] = tab[x[i]] (low 16 bits) for i < 16 n16.  A wave takes 1024-code
+// units: lane l converts codes 8 l .. 8 l + 7 of each half, so both of its
+// 16-byte stores belong to one contiguous 1 KB wave store; GATHER_UNROLL
+// units are in flight per wave.  The last n16 % 64 groups of 16 codes go one
+// per thread.
 constexpr int GATHER_UNROLL = 4;
+
+__device__ __forceinline__ uint4 gather8(uint2 c, const uint32_t* tab) {
+  return make_uint4(tab[c.x & 0xffu] | (tab[(c.x >> 8) & 0xffu] << 16),
+                    tab[(c.x >> 16) & 0xffu] | (tab[c.x >> 24] << 16),
+                    tab[c.y & 0xffu] | (tab[(c.y >> 8) & 0xffu] << 16),
+                    tab[(c.y >> 16) & 0xffu] | (tab[c.y >> 24] << 16));
+}
 
 __device__ __forceinline__ void gather16(const uint8_t* __restrict__ x, int64_t n16, const uint32_t* tab,
                                          uint16_t* __restrict__ out) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n16; i0 += stride * GATHER_UNROLL) {
-    uint4 c[GATHER_UNROLL];
+  const int lane = threadIdx.x & 63;
+  const int64_t units = n16 / 64;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t u0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; u0 < units; u0 += nwaves * GATHER_UNROLL) {
+    uint2 c[GATHER_UNROLL][2];
 #pragma unroll
     for (int u = 0; u < GATHER_UNROLL; ++u) {
-      const int64_t i = i0 + u * stride;
-      c[u] = i < n16 ? ld_stream16(x + i * 16) : make_uint4(0, 0, 0, 0);
+      const int64_t unit = u0 + u * nwaves;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        c[u][h] = unit < units ? ld_stream8(x + unit * 1024 + h * 512 + lane * 8) : make_uint2(0, 0);
     }
 #pragma unroll
     for (int u = 0; u < GATHER_UNROLL; ++u) {
-      const int64_t i = i0 + u * stride;
-      const uint32_t w[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
-      uint32_t o[8];
+      const int64_t unit = u0 + u * nwaves;
+      if (unit < units) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        o[2 * j] = tab[w[j] & 0xffu] | (tab[(w[j] >> 8) & 0xffu] << 16);
-        o[2 * j + 1] = tab[(w[j] >> 16) & 0xffu] | (tab[w[j] >> 24] << 16);
-      }
-      if (i < n16) {
-        st_stream16(out + i * 16, make_uint4(o[0], o[1], o[2], o[3]));
-        st_stream16(out + i * 16 + 8, make_uint4(o[4], o[5], o[6], o[7]));
+        for (int h = 0; h < 2; ++h) st_stream16(out + unit * 1024 + h * 512 + lane * 8, gather8(c[u][h], tab));
       }
     }
+  }
+  const int64_t i = units * 64 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) {
+    const uint4 c = ld_stream16(x + i * 16);
+    st_stream16(out + i * 16, gather8(make_uint2(c.x, c.y), tab));
+    st_stream16(out + i * 16 + 8, gather8(make_uint2(c.z, c.w), tab));
   }
 }
 
