@@ -1,0 +1,39 @@
+"""voyager_amd.lower without a GPU: sites of a graph whose constants are on
+the CPU are reported with the reason, as the reference's find_sites reports
+a device it cannot run (backend/gpu/__init__.py:102-131)."""
+
+import torch
+
+import voyager_amd  # noqa: F401  (registers quantized_ops)
+from voyager_amd import lower
+from oracle import tables as T
+
+Q = torch.ops.quantized_ops
+
+
+class _Site(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        g = torch.Generator().manual_seed(0)
+        self.register_buffer("sx", torch.tensor(0.01, dtype=torch.bfloat16))
+        self.register_buffer("wq", (torch.randn(32, 64, generator=g) * 0.02).bfloat16())
+        self.register_buffer("qmap", T.quantization_map("fp8_e4m3"))
+
+    def forward(self, x):
+        xq = Q.quantize.default(x, self.sx, None, None, None, self.qmap)
+        return torch.ops.aten.linear.default(xq, self.wq)
+
+
+def test_cpu_graph_sites_are_reported_not_lowered():
+    gm = torch.fx.symbolic_trace(_Site())
+    before = [n.target for n in gm.graph.nodes]
+    sites, skipped = lower.find_sites(gm)
+    assert sites == [] and list(skipped.values()) == ["cpu is not a GPU"]
+    assert list(lower.lower(gm).values()) == ["cpu is not a GPU"]
+    assert [n.target for n in gm.graph.nodes] == before
+
+
+def test_unsupported_device_reasons():
+    cpu = torch.device("cpu")
+    assert lower.fp8_unsupported(cpu) == "cpu is not a GPU"
+    assert lower.nvfp4_unsupported(cpu) == "cpu is not a GPU"
