@@ -153,3 +153,65 @@ def test_lower_reports_unmatched_sites():
     report = lower.lower(gm)
     assert list(report.values()) == ["bias is not lowered"]
     assert torch.equal(gm(x.cuda()), ref)
+
+
+def test_lowered_graph_replays_under_hip_graph_capture():
+    """A lowered graph with all four site kinds, captured in a HIP graph
+    after one eager run: every replay (with eager work and synchronisation
+    between them) equals the eager result bit for bit."""
+    from voyager_amd import lower
+
+    f8, p8, i8 = T.quantization_map("fp8_e4m3"), T.quantization_map("posit8_1"), T.quantization_map("int8")
+    vt = T.quantization_map("lut4_to_int6")
+    index, entries, mid = T.codebook_index_table(vt)
+    stab = T.quantization_map("fp8_e5m3")
+    one = torch.tensor(1.0, dtype=torch.bfloat16)
+    x = _rand((8, 256), 20)
+    w1, w2, w3, w4 = (_rand((256, 256), 21 + i, 0.02) for i in range(4))
+    sx = O.per_tensor_scale(x, 448.0)
+    sw1 = O.per_tensor_scale(w1, 448.0)
+    wq1 = O.quantize(w1, sw1, qmap=f8)
+    wq2 = O.quantize(w2, one, qmap=p8)
+    s3, c3 = O.quantize_mx(w3, i8, [-1], 16, 127.0, True)
+    s4, c4 = O.quantize_mx(w4, index, [-1], 64, 31.0, False, stab)
+
+    class M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            for name, t in dict(sx=sx, s=sx * sw1, one=one, wq1=wq1, wq2=wq2, c3=c3, s3=s3, c4=c4, s4=s4, f8=f8,
+                                p8=p8, i8=i8, ident=T.quantization_map(None), index=index, entries=entries, mid=mid,
+                                stab=stab).items():
+                self.register_buffer(name, t)
+
+        def forward(self, x):
+            a = Q.dequantize.default(
+                torch.ops.aten.linear.default(Q.quantize.default(x, self.sx, None, None, None, self.f8), self.wq1),
+                self.s, None, None, None, self.ident)
+            b = torch.ops.aten.linear.default(Q.quantize.default(a, self.one, None, None, None, self.p8), self.wq2)
+            q = Q.quantize_mx.default(b, self.i8, [-1], 16, 127.0, True)
+            c = Q.linear_mx.default(q[1], self.c3, input_scale=q[0], weight_scale=self.s3, block_size=16)
+            r = Q.quantize_mx.default(c, self.index, [-1], 64, 31.0, False, self.stab, self.mid)
+            return Q.linear_mx.default(r[1], self.c4, input_scale=r[0], weight_scale=self.s4, block_size=64,
+                                       input_code=self.entries, weight_code=self.entries)
+
+    gm = torch.fx.symbolic_trace(M()).cuda()
+    xd = x.cuda()
+    ref = gm(xd)
+    report = lower.lower(gm)
+    assert sorted(report.values()) == ["fp8", "mxint8", "mxnf4", "posit8"], report
+    eager = gm(xd)
+    assert max_rel_err(eager, ref) < 0.05
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        gm(xd)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = gm(xd)
+    for _ in range(3):
+        torch.randn(1 << 16, device="cuda").sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)

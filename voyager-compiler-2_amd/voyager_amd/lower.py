@@ -301,15 +301,17 @@ def lowered_mxint8_linear(x, qmap, w_codes, w_scale, w_bias, block_size: int, bi
 
 
 def lowered_mxnf4_linear(x, index, scale_qmap, output_code, input_code, weight_code, w_packed, w_scale_bytes,
-                         w_codes, w_scale):
+                         levels: Tuple[int, ...], w_codes, w_scale):
     """quantize_mx(x, lut4_to_int6, [-1], 64, 31, fp8_e5m3) -> linear_mx: the
     GEMV on nibble-packed weights for up to 16 rows, the reference-form ops
-    otherwise."""
+    otherwise. ``levels`` are the codebook's 16 int8 levels, read from
+    ``weight_code`` once when the graph is lowered, so no call copies device
+    memory to the host (a lowered graph can be captured in a HIP graph)."""
     xr = _rows(x)
     N, K = w_codes.shape
     if xr.shape[0] <= 16:
         sc = formats.classify(scale_qmap)
-        wt = gemm.NF4Weight(w_packed, w_scale_bytes, sc, gemm._levels_of(weight_code), N, K)
+        wt = gemm.NF4Weight(w_packed, w_scale_bytes, sc, bytes(levels), N, K)
         y = gemm.linear_nf4(xr, wt, index, scale_qmap)
     else:
         s, c = torch.ops.quantized_ops.quantize_mx(xr, index, [-1], 64, 31.0, False, scale_qmap, output_code)
@@ -412,9 +414,10 @@ def _insert(model: GraphModule, site: Site) -> Node:
         wp, sb = _bake_mxnf4(w, ws, _attr(model, k["scale_qmap"]))
         wpn = _const(model, graph, f"{name}_nf4_weight", wp)
         sbn = _const(model, graph, f"{name}_nf4_scale", sb)
+        levels = tuple(gemm._levels_of(_attr(model, k["weight_code"])))
         return graph.call_function(lowered_mxnf4_linear,
                                    (x, k["qmap"], k["scale_qmap"], k["output_code"], k["input_code"],
-                                    k["weight_code"], wpn, sbn, site.weight, site.weight_scale))
+                                    k["weight_code"], wpn, sbn, levels, site.weight, site.weight_scale))
 
 
 def _erase_unused(model: GraphModule, nodes: List[Node]) -> None:
@@ -502,7 +505,8 @@ class _SiteCheck(Interpreter):
                                          _arg(site.quantize, 3, "block_size"), bias)
         wp, sb = _bake_mxnf4(w, ws, env[k["scale_qmap"]])
         return lowered_mxnf4_linear(x, env[k["qmap"]], env[k["scale_qmap"]], env[k["output_code"]],
-                                    env[k["input_code"]], env[k["weight_code"]], wp, sb, w, ws)
+                                    env[k["input_code"]], env[k["weight_code"]], wp, sb,
+                                    tuple(gemm._levels_of(env[k["weight_code"]])), w, ws)
 
 
 def check_sites(model: GraphModule, args, kwargs=None):
