@@ -20,7 +20,9 @@ Options: --gpus N (1 only), --steps K, --warmup W, --no-cpu (skip the CPU
 baseline), --copy-calibration BYTES (run only a plain device copy, for
 rocprofv3 counter calibration), --profile-shapes R (run only, shape by shape
 in SHAPES order, R quantize launches then R GEMM launches, eagerly: dispatch
-order names the shape in a rocprofv3 counter run).
+order names the shape in a rocprofv3 counter run), --calibrate (run only
+the reference points: plain device copies and the vendor GEMMs at the
+config-2 shapes).
 """
 
 import argparse
@@ -442,6 +444,40 @@ def copy_calibration(nbytes: int):
     print(json.dumps({"copy_bytes": nbytes, "launches": 5}))
 
 
+def calibrate():
+    """Reference points on the box, not this build's kernels: a plain device
+    copy at three sizes (buffers rotated over 1 GiB, so the Infinity Cache
+    cannot serve them) and the vendor GEMMs (hipBLASLt FP8 through
+    ``torch._scaled_mm``, torch's bf16 ``linear``) at the config-2 shapes,
+    each from graph replays timed with HIP events."""
+    dev = torch.device("cuda:0")
+    out = {}
+    for mb in (16, 64, 256):
+        n = mb << 20
+        nb = max(2, (1 << 30) // n)
+        src = [torch.ones(n, dtype=torch.uint8, device=dev) for _ in range(nb)]
+        dst = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(nb)]
+        g = capture(lambda: [d.copy_(s_) for d, s_ in zip(dst, src)])
+        out[f"copy_{mb}MB_GBs"] = round(2 * n * nb / time_graph(g, 5) / 1e6, 1)
+        del g, src, dst
+        log(f"calibrate: copy {mb} MB done")
+    one = torch.ones((), device=dev)
+    for K, N in SHAPES:
+        gen = torch.Generator().manual_seed(7)
+        a = torch.randn(M, K, generator=gen).to(dev).to(torch.float8_e4m3fn)
+        b = torch.randn(N, K, generator=gen).to(dev).to(torch.float8_e4m3fn)
+        flop = 2.0 * M * N * K
+        g = capture(lambda: [torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+                             for _ in range(10)])
+        out[f"hipblaslt_fp8_{M}x{K}x{N}_TFLOPs"] = round(flop / (time_graph(g, 5) / 10) / 1e9, 1)
+        ab, bb = a.to(torch.bfloat16), b.to(torch.bfloat16)
+        g = capture(lambda: [torch.nn.functional.linear(ab, bb) for _ in range(10)])
+        out[f"torch_bf16_{M}x{K}x{N}_TFLOPs"] = round(flop / (time_graph(g, 5) / 10) / 1e9, 1)
+        del g
+        log(f"calibrate: GEMMs (K, N) = ({K}, {N}) done")
+    print(json.dumps(out), flush=True)
+
+
 def profile_shapes(reps: int):
     """The config-2 kernels shape by shape, for rocprofv3 counter runs."""
     import voyager_amd  # noqa: F401
@@ -475,6 +511,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0)
     ap.add_argument("--profile-shapes", type=int, default=0)
+    ap.add_argument("--calibrate", action="store_true")
     ap.add_argument("--config", type=int, default=2,
                     help="2 (default): the headline line; 1, 3, 4, 5: that config's measurements")
     args = ap.parse_args()
@@ -487,6 +524,9 @@ def main():
         return
     if args.profile_shapes:
         profile_shapes(args.profile_shapes)
+        return
+    if args.calibrate:
+        calibrate()
         return
     if args.config in (1, 3, 4, 5):
         fn = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config]

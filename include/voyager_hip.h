@@ -317,6 +317,53 @@ typedef struct vh_kivi_desc {
  * graph (quant_folding.py:2391-2547 read path, eager attention). */
 int vh_kivi_attention(const vh_kivi_desc* desc, vh_stream_t stream);
 
+/* ------------------------------------------------------- outliers (CSR)
+ * The outlier path of an MX linear: activations whose magnitude reaches a
+ * threshold are kept exact in a CSR stream of fixed capacity and multiplied
+ * by the decoded weight beside the quantized GEMM.  CSR arrays: data
+ * (values), indices (int32 columns), indptr (int32 row pointers, rows + 1
+ * per matrix); capacity slots past the stored entries hold data 0 and index
+ * -1.  A matrix holding more entries than its capacity keeps the first ones
+ * in row-major order, and its row pointers are clamped at the capacity. */
+
+/* filter_outlier (ops/quantized.py:1286-1374, _pad_csr :1292-1319) and the
+ * filter of quantize_mx_outlier (:1396-1458): for each of `batch` dense row-major
+ * [rows, cols] matrices of x (dtype VH_BF16 / VH_F16 / VH_F32), the
+ * non-zero elements with |x| >= threshold (threshold already rounded to the
+ * dtype, as torch compares a tensor with a Python float) form a CSR of
+ * max_nnz slots per matrix (data in the input dtype, [batch, max_nnz];
+ * indices [batch, max_nnz]; indptr [batch, rows + 1], plus indptr_offset);
+ * inliers = x with every element whose magnitude reaches the threshold
+ * zeroed. Three launches: row counts (and the inliers), a scan per matrix,
+ * the fill. */
+int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols, float threshold,
+                      int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
+                      void* inliers, vh_stream_t stream);
+
+/* slice_csr_tensor (ops/quantized.py:1493-1545) of one CSR matrix with
+ * `rows` rows and `cap` slots (indptr[0] == 0), to out_cap slots.
+ * dim 0: rows [start, end), pointers rebased to 0.  dim 1: columns
+ * [start, end), entries compacted row by row in order and their columns
+ * shifted by -start.  out_indptr has end - start + 1 (dim 0) or rows + 1
+ * (dim 1) entries. */
+int vh_slice_csr(const void* data, int32_t dtype, const int32_t* indices, const int32_t* indptr, int64_t rows,
+                 int64_t cap, int32_t dim, int64_t start, int64_t end, int64_t out_cap, void* out_data,
+                 int32_t* out_indices, int32_t* out_indptr, vh_stream_t stream);
+
+/* spmm_csr (ops/quantized.py:1567-1645): for each of `batch` CSR matrices
+ * ([rows, K], `cap` slots; row pointers rebased on their first, clamped to
+ * [0, cap] and made non-decreasing as the reference's cummax; columns
+ * clamped to [0, K - 1]) times the dense B (b_layout 0: "kc", stored
+ * [N, K]; 1: "ck", stored [K, N]; b_batch_stride elements between batches,
+ * 0: one B for all), out[b, r, n] = sum over the row's entries, in order,
+ * of float32(data) * float32(B[k, n]), plus base[b, r, n] (float32,
+ * optional: the GEMM product it adds to), rounded once to out_dtype.
+ * work: int32 [batch, rows + 1] for the rebased row pointers. */
+int vh_spmm_csr(const void* data, int32_t data_dtype, const int32_t* indices, const int32_t* indptr, int64_t batch,
+                int64_t rows, int64_t cap, const void* B, int32_t b_dtype, int32_t b_layout, int64_t K, int64_t N,
+                int64_t b_batch_stride, const float* base, void* out, int32_t out_dtype, int32_t* work,
+                vh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

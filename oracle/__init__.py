@@ -29,4 +29,12 @@ Parity pins (each checked in ``tests/test_oracle_pins.py``):
 * ``quantize_affine``: hand-computed blocks and a float64 restatement.
 * GEMMs (``linear``/``linear_mx``/``matmul_mx``): float64 numpy matmul of
   the decoded operands.
+* Outliers (``filter_outlier``, ``quantize_mx_outlier``, ``slice_csr_tensor``,
+  ``spmm_csr`` and the CSR term of ``linear_mx``/``matmul_mx``; checked in
+  ``tests/test_oracle_outliers.py``): the CSR against a brute-force
+  row-major scan in plain Python (slot order, capacity cut, row-pointer
+  clamp, padding), dense reconstruction (CSR + inliers == input), the
+  threshold compared after rounding to the input dtype, slices against
+  slices of the dense matrix, and the products against float64 numpy
+  matmul of the densified CSR.
 """

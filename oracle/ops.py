@@ -252,9 +252,9 @@ def _with_xk(layout):
 
 def linear_mx(input, weight, bias=None, input_scale=None, weight_scale=None, block_size=None,
               input_code=None, weight_code=None, alpha=None, layout=LINEAR_LAYOUT,
-              out_dtype=None):
-    """``ops/quantized.py:651-723`` without the outlier (CSR) term."""
-    _, _, so = _parse_layout(layout)
+              out_dtype=None, A_data=None, A_indices=None, A_indptr=None):
+    """``ops/quantized.py:651-723``, the outlier (CSR) term included."""
+    _, sw, so = _parse_layout(layout)
     x = dequantize_mx_parts(input, input_scale, input_code, block_size)
     w = dequantize_mx_parts(weight, weight_scale, weight_code, block_size)
     dtype = x.dtype if out_dtype is None else out_dtype
@@ -264,15 +264,18 @@ def linear_mx(input, weight, bias=None, input_scale=None, weight_scale=None, blo
         out = out * alpha
         if bias is not None:
             out = out + bias
+    if A_data is not None:
+        out = out + spmm_csr(A_data, A_indices, A_indptr, weight, weight_scale, weight_code, block_size,
+                             sw, out_dtype=acc)
     out = out.to(dtype)
     return out.mT.contiguous() if so != "xk" else out
 
 
 def matmul_mx(input, other, input_scale=None, weight_scale=None, block_size=None,
               input_code=None, weight_code=None, alpha=None, layout=MATMUL_LAYOUT,
-              out_dtype=None):
-    """``ops/quantized.py:742-805`` without the outlier (CSR) term."""
-    _, _, so = _parse_layout(layout)
+              out_dtype=None, A_data=None, A_indices=None, A_indptr=None):
+    """``ops/quantized.py:742-805``, the outlier (CSR) term included."""
+    _, sw, so = _parse_layout(layout)
     x = dequantize_mx_parts(input, input_scale, input_code, block_size)
     w = dequantize_mx_parts(other, weight_scale, weight_code, block_size)
     dtype = x.dtype if out_dtype is None else out_dtype
@@ -280,8 +283,111 @@ def matmul_mx(input, other, input_scale=None, weight_scale=None, block_size=None
     out = matmul(x, w, layout=_with_xk(layout), out_dtype=acc)
     if alpha is not None:
         out = out * alpha
+    if A_data is not None:
+        out = out + spmm_csr(A_data, A_indices, A_indptr, other, weight_scale, weight_code, block_size,
+                             sw, out_dtype=acc)
     out = out.to(dtype)
     return out.mT.contiguous() if so != "xk" else out
+
+
+# ------------------------------------------------------------ outliers (CSR)
+
+def pad_csr(values, col_indices, crow_indices, max_nnz):
+    """``_pad_csr``, ``ops/quantized.py:1292-1319``: a CSR stream padded to
+    ``max_nnz`` slots (data 0, index -1), or cut to its first ``max_nnz``
+    entries with the row pointers clamped there.  Returns
+    ``(data, indices, crow_indices)``."""
+    nse = int(crow_indices[-1])
+    if max_nnz >= nse:
+        data = torch.nn.functional.pad(values, (0, max_nnz - nse), mode="constant", value=0)
+        indices = torch.nn.functional.pad(col_indices, (0, max_nnz - nse), mode="constant", value=-1)
+        return data, indices, crow_indices
+    return values[:max_nnz], col_indices[:max_nnz], crow_indices.clamp(max=max_nnz)
+
+
+def filter_outlier(input, threshold, max_pct=0.01):
+    """``ops/quantized.py:1322-1374``: ``(data, indices, indptr, inliers)``,
+    the elements with ``|x| >= threshold`` of each matrix (last two dims) as
+    a padded CSR of ``int(rows * cols * max_pct)`` slots."""
+    is_outlier = torch.abs(input) >= threshold
+    inliers = torch.where(is_outlier, 0, input)
+    outliers = torch.where(is_outlier, input, 0)
+    batch_shape, mat_shape = input.shape[:-2], input.shape[-2:]
+    max_nnz = int(math.prod(mat_shape) * max_pct)
+    per_matrix = outliers.reshape(int(math.prod(batch_shape)), *mat_shape)
+    parts = []
+    for mat in per_matrix:
+        csr = mat.to_sparse_csr()
+        parts.append(pad_csr(csr.values(), csr.col_indices().to(torch.int32),
+                             csr.crow_indices().to(torch.int32), max_nnz))
+    data = torch.stack([p[0] for p in parts]).reshape(*batch_shape, -1)
+    indices = torch.stack([p[1] for p in parts]).reshape(*batch_shape, -1)
+    indptr = torch.stack([p[2] for p in parts]).reshape(*batch_shape, -1)
+    return data, indices, indptr, inliers
+
+
+def quantize_mx_outlier(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
+                        scale_qmap=None, output_code=None, threshold=None, max_pct=0.01, indptr_offset=0):
+    """``ops/quantized.py:1405-1458``: ``(data, indices, indptr, scale,
+    inliers)``."""
+    data, indices, indptr, inliers = filter_outlier(input, threshold, max_pct)
+    if indptr_offset:
+        indptr = indptr + indptr_offset
+    scale, codes = quantize_mx(inliers, qmap, axes, block_size, quant_max, force_scale_power_of_two,
+                               scale_qmap, output_code)
+    return data, indices, indptr, scale, codes
+
+
+def slice_csr_tensor(data, indices, indptr, dim=0, start=None, end=None, size_factor=1.0):
+    """``ops/quantized.py:1500-1545``: rows (dim 0) or columns (dim 1)
+    ``[start, end)`` of one CSR matrix, padded to ``int(len(data) *
+    size_factor)`` slots."""
+    dim = dim + 2 if dim < 0 else dim
+    if dim not in (0, 1):
+        raise ValueError(f"Cannot slice sparse CSR matrix along dim {dim}")
+    if dim == 0:
+        first, last = int(indptr[start]), int(indptr[end])
+        new_indptr = indptr[start:end + 1] - first
+        values, cols = data[first:last], indices[first:last]
+    else:
+        keep = (indices >= start) & (indices < end)
+        lengths = (indptr[1:] - indptr[:-1]).to(torch.int64)
+        nse = int(indptr[-1])
+        counts = torch.segment_reduce(keep[:nse].to(torch.float32), "sum", lengths=lengths).to(indptr.dtype)
+        new_indptr = torch.empty_like(indptr)
+        new_indptr[0] = 0
+        new_indptr[1:] = counts.cumsum(0).to(indptr.dtype)
+        values, cols = data[keep], indices[keep] - start
+    return pad_csr(values, cols, new_indptr, int(data.shape[0] * size_factor))
+
+
+def spmm_csr(data, indices, indptr, B, B_scale=None, B_code=None, block_size=None, weight_layout="kc",
+             out_dtype=None):
+    """``ops/quantized.py:1574-1645``: the CSR matrices (batch dims leading)
+    times ``B`` decoded (code, then block scale), in float32 through
+    ``torch.sparse.mm``; rows rebased on their first pointer, clamped and made
+    non-decreasing, columns clamped into ``B``."""
+    assert weight_layout in ("kc", "ck"), weight_layout
+    B = dequantize_mx_parts(B, B_scale, B_code, block_size)
+    if weight_layout == "kc":
+        B = B.mT
+    batch_shape = indptr.shape[:-1]
+    nb = int(math.prod(batch_shape))
+    indptr = indptr.reshape(-1, indptr.shape[-1])
+    indices = indices.reshape(-1, indices.shape[-1])
+    data = data.reshape(-1, data.shape[-1])
+    if B.ndim > 2:
+        B = B.reshape(nb, B.shape[-2], B.shape[-1])
+    outs = []
+    for i in range(nb):
+        Bi = B[i] if B.ndim == 3 else B
+        crow = (indptr[i] - indptr[i][0]).clamp(0, data.shape[-1])
+        crow = torch.cummax(crow, 0).values
+        end = int(crow[-1])
+        csr = torch.sparse_csr_tensor(crow, indices[i, :end].clamp(0, Bi.shape[0] - 1), data[i, :end],
+                                      dtype=torch.float32, size=(indptr[i].numel() - 1, Bi.shape[0]))
+        outs.append(torch.sparse.mm(csr, Bi.to(torch.float32)).to(B.dtype if out_dtype is None else out_dtype))
+    return torch.stack(outs).reshape(*batch_shape, -1, B.shape[-1])
 
 
 def per_tensor_scale(x, quant_max):

@@ -192,10 +192,9 @@ def _decode(x, scale, code, block_size):
 
 
 def _mx_common(kind, x, w, bias, input_scale, weight_scale, block_size, input_code, weight_code, alpha, A_data,
-               layout, out_dtype):
-    _require_gpu(x, w, bias, input_scale, weight_scale, input_code, weight_code, alpha)
-    if A_data is not None:
-        raise NotImplementedError(f"quantized_ops.{kind}: the outlier (CSR) term is not supported on the GPU yet")
+               A_indices, A_indptr, layout, out_dtype):
+    _require_gpu(x, w, bias, input_scale, weight_scale, input_code, weight_code, alpha, A_data, A_indices,
+                 A_indptr)
     xd = _decode(x, input_scale, input_code, block_size)
     wd = _decode(w, weight_scale, weight_code, block_size)
     dtype = xd.dtype if out_dtype is None else out_dtype
@@ -204,7 +203,18 @@ def _mx_common(kind, x, w, bias, input_scale, weight_scale, block_size, input_co
     acc_bias = bias if kind == "linear_mx" else None
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise NotImplementedError(f"quantized_ops.{kind}: decoded operands must be bfloat16 on the GPU")
-    y = gemm_bf16(a, b, dtype, acc_bias, alpha)
+    if A_data is None:
+        y = gemm_bf16(a, b, dtype, acc_bias, alpha)
+    else:
+        # The outlier product (ops/quantized.py:709-720, 789-802): the GEMM's
+        # float32 result (alpha and bias applied) is the base the CSR product
+        # of the decoded weight adds to before the one rounding to dtype.
+        from .sparse import spmm_into
+
+        if torch.promote_types(dtype, torch.float32) != torch.float32:
+            raise NotImplementedError(f"quantized_ops.{kind}: {dtype} output with an outlier term")
+        y32 = gemm_bf16(a, b, torch.float32, acc_bias, alpha)
+        y = spmm_into(A_data, A_indices, A_indptr, wd, wl, dtype, base=y32)
     return y.mT.contiguous() if out_l != "xk" else y
 
 
@@ -212,14 +222,14 @@ def _linear_mx_cuda(input, weight, bias=None, *, input_scale=None, weight_scale=
                     input_code=None, weight_code=None, alpha=None, A_data=None, A_indices=None, A_indptr=None,
                     layout=LINEAR_LAYOUT, out_dtype=None):
     return _mx_common("linear_mx", input, weight, bias, input_scale, weight_scale, block_size, input_code,
-                      weight_code, alpha, A_data, layout, out_dtype)
+                      weight_code, alpha, A_data, A_indices, A_indptr, layout, out_dtype)
 
 
 def _matmul_mx_cuda(self, other, *, input_scale=None, weight_scale=None, block_size=None, input_code=None,
                     weight_code=None, alpha=None, A_data=None, A_indices=None, A_indptr=None,
                     layout=MATMUL_LAYOUT, out_dtype=None):
     return _mx_common("matmul_mx", self, other, None, input_scale, weight_scale, block_size, input_code,
-                      weight_code, alpha, A_data, layout, out_dtype)
+                      weight_code, alpha, A_data, A_indices, A_indptr, layout, out_dtype)
 
 
 lib.impl("linear_mx", _linear_mx_cuda, "CUDA")

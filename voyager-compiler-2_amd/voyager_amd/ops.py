@@ -2,7 +2,8 @@
 
 Defines the namespace with the reference's schema strings, byte for byte
 (``src/voyager_compiler/ops/quantized.py:147, 449-453, 518-522, 651-658,
-742-748, 958-962, 1070-1075, 1118-1121, 1218-1222``; ``ops/layout.py:221-228``),
+742-748, 958-962, 1070-1075, 1118-1121, 1218-1222, 1286-1289, 1396-1402,
+1493-1497, 1567-1571``; ``ops/layout.py:221-228``),
 a fake (meta) kernel for each op so FX shape propagation works, and a CUDA-key
 kernel (PyTorch-ROCm routes HIP tensors there) that validates arguments,
 allocates outputs with torch's caching allocator and launches the HIP library
@@ -82,6 +83,27 @@ SCHEMAS = {
     "matmul": (
         f'matmul(Tensor self, Tensor other, *, str layout="{MATMUL_LAYOUT}", '
         "ScalarType? out_dtype=None) -> Tensor"
+    ),
+    "filter_outlier": (
+        "filter_outlier(Tensor input, float threshold, float max_pct=0.01) "
+        "-> (Tensor, Tensor, Tensor, Tensor)"
+    ),
+    "quantize_mx_outlier": (
+        "quantize_mx_outlier(Tensor self, Tensor qmap, SymInt[] axes, "
+        "int block_size, float quant_max, bool force_scale_power_of_two=False, "
+        "Tensor scale_qmap=None, Tensor output_code=None, float? threshold=None, "
+        "float max_pct=0.01, SymInt indptr_offset=0) "
+        "-> (Tensor, Tensor, Tensor, Tensor, Tensor)"
+    ),
+    "slice_csr_tensor": (
+        "slice_csr_tensor(Tensor data, Tensor indices, Tensor indptr, int dim=0, "
+        "SymInt? start=None, SymInt? end=None, float size_factor=1.0) "
+        "-> (Tensor, Tensor, Tensor)"
+    ),
+    "spmm_csr": (
+        "spmm_csr(Tensor data, Tensor indices, Tensor indptr, Tensor B, "
+        "Tensor? B_scale=None, Tensor? B_code=None, int? block_size=None, "
+        'str weight_layout="kc", *, ScalarType? out_dtype=None) -> Tensor'
     ),
 }
 
