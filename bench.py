@@ -22,7 +22,8 @@ rocprofv3 counter calibration), --profile-shapes R (run only, shape by shape
 in SHAPES order, R quantize launches then R GEMM launches, eagerly: dispatch
 order names the shape in a rocprofv3 counter run), --calibrate (run only
 the reference points: plain device copies and the vendor GEMMs at the
-config-2 shapes).
+config-2 shapes), --outliers (the outlier (CSR) path: the filter's
+bandwidth and the config-1 linear with its outlier stream).
 """
 
 import argparse
@@ -230,6 +231,95 @@ def bench_config1(args):
                      "note": "k_gemm_mxi8: codes decoded to bf16 once per block tile, bf16 MFMA (2.5 PF); K split 4 ways + k_split_reduce"},
             "quantize_mx": {"us": round(q_ms * 1e3, 2), "GB/s": round(qbytes / (q_ms * 1e-3) / 1e9, 1)},
             "config": {"workload": "cfg1: MXINT8 bs=16 pot, X[256,4096] . W[4096,4096]^T"}}
+
+
+def bench_outliers(args):
+    """The outlier (CSR) path, not a headline config: (1) vh_filter_outlier
+    on a [2048, 14336] prefill activation with config 1's outlier pattern
+    (0.1% of entries x20), inputs rotated over > 256 MB; (2) the config-1
+    linear as a converted graph with an outlier spec runs it:
+    quantize_mx_outlier (threshold 5, a 1% stream) + linear_mx with the CSR
+    term, against quantize_mx + linear_mx without it; the spmm_csr of the
+    stream with the decoded weight alone; the oracle's step on the host."""
+    import voyager_amd  # noqa: F401
+    from voyager_amd import formats, sparse
+
+    Q = torch.ops.quantized_ops
+    dev = torch.device("cuda:0")
+
+    def outlier_input(rows, cols, seed):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(rows, cols, generator=g)
+        return torch.where(torch.rand(rows, cols, generator=g) < 0.001, x * 20, x).bfloat16(), g
+
+    # (1) the filter, HBM-bound
+    R, C = 2048, 14336
+    xf, _ = outlier_input(R, C, 0)
+    nbuf = max(2, -(-2 * MALL_BYTES // (R * C * 2)))
+    xs = [xf.to(dev) for _ in range(nbuf)]
+    gf = capture(lambda: [sparse.filter_outlier(x, 5.0, 0.01) for x in xs])
+    f_ms = time_graph(gf, 5) / nbuf
+    cap = int(R * C * 0.01)
+    nnz = int(sparse.filter_outlier(xs[0], 5.0, 0.01)[2][-1])
+    fbytes = R * C * 2 * 2 + cap * 6 + (R + 1) * 4
+    del gf, xs
+
+    # (2) the config-1 linear with the outlier stream
+    x, g = outlier_input(256, 4096, 0)
+    w = (torch.randn(4096, 4096, generator=g) * 0.02).bfloat16()
+    tab = formats.quantization_map("int8", dev)
+    xd, wdev = x.to(dev), w.to(dev)
+    ws, wc = Q.quantize_mx(wdev, tab, [-1], 16, 127.0, True)
+    st = {}
+
+    def with_csr():
+        d, i, p, s_, c_ = Q.quantize_mx_outlier(xd, tab, [-1], 16, 127.0, True, threshold=5.0, max_pct=0.01)
+        st["csr"] = (d, i, p)
+        st["y"] = Q.linear_mx(c_, wc, input_scale=s_, weight_scale=ws, block_size=16, A_data=d, A_indices=i,
+                              A_indptr=p)
+
+    def without():
+        s_, c_ = Q.quantize_mx(xd, tab, [-1], 16, 127.0, True)
+        st["y0"] = Q.linear_mx(c_, wc, input_scale=s_, weight_scale=ws, block_size=16)
+
+    g1 = capture(lambda: [with_csr() for _ in range(10)])
+    t_csr = time_graph(g1, 5) / 10
+    g0 = capture(lambda: [without() for _ in range(10)])
+    t_plain = time_graph(g0, 5) / 10
+    wdec = Q.dequantize_mx(wc, ws, 16)
+    base = torch.zeros(256, 4096, dtype=torch.float32, device=dev)
+    d, i, p = st["csr"]
+    gs = capture(lambda: [sparse.spmm_into(d, i, p, wdec, "kc", torch.bfloat16, base=base) for _ in range(10)])
+    t_spmm = time_graph(gs, 5) / 10
+    nnz1 = int(p[-1])
+    res = {"metric": "outlier (CSR) path: filter GB/s, step us", "unit": "us",
+           "filter": {"shape": [R, C], "stored_outliers": nnz, "capacity": cap, "us": round(f_ms * 1e3, 2),
+                      "GB/s": round(fbytes / (f_ms * 1e-3) / 1e9, 1),
+                      "hbm_frac": round(fbytes / (f_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
+                      "bytes": fbytes, "note": "x read + inliers written + capacity slots (6 B) + row pointers"},
+           "cfg1_step": {"with_csr_us": round(t_csr * 1e3, 2), "without_us": round(t_plain * 1e3, 2),
+                         "stored_outliers": nnz1, "spmm_us": round(t_spmm * 1e3, 2),
+                         "note": "ref-form ops as a converted graph runs them: quantize_mx_outlier + linear_mx "
+                                 "(decode + bf16 GEMM to fp32 + CSR product added before the bf16 rounding)"},
+           "config": {"workload": "outliers: cfg1 X[256,4096] (0.1% x20) . W[4096,4096]^T, threshold 5, "
+                                  "1% stream; filter on X[2048,14336]"}}
+    if not args.no_cpu:
+        from oracle import ops as O  # the CPU baseline only
+
+        tabc = tab.cpu()
+        wsc, wcc = O.quantize_mx(w, tabc, [-1], 16, 127.0, True)
+        times = []
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < 10.0 or len(times) < 3:
+            t0 = time.perf_counter()
+            dd, ii, pp, sc, cc = O.quantize_mx_outlier(x, tabc, [-1], 16, 127.0, True, threshold=5.0, max_pct=0.01)
+            O.linear_mx(cc, wcc, input_scale=sc, weight_scale=wsc, block_size=16, A_data=dd, A_indices=ii,
+                        A_indptr=pp)
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        res["cpu_baseline"] = {"us": round(times[len(times) // 2] * 1e6, 1), "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"{len(times)} cfg1 outlier steps of the oracle, median"}
+    return res
 
 
 def bench_config3(args):
@@ -512,6 +602,7 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0)
     ap.add_argument("--profile-shapes", type=int, default=0)
     ap.add_argument("--calibrate", action="store_true")
+    ap.add_argument("--outliers", action="store_true")
     ap.add_argument("--config", type=int, default=2,
                     help="2 (default): the headline line; 1, 3, 4, 5: that config's measurements")
     args = ap.parse_args()
@@ -527,6 +618,9 @@ def main():
         return
     if args.calibrate:
         calibrate()
+        return
+    if args.outliers:
+        print(json.dumps(bench_outliers(args)), flush=True)
         return
     if args.config in (1, 3, 4, 5):
         fn = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config]

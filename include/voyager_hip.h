@@ -334,11 +334,18 @@ int vh_kivi_attention(const vh_kivi_desc* desc, vh_stream_t stream);
  * max_nnz slots per matrix (data in the input dtype, [batch, max_nnz];
  * indices [batch, max_nnz]; indptr [batch, rows + 1], plus indptr_offset);
  * inliers = x with every element whose magnitude reaches the threshold
- * zeroed. Three launches: row counts (and the inliers), a scan per matrix,
- * the fill. */
+ * zeroed.  Three launches: segment counts (and the inliers), a scan per
+ * matrix, the fill.  work: vh_filter_outlier_workspace_bytes(batch, rows,
+ * cols) bytes of device memory, 16-byte aligned (segment counts and the
+ * outliers each segment keeps for the fill). */
 int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols, float threshold,
                       int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
-                      void* inliers, vh_stream_t stream);
+                      void* inliers, void* work, int64_t work_bytes, vh_stream_t stream);
+
+/* Workspace bytes vh_filter_outlier needs.  No counterpart in the
+ * reference, whose CPU filter builds each matrix's CSR with
+ * Tensor.to_sparse_csr. */
+int64_t vh_filter_outlier_workspace_bytes(int64_t batch, int64_t rows, int64_t cols);
 
 /* slice_csr_tensor (ops/quantized.py:1493-1545) of one CSR matrix with
  * `rows` rows and `cap` slots (indptr[0] == 0), to out_cap slots.

@@ -123,6 +123,33 @@ VH_DEV int64_t param_offset(const vh_param& p, const Shape& s, int64_t flat) {
 // One thread: VEC consecutive elements.
 constexpr int VEC = 8;
 
+// Parameter values of elements base .. base + VEC - 1 (those below n).  The
+// index is decomposed once per group; within a row of the innermost dim the
+// offsets step by the innermost block, and a group whose elements share one
+// offset (a block of >= 8 along the innermost dim) loads it once.
+VH_DEV void param_values(const vh_param& p, const Shape& s, int64_t base, int64_t n, float* v) {
+  const int last = s.ndim - 1;
+  const int64_t L = last >= 0 ? s.dim[last] : 1;
+  const int64_t c0 = base % L;
+  if (last >= 0 && c0 + VEC <= L && base + VEC <= n && L < (1ll << 31)) {
+    const int64_t o0 = param_offset(p, s, base);
+    const int32_t dv = (int32_t)p.div[last], q0 = (int32_t)c0 / dv;
+    const int32_t q7 = ((int32_t)c0 + VEC - 1) / dv;
+    if (q7 == q0 || p.stride[last] == 0) {
+      const float v0 = load_any(p.ptr, p.dtype, o0);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) v[j] = v0;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        v[j] = load_any(p.ptr, p.dtype, o0 + (int64_t)(((int32_t)c0 + j) / dv - q0) * p.stride[last]);
+    }
+    return;
+  }
+  for (int j = 0; j < VEC; ++j)
+    if (base + j < n) v[j] = load_any(p.ptr, p.dtype, param_offset(p, s, base + j));
+}
+
 template <int KIND>
 __global__ void __launch_bounds__(256)
 k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_param sp, vh_param zp,
@@ -154,12 +181,8 @@ k_quantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_p
     sv[j] = s0;
     zv[j] = z0;
   }
-  if (sp.ptr && !sp.scalar)
-    for (int j = 0; j < VEC; ++j)
-      if (base + j < n) sv[j] = load_any(sp.ptr, sp.dtype, param_offset(sp, shape, base + j));
-  if (zp.ptr && !zp.scalar)
-    for (int j = 0; j < VEC; ++j)
-      if (base + j < n) zv[j] = load_any(zp.ptr, zp.dtype, param_offset(zp, shape, base + j));
+  if (sp.ptr && !sp.scalar) param_values(sp, shape, base, n, sv);
+  if (zp.ptr && !zp.scalar) param_values(zp, shape, base, n, zv);
   const bool has_s = sp.ptr != nullptr, has_z = zp.ptr != nullptr;
   uint32_t res[VEC];
   float outv[VEC];
@@ -745,30 +768,60 @@ k_dequantize(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh
   if (has_out) stage_steps(fout, lds_out);
   int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
   if (base >= n) return;
-  float sv = 1.0f, zv = 0.0f;
-  if (sp.ptr && sp.scalar) sv = load_any(sp.ptr, sp.dtype, 0);
-  if (zp.ptr && zp.scalar) zv = load_any(zp.ptr, zp.dtype, 0);
+  const bool full = base + VEC <= n;
+  float sv[VEC], zv[VEC];
+  const float s0 = (sp.ptr && sp.scalar) ? load_any(sp.ptr, sp.dtype, 0) : 1.0f;
+  const float z0 = (zp.ptr && zp.scalar) ? load_any(zp.ptr, zp.dtype, 0) : 0.0f;
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
-    int64_t i = base + j;
-    if (i >= n) break;
-    float v;
-    if (x_dtype == VH_U8) {
-      v = fmt_decode_k<KIN>(((const uint8_t*)x)[i], fin, lds_in);
-    } else {
-      v = load_any(x, x_dtype, i);
-      if constexpr (KIN != K_NONE) {
-        uint32_t b = x_dtype == VH_BF16 ? (uint32_t)((const uint16_t*)x)[i] : f2bf(v);
-        v = round_to(fmt_value_k<KIN>(b, fin, lds_in), x_dtype);
-      }
+    sv[j] = s0;
+    zv[j] = z0;
+  }
+  if (sp.ptr && !sp.scalar) param_values(sp, shape, base, n, sv);
+  if (zp.ptr && !zp.scalar) param_values(zp, shape, base, n, zv);
+  // inputs: bf16 patterns (16-byte loads when the group is whole)
+  uint32_t xb[VEC];
+  if (x_dtype == VH_BF16 && full) {
+    const uint4 raw = ld_stream16((const uint16_t*)x + base);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xb[2 * j] = w[j] & 0xffffu;
+      xb[2 * j + 1] = w[j] >> 16;
     }
-    float s = sv, z = zv;
-    if (sp.ptr && !sp.scalar) s = load_any(sp.ptr, sp.dtype, param_offset(sp, shape, i));
-    if (zp.ptr && !zp.scalar) z = load_any(zp.ptr, zp.dtype, param_offset(zp, shape, i));
-    if (zp.ptr) v = round_to(v - z, cdt);
-    if (sp.ptr) v = round_to(v * s, cdt);
-    if (has_out) v = round_to(fmt_value(f2bf(v), fout, lds_out), cdt);
-    store_any(out, out_dtype, i, v);
+  }
+  float outv[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const int64_t i = base + j;
+    float v = 0.0f;
+    if (full || i < n) {
+      if (x_dtype == VH_U8) {
+        v = fmt_decode_k<KIN>(((const uint8_t*)x)[i], fin, lds_in);
+      } else {
+        const bool vec = x_dtype == VH_BF16 && full;
+        v = vec ? bf2f(xb[j]) : load_any(x, x_dtype, i);
+        if constexpr (KIN != K_NONE) {
+          const uint32_t b = vec ? xb[j] : x_dtype == VH_BF16 ? (uint32_t)((const uint16_t*)x)[i] : f2bf(v);
+          v = round_to(fmt_value_k<KIN>(b, fin, lds_in), x_dtype);
+        }
+      }
+      if (zp.ptr) v = round_to(v - zv[j], cdt);
+      if (sp.ptr) v = round_to(v * sv[j], cdt);
+      if (has_out) v = round_to(fmt_value(f2bf(v), fout, lds_out), cdt);
+    }
+    outv[j] = v;
+  }
+  if (out_dtype == VH_BF16 && full) {
+    uint4 pk;
+    pk.x = f2bf(outv[0]) | (f2bf(outv[1]) << 16);
+    pk.y = f2bf(outv[2]) | (f2bf(outv[3]) << 16);
+    pk.z = f2bf(outv[4]) | (f2bf(outv[5]) << 16);
+    pk.w = f2bf(outv[6]) | (f2bf(outv[7]) << 16);
+    st_stream16((uint16_t*)out + base, pk);
+  } else {
+    for (int j = 0; j < VEC; ++j)
+      if (base + j < n) store_any(out, out_dtype, base + j, outv[j]);
   }
 }
 

@@ -9,14 +9,17 @@
 // All of it is integer and byte work bounded by HBM (the filter) or by the
 // gather of one B value per stored entry and output column (the product),
 // so nothing here is shaped for MFMA:
-//  - filter: one wave per matrix row streams the row twice (count, then
-//    fill), with ballot + mbcnt ranks giving every entry its slot; a scan
-//    per matrix between the two turns row counts into row pointers, clamped
-//    at the capacity as _pad_csr does.  Capacity slots past the stored
-//    entries are padded by extra workgroups of the fill launch.
+//  - filter: one wave per 2048-element row segment writes the inliers,
+//    counts the segment's stored outliers (ballot + mbcnt ranks) and keeps
+//    the first 16 in a workspace; a scan per matrix turns segment counts
+//    into slot starts and row pointers, clamped at the capacity as _pad_csr
+//    does; the fill copies the kept entries to their slots, re-reading only
+//    segments with more.  Capacity slots past the stored entries are padded
+//    by extra workgroups of the fill launch.
 //  - column slice: the same count / scan / fill over each row's segment.
 //  - product: a workgroup stages NT columns of B (all of K, 16- or 32-bit
-//    as stored, rows padded against bank conflicts) in LDS; each lane owns
+//    as stored, 16-byte loads, rows padded 16 bytes so the NT lanes that
+//    gather one column of the tile hit different banks) in LDS; each lane owns
 //    one (row, column) pair and sums its row's entries in stored order in
 //    float32, so 64 / NT rows share a wave and NT lanes read each entry
 //    (one address per NT lanes).
@@ -93,7 +96,36 @@ __device__ __forceinline__ int64_t block_scan(int64_t v, int64_t* s_wave, int64_
 }
 
 // ------------------------------------------------------------ filter
-// Elements per lane per step: 8 bytes when the row length allows.
+// A row is cut into segments of SEG elements, one wave each, so a prefill
+// activation gives tens of thousands of waves.  Pass 1 writes the inliers,
+// counts each segment's stored outliers and keeps up to SEG_STAGE of them
+// (value bits and column) in the workspace; the scan turns counts into slot
+// starts; pass 3 copies the kept outliers to their slots, re-reading only
+// segments that held more than SEG_STAGE.
+constexpr int SEG = 2048;
+constexpr int SEG_STAGE = 16;
+constexpr int SCAN_ITEMS = 16;
+
+struct FilterWork {
+  int32_t* seg;   // [nseg + 1] counts, then slot starts (seg[nseg]: the total)
+  uint32_t* val;  // [nseg][SEG_STAGE] value bits
+  int32_t* col;   // [nseg][SEG_STAGE] columns
+};
+
+__host__ __device__ inline int64_t filter_work_bytes_per_matrix(int64_t nseg) {
+  return ((nseg + 1) * 4 + 15) / 16 * 16 + nseg * SEG_STAGE * 8;
+}
+
+__device__ __forceinline__ FilterWork filter_work(void* work, int64_t b, int64_t nseg) {
+  uint8_t* p = (uint8_t*)work + b * filter_work_bytes_per_matrix(nseg);
+  FilterWork w;
+  w.seg = (int32_t*)p;
+  w.val = (uint32_t*)(p + ((nseg + 1) * 4 + 15) / 16 * 16);
+  w.col = (int32_t*)(w.val + nseg * SEG_STAGE);
+  return w;
+}
+
+// EPV elements of a lane's 16-byte chunk (or one element when EPV == 1).
 template <int DT, int EPV>
 struct Chunk {
   uint32_t v[EPV];
@@ -105,11 +137,16 @@ __device__ __forceinline__ Chunk<DT, EPV> load_chunk(const raw_t<DT>* p) {
   if constexpr (EPV == 1) {
     c.v[0] = p[0];
   } else {
-    const uint2 u = *(const uint2*)p;
-    if constexpr (DT == VH_F32) {
-      c.v[0] = u.x, c.v[1] = u.y;
-    } else {
-      c.v[0] = u.x & 0xffffu, c.v[1] = u.x >> 16, c.v[2] = u.y & 0xffffu, c.v[3] = u.y >> 16;
+    const uint4 u = ld_stream16(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (DT == VH_F32) {
+        c.v[k] = w[k];
+      } else {
+        c.v[2 * k] = w[k] & 0xffffu;
+        c.v[2 * k + 1] = w[k] >> 16;
+      }
     }
   }
   return c;
@@ -120,42 +157,215 @@ __device__ __forceinline__ void store_chunk(raw_t<DT>* p, const Chunk<DT, EPV>& 
   if constexpr (EPV == 1) {
     p[0] = (raw_t<DT>)c.v[0];
   } else if constexpr (DT == VH_F32) {
-    *(uint2*)p = make_uint2(c.v[0], c.v[1]);
+    *(uint4*)p = make_uint4(c.v[0], c.v[1], c.v[2], c.v[3]);
   } else {
-    *(uint2*)p = make_uint2(c.v[0] | (c.v[1] << 16), c.v[2] | (c.v[3] << 16));
+    *(uint4*)p = make_uint4(c.v[0] | (c.v[1] << 16), c.v[2] | (c.v[3] << 16), c.v[4] | (c.v[5] << 16),
+                            c.v[6] | (c.v[7] << 16));
   }
 }
 
-// Pass 1: the inliers, and each row's count of stored outliers (non-zero
-// elements whose magnitude reaches thr) into indptr[row + 1].
+// The stored outliers among a lane's chunk: bit e set for element e.
+template <int DT, int EPV>
+__device__ __forceinline__ uint32_t keep_bits(const Chunk<DT, EPV>& v, bool live, float thr) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) {
+    const float f = as_float<DT>(v.v[e]);
+    if (live && fabsf(f) >= thr && f != 0.0f) m |= 1u << e;
+  }
+  return m;
+}
+
+// Ranks of a wave's kept elements in element order: `before` counts those
+// in lanes below, `total` the wave's.
+template <int EPV>
+__device__ __forceinline__ void wave_ranks(uint32_t keep, int& before, int& total) {
+  before = 0;
+  total = 0;
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) {
+    const uint64_t m = __ballot((keep >> e) & 1u);
+    before += rank_below(m);
+    total += __popcll(m);
+  }
+}
+
+// Pass 1: inliers; per segment the count of stored outliers and the first
+// SEG_STAGE of them.
 template <int DT, int EPV>
 __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_count(const raw_t<DT>* __restrict__ x, int64_t rows,
-                                                                  int64_t cols, float thr, raw_t<DT>* __restrict__ inl,
-                                                                  int32_t* __restrict__ indptr) {
+                                                                  int64_t cols, int64_t S, float thr,
+                                                                  raw_t<DT>* __restrict__ inl, void* work) {
+  constexpr int IT = SEG / (64 * EPV);  // chunks per lane and segment
   const int lane = threadIdx.x & 63;
   const int64_t b = blockIdx.y;
-  const int64_t r = (int64_t)blockIdx.x * ROW_WAVES + (threadIdx.x >> 6);
-  if (r >= rows) return;
+  const int64_t w = (int64_t)blockIdx.x * ROW_WAVES + (threadIdx.x >> 6);
+  const int64_t nseg = rows * S;
+  if (w >= nseg) return;
+  const int64_t r = w / S, c_begin = (w % S) * SEG;
+  const int64_t c_end = c_begin + SEG < cols ? c_begin + SEG : cols;
   const int64_t base = (b * rows + r) * cols;
+  const FilterWork fw = filter_work(work, b, nseg);
+  Chunk<DT, EPV> v[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t c = c_begin + (int64_t)(it * 64 + lane) * EPV;
+    if (c < c_end) {
+      v[it] = load_chunk<DT, EPV>(x + base + c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) v[it].v[e] = 0u;
+    }
+  }
   int cnt = 0;
-#pragma unroll 2
-  for (int64_t c = (int64_t)lane * EPV; c < cols; c += 64 * EPV) {
-    Chunk<DT, EPV> v = load_chunk<DT, EPV>(x + base + c);
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t c = c_begin + (int64_t)(it * 64 + lane) * EPV;
+    const bool live = c < c_end;
+    const uint32_t keep = keep_bits<DT, EPV>(v[it], live, thr);
+    int before, total;
+    wave_ranks<EPV>(keep, before, total);
+    int mine = 0;
+    Chunk<DT, EPV> o = v[it];
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
-      const float f = as_float<DT>(v.v[e]);
-      const bool out = fabsf(f) >= thr;
-      cnt += (out && f != 0.0f) ? 1 : 0;
-      if (out) v.v[e] = 0u;
+      if (fabsf(as_float<DT>(o.v[e])) >= thr) o.v[e] = 0u;
+      if ((keep >> e) & 1u) {
+        const int s = cnt + before + mine;
+        if (s < SEG_STAGE) {
+          fw.val[w * SEG_STAGE + s] = v[it].v[e];
+          fw.col[w * SEG_STAGE + s] = (int32_t)(c + e);
+        }
+        ++mine;
+      }
     }
-    store_chunk<DT, EPV>(inl + base + c, v);
+    if (live) store_chunk<DT, EPV>(inl + base + c, o);
+    cnt += total;
   }
-  cnt = wave_sum(cnt);
-  if (lane == 0) indptr[b * (rows + 1) + r + 1] = cnt;
+  if (lane == 0) fw.seg[w] = cnt;
 }
 
-// Pass 2 (one workgroup per matrix): indptr[1 .. rows] from counts to
-// running sums clamped at cap, plus offset; indptr[0] = offset.
+// Pass 2 (one workgroup per matrix): segment counts to slot starts, the
+// total in seg[nseg]; row pointers = starts of each row's first segment,
+// clamped at cap, plus offset.
+__global__ void __launch_bounds__(SCAN_THREADS) k_segment_scan(void* work, int64_t rows, int64_t S, int64_t cap,
+                                                               int32_t offset, int32_t* __restrict__ indptr) {
+  __shared__ int64_t s_wave[SCAN_THREADS / 64];
+  const int64_t nseg = rows * S;
+  const FilterWork fw = filter_work(work, blockIdx.x, nseg);
+  int32_t* p = indptr + (int64_t)blockIdx.x * (rows + 1);
+  // SCAN_ITEMS consecutive counts per thread: a serial sum, one block scan
+  // of the thread sums, then the thread's starts.
+  // (segment and row counts stay below 2**31: the matrix does)
+  const int32_t n32 = (int32_t)nseg, S32 = (int32_t)S;
+  int64_t carry = 0;
+  for (int32_t i0 = 0; i0 < n32; i0 += SCAN_THREADS * SCAN_ITEMS) {
+    const int32_t ib = i0 + (int32_t)threadIdx.x * SCAN_ITEMS;
+    int32_t v[SCAN_ITEMS];
+    int32_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < SCAN_ITEMS; ++k) {
+      v[k] = ib + k < n32 ? fw.seg[ib + k] : 0;
+      sum += v[k];
+    }
+    int64_t total;
+    int64_t excl = block_scan<false>((int64_t)sum, s_wave, total) - sum + carry;
+    int32_t r = ib / S32, rem = ib - r * S32;
+#pragma unroll
+    for (int k = 0; k < SCAN_ITEMS; ++k) {
+      if (ib + k < n32) {
+        fw.seg[ib + k] = (int32_t)excl;
+        if (rem == 0) p[r] = (int32_t)((excl < cap ? excl : cap) + offset);
+      }
+      excl += v[k];
+      if (++rem == S32) rem = 0, ++r;
+    }
+    carry += total;
+  }
+  if (threadIdx.x == 0) {
+    fw.seg[nseg] = (int32_t)carry;
+    p[rows] = (int32_t)((carry < cap ? carry : cap) + offset);
+  }
+}
+
+// Pass 3: each segment's outliers to their slots (below cap): from the
+// workspace, or by re-reading a segment that held more than SEG_STAGE.
+// Workgroups past the segments pad slots [nse, cap).
+template <int DT, int EPV>
+__global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_fill(const raw_t<DT>* __restrict__ x, int64_t rows,
+                                                                 int64_t cols, int64_t S, float thr, int64_t cap,
+                                                                 const void* work, int seg_blocks,
+                                                                 raw_t<DT>* __restrict__ data,
+                                                                 int32_t* __restrict__ indices) {
+  constexpr int IT = SEG / (64 * EPV);
+  const int64_t b = blockIdx.y;
+  const int64_t nseg = rows * S;
+  const FilterWork fw = filter_work(const_cast<void*>(work), b, nseg);
+  raw_t<DT>* d = data + b * cap;
+  int32_t* ix = indices + b * cap;
+  if ((int)blockIdx.x >= seg_blocks) {
+    const int64_t nse = fw.seg[nseg];
+    const int64_t step = (int64_t)(gridDim.x - seg_blocks) * blockDim.x;
+    for (int64_t s = (int64_t)(blockIdx.x - seg_blocks) * blockDim.x + threadIdx.x; s < cap; s += step) {
+      if (s >= nse) {
+        d[s] = (raw_t<DT>)0;
+        ix[s] = -1;
+      }
+    }
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * ROW_WAVES + (threadIdx.x >> 6);
+  if (w >= nseg) return;
+  const int64_t start = fw.seg[w];
+  const int64_t n = (int64_t)fw.seg[w + 1] - start;
+  if (start >= cap || n == 0) return;
+  if (n <= SEG_STAGE) {
+    if (lane < n && start + lane < cap) {
+      d[start + lane] = (raw_t<DT>)fw.val[w * SEG_STAGE + lane];
+      ix[start + lane] = fw.col[w * SEG_STAGE + lane];
+    }
+    return;
+  }
+  const int64_t r = w / S, c_begin = (w % S) * SEG;
+  const int64_t c_end = c_begin + SEG < cols ? c_begin + SEG : cols;
+  const int64_t base = (b * rows + r) * cols;
+  int64_t pos = start;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t c = c_begin + (int64_t)(it * 64 + lane) * EPV;
+    const bool live = c < c_end;
+    Chunk<DT, EPV> v;
+    if (live) {
+      v = load_chunk<DT, EPV>(x + base + c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) v.v[e] = 0u;
+    }
+    const uint32_t keep = keep_bits<DT, EPV>(v, live, thr);
+    int before, total;
+    wave_ranks<EPV>(keep, before, total);
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      if ((keep >> e) & 1u) {
+        const int64_t s = pos + before + mine;
+        if (s < cap) {
+          d[s] = (raw_t<DT>)v.v[e];
+          ix[s] = (int32_t)(c + e);
+        }
+        ++mine;
+      }
+    }
+    pos += total;
+  }
+}
+
+// ------------------------------------------------------------ column slice
+// Each row's entries whose column lies in [start, end): count, then fill.
+
+// One workgroup per matrix: indptr[1 .. rows] from counts to running sums
+// clamped at cap, plus offset; indptr[0] = offset.
 __global__ void __launch_bounds__(SCAN_THREADS) k_rowptr_scan(int32_t* __restrict__ indptr, int64_t rows, int64_t cap,
                                                               int32_t offset) {
   __shared__ int64_t s_wave[SCAN_THREADS / 64];
@@ -171,73 +381,6 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_rowptr_scan(int32_t* __restric
     carry += total;
   }
 }
-
-// Pass 3: every stored outlier at its slot (row pointer + rank in the row),
-// for slots below cap; workgroups past the rows pad slots [nse, cap).
-template <int DT, int EPV>
-__global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_fill(const raw_t<DT>* __restrict__ x, int64_t rows,
-                                                                 int64_t cols, float thr, int64_t cap, int32_t offset,
-                                                                 const int32_t* __restrict__ indptr, int row_blocks,
-                                                                 raw_t<DT>* __restrict__ data,
-                                                                 int32_t* __restrict__ indices) {
-  const int64_t b = blockIdx.y;
-  const int32_t* ip = indptr + b * (rows + 1);
-  raw_t<DT>* d = data + b * cap;
-  int32_t* ix = indices + b * cap;
-  if ((int)blockIdx.x >= row_blocks) {
-    const int64_t nse = (int64_t)ip[rows] - offset;
-    const int64_t step = (int64_t)(gridDim.x - row_blocks) * blockDim.x;
-    for (int64_t s = (int64_t)(blockIdx.x - row_blocks) * blockDim.x + threadIdx.x; s < cap; s += step) {
-      if (s >= nse) {
-        d[s] = (raw_t<DT>)0;
-        ix[s] = -1;
-      }
-    }
-    return;
-  }
-  const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * ROW_WAVES + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  int64_t pos = (int64_t)ip[r] - offset;
-  const int64_t base = (b * rows + r) * cols;
-  for (int64_t c0 = 0; c0 < cols && pos < cap; c0 += 64 * EPV) {
-    const int64_t c = c0 + (int64_t)lane * EPV;
-    Chunk<DT, EPV> v;
-    bool keep[EPV];
-    if (c < cols) {
-      v = load_chunk<DT, EPV>(x + base + c);
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) v.v[e] = 0u;
-    }
-    int before = 0, total = 0;
-    uint64_t m[EPV];
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      const float f = as_float<DT>(v.v[e]);
-      keep[e] = c < cols && fabsf(f) >= thr && f != 0.0f;
-      m[e] = __ballot(keep[e]);
-      before += rank_below(m[e]);
-      total += __popcll(m[e]);
-    }
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      if (keep[e]) {
-        const int64_t s = pos + before + mine;
-        if (s < cap) {
-          d[s] = (raw_t<DT>)v.v[e];
-          ix[s] = (int32_t)(c + e);
-        }
-        ++mine;
-      }
-    }
-    pos += total;
-  }
-}
-
-// ------------------------------------------------------------ column slice
-// Each row's entries whose column lies in [start, end): count, then fill.
 __global__ void __launch_bounds__(ROW_WAVES * 64) k_cols_count(const int32_t* __restrict__ indices,
                                                                const int32_t* __restrict__ indptr, int64_t rows,
                                                                int64_t cap, int64_t start, int64_t end,
@@ -369,13 +512,33 @@ __global__ void __launch_bounds__(SPMM_THREADS) k_spmm(const void* __restrict__ 
                                                        const float* __restrict__ base, void* __restrict__ out,
                                                        int out_dt) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  constexpr int PAD = ESZ == 2 ? 2 : 1;  // one 4-byte bank of shift per tile row
+  constexpr int PAD = 16 / ESZ;  // 16 bytes: tile rows stay 16-byte aligned, 4 banks apart
+  constexpr int E16 = 16 / ESZ;  // elements per 16-byte load
   const int64_t KP = K + PAD;
   const int64_t b = blockIdx.z;
   const int64_t n0 = (int64_t)blockIdx.x * NT;
   const uint8_t* Bb = (const uint8_t*)B + b * b_stride * ESZ;
   // stage B[:, n0 .. n0 + NT) as [NT][KP]
-  if (b_layout == 0) {  // "kc": row n of B is contiguous over k
+  if (b_layout == 0 && K % E16 == 0 && ((uintptr_t)Bb % 16) == 0) {  // "kc", 16-byte rows
+    // chunk c = t * k16 + q; eight loads in flight per thread, then their stores
+    const int64_t k16 = K / E16, nchunk = NT * k16;
+    for (int64_t c0 = threadIdx.x; c0 < nchunk; c0 += 8 * SPMM_THREADS) {
+      uint4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t c = c0 + u * SPMM_THREADS;
+        const int64_t t = c / k16, q = c - t * k16;
+        v[u] = c < nchunk && n0 + t < N ? *(const uint4*)(Bb + ((n0 + t) * K + q * E16) * ESZ)
+                                        : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t c = c0 + u * SPMM_THREADS;
+        const int64_t t = c / k16, q = c - t * k16;
+        if (c < nchunk) *(uint4*)(smem + (t * KP + q * E16) * ESZ) = v[u];
+      }
+    }
+  } else if (b_layout == 0) {  // "kc": row n of B is contiguous over k
     for (int t = 0; t < NT; ++t) {
       const int64_t n = n0 + t;
       for (int64_t k = threadIdx.x; k < K; k += SPMM_THREADS) {
@@ -412,19 +575,28 @@ __global__ void __launch_bounds__(SPMM_THREADS) k_spmm(const void* __restrict__ 
   const uint8_t* tile = smem + t * KP * ESZ;
   for (int64_t r = r_begin + wave * RPW + lane / NT; r < r_end; r += RPB) {
     const int64_t j0 = rp[r], j1 = rp[r + 1];
+    const int64_t o = (b * rows + r) * N + n;
+    const float bv = (base != nullptr && n < N) ? base[o] : 0.0f;
     float acc = 0.0f;
-    for (int64_t j = j0; j < j1; ++j) {
-      int64_t k = ix[j];
-      k = k < 0 ? 0 : k >= K ? K - 1 : k;
-      const float v = raw_to_float(load_raw(dv, j, data_dt), data_dt);
-      const uint32_t braw = ESZ == 2 ? (uint32_t)((const uint16_t*)tile)[k] : ((const uint32_t*)tile)[k];
-      acc = fmaf(v, raw_to_float(braw, b_dt), acc);
+    // entries four at a time: their loads in flight together, the sum in order
+    for (int64_t j = j0; j < j1; j += 4) {
+      int32_t kk[4];
+      uint32_t vv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kk[u] = j + u < j1 ? ix[j + u] : 0;
+        vv[u] = j + u < j1 ? load_raw(dv, j + u, data_dt) : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (j + u < j1) {
+          const int64_t k = kk[u] < 0 ? 0 : kk[u] >= K ? K - 1 : kk[u];
+          const uint32_t braw = ESZ == 2 ? (uint32_t)((const uint16_t*)tile)[k] : ((const uint32_t*)tile)[k];
+          acc = fmaf(raw_to_float(vv[u], data_dt), raw_to_float(braw, b_dt), acc);
+        }
+      }
     }
-    if (n < N) {
-      const int64_t o = (b * rows + r) * N + n;
-      if (base != nullptr) acc += base[o];
-      store_float(out, o, acc, out_dt);
-    }
+    if (n < N) store_float(out, o, base != nullptr ? acc + bv : acc, out_dt);
   }
 }
 
@@ -432,7 +604,7 @@ template <int NT, int ESZ>
 int launch_spmm(const void* data, int data_dt, const int32_t* indices, const int32_t* rowptr, int64_t batch,
                 int64_t rows, int64_t cap, const void* B, int b_dt, int b_layout, int64_t K, int64_t N,
                 int64_t b_stride, const float* base, void* out, int out_dt, hipStream_t st) {
-  constexpr int PAD = ESZ == 2 ? 2 : 1;
+  constexpr int PAD = 16 / ESZ;
   const size_t smem = (size_t)NT * (size_t)(K + PAD) * ESZ;
   static bool attr_set = false;
   if (!attr_set) {
@@ -467,55 +639,63 @@ unsigned pad_blocks(int64_t cap) {
 
 template <int DT, int EPV>
 int filter_launch(const void* x, int64_t batch, int64_t rows, int64_t cols, float thr, int64_t cap,
-                  int32_t offset, void* data, int32_t* indices, int32_t* indptr, void* inl, hipStream_t st) {
+                  int32_t offset, void* data, int32_t* indices, int32_t* indptr, void* inl, void* work,
+                  hipStream_t st) {
   using R = raw_t<DT>;
-  const unsigned row_blocks = (unsigned)((rows + ROW_WAVES - 1) / ROW_WAVES);
-  if (row_blocks > 0) {
-    hipLaunchKernelGGL((k_outlier_count<DT, EPV>), dim3(row_blocks, (unsigned)batch), dim3(ROW_WAVES * 64), 0, st,
-                       (const R*)x, rows, cols, thr, (R*)inl, indptr);
+  const int64_t S = (cols + SEG - 1) / SEG;
+  const int64_t nseg = rows * S;
+  const unsigned seg_blocks = (unsigned)((nseg + ROW_WAVES - 1) / ROW_WAVES);
+  if (seg_blocks > 0) {
+    hipLaunchKernelGGL((k_outlier_count<DT, EPV>), dim3(seg_blocks, (unsigned)batch), dim3(ROW_WAVES * 64), 0, st,
+                       (const R*)x, rows, cols, S, thr, (R*)inl, work);
     if (int e = vh::check_launch("vh_filter_outlier")) return e;
   }
-  hipLaunchKernelGGL(k_rowptr_scan, dim3((unsigned)batch), dim3(SCAN_THREADS), 0, st, indptr, rows, cap, offset);
+  hipLaunchKernelGGL(k_segment_scan, dim3((unsigned)batch), dim3(SCAN_THREADS), 0, st, work, rows, S, cap, offset,
+                     indptr);
   if (int e = vh::check_launch("vh_filter_outlier")) return e;
   const unsigned pads = cap > 0 ? pad_blocks(cap) : 0;
-  if (row_blocks + pads == 0) return VH_OK;
-  hipLaunchKernelGGL((k_outlier_fill<DT, EPV>), dim3(row_blocks + pads, (unsigned)batch), dim3(ROW_WAVES * 64), 0,
-                     st, (const R*)x, rows, cols, thr, cap, offset, (const int32_t*)indptr, (int)row_blocks, (R*)data,
-                     indices);
+  if (cap == 0 || seg_blocks + pads == 0) return VH_OK;
+  hipLaunchKernelGGL((k_outlier_fill<DT, EPV>), dim3(seg_blocks + pads, (unsigned)batch), dim3(ROW_WAVES * 64), 0,
+                     st, (const R*)x, rows, cols, S, thr, cap, (const void*)work, (int)seg_blocks, (R*)data, indices);
   return vh::check_launch("vh_filter_outlier");
 }
 
 }  // namespace
 
+extern "C" int64_t vh_filter_outlier_workspace_bytes(int64_t batch, int64_t rows, int64_t cols) {
+  if (batch < 0 || rows < 0 || cols < 0) return 0;
+  return batch * filter_work_bytes_per_matrix(rows * ((cols + SEG - 1) / SEG));
+}
+
 extern "C" int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
                                  float threshold, int64_t max_nnz, int32_t indptr_offset, void* data,
-                                 int32_t* indices, int32_t* indptr, void* inliers, vh_stream_t stream) {
+                                 int32_t* indices, int32_t* indptr, void* inliers, void* work, int64_t work_bytes,
+                                 vh_stream_t stream) {
   VH_REQUIRE(float_dtype(dtype), "vh_filter_outlier: dtype must be bf16, fp16 or fp32");
   VH_REQUIRE(batch >= 1 && batch <= 65535 && rows >= 0 && cols >= 0 && max_nnz >= 0,
              "vh_filter_outlier: bad sizes (batch %lld, rows %lld, cols %lld, max_nnz %lld)", (long long)batch,
              (long long)rows, (long long)cols, (long long)max_nnz);
-  VH_REQUIRE(rows * cols < ((int64_t)1 << 31) && max_nnz < ((int64_t)1 << 31) && rows < (1 << 26),
+  VH_REQUIRE(rows * cols < ((int64_t)1 << 31) && max_nnz < ((int64_t)1 << 31),
              "vh_filter_outlier: a matrix must hold fewer than 2**31 elements (int32 row pointers)");
   VH_REQUIRE(rows * cols == 0 || (x != nullptr && inliers != nullptr), "vh_filter_outlier: null tensor");
+  VH_REQUIRE(work != nullptr && ((uintptr_t)work % 16) == 0 &&
+                 work_bytes >= vh_filter_outlier_workspace_bytes(batch, rows, cols),
+             "vh_filter_outlier: workspace needs %lld bytes, 16-byte aligned",
+             (long long)vh_filter_outlier_workspace_bytes(batch, rows, cols));
+  const int64_t S = (cols + SEG - 1) / SEG;
+  VH_REQUIRE(rows * S / ROW_WAVES < ((int64_t)1 << 31), "vh_filter_outlier: too many rows");
   const hipStream_t st = vh::as_stream(stream);
-  const bool vec = cols % (dtype == VH_F32 ? 2 : 4) == 0 && ((uintptr_t)x % 8) == 0 && ((uintptr_t)inliers % 8) == 0;
+  const int epv = dtype == VH_F32 ? 4 : 8;
+  const bool vec = cols % epv == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)inliers % 16) == 0;
+#define VH_FILTER(DT, EPV)                                                                                        \
+  filter_launch<DT, EPV>(x, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inliers, \
+                         work, st)
   switch (dtype) {
-    case VH_BF16:
-      return vec ? filter_launch<VH_BF16, 4>(x, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices,
-                                             indptr, inliers, st)
-                 : filter_launch<VH_BF16, 1>(x, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices,
-                                             indptr, inliers, st);
-    case VH_F16:
-      return vec ? filter_launch<VH_F16, 4>(x, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices,
-                                            indptr, inliers, st)
-                 : filter_launch<VH_F16, 1>(x, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices,
-                                            indptr, inliers, st);
-    default:
-      return vec ? filter_launch<VH_F32, 2>(x, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices,
-                                            indptr, inliers, st)
-                 : filter_launch<VH_F32, 1>(x, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices,
-                                            indptr, inliers, st);
+    case VH_BF16: return vec ? VH_FILTER(VH_BF16, 8) : VH_FILTER(VH_BF16, 1);
+    case VH_F16: return vec ? VH_FILTER(VH_F16, 8) : VH_FILTER(VH_F16, 1);
+    default: return vec ? VH_FILTER(VH_F32, 4) : VH_FILTER(VH_F32, 1);
   }
+#undef VH_FILTER
 }
 
 extern "C" int vh_slice_csr(const void* data, int32_t dtype, const int32_t* indices, const int32_t* indptr,
@@ -566,7 +746,7 @@ extern "C" int vh_spmm_csr(const void* data, int32_t data_dtype, const int32_t* 
              "vh_spmm_csr: bad sizes (batch %lld, rows %lld, cap %lld, K %lld, N %lld)", (long long)batch,
              (long long)rows, (long long)cap, (long long)K, (long long)N);
   const int esz = b_dtype == VH_F32 ? 4 : 2;
-  VH_REQUIRE((K + 2) * esz <= SPMM_LDS,
+  VH_REQUIRE(K * esz + 16 <= SPMM_LDS,
              "vh_spmm_csr: K = %lld does not fit one LDS tile column (at most %d bytes per column)", (long long)K,
              SPMM_LDS);
   const hipStream_t st = vh::as_stream(stream);
@@ -575,7 +755,7 @@ extern "C" int vh_spmm_csr(const void* data, int32_t data_dtype, const int32_t* 
   if (rows == 0 || N == 0) return VH_OK;
   // the widest tile of B columns whose K rows fit the LDS budget
   int nt = 16;
-  while (nt > 1 && (int64_t)nt * (K + 2) * esz > SPMM_LDS) nt >>= 1;
+  while (nt > 1 && (int64_t)nt * (K * esz + 16) > SPMM_LDS) nt >>= 1;
 #define VH_SPMM(NT)                                                                                                  \
   return esz == 2 ? launch_spmm<NT, 2>(data, data_dtype, indices, work, batch, rows, cap, B, b_dtype, b_layout, K, N, \
                                        b_batch_stride, base, out, out_dtype, st)                                     \

@@ -8,8 +8,9 @@ stream's product with the decoded weight (``A_data``, ``A_indices``,
 ``A_indptr``; ``ops/quantized.py:709-720``).  Here:
 
 * ``filter_outlier`` / ``quantize_mx_outlier`` (``ops/quantized.py:1286-1458``)
-  run ``vh_filter_outlier`` (row counts with the inliers, a scan per matrix,
-  the fill), then the package's ``quantize_mx`` on the inliers;
+  run ``vh_filter_outlier`` (segment counts with the inliers, a scan per
+  matrix, the fill; a small workspace from torch's allocator), then the
+  package's ``quantize_mx`` on the inliers;
 * ``slice_csr_tensor`` (``:1493-1545``) runs ``vh_slice_csr``;
 * ``spmm_csr`` (``:1567-1645``) decodes ``B`` with the package's
   ``dequantize_mx`` and runs ``vh_spmm_csr``; ``linear_mx`` / ``matmul_mx``
@@ -81,9 +82,12 @@ def filter_outlier(input: torch.Tensor, threshold: float, max_pct: float = 0.01,
     if nb == 0:
         return data, indices, indptr, inliers
     thr = threshold_in(input.dtype, threshold)
-    st = load().vh_filter_outlier(ptr(x), dtype_code(x.dtype), nb, rows, cols, ctypes.c_float(thr), cap,
-                                  int(indptr_offset), ptr(data), ptr(indices), ptr(indptr), ptr(inliers),
-                                  ctypes.c_void_p(stream_of(x)))
+    lib_ = load()
+    nbytes = lib_.vh_filter_outlier_workspace_bytes(nb, rows, cols)
+    work = torch.empty((nbytes + 15) // 16, 16, dtype=torch.uint8, device=input.device)
+    st = lib_.vh_filter_outlier(ptr(x), dtype_code(x.dtype), nb, rows, cols, ctypes.c_float(thr), cap,
+                                int(indptr_offset), ptr(data), ptr(indices), ptr(indptr), ptr(inliers), ptr(work),
+                                work.numel(), ctypes.c_void_p(stream_of(x)))
     _lib.check(st, "vh_filter_outlier")
     return data, indices, indptr, inliers
 
