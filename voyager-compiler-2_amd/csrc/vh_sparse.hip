@@ -104,7 +104,7 @@ __device__ __forceinline__ int64_t block_scan(int64_t v, int64_t* s_wave, int64_
 // segments that held more than SEG_STAGE.
 constexpr int SEG = 2048;
 constexpr int SEG_STAGE = 16;
-constexpr int SCAN_ITEMS = 16;
+constexpr int SCAN_ITEMS = 8;
 
 struct FilterWork {
   int32_t* seg;   // [nseg + 1] counts, then slot starts (seg[nseg]: the total)
@@ -251,35 +251,51 @@ __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_count(const raw_t<DT
 __global__ void __launch_bounds__(SCAN_THREADS) k_segment_scan(void* work, int64_t rows, int64_t S, int64_t cap,
                                                                int32_t offset, int32_t* __restrict__ indptr) {
   __shared__ int64_t s_wave[SCAN_THREADS / 64];
+  // a chunk of counts, one pad word per 16 so a thread's reads hit distinct banks
+  __shared__ int32_t s_tile[SCAN_THREADS * SCAN_ITEMS * 17 / 16];
   const int64_t nseg = rows * S;
   const FilterWork fw = filter_work(work, blockIdx.x, nseg);
   int32_t* p = indptr + (int64_t)blockIdx.x * (rows + 1);
-  // SCAN_ITEMS consecutive counts per thread: a serial sum, one block scan
-  // of the thread sums, then the thread's starts.
+  // Chunks of SCAN_THREADS * SCAN_ITEMS counts: coalesced loads into LDS,
+  // SCAN_ITEMS consecutive counts per thread (a serial sum, one block scan
+  // of the thread sums, the thread's starts back to LDS), coalesced stores.
   // (segment and row counts stay below 2**31: the matrix does)
   const int32_t n32 = (int32_t)nseg, S32 = (int32_t)S;
+  const int tid = threadIdx.x;
+  auto pad = [](int i) { return i + (i >> 4); };
   int64_t carry = 0;
   for (int32_t i0 = 0; i0 < n32; i0 += SCAN_THREADS * SCAN_ITEMS) {
-    const int32_t ib = i0 + (int32_t)threadIdx.x * SCAN_ITEMS;
+#pragma unroll
+    for (int k = 0; k < SCAN_ITEMS; ++k) {
+      const int32_t i = i0 + k * SCAN_THREADS + tid;
+      s_tile[pad(k * SCAN_THREADS + tid)] = i < n32 ? fw.seg[i] : 0;
+    }
+    __syncthreads();
     int32_t v[SCAN_ITEMS];
     int32_t sum = 0;
 #pragma unroll
     for (int k = 0; k < SCAN_ITEMS; ++k) {
-      v[k] = ib + k < n32 ? fw.seg[ib + k] : 0;
+      v[k] = s_tile[pad(tid * SCAN_ITEMS + k)];
       sum += v[k];
     }
     int64_t total;
     int64_t excl = block_scan<false>((int64_t)sum, s_wave, total) - sum + carry;
+    const int32_t ib = i0 + tid * SCAN_ITEMS;
     int32_t r = ib / S32, rem = ib - r * S32;
 #pragma unroll
     for (int k = 0; k < SCAN_ITEMS; ++k) {
-      if (ib + k < n32) {
-        fw.seg[ib + k] = (int32_t)excl;
-        if (rem == 0) p[r] = (int32_t)((excl < cap ? excl : cap) + offset);
-      }
+      s_tile[pad(tid * SCAN_ITEMS + k)] = (int32_t)excl;
+      if (ib + k < n32 && rem == 0) p[r] = (int32_t)((excl < cap ? excl : cap) + offset);
       excl += v[k];
       if (++rem == S32) rem = 0, ++r;
     }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SCAN_ITEMS; ++k) {
+      const int32_t i = i0 + k * SCAN_THREADS + tid;
+      if (i < n32) fw.seg[i] = s_tile[pad(k * SCAN_THREADS + tid)];
+    }
+    __syncthreads();
     carry += total;
   }
   if (threadIdx.x == 0) {
