@@ -101,6 +101,21 @@ int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t nd
                 const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
                 const vh_format* fmt, void* out, int32_t out_dtype, vh_stream_t stream);
 
+/* quantize with stochastic rounding (a `seed`): out = x / scale (+ zp) as
+ * vh_quantize computes it, rounded to one of the two of `levels` around it
+ * (levels ascending, device memory, bf16/fp16/fp32; a table's distinct
+ * finite entries with one +0, or a codebook's entries).  Element i in the
+ * row-major order of `shape` takes byte i % 4 of word (i % 16) / 4 of the
+ * Philox4x32-10 draw of counter i / 16 keyed by *seed (int64, device
+ * memory), and rounds away from zero when |v| + byte / 256 * (high - low)
+ * >= |far| in float32.  Replaces _stochastic_round / _random_bytes /
+ * _philox (ops/quantized.py:318-446) inside quantize (:449-515) and
+ * quantize_mx (:1076-1115). */
+#define VH_SR_MAX_LEVELS 16384
+int vh_quantize_sr(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim, const vh_param* scale,
+                   const vh_param* zero_point, int32_t compute_dtype, const void* levels, int32_t levels_dtype,
+                   int32_t nlevels, const int64_t* seed, void* out, int32_t out_dtype, vh_stream_t stream);
+
 /* dequantize: out = G((Fin(x) - zp) * scale).  Replaces
  * quantized_ops.dequantize (ops/quantized.py:518-571).  x_dtype VH_U8 reads
  * packed codes of fmt_in. */

@@ -59,10 +59,74 @@ def decode(input, codebook):
     return codebook[input.to(torch.long)].to(input.dtype)
 
 
+# ------------------------------------------------------ stochastic rounding
+# Philox4x32-10 (Salmon et al., SC'11): round multipliers, key increments.
+PHILOX_M = (0xD2511F53, 0xCD9E8D57)
+PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+MASK32 = 0xFFFFFFFF
+
+
+def _mulhilo32(a, b):
+    """High and low words of ``a * b``: uint32 values held in int64, the
+    product taken over the 16-bit halves of ``b`` so nothing overflows
+    (``ops/quantized.py:327-336``)."""
+    lo_part = a * (b & 0xFFFF)
+    hi_part = a * (b >> 16)
+    low = lo_part + ((hi_part & 0xFFFF) << 16)
+    return (hi_part >> 16) + (low >> 32), low & MASK32
+
+
+def philox(counter, seed):
+    """``_philox``, ``ops/quantized.py:339-360``: the four words of the
+    Philox4x32-10 draw of each int64 ``counter`` (high 64 counter bits zero)
+    under the 64-bit key ``seed``; int64 ``[*counter.shape, 4]``."""
+    c0, c1 = counter & MASK32, (counter >> 32) & MASK32
+    c2 = torch.zeros_like(counter)
+    c3 = torch.zeros_like(counter)
+    k0, k1 = seed & MASK32, (seed >> 32) & MASK32
+    for _ in range(10):
+        hi0, lo0 = _mulhilo32(c0, PHILOX_M[0])
+        hi1, lo1 = _mulhilo32(c2, PHILOX_M[1])
+        c0, c1, c2, c3 = hi1 ^ c1 ^ k0, lo1, hi0 ^ c3 ^ k1, lo0
+        k0 = (k0 + PHILOX_W[0]) & MASK32
+        k1 = (k1 + PHILOX_W[1]) & MASK32
+    return torch.stack([c0, c1, c2, c3], -1)
+
+
+def random_bytes(seed, shape):
+    """``_random_bytes``, ``ops/quantized.py:363-381``: element ``i`` takes
+    byte ``i % 4`` of word ``i % 16 // 4`` of draw ``i // 16``."""
+    numel = math.prod(shape)
+    words = philox(torch.arange(-(-numel // 16)), seed)
+    shifts = torch.arange(0, 32, 8)
+    return ((words[..., None] >> shifts) & 0xFF).flatten()[:numel].view(shape)
+
+
+def qmap_levels(qmap):
+    """``qmap_levels``, ``ops/quantized.py:384-396``: a table's distinct finite values,
+    ascending, float32, one +0."""
+    table = qmap.float()
+    return torch.unique(table[torch.isfinite(table)]) + 0.0
+
+
+def stochastic_round(input, qmap, seed):
+    """``_stochastic_round`` / ``_neighbors``, ``ops/quantized.py:399-446``."""
+    levels = qmap_levels(qmap) if qmap.numel() == QMAP_SIZE else qmap
+    levels = levels.float()
+    value = input.float().clamp(levels[0], levels[-1])
+    upper = torch.searchsorted(levels, value).clamp(max=levels.numel() - 1)
+    high = levels[upper]
+    low = torch.where(high == value, high, levels[(upper - 1).clamp(min=0)])
+    noise = random_bytes(seed, input.shape) / 256
+    near = torch.where(value < 0, high, low)
+    far = torch.where(value < 0, low, high)
+    away = value.abs() + noise * (high - low) >= far.abs()
+    return torch.where(away, far, near).to(input.dtype)
+
+
 def quantize(input, scale, zero_point=None, axes=None, block_size=None,
              qmap=None, output_code=None, seed=None):
-    """``ops/quantized.py:449-515`` (nearest rounding only)."""
-    assert seed is None
+    """``ops/quantized.py:449-515``; with a ``seed``, stochastic rounding."""
     if block_size is not None:
         scale = repeat_per_block(scale, input, block_size)
         if zero_point is not None:
@@ -73,6 +137,8 @@ def quantize(input, scale, zero_point=None, axes=None, block_size=None,
         x = input / scale + zero_point
     if qmap is None:
         return x
+    if seed is not None:
+        return stochastic_round(x, qmap, seed)
     if qmap.numel() == QMAP_SIZE and qmap.dim() == 1:
         return vmap(x, qmap)
     return encode(x, qmap, output_code)

@@ -757,6 +757,121 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
   });
 }
 
+// ------------------------------------------------------------ stochastic rounding
+// quantize with a seed (ops/quantized.py:318-446, 449-515): x / scale (+ zp)
+// as quantize computes it, then rounded to one of the two levels around it.
+// Element i (logical row-major order) takes byte i % 4 of word i % 16 / 4 of
+// the Philox4x32-10 draw (Salmon et al., SC'11) of counter i / 16 keyed by
+// the 64-bit seed; it rounds to the level farther from zero when
+// |v| + byte / 256 * (high - low) >= |far| in float32.  One thread: the 16
+// elements of one draw.  Levels in LDS, searched as torch.searchsorted
+// (first level >= v; NaN past the end).
+constexpr int SR_ELEMS = 16;
+
+VH_DEV void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t hi0 = __umulhi(c[0], 0xD2511F53u), lo0 = c[0] * 0xD2511F53u;
+    const uint32_t hi1 = __umulhi(c[2], 0xCD9E8D57u), lo1 = c[2] * 0xCD9E8D57u;
+    const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0, c[1] = lo1, c[2] = n2, c[3] = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+// The rounding rule on one value: no contraction, each float32 operation
+// rounded as torch's eager ops round it.
+VH_DEV float sr_round(float v, const float* lv, int nlev, uint32_t byte) {
+#pragma clang fp contract(off)
+  if (!isnan_f(v)) v = fminf(fmaxf(v, lv[0]), lv[nlev - 1]);
+  int lo = 0, hi = nlev;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (!(lv[mid] >= v)) lo = mid + 1;
+    else hi = mid;
+  }
+  const int upper = lo < nlev - 1 ? lo : nlev - 1;
+  const float high = lv[upper];
+  const float low = high == v ? high : lv[upper > 0 ? upper - 1 : 0];
+  const bool neg = v < 0.0f;
+  const float near = neg ? high : low, far = neg ? low : high;
+  const float noise = (float)byte / 256.0f;
+  const float gap = high - low;
+  const float step = noise * gap;
+  const float lhs = fabsf(v) + step;
+  return lhs >= fabsf(far) ? far : near;
+}
+
+__global__ void __launch_bounds__(256)
+k_quantize_sr(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_param sp, vh_param zp, int cdt,
+              const void* __restrict__ levels, int lv_dtype, int nlev, const int64_t* __restrict__ seed,
+              void* __restrict__ out, int out_dtype) {
+  extern __shared__ float s_lv[];
+  for (int i = threadIdx.x; i < nlev; i += blockDim.x) s_lv[i] = load_any(levels, lv_dtype, i);
+  __syncthreads();
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t base = t * SR_ELEMS;
+  if (base >= n) return;
+  const uint64_t sd = (uint64_t)seed[0];
+  uint32_t w[4] = {(uint32_t)t, (uint32_t)((uint64_t)t >> 32), 0u, 0u};
+  philox4x32_10(w, (uint32_t)sd, (uint32_t)(sd >> 32));
+  const float s0 = (sp.ptr && sp.scalar) ? load_any(sp.ptr, sp.dtype, 0) : 1.0f;
+  const float z0 = (zp.ptr && zp.scalar) ? load_any(zp.ptr, zp.dtype, 0) : 0.0f;
+#pragma unroll
+  for (int h = 0; h < SR_ELEMS / VEC; ++h) {
+    const int64_t b8 = base + h * VEC;
+    if (b8 >= n) break;
+    float sv[VEC], zv[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      sv[j] = s0;
+      zv[j] = z0;
+    }
+    if (sp.ptr && !sp.scalar) param_values(sp, shape, b8, n, sv);
+    if (zp.ptr && !zp.scalar) param_values(zp, shape, b8, n, zv);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int64_t i = b8 + j;
+      if (i >= n) break;
+      float q = load_any(x, x_dtype, i);
+      if (sp.ptr) q = div_round(q, sv[j], cdt);
+      if (zp.ptr) q = round_to(q + zv[j], cdt);
+      const int e = h * VEC + j;
+      const uint32_t byte = (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+      store_any(out, out_dtype, i, sr_round(q, s_lv, nlev, byte));
+    }
+  }
+}
+
+extern "C" int vh_quantize_sr(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                              const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
+                              const void* levels, int32_t levels_dtype, int32_t nlevels, const int64_t* seed,
+                              void* out, int32_t out_dtype, vh_stream_t stream) {
+  Shape s;
+  int64_t n;
+  int rc;
+  if ((rc = check_shape(shape, ndim, &s, &n))) return rc;
+  VH_REQUIRE(x && out && levels && seed, "vh_quantize_sr: null pointer");
+  VH_REQUIRE(vh::is_float_dtype(x_dtype) && vh::is_float_dtype(compute_dtype) && vh::is_float_dtype(out_dtype) &&
+                 vh::is_float_dtype(levels_dtype),
+             "vh_quantize_sr: dtypes must be bf16, fp16 or fp32");
+  VH_REQUIRE(nlevels >= 1 && nlevels <= VH_SR_MAX_LEVELS, "vh_quantize_sr: %d levels (1 .. %d supported)", nlevels,
+             VH_SR_MAX_LEVELS);
+  if ((rc = check_param(scale, s, "scale"))) return rc;
+  if ((rc = check_param(zero_point, s, "zero_point"))) return rc;
+  if (n == 0) return VH_OK;
+  const vh_param sp = scale ? *scale : null_param();
+  const vh_param zp = zero_point ? *zero_point : null_param();
+  const int64_t threads = (n + SR_ELEMS - 1) / SR_ELEMS;
+  const int64_t blocks = (threads + 255) / 256;
+  VH_REQUIRE(blocks < (1ll << 31), "vh_quantize_sr: tensor too large");
+  hipLaunchKernelGGL(k_quantize_sr, dim3((unsigned)blocks), dim3(256), (size_t)nlevels * sizeof(float),
+                     vh::as_stream(stream), x, x_dtype, n, s, sp, zp, compute_dtype, levels, levels_dtype, nlevels,
+                     seed, out, out_dtype);
+  return vh::check_launch("vh_quantize_sr");
+}
+
 // ------------------------------------------------------------ dequantize
 template <int KIN>
 __global__ void __launch_bounds__(256)

@@ -89,6 +89,7 @@ _SIGNATURES = {
          ctypes.POINTER(Format), _P, _I32, _P],
         _I32,
     ),
+    "vh_quantize_sr": ([_P, _I32, _P, _I32, _P, _P, _I32, _P, _I32, _I32, _P, _P, _I32, _P], _I32),
     "vh_dequantize": (
         [_P, _I32, ctypes.POINTER(_I64), _I32, ctypes.POINTER(Param), ctypes.POINTER(Param), _I32,
          ctypes.POINTER(Format), ctypes.POINTER(Format), _P, _I32, _P],

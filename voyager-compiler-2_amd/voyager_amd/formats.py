@@ -411,6 +411,27 @@ def classify(table: torch.Tensor) -> Classified:
     return result
 
 
+def sr_levels(qmap: torch.Tensor) -> torch.Tensor:
+    """The levels stochastic rounding rounds between
+    (``qmap_levels``, ``ops/quantized.py:384-396``): a 65,536-entry table's
+    distinct finite entries, ascending, with one +0 (float32, computed on the
+    host once per table and cached on it); a smaller map is a codebook whose
+    entries are the levels as given."""
+    if qmap.dim() != 1 or qmap.numel() != QMAP_SIZE:
+        return qmap
+    cached = getattr(qmap, "_vh_sr_levels", None)
+    if cached is not None and cached[0] == qmap._version and cached[1] == qmap.data_ptr():
+        return cached[2]
+    vals = qmap.detach().cpu().to(torch.float32).numpy()
+    lv = (np.unique(vals[np.isfinite(vals)]) + np.float32(0.0)).astype(np.float32)
+    levels = torch.from_numpy(lv).to(qmap.device)
+    try:
+        qmap._vh_sr_levels = (qmap._version, qmap.data_ptr(), levels)
+    except (AttributeError, RuntimeError):
+        pass
+    return levels
+
+
 def describe(fmt: Format) -> str:
     names = {FMT_IDENTITY: "identity", FMT_INT: "int", FMT_MINIFLOAT: "minifloat", FMT_POSIT: "posit",
              FMT_STEPS: "steps", FMT_LUT: "lut"}

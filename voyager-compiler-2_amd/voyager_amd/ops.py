@@ -241,12 +241,40 @@ def _quantize_dtype(input, scale, zero_point):
     return d
 
 
+def _quantize_sr(input, scale, zero_point, block_size, qmap, seed, cdt):
+    """``quantize`` with a seed (``ops/quantized.py:318-446``): the division,
+    then stochastic rounding between the levels of ``qmap``, through
+    ``vh_quantize_sr``; elements in logical row-major order (the order of the
+    random bytes), result contiguous in ``cdt``."""
+    levels = formats.sr_levels(qmap)
+    if levels.dim() != 1:
+        raise NotImplementedError("quantized_ops.quantize: stochastic rounding against per-head codebooks is not "
+                                  "supported on the GPU")
+    if levels.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        levels = levels.to(torch.float32)
+    if seed.dtype != torch.int64 or seed.numel() != 1:
+        raise ValueError("quantized_ops.quantize: seed must be an int64 scalar")
+    x = input.contiguous()
+    shape = list(x.shape)
+    sp, keep_s = _param(scale, shape, block_size, cdt, "scale")
+    zpp, keep_z = _param(zero_point, shape, block_size, cdt, "zero_point")
+    out = torch.empty(shape, dtype=cdt, device=x.device)
+    sd = seed.reshape(()).contiguous()
+    st = load().vh_quantize_sr(ptr(x), dtype_code(x.dtype), _shape_arr(shape), len(shape),
+                               ctypes.byref(sp) if sp else None, ctypes.byref(zpp) if zpp else None, dtype_code(cdt),
+                               ptr(levels), dtype_code(levels.dtype), levels.numel(), ptr(sd), ptr(out),
+                               dtype_code(cdt), ctypes.c_void_p(stream_of(x)))
+    _lib.check(st, "vh_quantize_sr")
+    del keep_s, keep_z
+    return out
+
+
 def _quantize_cuda(input, scale, zero_point=None, axes=None, block_size=None, qmap=None,
                    output_code=None, seed=None):
-    _require_gpu(input, scale, zero_point, qmap)
-    if seed is not None:
-        raise NotImplementedError("quantized_ops.quantize: stochastic rounding (seed) is not supported on the GPU")
+    _require_gpu(input, scale, zero_point, qmap, seed)
     cdt = _quantize_dtype(input, scale, zero_point)
+    if seed is not None and qmap is not None:
+        return _quantize_sr(input, scale, zero_point, block_size, qmap, seed, cdt)
     if qmap is not None and not _is_table(qmap):
         raise NotImplementedError("quantized_ops.quantize: codebook (searchsorted) maps are not supported yet")
     fmt = _fmt_of(qmap).fmt if qmap is not None else None
@@ -359,9 +387,16 @@ def _calculate_mx_qparam_fake(input, axes, block_size, quant_max, force_scale_po
 
 def _quantize_mx_cuda(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
                       scale_qmap=None, output_code=None, seed=None, global_scale=None):
-    _require_gpu(input, qmap, scale_qmap, global_scale)
+    _require_gpu(input, qmap, scale_qmap, global_scale, seed)
     if seed is not None:
-        raise NotImplementedError("quantized_ops.quantize_mx: stochastic rounding (seed) is not supported on the GPU")
+        # ops/quantized.py:1097-1115: the block scales, then quantize with the seed
+        if global_scale is not None:
+            raise NotImplementedError("quantized_ops.quantize_mx: stochastic rounding with a global scale is not "
+                                      "supported on the GPU")
+        scale, _ = _mx_launch(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, None, None,
+                              False)
+        cdt = _quantize_dtype(input, scale, None)
+        return scale, _quantize_sr(input, scale, None, block_size, qmap, seed, cdt)
     if not _is_table(qmap):
         raise NotImplementedError("quantized_ops.quantize_mx: codebook (searchsorted) maps are not supported yet")
     return _mx_launch(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, global_scale, qmap,
