@@ -152,3 +152,25 @@ def test_quantize_affine_partial_blocks():
         assert_same_bits(gs, es, f"scale {axis}")
         assert_same_bits(gz, ez, f"zp {axis}")
         assert_same_bits(gv, ev, f"codes {axis}")
+
+
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(64, 256), (3, 16, 96)])
+def test_nvfp4_global_scale_bit_exact(gdtype, shape):
+    """NVFP4's two-level scaling (ops/quantized.py:1016-1021, 1094-1115):
+    fp4_e2m1 codes, fp8_e4m3 block scales over 16 elements, and a 0-d
+    global scale that divides out the tensor's magnitude before the block
+    scales are quantized and multiplies them back into the elements'
+    divisor; calculate_mx_qparam and quantize_mx bit-exact."""
+    g = torch.Generator().manual_seed(sum(shape))
+    x = (torch.randn(*shape, generator=g) * 7).bfloat16()
+    fp4, e4m3 = T.quantization_map("fp4_e2m1"), T.quantization_map("fp8_e4m3")
+    gs = (x.float().abs().amax() / (6.0 * 448.0)).clamp_min(torch.finfo(torch.float32).tiny).to(gdtype)
+    es = O.calculate_mx_qparam(x, [-1], 16, 6.0, False, e4m3, gs)
+    got = torch.ops.quantized_ops.calculate_mx_qparam(x.cuda(), [-1], 16, 6.0, False, e4m3.cuda(), gs.cuda())
+    assert_same_bits(got, es, "scale")
+    es2, ec2 = O.quantize_mx(x, fp4, [-1], 16, 6.0, False, e4m3, None, None, gs)
+    gs2, gc2 = torch.ops.quantized_ops.quantize_mx(x.cuda(), fp4.cuda(), [-1], 16, 6.0, False, e4m3.cuda(), None,
+                                                   None, gs.cuda())
+    assert_same_bits(gs2, es2, "quantize_mx scale")
+    assert_same_bits(gc2, ec2, "quantize_mx codes")

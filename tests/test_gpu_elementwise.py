@@ -196,3 +196,25 @@ def test_dequantize_packed_table(dtype, scale):
             got = _elementwise("dequantize", c, sv.cuda(), None, None, torch.bfloat16, fmt, None,
                                torch.bfloat16).cpu()
             assert_same_bits(got, O.dequantize(v, sv), f"{dtype} n={n} scale {scale}")
+
+
+@pytest.mark.parametrize("op", ["quantize", "dequantize"])
+@pytest.mark.parametrize("sdtype", [torch.float32, torch.float16])
+def test_zero_dim_scale_of_another_dtype(op, sdtype):
+    """A bf16 tensor with a 0-d float32 / float16 scale and zero point, as
+    eager torch (CPU) combines them: the division (multiplication) by the
+    scale at its own precision, rounded once to bf16; the zero point
+    rounded to bf16 before it is added (subtracted)."""
+    g = torch.Generator().manual_seed(77)
+    x = (torch.randn(64, 128, generator=g) * 5).bfloat16()
+    s = torch.tensor(0.0123456789, dtype=sdtype)
+    zp = torch.tensor(3.3, dtype=sdtype)
+    tab = T.quantization_map("int8")
+    if op == "quantize":
+        exp = O.quantize(x, s, zp, qmap=tab)
+        got = torch.ops.quantized_ops.quantize(x.cuda(), s.cuda(), zp.cuda(), qmap=tab.cuda())
+    else:
+        exp = O.dequantize(x, s, zp)
+        got = torch.ops.quantized_ops.dequantize(x.cuda(), s.cuda(), zp.cuda())
+    assert got.dtype == exp.dtype == torch.bfloat16
+    assert_same_bits(got, exp, f"{op} {sdtype}")

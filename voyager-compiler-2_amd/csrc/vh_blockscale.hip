@@ -117,7 +117,9 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
   }
   if (P.mode == MX_SCALED) {
     float s = div_round(hi, P.quant_max, cdt);
-    const float gs = P.gs ? round_to(load_x(P.gs, P.gs_dtype, 0), cdt) : 1.0f;
+    // A 0-d global scale enters the bf16 ops at its own precision: eager
+    // bf16 / fp32-scalar divides (and multiplies) in float32, then rounds.
+    const float gs = P.gs ? load_x(P.gs, P.gs_dtype, 0) : 1.0f;
     if (P.gs) s = div_round(s, gs, cdt);
     if constexpr (SKIND != K_NONE) {
       const uint32_t sb = f2bf(s);

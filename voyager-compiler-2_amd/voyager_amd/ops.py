@@ -138,14 +138,21 @@ def _layout_order(x: torch.Tensor):
 
 
 def _param(p: Optional[torch.Tensor], shape: Sequence[int], block_size: Optional[int],
-           dtype: torch.dtype, name: str, order=None):
+           dtype: torch.dtype, name: str, order=None, own_precision: bool = False):
     """``vh_param`` of a scale / zero point read against a tensor of
     ``shape`` (already in memory order when ``order`` is given).  Follows
     ``repeat_per_block`` (``ops/quantized.py:124-144``) with a block size and
     torch broadcasting without one."""
     if p is None:
         return None, None
-    p = p.to(dtype)
+    # How eager torch (CPU) combines a tensor with a 0-d tensor of a wider
+    # float dtype: mul and div use the 0-d value at its own precision (then
+    # round once), add and sub round it to the tensor's dtype first.  So a
+    # float scale keeps its dtype (the kernels read any float dtype into
+    # float32) and a zero point takes the compute dtype; a wider n-d
+    # parameter has already widened `dtype`, where either is exact.
+    if not (own_precision and p.dtype in (torch.bfloat16, torch.float16, torch.float32)):
+        p = p.to(dtype)
     nd = len(shape)
     if p.dim() > nd:
         raise ValueError(f"{name} has more dims ({p.dim()}) than the input ({nd})")
@@ -154,7 +161,7 @@ def _param(p: Optional[torch.Tensor], shape: Sequence[int], block_size: Optional
     if order is not None:
         p = p.permute(order)
     prm = Param()
-    prm.dtype = dtype_code(dtype)
+    prm.dtype = dtype_code(p.dtype)
     if p.numel() == 1:
         p = p.reshape(()).contiguous()
         prm.ptr = p.data_ptr()
@@ -190,7 +197,7 @@ def _elementwise(kind: str, x: torch.Tensor, scale, zp, block_size, cdt, fmt_a: 
     order = _layout_order(x)
     xv = x.permute(order) if order is not None else x.contiguous()
     shape = list(xv.shape)
-    sp, keep_s = _param(scale, shape, block_size, cdt, "scale", order)
+    sp, keep_s = _param(scale, shape, block_size, cdt, "scale", order, own_precision=True)
     zpp, keep_z = _param(zp, shape, block_size, cdt, "zero_point", order)
     out = torch.empty(shape, dtype=out_dtype, device=x.device)
     args_common = (ptr(xv), dtype_code(xv.dtype), _shape_arr(shape), len(shape),
@@ -256,7 +263,7 @@ def _quantize_sr(input, scale, zero_point, block_size, qmap, seed, cdt):
         raise ValueError("quantized_ops.quantize: seed must be an int64 scalar")
     x = input.contiguous()
     shape = list(x.shape)
-    sp, keep_s = _param(scale, shape, block_size, cdt, "scale")
+    sp, keep_s = _param(scale, shape, block_size, cdt, "scale", own_precision=True)
     zpp, keep_z = _param(zero_point, shape, block_size, cdt, "zero_point")
     out = torch.empty(shape, dtype=cdt, device=x.device)
     sd = seed.reshape(()).contiguous()
