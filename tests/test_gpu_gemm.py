@@ -267,3 +267,34 @@ def test_linear_nf4_gemv_cfg3(M, K, N):
     got = gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d))
     assert got.dtype == torch.bfloat16 and list(got.shape) == [M, N]
     assert max_rel_err(got, exp) < TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (7, 96, 160)])
+def test_linear_mx_nvfp4(M, N, K):
+    """NVFP4 as the reference's converted graph runs it: quantize_mx of both
+    operands to fp4_e2m1 with fp8_e4m3 block scales over 16 and a float32
+    global scale each (ops/quantized.py:1076-1115), then linear_mx with the
+    global scales' product as alpha (:651-723); codes and scales bit-exact,
+    the product within 1e-2 of the oracle and of float64."""
+    fp4, e4m3 = T.quantization_map("fp4_e2m1"), T.quantization_map("fp8_e4m3")
+    x, w = _rand((M, K), 31, 3.0), _rand((N, K), 32, 0.02)
+
+    def gscale(t):
+        return (t.float().abs().amax() / (6.0 * 448.0)).clamp_min(torch.finfo(torch.float32).tiny)
+
+    gx, gw = gscale(x), gscale(w)
+    exs, exc = O.quantize_mx(x, fp4, [-1], 16, 6.0, False, e4m3, None, None, gx)
+    ews, ewc = O.quantize_mx(w, fp4, [-1], 16, 6.0, False, e4m3, None, None, gw)
+    alpha = gx * gw
+    exp = O.linear_mx(exc, ewc, input_scale=exs, weight_scale=ews, block_size=16, alpha=alpha)
+    Q = torch.ops.quantized_ops
+    d = lambda t: t.cuda()  # noqa: E731
+    gxs, gxc = Q.quantize_mx(d(x), d(fp4), [-1], 16, 6.0, False, d(e4m3), None, None, d(gx))
+    gws, gwc = Q.quantize_mx(d(w), d(fp4), [-1], 16, 6.0, False, d(e4m3), None, None, d(gw))
+    for g, e, what in ((gxs, exs, "x scale"), (gxc, exc, "x codes"), (gws, ews, "w scale"), (gwc, ewc, "w codes")):
+        assert_same_bits(g, e, what)
+    got = Q.linear_mx(gxc, gwc, input_scale=gxs, weight_scale=gws, block_size=16, alpha=d(alpha))
+    assert got.dtype == exp.dtype and max_rel_err(got, exp) < TOL
+    ref64 = (O.dequantize_mx_parts(exc, exs, None, 16).double() @ O.dequantize_mx_parts(ewc, ews, None, 16).double().T
+             ) * alpha.double()
+    assert max_rel_err(got, ref64) < TOL
