@@ -386,6 +386,30 @@ int vh_spmm_csr(const void* data, int32_t data_dtype, const int32_t* indices, co
                 int64_t b_batch_stride, const float* base, void* out, int32_t out_dtype, int32_t* work,
                 vh_stream_t stream);
 
+/* ------------------------------------------------------------ conv2d
+ * quantized_ops.conv2d (ops/layout.py:170-215) and the convolution of
+ * conv2d_mx (ops/quantized.py:596-643) as im2col + vh_gemm: per group, A
+ * [N*OH*OW, kp] holds each output pixel's input patch (columns (c, kh, kw)
+ * of the group's channels, zero past Cg*KH*KW), B [K/groups, kp] the
+ * group's filters in the same column order; vh_gemm writes the group's
+ * output channels of an NHWC result, vh_nhwc_to_nchw transposes it for an
+ * NCHW layout.  Feature maps NCHW or NHWC (nhwc != 0); weights OIHW, or
+ * HWIO (hwio != 0, dense convolutions only). */
+typedef struct vh_conv_geom {
+  int64_t N, C, H, W; /* input */
+  int64_t K, KH, KW;  /* output channels, filter size */
+  int64_t OH, OW;     /* output size (must follow from the rest, as aten computes it) */
+  int32_t stride[2], padding[2], dilation[2];
+  int32_t groups;
+} vh_conv_geom;
+
+int vh_conv_im2col(const void* x, int32_t dtype, const vh_conv_geom* geom, int32_t nhwc, int32_t group, int64_t kp,
+                   void* a, vh_stream_t stream);
+int vh_conv_pack_weight(const void* w, int32_t dtype, const vh_conv_geom* geom, int32_t hwio, int32_t group,
+                        int64_t kp, void* out, vh_stream_t stream);
+/* dst [n, c, p] = src [n, p, c] (bf16, fp16 or fp32). */
+int vh_nhwc_to_nchw(const void* src, int32_t dtype, int64_t n, int64_t p, int64_t c, void* dst, vh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -356,6 +356,40 @@ def matmul_mx(input, other, input_scale=None, weight_scale=None, block_size=None
     return out.mT.contiguous() if so != "xk" else out
 
 
+# ------------------------------------------------------------ conv2d
+
+def _pair(v):
+    return tuple(v) if isinstance(v, (list, tuple)) else (v, v)
+
+
+def conv2d(input, weight, bias=None, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1,
+           layout="nchw", out_dtype=None):
+    """``quantized_ops.conv2d``, ``ops/layout.py:187-214``: aten's conv2d on
+    NCHW maps, or NHWC ones with an HWIO weight when dense."""
+    assert layout in ("nchw", "nhwc"), layout
+    nhwc = layout == "nhwc"
+    if nhwc:
+        input = input.permute(0, 3, 1, 2)
+        if groups == 1:
+            weight = weight.permute(3, 2, 0, 1)
+    if out_dtype is not None:
+        input, weight = input.float(), weight.float()
+        bias = None if bias is None else bias.float()
+    out = torch.ops.aten.conv2d(input, weight, bias, _pair(stride), _pair(padding), _pair(dilation), groups)
+    if out_dtype is not None:
+        out = out.to(out_dtype)
+    return out.permute(0, 2, 3, 1) if nhwc else out
+
+
+def conv2d_mx(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1, input_scale=None,
+              weight_scale=None, block_size=None, input_code=None, weight_code=None, layout="nchw",
+              out_dtype=None):
+    """``ops/quantized.py:606-643``: both operands decoded, then ``conv2d``."""
+    x = dequantize_mx_parts(input, input_scale, input_code, block_size)
+    w = dequantize_mx_parts(weight, weight_scale, weight_code, block_size)
+    return conv2d(x, w, bias, stride, padding, dilation, groups, layout, out_dtype)
+
+
 # ------------------------------------------------------------ outliers (CSR)
 
 def pad_csr(values, col_indices, crow_indices, max_nnz):

@@ -7,6 +7,6 @@ Importing the package registers the ``quantized_ops`` torch.library namespace
 
 from . import _lib, formats, ops  # noqa: F401  (ops registers the library)
 from . import gemm, packed  # noqa: F401  (gemm registers the GEMM ops)
-from . import decode, sparse  # noqa: F401  (sparse registers the outlier ops)
+from . import conv, decode, sparse  # noqa: F401  (conv and sparse register their ops)
 
-__all__ = ["decode", "formats", "gemm", "ops", "packed", "sparse"]
+__all__ = ["conv", "decode", "formats", "gemm", "ops", "packed", "sparse"]

@@ -120,6 +120,9 @@ _SIGNATURES = {
     "vh_kivi_bake_residual": ([_P, _P, _I64, _I64, _P, _P, _P], _I32),
     # vh_kivi_attention takes a vh_kivi_desc*; voyager_amd.decode.KiviDesc mirrors it.
     "vh_kivi_attention": ([_P, _P], _I32),
+    "vh_conv_im2col": ([_P, _I32, _P, _I32, _I32, _I64, _P, _P], _I32),
+    "vh_conv_pack_weight": ([_P, _I32, _P, _I32, _I32, _I64, _P, _P], _I32),
+    "vh_nhwc_to_nchw": ([_P, _I32, _I64, _I64, _I64, _P, _P], _I32),
     "vh_filter_outlier": ([_P, _I32, _I64, _I64, _I64, _F32, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P], _I32),
     "vh_filter_outlier_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "vh_slice_csr": ([_P, _I32, _P, _P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _P, _P, _P], _I32),

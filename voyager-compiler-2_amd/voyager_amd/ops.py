@@ -2,8 +2,8 @@
 
 Defines the namespace with the reference's schema strings, byte for byte
 (``src/voyager_compiler/ops/quantized.py:147, 449-453, 518-522, 651-658,
-742-748, 958-962, 1070-1075, 1118-1121, 1218-1222, 1286-1289, 1396-1402,
-1493-1497, 1567-1571``; ``ops/layout.py:221-228``),
+596-603, 742-748, 958-962, 1070-1075, 1118-1121, 1218-1222, 1286-1289,
+1396-1402, 1493-1497, 1567-1571``; ``ops/layout.py:176-181, 221-228``),
 a fake (meta) kernel for each op so FX shape propagation works, and a CUDA-key
 kernel (PyTorch-ROCm routes HIP tensors there) that validates arguments,
 allocates outputs with torch's caching allocator and launches the HIP library
@@ -82,6 +82,21 @@ SCHEMAS = {
     ),
     "matmul": (
         f'matmul(Tensor self, Tensor other, *, str layout="{MATMUL_LAYOUT}", '
+        "ScalarType? out_dtype=None) -> Tensor"
+    ),
+    "conv2d": (
+        "conv2d(Tensor input, Tensor weight, Tensor? bias=None, "
+        "SymInt[2] stride=[1, 1], SymInt[2] padding=[0, 0], "
+        "SymInt[2] dilation=[1, 1], SymInt groups=1, *, "
+        'str layout="nchw", ScalarType? out_dtype=None) '
+        "-> Tensor"
+    ),
+    "conv2d_mx": (
+        "conv2d_mx(Tensor input, Tensor weight, Tensor? bias=None, "
+        "SymInt[2] stride=1, SymInt[2] padding=0, SymInt[2] dilation=1, "
+        "SymInt groups=1, *, Tensor? input_scale=None, Tensor? weight_scale=None, "
+        "int? block_size=None, Tensor? input_code=None, "
+        'Tensor? weight_code=None, str layout="nchw", '
         "ScalarType? out_dtype=None) -> Tensor"
     ),
     "filter_outlier": (
