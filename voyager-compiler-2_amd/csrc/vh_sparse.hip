@@ -11,10 +11,10 @@
 // so nothing here is shaped for MFMA:
 //  - filter: one wave per 2048-element row segment writes the inliers,
 //    counts the segment's stored outliers (ballot + mbcnt ranks) and keeps
-//    the first 16 in a workspace; a scan per matrix turns segment counts
-//    into slot starts and row pointers, clamped at the capacity as _pad_csr
-//    does; the fill copies the kept entries to their slots, re-reading only
-//    segments with more.  Capacity slots past the stored entries are padded
+//    the first 16 in a workspace; a scan per matrix turns the rows' counts
+//    into row pointers, clamped at the capacity as _pad_csr does; the fill
+//    copies the kept entries to their slots (row pointer + the row's earlier
+//    segments), re-reading only segments with more.  Capacity slots past the stored entries are padded
 //    by extra workgroups of the fill launch.
 //  - column slice: the same count / scan / fill over each row's segment.
 //  - product: a workgroup stages NT columns of B (all of K, 16- or 32-bit
@@ -99,15 +99,15 @@ __device__ __forceinline__ int64_t block_scan(int64_t v, int64_t* s_wave, int64_
 // A row is cut into segments of SEG elements, one wave each, so a prefill
 // activation gives tens of thousands of waves.  Pass 1 writes the inliers,
 // counts each segment's stored outliers and keeps up to SEG_STAGE of them
-// (value bits and column) in the workspace; the scan turns counts into slot
-// starts; pass 3 copies the kept outliers to their slots, re-reading only
-// segments that held more than SEG_STAGE.
+// (value bits and column) in the workspace; the scan turns the rows' counts
+// into row pointers; pass 3 copies the kept outliers to their slots,
+// re-reading only segments that held more than SEG_STAGE.
 constexpr int SEG = 2048;
 constexpr int SEG_STAGE = 16;
-constexpr int SCAN_ITEMS = 8;
+constexpr int SCAN_ITEMS = 4;  // rows per thread of the row scan
 
 struct FilterWork {
-  int32_t* seg;   // [nseg + 1] counts, then slot starts (seg[nseg]: the total)
+  int32_t* seg;   // [nseg + 1] per-segment counts of stored outliers
   uint32_t* val;  // [nseg][SEG_STAGE] value bits
   int32_t* col;   // [nseg][SEG_STAGE] columns
 };
@@ -245,63 +245,37 @@ __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_count(const raw_t<DT
   if (lane == 0) fw.seg[w] = cnt;
 }
 
-// Pass 2 (one workgroup per matrix): segment counts to slot starts, the
-// total in seg[nseg]; row pointers = starts of each row's first segment,
-// clamped at cap, plus offset.
-__global__ void __launch_bounds__(SCAN_THREADS) k_segment_scan(void* work, int64_t rows, int64_t S, int64_t cap,
-                                                               int32_t offset, int32_t* __restrict__ indptr) {
+// Pass 2 (one workgroup per matrix): row pointers from the segment counts,
+// clamped at cap, plus offset (the counts stay: a segment's slots start at
+// its row's pointer plus the counts of the row's earlier segments).
+// SCAN_ITEMS rows per thread: serial sums, one block scan of the sums.
+__global__ void __launch_bounds__(SCAN_THREADS) k_row_scan(const void* work, int64_t rows, int64_t S, int64_t cap,
+                                                           int32_t offset, int32_t* __restrict__ indptr) {
   __shared__ int64_t s_wave[SCAN_THREADS / 64];
-  // a chunk of counts, one pad word per 16 so a thread's reads hit distinct banks
-  __shared__ int32_t s_tile[SCAN_THREADS * SCAN_ITEMS * 17 / 16];
-  const int64_t nseg = rows * S;
-  const FilterWork fw = filter_work(work, blockIdx.x, nseg);
+  const FilterWork fw = filter_work(const_cast<void*>(work), blockIdx.x, rows * S);
   int32_t* p = indptr + (int64_t)blockIdx.x * (rows + 1);
-  // Chunks of SCAN_THREADS * SCAN_ITEMS counts: coalesced loads into LDS,
-  // SCAN_ITEMS consecutive counts per thread (a serial sum, one block scan
-  // of the thread sums, the thread's starts back to LDS), coalesced stores.
-  // (segment and row counts stay below 2**31: the matrix does)
-  const int32_t n32 = (int32_t)nseg, S32 = (int32_t)S;
-  const int tid = threadIdx.x;
-  auto pad = [](int i) { return i + (i >> 4); };
   int64_t carry = 0;
-  for (int32_t i0 = 0; i0 < n32; i0 += SCAN_THREADS * SCAN_ITEMS) {
+  for (int64_t r0 = 0; r0 < rows; r0 += (int64_t)SCAN_THREADS * SCAN_ITEMS) {
+    const int64_t rb = r0 + (int64_t)threadIdx.x * SCAN_ITEMS;
+    int64_t v[SCAN_ITEMS];
+    int64_t sum = 0;
 #pragma unroll
     for (int k = 0; k < SCAN_ITEMS; ++k) {
-      const int32_t i = i0 + k * SCAN_THREADS + tid;
-      s_tile[pad(k * SCAN_THREADS + tid)] = i < n32 ? fw.seg[i] : 0;
-    }
-    __syncthreads();
-    int32_t v[SCAN_ITEMS];
-    int32_t sum = 0;
-#pragma unroll
-    for (int k = 0; k < SCAN_ITEMS; ++k) {
-      v[k] = s_tile[pad(tid * SCAN_ITEMS + k)];
+      v[k] = 0;
+      if (rb + k < rows)
+        for (int64_t sg = 0; sg < S; ++sg) v[k] += fw.seg[(rb + k) * S + sg];
       sum += v[k];
     }
     int64_t total;
-    int64_t excl = block_scan<false>((int64_t)sum, s_wave, total) - sum + carry;
-    const int32_t ib = i0 + tid * SCAN_ITEMS;
-    int32_t r = ib / S32, rem = ib - r * S32;
+    int64_t excl = block_scan<false>(sum, s_wave, total) - sum + carry;
 #pragma unroll
     for (int k = 0; k < SCAN_ITEMS; ++k) {
-      s_tile[pad(tid * SCAN_ITEMS + k)] = (int32_t)excl;
-      if (ib + k < n32 && rem == 0) p[r] = (int32_t)((excl < cap ? excl : cap) + offset);
+      if (rb + k < rows) p[rb + k] = (int32_t)((excl < cap ? excl : cap) + offset);
       excl += v[k];
-      if (++rem == S32) rem = 0, ++r;
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < SCAN_ITEMS; ++k) {
-      const int32_t i = i0 + k * SCAN_THREADS + tid;
-      if (i < n32) fw.seg[i] = s_tile[pad(k * SCAN_THREADS + tid)];
-    }
-    __syncthreads();
     carry += total;
   }
-  if (threadIdx.x == 0) {
-    fw.seg[nseg] = (int32_t)carry;
-    p[rows] = (int32_t)((carry < cap ? carry : cap) + offset);
-  }
+  if (threadIdx.x == 0) p[rows] = (int32_t)((carry < cap ? carry : cap) + offset);
 }
 
 // Pass 3: each segment's outliers to their slots (below cap): from the
@@ -310,6 +284,7 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_segment_scan(void* work, int64
 template <int DT, int EPV>
 __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_fill(const raw_t<DT>* __restrict__ x, int64_t rows,
                                                                  int64_t cols, int64_t S, float thr, int64_t cap,
+                                                                 int32_t offset, const int32_t* __restrict__ indptr,
                                                                  const void* work, int seg_blocks,
                                                                  raw_t<DT>* __restrict__ data,
                                                                  int32_t* __restrict__ indices) {
@@ -317,10 +292,11 @@ __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_fill(const raw_t<DT>
   const int64_t b = blockIdx.y;
   const int64_t nseg = rows * S;
   const FilterWork fw = filter_work(const_cast<void*>(work), b, nseg);
+  const int32_t* ip = indptr + b * (rows + 1);
   raw_t<DT>* d = data + b * cap;
   int32_t* ix = indices + b * cap;
   if ((int)blockIdx.x >= seg_blocks) {
-    const int64_t nse = fw.seg[nseg];
+    const int64_t nse = (int64_t)ip[rows] - offset;
     const int64_t step = (int64_t)(gridDim.x - seg_blocks) * blockDim.x;
     for (int64_t s = (int64_t)(blockIdx.x - seg_blocks) * blockDim.x + threadIdx.x; s < cap; s += step) {
       if (s >= nse) {
@@ -333,8 +309,12 @@ __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_fill(const raw_t<DT>
   const int lane = threadIdx.x & 63;
   const int64_t w = (int64_t)blockIdx.x * ROW_WAVES + (threadIdx.x >> 6);
   if (w >= nseg) return;
-  const int64_t start = fw.seg[w];
-  const int64_t n = (int64_t)fw.seg[w + 1] - start;
+  // slots start at the row's pointer (clamped: at cap, nothing of the row
+  // is kept) plus the row's earlier segments' counts
+  const int64_t r = w / S;
+  int64_t start = (int64_t)ip[r] - offset;
+  for (int64_t sg = r * S; sg < w && start < cap; ++sg) start += fw.seg[sg];
+  const int64_t n = fw.seg[w];
   if (start >= cap || n == 0) return;
   if (n <= SEG_STAGE) {
     if (lane < n && start + lane < cap) {
@@ -343,7 +323,7 @@ __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_fill(const raw_t<DT>
     }
     return;
   }
-  const int64_t r = w / S, c_begin = (w % S) * SEG;
+  const int64_t c_begin = (w % S) * SEG;
   const int64_t c_end = c_begin + SEG < cols ? c_begin + SEG : cols;
   const int64_t base = (b * rows + r) * cols;
   int64_t pos = start;
@@ -666,13 +646,14 @@ int filter_launch(const void* x, int64_t batch, int64_t rows, int64_t cols, floa
                        (const R*)x, rows, cols, S, thr, (R*)inl, work);
     if (int e = vh::check_launch("vh_filter_outlier")) return e;
   }
-  hipLaunchKernelGGL(k_segment_scan, dim3((unsigned)batch), dim3(SCAN_THREADS), 0, st, work, rows, S, cap, offset,
-                     indptr);
+  hipLaunchKernelGGL(k_row_scan, dim3((unsigned)batch), dim3(SCAN_THREADS), 0, st, (const void*)work, rows, S, cap,
+                     offset, indptr);
   if (int e = vh::check_launch("vh_filter_outlier")) return e;
   const unsigned pads = cap > 0 ? pad_blocks(cap) : 0;
   if (cap == 0 || seg_blocks + pads == 0) return VH_OK;
   hipLaunchKernelGGL((k_outlier_fill<DT, EPV>), dim3(seg_blocks + pads, (unsigned)batch), dim3(ROW_WAVES * 64), 0,
-                     st, (const R*)x, rows, cols, S, thr, cap, (const void*)work, (int)seg_blocks, (R*)data, indices);
+                     st, (const R*)x, rows, cols, S, thr, cap, offset, (const int32_t*)indptr, (const void*)work,
+                     (int)seg_blocks, (R*)data, indices);
   return vh::check_launch("vh_filter_outlier");
 }
 
