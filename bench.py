@@ -608,7 +608,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU design is described in DESIGN.md but not run)", file=sys.stderr)
+              "(the kernels run one GPU's share; sharding across GPUs is designed, not built)", file=sys.stderr)
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
