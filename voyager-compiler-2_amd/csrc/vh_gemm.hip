@@ -161,6 +161,14 @@ __host__ __device__ inline bool lds_epilogue_ok(const void* C, int out_dtype, in
   return out_dtype == VH_BF16 && ((uintptr_t)C % 16) == 0 && (ldc % 8) == 0 && (N % 8) == 0;
 }
 
+// The epilogues of the direct-to-LDS kernels: the bf16 one above, or a
+// float32 result stored from the (transposed) accumulators in 16-byte runs
+// of four columns (store_tile_t_f32), which needs 16-byte aligned rows.
+__host__ __device__ inline bool f8dl_epilogue_ok(const void* C, int out_dtype, int64_t ldc, int64_t N) {
+  if (out_dtype == VH_F32) return ((uintptr_t)C % 16) == 0 && (ldc % 4) == 0;
+  return lds_epilogue_ok(C, out_dtype, ldc, N);
+}
+
 __device__ __forceinline__ float epi_scale(const vh_epilogue& e) {
   if (!e.scale) return 1.0f;
   return e.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)e.scale) : *(const float*)e.scale;
@@ -341,6 +349,40 @@ __device__ __forceinline__ void store_tile_direct(const GemmArgs& g, f32x16 (&ac
         else ((float*)g.C)[row * g.ldc + col] = v;
       }
     }
+  }
+}
+
+// Float32 result of transposed accumulators (B was the row operand: lane l
+// holds row m = l % 32 of each 32 x 32 tile, columns (r / 4) * 8 +
+// (l / 32) * 4 + r % 4): four consecutive columns per 16-byte store.
+template <int TM, int TN>
+__device__ __forceinline__ void store_tile_t_f32(const GemmArgs& g, f32x16 (&acc)[TM][TN], int64_t m0, int64_t n0,
+                                                 int wm, int wn, int lane) {
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const vh_epilogue& e = g.epi;
+  const float sc = epi_scale(e);
+  constexpr int SUBM = TM * 32, SUBN = TN * 32;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t row = m0 + wm * SUBM + i * 32 + lrow;
+    if (row >= g.M) continue;
+    float* crow = (float*)g.C + row * g.ldc;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t col = n0 + wn * SUBN + j * 32 + q * 8 + lhalf * 4;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = epi_value(e, acc[i][j][4 * q + u], sc, col + u < g.N ? epi_bias(e, col + u) : 0.0f);
+        if (col + 3 < g.N) {
+          *(float4*)(crow + col) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (col + u < g.N) crow[col + u] = v[u];
+        }
+      }
   }
 }
 
@@ -1004,10 +1046,14 @@ __device__ __forceinline__ void lds_barrier() {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // Buffer descriptor words of a raw (unswizzled) resource over [p, p + bytes).
+// The words are workgroup-uniform; readfirstlane keeps them in SGPRs, as the
+// inline asm that consumes them requires.
 __device__ __forceinline__ i32x4 raw_desc(const void* p, int64_t bytes) {
   const uint64_t a = (uint64_t)(uintptr_t)p;
   const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
-  return i32x4{(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xffffu), n, RSRC_WORD3};
+  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+               __builtin_amdgcn_readfirstlane((int)(uint32_t)((a >> 32) & 0xffffu)),
+               __builtin_amdgcn_readfirstlane(n), RSRC_WORD3};
 }
 
 // 16 bytes per lane from rsrc + voff straight into LDS at lds + 16 lane.
@@ -1047,7 +1093,7 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   const int64_t bat = blockIdx.y;
   g.A += bat * g.sa;
   g.B += bat * g.sb;
-  g.C = (uint8_t*)g.C + bat * g.sc * 2;
+  g.C = (uint8_t*)g.C + bat * g.sc * (g.epi.out_dtype == VH_F32 ? 4 : 2);
   const int64_t rows_a = (g.M - m0) < BM ? (g.M - m0) : BM;
   const int64_t rows_b = (g.N - n0) < BN ? (g.N - n0) : BN;
   const i32x4 ra = raw_desc(g.A + m0 * g.lda, rows_a * g.lda);
@@ -1186,7 +1232,8 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   // every DMA has landed and every wave is done with the stage buffers
   wait_vmcnt<0>();
   __syncthreads();
-  store_tile_lds_t<TM, TN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+  if (g.epi.out_dtype == VH_F32) store_tile_t_f32<TM, TN>(g, acc, m0, n0, wm, wn, lane);
+  else store_tile_lds_t<TM, TN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
 }
 
 // Tile-rows per column walk for a BM x BN grid: the group whose per-XCD
@@ -1417,7 +1464,7 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       default: return launch_tile<128, 64, 2, 2, 2, 2, AF, BF>(g, batch, st);
     }
   };
-  if (fp8 && lds_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N)) {
+  if (fp8 && f8dl_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N)) {
     if (d->tile_hint == 0) {
       // Direct-to-LDS kernels with 128-byte stages.  Measured on MI355X at
       // M = 2048 (K in {4096, 14336}, N in {1024, 4096, 14336}): the
@@ -1450,7 +1497,7 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
     }
   }
   if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
-  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16 && lds_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N) &&
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16 && f8dl_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N) &&
       (d->tile_hint == 0 || d->tile_hint >= 20)) {
     int bcfg = d->tile_hint;
     if (bcfg == 0) {
