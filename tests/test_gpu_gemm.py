@@ -298,3 +298,23 @@ def test_linear_mx_nvfp4(M, N, K):
     ref64 = (O.dequantize_mx_parts(exc, exs, None, 16).double() @ O.dequantize_mx_parts(ewc, ews, None, 16).double().T
              ) * alpha.double()
     assert max_rel_err(got, ref64) < TOL
+
+
+@pytest.mark.parametrize("M,N,K,batch", [(2048, 1024, 4096, 0), (512, 1030, 256, 0), (300, 520, 136, 3)])
+def test_gemm_float32_results(M, N, K, batch):
+    """Float32 results of the bf16 GEMM (the direct-to-LDS kernel's float32
+    epilogue where the rows allow it): alpha and bias, a ragged N, and a
+    batch (each batch's result at its own offset), against float64."""
+    from voyager_amd import gemm
+
+    g = torch.Generator().manual_seed(M + N)
+    shape_a = (batch, M, K) if batch else (M, K)
+    shape_b = (batch, N, K) if batch else (N, K)
+    a = torch.randn(*shape_a, generator=g).bfloat16()
+    b = (torch.randn(*shape_b, generator=g) * 0.05).bfloat16()
+    bias = torch.randn(N, generator=g).bfloat16()
+    alpha = torch.tensor(0.75)
+    got = gemm.gemm_bf16(a.cuda(), b.cuda(), torch.float32, bias.cuda(), alpha.cuda())
+    ref = (a.double() @ b.double().mT) * 0.75 + bias.double()
+    assert got.dtype == torch.float32 and got.shape == ref.shape
+    assert max_rel_err(got, ref) < 1e-5
