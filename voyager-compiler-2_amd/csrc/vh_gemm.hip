@@ -1501,13 +1501,20 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       (d->tile_hint == 0 || d->tile_hint >= 20)) {
     int bcfg = d->tile_hint;
     if (bcfg == 0) {
+      // As for fp8; a grid under 224 tiles of 128 x 128 takes 128 x 64
+      // (M = 256, K = 4096 on MI355X: N = 4096 in 18.5 us against 24.6 us,
+      // 21.4 against 30.1 with a float32 result; N = 14336, 224 tiles,
+      // stays at 128 x 128: 33.7 us against 46.1).
       const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
-      bcfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : 33;
+      const int64_t t128 = tiles(128, 128) * batch;
+      bcfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : t128 >= 224 ? 33 : 35;
     }
     switch (bcfg) {
       case 41: return launch_f8dl<256, 256, 2, 128, 4, 2, OP_BF16>(g, batch, st);
       case 31: return launch_f8dl<256, 128, 3, 128, 2, 2, OP_BF16>(g, batch, st);
       case 33: return launch_f8dl<128, 128, 4, 128, 2, 2, OP_BF16>(g, batch, st);
+      case 35: return launch_f8dl<128, 64, 4, 128, 2, 2, OP_BF16>(g, batch, st);
+      case 37: return launch_f8dl<64, 128, 4, 128, 1, 4, OP_BF16>(g, batch, st);
       default: break;
     }
   }
