@@ -104,9 +104,22 @@ VH_DEV void store_any(void* p, int dtype, int64_t i, float v) {
   }
 }
 
-// Offset of element `flat`'s parameter.
-VH_DEV int64_t param_offset(const vh_param& p, const Shape& s, int64_t flat) {
+// Offset of element `flat`'s parameter.  `narrow`: the tensor has fewer than
+// 2^31 elements, so every index and dim fits 32-bit unsigned division (a
+// block wider than 2^32 - 1 acts as 2^32 - 1 on such indices).
+VH_DEV int64_t param_offset(const vh_param& p, const Shape& s, int64_t flat, bool narrow) {
   int64_t off = 0;
+  if (narrow) {
+    uint32_t f = (uint32_t)flat;
+    for (int d = s.ndim - 1; d >= 0; --d) {
+      const uint32_t n = (uint32_t)s.dim[d];
+      const uint32_t i = f % n;
+      f /= n;
+      const uint32_t dv = p.div[d] > 0xffffffffll ? 0xffffffffu : (uint32_t)p.div[d];
+      off += (int64_t)(i / dv) * p.stride[d];
+    }
+    return off;
+  }
   for (int d = s.ndim - 1; d >= 0; --d) {
     int64_t n = s.dim[d];
     int64_t i = flat % n;
@@ -130,9 +143,10 @@ constexpr int VEC = 8;
 VH_DEV void param_values(const vh_param& p, const Shape& s, int64_t base, int64_t n, float* v) {
   const int last = s.ndim - 1;
   const int64_t L = last >= 0 ? s.dim[last] : 1;
-  const int64_t c0 = base % L;
+  const bool narrow = n < (1ll << 31);
+  const int64_t c0 = narrow ? (int64_t)((uint32_t)base % (uint32_t)L) : base % L;
   if (last >= 0 && c0 + VEC <= L && base + VEC <= n && L < (1ll << 31)) {
-    const int64_t o0 = param_offset(p, s, base);
+    const int64_t o0 = param_offset(p, s, base, narrow);
     const int32_t dv = (int32_t)p.div[last], q0 = (int32_t)c0 / dv;
     const int32_t q7 = ((int32_t)c0 + VEC - 1) / dv;
     if (q7 == q0 || p.stride[last] == 0) {
@@ -147,7 +161,7 @@ VH_DEV void param_values(const vh_param& p, const Shape& s, int64_t base, int64_
     return;
   }
   for (int j = 0; j < VEC; ++j)
-    if (base + j < n) v[j] = load_any(p.ptr, p.dtype, param_offset(p, s, base + j));
+    if (base + j < n) v[j] = load_any(p.ptr, p.dtype, param_offset(p, s, base + j, narrow));
 }
 
 template <int KIND>
