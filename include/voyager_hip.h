@@ -221,6 +221,19 @@ int vh_gemm(const vh_gemm_desc* desc, vh_stream_t stream);
  * No counterpart in the reference, whose CPU GEMM needs no workspace. */
 int64_t vh_gemm_workspace_bytes(const vh_gemm_desc* desc);
 
+/* The kernel vh_gemm runs for `desc` (the same rule, evaluated on the host;
+ * the output pointer C enters through its alignment): family 1 the
+ * register-staged kernel (tiles 2..10 as tile_hint names them), 2 the
+ * direct-to-LDS kernel on E4M3 operands (tiles 20..43), 3 the direct-to-LDS
+ * kernel on bf16 operands (31, 33, 35, 37, 41), 4 the MX-int8 kernels
+ * (50..56) with `splits` K splits.  No counterpart in the reference, whose
+ * GEMM is one aten call; tests use it to assert which tile a shape takes. */
+#define VH_GEMM_FAMILY_STAGED 1
+#define VH_GEMM_FAMILY_DIRECT_FP8 2
+#define VH_GEMM_FAMILY_DIRECT_BF16 3
+#define VH_GEMM_FAMILY_MXI8 4
+int vh_gemm_plan(const vh_gemm_desc* desc, int32_t* family, int32_t* tile, int32_t* splits);
+
 /* ------------------------------------------------------------ MXNF4 GEMV
  * Decode-shape linear_mx (ops/quantized.py:651-723) for codebook weights
  * with 64-element blocks (lut4_to_int6 + fp8_e5m3 scales), M <= 16.

@@ -88,6 +88,32 @@ def test_mxnf4_cfg3_shapes():
         assert_same_bits(got, exp, f"dequantize_mx {shape}")
 
 
+def test_decode_table_follows_the_codebook_tensor():
+    """dequantize_mx with per-call codebooks (ops/quantized.py:290-315): a
+    second, different 16-entry codebook allocated where a freed one lived
+    (same size, same address, version 0) must decode with its own entries,
+    and an in-place change to a codebook must be seen."""
+    g = torch.Generator().manual_seed(11)
+    codes = torch.randint(0, 16, (64, 128), generator=g).to(torch.bfloat16)
+    scale = torch.pow(2.0, torch.randint(-3, 3, (64, 2), generator=g).float()).bfloat16()
+    books = [torch.randn(16, generator=g).bfloat16() for _ in range(3)]
+    ptrs = []
+    for book in books:
+        dev = book.cuda()
+        ptrs.append(dev.data_ptr())
+        got = torch.ops.quantized_ops.dequantize_mx(codes.cuda(), scale.cuda(), 64, dev)
+        assert_same_bits(got, O.dequantize_mx(codes, scale, 64, book), f"codebook at {dev.data_ptr():#x}")
+        del dev, got
+        torch.cuda.synchronize()
+    # the caching allocator hands the freed block back: the case a pointer-keyed cache got wrong
+    assert len(set(ptrs)) < len(ptrs)
+    dev = books[0].cuda()
+    torch.ops.quantized_ops.dequantize_mx(codes.cuda(), scale.cuda(), 64, dev)
+    dev.mul_(-2)
+    got = torch.ops.quantized_ops.dequantize_mx(codes.cuda(), scale.cuda(), 64, dev)
+    assert_same_bits(got, O.dequantize_mx(codes, scale, 64, (books[0] * -2).bfloat16()), "after an in-place change")
+
+
 def test_mx_generic_paths():
     """Column blocks (axis 0), partial blocks, odd lengths, fp32 input."""
     g = torch.Generator().manual_seed(6)

@@ -1376,6 +1376,102 @@ struct Fmts {
 
 }  // namespace
 
+namespace {
+
+// Kernel families a descriptor can be dispatched to (vh_gemm_plan reports
+// the family and the tile number within it).
+constexpr int FAM_STAGED = 1;       // k_gemm: register-staged, decodes in staging
+constexpr int FAM_DIRECT_FP8 = 2;   // k_gemm_f8dl, E4M3 operands
+constexpr int FAM_DIRECT_BF16 = 3;  // k_gemm_f8dl, bf16 operands
+constexpr int FAM_MXI8 = 4;         // k_gemm_mxi8 / k_gemm_mxi8_ws (+ k_split_reduce)
+
+struct Plan {
+  int family, tile, splits;
+};
+
+bool is_direct_fp8_tile(int c) {
+  switch (c) {
+    case 20: case 21: case 23: case 24: case 30: case 31: case 32: case 33: case 34:
+    case 35: case 36: case 37: case 40: case 41: case 42: case 43: return true;
+    default: return false;
+  }
+}
+
+bool is_direct_bf16_tile(int c) { return c == 31 || c == 33 || c == 35 || c == 37 || c == 41; }
+
+int staged_tile(int c) {
+  switch (c) {
+    case 2: case 3: case 5: case 6: case 7: case 8: case 9: case 10: return c;
+    default: return 4;
+  }
+}
+
+// The one dispatch rule of vh_gemm: which kernel and tile a descriptor runs
+// (after validation), from the operand formats, the output's alignment, the
+// grid size and tile_hint.
+Plan plan_gemm(const vh_gemm_desc* d) {
+  const int64_t batch = d->batch < 1 ? 1 : d->batch;
+  auto tiles = [&](int bm, int bn) { return ((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn) * batch; };
+  const bool fp8 = d->a_fmt == OP_FP8;
+  const bool dl_ok = f8dl_epilogue_ok(d->C, d->epi.out_dtype, d->ldc, d->N);
+  // Register-staged kernel (bf16, MX-int8 and posit8 operands; fp8 when the
+  // LDS epilogue does not apply).  Measured on MI355X at M = 2048 with fp8
+  // data (K in {4096, 14336}, N in {1024, 4096, 14336}): 8-wave blocks (two
+  // waves per SIMD) cover the operand loads; the largest tile that still
+  // fills the GPU wins (less LDS and L2 traffic per MFMA); a grid too small
+  // for 256 CUs takes 128 x 64.
+  int staged = d->tile_hint;
+  if (staged == 0) {
+    if (tiles(256, 256) >= 384) staged = 6;
+    else if (tiles(256, 128) >= 256 && d->K >= 8192) staged = 9;
+    else if (tiles(128, 128) >= 256) staged = 10;
+    else staged = 4;
+  }
+  staged = staged_tile(staged);
+  if (fp8 && dl_ok) {
+    // Direct-to-LDS kernels with 128-byte stages.  Measured on MI355X at
+    // M = 2048 (K in {4096, 14336}, N in {1024, 4096, 14336}): the largest
+    // tile that still gives every CU a block wins, since each CU's operand
+    // stream from L2 is the limit; 256 x 256 only pays when the grid covers
+    // the GPU well over once; a grid too small even for 128 x 128 takes
+    // 64 x 128 (1 x 4 waves).
+    int c = d->tile_hint;
+    if (c == 0) c = tiles(256, 256) >= 384 ? 41 : tiles(256, 128) >= 224 ? 31 : tiles(128, 128) >= 224 ? 33 : 37;
+    if (is_direct_fp8_tile(c)) return {FAM_DIRECT_FP8, c, 1};
+  }
+  if (fp8) return {FAM_STAGED, staged, 1};
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16 && dl_ok && (d->tile_hint == 0 || d->tile_hint >= 20)) {
+    // As for fp8; a grid under 224 tiles of 128 x 128 takes 128 x 64
+    // (M = 256, K = 4096 on MI355X: N = 4096 in 18.5 us against 24.6 us,
+    // 21.4 against 30.1 with a float32 result; N = 14336, 224 tiles, stays
+    // at 128 x 128: 33.7 us against 46.1).
+    int c = d->tile_hint;
+    if (c == 0) c = tiles(256, 256) >= 384 ? 41 : tiles(256, 128) >= 224 ? 31 : tiles(128, 128) >= 224 ? 33 : 35;
+    if (is_direct_bf16_tile(c)) return {FAM_DIRECT_BF16, c, 1};
+  }
+  if (d->a_fmt == OP_MXI8 && d->b_fmt == OP_MXI8) {
+    int mcfg, splits;
+    mxi8_plan(d, mcfg, splits);
+    if (mcfg) {
+      const int64_t need = mxi8_workspace(d, splits);
+      if (splits > 1 && (!d->workspace || d->workspace_bytes < need || (uintptr_t)d->workspace % 16)) splits = 1;
+      return {FAM_MXI8, mcfg, splits};
+    }
+  }
+  return {FAM_STAGED, staged, 1};
+}
+
+}  // namespace
+
+extern "C" int vh_gemm_plan(const vh_gemm_desc* d, int32_t* family, int32_t* tile, int32_t* splits) {
+  VH_REQUIRE(d && family && tile && splits, "vh_gemm_plan: null argument");
+  const Plan p = plan_gemm(d);
+  *family = p.family;
+  *tile = p.tile;
+  *splits = p.splits;
+  return VH_OK;
+}
+
 extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
   VH_REQUIRE(d, "vh_gemm: null descriptor");
   VH_REQUIRE(d->A && d->B && d->C, "vh_gemm: null operand");
@@ -1385,6 +1481,12 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
   VH_REQUIRE(d->a_fmt >= OP_BF16 && d->a_fmt <= OP_P8 && d->b_fmt >= OP_BF16 && d->b_fmt <= OP_P8,
              "vh_gemm: bad operand format");
   VH_REQUIRE(d->epi.out_dtype == VH_BF16 || d->epi.out_dtype == VH_F32, "vh_gemm: output must be bf16 or f32");
+  // the epilogue reads its scalar and bias as bf16 or float32
+  VH_REQUIRE(!d->epi.scale || d->epi.scale_dtype == VH_BF16 || d->epi.scale_dtype == VH_F32,
+             "vh_gemm: epilogue scale must be bf16 or f32");
+  VH_REQUIRE(!d->epi.bias || d->epi.bias_dtype == VH_BF16 || d->epi.bias_dtype == VH_F32,
+             "vh_gemm: bias must be bf16 or f32");
+  VH_REQUIRE(d->epi.mode == EPI_PLAIN || d->epi.mode == EPI_ROUND_SCALE, "vh_gemm: bad epilogue mode");
   // 16-byte aligned rows (the loads are 16 / 8 bytes wide)
   auto rowbytes_ok = [](int fmt, int64_t ld) { return fmt == OP_BF16 ? (ld % 16 == 0) : (ld % 8 == 0); };
   VH_REQUIRE(rowbytes_ok(d->a_fmt, d->lda) && rowbytes_ok(d->b_fmt, d->ldb), "vh_gemm: row pitch misaligned");
@@ -1433,50 +1535,9 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
   const int64_t batch = d->batch < 1 ? 1 : d->batch;
   VH_REQUIRE(batch < 65536, "vh_gemm: batch too large");
   hipStream_t st = vh::as_stream(stream);
-  // Tile choice: enough tiles to fill 256 CUs before growing the tile.
-  auto tiles = [&](int bm, int bn) { return ((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn); };
-  int cfg = d->tile_hint;
-  if (cfg == 0) {
-    // Register-staged kernel (bf16, MX-int8 and posit8 operands; fp8 when
-    // the LDS epilogue does not apply).  Measured on MI355X at M = 2048 with
-    // fp8 data (K in {4096, 14336}, N in {1024, 4096, 14336}): 8-wave
-    // blocks (two waves per SIMD) cover the operand loads; the largest tile
-    // that still fills the GPU wins (less LDS and L2 traffic per MFMA); a
-    // grid too small for 256 CUs takes 128 x 64.
-    const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
-    const int64_t t128 = tiles(128, 128) * batch;
-    if (t256 >= 384) cfg = 6;
-    else if (t2561 >= 256 && d->K >= 8192) cfg = 9;
-    else if (t128 >= 256) cfg = 10;
-    else cfg = 4;
-  }
-  auto pick = [&](auto tag) -> int {
-    constexpr int AF = decltype(tag)::a, BF = decltype(tag)::b;
-    switch (cfg) {
-      case 2: return launch_tile<256, 128, 2, 2, 1, 1, AF, BF>(g, batch, st);
-      case 3: return launch_tile<128, 128, 2, 2, 2, 2, AF, BF>(g, batch, st);
-      case 5: return launch_tile<256, 128, 4, 2, 1, 2, AF, BF>(g, batch, st);
-      case 6: return launch_tile<256, 256, 4, 2, 1, 1, AF, BF>(g, batch, st);
-      case 7: return launch_tile<128, 256, 2, 4, 1, 2, AF, BF>(g, batch, st);
-      case 8: return launch_tile<128, 128, 4, 2, 1, 2, AF, BF>(g, batch, st);
-      case 9: return launch_tile<256, 128, 4, 2, 1, 1, AF, BF>(g, batch, st);
-      case 10: return launch_tile<128, 128, 4, 2, 1, 1, AF, BF>(g, batch, st);
-      default: return launch_tile<128, 64, 2, 2, 2, 2, AF, BF>(g, batch, st);
-    }
-  };
-  if (fp8 && f8dl_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N)) {
-    if (d->tile_hint == 0) {
-      // Direct-to-LDS kernels with 128-byte stages.  Measured on MI355X at
-      // M = 2048 (K in {4096, 14336}, N in {1024, 4096, 14336}): the
-      // largest tile that still gives every CU a block wins, since each
-      // CU's operand stream from L2 is the limit; 256 x 256 only pays when
-      // the grid covers the GPU well over once; a grid too small even for
-      // 128 x 128 takes 64 x 128 (1 x 4 waves).
-      const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
-      const int64_t t128 = tiles(128, 128) * batch;
-      cfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : t128 >= 224 ? 33 : 37;
-    }
-    switch (cfg) {
+  const Plan p = plan_gemm(d);
+  if (p.family == FAM_DIRECT_FP8) {
+    switch (p.tile) {
       case 20: return launch_f8dl<256, 256, 4, 64>(g, batch, st);
       case 21: return launch_f8dl<256, 128, 4, 64>(g, batch, st);
       case 23: return launch_f8dl<128, 128, 8, 64>(g, batch, st);
@@ -1495,21 +1556,8 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       case 37: return launch_f8dl<64, 128, 4, 128, 1, 4>(g, batch, st);
       default: break;
     }
-  }
-  if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
-  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16 && f8dl_epilogue_ok(g.C, g.epi.out_dtype, g.ldc, g.N) &&
-      (d->tile_hint == 0 || d->tile_hint >= 20)) {
-    int bcfg = d->tile_hint;
-    if (bcfg == 0) {
-      // As for fp8; a grid under 224 tiles of 128 x 128 takes 128 x 64
-      // (M = 256, K = 4096 on MI355X: N = 4096 in 18.5 us against 24.6 us,
-      // 21.4 against 30.1 with a float32 result; N = 14336, 224 tiles,
-      // stays at 128 x 128: 33.7 us against 46.1).
-      const int64_t t256 = tiles(256, 256) * batch, t2561 = tiles(256, 128) * batch;
-      const int64_t t128 = tiles(128, 128) * batch;
-      bcfg = t256 >= 384 ? 41 : t2561 >= 224 ? 31 : t128 >= 224 ? 33 : 35;
-    }
-    switch (bcfg) {
+  } else if (p.family == FAM_DIRECT_BF16) {
+    switch (p.tile) {
       case 41: return launch_f8dl<256, 256, 2, 128, 4, 2, OP_BF16>(g, batch, st);
       case 31: return launch_f8dl<256, 128, 3, 128, 2, 2, OP_BF16>(g, batch, st);
       case 33: return launch_f8dl<128, 128, 4, 128, 2, 2, OP_BF16>(g, batch, st);
@@ -1517,28 +1565,36 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       case 37: return launch_f8dl<64, 128, 4, 128, 1, 4, OP_BF16>(g, batch, st);
       default: break;
     }
-  }
-  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16) return pick(Fmts<OP_BF16, OP_BF16>{});
-  if (d->a_fmt == OP_MXI8 && d->b_fmt == OP_MXI8) {
-    int mcfg, splits;
-    mxi8_plan(d, mcfg, splits);
-    if (mcfg) {
-      const int64_t need = mxi8_workspace(d, splits);
-      if (splits > 1 && (!d->workspace || d->workspace_bytes < need || (uintptr_t)d->workspace % 16)) splits = 1;
-      float* part = (float*)d->workspace;
-      switch (mcfg) {
-        case 50: return launch_mxi8<128, 128, 2, 2>(g, splits, part, st);
-        case 51: return launch_mxi8<128, 128, 4, 2>(g, splits, part, st);
-        case 52: return launch_mxi8<128, 64, 2, 2>(g, splits, part, st);
-        case 53: return launch_mxi8<256, 128, 4, 2>(g, splits, part, st);
-        case 54: return launch_mxi8<64, 128, 1, 4>(g, splits, part, st);
-        case 55: return launch_mxi8<128, 128, 2, 2, 2, true>(g, splits, part, st);
-        case 56: return launch_mxi8<256, 128, 2, 2, 2, true>(g, splits, part, st);
-        default: break;
-      }
+  } else if (p.family == FAM_MXI8) {
+    float* part = (float*)d->workspace;
+    switch (p.tile) {
+      case 50: return launch_mxi8<128, 128, 2, 2>(g, p.splits, part, st);
+      case 51: return launch_mxi8<128, 128, 4, 2>(g, p.splits, part, st);
+      case 52: return launch_mxi8<128, 64, 2, 2>(g, p.splits, part, st);
+      case 53: return launch_mxi8<256, 128, 4, 2>(g, p.splits, part, st);
+      case 54: return launch_mxi8<64, 128, 1, 4>(g, p.splits, part, st);
+      case 55: return launch_mxi8<128, 128, 2, 2, 2, true>(g, p.splits, part, st);
+      case 56: return launch_mxi8<256, 128, 2, 2, 2, true>(g, p.splits, part, st);
+      default: break;
     }
-    return pick(Fmts<OP_MXI8, OP_MXI8>{});
   }
+  auto pick = [&](auto tag) -> int {
+    constexpr int AF = decltype(tag)::a, BF = decltype(tag)::b;
+    switch (p.tile) {
+      case 2: return launch_tile<256, 128, 2, 2, 1, 1, AF, BF>(g, batch, st);
+      case 3: return launch_tile<128, 128, 2, 2, 2, 2, AF, BF>(g, batch, st);
+      case 5: return launch_tile<256, 128, 4, 2, 1, 2, AF, BF>(g, batch, st);
+      case 6: return launch_tile<256, 256, 4, 2, 1, 1, AF, BF>(g, batch, st);
+      case 7: return launch_tile<128, 256, 2, 4, 1, 2, AF, BF>(g, batch, st);
+      case 8: return launch_tile<128, 128, 4, 2, 1, 2, AF, BF>(g, batch, st);
+      case 9: return launch_tile<256, 128, 4, 2, 1, 1, AF, BF>(g, batch, st);
+      case 10: return launch_tile<128, 128, 4, 2, 1, 1, AF, BF>(g, batch, st);
+      default: return launch_tile<128, 64, 2, 2, 2, 2, AF, BF>(g, batch, st);
+    }
+  };
+  if (fp8) return pick(Fmts<OP_FP8, OP_FP8>{});
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16) return pick(Fmts<OP_BF16, OP_BF16>{});
+  if (d->a_fmt == OP_MXI8 && d->b_fmt == OP_MXI8) return pick(Fmts<OP_MXI8, OP_MXI8>{});
   if (d->a_fmt == OP_P8 && d->b_fmt == OP_P8) return pick(Fmts<OP_P8, OP_P8>{});
   if (d->a_fmt == OP_BF16 && d->b_fmt == OP_MXI8) return pick(Fmts<OP_BF16, OP_MXI8>{});
   if (d->a_fmt == OP_BF16 && d->b_fmt == OP_P8) return pick(Fmts<OP_BF16, OP_P8>{});

@@ -56,7 +56,26 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+FAMILY_STAGED, FAMILY_DIRECT_FP8, FAMILY_DIRECT_BF16, FAMILY_MXI8 = 1, 2, 3, 4
+
+#: When set to a list, every ``vh_gemm`` launch appends ``(family, tile,
+#: splits, M, N, K)`` of the kernel it runs (``vh_gemm_plan``), so tests can
+#: assert which tile a shape takes.  None (the default) costs nothing.
+plan_log = None
+
+
+def plan(desc: GemmDesc):
+    """``(family, tile, splits)`` of the kernel ``vh_gemm`` runs for ``desc``."""
+    fam, tile, splits = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    st = load().vh_gemm_plan(ctypes.c_void_p(ctypes.addressof(desc)), ctypes.byref(fam), ctypes.byref(tile),
+                             ctypes.byref(splits))
+    _lib.check(st, "vh_gemm_plan")
+    return fam.value, tile.value, splits.value
+
+
 def run(desc: GemmDesc, device) -> None:
+    if plan_log is not None:
+        plan_log.append(plan(desc) + (desc.M, desc.N, desc.K))
     st = load().vh_gemm(ctypes.c_void_p(ctypes.addressof(desc)),
                         ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
     _lib.check(st, "vh_gemm")

@@ -170,6 +170,9 @@ def _match_linear(model: GraphModule, linear: Node) -> "Site | str":
             s = _attr(model, output.args[1])
             if s is None or s.numel() != 1:
                 return "output scale is not a per-tensor constant"
+            if s.dtype not in (torch.bfloat16, torch.float32):
+                # the GEMM epilogue reads its scale as bf16 or float32
+                return f"output scale is {s.dtype}, not bfloat16 or float32"
             out_scale = output.args[1]
         return Site("fp8", linear, output, x, weight, out_scale=out_scale,
                     consts={"scale": x.args[1], "qmap": _arg(x, 5, "qmap")})

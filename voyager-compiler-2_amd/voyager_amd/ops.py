@@ -470,27 +470,29 @@ def _quantize_affine_fake(input, qmap, axes, block_size, quant_min, quant_max, s
 
 
 # ----------------------------------------------------------------- dequantize_mx
-_decode_cache = {}
-
-
 def decode_table(code: torch.Tensor) -> torch.Tensor:
     """The 65,536-entry bfloat16 table of ``decode`` (``ops/quantized.py:290-315``):
     entry ``v`` is ``code[long(v)]`` (negative indices counting from the end,
-    as torch indexing does), NaN where torch would raise."""
-    key = (code.data_ptr(), code._version, code.numel(), code.dtype)
-    hit = _decode_cache.get(key)
-    if hit is not None:
-        return hit
-    v = torch.arange(QMAP_SIZE, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    as torch indexing does), NaN where torch would raise.  Built on the
+    codebook's device with no host round trip, and cached on the codebook
+    tensor itself (a codebook is a graph buffer; an in-place change or a new
+    tensor at a reused address rebuilds it)."""
+    cached = getattr(code, "_vh_decode_table", None)
+    if cached is not None and cached[0] == code._version and cached[1] == code.data_ptr():
+        return cached[2]
+    dev = code.device
+    v = torch.arange(QMAP_SIZE, dtype=torch.int32, device=dev).to(torch.int16).view(torch.bfloat16).float()
     n = code.numel()
-    vals = code.detach().to("cpu", torch.float32)
+    vals = code.detach().reshape(-1).to(torch.float32)
     fin = torch.isfinite(v)
     idx = torch.where(fin, v, torch.zeros_like(v)).trunc().to(torch.int64)
     ok = fin & (idx >= -n) & (idx < n)
     idx = torch.where(idx < 0, idx + n, idx).clamp(0, n - 1)
-    out = torch.where(ok, vals[idx], torch.full_like(v, float("nan")))
-    table = out.to(torch.bfloat16).to(code.device)
-    _decode_cache[key] = table
+    table = torch.where(ok, vals[idx], torch.full_like(v, float("nan"))).to(torch.bfloat16)
+    try:
+        code._vh_decode_table = (code._version, code.data_ptr(), table)
+    except (AttributeError, RuntimeError):
+        pass
     return table
 
 
