@@ -102,7 +102,7 @@ MALL_BYTES = 256 << 20
 
 
 def gpu_bench(args):
-    import voyager_amd  # noqa: F401
+    import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from voyager_amd import formats, gemm, packed
     from voyager_amd.ops import _elementwise
 
@@ -190,7 +190,7 @@ def bench_config1(args):
     """Config 1: MXINT8 linear, X [256,4096] (0.1% outliers x20, seed 0), W
     [4096,4096] N(0,0.02); int8 bs=16 pot scales.  Step = quantize_mx(X) to
     packed codes + scale bytes, then the packed MX-int8 GEMM."""
-    import voyager_amd  # noqa: F401
+    import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from voyager_amd import formats, gemm, packed
 
     dev = torch.device("cuda:0")
@@ -241,7 +241,7 @@ def bench_outliers(args):
     quantize_mx_outlier (threshold 5, a 1% stream) + linear_mx with the CSR
     term, against quantize_mx + linear_mx without it; the spmm_csr of the
     stream with the decoded weight alone; the oracle's step on the host."""
-    import voyager_amd  # noqa: F401
+    import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from voyager_amd import formats, sparse
 
     Q = torch.ops.quantized_ops
@@ -325,7 +325,7 @@ def bench_outliers(args):
 def bench_config3(args):
     """Config 3: MXNF4 decode linear at M in {1, 16} over the four Llama-3.1-8B
     projections; weights baked once, rotated over > 256 MB."""
-    import voyager_amd  # noqa: F401
+    import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from voyager_amd import formats, gemm
 
     dev = torch.device("cuda:0")
@@ -360,7 +360,7 @@ def bench_config3(args):
 def bench_config4(args):
     """Config 4: posit8 (es=1) quantize / dequantize of a 64M-element bf16
     tensor N(0,4), and the posit8 GEMM 2048x4096x4096."""
-    import voyager_amd  # noqa: F401
+    import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from voyager_amd import formats, gemm, packed
 
     dev = torch.device("cuda:0")
@@ -407,7 +407,7 @@ def bench_config5(args):
     residual, this step's).  Two such layers (and caches) alternate in the
     graph, as consecutive layers of a model do, so neither fits the 256 MB
     Infinity Cache; the time of one layer step is half a replay."""
-    import voyager_amd  # noqa: F401
+    import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from oracle import decode as D
     from voyager_amd import decode
 
@@ -570,7 +570,7 @@ def calibrate():
 
 def profile_shapes(reps: int):
     """The config-2 kernels shape by shape, for rocprofv3 counter runs."""
-    import voyager_amd  # noqa: F401
+    import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from voyager_amd import formats, gemm, packed
     from voyager_amd.ops import _elementwise
 

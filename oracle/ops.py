@@ -501,3 +501,82 @@ def per_tensor_scale(x, quant_max):
     sf = torch.where(amax > 0.0, sf, one)
     sf = torch.where(torch.isfinite(amax), sf, one)
     return sf
+
+
+# ------------------------------------------------------------ attention twins
+HADAMARD_SIZE = 16
+
+
+def hadamard_rotate(x, axis, matrix):
+    """``ops/quantized.py:1038-1067``: runs of 16 along ``axis`` (last or
+    second-to-last, zero-padded to whole runs) times ``matrix`` in float32."""
+    axis %= x.ndim
+    assert axis >= x.ndim - 2
+    pad = -x.shape[axis] % HADAMARD_SIZE
+    if pad:
+        x = torch.nn.functional.pad(x, (0, 0) * (x.ndim - 1 - axis) + (0, pad))
+    runs = x.float().unflatten(axis, (-1, HADAMARD_SIZE))
+    m = matrix.float()
+    out = runs @ m if axis == x.ndim - 1 else m.T @ runs
+    return out.flatten(axis, axis + 1).to(x.dtype)
+
+
+def quantize_mx_transpose(input, qmap, block_size, quant_max, force_scale_power_of_two=False, scale_qmap=None,
+                          output_code=None, seed=None, global_scale=None, transpose_seed=None,
+                          transpose_global_scale=None, hadamard=None):
+    """``ops/quantized.py:1168-1215``."""
+    t = input.mT
+    if hadamard is not None:
+        t = hadamard_rotate(t, -1, hadamard)
+    args = (qmap, (-1,), block_size, quant_max, force_scale_power_of_two, scale_qmap, output_code)
+    return (*quantize_mx(input, *args, seed, global_scale), *quantize_mx(t, *args, transpose_seed,
+                                                                         transpose_global_scale))
+
+
+def _masked(scores, mask):
+    """``ops/quantized.py:924-932``."""
+    if mask is None:
+        return scores
+    if mask.dtype == torch.bool:
+        return scores.masked_fill(~mask, float("-inf"))
+    return scores + mask
+
+
+def sdpa_mx(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, query_residual=None,
+            key_residual=None, value_residual=None, residual_mask=None, scale=None, enable_gqa=False,
+            query_scale=None, key_scale=None, value_scale=None, block_size=None, input_code=None,
+            weight_code=None, probs_qmap=None, probs_quant_max=None, probs_scale_qmap=None, probs_code=None,
+            force_scale_power_of_two=False):
+    """``ops/quantized.py:834-921``."""
+    if is_causal and attn_mask is not None:
+        raise ValueError("is_causal excludes an explicit attn_mask")
+    query = dequantize_mx_parts(query, query_scale, input_code, block_size)
+    key = dequantize_mx_parts(key, key_scale, weight_code, block_size)
+    value = dequantize_mx_parts(value, value_scale, weight_code, block_size)
+    residual = key_residual is not None
+    if enable_gqa:
+        g = query.shape[-3] // key.shape[-3]
+        key, value = key.repeat_interleave(g, dim=-3), value.repeat_interleave(g, dim=-3)
+        if residual:
+            key_residual = key_residual.repeat_interleave(g, dim=-3)
+            value_residual = value_residual.repeat_interleave(g, dim=-3)
+    if scale is None:
+        scale = 1.0 / math.sqrt(query.shape[-1])
+    scores = torch.matmul(query, key.transpose(-1, -2)) * scale
+    if is_causal:
+        attn_mask = torch.ones(scores.shape[-2:], dtype=torch.bool).tril()
+    scores = _masked(scores, attn_mask)
+    keys = scores.shape[-1]
+    if residual:
+        rs = _masked((query_residual @ key_residual.transpose(-1, -2)) * scale, residual_mask)
+        scores = torch.cat([scores, rs], dim=-1)
+    probs = torch.softmax(scores, dim=-1)
+    probs, residual_probs = probs[..., :keys], probs[..., keys:]
+    if probs_qmap is not None:
+        ps, probs = quantize_mx(probs, probs_qmap, [-1], block_size, probs_quant_max, force_scale_power_of_two,
+                                probs_scale_qmap, probs_code)
+        probs = dequantize_mx_parts(probs, ps, input_code, block_size)
+    out = torch.matmul(probs, value)
+    if residual:
+        out = out + torch.matmul(residual_probs, value_residual)
+    return out

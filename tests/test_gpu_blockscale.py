@@ -4,7 +4,7 @@ GPU against the oracle, at the configs' shapes and on edge blocks."""
 import pytest
 import torch
 
-import voyager_amd  # noqa: F401  (registers quantized_ops)
+import voyager_amd.library  # noqa: F401  (defines quantized_ops)
 from helpers import assert_same_bits
 from oracle import ops as O
 from oracle import tables as T

@@ -6,7 +6,7 @@ of the same operands."""
 import pytest
 import torch
 
-import voyager_amd  # noqa: F401  (registers quantized_ops)
+import voyager_amd.library  # noqa: F401  (defines quantized_ops)
 from helpers import assert_within_bf16_ulps, max_rel_err
 from oracle import ops as O
 from oracle import tables as T

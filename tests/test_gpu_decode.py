@@ -5,7 +5,7 @@ quantization, KIVI attention and the whole layer."""
 import pytest
 import torch
 
-import voyager_amd  # noqa: F401
+import voyager_amd.library  # noqa: F401  (defines quantized_ops)
 from helpers import assert_within_bf16_ulps, max_rel_err
 from oracle import decode as D
 from voyager_amd import _lib, decode

@@ -4,7 +4,7 @@ out, fp32 accumulation) and, where cheap, a float64 matmul."""
 import pytest
 import torch
 
-import voyager_amd  # noqa: F401  (registers quantized_ops)
+import voyager_amd.library  # noqa: F401  (defines quantized_ops)
 from helpers import assert_same_bits, max_rel_err
 from oracle import ops as O
 from oracle import tables as T

@@ -13,7 +13,7 @@ float32 product of the same operand values."""
 import pytest
 import torch
 
-import voyager_amd  # noqa: F401  (registers quantized_ops)
+import voyager_amd.library  # noqa: F401  (defines quantized_ops)
 from helpers import max_rel_err
 from oracle import ops as O
 from oracle import tables as T

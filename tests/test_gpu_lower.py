@@ -5,7 +5,7 @@ the converted graph's (1e-2 max-abs-normalized, the GEMM tolerance)."""
 import pytest
 import torch
 
-import voyager_amd  # noqa: F401  (registers quantized_ops)
+import voyager_amd.library  # noqa: F401  (defines quantized_ops)
 from helpers import max_rel_err
 from oracle import ops as O
 from oracle import tables as T

@@ -4,7 +4,7 @@ a device it cannot run (backend/gpu/__init__.py:102-131)."""
 
 import torch
 
-import voyager_amd  # noqa: F401  (registers quantized_ops)
+import voyager_amd.library  # noqa: F401  (defines quantized_ops)
 from voyager_amd import lower
 from oracle import tables as T
 

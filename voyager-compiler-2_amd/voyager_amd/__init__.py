@@ -1,12 +1,15 @@
 """MI355X-native (gfx950) execution of Voyager's quantized-operator path.
 
-Importing the package registers the ``quantized_ops`` torch.library namespace
-(``voyager_amd.ops``) whose CUDA-key kernels launch the HIP library
-``_lib/libvoyager_hip.so`` through its C ABI (``include/voyager_hip.h``).
+The ``quantized_ops`` kernels launch the HIP library ``_lib/libvoyager_hip.so``
+through its C ABI (``include/voyager_hip.h``).  Importing the package
+registers nothing:
+
+* ``import voyager_amd.library`` defines the ``quantized_ops`` namespace
+  standalone (the reference's schema strings) with these kernels bound;
+* ``voyager_amd.kernels.register(lib)`` binds them onto a namespace another
+  library defined -- the reference's ``quantized_ops_lib``.
 """
 
-from . import _lib, formats, ops  # noqa: F401  (ops registers the library)
-from . import gemm, packed  # noqa: F401  (gemm registers the GEMM ops)
-from . import conv, decode, sparse  # noqa: F401  (conv and sparse register their ops)
+from . import _lib, formats  # noqa: F401
 
-__all__ = ["conv", "decode", "formats", "gemm", "ops", "packed", "sparse"]
+__all__ = ["formats"]

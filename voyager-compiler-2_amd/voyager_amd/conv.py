@@ -21,7 +21,8 @@ import torch
 from . import _lib
 from ._lib import VH_BF16, dtype_code, load, ptr, stream_of
 from .gemm import EPI_PLAIN, OP_BF16, GemmDesc, _decode, _epilogue, run
-from .ops import _require_gpu, lib
+from .ops import _require_gpu
+from .registry import cuda_kernel, fake_kernel
 
 TENSOR_LAYOUTS = ("nchw", "nhwc")
 
@@ -122,8 +123,8 @@ def _conv2d_mx_cuda(input, weight, bias=None, stride=1, padding=0, dilation=1, g
                         out_dtype=out_dtype)
 
 
-lib.impl("conv2d", _conv2d_cuda, "CUDA")
-lib.impl("conv2d_mx", _conv2d_mx_cuda, "CUDA")
+cuda_kernel("conv2d")(_conv2d_cuda)
+cuda_kernel("conv2d_mx")(_conv2d_mx_cuda)
 
 
 def _conv_shape(input, weight, stride, padding, dilation, groups, layout):
@@ -140,14 +141,14 @@ def _conv_shape(input, weight, stride, padding, dilation, groups, layout):
     return (N, OH, OW, K) if nhwc else (N, K, OH, OW)
 
 
-@torch.library.register_fake("quantized_ops::conv2d")
+@fake_kernel("conv2d")
 def _conv2d_fake(input, weight, bias=None, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1, *,
                  layout="nchw", out_dtype=None):
     shape = _conv_shape(input, weight, stride, padding, dilation, groups, layout)
     return input.new_empty(shape, dtype=input.dtype if out_dtype is None else out_dtype)
 
 
-@torch.library.register_fake("quantized_ops::conv2d_mx")
+@fake_kernel("conv2d_mx")
 def _conv2d_mx_fake(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1, *,
                     input_scale=None, weight_scale=None, block_size=None, input_code=None, weight_code=None,
                     layout="nchw", out_dtype=None):

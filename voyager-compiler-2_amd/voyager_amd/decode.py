@@ -22,6 +22,7 @@ import torch
 
 from . import _lib, formats, packed
 from ._lib import check, load, ptr
+from .ops import _quantize_affine_cuda
 
 MX_BLOCK = 16
 KIVI_GROUP = 32
@@ -174,8 +175,8 @@ class KiviCache:
         if T:
             qtab = formats.quantization_map("uint2", dev)
             stab = formats.quantization_map("fp16_e5m10", dev)
-            kq = torch.ops.quantized_ops.quantize_affine(k_main, qtab, [-2], KIVI_GROUP, 0.0, 3.0, stab)
-            vq = torch.ops.quantized_ops.quantize_affine(v_main, qtab, [-1], KIVI_GROUP, 0.0, 3.0, stab)
+            kq = _quantize_affine_cuda(k_main, qtab, [-2], KIVI_GROUP, 0.0, 3.0, stab)
+            vq = _quantize_affine_cuda(v_main, qtab, [-1], KIVI_GROUP, 0.0, 3.0, stab)
             c.load_main(kq, vq)
         c.load_residual(k_res, v_res)
         return c, kq, vq

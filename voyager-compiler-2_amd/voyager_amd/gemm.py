@@ -17,7 +17,9 @@ import torch
 
 from . import _lib, formats
 from ._lib import VH_BF16, VH_F32, dtype_code, load, ptr, stream_of
-from .ops import LINEAR_LAYOUT, MATMUL_LAYOUT, _require_gpu, decode_table, lib
+from .ops import _dequantize_mx_cuda, _require_gpu, _vmap_cuda, decode_table
+from .registry import cuda_kernel, fake_kernel
+from .schemas import LINEAR_LAYOUT, MATMUL_LAYOUT
 
 OP_BF16, OP_FP8, OP_MXI8, OP_P8 = 0, 1, 2, 3
 EPI_PLAIN, EPI_ROUND_SCALE = 0, 1
@@ -170,8 +172,8 @@ def _matmul_cuda(input, other, *, layout=MATMUL_LAYOUT, out_dtype=None):
     return _gemm_in_layout(input, other, layout, out_dtype, None, MATMUL_LAYOUT)
 
 
-lib.impl("linear", _linear_cuda, "CUDA")
-lib.impl("matmul", _matmul_cuda, "CUDA")
+cuda_kernel("linear")(_linear_cuda)
+cuda_kernel("matmul")(_matmul_cuda)
 
 
 def _gemm_shape(a, b, layout, bias, out_dtype):
@@ -188,13 +190,13 @@ def _gemm_shape(a, b, layout, bias, out_dtype):
     return shape, dtype
 
 
-@torch.library.register_fake("quantized_ops::linear")
+@fake_kernel("linear")
 def _linear_fake(input, weight, bias=None, *, layout=LINEAR_LAYOUT, out_dtype=None):
     shape, dtype = _gemm_shape(input, weight, layout, bias, out_dtype)
     return input.new_empty(shape, dtype=dtype)
 
 
-@torch.library.register_fake("quantized_ops::matmul")
+@fake_kernel("matmul")
 def _matmul_fake(input, other, *, layout=MATMUL_LAYOUT, out_dtype=None):
     shape, dtype = _gemm_shape(input, other, layout, None, out_dtype)
     return input.new_empty(shape, dtype=dtype)
@@ -206,8 +208,8 @@ def _decode(x, scale, code, block_size):
     if code is None and scale is None:
         return x
     if scale is None:
-        return torch.ops.quantized_ops.vmap(x, decode_table(code)) if code is not None else x
-    return torch.ops.quantized_ops.dequantize_mx(x, scale, block_size, code)
+        return _vmap_cuda(x, decode_table(code)) if code is not None else x
+    return _dequantize_mx_cuda(x, scale, block_size, code)
 
 
 def _mx_common(kind, x, w, bias, input_scale, weight_scale, block_size, input_code, weight_code, alpha, A_data,
@@ -251,17 +253,17 @@ def _matmul_mx_cuda(self, other, *, input_scale=None, weight_scale=None, block_s
                       weight_code, alpha, A_data, A_indices, A_indptr, layout, out_dtype)
 
 
-lib.impl("linear_mx", _linear_mx_cuda, "CUDA")
-lib.impl("matmul_mx", _matmul_mx_cuda, "CUDA")
+cuda_kernel("linear_mx")(_linear_mx_cuda)
+cuda_kernel("matmul_mx")(_matmul_mx_cuda)
 
 
-@torch.library.register_fake("quantized_ops::linear_mx")
+@fake_kernel("linear_mx")
 def _linear_mx_fake(input, weight, bias=None, **kwargs):
     shape, dtype = _gemm_shape(input, weight, kwargs.get("layout", LINEAR_LAYOUT), bias, kwargs.get("out_dtype"))
     return input.new_empty(shape, dtype=dtype)
 
 
-@torch.library.register_fake("quantized_ops::matmul_mx")
+@fake_kernel("matmul_mx")
 def _matmul_mx_fake(self, other, **kwargs):
     shape, dtype = _gemm_shape(self, other, kwargs.get("layout", MATMUL_LAYOUT), None, kwargs.get("out_dtype"))
     return self.new_empty(shape, dtype=dtype)

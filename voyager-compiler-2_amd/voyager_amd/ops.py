@@ -24,106 +24,8 @@ from ._lib import Format, Param, VH_U8, dtype_code, load, ptr, stream_of
 
 QMAP_SIZE = formats.QMAP_SIZE
 
-LINEAR_LAYOUT = "xc,kc->xk"
-MATMUL_LAYOUT = "xc,ck->xk"
-
-lib = torch.library.Library("quantized_ops", "DEF")
-
-SCHEMAS = {
-    "vmap": "vmap(Tensor self, Tensor other) -> Tensor",
-    "quantize": (
-        "quantize(Tensor input, Tensor scale, Tensor? zero_point=None, "
-        "SymInt[]? axes=None, int? block_size=None, Tensor? qmap=None, "
-        "Tensor? output_code=None, Tensor? seed=None) -> Tensor"
-    ),
-    "dequantize": (
-        "dequantize(Tensor input, Tensor scale, Tensor? zero_point=None, "
-        "SymInt[]? axes=None, int? block_size=None, Tensor? input_qmap=None, "
-        "Tensor? output_qmap=None) -> Tensor"
-    ),
-    "linear_mx": (
-        "linear_mx(Tensor input, Tensor weight, Tensor? bias=None, *, "
-        "Tensor? input_scale=None, Tensor? weight_scale=None, "
-        "int? block_size=None, Tensor? input_code=None, Tensor? weight_code=None, "
-        "Tensor? alpha=None, Tensor? A_data=None, Tensor? A_indices=None, "
-        f'Tensor? A_indptr=None, str layout="{LINEAR_LAYOUT}", '
-        "ScalarType? out_dtype=None) -> Tensor"
-    ),
-    "matmul_mx": (
-        "matmul_mx(Tensor self, Tensor other, *, Tensor? input_scale=None, "
-        "Tensor? weight_scale=None, int? block_size=None, Tensor? input_code=None, "
-        "Tensor? weight_code=None, Tensor? alpha=None, Tensor? A_data=None, "
-        "Tensor? A_indices=None, Tensor? A_indptr=None, "
-        f'str layout="{MATMUL_LAYOUT}", ScalarType? out_dtype=None) -> Tensor'
-    ),
-    "calculate_mx_qparam": (
-        "calculate_mx_qparam(Tensor self, SymInt[] axes, int block_size, "
-        "float quant_max, bool force_scale_power_of_two=False, "
-        "Tensor scale_qmap=None, Tensor? global_scale=None) -> Tensor"
-    ),
-    "quantize_mx": (
-        "quantize_mx(Tensor self, Tensor qmap, SymInt[] axes, int block_size, "
-        "float quant_max, bool force_scale_power_of_two=False, "
-        "Tensor scale_qmap=None, Tensor output_code=None, Tensor? seed=None, "
-        "Tensor? global_scale=None) -> (Tensor, Tensor)"
-    ),
-    "dequantize_mx": (
-        "dequantize_mx(Tensor self, Tensor scale, int block_size, "
-        "Tensor? code=None, Tensor? global_scale=None) -> Tensor"
-    ),
-    "quantize_affine": (
-        "quantize_affine(Tensor self, Tensor qmap, SymInt[] axes, int block_size, "
-        "float quant_min, float quant_max, Tensor scale_qmap=None) "
-        "-> (Tensor, Tensor, Tensor)"
-    ),
-    "linear": (
-        "linear(Tensor input, Tensor weight, Tensor? bias=None, *, "
-        f'str layout="{LINEAR_LAYOUT}", ScalarType? out_dtype=None) -> Tensor'
-    ),
-    "matmul": (
-        f'matmul(Tensor self, Tensor other, *, str layout="{MATMUL_LAYOUT}", '
-        "ScalarType? out_dtype=None) -> Tensor"
-    ),
-    "conv2d": (
-        "conv2d(Tensor input, Tensor weight, Tensor? bias=None, "
-        "SymInt[2] stride=[1, 1], SymInt[2] padding=[0, 0], "
-        "SymInt[2] dilation=[1, 1], SymInt groups=1, *, "
-        'str layout="nchw", ScalarType? out_dtype=None) '
-        "-> Tensor"
-    ),
-    "conv2d_mx": (
-        "conv2d_mx(Tensor input, Tensor weight, Tensor? bias=None, "
-        "SymInt[2] stride=1, SymInt[2] padding=0, SymInt[2] dilation=1, "
-        "SymInt groups=1, *, Tensor? input_scale=None, Tensor? weight_scale=None, "
-        "int? block_size=None, Tensor? input_code=None, "
-        'Tensor? weight_code=None, str layout="nchw", '
-        "ScalarType? out_dtype=None) -> Tensor"
-    ),
-    "filter_outlier": (
-        "filter_outlier(Tensor input, float threshold, float max_pct=0.01) "
-        "-> (Tensor, Tensor, Tensor, Tensor)"
-    ),
-    "quantize_mx_outlier": (
-        "quantize_mx_outlier(Tensor self, Tensor qmap, SymInt[] axes, "
-        "int block_size, float quant_max, bool force_scale_power_of_two=False, "
-        "Tensor scale_qmap=None, Tensor output_code=None, float? threshold=None, "
-        "float max_pct=0.01, SymInt indptr_offset=0) "
-        "-> (Tensor, Tensor, Tensor, Tensor, Tensor)"
-    ),
-    "slice_csr_tensor": (
-        "slice_csr_tensor(Tensor data, Tensor indices, Tensor indptr, int dim=0, "
-        "SymInt? start=None, SymInt? end=None, float size_factor=1.0) "
-        "-> (Tensor, Tensor, Tensor)"
-    ),
-    "spmm_csr": (
-        "spmm_csr(Tensor data, Tensor indices, Tensor indptr, Tensor B, "
-        "Tensor? B_scale=None, Tensor? B_code=None, int? block_size=None, "
-        'str weight_layout="kc", *, ScalarType? out_dtype=None) -> Tensor'
-    ),
-}
-
-for _schema in SCHEMAS.values():
-    lib.define(_schema)
+from .registry import cuda_kernel, fake_kernel
+from .schemas import LINEAR_LAYOUT, MATMUL_LAYOUT, SCHEMAS  # noqa: F401
 
 
 # ----------------------------------------------------------------- helpers
@@ -246,10 +148,10 @@ def _vmap_cuda(input, qmap):
     return _elementwise("quantize", input, None, None, None, input.dtype, c.fmt, None, input.dtype)
 
 
-lib.impl("vmap", _vmap_cuda, "CUDA")
+cuda_kernel("vmap")(_vmap_cuda)
 
 
-@torch.library.register_fake("quantized_ops::vmap")
+@fake_kernel("vmap")
 def _vmap_fake(input, qmap):
     return torch.empty_like(input)
 
@@ -303,10 +205,10 @@ def _quantize_cuda(input, scale, zero_point=None, axes=None, block_size=None, qm
     return _elementwise("quantize", input, scale, zero_point, block_size, cdt, fmt, None, cdt)
 
 
-lib.impl("quantize", _quantize_cuda, "CUDA")
+cuda_kernel("quantize")(_quantize_cuda)
 
 
-@torch.library.register_fake("quantized_ops::quantize")
+@fake_kernel("quantize")
 def _quantize_fake(input, scale, zero_point=None, axes=None, block_size=None, qmap=None,
                    output_code=None, seed=None):
     return torch.empty_like(input, dtype=_quantize_dtype(input, scale, zero_point))
@@ -330,10 +232,10 @@ def _dequantize_cuda(input, scale, zero_point=None, axes=None, block_size=None, 
     return _elementwise("dequantize", input, scale, zero_point, block_size, cdt, fi, fo, cdt)
 
 
-lib.impl("dequantize", _dequantize_cuda, "CUDA")
+cuda_kernel("dequantize")(_dequantize_cuda)
 
 
-@torch.library.register_fake("quantized_ops::dequantize")
+@fake_kernel("dequantize")
 def _dequantize_fake(input, scale, zero_point=None, axes=None, block_size=None, input_qmap=None,
                      output_qmap=None):
     return torch.empty_like(input, dtype=_dequantize_dtype(input, scale, zero_point))
@@ -396,10 +298,10 @@ def _calculate_mx_qparam_cuda(input, axes, block_size, quant_max, force_scale_po
     return scale
 
 
-lib.impl("calculate_mx_qparam", _calculate_mx_qparam_cuda, "CUDA")
+cuda_kernel("calculate_mx_qparam")(_calculate_mx_qparam_cuda)
 
 
-@torch.library.register_fake("quantized_ops::calculate_mx_qparam")
+@fake_kernel("calculate_mx_qparam")
 def _calculate_mx_qparam_fake(input, axes, block_size, quant_max, force_scale_power_of_two=False,
                               scale_qmap=None, global_scale=None):
     axes = [axes] if isinstance(axes, int) else list(axes)
@@ -425,10 +327,10 @@ def _quantize_mx_cuda(input, qmap, axes, block_size, quant_max, force_scale_powe
                       True)
 
 
-lib.impl("quantize_mx", _quantize_mx_cuda, "CUDA")
+cuda_kernel("quantize_mx")(_quantize_mx_cuda)
 
 
-@torch.library.register_fake("quantized_ops::quantize_mx")
+@fake_kernel("quantize_mx")
 def _quantize_mx_fake(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
                       scale_qmap=None, output_code=None, seed=None, global_scale=None):
     axes = [axes] if isinstance(axes, int) else list(axes)
@@ -459,10 +361,10 @@ def _quantize_affine_cuda(input, qmap, axes, block_size, quant_min, quant_max, s
     return scale, zp, codes
 
 
-lib.impl("quantize_affine", _quantize_affine_cuda, "CUDA")
+cuda_kernel("quantize_affine")(_quantize_affine_cuda)
 
 
-@torch.library.register_fake("quantized_ops::quantize_affine")
+@fake_kernel("quantize_affine")
 def _quantize_affine_fake(input, qmap, axes, block_size, quant_min, quant_max, scale_qmap=None):
     ax = axes[0] % input.dim()
     s = input.new_empty(_scale_shape(input, ax, block_size))
@@ -510,10 +412,10 @@ def _dequantize_mx_cuda(input, scale, block_size, code=None, global_scale=None):
     return out
 
 
-lib.impl("dequantize_mx", _dequantize_mx_cuda, "CUDA")
+cuda_kernel("dequantize_mx")(_dequantize_mx_cuda)
 
 
-@torch.library.register_fake("quantized_ops::dequantize_mx")
+@fake_kernel("dequantize_mx")
 def _dequantize_mx_fake(input, scale, block_size, code=None, global_scale=None):
     dtype = torch.promote_types(input.dtype, scale.dtype)
     if global_scale is not None:

@@ -31,7 +31,8 @@ import torch
 
 from . import _lib
 from ._lib import dtype_code, load, ptr, stream_of
-from .ops import _require_gpu, lib
+from .ops import _quantize_mx_cuda, _require_gpu
+from .registry import cuda_kernel, fake_kernel
 
 FLOAT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 _LAYOUTS = {"kc": 0, "ck": 1}
@@ -101,16 +102,16 @@ def _quantize_mx_outlier_cuda(self, qmap, axes, block_size, quant_max, force_sca
     """``ops/quantized.py:1405-1458``: the filter, then ``quantize_mx`` of
     the inliers; ``(data, indices, indptr, scale, inliers)``."""
     data, indices, indptr, inliers = filter_outlier(self, threshold, max_pct, indptr_offset)
-    scale, codes = torch.ops.quantized_ops.quantize_mx(inliers, qmap, axes, block_size, quant_max,
-                                                       force_scale_power_of_two, scale_qmap, output_code)
+    scale, codes = _quantize_mx_cuda(inliers, qmap, axes, block_size, quant_max, force_scale_power_of_two,
+                                     scale_qmap, output_code)
     return data, indices, indptr, scale, codes
 
 
-lib.impl("filter_outlier", _filter_outlier_cuda, "CUDA")
-lib.impl("quantize_mx_outlier", _quantize_mx_outlier_cuda, "CUDA")
+cuda_kernel("filter_outlier")(_filter_outlier_cuda)
+cuda_kernel("quantize_mx_outlier")(_quantize_mx_outlier_cuda)
 
 
-@torch.library.register_fake("quantized_ops::filter_outlier")
+@fake_kernel("filter_outlier")
 def _filter_outlier_fake(input, threshold, max_pct=0.01):
     batch_shape = input.shape[:-2]
     cap = _max_nnz(input.shape[-2:], max_pct)
@@ -120,7 +121,7 @@ def _filter_outlier_fake(input, threshold, max_pct=0.01):
     return data, indices, indptr, torch.empty_like(input)
 
 
-@torch.library.register_fake("quantized_ops::quantize_mx_outlier")
+@fake_kernel("quantize_mx_outlier")
 def _quantize_mx_outlier_fake(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
                               scale_qmap=None, output_code=None, threshold=None, max_pct=0.01, indptr_offset=0):
     batch_shape = input.shape[:-2]
@@ -173,10 +174,10 @@ def _slice_csr_tensor_cuda(data, indices, indptr, dim=0, start=None, end=None, s
     return out_data, out_indices, out_indptr.to(indptr.dtype)
 
 
-lib.impl("slice_csr_tensor", _slice_csr_tensor_cuda, "CUDA")
+cuda_kernel("slice_csr_tensor")(_slice_csr_tensor_cuda)
 
 
-@torch.library.register_fake("quantized_ops::slice_csr_tensor")
+@fake_kernel("slice_csr_tensor")
 def _slice_csr_tensor_fake(data, indices, indptr, dim=0, start=None, end=None, size_factor=1.0):
     fake_indptr = torch.empty_like(indptr)
     if dim == 0 or dim == -2:
@@ -240,10 +241,10 @@ def _spmm_csr_cuda(data, indices, indptr, B, B_scale=None, B_code=None, block_si
     return spmm_into(data, indices, indptr, Bd, weight_layout, Bd.dtype if out_dtype is None else out_dtype)
 
 
-lib.impl("spmm_csr", _spmm_csr_cuda, "CUDA")
+cuda_kernel("spmm_csr")(_spmm_csr_cuda)
 
 
-@torch.library.register_fake("quantized_ops::spmm_csr")
+@fake_kernel("spmm_csr")
 def _spmm_csr_fake(data, indices, indptr, B, B_scale=None, B_code=None, block_size=None, weight_layout="kc", *,
                    out_dtype=None):
     batch_shape = indptr.shape[:-1]
