@@ -375,6 +375,20 @@ int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, int64_t rows,
  * Tensor.to_sparse_csr. */
 int64_t vh_filter_outlier_workspace_bytes(int64_t batch, int64_t rows, int64_t cols);
 
+/* vh_filter_outlier with no workspace argument and no allocation, for
+ * callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  No counterpart in
+ * the reference.  The workspace is the library's own fixed scratch of
+ * VH_FILTER_NOALLOC_SCRATCH_BYTES per GPU (a device array each GPU the
+ * library runs on holds until the process ends); sizes whose
+ * vh_filter_outlier_workspace_bytes exceed it return VH_EINVAL with a
+ * message.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (different streams, threads) race. */
+#define VH_FILTER_NOALLOC_SCRATCH_BYTES (8ll << 20)
+int vh_filter_outlier_noalloc(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
+                              float threshold, int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices,
+                              int32_t* indptr, void* inliers, vh_stream_t stream);
+
 /* slice_csr_tensor (ops/quantized.py:1493-1545) of one CSR matrix with
  * `rows` rows and `cap` slots (indptr[0] == 0), to out_cap slots.
  * dim 0: rows [start, end), pointers rebased to 0.  dim 1: columns

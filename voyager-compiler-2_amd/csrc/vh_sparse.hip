@@ -25,6 +25,8 @@
 //    (one address per NT lanes).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "vh_device.h"
 #include "vh_host.h"
 
@@ -664,10 +666,13 @@ extern "C" int64_t vh_filter_outlier_workspace_bytes(int64_t batch, int64_t rows
   return batch * filter_work_bytes_per_matrix(rows * ((cols + SEG - 1) / SEG));
 }
 
-extern "C" int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
-                                 float threshold, int64_t max_nnz, int32_t indptr_offset, void* data,
-                                 int32_t* indices, int32_t* indptr, void* inliers, void* work, int64_t work_bytes,
-                                 vh_stream_t stream) {
+namespace {
+
+// Everything vh_filter_outlier checks and launches, given a workspace of at
+// least vh_filter_outlier_workspace_bytes(batch, rows, cols) bytes.
+int filter_outlier_run(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols, float threshold,
+                       int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
+                       void* inliers, void* work, vh_stream_t stream) {
   VH_REQUIRE(float_dtype(dtype), "vh_filter_outlier: dtype must be bf16, fp16 or fp32");
   VH_REQUIRE(batch >= 1 && batch <= 65535 && rows >= 0 && cols >= 0 && max_nnz >= 0,
              "vh_filter_outlier: bad sizes (batch %lld, rows %lld, cols %lld, max_nnz %lld)", (long long)batch,
@@ -675,10 +680,6 @@ extern "C" int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, in
   VH_REQUIRE(rows * cols < ((int64_t)1 << 31) && max_nnz < ((int64_t)1 << 31),
              "vh_filter_outlier: a matrix must hold fewer than 2**31 elements (int32 row pointers)");
   VH_REQUIRE(rows * cols == 0 || (x != nullptr && inliers != nullptr), "vh_filter_outlier: null tensor");
-  VH_REQUIRE(work != nullptr && ((uintptr_t)work % 16) == 0 &&
-                 work_bytes >= vh_filter_outlier_workspace_bytes(batch, rows, cols),
-             "vh_filter_outlier: workspace needs %lld bytes, 16-byte aligned",
-             (long long)vh_filter_outlier_workspace_bytes(batch, rows, cols));
   const int64_t S = (cols + SEG - 1) / SEG;
   VH_REQUIRE(rows * S / ROW_WAVES < ((int64_t)1 << 31), "vh_filter_outlier: too many rows");
   const hipStream_t st = vh::as_stream(stream);
@@ -693,6 +694,65 @@ extern "C" int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, in
     default: return vec ? VH_FILTER(VH_F32, 4) : VH_FILTER(VH_F32, 1);
   }
 #undef VH_FILTER
+}
+
+// The workspace of vh_filter_outlier_noalloc: a file-scope device array,
+// one copy per GPU, held until the process ends.  Host code never passes
+// the array's name to a kernel (on the host it is a stand-in, not a device
+// address); it takes each device's address once with hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[VH_FILTER_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[MAX_DEVICES] = {};
+
+// This device's address of `scratch`, looked up on the device's first call.
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  VH_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < MAX_DEVICES,
+             "vh_filter_outlier_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    VH_REQUIRE(e == hipSuccess && p != nullptr, "vh_filter_outlier_noalloc: hipGetSymbolAddress failed: %s",
+               hipGetErrorString(e));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return VH_OK;
+}
+
+}  // namespace
+
+extern "C" int vh_filter_outlier(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
+                                 float threshold, int64_t max_nnz, int32_t indptr_offset, void* data,
+                                 int32_t* indices, int32_t* indptr, void* inliers, void* work, int64_t work_bytes,
+                                 vh_stream_t stream) {
+  VH_REQUIRE(work != nullptr && ((uintptr_t)work % 16) == 0 &&
+                 work_bytes >= vh_filter_outlier_workspace_bytes(batch, rows, cols),
+             "vh_filter_outlier: workspace needs %lld bytes, 16-byte aligned",
+             (long long)vh_filter_outlier_workspace_bytes(batch, rows, cols));
+  return filter_outlier_run(x, dtype, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr,
+                            inliers, work, stream);
+}
+
+extern "C" int vh_filter_outlier_noalloc(const void* x, int32_t dtype, int64_t batch, int64_t rows, int64_t cols,
+                                         float threshold, int64_t max_nnz, int32_t indptr_offset, void* data,
+                                         int32_t* indices, int32_t* indptr, void* inliers, vh_stream_t stream) {
+  const int64_t need = vh_filter_outlier_workspace_bytes(batch, rows, cols);
+  VH_REQUIRE(need <= VH_FILTER_NOALLOC_SCRATCH_BYTES,
+             "vh_filter_outlier_noalloc: %lld x %lld x %lld needs %lld bytes of workspace, more than the %lld of the "
+             "library's fixed scratch; call vh_filter_outlier with a workspace",
+             (long long)batch, (long long)rows, (long long)cols, (long long)need,
+             (long long)VH_FILTER_NOALLOC_SCRATCH_BYTES);
+  void* work = nullptr;
+  if (int e = scratch_of_current_device(&work)) return e;
+  // Every workspace word a launch reads was written earlier in the same
+  // call (segment counts for every segment, staged outliers below each
+  // segment's count), so the scratch needs no clearing between calls.
+  return filter_outlier_run(x, dtype, batch, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr,
+                            inliers, work, stream);
 }
 
 extern "C" int vh_slice_csr(const void* data, int32_t dtype, const int32_t* indices, const int32_t* indptr,

@@ -126,6 +126,7 @@ _SIGNATURES = {
     "vh_nhwc_to_nchw": ([_P, _I32, _I64, _I64, _I64, _P, _P], _I32),
     "vh_filter_outlier": ([_P, _I32, _I64, _I64, _I64, _F32, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P], _I32),
     "vh_filter_outlier_workspace_bytes": ([_I64, _I64, _I64], _I64),
+    "vh_filter_outlier_noalloc": ([_P, _I32, _I64, _I64, _I64, _F32, _I64, _I32, _P, _P, _P, _P, _P], _I32),
     "vh_slice_csr": ([_P, _I32, _P, _P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _P, _P, _P], _I32),
     "vh_spmm_csr": ([_P, _I32, _P, _P, _I64, _I64, _I64, _P, _I32, _I32, _I64, _I64, _I64, _P, _P, _I32, _P, _P],
                     _I32),
@@ -134,6 +135,7 @@ _SIGNATURES = {
 DECODE_ERR_FP16_RANGE = 1
 DECODE_ERR_WEIGHT_RANGE = 2
 KIVI_RES_CAP = 128
+FILTER_NOALLOC_SCRATCH_BYTES = 8 << 20
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
 
 #: Every symbol ``include/voyager_hip.h`` declares.
