@@ -424,7 +424,7 @@ def bench_config5(args):
         wd = {k: v.to(dev) for k, v in w.items()}
         layer = decode.DecoderLayer(wd, cfg.n_heads, cfg.n_kv_heads, cfg.eps, cfg.rope_theta, max_batch=B,
                                     max_pos=pos + 1)
-        cache, kq, vq = decode.KiviCache.from_bf16(*[t.to(dev) for t in kv])
+        cache, kq, vq = decode.KiviCache.from_bf16(*[t.to(dev) for t in kv], capacity=n_main + 128)
         if li == 0 and not args.no_cpu:
             tab = voyager_amd.formats.quantization_map("int8", dev)
             mx = {}
@@ -439,14 +439,18 @@ def bench_config5(args):
         caches.append(cache)
         xs.append(x.to(dev))
     torch.cuda.synchronize()
-    stage_lists = [l.stages(x, c, pos) for l, c, x in zip(layers, caches, xs)]
+    # The compute stages with the cache state held at position 4095 (every
+    # replay is the same context-4096 step); the state advance that follows
+    # each step in a real decode, and the fold of a completed chunk (one step
+    # in 128), are timed on their own below and added.
+    stage_lists = [l.stages(x, c, advance=False) for l, c, x in zip(layers, caches, xs)]
     names = [n for n, _ in stage_lists[0]]
     reps = 10
     step_g = capture(lambda: [fn() for _ in range(reps) for st in stage_lists for _, fn in st])
     for _ in range(max(1, args.warmup // 10)):
         step_g.replay()
     torch.cuda.synchronize()
-    step_ms = time_graph(step_g, max(1, args.steps // 10)) / (2 * reps)
+    compute_ms = time_graph(step_g, max(1, args.steps // 10)) / (2 * reps)
     layers[0].flag.check()
     per = {}
     sbytes = layers[0].stage_bytes(B, caches[0])
@@ -454,6 +458,36 @@ def bench_config5(args):
         gi = capture(lambda: [st[i][1]() for _ in range(reps) for st in stage_lists])
         ms = time_graph(gi, 5) / (2 * reps)
         per[name] = {"us": round(ms * 1e3, 2), "GB/s": round(sbytes[name] / (ms * 1e-3) / 1e9, 1)}
+    # the attention with the state advance a real decode step does: from
+    # residual slot 0 (nothing completes), then one step that folds a chunk
+    for c in caches:
+        c.state.copy_(torch.tensor([n_main, 0, 0, 0], dtype=torch.int32))
+    att_i = names.index("attention")
+    adv_lists = [l.stages(x, c, advance=True) for l, c, x in zip(layers, caches, xs)]
+    adv_g = capture(lambda: [st[att_i][1]() for _ in range(reps) for st in adv_lists])
+    adv_ms = time_graph(adv_g, 5) / (2 * reps)
+    for c in caches:
+        c.state.copy_(torch.tensor([n_main, n_res, 0, 0], dtype=torch.int32))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fold_g = capture(lambda: adv_lists[0][att_i][1]())
+    for c in caches:
+        c.state.copy_(torch.tensor([n_main, n_res, 0, 0], dtype=torch.int32))
+    torch.cuda.synchronize()
+    e0.record()
+    fold_g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    fold_ms = e0.elapsed_time(e1)
+    for l, c in zip(layers, caches):
+        c.state.copy_(torch.tensor([n_main, n_res, 0, 0], dtype=torch.int32))
+        c.n_main, c.n_res = n_main, n_res
+        l.flag.check()
+    per["attention_advancing"] = {"us": round(adv_ms * 1e3, 2), "fold_step_us": round(fold_ms * 1e3, 2),
+                                  "note": "the attention stage with the cache advance (from residual slot 0), "
+                                          "and one step that folds a completed 128-token chunk (one step in 128)"}
+    att_ms = per["attention"]["us"] * 1e-3
+    step_ms = compute_ms + (adv_ms - att_ms) + (fold_ms - adv_ms) / 128
     total_b = sum(sbytes.values())
     gbs = total_b / (step_ms * 1e-3) / 1e9
     dom = max(("gate_up_proj", "down_proj", "qkv_proj", "o_proj", "attention"), key=lambda n: sbytes[n])

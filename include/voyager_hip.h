@@ -270,6 +270,9 @@ int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t M, const u
  * into a caller-owned device int32 (`flag`); the caller checks it. */
 #define VH_DECODE_ERR_FP16_RANGE 1   /* an activation block exceeds fp16 (|x| > 65504) */
 #define VH_DECODE_ERR_WEIGHT_RANGE 2 /* a weight block exponent outside [-24, 5] */
+#define VH_DECODE_ERR_KV_CODE 4      /* a folded KIVI chunk held a value whose code is NaN */
+#define VH_DECODE_ERR_KV_FULL 8      /* the main cache had no room for a completed chunk */
+#define VH_DECODE_ERR_KV_STATE 16    /* the cache state was out of range (nothing was computed) */
 #define VH_KIVI_RES_CAP 128          /* residual window slots */
 
 #define VH_GEMV_STORE 0    /* y = bf16(x W^T) */
@@ -303,46 +306,70 @@ int vh_gemv_mx8(const uint16_t* x_fq, int64_t M, int64_t K, const uint8_t* w_cod
                 int32_t mode, int32_t tiles_per_block, const uint16_t* residual, uint16_t* y, uint16_t* fq_out,
                 int32_t* flag, vh_stream_t stream);
 
-/* Bake a KIVI main cache of P = batch x kv-heads sequences of T tokens
- * (T % 32 == 0, head_dim 128): codes (0..3, one per byte) [P, T, 128] and
- * bf16 scale / zero point as quantize_affine returns them -- keys
+/* Bake a KIVI main cache: T tokens (T % 32 == 0, head_dim 128) of each of
+ * P = batch x kv-heads sequences -- codes (0..3, one per byte) [P, T, 128]
+ * and bf16 scale / zero point as quantize_affine returns them: keys
  * [P, T/32, 128] (grouped along tokens), values [P, T, 4] (grouped along
- * channels) -- into the attention layout: one 3072-byte block per 32 tokens
- * (key codes, value codes, key and value scale / zero point as fp16),
- * main_out P*T*96 bytes. */
+ * channels) -- into groups [g0, g0 + T/32) of a main cache with room for
+ * group_cap groups of 32 tokens per sequence (main_out P * group_cap * 3072
+ * bytes: per group key codes, value codes, key and value scale / zero point
+ * as fp16 -- exactly the algorithmic 96 bytes per token per kv head).
+ * Replaces the store of the main cache (quantize_affine,
+ * codegen/transform/quant_folding.py:2213-2314). */
 int vh_kivi_bake(const uint8_t* k_codes, const uint16_t* k_scale, const uint16_t* k_zp, const uint8_t* v_codes,
-                 const uint16_t* v_scale, const uint16_t* v_zp, int64_t P, int64_t T, uint8_t* main_out,
-                 vh_stream_t stream);
+                 const uint16_t* v_scale, const uint16_t* v_zp, int64_t P, int64_t T, int64_t group_cap, int64_t g0,
+                 uint8_t* main_out, vh_stream_t stream);
 
 /* Fill the first n residual slots from k, v [P, n, 128] (bf16): kr and vr
  * are [P, 128 slots, 128] bf16. */
 int vh_kivi_bake_residual(const uint16_t* k, const uint16_t* v, int64_t P, int64_t n, uint16_t* kr, uint16_t* vr,
                           vh_stream_t stream);
 
+/* KIVI cache state, device int32[4]: {tokens in the main cache (a multiple
+ * of 32), residual slots filled before the step (< 128), a counter the
+ * advance kernel keeps at 0 between launches, unused}.  The step's position
+ * is their sum.  The kernels read it on the device, so one captured step
+ * replays at every position. */
 typedef struct vh_kivi_desc {
   const uint16_t* qkv;     /* [batch, qkv_ld] bf16: nq query heads, nkv key heads, nkv value heads (pre-RoPE) */
   int64_t qkv_ld;
-  const uint16_t* cos;     /* [128] bf16 RoPE tables at this step's position */
-  const uint16_t* sin;
-  const uint8_t* main;     /* main cache (vh_kivi_bake); unused when n_main == 0 */
+  const uint16_t* rope;    /* [2][max_pos][128] bf16: cos, then sin, of each position */
+  int64_t max_pos;
+  uint8_t* main;           /* main cache [P][group_cap][3072] (vh_kivi_bake) */
+  int64_t group_cap;       /* groups of 32 tokens the main cache holds per sequence */
   uint16_t* kr;            /* residual window (this step's key and value are written to slot n_res) */
   uint16_t* vr;
+  int32_t* state;          /* device int32[4], see above */
   int64_t batch, nkv, nq, head_dim; /* nq == 4 nkv, head_dim == 128 */
-  int64_t n_main;          /* main-cache tokens (multiple of 32) */
-  int64_t n_res;           /* residual slots filled before this step (< 128) */
   float softmax_scale;     /* 1 / sqrt(head_dim) */
   float* part;             /* workspace of part_floats floats */
-  int64_t part_floats;     /* >= batch * nkv * ceil(n_main / 512) * 4 * 130 */
+  int64_t part_floats;     /* >= batch * nkv * ceil(group_cap / 16) * 4 * 130 */
   uint16_t* attn;          /* [batch, nq * 128] bf16 attention output (optional) */
   uint16_t* attn_fq;       /* [batch, nq * 128] fp16 bits: its MX-int8 fake quantization */
   int32_t* flag;
+  int32_t advance;         /* nonzero: advance the state after the step (below) */
+  vh_format scale_fmt;     /* advance: the scale / zero-point map of the fold (fp16_e5m10) */
+  vh_format code_fmt;      /* advance: the code map of the fold (uint2) */
 } vh_kivi_desc;
 
 /* Decode attention over main + residual: RoPE on this step's query and key,
  * the key / value appended at residual slot n_res, then softmax(q K^T *
  * softmax_scale) V over the n_main + n_res + 1 positions (GQA, 4 query heads
- * per kv head).  Replaces the split-cache attention of a converted decode
- * graph (quant_folding.py:2391-2547 read path, eager attention). */
+ * per kv head), with the main keys dequantized and each score rounded as the
+ * reference's bf16 eager attention rounds them.  Replaces the split-cache
+ * attention of a converted decode graph (quant_folding.py:1025-1120 split,
+ * :2391-2547 read path, eager attention).
+ *
+ * With desc->advance the step also does the cache bookkeeping: when it filled
+ * the residual's last slot (n_res == 127), the 128 residual tokens are
+ * quantized with the KIVI specs (quantize_affine through code_fmt /
+ * scale_fmt, keys along tokens, values along channels, group 32) into the
+ * next 4 groups of the main cache and the residual restarts; otherwise n_res
+ * grows by one.  This replaces the fold of a completed chunk
+ * (quant_folding.py:1994-2065, :2634-2700, move_folds_out) -- here on the
+ * device, so replays need no host step.  A chunk with no room flags
+ * VH_DECODE_ERR_KV_FULL and leaves the state; a value whose code is NaN
+ * flags VH_DECODE_ERR_KV_CODE.  Without it the state is left as it was. */
 int vh_kivi_attention(const vh_kivi_desc* desc, vh_stream_t stream);
 
 /* ------------------------------------------------------- outliers (CSR)

@@ -168,3 +168,55 @@ def decode_layer(x: torch.Tensor, weights: Dict[str, torch.Tensor], k_past: torc
     act = torch.nn.functional.silu(lin("wg", h2)) * lin("wu", h2)
     out = x1 + lin("wd", act)
     return {"h1": h1, "q": q, "k": k, "v": v, "attn": attn, "x1": x1, "h2": h2, "act": act, "out": out}
+
+
+class KiviCacheRef:
+    """The reference's split KIVI cache of one layer (test only).
+
+    ``split_kv_cache`` (``codegen/transform/quant_folding.py:1025-1120``)
+    keeps whole chunks of ``residual_length`` positions in the quantized main
+    cache and the chunk being filled in a full-precision residual, position
+    ``p`` in slot ``p mod residual_length``.  The attention reads the
+    dequantized main cache followed by the residual.  After the step whose
+    token lands in the residual's last slot, the fold quantizes the residual
+    with the cache's own quantizer and stores it as the next chunk of the main
+    cache (``_store_chunk``, ``:1994-2065``; run after the step by
+    ``move_folds_out``, ``:2634-2700``).  Here the quantizer is the KIVI spec
+    (``kivi_quantize``: keys grouped along tokens, values along channels),
+    and the main cache is kept as its reference-form outputs, chunk by chunk.
+    The starting main part may be any whole number of 32-token groups."""
+
+    def __init__(self, k_main, v_main, k_res, v_res, residual_length: int = 128):
+        self.length = residual_length
+        self.k_chunks, self.v_chunks = [], []  # (scale, zp, codes) per stored run
+        if k_main.shape[2]:
+            self.k_chunks.append(kivi_quantize(k_main, -2))
+            self.v_chunks.append(kivi_quantize(v_main, -1))
+        self.n_main = k_main.shape[2]
+        self.k_res, self.v_res = k_res.clone(), v_res.clone()
+        self.folds = 0
+
+    @property
+    def position(self) -> int:
+        return self.n_main + self.k_res.shape[2]
+
+    def past(self):
+        """Keys and values the step's attention reads before its own token:
+        the dequantized main cache, then the residual (``[B, nkv, T, D]``)."""
+        ks = [kivi_dequantize(c, s, z, -2) for s, z, c in self.k_chunks] + [self.k_res]
+        vs = [kivi_dequantize(c, s, z, -1) for s, z, c in self.v_chunks] + [self.v_res]
+        return torch.cat(ks, dim=2), torch.cat(vs, dim=2)
+
+    def append(self, k, v) -> bool:
+        """The step's key / value ``[B, nkv, 1, D]`` enter the residual; when
+        they fill its last slot the chunk is folded.  Returns whether it was."""
+        self.k_res = torch.cat((self.k_res, k), dim=2)
+        self.v_res = torch.cat((self.v_res, v), dim=2)
+        if self.k_res.shape[2] < self.length:
+            return False
+        self.k_chunks.append(kivi_quantize(self.k_res, -2))
+        self.v_chunks.append(kivi_quantize(self.v_res, -1))
+        self.n_main += self.length
+        self.k_res, self.v_res = self.k_res[:, :, :0], self.v_res[:, :, :0]
+        self.folds += 1
+        return True

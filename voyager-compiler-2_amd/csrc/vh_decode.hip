@@ -15,11 +15,17 @@
 //   The activations are the fake-quantized values code_x * 2**e_x in fp16, so
 //   every product is exact and only the fp32 summation order differs from
 //   the reference's fp32 GEMM of the dequantized operands.
-// * KIVI attention: flash-decoding over 32-token steps.  Codes (0..3) become
-//   exact fp16 MFMA operands with two or three VALU ops per pair; the affine
-//   scale moves to the other operand (q * s for keys, p * s for values) and
-//   the zero-point term is a per-group dot product, so the cache is never
-//   dequantized element by element.
+// * KIVI attention: flash-decoding over 32-token groups.  Keys are
+//   dequantized element by element exactly as the reference's bf16
+//   dequantize rounds them ((code - zp) rounded, times scale rounded) and meet
+//   the bf16 query on a bf16 MFMA, so each score is the reference's matmul up
+//   to summation order, then rounded where eager attention rounds it.  Value
+//   codes stay exact fp16 MFMA operands (1024 + c * 4**p, one VALU op per
+//   pair); their affine scale moves to the probabilities' operand and the
+//   zero-point term is a per-group dot product.  The cache state (main
+//   tokens, residual slots) lives in device memory, so a captured step
+//   replays across positions, and the fold of a completed residual chunk
+//   into the main cache runs on the device.
 #include <hip/hip_runtime.h>
 
 #include "vh_device.h"
@@ -37,9 +43,6 @@ constexpr int GEMV_WAVES = 8;  // two workgroups per CU: one streams while the o
 constexpr int HEAD_DIM = 128;
 constexpr int GQA = 4;        // query heads per kv head
 constexpr int KV_GROUP = 32;  // KIVI group: tokens per key group, channels per value group
-constexpr int ATT_WAVES = 4;
-constexpr int GROUPS_PER_WAVE = 4;  // one super-step of 128 tokens per wave
-constexpr int STEPS_PER_SPLIT = ATT_WAVES * GROUPS_PER_WAVE;
 constexpr int RES_CAP = VH_KIVI_RES_CAP;
 constexpr int PART = HEAD_DIM + 2;  // m, l, o[128]
 
@@ -337,38 +340,70 @@ __global__ void __launch_bounds__(256) k_bake_mx8_scales(const uint8_t* __restri
 }
 
 // ------------------------------------------------------------ KIVI attention
-// Main-cache layout (P = batch x kv heads, G = groups of 32 tokens): one
-// 3 KB block per (P, g), read by one wave with three 16-byte loads per lane
-// and staged through LDS:
-//   [0, 1024)     key codes [2 tiles][64 lanes][8 B]: lane l of tile t holds
-//                 token 32 g + 16 t + l % 16, channels 32 cs + 8 (l / 16) + j
-//                 as 2-bit fields (dword cs / 2; pair (cs % 2) 4 + p at bits
-//                 2k and 16 + 2k for j = 2p, 2p + 1).
-//   [1024, 2048)  value codes [64 lanes][16 B]: lane l dword d holds tiles
-//                 2d, 2d + 1 (channel 16 r8 + l % 16) at tokens tok(l / 16, j),
-//                 pair hh 4 + p for j = 2p, 2p + 1.
-//   [2048, 2560)  key scale / zero point fp16 [4 cs][4 q][8 scale, 8 zp] for
-//                 channels 32 cs + 8 q + j (the group's per-channel affine).
-//   [2560, 3072)  value scale / zero point fp16 [4 q][8 j][4 groups][2] of
-//                 token tok(q, j) (per-token affine of each 32 channels).
-// tok(q, j) = 16 (j / 4) + 4 q + j % 4 is the token the score MFMA leaves in
-// lane group q, register j % 4 of tile j / 4.
-// Residual window: keys and values bf16 [P][RES_CAP][128].
+// ------------------------------------------------------------ KIVI cache
+// Main-cache layout: P = batch x kv heads sequences, each with room for
+// group_cap groups of 32 tokens; one 3072-byte block per (P, group), read by
+// one wave with three 16-byte loads per lane:
+//   [0, 1024)     key codes, lane l (kq = l / 16, r = l % 16): dwords
+//                 D[2 tile + cs / 2] hold token 16 tile + r, channels
+//                 32 kq + 8 cs + j (j < 8): code (cs, j) at bit
+//                 16 (cs % 2) + 2 j, so the codes of channels j = 2p, 2p + 1
+//                 (one MFMA operand dword) form nibble 4 (cs % 2) + p.
+//   [1024, 2048)  value codes, lane l: dword w holds row tiles r8 = 2 w and
+//                 2 w + 1 (channel 16 r8 + r) at tokens tok(kq, j): code at
+//                 bit 8 (r8 % 2) + 16 (j % 2) + 2 (j / 2).
+//   [2048, 2560)  key scale / zero point, fp16 [128 channels][2].
+//   [2560, 3072)  value scale / zero point, fp16 [4 kq][8 j][4 channel
+//                 groups][2] of token tok(kq, j).
+// tok(kq, j) = 16 (j / 4) + 4 kq + j % 4: the token the score MFMA leaves in
+// lane quarter kq, register j % 4 of tile j / 4.
+// Residual window: keys and values bf16 [P][RES_CAP][128]; slot s holds the
+// token at position n_main + s.
+// Cache state (device int32[4]): {tokens in the main cache, residual slots
+// filled, completion counter of the advance kernel, unused}.
 constexpr int GROUP_BYTES = 3072;
+constexpr int SPLIT_WAVES = 8;
+constexpr int GROUPS_PER_WAVE = 2;
+constexpr int GROUPS_PER_SPLIT = SPLIT_WAVES * GROUPS_PER_WAVE;
+constexpr int GROUPS_PER_CHUNK = RES_CAP / KV_GROUP;  // groups a fold appends
+constexpr float LOG2E = 1.4426950408889634f;
+// value operands are p * s * 2**(V_EXP - e), e = floor(log2) of the largest
+// value scale the wave reads: at most 2**(V_EXP + 1), far above fp16
+// subnormals for any term that matters
+constexpr int V_EXP = 14;
 
 struct KiviArgs {
   const uint16_t* qkv;
   int64_t qkv_ld;
-  const uint16_t* cos;
-  const uint16_t* sin;
-  const uint8_t* main;
+  const uint16_t* rope;  // [2][max_pos][128] bf16 cos / sin
+  int64_t max_pos;
+  uint8_t* main;
+  int64_t group_cap;
   uint16_t* kr;
   uint16_t* vr;
-  int32_t n_groups, n_res, nkv, nq, splits;
-  float scale_log2;
-  float* part;
+  int32_t* state;  // written by the combine's last workgroup when advancing
+  int32_t nkv, nq, splits_cap;
+  float scale;  // softmax scale (1 / sqrt(head_dim))
+  float* part;  // [P][splits_cap][GQA][PART]
+  int32_t advance;
+  vh_format sf;  // fold: scale / zero-point map
+  vh_format cf;  // fold: code map
 };
 
+// The device state is what the kernels index with: anything out of range
+// (which a caller's corrupted state could hold) stops them before any
+// access, and the combine flags it.
+VH_DEV bool state_ok(const KiviArgs& a, int n_main, int n_res) {
+  return n_main >= 0 && n_main % KV_GROUP == 0 && n_main / KV_GROUP <= a.group_cap && n_res >= 0 &&
+         n_res < RES_CAP && (int64_t)n_main + n_res < a.max_pos;
+}
+
+// A score as eager attention forms it, in log2 units for exp2: q . k rounded
+// to bf16 (the bf16 matmul), times the scale rounded to bf16 again
+// (transformers' eager_attention_forward: matmul(q, k^T) * scaling).
+VH_DEV float eager_score_log2(float qk, float scale) {
+  return __uint_as_float(f2bf2_hw(__uint_as_float(f2bf2_hw(qk, 0.0f) << 16) * scale, 0.0f) << 16) * LOG2E;
+}
 
 VH_DEV uint16_t rope1(const uint16_t* base, const uint16_t* cs, const uint16_t* sn, int c) {
   const float x = bf2f(base[c]);
@@ -381,25 +416,16 @@ VH_DEV uint32_t pack_h2(float a, float b) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-// Cross-lane reductions: DPP row rotations (row_ror:4 / :8, lane i reads
-// lane (i - 4) / (i - 8) mod 16 of its row) combine the four group columns of
-// a head (lanes n, n + 4, n + 8, n + 12 of a 16-lane row).
-VH_DEV float ror4(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
-}
-VH_DEV float ror8(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-}
 // lane l and lane l ^ 16 (l ^ 32)
 VH_DEV float sum_x16(float v) { return v + __shfl_xor(v, 16); }
 VH_DEV float sum_x32(float v) { return v + __shfl_xor(v, 32); }
 VH_DEV float max_x16(float v) { return fmaxf(v, __shfl_xor(v, 16)); }
 VH_DEV float max_x32(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
 
-// Code operands: the pair of 2-bit fields at bits 2p and 16 + 2p of W
+// Value code operands: the pair of 2-bit fields at bits 2p and 16 + 2p of W
 // becomes the fp16 pair (1024 + c * 4**p), one v_and_or_b32 with a mask
-// held in a VGPR; the 4**-p goes into the other operand.  mk[p] =
-// 0x00030003 << 2p.
+// held in a VGPR; the 4**-p goes into the other operand and the 1024 offset
+// is removed by one MFMA against -1024.  mk[p] = 0x00030003 << 2p.
 struct CodeMasks {
   uint32_t mk[4];
 };
@@ -411,243 +437,405 @@ VH_DEV CodeMasks code_masks() {
   return m;
 }
 
-// The four operand dwords of pairs kb .. kb + 3 (kb = 0 or 4) of W.
-VH_DEV f16x8 code_operand(uint32_t W, int kb, const CodeMasks& m) {
-  const uint32_t w = kb ? (W >> 8) : W;
+// The four operand dwords of the codes at bits 8 half + [0, 8) and
+// 16 + 8 half + [0, 8) of W.
+VH_DEV f16x8 code_operand(uint32_t W, int half, const CodeMasks& m) {
+  const uint32_t w = half ? (W >> 8) : W;
   return __builtin_bit_cast(f16x8, make_uint4((w & m.mk[0]) | 0x64006400u, (w & m.mk[1]) | 0x64006400u,
                                               (w & m.mk[2]) | 0x64006400u, (w & m.mk[3]) | 0x64006400u));
 }
 
-VH_DEV uint4 sel4(bool c, const uint4& v) { return c ? v : make_uint4(0u, 0u, 0u, 0u); }
+// Per wave and group, a table of every key operand the group can hold: for
+// each pair of channels (2p, 2p + 1 of 8 cs + [0, 8) in block kq) and each of
+// the 16 pairs of codes, the bf16 pair of dequantized keys -- (code -
+// zero_point) * scale, each bfloat16 op rounding its result as the
+// reference's dequantize does (ops/quantized.py:518-571).  An MFMA operand
+// dword is then one 32-bit LDS read at its pair's table + 4 * nibble.
+// Blocks kq are KEY_TAB_BLOCK bytes apart (a 64-byte pad spreads the four
+// blocks a wave reads at once over the LDS banks).
+constexpr int PAIR_TAB = 16 * 4;
+constexpr int KEY_TAB_BLOCK = 16 * PAIR_TAB + 64;
+constexpr int KEY_TAB_BYTES = 4 * KEY_TAB_BLOCK;
 
-constexpr float V_SCALE = 256.0f;  // value operands carry 2**8 (kept clear of fp16 subnormals)
-
-// One super-step (ng of 4 consecutive 32-token groups staged at blk0) for one
-// wave, from a fresh softmax state.  MFMA column n = lane % 16 is (group
-// gq = n / 4, head h = n % 4): the lane's B operands (q * s for keys, p * s
-// for values) are built once, for its own group.  Scores come from per-group
-// accumulators (each column reads its own group's); the value MFMAs take the
-// operand masked to the group.  The +1024 offset of the code operands is one
-// MFMA against a constant operand.  Outputs: the head's max m (all lanes of
-// the head), the lane's partial sum, acc (o^T, scaled by V_SCALE, column n)
-// and zt (the zero-point and offset terms of column n, per channel group,
-// partial over the lane group q).
-VH_DEV void main_superstep(const uint8_t* blk0, int ng, const uint4 (&qh)[4], int lane, float scale_log2, float& m,
-                           float& lsum, f32x4 (&acc)[8], float (&zt)[4]) {
-  const int n = lane & 15, q = lane >> 4, gq = n >> 2;
-  const bool own_live = gq < ng;
-  const uint8_t* own = blk0 + gq * GROUP_BYTES;
-  const CodeMasks cm = code_masks();
-  const f16x8 ONE = __builtin_bit_cast(f16x8, make_uint4(0x64006400u, 0x64006400u, 0x64006400u, 0x64006400u));
-  // keys: (q * s) * 4**-p of the own group (fp16) and the zero-point term
-  f16x8 Bk[4];
-  float bias = 0.0f;
+// Lanes 0-31: the pairs of channels 4 l .. 4 l + 3 from the lane's parameter
+// piece (fp16 scale / zero point pairs).
+VH_DEV void build_key_table(const uint4& piece, int lane, uint8_t* tab) {
+  const f16x8 e = __builtin_bit_cast(f16x8, piece);
+  uint32_t v01[4], v23[4];  // per channel: keys of codes 0, 1 and 2, 3 (bf16 pairs)
 #pragma unroll
-  for (int cs = 0; cs < 4; ++cs) {
-    const f16x8 sv = *(const f16x8*)(own + 2048 + (cs * 4 + q) * 32);
-    const f16x8 zv = *(const f16x8*)(own + 2048 + (cs * 4 + q) * 32 + 16);
-    const uint32_t qw[4] = {qh[cs].x, qh[cs].y, qh[cs].z, qh[cs].w};
-    uint32_t bq[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float q0 = bf2f(qw[p] & 0xffffu) * (float)sv[2 * p];
-      const float q1 = bf2f(qw[p] >> 16) * (float)sv[2 * p + 1];
-      bias = fmaf(q0, (float)zv[2 * p], bias);
-      bias = fmaf(q1, (float)zv[2 * p + 1], bias);
-      const float f = 1.0f / (float)(1 << (2 * p));
-      bq[p] = pack_h2(q0 * f, q1 * f);
-    }
-    Bk[cs] = __builtin_bit_cast(f16x8, make_uint4(bq[0], bq[1], bq[2], bq[3]));
+  for (int q = 0; q < 4; ++q) {
+    const float sc = (float)e[2 * q], zp = (float)e[2 * q + 1];
+    const uint32_t t01 = f2bf2_hw(0.0f - zp, 1.0f - zp), t23 = f2bf2_hw(2.0f - zp, 3.0f - zp);
+    v01[q] = f2bf2_hw(__uint_as_float(t01 << 16) * sc, __uint_as_float(t01 & 0xffff0000u) * sc);
+    v23[q] = f2bf2_hw(__uint_as_float(t23 << 16) * sc, __uint_as_float(t23 & 0xffff0000u) * sc);
   }
-  f32x4 Sc = {0.0f, 0.0f, 0.0f, 0.0f};
+  uint8_t* dst = tab + (lane >> 3) * KEY_TAB_BLOCK + (lane & 7) * 2 * PAIR_TAB;
 #pragma unroll
-  for (int cs = 0; cs < 4; ++cs) Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ONE, Bk[cs], Sc, 0, 0, 0);
-  f32x4 S[4][2];
+  for (int pr = 0; pr < 2; ++pr) {
+    uint32_t ent[16];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    S[g][0] = {0.0f, 0.0f, 0.0f, 0.0f};
-    S[g][1] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (g >= ng) continue;
-    const uint8_t* blk = blk0 + g * GROUP_BYTES;
-    const uint2 kc0 = *(const uint2*)(blk + lane * 8);
-    const uint2 kc1 = *(const uint2*)(blk + 512 + lane * 8);
-#pragma unroll
-    for (int cs = 0; cs < 4; ++cs) {
-      const int kb = (cs & 1) * 4;
-      S[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(cs < 2 ? kc0.x : kc0.y, kb, cm), Bk[cs], S[g][0],
-                                                      0, 0, 0);
-      S[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(cs < 2 ? kc1.x : kc1.y, kb, cm), Bk[cs], S[g][1],
-                                                      0, 0, 0);
+    for (int v = 0; v < 16; ++v) {
+      const int c0 = v & 3, c1 = v >> 2;
+      // bytes 0-3 of the selection: channel 2 pr's key of c0 (low), channel 2 pr + 1's of c1 (high)
+      const uint32_t lo = c0 < 2 ? v01[2 * pr] : v23[2 * pr], hi = c1 < 2 ? v01[2 * pr + 1] : v23[2 * pr + 1];
+      const uint32_t sl = (uint32_t)(2 * (c0 & 1)), sh = (uint32_t)(4 + 2 * (c1 & 1));
+      ent[v] = __builtin_amdgcn_perm(hi, lo, sl | (sl + 1) << 8 | sh << 16 | (sh + 1) << 24);
     }
-  }
-  bias = sum_x32(sum_x16(bias));
-  const float off = Sc[0] + bias;
-  float sc[2][4];
-  float mloc = -__builtin_inff();
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = gq == 0 ? S[0][t][r] : gq == 1 ? S[1][t][r] : gq == 2 ? S[2][t][r] : S[3][t][r];
-      sc[t][r] = own_live ? (v - off) * scale_log2 : -__builtin_inff();
-      mloc = fmaxf(mloc, sc[t][r]);
-    }
-  mloc = fmaxf(mloc, ror4(mloc));
-  mloc = fmaxf(mloc, ror8(mloc));
-  m = max_x32(max_x16(mloc));
-  float p[8];
-  lsum = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    p[j] = exp2f(sc[j >> 2][j & 3] - m);
-    lsum += p[j];
-  }
-  // values: (p * s) * 2**8 * 4**-pp of the own group per channel group
-  f16x8 Bv[4];
-#pragma unroll
-  for (int gc = 0; gc < 4; ++gc) {
-    uint32_t pw[4];
-    zt[gc] = 0.0f;
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      const f16x8 e0 = *(const f16x8*)(own + 2560 + (q * 8 + 2 * pp) * 16);
-      const f16x8 e1 = *(const f16x8*)(own + 2560 + (q * 8 + 2 * pp + 1) * 16);
-      // (an absent group's block is a staged copy of a present one: finite, and its p are 0)
-      const float p0 = p[2 * pp] * (float)e0[2 * gc], p1 = p[2 * pp + 1] * (float)e1[2 * gc];
-      zt[gc] = fmaf(p0, (float)e0[2 * gc + 1], zt[gc]);
-      zt[gc] = fmaf(p1, (float)e1[2 * gc + 1], zt[gc]);
-      const float f = V_SCALE / (float)(1 << (2 * pp));
-      pw[pp] = pack_h2(p0 * f, p1 * f);
-    }
-    Bv[gc] = __builtin_bit_cast(f16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-    // the +1024 offset of the value codes, for this column (lane group 0 only)
-    f32x4 vc = {0.0f, 0.0f, 0.0f, 0.0f};
-    vc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ONE, Bv[gc], vc, 0, 0, 0);
-    if (q == 0) zt[gc] += vc[0] * (1.0f / V_SCALE);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    if (g >= ng) break;
-    const uint4 vcode = *(const uint4*)(blk0 + g * GROUP_BYTES + 1024 + lane * 16);
-    const uint32_t vw[4] = {vcode.x, vcode.y, vcode.z, vcode.w};
-    f16x8 Bm[4];
-#pragma unroll
-    for (int gc = 0; gc < 4; ++gc) Bm[gc] = __builtin_bit_cast(f16x8, sel4(gq == g, __builtin_bit_cast(uint4, Bv[gc])));
-#pragma unroll
-    for (int r8 = 0; r8 < 8; ++r8)
-      acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(vw[r8 >> 1], (r8 & 1) * 4, cm), Bm[r8 >> 1],
-                                                      acc[r8], 0, 0, 0);
+    for (int k = 0; k < 4; ++k)
+      *(uint4*)(dst + pr * PAIR_TAB + 16 * k) = make_uint4(ent[4 * k], ent[4 * k + 1], ent[4 * k + 2], ent[4 * k + 3]);
   }
 }
 
-// Workgroups (split, P) stream the main cache: each wave stages one
-// super-step (GROUPS_PER_WAVE groups, 12 KB) in LDS and computes it.
-__global__ void __launch_bounds__(ATT_WAVES * 64) k_kivi_split(KiviArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
-  __shared__ __attribute__((aligned(16))) uint4 s_stage[ATT_WAVES][GROUPS_PER_WAVE * GROUP_BYTES / 16];
-  float (*s_part)[GQA][PART] = (float (*)[GQA][PART])&s_stage[0][0];  // reused once the waves are done
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int P = blockIdx.y, split = blockIdx.x;
-  const int b = P / a.nkv, kvh = P % a.nkv;
-  const int n = lane & 15, q = lane >> 4;
-  const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
+// bf16 rounding on the hardware converter (round half to even).
+VH_DEV float rbf_hw(float x) { return __uint_as_float(f2bf2_hw(x, 0.0f) << 16); }
 
-  // this wave's blocks go out before anything else
-  // (a partial super-step re-reads its last group for the absent ones; they are masked)
-  const int g0 = split * STEPS_PER_SPLIT + wave * GROUPS_PER_WAVE;
-  const int ng = max(0, min(GROUPS_PER_WAVE, a.n_groups - g0));
-  static_assert(GROUPS_PER_WAVE == 4, "the prefetch registers below are spelled out for 4 groups");
-  uint4 pa0, pa1, pa2, pb0, pb1, pb2, pc0, pc1, pc2, pd0, pd1, pd2;  // [group][third of the block]
-  const uint4* gsrc = (const uint4*)(a.main + ((int64_t)P * a.n_groups + g0) * GROUP_BYTES) + lane;
-  if (ng > 0) {
-    const uint4* ga = gsrc;
-    const uint4* gb = gsrc + min(1, ng - 1) * (GROUP_BYTES / 16);
-    const uint4* gc = gsrc + min(2, ng - 1) * (GROUP_BYTES / 16);
-    const uint4* gd = gsrc + min(3, ng - 1) * (GROUP_BYTES / 16);
-    pa0 = ga[0]; pa1 = ga[64]; pa2 = ga[128];
-    pb0 = gb[0]; pb1 = gb[64]; pb2 = gb[128];
-    pc0 = gc[0]; pc1 = gc[64]; pc2 = gc[128];
-    pd0 = gd[0]; pd1 = gd[64]; pd2 = gd[128];
+// Workgroups (split, P) stream the main cache: wave w takes groups
+// GROUPS_PER_SPLIT split + SPLIT_WAVES i + w (i < GROUPS_PER_WAVE) with one
+// online softmax, the waves merge through LDS and the workgroup leaves one
+// (max, sum, output) partial per query head.  Splits past the cache's groups
+// return at once (the combine merges only the live ones), so one launch
+// shape serves every cache length up to the capacity.
+__global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
+  __shared__ __attribute__((aligned(64))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
+  __shared__ __attribute__((aligned(16))) uint4 s_vprm[SPLIT_WAVES][GROUPS_PER_WAVE][32];
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
+  __shared__ float s_part[SPLIT_WAVES][GQA][PART];
+  const int n_main = a.state[0], n_res = a.state[1];
+  const int G = n_main / KV_GROUP;
+  const int split = blockIdx.x, P = blockIdx.y;
+  const int g_begin = split * GROUPS_PER_SPLIT;
+  if (!state_ok(a, n_main, n_res) || g_begin >= G) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, kq = lane >> 4;
+  const int b = P / a.nkv, kvh = P % a.nkv;
+  const int pos = n_main + n_res;
+
+  // this wave's blocks go out first (an absent group re-reads a live one; it is skipped)
+  uint4 kc[GROUPS_PER_WAVE], vc[GROUPS_PER_WAVE], pr[GROUPS_PER_WAVE];
+  int ng = 0;
+  const uint8_t* seq = a.main + (int64_t)P * a.group_cap * GROUP_BYTES;
+#pragma unroll
+  for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
+    const int g = g_begin + i * SPLIT_WAVES + wave;
+    ng += g < G ? 1 : 0;
+    const uint8_t* blk = seq + (int64_t)(g < G ? g : G - 1) * GROUP_BYTES;
+    kc[i] = *(const uint4*)(blk + lane * 16);
+    vc[i] = *(const uint4*)(blk + 1024 + lane * 16);
+    pr[i] = *(const uint4*)(blk + 2048 + lane * 16);
   }
-  for (int i = tid; i < GQA * HEAD_DIM; i += ATT_WAVES * 64) {
+  const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
+  const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
+  const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
+  for (int i = tid; i < GQA * HEAD_DIM; i += SPLIT_WAVES * 64) {
     const int h = i / HEAD_DIM, c = i % HEAD_DIM;
-    s_q[h][c] = rope1(qrow + (kvh * GQA + h) * HEAD_DIM, a.cos, a.sin, c);
+    s_q[h][c] = rope1(qrow + (kvh * GQA + h) * HEAD_DIM, cs_, sn_, c);
   }
-  if (ng > 0) {
-    uint4* sa = s_stage[wave] + lane;
-    uint4* sb = sa + GROUP_BYTES / 16;
-    uint4* sc = sb + GROUP_BYTES / 16;
-    uint4* sd = sc + GROUP_BYTES / 16;
-    sa[0] = pa0; sa[64] = pa1; sa[128] = pa2;
-    sb[0] = pb0; sb[64] = pb1; sb[128] = pb2;
-    sc[0] = pc0; sc[64] = pc1; sc[128] = pc2;
-    sd[0] = pd0; sd[64] = pd1; sd[128] = pd2;
+  // value parameters (lanes 32-63) to LDS; the largest value scale of the wave's groups
+  float vmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
+    if (lane >= 32) {
+      s_vprm[wave][i][lane - 32] = pr[i];
+      if (i < ng) {
+        const f16x8 e = __builtin_bit_cast(f16x8, pr[i]);
+        vmax = fmaxf(vmax, fmaxf(fmaxf((float)e[0], (float)e[2]), fmaxf((float)e[4], (float)e[6])));
+      }
+    }
   }
+  vmax = max_x32(max_x16(vmax));
+  vmax = fmaxf(vmax, __shfl_xor(vmax, 8));
+  vmax = fmaxf(vmax, __shfl_xor(vmax, 4));
+  vmax = fmaxf(vmax, __shfl_xor(vmax, 2));
+  vmax = fmaxf(vmax, __shfl_xor(vmax, 1));
+  const int ve = (vmax > 0.0f && vmax < __builtin_inff()) ? floor_log2(vmax) : 0;
+  const float bscale = ldexpf(1.0f, V_EXP - ve), oscale = ldexpf(1.0f, ve - V_EXP);
   __syncthreads();
 
-  float m = -__builtin_inff(), lsum = 0.0f;
-  f32x4 acc[8];
-  float zt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const bool head_lane = n < GQA;
+  // key B operands: q[head n][32 kq + 8 cs + j] (zero past the heads)
+  bf16x8 Bq[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (ng > 0) {
-    uint4 qh[4];
-#pragma unroll
-    for (int cs = 0; cs < 4; ++cs) qh[cs] = *(const uint4*)&s_q[n & 3][cs * 32 + q * 8];
-    main_superstep((const uint8_t*)s_stage[wave], ng, qh, lane, a.scale_log2, m, lsum, acc, zt);
+  for (int cs = 0; cs < 4; ++cs) {
+    const uint4 v = head_lane ? *(const uint4*)&s_q[n][32 * kq + 8 * cs] : make_uint4(0u, 0u, 0u, 0u);
+    Bq[cs] = __builtin_bit_cast(bf16x8, v);
   }
-  // columns -> heads: o = acc / V_SCALE - zt summed over the four group
-  // columns of the head (and zt over the lane groups)
+  const CodeMasks cm = code_masks();
+  const f16x8 NEG = __builtin_bit_cast(f16x8, make_uint4(0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u));
+  float m = -__builtin_inff(), lsum = 0.0f;
+  float zt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 acc[8];
 #pragma unroll
-  for (int gc = 0; gc < 4; ++gc) zt[gc] = sum_x32(sum_x16(zt[gc]));
+  for (int r8 = 0; r8 < 8; ++r8) acc[r8] = {0.0f, 0.0f, 0.0f, 0.0f};
+
 #pragma unroll
-  for (int r8 = 0; r8 < 8; ++r8)
+  for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
+    if (i >= ng) break;
+    // this group's key table (lanes 0-31 build it; the wave's LDS accesses
+    // stay in order, and the previous group's reads precede these writes)
+    if (lane < 32) build_key_table(pr[i], lane, s_tab[wave]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // scores: S[tile][r] = q[head n] . k[token 16 tile + 4 kq + r]; operand
+    // dword p of channel chunk cs is the table entry of its code nibble
+    const uint8_t* tab = s_tab[wave] + kq * KEY_TAB_BLOCK;
+    f32x4 S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    const uint32_t kd[4] = {kc[i].x, kc[i].y, kc[i].z, kc[i].w};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = acc[r8][r] * (1.0f / V_SCALE) - zt[r8 >> 1];
-      v += ror4(v);
-      v += ror8(v);
-      acc[r8][r] = v;
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int cs = 0; cs < 4; ++cs) {
+        const uint32_t D = kd[2 * t + (cs >> 1)];
+        uint32_t w[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const int nib = 4 * (cs & 1) + p;
+          const uint32_t off = (nib ? (D >> (4 * nib - 2)) : (D << 2)) & 0x3cu;
+          w[p] = *(const uint32_t*)(tab + off + (4 * cs + p) * PAIR_TAB);
+        }
+        S[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3])),
+                                                       Bq[cs], S[t], 0, 0, 0);
+      }
+    // online softmax (every lane of a head holds its running max)
+    float sc[8];
+    float mg = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sc[j] = eager_score_log2(S[j >> 2][j & 3], a.scale);
+      mg = fmaxf(mg, sc[j]);
     }
-  lsum += ror4(lsum);
-  lsum += ror8(lsum);
+    mg = max_x32(max_x16(mg));
+    const float m_new = fmaxf(m, mg);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    m = m_new;
+    float p[8];
+    float ps = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = __builtin_amdgcn_exp2f(sc[j] - m_new);
+      ps += p[j];
+    }
+    lsum = lsum * alpha + ps;
+    if (i > 0) {  // the first group starts from zero
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) zt[cg] *= alpha;
+#pragma unroll
+      for (int r8 = 0; r8 < 8; ++r8) acc[r8] *= alpha;
+    }
+    // value B operands per channel group: p * s * 2**(V_EXP - ve) * 4**-(j / 2)
+    // (zero past the heads); the zero-point terms accumulate p * s * zp in the
+    // same 2**(V_EXP - ve) units
+    const float vf = head_lane ? bscale : 0.0f;
+    const uint8_t* vprm = (const uint8_t*)s_vprm[wave][i];
+    uint32_t bv[4][4];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const f16x8 e0 = *(const f16x8*)(vprm + (kq * 8 + 2 * pp) * 16);
+      const f16x8 e1 = *(const f16x8*)(vprm + (kq * 8 + 2 * pp + 1) * 16);
+      const float f = vf * (1.0f / (float)(1 << (2 * pp)));
+      const float p0 = p[2 * pp] * f, p1 = p[2 * pp + 1] * f;
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) {
+        const float b0 = fmaf(p0, (float)e0[2 * cg], 0.0f), b1 = fmaf(p1, (float)e1[2 * cg], 0.0f);
+        const float z = fmaf(b1, (float)e1[2 * cg + 1], b0 * (float)e0[2 * cg + 1]);
+        zt[cg] = fmaf(z, (float)(1 << (2 * pp)), zt[cg]);
+        bv[cg][pp] = pack_h2(b0, b1);
+      }
+    }
+    const uint32_t vw[4] = {vc[i].x, vc[i].y, vc[i].z, vc[i].w};
+#pragma unroll
+    for (int r8 = 0; r8 < 8; ++r8) {
+      const f16x8 B = __builtin_bit_cast(f16x8, make_uint4(bv[r8 >> 1][0], bv[r8 >> 1][1], bv[r8 >> 1][2],
+                                                           bv[r8 >> 1][3]));
+      acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(vw[r8 >> 1], r8 & 1, cm), B, acc[r8], 0, 0, 0);
+      acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(NEG, B, acc[r8], 0, 0, 0);
+    }
+  }
+  // wave totals: sums over the lane quarters; output o[head n][16 r8 + 4 kq + r]
   lsum = sum_x32(sum_x16(lsum));
-  __syncthreads();  // the stage area becomes s_part
-  // wave result in lanes n < 4 (head n): o[ch] for ch = 16 r8 + 4 q + r
-  if (n < GQA) {
+#pragma unroll
+  for (int cg = 0; cg < 4; ++cg) zt[cg] = sum_x32(sum_x16(zt[cg]));
+  if (head_lane) {
 #pragma unroll
     for (int r8 = 0; r8 < 8; ++r8)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_part[wave][n][2 + r8 * 16 + q * 4 + r] = acc[r8][r];
-    if (q == 0) {
+      for (int r = 0; r < 4; ++r)
+        s_part[wave][n][2 + 16 * r8 + 4 * kq + r] = (acc[r8][r] - zt[r8 >> 1]) * oscale;
+    if (kq == 0) {
       s_part[wave][n][0] = m;
       s_part[wave][n][1] = lsum;
     }
   }
   __syncthreads();
-  // merge the waves: thread (h, pair of channels)
-  const int h = tid >> 6, c2 = (tid & 63) * 2;
+  // merge the waves: thread (head, channel)
+  const int h = tid >> 7, c = tid & (HEAD_DIM - 1);
   float M = -__builtin_inff();
 #pragma unroll
-  for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, s_part[w][h][0]);
-  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int w = 0; w < SPLIT_WAVES; ++w) M = fmaxf(M, s_part[w][h][0]);
+  float L = 0.0f, O = 0.0f;
 #pragma unroll
-  for (int w = 0; w < ATT_WAVES; ++w) {
+  for (int w = 0; w < SPLIT_WAVES; ++w) {
     const float mw = s_part[w][h][0];
-    const float f = mw == -__builtin_inff() ? 0.0f : exp2f(mw - M);
+    const float f = mw == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
     L = fmaf(f, s_part[w][h][1], L);
-    o0 = fmaf(f, s_part[w][h][2 + c2], o0);
-    o1 = fmaf(f, s_part[w][h][3 + c2], o1);
+    O = fmaf(f, s_part[w][h][2 + c], O);
   }
-  float* out = a.part + (((int64_t)P * a.splits + split) * GQA + h) * PART;
-  if ((tid & 63) == 0) {
+  float* out = a.part + (((int64_t)P * a.splits_cap + split) * GQA + h) * PART;
+  if (c == 0) {
     out[0] = M;
     out[1] = L;
   }
-  out[2 + c2] = o0;
-  out[3 + c2] = o1;
+  out[2 + c] = O;
+}
+
+// Writes one group block from codes (bytes 0..3) and bf16 scale / zero
+// point values: keys kcode[t * kstride + ch] (32 tokens), key parameters
+// ks / kz [ch]; values vcode[t * vstride + ch], value parameters
+// vs / vz[t * 4 + cg].  Thread `lane` writes its 48 bytes.
+VH_DEV void write_group(const uint8_t* kcode, int64_t kstride, const uint16_t* ks, const uint16_t* kz,
+                        const uint8_t* vcode, int64_t vstride, const uint16_t* vs, const uint16_t* vz, int lane,
+                        uint8_t* blk) {
+  const int kq = lane >> 4, r = lane & 15;
+  uint32_t D[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t code = kcode[(int64_t)(16 * t + r) * kstride + 32 * kq + 8 * cs + j] & 3u;
+        D[2 * t + (cs >> 1)] |= code << (16 * (cs & 1) + 2 * j);
+      }
+  *(uint4*)(blk + lane * 16) = make_uint4(D[0], D[1], D[2], D[3]);
+  uint32_t V[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int r8 = 0; r8 < 8; ++r8)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int tok = 16 * (j >> 2) + 4 * kq + (j & 3);
+      const uint32_t code = vcode[(int64_t)tok * vstride + 16 * r8 + r] & 3u;
+      V[r8 >> 1] |= code << (8 * (r8 & 1) + 16 * (j & 1) + 2 * (j >> 1));
+    }
+  *(uint4*)(blk + 1024 + lane * 16) = make_uint4(V[0], V[1], V[2], V[3]);
+  // parameters: lanes 0-31 four key channels each, lanes 32-63 one value token each
+  _Float16 piece[8];
+  if (lane < 32) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      piece[2 * k] = (_Float16)bf2f(ks[4 * lane + k]);
+      piece[2 * k + 1] = (_Float16)bf2f(kz[4 * lane + k]);
+    }
+  } else {
+    const int i = lane - 32, qq = i >> 3, j = i & 7;
+    const int tok = 16 * (j >> 2) + 4 * qq + (j & 3);
+#pragma unroll
+    for (int cg = 0; cg < 4; ++cg) {
+      piece[2 * cg] = (_Float16)bf2f(vs[tok * 4 + cg]);
+      piece[2 * cg + 1] = (_Float16)bf2f(vz[tok * 4 + cg]);
+    }
+  }
+  *(f16x8*)(blk + 2048 + lane * 16) = *(const f16x8*)piece;
+}
+
+// quantize_affine of one 32-element block in bfloat16 with quant range
+// [0, 3] and a scale map (ops/quantized.py:1262-1281): scale = (max - min)
+// / 3, 1 where not positive, mapped, 1 where not positive; zero point =
+// -min / scale + 0, mapped.
+struct Affine {
+  float s, zp;
+};
+
+VH_DEV Affine kivi_affine(float lo, float hi, const vh_format& sf) {
+  float s = div_bf16(rbf(hi - lo), 3.0f);
+  if (!(s > 0.0f)) s = 1.0f;
+  s = fmt_value(f2bf(s), sf, nullptr);
+  if (!(s > 0.0f)) s = 1.0f;
+  float zp = rbf(div_bf16(-lo, s) + 0.0f);
+  zp = fmt_value(f2bf(zp), sf, nullptr);
+  return {s, zp};
+}
+
+// The code of x in its block: map(bf16(bf16(x / scale) + zero_point)),
+// a byte 0..3; a NaN code (not representable in the packed cache) flags.
+VH_DEV uint8_t kivi_code(float x, const Affine& af, const vh_format& cf, int* bad) {
+  const float q = rbf(div_bf16(x, af.s) + af.zp);
+  const float c = fmt_value(f2bf(q), cf, nullptr);
+  if (isnan_f(c)) {
+    *bad = 1;
+    return 0;
+  }
+  return (uint8_t)(int)c;
+}
+
+// The fold of a completed chunk for sequence P: the RES_CAP residual tokens
+// quantized with the KIVI specs (quantize_affine: keys grouped along tokens,
+// values along channels, group 32) into groups [g0, g0 + GROUPS_PER_CHUNK)
+// of the main cache -- what a lowered decode graph stores for a completed
+// chunk (codegen/transform/quant_folding.py:1994-2065, 2634-2700).  The
+// last token (slot RES_CAP - 1, written by this step) comes from LDS.  All
+// threads of the workgroup; returns with them synchronised.
+struct FoldLds {
+  uint8_t kc[RES_CAP][HEAD_DIM];
+  uint8_t vc[RES_CAP][HEAD_DIM];
+  uint16_t ks[GROUPS_PER_CHUNK][HEAD_DIM], kz[GROUPS_PER_CHUNK][HEAD_DIM];
+  uint16_t vs[RES_CAP][4], vz[RES_CAP][4];
+  int bad;
+};
+
+VH_DEV float res_at(const uint16_t* R, const uint16_t* last, int t, int ch) {
+  return bf2f(t == RES_CAP - 1 ? last[ch] : R[t * HEAD_DIM + ch]);
+}
+
+VH_DEV void fold_chunk(const KiviArgs& a, int P, int g0, const uint16_t* newk, const uint16_t* newv, FoldLds& L,
+                       int* flag) {
+  const int tid = threadIdx.x, nthreads = blockDim.x;
+  if (tid == 0) L.bad = 0;
+  __syncthreads();
+  int bad = 0;
+  const uint16_t* K = a.kr + (int64_t)P * RES_CAP * HEAD_DIM;
+  const uint16_t* V = a.vr + (int64_t)P * RES_CAP * HEAD_DIM;
+  // keys: one column (group, channel) of 32 tokens per pass
+  for (int col = tid; col < GROUPS_PER_CHUNK * HEAD_DIM; col += nthreads) {
+    const int g = col / HEAD_DIM, ch = col % HEAD_DIM;
+    float lo = res_at(K, newk, g * KV_GROUP, ch), hi = lo;
+    for (int t = 1; t < KV_GROUP; ++t) {
+      const float x = res_at(K, newk, g * KV_GROUP + t, ch);
+      lo = nmin(lo, x);
+      hi = nmax(hi, x);
+    }
+    const Affine af = kivi_affine(lo, hi, a.sf);
+    L.ks[g][ch] = (uint16_t)f2bf(af.s);
+    L.kz[g][ch] = (uint16_t)f2bf(af.zp);
+    for (int t = 0; t < KV_GROUP; ++t)
+      L.kc[g * KV_GROUP + t][ch] = kivi_code(res_at(K, newk, g * KV_GROUP + t, ch), af, a.cf, &bad);
+  }
+  // values: one row (token, channel group) of 32 channels per pass
+  for (int row = tid; row < RES_CAP * 4; row += nthreads) {
+    const int t = row / 4, cg = row % 4;
+    float lo = res_at(V, newv, t, cg * KV_GROUP), hi = lo;
+    for (int c = 1; c < KV_GROUP; ++c) {
+      const float x = res_at(V, newv, t, cg * KV_GROUP + c);
+      lo = nmin(lo, x);
+      hi = nmax(hi, x);
+    }
+    const Affine af = kivi_affine(lo, hi, a.sf);
+    L.vs[t][cg] = (uint16_t)f2bf(af.s);
+    L.vz[t][cg] = (uint16_t)f2bf(af.zp);
+    for (int c = 0; c < KV_GROUP; ++c)
+      L.vc[t][cg * KV_GROUP + c] = kivi_code(res_at(V, newv, t, cg * KV_GROUP + c), af, a.cf, &bad);
+  }
+  if (bad) L.bad = 1;
+  __syncthreads();
+  // thread (group, lane) writes its 48 bytes of the group's block
+  for (int i = tid; i < GROUPS_PER_CHUNK * 64; i += nthreads) {
+    const int g = i >> 6, lane = i & 63;
+    uint8_t* blk = a.main + ((int64_t)P * a.group_cap + g0 + g) * GROUP_BYTES;
+    write_group(&L.kc[g * KV_GROUP][0], HEAD_DIM, L.ks[g], L.kz[g], &L.vc[g * KV_GROUP][0], HEAD_DIM,
+                &L.vs[g * KV_GROUP][0], &L.vz[g * KV_GROUP][0], lane, blk);
+  }
+  if (tid == 0 && L.bad) atomicOr(flag, VH_DECODE_ERR_KV_CODE);
+  __syncthreads();
 }
 
 // Per (batch, query head): attention over the residual window (its n_res
@@ -685,44 +873,62 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   __shared__ float s_p[RES_CAP];
   __shared__ float s_o[16][HEAD_DIM];
   __shared__ float s_red[4];
+  __shared__ uint16_t s_newk[HEAD_DIM], s_newv[HEAD_DIM];
+  __shared__ FoldLds s_fold;
+  const int n_main = a.state[0], n_res = a.state[1];
+  const int pos = n_main + n_res;
+  const int splits = (n_main / KV_GROUP + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
   const int bh = blockIdx.x, b = bh / a.nq, H = bh % a.nq, kvh = H / GQA, h = H % GQA;
   const int P = b * a.nkv + kvh, tid = threadIdx.x;
+  if (!state_ok(a, n_main, n_res)) {
+    if (tid < HEAD_DIM) {
+      const int64_t idx = (int64_t)b * a.nq * HEAD_DIM + H * HEAD_DIM + tid;
+      if (attn) attn[idx] = 0;
+      fq[idx] = (_Float16)0.0f;
+    }
+    if (bh == 0 && tid == 0) atomicOr(flag, VH_DECODE_ERR_KV_STATE);
+    return;
+  }
   const int c = tid & (HEAD_DIM - 1);              // channel (first half of the block: merge / output)
   const int tk = tid >> 1, kh = tid & 1;           // key row tk, channel half kh
   const int co = tid & 15, ts = tid >> 4;          // value octet co, token subset ts (slots ts + 16u)
   const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
+  const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
+  const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
   // every independent load goes out first (one round trip)
   uint4 kw[HEAD_DIM / 16], vw[RES_CAP / 16];
   const uint4* kp = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + tk) * HEAD_DIM + kh * (HEAD_DIM / 2));
   const uint4* vp = (const uint4*)(a.vr + (int64_t)P * RES_CAP * HEAD_DIM) + co;
 #pragma unroll
-  for (int i = 0; i < HEAD_DIM / 16; ++i) kw[i] = tk < a.n_res ? kp[i] : make_uint4(0u, 0u, 0u, 0u);
+  for (int i = 0; i < HEAD_DIM / 16; ++i) kw[i] = tk < n_res ? kp[i] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
   for (int u = 0; u < RES_CAP / 16; ++u)
-    vw[u] = ts + 16 * u < a.n_res ? vp[(int64_t)(ts + 16 * u) * (HEAD_DIM / 8)] : make_uint4(0u, 0u, 0u, 0u);
-  const float* base = a.part + ((int64_t)P * a.splits * GQA + h) * PART;
+    vw[u] = ts + 16 * u < n_res ? vp[(int64_t)(ts + 16 * u) * (HEAD_DIM / 8)] : make_uint4(0u, 0u, 0u, 0u);
+  const float* base = a.part + ((int64_t)P * a.splits_cap * GQA + h) * PART;
   float pm[COMBINE_PRELOAD], pl[COMBINE_PRELOAD], po[COMBINE_PRELOAD];
   const bool merger = tid < HEAD_DIM;
 #pragma unroll
   for (int s = 0; s < COMBINE_PRELOAD; ++s) {
-    const bool ok = merger && s < a.splits;
+    const bool ok = merger && s < splits;
     const float* ps = base + (int64_t)s * GQA * PART;
     pm[s] = ok ? ps[0] : -__builtin_inff();
     pl[s] = ok ? ps[1] : 0.0f;
     po[s] = ok ? ps[2 + c] : 0.0f;
   }
   // RoPE of this step's query / key (channel c; the second half of the block duplicates)
-  const float qc = bf2f(rope1(qrow + H * HEAD_DIM, a.cos, a.sin, c));
-  const uint16_t kn = rope1(qrow + (a.nq + kvh) * HEAD_DIM, a.cos, a.sin, c);
+  const float qc = bf2f(rope1(qrow + H * HEAD_DIM, cs_, sn_, c));
+  const uint16_t kn = rope1(qrow + (a.nq + kvh) * HEAD_DIM, cs_, sn_, c);
   const uint16_t vn = qrow[(a.nq + a.nkv + kvh) * HEAD_DIM + c];
   if (merger) s_q[c] = qc;
   // this step's own score, q . k_new
-  const float s_new = block_sum256(merger ? qc * bf2f(kn) : 0.0f, s_red) * a.scale_log2;
+  const float s_new = eager_score_log2(block_sum256(merger ? qc * bf2f(kn) : 0.0f, s_red), a.scale);
   if (h == 0 && merger) {
     // this step's key (after RoPE) and value enter residual slot n_res (read
     // by later steps only: this step takes them from the qkv row)
-    a.kr[((int64_t)P * RES_CAP + a.n_res) * HEAD_DIM + c] = kn;
-    a.vr[((int64_t)P * RES_CAP + a.n_res) * HEAD_DIM + c] = vn;
+    a.kr[((int64_t)P * RES_CAP + n_res) * HEAD_DIM + c] = kn;
+    a.vr[((int64_t)P * RES_CAP + n_res) * HEAD_DIM + c] = vn;
+    s_newk[c] = kn;
+    s_newv[c] = vn;
   }
   // score of residual slot tk: two threads, 64 channels each
   float acc = 0.0f;
@@ -744,10 +950,10 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   }
   acc += __shfl_xor(acc, 1);
   float sc = -__builtin_inff();
-  if (tk < a.n_res) sc = acc * a.scale_log2;
-  else if (tk == a.n_res) sc = s_new;
+  if (tk < n_res) sc = eager_score_log2(acc, a.scale);
+  else if (tk == n_res) sc = s_new;
   const float mr = block_max256(kh == 0 ? sc : -__builtin_inff(), s_red);
-  const float p = tk <= a.n_res ? exp2f(sc - mr) : 0.0f;
+  const float p = tk <= n_res ? exp2f(sc - mr) : 0.0f;
   if (kh == 0) s_p[tk] = p;
   const float lr = block_sum256(kh == 0 ? p : 0.0f, s_red);
   {
@@ -766,95 +972,79 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
     for (int j = 0; j < 8; ++j) s_o[ts][co * 8 + j] = o8[j];
   }
   __syncthreads();
-  if (!merger) return;
-  float orr = s_p[a.n_res] * bf2f(vn);
+  if (merger) {
+    float orr = s_p[n_res] * bf2f(vn);
 #pragma unroll
-  for (int t16 = 0; t16 < 16; ++t16) orr += s_o[t16][c];
-  // merge with the main-cache splits
-  float M = mr;
+    for (int t16 = 0; t16 < 16; ++t16) orr += s_o[t16][c];
+    // merge with the main-cache splits
+    float M = mr;
 #pragma unroll
-  for (int s = 0; s < COMBINE_PRELOAD; ++s) M = fmaxf(M, pm[s]);
-  for (int s = COMBINE_PRELOAD; s < a.splits; ++s) M = fmaxf(M, base[(int64_t)s * GQA * PART]);
-  const float fr = exp2f(mr - M);
-  float L = lr * fr, O = orr * fr;
+    for (int s = 0; s < COMBINE_PRELOAD; ++s) M = fmaxf(M, pm[s]);
+    for (int s = COMBINE_PRELOAD; s < splits; ++s) M = fmaxf(M, base[(int64_t)s * GQA * PART]);
+    const float fr = exp2f(mr - M);
+    float L = lr * fr, O = orr * fr;
 #pragma unroll
-  for (int s = 0; s < COMBINE_PRELOAD; ++s) {
-    const float f = pm[s] == -__builtin_inff() ? 0.0f : exp2f(pm[s] - M);
-    L = fmaf(f, pl[s], L);
-    O = fmaf(f, po[s], O);
+    for (int s = 0; s < COMBINE_PRELOAD; ++s) {
+      const float f = pm[s] == -__builtin_inff() ? 0.0f : exp2f(pm[s] - M);
+      L = fmaf(f, pl[s], L);
+      O = fmaf(f, po[s], O);
+    }
+    for (int s = COMBINE_PRELOAD; s < splits; ++s) {
+      const float* ps = base + (int64_t)s * GQA * PART;
+      const float f = ps[0] == -__builtin_inff() ? 0.0f : exp2f(ps[0] - M);
+      L = fmaf(f, ps[1], L);
+      O = fmaf(f, ps[2 + c], O);
+    }
+    const float o = rbf(O / L);
+    const int64_t idx = (int64_t)b * a.nq * HEAD_DIM + H * HEAD_DIM + c;
+    if (attn) attn[idx] = (uint16_t)f2bf(o);
+    const Mx8Scale scl = mx8_scale(max16(fabsf(o)));
+    fq[idx] = fq_half(mx8_fq(o, scl), flag);
   }
-  for (int s = COMBINE_PRELOAD; s < a.splits; ++s) {
-    const float* ps = base + (int64_t)s * GQA * PART;
-    const float f = ps[0] == -__builtin_inff() ? 0.0f : exp2f(ps[0] - M);
-    L = fmaf(f, ps[1], L);
-    O = fmaf(f, ps[2 + c], O);
+  if (!a.advance) return;
+  // The cache bookkeeping after the step: when this step filled the
+  // residual's last slot, head 0's workgroup of each sequence folds the
+  // sequence's chunk into the main cache (no other workgroup writes it, and
+  // this step reads no main group at or past g0); then the last workgroup to
+  // finish -- every one has read the state by then -- writes the new state.
+  const bool fold = n_res + 1 == RES_CAP;
+  const int g0 = n_main / KV_GROUP;
+  const bool room = g0 + GROUPS_PER_CHUNK <= a.group_cap;
+  if (fold && room && h == 0) fold_chunk(a, P, g0, s_newk, s_newv, s_fold, flag);
+  if (tid == 0) {
+    if (fold && !room && bh == 0) atomicOr(flag, VH_DECODE_ERR_KV_FULL);
+    __threadfence();
+    const int done = atomicAdd(&a.state[2], 1);
+    if (done == (int)gridDim.x - 1) {
+      if (fold && room) {
+        a.state[0] = n_main + RES_CAP;
+        a.state[1] = 0;
+      } else if (!fold) {
+        a.state[1] = n_res + 1;
+      }
+      a.state[2] = 0;
+      __threadfence();
+    }
   }
-  const float o = rbf(O / L);
-  const int64_t idx = (int64_t)b * a.nq * HEAD_DIM + H * HEAD_DIM + c;
-  if (attn) attn[idx] = (uint16_t)f2bf(o);
-  const Mx8Scale scl = mx8_scale(max16(fabsf(o)));
-  fq[idx] = fq_half(mx8_fq(o, scl), flag);
 }
 
-// Bake the main cache: one thread per (P, g, lane) writes its key codes
-// (2 x 8 B), value codes (16 B) and one 16-byte piece of the scale / zero
-// point quarter (lanes 0-31 keys, 32-63 values).
+// Bake reference-form quantize_affine outputs (codes as bytes, bf16
+// parameters) of T tokens into groups [g0, g0 + T / 32) of each sequence:
+// one thread per (P, group, lane).
 __global__ void __launch_bounds__(256) k_bake_kivi(const uint8_t* __restrict__ kcode, const uint16_t* __restrict__ ks,
                                                    const uint16_t* __restrict__ kz, const uint8_t* __restrict__ vcode,
                                                    const uint16_t* __restrict__ vs, const uint16_t* __restrict__ vz,
-                                                   int64_t P, int64_t T, uint8_t* __restrict__ out) {
+                                                   int64_t P, int64_t T, int64_t group_cap, int64_t g0,
+                                                   uint8_t* __restrict__ out) {
   const int64_t G = T / KV_GROUP;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= P * G * 64) return;
-  const int lane = (int)(t % 64), q = lane >> 4;
+  const int lane = (int)(t % 64);
   const int64_t g = (t / 64) % G, p = t / (64 * G);
-  uint8_t* blk = out + (p * G + g) * GROUP_BYTES;
-  // keys: tile tt, token 32 g + 16 tt + lane % 16
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const uint8_t* src = kcode + (p * T + g * KV_GROUP + tt * 16 + (lane & 15)) * HEAD_DIM;
-    uint32_t w[2] = {0u, 0u};
-#pragma unroll
-    for (int cs = 0; cs < 4; ++cs)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t c = src[cs * 32 + q * 8 + j] & 3u;
-        const int k = (cs & 1) * 4 + j / 2;
-        w[cs >> 1] |= c << ((j & 1) * 16 + 2 * k);
-      }
-    *(uint2*)(blk + tt * 512 + lane * 8) = make_uint2(w[0], w[1]);
-  }
-  // values: tile r8 (channel 16 r8 + lane % 16), tokens tok(q, j)
-  uint32_t v[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int r8 = 0; r8 < 8; ++r8)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t tok = g * KV_GROUP + 16 * (j / 4) + 4 * q + (j % 4);
-      const uint32_t c = vcode[(p * T + tok) * HEAD_DIM + r8 * 16 + (lane & 15)] & 3u;
-      const int k = (r8 & 1) * 4 + j / 2;
-      v[r8 >> 1] |= c << ((j & 1) * 16 + 2 * k);
-    }
-  *(uint4*)(blk + 1024 + lane * 16) = make_uint4(v[0], v[1], v[2], v[3]);
-  _Float16 piece[8];
-  if (lane < 32) {
-    // key piece: slot (cs, qq) = lane / 2, half 0 scale / 1 zp
-    const int slot = lane >> 1, cs = slot >> 2, qq = slot & 3;
-    const uint16_t* src = ((lane & 1) ? kz : ks) + (p * G + g) * HEAD_DIM + cs * 32 + qq * 8;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) piece[j] = (_Float16)bf2f(src[j]);
-    *(f16x8*)(blk + 2048 + lane * 16) = *(const f16x8*)piece;
-  } else {
-    // value piece: (qq, j) = (lane - 32) / 8, % 8 -> 4 groups x (scale, zp)
-    const int i = lane - 32, qq = i >> 3, j = i & 7;
-    const int64_t tok = g * KV_GROUP + 16 * (j / 4) + 4 * qq + (j % 4);
-#pragma unroll
-    for (int gc = 0; gc < 4; ++gc) {
-      piece[2 * gc] = (_Float16)bf2f(vs[(p * T + tok) * 4 + gc]);
-      piece[2 * gc + 1] = (_Float16)bf2f(vz[(p * T + tok) * 4 + gc]);
-    }
-    *(f16x8*)(blk + 2560 + i * 16) = *(const f16x8*)piece;
-  }
+  uint8_t* blk = out + (p * group_cap + g0 + g) * GROUP_BYTES;
+  const int64_t tok0 = p * T + g * KV_GROUP;
+  write_group(kcode + tok0 * HEAD_DIM, HEAD_DIM, ks + (p * G + g) * HEAD_DIM, kz + (p * G + g) * HEAD_DIM,
+              vcode + tok0 * HEAD_DIM, HEAD_DIM, vs + tok0 * 4, vz + tok0 * 4, lane, blk);
 }
 
 __global__ void __launch_bounds__(256) k_bake_kivi_residual(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -926,12 +1116,14 @@ extern "C" int vh_gemv_mx8(const uint16_t* x_fq, int64_t M, int64_t K, const uin
 
 extern "C" int vh_kivi_bake(const uint8_t* k_codes, const uint16_t* k_scale, const uint16_t* k_zp,
                             const uint8_t* v_codes, const uint16_t* v_scale, const uint16_t* v_zp, int64_t P,
-                            int64_t T, uint8_t* main_out, vh_stream_t stream) {
+                            int64_t T, int64_t group_cap, int64_t g0, uint8_t* main_out, vh_stream_t stream) {
   VH_REQUIRE(k_codes && k_scale && k_zp && v_codes && v_scale && v_zp && main_out, "vh_kivi_bake: null argument");
   VH_REQUIRE(P > 0 && T > 0 && T % KV_GROUP == 0, "vh_kivi_bake: needs T %% 32 == 0");
+  VH_REQUIRE(g0 >= 0 && g0 + T / KV_GROUP <= group_cap, "vh_kivi_bake: groups [%lld, %lld) exceed the capacity %lld",
+             (long long)g0, (long long)(g0 + T / KV_GROUP), (long long)group_cap);
   const int64_t G = T / KV_GROUP;
   hipLaunchKernelGGL(k_bake_kivi, dim3(blocks_for(P * G * 64, 256)), dim3(256), 0, vh::as_stream(stream), k_codes,
-                     k_scale, k_zp, v_codes, v_scale, v_zp, P, T, main_out);
+                     k_scale, k_zp, v_codes, v_scale, v_zp, P, T, group_cap, g0, main_out);
   return vh::check_launch("vh_kivi_bake");
 }
 
@@ -945,27 +1137,45 @@ extern "C" int vh_kivi_bake_residual(const uint16_t* k, const uint16_t* v, int64
   return vh::check_launch("vh_kivi_bake_residual");
 }
 
-extern "C" int vh_kivi_attention(const vh_kivi_desc* d, vh_stream_t stream) {
-  VH_REQUIRE(d && d->qkv && d->cos && d->sin && d->kr && d->vr && d->attn_fq && d->flag,
-             "vh_kivi_attention: null argument");
-  VH_REQUIRE(d->batch >= 1 && d->nkv >= 1 && d->nq == GQA * d->nkv, "vh_kivi_attention: needs nq == 4 nkv");
-  VH_REQUIRE(d->head_dim == HEAD_DIM, "vh_kivi_attention: head_dim must be %d", HEAD_DIM);
-  VH_REQUIRE(d->n_main >= 0 && d->n_main % KV_GROUP == 0, "vh_kivi_attention: n_main must be a multiple of 32");
-  VH_REQUIRE(d->n_main == 0 || d->main, "vh_kivi_attention: missing main cache");
-  VH_REQUIRE(d->n_res >= 0 && d->n_res < RES_CAP, "vh_kivi_attention: n_res must be in [0, %d)", RES_CAP);
+namespace {
+
+int kivi_common(const vh_kivi_desc* d, KiviArgs& a) {
+  VH_REQUIRE(d && d->main && d->kr && d->vr && d->state && d->flag, "vh_kivi: null argument");
+  VH_REQUIRE(d->batch >= 1 && d->nkv >= 1 && d->nq == GQA * d->nkv, "vh_kivi: needs nq == 4 nkv");
+  VH_REQUIRE(d->head_dim == HEAD_DIM, "vh_kivi: head_dim must be %d", HEAD_DIM);
+  VH_REQUIRE(d->group_cap >= GROUPS_PER_CHUNK, "vh_kivi: the main cache must hold at least one chunk");
+  const int64_t splits_cap = (d->group_cap + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
+  VH_REQUIRE(splits_cap <= 65535 && d->batch * d->nkv <= 65535, "vh_kivi: cache too large");
+  VH_REQUIRE(d->qkv && d->rope && d->attn_fq && d->part, "vh_kivi_attention: null argument");
+  VH_REQUIRE(d->max_pos >= 1, "vh_kivi_attention: empty RoPE table");
   VH_REQUIRE(d->qkv_ld >= (int64_t)(d->nq + 2 * d->nkv) * HEAD_DIM, "vh_kivi_attention: qkv_ld too small");
-  const int G = (int)(d->n_main / KV_GROUP);
-  const int splits = (G + STEPS_PER_SPLIT - 1) / STEPS_PER_SPLIT;
-  VH_REQUIRE(d->part_floats >= (int64_t)d->batch * d->nkv * splits * GQA * PART,
+  VH_REQUIRE(d->part_floats >= d->batch * d->nkv * splits_cap * GQA * PART,
              "vh_kivi_attention: workspace too small (needs %lld floats)",
-             (long long)d->batch * d->nkv * splits * GQA * PART);
-  VH_REQUIRE(splits == 0 || d->part, "vh_kivi_attention: missing workspace");
-  KiviArgs a{d->qkv, d->qkv_ld, d->cos, d->sin, d->main, d->kr, d->vr, G, (int32_t)d->n_res, (int32_t)d->nkv,
-             (int32_t)d->nq, splits, d->softmax_scale * 1.4426950408889634f, d->part};
+             (long long)(d->batch * d->nkv * splits_cap * GQA * PART));
+  a = KiviArgs{d->qkv, d->qkv_ld, d->rope, d->max_pos, d->main, d->group_cap, d->kr, d->vr, d->state,
+               (int32_t)d->nkv, (int32_t)d->nq, (int32_t)splits_cap, d->softmax_scale, d->part,
+               d->advance ? 1 : 0, d->scale_fmt, d->code_fmt};
+  return VH_OK;
+}
+
+}  // namespace
+
+extern "C" int vh_kivi_attention(const vh_kivi_desc* d, vh_stream_t stream) {
+  KiviArgs a;
+  if (int e = kivi_common(d, a)) return e;
+  if (d->advance) {
+    VH_REQUIRE(d->scale_fmt.kind == VH_FMT_MINIFLOAT || d->scale_fmt.kind == VH_FMT_INT ||
+                   d->scale_fmt.kind == VH_FMT_IDENTITY || d->scale_fmt.kind == VH_FMT_POSIT,
+               "vh_kivi_attention: the scale map must be a closed form (minifloat, int, posit or identity)");
+    VH_REQUIRE(d->code_fmt.kind == VH_FMT_INT && d->code_fmt.p0 >= 0 && d->code_fmt.p1 <= 3,
+               "vh_kivi_attention: the code map must be an integer range within [0, 3]");
+  }
   hipStream_t s = vh::as_stream(stream);
   const unsigned P = (unsigned)(d->batch * d->nkv);
-  if (splits > 0) hipLaunchKernelGGL(k_kivi_split, dim3((unsigned)splits, P), dim3(ATT_WAVES * 64), 0, s, a);
+  hipLaunchKernelGGL(k_kivi_split, dim3((unsigned)a.splits_cap, P), dim3(SPLIT_WAVES * 64), 0, s, a);
   hipLaunchKernelGGL(k_kivi_combine, dim3((unsigned)(d->batch * d->nq)), dim3(COMBINE_THREADS), 0, s, a, d->attn,
                      (_Float16*)d->attn_fq, (int*)d->flag);
   return vh::check_launch("vh_kivi_attention");
 }
+
+

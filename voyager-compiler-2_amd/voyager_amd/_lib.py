@@ -117,7 +117,7 @@ _SIGNATURES = {
     "vh_rmsnorm_mx8": ([_P, _P, _I64, _I64, _F32, _P, _P, _P, _P], _I32),
     "vh_mx8_bake": ([_P, _P, _I32, _I64, _I64, _I32, _P, _P, _P, _P], _I32),
     "vh_gemv_mx8": ([_P, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P], _I32),
-    "vh_kivi_bake": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P], _I32),
+    "vh_kivi_bake": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "vh_kivi_bake_residual": ([_P, _P, _I64, _I64, _P, _P, _P], _I32),
     # vh_kivi_attention takes a vh_kivi_desc*; voyager_amd.decode.KiviDesc mirrors it.
     "vh_kivi_attention": ([_P, _P], _I32),
@@ -134,6 +134,9 @@ _SIGNATURES = {
 
 DECODE_ERR_FP16_RANGE = 1
 DECODE_ERR_WEIGHT_RANGE = 2
+DECODE_ERR_KV_CODE = 4
+DECODE_ERR_KV_FULL = 8
+DECODE_ERR_KV_STATE = 16
 KIVI_RES_CAP = 128
 FILTER_NOALLOC_SCRATCH_BYTES = 8 << 20
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2

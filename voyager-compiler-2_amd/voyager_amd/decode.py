@@ -35,20 +35,27 @@ def _stream(t: torch.Tensor) -> ctypes.c_void_p:
 
 
 class ErrorFlag:
-    """The device int32 the decode kernels OR ``DECODE_ERR_*`` bits into."""
+    """The device int32 the decode kernels OR ``DECODE_ERR_*`` bits into.
+    Kernels never clear it: read it with :meth:`check`, which clears it."""
 
     def __init__(self, device):
         self.t = torch.zeros(1, dtype=torch.int32, device=device)
 
+    _WHAT = (
+        (_lib.DECODE_ERR_FP16_RANGE, "an activation block exceeds the fp16 range of the GEMV operand"),
+        (_lib.DECODE_ERR_WEIGHT_RANGE, "a weight block exponent is outside [-24, 5]"),
+        (_lib.DECODE_ERR_KV_CODE, "a KIVI chunk folded into the main cache held a value whose code is NaN"),
+        (_lib.DECODE_ERR_KV_FULL, "the KIVI main cache had no room for a completed chunk"),
+        (_lib.DECODE_ERR_KV_STATE, "the KIVI cache state was out of range (nothing was computed)"),
+    )
+
     def check(self) -> None:
-        """Synchronising check: raise if a kernel flagged unrepresentable data."""
+        """Synchronising check: clear the flag, and raise if a kernel flagged
+        unrepresentable data since the last check."""
         v = int(self.t.item())
         if v:
-            what = []
-            if v & _lib.DECODE_ERR_FP16_RANGE:
-                what.append("an activation block exceeds the fp16 range of the GEMV operand")
-            if v & _lib.DECODE_ERR_WEIGHT_RANGE:
-                what.append("a weight block exponent is outside [-24, 5]")
+            self.t.zero_()
+            what = [msg for bit, msg in self._WHAT if v & bit]
             raise RuntimeError("voyager_amd decode: " + "; ".join(what))
 
 
@@ -125,14 +132,16 @@ class KiviDesc(ctypes.Structure):
 
     _fields_ = [
         ("qkv", ctypes.c_void_p), ("qkv_ld", ctypes.c_int64),
-        ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
-        ("main", ctypes.c_void_p),
+        ("rope", ctypes.c_void_p), ("max_pos", ctypes.c_int64),
+        ("main", ctypes.c_void_p), ("group_cap", ctypes.c_int64),
         ("kr", ctypes.c_void_p), ("vr", ctypes.c_void_p),
+        ("state", ctypes.c_void_p),
         ("batch", ctypes.c_int64), ("nkv", ctypes.c_int64), ("nq", ctypes.c_int64), ("head_dim", ctypes.c_int64),
-        ("n_main", ctypes.c_int64), ("n_res", ctypes.c_int64),
         ("softmax_scale", ctypes.c_float),
         ("part", ctypes.c_void_p), ("part_floats", ctypes.c_int64),
         ("attn", ctypes.c_void_p), ("attn_fq", ctypes.c_void_p), ("flag", ctypes.c_void_p),
+        ("advance", ctypes.c_int32),
+        ("scale_fmt", _lib.Format), ("code_fmt", _lib.Format),
     ]
 
 
@@ -140,53 +149,78 @@ def _vp(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-class KiviCache:
-    """A KIVI KV cache for ``batch x nkv`` sequences: the quantized main part
-    (``n_main`` tokens, a multiple of 32) in the attention layout and a
-    ``VH_KIVI_RES_CAP``-slot full-precision residual window holding
-    ``n_res`` tokens."""
+RES_CAP = _lib.KIVI_RES_CAP
+GROUPS_PER_SPLIT = 16  # groups one attention workgroup streams
 
-    def __init__(self, batch: int, nkv: int, n_main: int, device):
-        if n_main % KIVI_GROUP:
-            raise ValueError("KiviCache: n_main must be a multiple of 32")
-        self.batch, self.nkv, self.n_main, self.n_res = batch, nkv, n_main, 0
-        P = batch * nkv
-        self.P = P
-        G = n_main // KIVI_GROUP
+
+class KiviCache:
+    """A KIVI KV cache for ``batch x nkv`` sequences with room for
+    ``capacity`` tokens: a quantized main part in the attention layout
+    (whole groups of 32 tokens) and a ``RES_CAP``-slot full-precision
+    residual window holding the chunk being filled (the split cache of
+    ``codegen/transform/quant_folding.py:1025-1120``).  The state the kernels
+    use -- tokens in the main part, residual slots filled -- lives in device
+    memory (``state``); ``n_main`` / ``n_res`` mirror it on the host, advanced
+    by the same rule without a device read."""
+
+    def __init__(self, batch: int, nkv: int, capacity: int, device):
+        if capacity % KIVI_GROUP or capacity < RES_CAP:
+            raise ValueError(f"KiviCache: capacity must be a multiple of 32 and at least {RES_CAP}")
+        self.batch, self.nkv, self.capacity = batch, nkv, capacity
+        self.P = batch * nkv
+        self.group_cap = capacity // KIVI_GROUP
+        self.n_main = self.n_res = 0
         bf = torch.bfloat16
         # one 3072-byte block per 32 tokens: key / value codes, key / value scale + zero point
-        self.main = torch.zeros(P * G * 3072, dtype=torch.uint8, device=device)
-        cap = _lib.KIVI_RES_CAP
-        self.kr = torch.zeros(P, cap, HEAD_DIM, dtype=bf, device=device)
-        self.vr = torch.zeros(P, cap, HEAD_DIM, dtype=bf, device=device)
+        self.main = torch.zeros(self.P * self.group_cap * 3072, dtype=torch.uint8, device=device)
+        self.kr = torch.zeros(self.P, RES_CAP, HEAD_DIM, dtype=bf, device=device)
+        self.vr = torch.zeros(self.P, RES_CAP, HEAD_DIM, dtype=bf, device=device)
+        self.state = torch.zeros(4, dtype=torch.int32, device=device)
+        # the KIVI specs' maps (uint2 codes, fp16_e5m10 scale / zero point), for the device fold
+        self.code_map = formats.quantization_map("uint2", device)
+        self.scale_map = formats.quantization_map("fp16_e5m10", device)
+        self.code_fmt = formats.classify(self.code_map).fmt
+        self.scale_fmt = formats.classify(self.scale_map).fmt
+
+    @property
+    def position(self) -> int:
+        """The position of the next step's token."""
+        return self.n_main + self.n_res
 
     @classmethod
-    def from_bf16(cls, k_main: torch.Tensor, v_main: torch.Tensor, k_res: torch.Tensor, v_res: torch.Tensor):
+    def from_bf16(cls, k_main: torch.Tensor, v_main: torch.Tensor, k_res: torch.Tensor, v_res: torch.Tensor,
+                  capacity: Optional[int] = None):
         """Quantize ``[batch, nkv, T, 128]`` keys / values with the KIVI specs
         (``quantize_affine`` on the GPU) and bake them; the residual tokens
-        ``[batch, nkv, n, 128]`` fill the first n slots.  Returns the cache and
-        the reference-form ``(scale, zero_point, codes)`` of keys and values."""
+        ``[batch, nkv, n, 128]`` fill the first n slots.  ``capacity``
+        (default: T plus two chunks) bounds the tokens the cache can grow to.
+        Returns the cache and the reference-form ``(scale, zero_point,
+        codes)`` of keys and values."""
         B, nkv, T, D = k_main.shape
         if D != HEAD_DIM:
             raise ValueError(f"KiviCache: head_dim must be {HEAD_DIM}")
         dev = k_main.device
-        c = cls(B, nkv, T, dev)
+        c = cls(B, nkv, capacity if capacity is not None else T + 2 * RES_CAP, dev)
         kq = vq = None
         if T:
-            qtab = formats.quantization_map("uint2", dev)
-            stab = formats.quantization_map("fp16_e5m10", dev)
-            kq = _quantize_affine_cuda(k_main, qtab, [-2], KIVI_GROUP, 0.0, 3.0, stab)
-            vq = _quantize_affine_cuda(v_main, qtab, [-1], KIVI_GROUP, 0.0, 3.0, stab)
+            kq = _quantize_affine_cuda(k_main, c.code_map, [-2], KIVI_GROUP, 0.0, 3.0, c.scale_map)
+            vq = _quantize_affine_cuda(v_main, c.code_map, [-1], KIVI_GROUP, 0.0, 3.0, c.scale_map)
             c.load_main(kq, vq)
         c.load_residual(k_res, v_res)
         return c, kq, vq
 
     def load_main(self, kq, vq) -> None:
         """Bake reference-form ``quantize_affine`` outputs (keys grouped along
-        tokens, values along channels) into the main cache."""
+        tokens, values along channels) of T tokens as the main cache."""
         ks, kz, kcode = kq
         vs, vz, vcode = vq
-        P, T = self.P, self.n_main
+        P = self.P
+        T = kcode.numel() // (P * HEAD_DIM)
+        if T % KIVI_GROUP or T + RES_CAP > self.capacity:
+            raise ValueError(f"KiviCache: {T} main tokens (a multiple of 32) plus a chunk must fit the capacity "
+                             f"{self.capacity}")
+        self.n_main = T
+        self._sync_state()
         if T == 0:
             return
         kc8 = kcode.reshape(P, T, HEAD_DIM).to(torch.uint8).contiguous()
@@ -196,15 +230,16 @@ class KiviCache:
         for t in (ks_, kz_, vs_, vz_):
             if t.dtype != torch.bfloat16:
                 raise TypeError("KiviCache: scales / zero points must be bfloat16")
-        st = load().vh_kivi_bake(ptr(kc8), ptr(ks_), ptr(kz_), ptr(vc8), ptr(vs_), ptr(vz_), P, T, ptr(self.main),
-                                 _stream(kc8))
+        st = load().vh_kivi_bake(ptr(kc8), ptr(ks_), ptr(kz_), ptr(vc8), ptr(vs_), ptr(vz_), P, T, self.group_cap, 0,
+                                 ptr(self.main), _stream(kc8))
         check(st, "vh_kivi_bake")
 
     def load_residual(self, k_res: torch.Tensor, v_res: torch.Tensor) -> None:
         n = k_res.shape[2]
-        if n >= _lib.KIVI_RES_CAP:
-            raise ValueError("KiviCache: the residual window holds at most 127 tokens before a step")
+        if n >= RES_CAP:
+            raise ValueError(f"KiviCache: the residual window holds at most {RES_CAP - 1} tokens before a step")
         self.n_res = n
+        self._sync_state()
         if n == 0:
             return
         k = k_res.reshape(self.P, n, HEAD_DIM).bfloat16().contiguous()
@@ -212,39 +247,64 @@ class KiviCache:
         st = load().vh_kivi_bake_residual(ptr(k), ptr(v), self.P, n, ptr(self.kr), ptr(self.vr), _stream(k))
         check(st, "vh_kivi_bake_residual")
 
+    def _sync_state(self) -> None:
+        self.state.copy_(torch.tensor([self.n_main, self.n_res, 0, 0], dtype=torch.int32))
+
+    def advance_host(self) -> None:
+        """Move the host mirror past one step, as ``vh_kivi_advance`` moves the
+        device state: a step that fills the last residual slot folds the
+        chunk into the main cache."""
+        if self.n_res + 1 == RES_CAP:
+            if self.n_main + RES_CAP <= self.capacity:
+                self.n_main += RES_CAP
+                self.n_res = 0
+        else:
+            self.n_res += 1
+
+    def device_state(self):
+        """``(n_main, n_res)`` read from the device (synchronising)."""
+        v = self.state.tolist()
+        return int(v[0]), int(v[1])
+
     def residual_tokens(self, n: int):
         """The first n residual keys / values as ``[batch, nkv, n, 128]`` bf16."""
         k = self.kr[:, :n].reshape(self.batch, self.nkv, n, HEAD_DIM)
         v = self.vr[:, :n].reshape(self.batch, self.nkv, n, HEAD_DIM)
         return k, v
 
+    def splits_cap(self) -> int:
+        return -(-self.group_cap // GROUPS_PER_SPLIT)
 
-def part_floats(batch: int, nkv: int, n_main: int) -> int:
-    splits = -(-(n_main // KIVI_GROUP) // 16)
-    return max(1, batch * nkv * splits * GQA * (HEAD_DIM + 2))
+    def part_floats(self) -> int:
+        return self.P * self.splits_cap() * GQA * (HEAD_DIM + 2)
 
 
-def kivi_attention(qkv: torch.Tensor, cache: KiviCache, cos: torch.Tensor, sin: torch.Tensor, nq: int,
-                   flag: ErrorFlag, part: Optional[torch.Tensor] = None, attn: Optional[torch.Tensor] = None,
-                   attn_fq: Optional[torch.Tensor] = None, advance: bool = True) -> torch.Tensor:
-    """Attention of this step's queries over the cache (RoPE applied to q and
-    the new key inside; the new key / value enter residual slot ``n_res``).
-    Returns the fp16 fake quantization of the attention output; ``attn``
-    receives the bf16 output."""
+def kivi_attention(qkv: torch.Tensor, cache: KiviCache, rope: torch.Tensor, nq: int, flag: ErrorFlag,
+                   part: Optional[torch.Tensor] = None, attn: Optional[torch.Tensor] = None,
+                   attn_fq: Optional[torch.Tensor] = None, advance: bool = False) -> torch.Tensor:
+    """Attention of this step's queries over the cache at the cache's own
+    position (RoPE from ``rope`` [2, max_pos, 128] applied to q and the new
+    key inside; the new key / value enter residual slot ``n_res``).  With
+    ``advance`` the cache moves past the step's token on the device (folding
+    a completed residual chunk into the main cache), and its host mirror
+    with it.  Returns the fp16 fake quantization of the attention output;
+    ``attn`` receives the bf16 output."""
     B = cache.batch
     dev = qkv.device
     if part is None:
-        part = torch.empty(part_floats(B, cache.nkv, cache.n_main), dtype=torch.float32, device=dev)
+        part = torch.empty(cache.part_floats(), dtype=torch.float32, device=dev)
     if attn_fq is None:
         attn_fq = torch.empty(B, nq * HEAD_DIM, dtype=torch.float16, device=dev)
-    d = KiviDesc(qkv=qkv.data_ptr(), qkv_ld=qkv.stride(0), cos=cos.data_ptr(), sin=sin.data_ptr(),
-                 main=_vp(cache.main) if cache.n_main else None, kr=_vp(cache.kr), vr=_vp(cache.vr), batch=B, nkv=cache.nkv, nq=nq, head_dim=HEAD_DIM,
-                 n_main=cache.n_main, n_res=cache.n_res, softmax_scale=HEAD_DIM ** -0.5, part=part.data_ptr(),
-                 part_floats=part.numel(), attn=_vp(attn), attn_fq=attn_fq.data_ptr(), flag=flag.t.data_ptr())
+    d = KiviDesc(qkv=qkv.data_ptr(), qkv_ld=qkv.stride(0), rope=rope.data_ptr(), max_pos=rope.shape[1],
+                 main=cache.main.data_ptr(), group_cap=cache.group_cap, kr=cache.kr.data_ptr(),
+                 vr=cache.vr.data_ptr(), state=cache.state.data_ptr(), batch=B, nkv=cache.nkv, nq=nq,
+                 head_dim=HEAD_DIM, softmax_scale=HEAD_DIM ** -0.5, part=part.data_ptr(), part_floats=part.numel(),
+                 attn=_vp(attn), attn_fq=attn_fq.data_ptr(), flag=flag.t.data_ptr(), advance=1 if advance else 0,
+                 scale_fmt=cache.scale_fmt, code_fmt=cache.code_fmt)
     st = load().vh_kivi_attention(ctypes.byref(d), _stream(qkv))
     check(st, "vh_kivi_attention")
     if advance:
-        cache.n_res += 1
+        cache.advance_host()
     return attn_fq
 
 
@@ -292,20 +352,23 @@ class DecoderLayer:
         }
         self.part = None
 
-    def stages(self, x: torch.Tensor, cache: KiviCache, pos: int):
-        """The step's launches as ``(name, fn)`` pairs, in order (the cache's
-        residual count is not advanced by them)."""
+    def stages(self, x: torch.Tensor, cache: KiviCache, advance: bool = True):
+        """The step's launches as ``(name, fn)`` pairs, in order.  The step's
+        position is the cache's (read on the device); with ``advance`` the
+        attention also moves the cache past the step's token (folding a
+        completed residual chunk into the main cache)."""
         B = x.shape[0]
+        if B != cache.batch:
+            raise ValueError(f"DecoderLayer: batch {B} does not match the cache's {cache.batch}")
         b = {k: v[:B] for k, v in self.buf.items()}
-        if self.part is None or self.part.numel() < part_floats(B, cache.nkv, cache.n_main):
-            self.part = torch.empty(part_floats(B, cache.nkv, cache.n_main), dtype=torch.float32, device=x.device)
+        if self.part is None or self.part.numel() < cache.part_floats():
+            self.part = torch.empty(cache.part_floats(), dtype=torch.float32, device=x.device)
         f = self.flag
-        return [
+        out = [
             ("rmsnorm_1", lambda: rmsnorm_mx8(x, self.ln1, self.eps, f, fq=b["fq1"])),
             ("qkv_proj", lambda: gemv_mx8(b["fq1"], self.qkv, f, _lib.GEMV_STORE, y=b["qkv"])),
-            ("attention", lambda: kivi_attention(b["qkv"], cache, self.rope[0, pos], self.rope[1, pos], self.nq, f,
-                                                 part=self.part, attn=b["attn"], attn_fq=b["attn_fq"],
-                                                 advance=False)),
+            ("attention", lambda: kivi_attention(b["qkv"], cache, self.rope, self.nq, f, part=self.part,
+                                                 attn=b["attn"], attn_fq=b["attn_fq"], advance=advance)),
             ("o_proj", lambda: gemv_mx8(b["attn_fq"], self.o, f, _lib.GEMV_RESIDUAL, residual=x, y=b["x1"])),
             ("rmsnorm_2", lambda: rmsnorm_mx8(b["x1"], self.ln2, self.eps, f, fq=b["fq3"])),
             ("gate_up_proj", lambda: gemv_mx8(b["fq3"], self.gate_up, f, _lib.GEMV_SWIGLU, y=b["act"],
@@ -313,16 +376,34 @@ class DecoderLayer:
             ("down_proj", lambda: gemv_mx8(b["act_fq"], self.down, f, _lib.GEMV_RESIDUAL, residual=b["x1"],
                                            y=b["out"])),
         ]
+        return out
 
-    def step(self, x: torch.Tensor, cache: KiviCache, pos: int, advance: bool = True) -> torch.Tensor:
-        """One decode step of ``x [B, hidden]`` (bf16) at position ``pos``;
-        returns the layer output (a view of an internal buffer).  With
-        ``advance`` the cache's residual count moves past this step's token."""
-        for _, fn in self.stages(x, cache, pos):
+    def step(self, x: torch.Tensor, cache: KiviCache, advance: bool = True) -> torch.Tensor:
+        """One decode step of ``x [B, hidden]`` (bf16) at the cache's position;
+        returns the layer output (a view of an internal buffer).  Nothing
+        synchronises: read ``self.flag.check()`` to learn of data the kernels
+        could not represent."""
+        for _, fn in self.stages(x, cache, advance):
             fn()
-        if advance:
-            cache.n_res += 1
         return self.buf["out"][: x.shape[0]]
+
+    def capture(self, x: torch.Tensor, cache: KiviCache, warmup: int = 0) -> "torch.cuda.CUDAGraph":
+        """A HIP graph of one whole step (the cache advance included) reading
+        ``x`` and the cache state from device memory, so each ``replay()`` is
+        the next decode step; call ``cache.advance_host()`` after each replay
+        to keep the host mirror.  ``warmup`` eager steps run first (they
+        advance the cache)."""
+        for _ in range(warmup):
+            self.step(x, cache)
+        self.stages(x, cache)  # allocates the attention workspace outside the capture
+        g = torch.cuda.CUDAGraph()
+        n_main, n_res = cache.n_main, cache.n_res
+        with torch.cuda.graph(g):
+            for _, fn in self.stages(x, cache):
+                fn()
+        # capture ran the host bookkeeping once without device work
+        cache.n_main, cache.n_res = n_main, n_res
+        return g
 
     def stage_bytes(self, batch: int, cache: KiviCache) -> Dict[str, int]:
         """Algorithmic HBM bytes of each stage: weights (one code byte per
