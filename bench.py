@@ -186,6 +186,12 @@ def gpu_bench(args):
     return res, cpu_data
 
 
+# The configs' quantization specs, in the reference's spec-string grammar
+# (quantization/qspec.py), parsed by the same rules the compiler uses.
+CFG1_SPEC = "int8,qs=microscaling,bs=16,pot=1"
+CFG3_SPEC = "lut4_to_int6,qs=microscaling,bs=64,scale=fp8_e5m3"
+
+
 def bench_config1(args):
     """Config 1: MXINT8 linear, X [256,4096] (0.1% outliers x20, seed 0), W
     [4096,4096] N(0,0.02); int8 bs=16 pot scales.  Step = quantize_mx(X) to
@@ -198,17 +204,19 @@ def bench_config1(args):
     x = torch.randn(256, 4096, generator=g)
     x = torch.where(torch.rand(256, 4096, generator=g) < 0.001, x * 20, x).bfloat16()
     w = (torch.randn(4096, 4096, generator=g) * 0.02).bfloat16()
-    tab = formats.quantization_map("int8", dev)
+    sp = formats.parse_spec(CFG1_SPEC)
+    bs, qmax, pot = sp["block_size"], sp["quant_max"], sp["power_2_scale"]
+    tab = formats.quantization_map(sp["dtype"], dev)
     xd, wd = x.to(dev), w.to(dev)
-    pw = packed.quantize_mx_packed(wd, tab, [-1], 16, 127.0, True)
+    pw = packed.quantize_mx_packed(wd, tab, [-1], bs, qmax, pot)
     st = {}
 
     def quant():
-        st["px"] = packed.quantize_mx_packed(xd, tab, [-1], 16, 127.0, True)
+        st["px"] = packed.quantize_mx_packed(xd, tab, [-1], bs, qmax, pot)
 
     def mm():
         px = st["px"]
-        st["y"] = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias)
+        st["y"] = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, bs, px.bias, pw.bias)
 
     def step():
         quant()
@@ -329,8 +337,9 @@ def bench_config3(args):
     from voyager_amd import formats, gemm
 
     dev = torch.device("cuda:0")
-    index, entries, mid = formats.codebook_tables("lut4_to_int6", dev)
-    stab = formats.quantization_map("fp8_e5m3", dev)
+    sp = formats.parse_spec(CFG3_SPEC)
+    index, entries, mid = formats.codebook_tables(sp["dtype"], dev)
+    stab = formats.quantization_map(sp["scale_dtype"], dev)
     res = {}
     tot_b, tot_t = 0.0, 0.0
     for i, (K, N) in enumerate(SHAPES):
@@ -496,7 +505,6 @@ def bench_config5(args):
     if cpu_data is not None:
         x, w, k_past, v_past, mx = cpu_data
         cos, sin = D.rope_cos_sin(torch.tensor([pos]), 128, cfg.rope_theta)
-        torch.set_num_threads(os.cpu_count() or 1)
         D.decode_layer(x, w, k_past, v_past, cos, sin, cfg, mx=mx)
         t0 = time.perf_counter()
         n = 0
@@ -519,11 +527,43 @@ def bench_config5(args):
                                    "linears, KIVI 2-bit K/V (group 32, fp16 scale/zero), 128-token residual"}}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (``/proc/cpuinfo``), as lscpu reports it."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_cpu(step, threads, budget_s, min_runs=5):
+    """Median wall time of ``step`` on ``threads`` torch CPU threads after one
+    warm-up run: at least ``min_runs`` runs, more while within ``budget_s``."""
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        step()
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < min_runs or time.perf_counter() - t_start < budget_s:
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        return times[len(times) // 2], len(times), time.perf_counter() - t_start
+    finally:
+        torch.set_num_threads(prev)
+
+
 def cpu_baseline(cpu_data, budget_s=10.0):
-    """The reference's CPU op sequence (the oracle) on the host, all threads:
-    whole config-2 steps (per shape: quantize X with its calibrated scale,
-    linear, dequantize by the scale product; weights quantized once, as
-    baked), repeated until ``budget_s`` has elapsed; median step time."""
+    """The reference's CPU op sequence (the oracle) on the host: whole
+    config-2 steps (per shape: quantize X with its calibrated scale, linear,
+    dequantize by the scale product; weights quantized once, as baked), on
+    every host core and on one thread (the reference's own ``--debug``
+    setting); median step time of each."""
     from oracle import ops as O
     from oracle import tables as T
 
@@ -534,27 +574,23 @@ def cpu_baseline(cpu_data, budget_s=10.0):
         sx = O.per_tensor_scale(x, 448.0)
         sw = O.per_tensor_scale(w, 448.0)
         prep.append((x, sx, O.quantize(w, sw, qmap=tab), sx * sw))
-    threads = torch.get_num_threads()
 
     def step():
         for x, sx, wq, s in prep:
             xq = O.quantize(x, sx, qmap=tab)
             O.dequantize(O.linear(xq, wq), s, input_qmap=ident)
 
-    step()
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or time.perf_counter() - t_start < budget_s:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
     flops = sum(2.0 * x.shape[0] * wq.shape[0] * wq.shape[1] for x, _, wq, _ in prep)
-    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} whole config-2 steps (4 shapes, M=2048) of the oracle's quantize + linear + "
-                      f"dequantize, median {med * 1e3:.1f} ms, torch CPU threads={threads}, "
-                      f"{time.perf_counter() - t_start:.1f} s"}
+    cores = torch.get_num_threads()  # the job's share (OMP_NUM_THREADS), not every core of the host
+    med, n, el = _time_cpu(step, cores, budget_s)
+    med1, n1, el1 = _time_cpu(step, 1, budget_s)
+    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+            "sample": f"{n} whole config-2 steps (4 shapes, M=2048) of the oracle's quantize + linear + "
+                      f"dequantize, median {med * 1e3:.1f} ms, torch CPU threads={cores}, {el:.1f} s",
+            "one_thread": {"value": round(flops / med1 / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
+                           "sample": f"{n1} whole config-2 steps on 1 thread (the reference's --debug "
+                                     f"setting), median {med1 * 1e3:.1f} ms, {el1:.1f} s"}}
 
 
 def copy_calibration(nbytes: int):

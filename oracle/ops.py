@@ -33,14 +33,25 @@ def repeat_per_block(scale, input, block_size):
     return torch.empty_like(input, dtype=scale.dtype).copy_(scale)
 
 
-def vmap(input, table):
+def vmap(input, table, chunk_size=1024 * 1024):
     """``table[bits(bf16(input))]`` in ``input``'s dtype and layout;
-    ``ops/quantized.py:147-184`` (one gather instead of the chunk loop)."""
+    ``ops/quantized.py:147-184``.  Gathers in chunks of ``chunk_size``
+    elements in memory order, as the reference's eager path does, so the
+    CPU baseline times the same loop."""
     in_dtype = input.dtype
     x = input.to(torch.bfloat16) if input.dtype != torch.bfloat16 else input
-    idx = x.view(torch.int16).to(torch.int32) & 0xFFFF
-    out = torch.empty_like(x)
-    out.copy_(table[idx].to(x.dtype))
+    idx = x.view(torch.int16)
+    order = sorted(range(x.ndim), key=x.stride, reverse=True)
+    if x.permute(order).is_contiguous():
+        out = torch.empty_like(x)
+    else:
+        order = list(range(x.ndim))
+        out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    idx_flat = idx.permute(order).reshape(-1)
+    out_flat = out.permute(order).view(-1)
+    for start in range(0, idx_flat.numel(), chunk_size):
+        end = min(start + chunk_size, idx_flat.numel())
+        out_flat[start:end] = table[idx_flat[start:end].to(torch.int32) & 0xFFFF].to(x.dtype)
     return out.to(in_dtype)
 
 

@@ -251,9 +251,9 @@ class KiviCache:
         self.state.copy_(torch.tensor([self.n_main, self.n_res, 0, 0], dtype=torch.int32))
 
     def advance_host(self) -> None:
-        """Move the host mirror past one step, as ``vh_kivi_advance`` moves the
-        device state: a step that fills the last residual slot folds the
-        chunk into the main cache."""
+        """Move the host mirror past one step, as an advancing
+        ``vh_kivi_attention`` moves the device state: a step that fills the
+        last residual slot folds the chunk into the main cache."""
         if self.n_res + 1 == RES_CAP:
             if self.n_main + RES_CAP <= self.capacity:
                 self.n_main += RES_CAP
