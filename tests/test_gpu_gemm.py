@@ -93,21 +93,28 @@ def _deq_mxint8(p):
     return c * torch.pow(2.0, e.double())
 
 
-@pytest.mark.parametrize("M,N,K,block,hint,split", [
-    (256, 4096, 4096, 16, 0, 0),     # config 1: automatic tile and split
-    (256, 4096, 4096, 16, 50, 1),    # same tile unsplit
-    (130, 200, 1024, 16, 50, 3),     # ragged M / N; 16 stages in splits of 6, 6, 4
-    (130, 200, 1024, 32, 51, 2),
-    (64, 128, 64, 16, 52, 0),        # a single K stage
-    (300, 520, 640, 16, 53, 5),
-    (70, 260, 1152, 32, 54, 4),
-    (256, 4096, 4096, 16, 55, 4),    # producer / consumer waves
-    (130, 200, 1024, 16, 55, 3),
-    (300, 520, 640, 32, 56, 1),
-    (64, 128, 64, 16, 55, 0),
-    (2048, 4096, 256, 16, 0, 0),     # a grid that fills the GPU: automatic 56, unsplit
+@pytest.mark.parametrize("M,N,K,block,hint,split,tile", [
+    (256, 4096, 4096, 16, 0, 0, 51),     # config 1: automatic tile and split
+    (256, 4096, 4096, 16, 50, 1, 50),    # bf16 operands, unsplit
+    (130, 200, 1024, 16, 50, 3, 50),     # ragged M / N; 16 stages in splits of 6, 6, 4
+    (130, 200, 1024, 32, 51, 2, 51),
+    (64, 128, 64, 16, 52, 0, 52),        # a single K stage
+    (300, 520, 640, 16, 53, 5, 53),
+    (70, 260, 1152, 32, 54, 4, 54),
+    (256, 4096, 4096, 16, 55, 4, 55),    # producer / consumer waves
+    (130, 200, 1024, 16, 55, 3, 55),
+    (300, 520, 640, 32, 56, 1, 56),
+    (64, 128, 64, 16, 55, 0, 55),
+    (2048, 4096, 256, 16, 0, 0, 56),     # a grid that fills the GPU: automatic 56, unsplit
+        (256, 4096, 4096, 16, 60, 0, 60),    # fp16 operands, 256 x 64: automatic split (4)
+    (2048, 1024, 4096, 16, 60, 0, 60),   # 128 tiles: split 2
+    (256, 4096, 4096, 16, 60, 1, 60),
+    (300, 200, 1024, 16, 60, 3, 60),     # ragged M / N; 4 K granules in splits of 2, 2
+    (130, 520, 768, 16, 60, 2, 60),      # 3 K granules (256 each) in splits of 2, 1
+    (512, 256, 256, 16, 60, 0, 60),
+    (300, 520, 640, 32, 60, 1, 51),      # 32-element blocks: the fp16 kernel does not apply
 ])
-def test_linear_mxint8_split_k(M, N, K, block, hint, split):
+def test_linear_mxint8_split_k(M, N, K, block, hint, split, tile):
     """The MX-int8 kernels (tiles 50..56, K split across workgroups with fp32
     partials added in split order) against the exact float64 product of the
     decoded operands, and against the register-staged kernel (tile 4).  The
@@ -121,8 +128,13 @@ def test_linear_mxint8_split_k(M, N, K, block, hint, split):
     px = packed.quantize_mx_packed(x, tab, [-1], block, 127.0, True)
     pw = packed.quantize_mx_packed(w, tab, [-1], block, 127.0, True)
     ref = _deq_mxint8(px) @ _deq_mxint8(pw).T
-    got = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, block, px.bias, pw.bias, tile_hint=hint,
-                             split_k=split)
+    gemm.plan_log = log = []
+    try:
+        got = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, block, px.bias, pw.bias, tile_hint=hint,
+                                 split_k=split)
+    finally:
+        gemm.plan_log = None
+    assert [(f, t) for f, t, *_ in log] == [(gemm.FAMILY_MXI8, tile)]
     assert max_rel_err(got, ref) < TOL
     old = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, block, px.bias, pw.bias, tile_hint=4)
     assert max_rel_err(got, old) < 1e-2
@@ -134,6 +146,32 @@ def test_linear_mxint8_split_k(M, N, K, block, hint, split):
     ref32 = ref * 0.75 + bias.cpu().double()
     assert got32.dtype == torch.float32
     assert max_rel_err(got32, ref32) < 1e-5
+
+
+def test_linear_mxint8_fp16_operands_exponent_range():
+    """k_gemm_mx8h rebases each row to its largest block exponent: rows whose
+    blocks span 2**-40 .. 2**20 (blocks more than 24 binades below the row's
+    largest are flushed) and rows of equal exponents, against the exact
+    float64 product, with a float32 result."""
+    from voyager_amd import gemm, packed
+
+    M, N, K = 256, 128, 1024
+    tab = T.quantization_map("int8").cuda()
+    g = torch.Generator().manual_seed(33)
+    ex = torch.randint(-40, 21, (M, K // 16), generator=g).repeat_interleave(16, dim=1)
+    x = (torch.randn(M, K, generator=g) * torch.pow(2.0, ex.float())).bfloat16().cuda()
+    ew = torch.randint(-12, 4, (N, K // 16), generator=g).repeat_interleave(16, dim=1)
+    w = (torch.randn(N, K, generator=g) * torch.pow(2.0, ew.float())).bfloat16().cuda()
+    px = packed.quantize_mx_packed(x, tab, [-1], 16, 127.0, True)
+    pw = packed.quantize_mx_packed(w, tab, [-1], 16, 127.0, True)
+    ref = _deq_mxint8(px) @ _deq_mxint8(pw).T
+    for split in (1, 4):
+        got = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias,
+                                 out_dtype=torch.float32, tile_hint=60, split_k=split)
+        assert max_rel_err(got, ref) < 1e-5
+        # row by row: each row's own largest term sets its scale
+        rel = ((got.cpu().double() - ref).abs().amax(dim=1) / ref.abs().amax(dim=1)).max().item()
+        assert rel < 1e-5
 
 
 def test_gemm_workspace_query():

@@ -1236,6 +1236,272 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   else store_tile_lds_t<TM, TN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
 }
 
+// ------------------------------------------------------------ MX-int8, fp16
+// MX-int8 x MX-int8 with 16-element blocks on v_mfma_f32_32x32x16_f16.  A
+// code c of a block with exponent e enters as the fp16 value c * 2**(e - E),
+// E the largest block exponent of the code's row within the workgroup's K
+// range: the byte c ^ 0x80 under the fp16 high byte 0x64 is 1152 + c (one
+// v_perm per two codes), and one packed fma by 2**(e - E) and
+// -1152 * 2**(e - E) leaves c * 2**(e - E) exactly (e - E >= -24; a block
+// further below its row's largest is flushed, a change under 2**-17 of that
+// block's magnitude).  Products are exact and accumulate in fp32, as with
+// bf16 operands; the epilogue multiplies by 2**(E_row + E_col), exact in
+// fp32 -- 1.25 VALU operations per decoded code against 2.5 for bf16.
+//
+// Block tile 256 x 64, eight waves (two per SIMD, so one's decode overlaps
+// the other's MFMAs): wave w owns A rows 32 w .. 32 w + 31 and B rows
+// 8 w .. 8 w + 7, and multiplies its A rows by all 64 B columns.  A stage
+// is 64 K elements.  Every global load moves data straight into LDS
+// (buffer_load ... lds, four lanes per 64-byte row segment), and a wave
+// only ever reads raw data it loaded itself, so the raw stages need no
+// barrier and the waits are explicit vmcnt counts (the compiler issues no
+// global loads in the loop):
+// * the split's scale bytes, once, before the loop ([320 rows][nb]);
+// * A codes, NS - 1 stages ahead: 1 KB blocks of 16 rows x 64 bytes, chunk
+//   c of row r at slot 4 (r % 16) + (c ^ (r / 4 % 4)) (the MFMA-layout
+//   read -- 16 rows, one chunk -- hits 16 distinct bank groups), decoded in
+//   registers straight into MFMA operands, once per block tile;
+// * B codes, likewise (half of each wave's 1 KB DMA is unused), decoded by
+//   the loading lanes into a shared fp16 stage (rows padded to MH_PITCH
+//   bytes) that every wave reads after the stage's one barrier.
+// MFMA step t (of 4) takes, in lane half h, K elements 32 h + 8 t .. + 7 of
+// the stage -- a permutation of K both operands share -- so a lane's A codes
+// of its row are two whole blocks.  gridDim.y splits K as k_gemm_mxi8 does
+// (the splits of a tile share an XCD); partials carry the 2**(E_row +
+// E_col) factor, so k_split_reduce adds them as they are.
+constexpr int MH_KE = 64;                        // K elements (code bytes) per stage
+constexpr int MH_PITCH = 2 * MH_KE + 16;         // LDS pitch of a decoded B row (bytes)
+constexpr int MH_BN = 64;
+constexpr int MH_NS = 4;                         // raw stages in LDS
+constexpr int MH_KQ = 4 * MH_KE;                 // K granule: splits and K are multiples of it
+constexpr int MH_KC_MAX = 2048;                  // K elements per split at most (128 scale bytes per row)
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
+// (2**d, 2**d) and (-1152 * 2**d, ...) as fp16 pairs; both 0 for d < -24.
+struct MhMul {
+  f16x2 m, o;
+};
+
+__device__ __forceinline__ MhMul mh_mul(int d) {
+  const _Float16 s = __builtin_amdgcn_ldexph((_Float16)1.0f, d);
+  const uint32_t bits = __builtin_bit_cast(unsigned short, s);
+  MhMul r;
+  r.m = __builtin_bit_cast(f16x2, bits * 0x10001u);
+  const f16x2 k = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  r.o = r.m * k;
+  return r;
+}
+
+// Eight codes (two dwords) of one block -> the fp16 operand c * 2**d.
+__device__ __forceinline__ f16x8 mh_decode8(uint32_t w0, uint32_t w1, const MhMul& mu) {
+  const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
+  const f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u));
+  const f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u));
+  const f16x2 p2 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u));
+  const f16x2 p3 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u));
+  const f16x2 y0 = __builtin_elementwise_fma(p0, mu.m, mu.o), y1 = __builtin_elementwise_fma(p1, mu.m, mu.o);
+  const f16x2 y2 = __builtin_elementwise_fma(p2, mu.m, mu.o), y3 = __builtin_elementwise_fma(p3, mu.m, mu.o);
+  return f16x8{y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
+}
+
+// The largest byte of 16.
+__device__ __forceinline__ uint32_t max_byte16(const uint4& v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t acc = 0u;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc = pk_max_u16(acc, w[q] & 0x00ff00ffu);
+    acc = pk_max_u16(acc, (w[q] >> 8) & 0x00ff00ffu);
+  }
+  const uint32_t a = acc & 0xffffu, b = acc >> 16;
+  return a > b ? a : b;
+}
+
+// LDS layout (bytes).
+struct MhLds {
+  static constexpr int STAGE = 256 * MH_KE + 8 * 1024;          // A blocks, then one B DMA block per wave
+  static constexpr int FP16 = MH_NS * STAGE;                   // 2 x 64 decoded B rows
+  static constexpr int SC = FP16 + 2 * MH_BN * MH_PITCH;       // the split's scale bytes, [256 + 64][nb]
+  static constexpr int BYTES = SC + (256 + MH_BN) * (MH_KC_MAX / 16);
+};
+
+// explicit vmcnt wait (the DMA loads are invisible to the compiler)
+template <int N>
+__device__ __forceinline__ void mh_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__global__ void __launch_bounds__(512, 1) k_gemm_mx8h(GemmArgs g, int64_t kc, float* __restrict__ part) {
+  constexpr int BM = 256, BN = MH_BN, TM = 1, TN = 2, NS = MH_NS;
+  constexpr int L = 3;  // DMA instructions per wave and stage: two A blocks, one B block
+  using Y = MhLds;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ uint32_t s_ea[BM], s_eb[BN];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  int64_t m0, n0;
+  tile_origin(g.M, g.N, BM, BN, g.group_m, m0, n0);
+  const int64_t k_lo = (int64_t)blockIdx.y * kc;
+  const int64_t k_hi = (k_lo + kc) < g.K ? (k_lo + kc) : g.K;
+  const int nk = (int)((k_hi - k_lo) / MH_KE);
+  const int nb = nk * (MH_KE / 16);  // scale bytes per row in the split
+  const int kb0 = (int)(k_lo / 16);
+
+  const int64_t rows_a = (g.M - m0) < BM ? (g.M - m0) : BM;
+  const int64_t rows_b = (g.N - n0) < BN ? (g.N - n0) : BN;
+  const i32x4 ra = raw_desc(g.A + m0 * g.lda, rows_a * g.lda);
+  const i32x4 rb = raw_desc(g.B + n0 * g.ldb, rows_b * g.ldb);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+
+  // DMA lanes: row lane / 4 of a 16-row block, chunk (lane % 4) ^ (lane / 16)
+  const int drow = lane >> 2, dch = (lane & 3) ^ ((lane >> 4) & 3);
+  const int voa0 = (32 * wave + drow) * (int)g.lda + 16 * dch + (int)k_lo;
+  const int voa1 = voa0 + 16 * (int)g.lda;
+  const bool b_live = lane < 32;  // B rows 8 wave + lane / 4
+  const int vob = (8 * wave + drow) * (int)g.ldb + 16 * dch + (int)k_lo;
+  auto dma = [&](int s) {
+    const bool live = s < nk;  // past the split: zeros, never used
+    const uint32_t base = lds0 + (uint32_t)((s % NS) * Y::STAGE);
+    const int ko = s * MH_KE;
+    dma16(ra, base + (2 * wave) * 1024, live ? voa0 + ko : (int)0x80000000);
+    dma16(ra, base + (2 * wave + 1) * 1024, live ? voa1 + ko : (int)0x80000000);
+    dma16(rb, base + 256 * MH_KE + wave * 1024, live && b_live ? vob + ko : (int)0x80000000);
+  };
+
+  // the split's scale bytes: DMA instruction i (wave i % 8) covers 64 / cpr
+  // rows of cpr 16-byte chunks, A rows then B rows; then the first stages
+  // (one round trip for both)
+  const int cpr = nb / 16;
+  const int ninst = (BM + BN) * nb / 1024;
+  {
+    const i32x4 rsa = raw_desc(g.a_scale + m0 * g.lds_a, rows_a * g.lds_a);
+    const i32x4 rsb = raw_desc(g.b_scale + n0 * g.lds_b, rows_b * g.lds_b);
+    const uint32_t sc0 = lds0 + Y::SC;
+    const int rpi = 64 / cpr, lrow = lane / cpr, lch = lane % cpr;
+    for (int i = wave; i < ninst; i += 8) {
+      const int row = i * rpi + lrow;
+      if (row < BM) dma16(rsa, sc0 + i * 1024, row * (int)g.lds_a + kb0 + 16 * lch);
+      else dma16(rsb, sc0 + i * 1024, (row - BM) * (int)g.lds_b + kb0 + 16 * lch);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) dma(s);
+  mh_wait<(NS - 1) * L>();  // this wave's scale DMA (older than the stages) has landed
+  __syncthreads();
+  // the rows' largest block exponents over this split's K range
+  if (tid < BM + BN) {
+    uint32_t m = 0u;
+    for (int c = 0; c < nb / 16; ++c) {
+      const uint32_t v = max_byte16(*(const uint4*)(smem + Y::SC + tid * nb + 16 * c));
+      m = v > m ? v : m;
+    }
+    if (tid < BM) s_ea[tid] = m;
+    else s_eb[tid - BM] = m;
+  }
+  __syncthreads();
+  const int ea = (int)s_ea[32 * wave + lr];
+  const int brow = 8 * wave + drow;
+  const int ebr = (int)s_eb[brow & (BN - 1)];
+  const uint8_t* sa_row = smem + Y::SC + (32 * wave + lr) * nb;
+  const uint8_t* sb_row = smem + Y::SC + (BM + (brow & (BN - 1))) * nb;
+
+  // this wave's B rows of stage s -> fp16 buffer s % 2 (lanes 0..31)
+  auto decode_b = [&](int s) {
+    if (b_live) {
+      const uint4 c = *(const uint4*)(smem + (s % NS) * Y::STAGE + 256 * MH_KE + wave * 1024 + 16 * lane);
+      const MhMul mu = mh_mul((int)sb_row[4 * s + dch] - ebr);
+      uint8_t* d = smem + Y::FP16 + (s & 1) * BN * MH_PITCH + brow * MH_PITCH + 32 * dch;
+      *(f16x8*)d = mh_decode8(c.x, c.y, mu);
+      *(f16x8*)(d + 16) = mh_decode8(c.z, c.w, mu);
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int n = 0; n < TN; ++n)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[0][n][r] = 0.0f;
+
+  const int rsw = (lr >> 2) & 3;  // the swizzle of the A row this lane reads
+  // every LDS read of the stage goes out first, then the decode / MFMA chain
+  auto compute = [&](int s) {
+    const uint8_t* blk = smem + (s % NS) * Y::STAGE + (2 * wave + (lr >> 4)) * 1024 + 64 * (lr & 15);
+    const uint8_t* bb = smem + Y::FP16 + (s & 1) * BN * MH_PITCH + lr * MH_PITCH + 64 * lh;
+    const uint4 c0 = *(const uint4*)(blk + 16 * ((2 * lh) ^ rsw));
+    const uint4 c1 = *(const uint4*)(blk + 16 * ((2 * lh + 1) ^ rsw));
+    const uint32_t sa = *(const uint32_t*)(sa_row + 4 * s);
+    f16x8 fb[4][TN];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int n = 0; n < TN; ++n) fb[t][n] = *(const f16x8*)(bb + n * 32 * MH_PITCH + 16 * t);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {  // block 2 lh + q: steps 2 q, 2 q + 1
+      const MhMul mu = mh_mul((int)((sa >> (8 * (2 * lh + q))) & 0xffu) - ea);
+      const uint4& c = q ? c1 : c0;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const f16x8 fa = t ? mh_decode8(c.z, c.w, mu) : mh_decode8(c.x, c.y, mu);
+#pragma unroll
+        for (int n = 0; n < TN; ++n)
+          acc[0][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa, fb[2 * q + t][n], acc[0][n], 0, 0, 0);
+      }
+    }
+  };
+
+  // iteration s: stage s + NS - 1 goes out; this wave's DMA of stages s and
+  // s + 1 has landed; the wave decodes its B rows of stage s + 1 and
+  // multiplies stage s; one barrier publishes the
+  // fp16 B stage and retires the buffers stage s used (the wave's LDS reads
+  // complete before it).
+  mh_wait<(NS - 2) * L>();
+  decode_b(0);
+  lds_barrier();
+  for (int s = 0; s < nk; ++s) {
+    dma(s + NS - 1);
+    mh_wait<(NS - 2) * L>();
+    if (s + 1 < nk) decode_b(s + 1);
+    compute(s);
+    lds_barrier();
+  }
+  mh_wait<0>();
+  __syncthreads();
+
+  // undo the row / column rebasing: 2**(E_row + E_col), exact in fp32
+#pragma unroll
+  for (int n = 0; n < TN; ++n) {
+    const int eb = (int)s_eb[32 * n + lr] - g.b_bias;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 32 * wave + (r >> 2) * 8 + lh * 4 + (r & 3);
+      acc[0][n][r] = ldexpf(acc[0][n][r], (int)s_ea[row] - g.a_bias + eb);
+    }
+  }
+  if (gridDim.y == 1) {
+    store_tile<TM, TN, 8, 1>(g, acc, smem, m0, n0, wave, wave, 0, lane);
+  } else {
+    GemmArgs p = g;
+    p.C = part + (int64_t)blockIdx.y * g.M * g.N;
+    p.ldc = g.N;
+    p.epi.mode = EPI_PLAIN;
+    p.epi.out_dtype = VH_F32;
+    p.epi.scale = nullptr;
+    p.epi.bias = nullptr;
+    store_tile_direct<TM, TN, 8, 1>(p, acc, m0, n0, wave, 0, lane);
+  }
+}
+
 // Tile-rows per column walk for a BM x BN grid: the group whose per-XCD
 // block of tiles (the XCD's share of the grid) streams the fewest operand
 // rows, GM BM of A plus (tiles per XCD / GM) BN of B.
@@ -1327,9 +1593,47 @@ int launch_mxi8(GemmArgs g, int splits, float* part, hipStream_t stream) {
   return vh::check_launch("vh_gemm");
 }
 
-// The MX-int8 kernel's tile (hint 50..54) and split count for a descriptor,
-// or cfg 0 when the pair takes k_gemm.  Splits fill the 256 CUs when the
-// tile grid alone does not; each split keeps at least two stages.
+int launch_mx8h(GemmArgs g, int splits, float* part, hipStream_t stream) {
+  g.group_m = group_rows(g.M, g.N, 256, MH_BN);
+  const int64_t tiles = ((g.M + 255) / 256) * ((g.N + MH_BN - 1) / MH_BN);
+  const int64_t quads = g.K / MH_KQ;
+  const int64_t kc = (quads + splits - 1) / splits * MH_KQ;
+  const int64_t sp = (g.K + kc - 1) / kc;
+  constexpr size_t stages = (size_t)MhLds::BYTES;
+  constexpr size_t epi = (size_t)8 * 32 * (MH_BN + 8) * 2;
+  constexpr size_t smem = stages > epi ? stages : epi;
+  static_assert(smem + 4 * (256 + MH_BN) <= 160 * 1024, "LDS");
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)k_gemm_mx8h, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
+        hipSuccess) {
+      vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
+      return VH_ELAUNCH;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(k_gemm_mx8h, dim3((unsigned)tiles, (unsigned)sp), dim3(512), smem, stream, g, kc,
+                     sp > 1 ? part : nullptr);
+  if (sp > 1) {
+    const int64_t q4 = g.M * g.N / 4;
+    hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((q4 + 255) / 256)), dim3(256), 0, stream, part, (int)sp, g.M,
+                       g.N, g.epi, g.C, g.ldc);
+  }
+  return vh::check_launch("vh_gemm");
+}
+
+// Whether k_gemm_mx8h takes a descriptor: 16-element blocks, K a whole
+// number of stage pairs, 16-byte aligned operand and scale rows.
+bool mx8h_fits(const vh_gemm_desc* d) {
+  auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  return d->a_block == 16 && d->b_block == 16 && d->K % MH_KQ == 0 && d->a_scale_ld % 16 == 0 &&
+         d->b_scale_ld % 16 == 0 && al(d->A) && al(d->B) && al(d->a_scale) && al(d->b_scale);
+}
+
+// The MX-int8 kernel's tile (hint 50..56 bf16 operands, 60 fp16 operands)
+// and split count for a descriptor, or cfg 0 when the pair takes k_gemm.
+// Splits fill the 256 CUs when the tile grid alone does not; each split
+// keeps at least two stages.
 void mxi8_plan(const vh_gemm_desc* d, int& cfg, int& splits) {
   cfg = 0;
   splits = 1;
@@ -1339,12 +1643,16 @@ void mxi8_plan(const vh_gemm_desc* d, int& cfg, int& splits) {
   if (!fits || d->M <= 0 || d->N <= 0) return;
   auto tiles = [&](int64_t bm, int64_t bn) { return ((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn); };
   cfg = d->tile_hint;
-  // Measured on MI355X (N = K = 4096): at M = 256, 128 x 128 tiles with 8
-  // waves split 4 ways take 25.8 us (4 waves: 30.3 us; 128 x 64 split 4:
-  // 28.6 us; producer / consumer waves 27.5 us; split 8 pays twice the
-  // partial traffic); at M = 2048, 256 x 128 with producer / consumer waves
-  // takes 95.1 us (722 TFLOP/s; uniform waves 101.7 us, the register-staged
-  // k_gemm 154 us).
+  const bool h = mx8h_fits(d);
+  // bf16 operands by default -- measured on MI355X (N = K = 4096): at
+  // M = 256, 128 x 128 tiles with 8 waves split 4 ways take 25.8 us (4
+  // waves: 30.3 us; 128 x 64 split 4: 28.6 us; producer / consumer waves
+  // 27.5 us; split 8 pays twice the partial traffic); at M = 2048, 256 x 128
+  // with producer / consumer waves takes 95.1 us.  The fp16-operand kernel
+  // (tile 60, k_gemm_mx8h) is taken on request: at M = 256 it ties the
+  // bf16 kernels (24 us plus the split reduction), bound by LDS traffic
+  // (every wave reads the whole decoded B stage) and the per-stage barrier.
+  if (cfg == 60 && !h) cfg = 0;
   if (cfg == 0) cfg = tiles(256, 128) >= 256 ? 56 : 51;
   int64_t bm = 128, bn = 128;
   switch (cfg) {
@@ -1354,10 +1662,20 @@ void mxi8_plan(const vh_gemm_desc* d, int& cfg, int& splits) {
     case 54: bm = 64; break;
     case 55: break;
     case 56: bm = 256; break;
+    case 60: bm = 256; bn = 64; break;
     default: cfg = 0; return;
   }
   const int64_t t = tiles(bm, bn);
   int64_t sp = d->split_k > 0 ? d->split_k : (t >= 192 ? 1 : (256 + t - 1) / t);
+  if (cfg >= 60) {
+    const int64_t quads = d->K / MH_KQ;
+    if (sp > quads) sp = quads;
+    const int64_t min_sp = (d->K + MH_KC_MAX - 1) / MH_KC_MAX;  // the split's scale bytes fit LDS
+    if (sp < min_sp) sp = min_sp;
+    const int64_t kc = (quads + sp - 1) / sp * MH_KQ;
+    splits = (int)((d->K + kc - 1) / kc);
+    return;
+  }
   const int64_t stages = d->K / MX_KE;
   if (sp > stages / 2) sp = stages / 2 > 1 ? stages / 2 : 1;
   if (d->split_k > 0 && d->split_k <= stages) sp = d->split_k;
@@ -1575,6 +1893,7 @@ extern "C" int vh_gemm(const vh_gemm_desc* d, vh_stream_t stream) {
       case 54: return launch_mxi8<64, 128, 1, 4>(g, p.splits, part, st);
       case 55: return launch_mxi8<128, 128, 2, 2, 2, true>(g, p.splits, part, st);
       case 56: return launch_mxi8<256, 128, 2, 2, 2, true>(g, p.splits, part, st);
+      case 60: return launch_mx8h(g, p.splits, part, st);
       default: break;
     }
   }
