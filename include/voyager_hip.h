@@ -147,6 +147,17 @@ int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int
                    void* scale_out, int32_t scale_dtype, int32_t pot_bias,
                    void* codes_out, int32_t codes_dtype, const uint8_t* code_lut, vh_stream_t stream);
 
+/* vh_quantize_mx for the decode GEMV's activations (rows <= 16, blocks along
+ * the last axis, a scale map, no power-of-two scales): the same scales and
+ * codes, with the scales written as float32 block-major [L / block][16]
+ * (row r of block b at b * 16 + r; rows past `rows` are not written) and the
+ * codes as bytes through code_lut.  No counterpart in the reference (a
+ * layout of quantized_ops.quantize_mx's outputs, ops/quantized.py:1070-1115,
+ * for vh_gemv_nf4). */
+int vh_quantize_mx_rows16(const void* x, int32_t x_dtype, int64_t rows, int64_t L, int64_t block,
+                          float quant_max, const vh_format* scale_fmt, const vh_format* fmt, float* scale_out,
+                          uint8_t* codes_out, const uint8_t* code_lut, vh_stream_t stream);
+
 /* quantize_affine: per block min/max -> (scale, zero_point, codes).
  * Replaces quantized_ops.quantize_affine (ops/quantized.py:1218-1283). */
 int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
@@ -247,10 +258,12 @@ int vh_gemm_plan(const vh_gemm_desc* desc, int32_t* family, int32_t* tile, int32
 int vh_pack_nf4(const uint8_t* codes, int64_t N, int64_t K, uint8_t* out, vh_stream_t stream);
 
 /* y[M, N] = sum over blocks b of s_x[m, b] * s_w[n, b] * sum_k Lx[m, k] Lw[n, k]
- * with Lx the activations' int8 levels [M, K], s_x float32 [M, K/64],
- * Lw = levels16[index] of the packed weights (levels16: 16 int8 values in
- * host memory, passed by value), s_w = w_scale_fmt(byte) [N, K/64]; int8
- * MFMA per block, float32 accumulation, epilogue as vh_gemm (EPI_PLAIN). */
+ * with Lx the activations' int8 levels [M, K], s_x float32 block-major
+ * [K/64][16] (vh_quantize_mx_rows16), Lw = levels16[index] of the packed
+ * weights (levels16: 16 int8 values in host memory, passed by value), s_w =
+ * w_scale_fmt(byte) with the bytes tile-major [N/16][K/64][16] (column n of
+ * block b at ((n / 16) * K/64 + b) * 16 + n % 16); int8 MFMA per block,
+ * float32 accumulation, epilogue as vh_gemm (EPI_PLAIN). */
 int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t M, const uint8_t* w_packed,
                 const uint8_t* w_scale, const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N,
                 int64_t K, const vh_epilogue* epi, void* y, vh_stream_t stream);

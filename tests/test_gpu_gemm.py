@@ -307,6 +307,44 @@ def test_linear_nf4_gemv_cfg3(M, K, N):
     assert max_rel_err(got, exp) < TOL
 
 
+@pytest.mark.parametrize("M,K", [(1, 4096), (16, 14336), (5, 320)])
+def test_quantize_mx_rows16(M, K):
+    """vh_quantize_mx_rows16 (the decode GEMV's activation quantize) writes
+    the same scales and level bytes as vh_quantize_mx, its scales
+    block-major [K/64][16]; the scales match the oracle's bit for bit."""
+    import ctypes
+
+    from voyager_amd import _lib, formats, gemm
+
+    vt = T.quantization_map("lut4_to_int6")
+    index, entries, mid = T.codebook_index_table(vt)
+    stab = T.quantization_map("fp8_e5m3")
+    x = _rand((M, K), 41, 2.0)
+    sx, _ = O.quantize_mx(x, index, [-1], 64, 31.0, False, stab, mid)
+    d = "cuda"
+    xd = x.to(d)
+    ec, sc = formats.classify(index.to(d)), formats.classify(stab.to(d))
+    lut = torch.arange(256, dtype=torch.uint8, device=d)
+    nb = K // 64
+    xs_t = torch.full((nb, 16), float("nan"), device=d)
+    xl_t = torch.empty(M, K, dtype=torch.uint8, device=d)
+    xs = torch.empty(M, nb, device=d)
+    xl = torch.empty(M, K, dtype=torch.uint8, device=d)
+    lib = _lib.load()
+    _lib.check(lib.vh_quantize_mx_rows16(ctypes.c_void_p(xd.data_ptr()), _lib.VH_BF16, M, K, 64, 31.0,
+                                         ctypes.byref(sc.fmt), ctypes.byref(ec.fmt), ctypes.c_void_p(xs_t.data_ptr()),
+                                         ctypes.c_void_p(xl_t.data_ptr()), ctypes.c_void_p(lut.data_ptr()), None),
+               "vh_quantize_mx_rows16")
+    _lib.check(lib.vh_quantize_mx(ctypes.c_void_p(xd.data_ptr()), _lib.VH_BF16, M, K, 1, 64, 31.0, 0,
+                                  ctypes.byref(sc.fmt), None, 0, ctypes.byref(ec.fmt), ctypes.c_void_p(xs.data_ptr()),
+                                  _lib.VH_F32, 0, ctypes.c_void_p(xl.data_ptr()), _lib.VH_U8,
+                                  ctypes.c_void_p(lut.data_ptr()), None), "vh_quantize_mx")
+    assert torch.equal(xl_t, xl)
+    assert_same_bits(xs_t[:, :M].T.contiguous().cpu(), xs.cpu(), "block-major scales")
+    assert_same_bits(xs.cpu(), sx.float(), "scales vs oracle")
+    assert torch.isnan(xs_t[:, M:]).all()  # rows past M untouched
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 256, 512), (7, 96, 160)])
 def test_linear_mx_nvfp4(M, N, K):
     """NVFP4 as the reference's converted graph runs it: quantize_mx of both

@@ -40,6 +40,7 @@ struct Params {
   int pot_bias;       // packed pot scale byte = e + pot_bias
   int codes_dtype;    // cdt or VH_U8
   const uint8_t* code_lut;  // packed codes are remapped through this (or null)
+  int scale_t16;            // scales written block-major [nblk][16] (rows <= 16)
 };
 
 VH_DEV float load_x(const void* p, int dt, int64_t i) {
@@ -235,7 +236,7 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
   BlockScale bs = block_scale<SKIND>(hi, lo, P, slds);
   const int64_t blk = v / g;
   if ((v % g) == 0 && blk < nblk) {
-    const int64_t si = row * nblk + blk;
+    const int64_t si = P.scale_t16 ? blk * 16 + row : row * nblk + blk;
     if (P.scale_dtype == VH_U8) ((uint8_t*)scale_out)[si] = (uint8_t)bs.packed;
     else store_f(scale_out, P.scale_dtype, si, bs.scale);
     if (P.mode == AFFINE) store_f(zp_out, P.cdt, si, bs.zp);
@@ -410,13 +411,11 @@ bool packable(const vh_format& f) {
   }
 }
 
-}  // namespace
-
-extern "C" int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
-                              int64_t block, float quant_max, int32_t pot, const vh_format* scale_fmt,
-                              const void* global_scale, int32_t gs_dtype, const vh_format* fmt, void* scale_out,
-                              int32_t scale_dtype, int32_t pot_bias, void* codes_out, int32_t codes_dtype,
-                              const uint8_t* code_lut, vh_stream_t stream) {
+int quantize_mx_impl(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner, int64_t block,
+                     float quant_max, int32_t pot, const vh_format* scale_fmt, const void* global_scale,
+                     int32_t gs_dtype, const vh_format* fmt, void* scale_out, int32_t scale_dtype, int32_t pot_bias,
+                     void* codes_out, int32_t codes_dtype, const uint8_t* code_lut, int scale_t16,
+                     vh_stream_t stream) {
   int rc;
   if ((rc = check_common(x, x_dtype, outer, L, inner, block, "vh_quantize_mx"))) return rc;
   VH_REQUIRE(scale_out, "vh_quantize_mx: null scale output");
@@ -457,9 +456,31 @@ extern "C" int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int
   P.pot_bias = pot_bias;
   P.codes_dtype = codes_dtype;
   P.code_lut = code_lut;
+  P.scale_t16 = scale_t16;
   if (outer * L * inner == 0) return VH_OK;
   return launch(x, outer, L, inner, block, P, scale_out, nullptr, codes_out, vh::as_stream(stream),
                 "vh_quantize_mx");
+}
+
+}  // namespace
+
+extern "C" int vh_quantize_mx(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                              int64_t block, float quant_max, int32_t pot, const vh_format* scale_fmt,
+                              const void* global_scale, int32_t gs_dtype, const vh_format* fmt, void* scale_out,
+                              int32_t scale_dtype, int32_t pot_bias, void* codes_out, int32_t codes_dtype,
+                              const uint8_t* code_lut, vh_stream_t stream) {
+  return quantize_mx_impl(x, x_dtype, outer, L, inner, block, quant_max, pot, scale_fmt, global_scale, gs_dtype, fmt,
+                          scale_out, scale_dtype, pot_bias, codes_out, codes_dtype, code_lut, 0, stream);
+}
+
+extern "C" int vh_quantize_mx_rows16(const void* x, int32_t x_dtype, int64_t rows, int64_t L, int64_t block,
+                                     float quant_max, const vh_format* scale_fmt, const vh_format* fmt,
+                                     float* scale_out, uint8_t* codes_out, const uint8_t* code_lut,
+                                     vh_stream_t stream) {
+  VH_REQUIRE(rows >= 1 && rows <= 16, "vh_quantize_mx_rows16: rows must be in [1, 16] (got %lld)", (long long)rows);
+  VH_REQUIRE(L % block == 0, "vh_quantize_mx_rows16: L must be a multiple of block");
+  return quantize_mx_impl(x, x_dtype, rows, L, 1, block, quant_max, 0, scale_fmt, nullptr, 0, fmt, scale_out, VH_F32,
+                          0, codes_out, VH_U8, code_lut, 1, stream);
 }
 
 extern "C" int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,

@@ -8,18 +8,20 @@
 // the reference only by its bf16 rounding of each decoded operand (at most
 // 2**-9 relative per element), well inside the 1e-2 GEMM tolerance.
 //
-// Layout: one workgroup per 16 output columns; its WAVES waves split K into
-// contiguous ranges, keep 4 or 8 blocks of loads in flight each, and reduce
-// through LDS.  WAVES = 4 when there are at least 512 column tiles (long
-// per-wave streams, 8+ waves per CU), 16 otherwise (fill the CUs by
-// splitting K further).  The tile's activation and weight scales are staged
-// in LDS once (decoded to fp32, block-major), so the block loop issues only
-// the weight and activation loads.  Weight nibbles are baked in MFMA lane
-// order so every lane's 8-byte load is one coalesced 512-byte wave access per
-// block; nibbles become int8 levels with three v_perm_b32 per 4 values.
+// Layout: a workgroup of 8 waves covers T 16-column tiles; the tile's K
+// blocks are split into 8 / T contiguous ranges, one per wave, so the T
+// waves of a range read the same activation bytes at the same time (they
+// hit in L1: the activations are re-read once per T tiles, not per tile).
+// Every load is issued per block straight from the baked layouts -- weight
+// nibbles in MFMA lane order (one coalesced 512-byte wave access per block),
+// the tile's 16 scale bytes of a block contiguous, the activations' scales
+// block-major [K/64][16] -- two rounds of UNROLL blocks in flight, with no
+// staging prologue; nibbles become int8 levels with three v_perm_b32 per 4
+// values.  The K ranges meet through LDS at the end.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <type_traits>
 
 #include "vh_device.h"
 #include "vh_host.h"
@@ -27,8 +29,6 @@
 namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int MAX_BLOCKS = 256;  // K <= 16384 (activation scales staged in LDS)
 
 // Bake: one thread per (tile, block, lane) -> 8 bytes.
 __global__ void __launch_bounds__(256) k_pack_nf4(const uint8_t* __restrict__ codes, int64_t N, int64_t K,
@@ -66,108 +66,100 @@ __device__ __forceinline__ uint32_t lut16(uint32_t idx, uint32_t t0, uint32_t t1
   return __builtin_amdgcn_perm(hi, lo, pick);
 }
 
-template <int WAVES>
+// SK: the weight scale map's kind (fmt_decode_k), fixed at compile time so
+// the block loop stays free of branches (a runtime switch there makes the
+// compiler drain every outstanding load at each merge).
+// NBW: blocks per chunk of a wave's K range (padded with empty blocks); a
+// chunk's two rounds are unrolled into straight-line code, where the
+// compiler's count of outstanding loads is exact (around a loop, or over
+// more rounds, it drains them all or spills).
+template <int T, int SK, int NBW, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64)
 k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, const uint8_t* __restrict__ wp,
            const uint8_t* __restrict__ ws, vh_format sfmt, uint4 lv, int64_t N, int64_t K, vh_epilogue epi,
            void* __restrict__ y) {
-  // activation and weight scales of this tile, block-major: a lane reads
-  // its row's / column's scale of block b at [b][.], no bank conflicts
-  __shared__ __attribute__((aligned(16))) float s_xs[MAX_BLOCKS][16];
-  __shared__ float s_ws[MAX_BLOCKS][16];
+  constexpr int KR = WAVES / T;  // K ranges per tile
+  constexpr int UNROLL = NBW < 8 ? NBW : 8;  // blocks per round; two rounds in flight (256 VGPRs)
+  constexpr int ROUNDS = NBW / UNROLL;
   __shared__ float s_red[WAVES][4][64];
-  // blocks per round: 16 waves fit 128 VGPRs (and see short K ranges)
-  constexpr int UNROLL = WAVES == 16 ? 4 : 8;
   const int tid = threadIdx.x;
   const int nb = (int)(K / 64);
-  // wave-uniform block range, kept in scalar registers
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t tile = blockIdx.x;
-  const int b0 = wave * nb / WAVES, b1 = (wave + 1) * nb / WAVES;
+  const int tl = wave % T, kr = wave / T;
+  const int64_t tile = (int64_t)blockIdx.x * T + tl;
+  const int b0 = kr * nb / KR, b1 = (kr + 1) * nb / KR;
   const int64_t n = tile * 16 + (lane & 15);
-  const int ma = lane & 15;         // activation row this lane feeds to the MFMA
-  const int mrow = (lane >> 4) * 4; // output rows this lane accumulates
-  const bool a_live = ma < M;
+  const int ma = lane & 15;          // activation row this lane feeds to the MFMA
+  const int mrow = (lane >> 4) * 4;  // output rows this lane accumulates
 
   // Buffer loads: a lane whose row is past M, or a block past this wave's
-  // range, reads out of range and gets zeros without a memory access, so
-  // it adds nothing to the dot products.  Each wave access is then one
-  // 512-byte weight run and at most 64 bytes per live activation row.
+  // range, reads out of range and gets zeros without a memory access.
   constexpr uint32_t OOB = 0x80000000u;
   const __amdgpu_buffer_rsrc_t wr =
       __builtin_amdgcn_make_buffer_rsrc((void*)(wp + tile * nb * 512), (short)0, nb * 512, 0x00020000);
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xl, (short)0, M * (int)K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wsr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(ws + tile * nb * 16), (short)0, nb * 16, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xsr = __builtin_amdgcn_make_buffer_rsrc((void*)xs, (short)0, nb * 64, 0x00020000);
   const uint32_t woff = (uint32_t)lane * 8u;
-  const uint32_t xoff = a_live ? (uint32_t)(ma * K + (lane >> 4) * 16) : OOB;
-  auto load = [&](int b, vh_u32x2* wv, vh_u32x4* xv) {
+  const uint32_t xoff = ma < M ? (uint32_t)(ma * K + (lane >> 4) * 16) : OOB;
+  const uint32_t wsoff = (uint32_t)(lane & 15), xsoff = (uint32_t)mrow * 4u;
+  struct Set {
+    vh_u32x2 w[UNROLL];
+    vh_u32x4 x[UNROLL];
+    vh_u32x4 sx[UNROLL];
+    uint32_t sw[UNROLL];
+  };
+  auto load = [&](int b, Set& st) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const bool ok = b + u < b1;
-      wv[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, ok ? woff + (uint32_t)(b + u) * 512u : OOB, 0, 0);
-      xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + (uint32_t)(b + u) * 64u : OOB, 0, 0);
+      const uint32_t bb = (uint32_t)(b + u);
+      st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, ok ? woff + bb * 512u : OOB, 0, 0);
+      st.x[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + bb * 64u : OOB, 0, 0);
+      st.sw[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, ok ? wsoff + bb * 16u : OOB, 0, 0);
+      st.sx[u] = __builtin_amdgcn_raw_buffer_load_b128(xsr, ok ? xsoff + bb * 64u : OOB, 0, 0);
     }
   };
-  // Rounds alternate between two register sets.  With 16 waves (4-block
-  // rounds) two rounds are always in flight, the first two loaded before the
-  // scales are staged; with 4 waves the second set is loaded once the first
-  // is being consumed (two 8-block rounds in flight would not fit 128 VGPRs).
-  constexpr bool DEEP = WAVES == 16;
-  vh_u32x2 w0[UNROLL], w1[UNROLL];
-  vh_u32x4 x0[UNROLL], x1[UNROLL];
-  if (b0 < b1) load(b0, w0, x0);
-  if (DEEP && b0 + UNROLL < b1) load(b0 + UNROLL, w1, x1);
-
-  const uint8_t* wst = ws + tile * 16 * nb;  // the tile's 16 scale rows are contiguous
-  for (int i = tid; i < 16 * nb; i += WAVES * 64) s_ws[i % nb][i / nb] = fmt_decode(wst[i], sfmt, nullptr);
-  for (int i = tid; i < nb * 16; i += WAVES * 64) {
-    const int bq = i / 16, m = i % 16;
-    s_xs[bq][m] = m < M ? xs[(int64_t)m * nb + bq] : 0.0f;
-  }
-  __syncthreads();
-
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  const int blast = b1 > b0 ? b1 - 1 : b0;
-  auto round = [&](int b, const vh_u32x2* w, const vh_u32x4* x) {
+  auto round = [&](const Set& st) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      const int bb = b + u < b1 ? b + u : blast;  // past the range: zero activations, any finite scale
       i32x4 wl;
-      wl[0] = (int)lut16(w[u].x & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      wl[1] = (int)lut16(w[u].y & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      wl[2] = (int)lut16((w[u].x >> 4) & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      wl[3] = (int)lut16((w[u].y >> 4) & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      i32x4 xa = {(int)x[u].x, (int)x[u].y, (int)x[u].z, (int)x[u].w};
+      wl[0] = (int)lut16(st.w[u].x & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
+      wl[1] = (int)lut16(st.w[u].y & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
+      wl[2] = (int)lut16((st.w[u].x >> 4) & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
+      wl[3] = (int)lut16((st.w[u].y >> 4) & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
+      const i32x4 xa = {(int)st.x[u].x, (int)st.x[u].y, (int)st.x[u].z, (int)st.x[u].w};
       i32x4 d = {0, 0, 0, 0};
       d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
-      const float swv = s_ws[bb][lane & 15];
-      const float4 sx = *(const float4*)&s_xs[bb][mrow];
-      acc[0] = fmaf((float)d[0], sx.x * swv, acc[0]);
-      acc[1] = fmaf((float)d[1], sx.y * swv, acc[1]);
-      acc[2] = fmaf((float)d[2], sx.z * swv, acc[2]);
-      acc[3] = fmaf((float)d[3], sx.w * swv, acc[3]);
+      // past the range: zero dot products (zero activations); the decoded
+      // scale of a zero byte is finite
+      const float swv = fmt_decode_k<SK>(st.sw[u], sfmt, nullptr);
+      acc[0] = fmaf((float)d[0], __uint_as_float(st.sx[u].x) * swv, acc[0]);
+      acc[1] = fmaf((float)d[1], __uint_as_float(st.sx[u].y) * swv, acc[1]);
+      acc[2] = fmaf((float)d[2], __uint_as_float(st.sx[u].z) * swv, acc[2]);
+      acc[3] = fmaf((float)d[3], __uint_as_float(st.sx[u].w) * swv, acc[3]);
     }
   };
-  if constexpr (DEEP) {
-    for (int b = b0; b < b1; b += 2 * UNROLL) {
-      round(b, w0, x0);
-      if (b + 2 * UNROLL < b1) load(b + 2 * UNROLL, w0, x0);
-      if (b + UNROLL >= b1) break;
-      round(b + UNROLL, w1, x1);
-      if (b + 3 * UNROLL < b1) load(b + 3 * UNROLL, w1, x1);
-    }
-  } else {
-    for (int b = b0; b < b1; b += 2 * UNROLL) {
-      if (b + UNROLL < b1) load(b + UNROLL, w1, x1);
-      round(b, w0, x0);
-      if (b + UNROLL >= b1) break;
-      if (b + 2 * UNROLL < b1) load(b + 2 * UNROLL, w0, x0);
-      round(b + UNROLL, w1, x1);
+  // blocks past the range load zeros without a memory access; a range
+  // longer than NBW blocks runs in chunks of NBW
+  for (int c0 = b0; c0 < b1; c0 += NBW) {
+    Set s[2];
+    load(c0, s[0]);
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+      if (r + 1 < ROUNDS) load(c0 + (r + 1) * UNROLL, s[(r + 1) & 1]);
+      round(s[r & 1]);
+      // keep later rounds' loads in place (two register sets, not ROUNDS):
+      // no memory access moves across this point
+      asm volatile("" ::: "memory");
     }
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) s_red[wave][r][lane] = acc[r];
   __syncthreads();
-  if (wave != 0) return;
+  if (kr != 0) return;
   float alpha = 1.0f;
   if (epi.scale) alpha = epi.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)epi.scale) : *(const float*)epi.scale;
   float bias = 0.0f;
@@ -178,7 +170,7 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
     if (m >= M) continue;
     float v = 0.0f;
 #pragma unroll
-    for (int wv = 0; wv < WAVES; ++wv) v += s_red[wv][r][lane];
+    for (int q = 0; q < KR; ++q) v += s_red[q * T + tl][r][lane];
     if (epi.scale) v *= alpha;
     if (epi.bias) v += bias;
     if (epi.out_dtype == VH_BF16) ((uint16_t*)y)[m * N + n] = (uint16_t)f2bf(v);
@@ -204,7 +196,7 @@ extern "C" int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t
              "vh_gemv_nf4: null argument");
   VH_REQUIRE(M >= 1 && M <= 16, "vh_gemv_nf4: M must be in [1, 16] (got %lld)", (long long)M);
   VH_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 64 == 0, "vh_gemv_nf4: needs N %% 16 == 0 and K %% 64 == 0");
-  VH_REQUIRE(K / 64 <= MAX_BLOCKS, "vh_gemv_nf4: K must be <= %d", MAX_BLOCKS * 64);
+  VH_REQUIRE(K / 64 <= 8 * 32, "vh_gemv_nf4: K must be <= %d", 8 * 32 * 64);
   VH_REQUIRE(((uintptr_t)x_levels % 16 == 0) && ((uintptr_t)w_packed % 8 == 0), "vh_gemv_nf4: misaligned operand");
   VH_REQUIRE(epi->mode == EPI_PLAIN && (epi->out_dtype == VH_BF16 || epi->out_dtype == VH_F32),
              "vh_gemv_nf4: unsupported epilogue");
@@ -214,11 +206,35 @@ extern "C" int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t
   uint32_t t[4];
   memcpy(t, levels16, 16);
   const uint4 lv = make_uint4(t[0], t[1], t[2], t[3]);
-  if (N / 16 >= 512)
-    hipLaunchKernelGGL(k_gemv_nf4<4>, dim3((unsigned)(N / 16)), dim3(4 * 64), 0, vh::as_stream(stream), x_levels,
-                       x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
-  else
-    hipLaunchKernelGGL(k_gemv_nf4<16>, dim3((unsigned)(N / 16)), dim3(16 * 64), 0, vh::as_stream(stream), x_levels,
-                       x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
+  // tiles per workgroup: one while that leaves the grid under 512
+  // workgroups, else 4 (activations re-read once per 4 tiles; 8 waves: two
+  // K ranges per tile)
+  const int64_t tiles = N / 16;
+  hipStream_t st = vh::as_stream(stream);
+  const bool four = tiles >= 512 && tiles % 4 == 0 && K / 64 <= 2 * 16;
+  // blocks per wave: the tile's K blocks over its K ranges, rounded up to 4,
+  // 8 or 16 (longer ranges in chunks of 16)
+  const int64_t nb = K / 64;
+  const int64_t kr = four ? 2 : 8, bpw = (nb + kr - 1) / kr;
+  auto go = [&](auto sk) {
+    constexpr int SK = decltype(sk)::value;
+    auto launch = [&](auto nbw) {
+      constexpr int NBW = decltype(nbw)::value;
+      if (four)
+        hipLaunchKernelGGL((k_gemv_nf4<4, SK, NBW, 8>), dim3((unsigned)(tiles / 4)), dim3(512), 0, st, x_levels,
+                           x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
+      else
+        hipLaunchKernelGGL((k_gemv_nf4<1, SK, NBW, 8>), dim3((unsigned)tiles), dim3(512), 0, st, x_levels, x_scale,
+                           (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
+    };
+    if (bpw <= 4) launch(std::integral_constant<int, 4>{});
+    else if (bpw <= 8) launch(std::integral_constant<int, 8>{});
+    else launch(std::integral_constant<int, 16>{});
+  };
+  const vh_format& f = *w_scale_fmt;
+  if (f.kind == VH_FMT_INT) go(std::integral_constant<int, K_INT>{});
+  else if (f.kind == VH_FMT_MINIFLOAT && (f.flags & VH_FMT_HW_E4M3)) go(std::integral_constant<int, K_E4M3>{});
+  else if (f.kind == VH_FMT_MINIFLOAT) go(std::integral_constant<int, K_MINI>{});
+  else go(std::integral_constant<int, K_POSIT>{});
   return vh::check_launch("vh_gemv_nf4");
 }

@@ -110,6 +110,8 @@ _SIGNATURES = {
     "vh_gemm": ([_P, _P], _I32),
     "vh_gemm_workspace_bytes": ([_P], _I64),
     "vh_gemm_plan": ([_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32), ctypes.POINTER(_I32)], _I32),
+    "vh_quantize_mx_rows16": ([_P, _I32, _I64, _I64, _I64, ctypes.c_float, ctypes.POINTER(Format),
+                               ctypes.POINTER(Format), _P, _P, _P, _P], _I32),
     "vh_pack_nf4": ([_P, _I64, _I64, _P, _P], _I32),
     # x_levels, x_scale, M, w_packed, w_scale, w_scale_fmt, levels16 (host), N, K, epilogue*, y, stream
     "vh_gemv_nf4": ([_P, _P, _I64, _P, _P, ctypes.POINTER(Format), _P, _I64, _I64, _P, _P, _P], _I32),

@@ -377,7 +377,7 @@ class NF4Weight(NamedTuple):
     the GEMV's MFMA lane order, plus one scale-map code per 64-block."""
 
     packed: torch.Tensor      # uint8, N * K / 2
-    scale: torch.Tensor       # uint8 [N, K / 64]
+    scale: torch.Tensor       # uint8 [N / 16, K / 64, 16], tile-major (nf4_tile_scales)
     scale_fmt: "formats.Classified"
     levels: bytes             # the 16 int8 codebook levels
     N: int
@@ -391,11 +391,18 @@ def _levels_of(entries: torch.Tensor) -> bytes:
     return bytes(int(v) & 0xFF for v in lv.tolist())
 
 
+def nf4_tile_scales(scale_bytes: torch.Tensor) -> torch.Tensor:
+    """Weight scale bytes ``[N, K/64]`` -> the GEMV's tile-major layout
+    ``[N/16, K/64, 16]`` (a tile's 16 bytes of a block contiguous)."""
+    N, nb = scale_bytes.shape
+    return scale_bytes.reshape(N // 16, 16, nb).transpose(1, 2).contiguous()
+
+
 def bake_nf4_weight(w: torch.Tensor, index_table: torch.Tensor, scale_qmap: torch.Tensor,
                     entries: torch.Tensor) -> NF4Weight:
     """``quantize_mx(w, index_table, [-1], 64, 31, scale_qmap=...)`` once (as
     convert bakes weights, ``quantization/quantize_pt2e.py:819-828``), then
-    packed for the GEMV."""
+    packed for the GEMV: nibbles in MFMA lane order, scale bytes tile-major."""
     from . import packed as _packed
 
     N, K = w.shape
@@ -404,7 +411,7 @@ def bake_nf4_weight(w: torch.Tensor, index_table: torch.Tensor, scale_qmap: torc
     st = load().vh_pack_nf4(ctypes.c_void_p(p.codes.data_ptr()), N, K, ctypes.c_void_p(out.data_ptr()),
                             ctypes.c_void_p(stream_of(w)))
     _lib.check(st, "vh_pack_nf4")
-    return NF4Weight(out, p.scale.contiguous(), p.scale_fmt, _levels_of(entries), N, K)
+    return NF4Weight(out, nf4_tile_scales(p.scale), p.scale_fmt, _levels_of(entries), N, K)
 
 
 _level_lut_cache = {}
@@ -433,14 +440,14 @@ def linear_nf4(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, sc
     ec = formats.classify(index_table)
     sc = formats.classify(scale_qmap)
     xl = torch.empty(M, K, dtype=torch.uint8, device=x.device)
-    xs = torch.empty(M, K // 64, dtype=torch.float32, device=x.device)
+    xs = torch.empty(K // 64, 16, dtype=torch.float32, device=x.device)  # block-major, rows past M unused
     lut = _level_lut(weight.levels, x.device)
     lib_ = load()
-    st = lib_.vh_quantize_mx(ctypes.c_void_p(xc.data_ptr()), dtype_code(xc.dtype), M, K, 1, 64, 31.0, 0,
-                             ctypes.byref(sc.fmt), None, 0, ctypes.byref(ec.fmt), ctypes.c_void_p(xs.data_ptr()),
-                             VH_F32, 0, ctypes.c_void_p(xl.data_ptr()), dtype_code(torch.uint8),
-                             ctypes.c_void_p(lut.data_ptr()), ctypes.c_void_p(stream_of(x)))
-    _lib.check(st, "vh_quantize_mx")
+    st = lib_.vh_quantize_mx_rows16(ctypes.c_void_p(xc.data_ptr()), dtype_code(xc.dtype), M, K, 64, 31.0,
+                                    ctypes.byref(sc.fmt), ctypes.byref(ec.fmt), ctypes.c_void_p(xs.data_ptr()),
+                                    ctypes.c_void_p(xl.data_ptr()), ctypes.c_void_p(lut.data_ptr()),
+                                    ctypes.c_void_p(stream_of(x)))
+    _lib.check(st, "vh_quantize_mx_rows16")
     y = torch.empty(M, weight.N, dtype=out_dtype, device=x.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()

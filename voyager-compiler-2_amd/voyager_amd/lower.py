@@ -373,7 +373,7 @@ def _bake_mxnf4(w: torch.Tensor, ws: torch.Tensor, scale_qmap: torch.Tensor) -> 
     sbytes = packed.quantize_packed(ws.contiguous(), one, scale_qmap)
     if not torch.equal(packed.unpack_codes(sbytes, scale_qmap), ws):
         raise ValueError("MX-NF4 weight scales off the scale map's grid")
-    return out, sbytes
+    return out, gemm.nf4_tile_scales(sbytes.reshape(N, K // 64))
 
 
 # ------------------------------------------------------------------ rewrite
