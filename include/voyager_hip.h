@@ -116,6 +116,52 @@ int vh_quantize_sr(const void* x, int32_t x_dtype, const int64_t* shape, int32_t
                    const vh_param* zero_point, int32_t compute_dtype, const void* levels, int32_t levels_dtype,
                    int32_t nlevels, const int64_t* seed, void* out, int32_t out_dtype, vh_stream_t stream);
 
+/* Codebook tables under a region grid (_region_view, ops/quantized.py:193-229):
+ * `regions` tables; element (i_0..i_n) uses table
+ * sum_d (i_d / region.div[d]) * region.stride[d] (region.ptr and dtype
+ * unused; region.scalar = 1: one table).  edges: [regions][nedges] float32
+ * in device memory, ascending, each the largest float32 not above the
+ * caller's edge (a search of bfloat16 values against it answers as against
+ * the edge itself).  entries: [regions][k] in device memory. */
+typedef struct vh_codebook {
+  const float* edges;
+  int32_t nedges;
+  int32_t k;
+  const void* entries;   /* NULL (encode only): write the index */
+  int32_t entries_dtype; /* VH_BF16, VH_F16 or VH_F32 */
+  int64_t regions;
+  vh_param region;
+} vh_codebook;
+
+/* quantize against a codebook: v = round_c(round_c(x / scale) + zp) as
+ * vh_quantize computes it, then the count of the element's table's edges e
+ * with !(e >= bf16(v)) (torch.searchsorted, left side: NaN past the end),
+ * written as that index or as its entry (nedges == k - 1), in the compute
+ * dtype.  Replaces encode (ops/quantized.py:232-287) as quantize
+ * (:449-515) calls it for a codebook qmap, with its `output_code` bounds or
+ * the midpoints of the entries. */
+int vh_quantize_codebook(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                         const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
+                         const vh_codebook* cb, void* out, vh_stream_t stream);
+
+/* Codebook lookup: out = round_out(round_x(entry[long(x)]) * scale) (no
+ * scale: round_x(entry[long(x)])), the element's table's entry; negative
+ * indices count from the end when wrap_negative (1-D indexing), NaN where
+ * torch's indexing or gather would raise.  Replaces decode
+ * (ops/quantized.py:290-315) and, with the block scale, _decode_and_scale
+ * inside dequantize_mx (:574-591, 1118-1150). */
+int vh_decode_codebook(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                       const vh_codebook* cb, int32_t wrap_negative, const vh_param* scale, void* out,
+                       int32_t out_dtype, vh_stream_t stream);
+
+/* max |x| (NaN propagating, zero past L) over blocks of `block` elements
+ * along L of a contiguous [outer, L, inner] tensor: out [outer, ceil(L /
+ * block), inner] in x_dtype.  One axis of the block reduction of
+ * calculate_mx_qparam over several axes (ops/quantized.py:958-1031,
+ * quantization/mx_utils.py:16-125); the axes are reduced one call at a time. */
+int vh_block_amax(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner, int64_t block,
+                  void* out, vh_stream_t stream);
+
 /* dequantize: out = G((Fin(x) - zp) * scale).  Replaces
  * quantized_ops.dequantize (ops/quantized.py:518-571).  x_dtype VH_U8 reads
  * packed codes of fmt_in. */
@@ -159,7 +205,8 @@ int vh_quantize_mx_rows16(const void* x, int32_t x_dtype, int64_t rows, int64_t 
                           uint8_t* codes_out, const uint8_t* code_lut, vh_stream_t stream);
 
 /* quantize_affine: per block min/max -> (scale, zero_point, codes).
- * Replaces quantized_ops.quantize_affine (ops/quantized.py:1218-1283). */
+ * Replaces quantized_ops.quantize_affine (ops/quantized.py:1218-1283).
+ * codes_out NULL (fmt then optional): scale and zero point only. */
 int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
                        int64_t block, float quant_min, float quant_max,
                        const vh_format* scale_fmt, const vh_format* fmt, void* scale_out,

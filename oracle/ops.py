@@ -55,19 +55,55 @@ def vmap(input, table, chunk_size=1024 * 1024):
     return out.to(in_dtype)
 
 
+def region_view(input, codebook):
+    """``_region_view``, ``ops/quantized.py:193-229``: ``input`` split by the
+    ``[*counts, k]`` grid of ``codebook`` with the region axes first, and the
+    permutation back."""
+    counts = tuple(codebook.shape[:-1])
+    if len(counts) != input.dim():
+        raise ValueError(f"a {list(counts)} region codebook tiles {len(counts)} axes, "
+                         f"but the tensor reaching it has {input.dim()}")
+    if any(n % c for n, c in zip(input.shape, counts)):
+        raise ValueError(f"a {list(counts)} region codebook does not divide the "
+                         f"{list(input.shape)} tensor reaching it")
+    split = []
+    for n, c in zip(input.shape, counts):
+        split += [c, n // c]
+    order = list(range(0, 2 * len(counts), 2)) + list(range(1, 2 * len(counts), 2))
+    inverse = [0] * len(order)
+    for pos, ax in enumerate(order):
+        inverse[ax] = pos
+    return input.reshape(split).permute(order), inverse
+
+
 def encode(input, codebook, bounds=None):
-    """1-D codebook search; ``ops/quantized.py:232-287`` (one table only)."""
-    assert codebook.dim() == 1
-    edges = bounds if bounds is not None else (codebook[:-1] + codebook[1:]) / 2
-    index = torch.searchsorted(edges, input.bfloat16().float())
-    picked = index if bounds is not None else codebook[index]
-    return picked.to(input.dtype)
+    """Codebook search, one table or a region grid; ``ops/quantized.py:232-287``."""
+    edges = bounds if bounds is not None else (codebook[..., :-1] + codebook[..., 1:]) / 2
+    if codebook.dim() == 1:
+        index = torch.searchsorted(edges, input.bfloat16().float())
+        picked = index if bounds is not None else codebook[index]
+        return picked.to(input.dtype)
+    moved, inverse = region_view(input, codebook)
+    regions = codebook.numel() // codebook.shape[-1]
+    flat = moved.reshape(regions, -1).bfloat16().float()
+    table = codebook.reshape(regions, -1)
+    index = torch.searchsorted(edges.reshape(regions, -1).contiguous(), flat.contiguous())
+    picked = index if bounds is not None else table.gather(1, index)
+    picked = picked.view(moved.shape).permute(inverse)
+    return picked.reshape(input.shape).to(input.dtype)
 
 
 def decode(input, codebook):
-    """``codebook[long(input)]``; ``ops/quantized.py:290-315`` (1-D)."""
-    assert codebook.dim() == 1
-    return codebook[input.to(torch.long)].to(input.dtype)
+    """The entry each index names, one table or a region grid;
+    ``ops/quantized.py:290-315``."""
+    index = input.to(torch.long)
+    if codebook.dim() == 1:
+        return codebook[index].to(input.dtype)
+    moved, inverse = region_view(index, codebook)
+    regions = codebook.numel() // codebook.shape[-1]
+    picked = codebook.reshape(regions, -1).gather(1, moved.reshape(regions, -1))
+    picked = picked.view(moved.shape).permute(inverse)
+    return picked.reshape(index.shape).to(input.dtype)
 
 
 # ------------------------------------------------------ stochastic rounding

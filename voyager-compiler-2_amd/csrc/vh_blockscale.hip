@@ -489,9 +489,11 @@ extern "C" int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer,
                                   int32_t codes_dtype, vh_stream_t stream) {
   int rc;
   if ((rc = check_common(x, x_dtype, outer, L, inner, block, "vh_quantize_affine"))) return rc;
-  VH_REQUIRE(scale_out && zp_out && fmt, "vh_quantize_affine: null output or map");
-  VH_REQUIRE(codes_dtype == x_dtype || codes_dtype == VH_U8, "vh_quantize_affine: bad codes dtype");
-  VH_REQUIRE(codes_dtype != VH_U8 || packable(*fmt), "vh_quantize_affine: element map has no packed form");
+  VH_REQUIRE(scale_out && zp_out, "vh_quantize_affine: null output");
+  VH_REQUIRE(!codes_out || fmt, "vh_quantize_affine: codes need an element map");
+  VH_REQUIRE(!codes_out || codes_dtype == x_dtype || codes_dtype == VH_U8, "vh_quantize_affine: bad codes dtype");
+  VH_REQUIRE(!(codes_out && codes_dtype == VH_U8) || packable(*fmt),
+             "vh_quantize_affine: element map has no packed form");
   Params P;
   memset(&P, 0, sizeof(P));
   P.mode = AFFINE;
@@ -502,8 +504,10 @@ extern "C" int vh_quantize_affine(const void* x, int32_t x_dtype, int64_t outer,
     P.has_sfmt = 1;
     P.sfmt = *scale_fmt;
   }
-  P.has_fmt = 1;
-  P.fmt = *fmt;
+  if (fmt) {
+    P.has_fmt = 1;
+    P.fmt = *fmt;
+  }
   P.scale_dtype = x_dtype;
   P.codes_dtype = codes_dtype;
   if (outer * L * inner == 0) return VH_OK;

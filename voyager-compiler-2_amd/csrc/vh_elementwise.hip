@@ -886,6 +886,225 @@ extern "C" int vh_quantize_sr(const void* x, int32_t x_dtype, const int64_t* sha
   return vh::check_launch("vh_quantize_sr");
 }
 
+// ------------------------------------------------------------ codebooks
+// encode (ops/quantized.py:232-287) and decode (:290-315) against codebook
+// tables under a region grid (_region_view, :193-229): element e uses table
+// region(e) = sum_d (i_d / div[d]) * stride[d].  encode rounds its value to
+// bfloat16 and counts the leading edges with !(edge >= v), which is
+// torch.searchsorted's left bisection (a NaN lands past the last edge), then
+// writes that index or its entry.  The edges are staged in LDS when all the
+// tables fit in CB_LDS_FLOATS; otherwise the search reads them through the
+// cache.
+constexpr int CB_LDS_FLOATS = 12288;
+
+struct CbDev {
+  const float* edges;
+  const void* entries;
+  int edt;
+  int nedges, k;
+  int top;  // the largest power of two <= nedges (0: no edges)
+  int64_t regions;
+  vh_param region;
+};
+
+VH_DEV int cb_search(const float* E, int nedges, int top, float v) {
+  int lo = 0;
+  for (int step = top; step > 0; step >>= 1) {
+    const int j = lo + step;
+    if (j <= nedges && !(E[j - 1] >= v)) lo = j;
+  }
+  return lo;
+}
+
+template <bool STAGE>
+__global__ void __launch_bounds__(256)
+k_encode(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, vh_param sp, vh_param zp, int cdt,
+         CbDev cb, void* __restrict__ out) {
+  extern __shared__ float s_edges[];
+  const float* E = cb.edges;
+  if constexpr (STAGE) {
+    const int total = (int)(cb.regions * cb.nedges);
+    for (int i = threadIdx.x; i < total; i += blockDim.x) s_edges[i] = cb.edges[i];
+    __syncthreads();
+    E = s_edges;
+  }
+  const int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (base >= n) return;
+  const bool narrow = n < (1ll << 31);
+  float sv[VEC], zv[VEC];
+  const float s0 = (sp.ptr && sp.scalar) ? load_any(sp.ptr, sp.dtype, 0) : 1.0f;
+  const float z0 = (zp.ptr && zp.scalar) ? load_any(zp.ptr, zp.dtype, 0) : 0.0f;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    sv[j] = s0;
+    zv[j] = z0;
+  }
+  if (sp.ptr && !sp.scalar) param_values(sp, shape, base, n, sv);
+  if (zp.ptr && !zp.scalar) param_values(zp, shape, base, n, zv);
+  for (int j = 0; j < VEC; ++j) {
+    const int64_t i = base + j;
+    if (i >= n) break;
+    float q = load_any(x, x_dtype, i);
+    if (sp.ptr) q = div_round(q, sv[j], cdt);
+    if (zp.ptr) q = round_to(q + zv[j], cdt);
+    const int64_t r = cb.region.scalar ? 0 : param_offset(cb.region, shape, i, narrow);
+    const int idx = cb_search(E + r * cb.nedges, cb.nedges, cb.top, rbf(q));
+    const float val = cb.entries ? load_any(cb.entries, cb.edt, r * cb.k + idx) : (float)idx;
+    store_any(out, cdt, i, round_to(val, cdt));
+  }
+}
+
+// decode: entry long(x) of the element's table (negative indices count from
+// the end when `wrap`), rounded to the codes' dtype, NaN where torch's
+// indexing would raise; then, with a scale, times the element's scale,
+// rounded to out_dtype.
+__global__ void __launch_bounds__(256)
+k_decode_cb(const void* __restrict__ x, int x_dtype, int64_t n, Shape shape, CbDev cb, int wrap, vh_param sp,
+            void* __restrict__ out, int out_dtype) {
+  const int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (base >= n) return;
+  const bool narrow = n < (1ll << 31);
+  float sv[VEC];
+  const float s0 = (sp.ptr && sp.scalar) ? load_any(sp.ptr, sp.dtype, 0) : 1.0f;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) sv[j] = s0;
+  if (sp.ptr && !sp.scalar) param_values(sp, shape, base, n, sv);
+  for (int j = 0; j < VEC; ++j) {
+    const int64_t i = base + j;
+    if (i >= n) break;
+    const float c = load_any(x, x_dtype, i);
+    float val = __builtin_nanf("");
+    if (fabsf(c) < 0x1p62f) {
+      int64_t t = (int64_t)c;
+      if (t < 0 && wrap) t += cb.k;
+      if (t >= 0 && t < cb.k) {
+        const int64_t r = cb.region.scalar ? 0 : param_offset(cb.region, shape, i, narrow);
+        val = round_to(load_any(cb.entries, cb.edt, r * cb.k + t), x_dtype);
+      }
+    }
+    if (sp.ptr) val = round_to(val * sv[j], out_dtype);
+    store_any(out, out_dtype, i, val);
+  }
+}
+
+static int check_codebook(const vh_codebook* cb, const Shape& s, bool encode, CbDev* d) {
+  VH_REQUIRE(cb, "codebook: null descriptor");
+  VH_REQUIRE(cb->k >= 1 && cb->k <= 65536, "codebook: %d entries per table (1 .. 65536 supported)", cb->k);
+  VH_REQUIRE(cb->regions >= 1, "codebook: %lld regions", (long long)cb->regions);
+  if (encode) {
+    VH_REQUIRE(cb->nedges >= 0 && cb->nedges < 65536, "codebook: %d edges per table", cb->nedges);
+    VH_REQUIRE(cb->nedges == 0 || cb->edges, "codebook: edges missing");
+    VH_REQUIRE(!cb->entries || cb->nedges == cb->k - 1, "codebook: %d edges for %d entries", cb->nedges, cb->k);
+  } else {
+    VH_REQUIRE(cb->entries, "codebook: entries missing");
+  }
+  VH_REQUIRE(!cb->entries || vh::is_float_dtype(cb->entries_dtype), "codebook: entry dtype %d unsupported",
+             cb->entries_dtype);
+  if (!cb->region.scalar) {
+    for (int dd = 0; dd < s.ndim; ++dd) {
+      VH_REQUIRE(cb->region.div[dd] >= 1 && cb->region.stride[dd] >= 0, "codebook: bad region grid on dim %d", dd);
+    }
+  }
+  d->edges = cb->edges;
+  d->entries = cb->entries;
+  d->edt = cb->entries_dtype;
+  d->nedges = cb->nedges;
+  d->k = cb->k;
+  int top = 0;
+  if (cb->nedges > 0) {
+    top = 1;
+    while (top * 2 <= cb->nedges) top *= 2;
+  }
+  d->top = top;
+  d->regions = cb->regions;
+  d->region = cb->region;
+  return VH_OK;
+}
+
+extern "C" int vh_quantize_codebook(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                                    const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
+                                    const vh_codebook* cb, void* out, vh_stream_t stream) {
+  Shape s;
+  int64_t n;
+  int rc;
+  if ((rc = check_shape(shape, ndim, &s, &n))) return rc;
+  VH_REQUIRE(x && out, "vh_quantize_codebook: null tensor");
+  VH_REQUIRE(vh::is_float_dtype(x_dtype) && vh::is_float_dtype(compute_dtype),
+             "vh_quantize_codebook: dtypes must be bf16, fp16 or fp32");
+  if ((rc = check_param(scale, s, "scale"))) return rc;
+  if ((rc = check_param(zero_point, s, "zero_point"))) return rc;
+  CbDev d;
+  if ((rc = check_codebook(cb, s, true, &d))) return rc;
+  if (n == 0) return VH_OK;
+  const vh_param sp = scale ? *scale : null_param();
+  const vh_param zp = zero_point ? *zero_point : null_param();
+  const int64_t blocks = ((n + VEC - 1) / VEC + 255) / 256;
+  VH_REQUIRE(blocks < (1ll << 31), "vh_quantize_codebook: tensor too large");
+  const int64_t total = d.regions * d.nedges;
+  if (total <= CB_LDS_FLOATS) {
+    hipLaunchKernelGGL(k_encode<true>, dim3((unsigned)blocks), dim3(256), (size_t)(total ? total : 1) * sizeof(float),
+                       vh::as_stream(stream), x, x_dtype, n, s, sp, zp, compute_dtype, d, out);
+  } else {
+    hipLaunchKernelGGL(k_encode<false>, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), x, x_dtype, n, s,
+                       sp, zp, compute_dtype, d, out);
+  }
+  return vh::check_launch("vh_quantize_codebook");
+}
+
+extern "C" int vh_decode_codebook(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,
+                                  const vh_codebook* cb, int32_t wrap_negative, const vh_param* scale, void* out,
+                                  int32_t out_dtype, vh_stream_t stream) {
+  Shape s;
+  int64_t n;
+  int rc;
+  if ((rc = check_shape(shape, ndim, &s, &n))) return rc;
+  VH_REQUIRE(x && out, "vh_decode_codebook: null tensor");
+  VH_REQUIRE(vh::is_float_dtype(x_dtype) && vh::is_float_dtype(out_dtype),
+             "vh_decode_codebook: dtypes must be bf16, fp16 or fp32");
+  if ((rc = check_param(scale, s, "scale"))) return rc;
+  CbDev d;
+  if ((rc = check_codebook(cb, s, false, &d))) return rc;
+  if (n == 0) return VH_OK;
+  const vh_param sp = scale ? *scale : null_param();
+  const int64_t blocks = ((n + VEC - 1) / VEC + 255) / 256;
+  VH_REQUIRE(blocks < (1ll << 31), "vh_decode_codebook: tensor too large");
+  hipLaunchKernelGGL(k_decode_cb, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), x, x_dtype, n, s, d,
+                     wrap_negative ? 1 : 0, sp, out, out_dtype);
+  return vh::check_launch("vh_decode_codebook");
+}
+
+// ------------------------------------------------------------ block amax
+// max |x| over blocks of `block` along L of contiguous [outer, L, inner]
+// (zero padding past L, NaN propagating as torch.amax): one stage of
+// _shared_exponents' / calculate_mx_qparam's reduction over several axes
+// (quantization/mx_utils.py:16-63, ops/quantized.py:958-1031).  One thread
+// per output element; consecutive threads take consecutive `inner`.
+__global__ void __launch_bounds__(256)
+k_block_amax(const void* __restrict__ x, int dt, int64_t outer, int64_t L, int64_t inner, int64_t block, int64_t nb,
+             void* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= outer * nb * inner) return;
+  const int64_t i = t % inner, b = (t / inner) % nb, o = t / (inner * nb);
+  const int64_t l0 = b * block, l1 = l0 + block < L ? l0 + block : L;
+  float m = 0.0f;
+  for (int64_t l = l0; l < l1; ++l) m = nmax(m, fabsf(load_any(x, dt, (o * L + l) * inner + i)));
+  store_any(out, dt, t, m);
+}
+
+extern "C" int vh_block_amax(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner, int64_t block,
+                             void* out, vh_stream_t stream) {
+  VH_REQUIRE(x && out, "vh_block_amax: null tensor");
+  VH_REQUIRE(vh::is_float_dtype(x_dtype), "vh_block_amax: dtype %d unsupported", x_dtype);
+  VH_REQUIRE(outer >= 0 && L >= 0 && inner >= 0 && block >= 1, "vh_block_amax: bad view");
+  const int64_t nb = (L + block - 1) / block, total = outer * nb * inner;
+  if (total == 0) return VH_OK;
+  const int64_t blocks = (total + 255) / 256;
+  VH_REQUIRE(blocks < (1ll << 31), "vh_block_amax: tensor too large");
+  hipLaunchKernelGGL(k_block_amax, dim3((unsigned)blocks), dim3(256), 0, vh::as_stream(stream), x, x_dtype, outer, L,
+                     inner, block, nb, out);
+  return vh::check_launch("vh_block_amax");
+}
+
 // ------------------------------------------------------------ dequantize
 template <int KIN>
 __global__ void __launch_bounds__(256)

@@ -73,6 +73,20 @@ class Param(ctypes.Structure):
     ]
 
 
+class Codebook(ctypes.Structure):
+    """``vh_codebook``: codebook tables under a region grid."""
+
+    _fields_ = [
+        ("edges", ctypes.c_void_p),
+        ("nedges", ctypes.c_int32),
+        ("k", ctypes.c_int32),
+        ("entries", ctypes.c_void_p),
+        ("entries_dtype", ctypes.c_int32),
+        ("regions", ctypes.c_int64),
+        ("region", Param),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 _P = ctypes.c_void_p
@@ -90,6 +104,16 @@ _SIGNATURES = {
         _I32,
     ),
     "vh_quantize_sr": ([_P, _I32, _P, _I32, _P, _P, _I32, _P, _I32, _I32, _P, _P, _I32, _P], _I32),
+    "vh_quantize_codebook": (
+        [_P, _I32, ctypes.POINTER(_I64), _I32, ctypes.POINTER(Param), ctypes.POINTER(Param), _I32,
+         ctypes.POINTER(Codebook), _P, _P],
+        _I32,
+    ),
+    "vh_decode_codebook": (
+        [_P, _I32, ctypes.POINTER(_I64), _I32, ctypes.POINTER(Codebook), _I32, ctypes.POINTER(Param), _P, _I32, _P],
+        _I32,
+    ),
+    "vh_block_amax": ([_P, _I32, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "vh_dequantize": (
         [_P, _I32, ctypes.POINTER(_I64), _I32, ctypes.POINTER(Param), ctypes.POINTER(Param), _I32,
          ctypes.POINTER(Format), ctypes.POINTER(Format), _P, _I32, _P],

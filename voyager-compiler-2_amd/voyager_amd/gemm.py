@@ -17,7 +17,7 @@ import torch
 
 from . import _lib, formats
 from ._lib import VH_BF16, VH_F32, dtype_code, load, ptr, stream_of
-from .ops import _dequantize_mx_cuda, _require_gpu, _vmap_cuda, decode_table
+from .ops import _dequantize_mx_cuda, _require_gpu, decode_codes
 from .registry import cuda_kernel, fake_kernel
 from .schemas import LINEAR_LAYOUT, MATMUL_LAYOUT
 
@@ -208,7 +208,7 @@ def _decode(x, scale, code, block_size):
     if code is None and scale is None:
         return x
     if scale is None:
-        return _vmap_cuda(x, decode_table(code)) if code is not None else x
+        return decode_codes(x, code) if code is not None else x
     return _dequantize_mx_cuda(x, scale, block_size, code)
 
 

@@ -15,12 +15,13 @@ in one process.
 """
 
 import ctypes
+import math
 from typing import List, Optional, Sequence
 
 import torch
 
 from . import _lib, formats
-from ._lib import Format, Param, VH_U8, dtype_code, load, ptr, stream_of
+from ._lib import Codebook, Format, Param, VH_U8, dtype_code, load, ptr, stream_of
 
 QMAP_SIZE = formats.QMAP_SIZE
 
@@ -156,6 +157,145 @@ def _vmap_fake(input, qmap):
     return torch.empty_like(input)
 
 
+# ----------------------------------------------------------------- codebooks
+_CB_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _floor_f32(e: torch.Tensor) -> torch.Tensor:
+    """``e`` as float32, each value the largest float32 not above it: a
+    search of bfloat16 (hence float32) values answers against it as against
+    ``e`` itself."""
+    e32 = e.to(torch.float32)
+    if e.dtype in _CB_DTYPES:
+        return e32.contiguous()
+    down = torch.nextafter(e32, torch.full_like(e32, float("-inf")))
+    return torch.where(e32.to(e.dtype) > e, down, e32).contiguous()
+
+
+def _region_grid(codebook: torch.Tensor, shape) -> tuple:
+    """The region grid of ``codebook`` over a contiguous tensor of ``shape``
+    (``_region_view``, ``ops/quantized.py:193-229``): ``(regions, Param)``,
+    the table of element ``(i_0..i_n)`` being ``sum_d (i_d / div[d]) *
+    stride[d]`` in row-major order over the grid."""
+    prm = Param()
+    if codebook.dim() == 1:
+        prm.scalar = 1
+        return 1, prm
+    counts = list(codebook.shape[:-1])
+    if len(counts) != len(shape):
+        raise ValueError(f"a {counts} region codebook tiles {len(counts)} axes, "
+                         f"but the tensor reaching it has {len(shape)}")
+    if any(n % c for n, c in zip(shape, counts)):
+        raise ValueError(f"a {counts} region codebook does not divide the {list(shape)} tensor reaching it")
+    stride = 1
+    for d in reversed(range(len(counts))):
+        prm.div[d] = max(shape[d] // counts[d], 1)
+        prm.stride[d] = stride if counts[d] > 1 else 0
+        stride *= counts[d]
+    return stride, prm
+
+
+def _cached_on(t: torch.Tensor, attr: str, key, build):
+    """``build()`` cached on tensor ``t`` under ``key`` (its version and
+    address included, so an in-place change or a new tensor rebuilds)."""
+    key = (t._version, t.data_ptr()) + key
+    hit = getattr(t, attr, None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    value = build()
+    try:
+        setattr(t, attr, (key, value))
+    except (AttributeError, RuntimeError):
+        pass
+    return value
+
+
+def _codebook_desc(codebook: torch.Tensor, shape, bounds: Optional[torch.Tensor], encode: bool):
+    """``vh_codebook`` for ``codebook`` (``[k]`` or ``[*counts, k]``) over a
+    contiguous tensor of ``shape``, and the device tensors it points to.
+    encode: the edges are ``bounds`` (the result is the index) or the
+    entries' midpoints in their dtype (the result is the entry), as
+    ``encode`` (``ops/quantized.py:232-287``) takes them."""
+    if codebook.dtype not in _CB_DTYPES:
+        raise NotImplementedError(f"codebook entries of dtype {codebook.dtype} are not supported on the GPU")
+    regions, grid = _region_grid(codebook, shape)
+    k = codebook.shape[-1]
+    cb = Codebook()
+    cb.k = k
+    cb.regions = regions
+    cb.region = grid
+    keep = []
+    if not encode or bounds is None:
+        entries = codebook.reshape(regions, k).contiguous()
+        cb.entries = entries.data_ptr()
+        cb.entries_dtype = dtype_code(entries.dtype)
+        keep.append(entries)
+    if encode:
+        if bounds is None:
+            edges = _cached_on(codebook, "_vh_cb_edges", (), lambda: _floor_f32(
+                (codebook[..., :-1] + codebook[..., 1:]) / 2).reshape(regions, k - 1))
+        else:
+            if codebook.dim() == 1 and bounds.dim() != 1:
+                raise NotImplementedError("a 1-D codebook with multi-dimensional bounds is not supported on the GPU")
+            if bounds.numel() % regions:
+                raise ValueError(f"{bounds.numel()} bounds do not split into {regions} region tables")
+            edges = _cached_on(bounds, "_vh_cb_edges", (regions,),
+                               lambda: _floor_f32(bounds).reshape(regions, -1))
+        cb.edges = edges.data_ptr()
+        cb.nedges = edges.shape[-1]
+        keep.append(edges)
+    return cb, keep
+
+
+def _encode_cuda(x, scale, zero_point, block_size, cdt, codebook, bounds):
+    """``quantize`` against a codebook: the division as ``quantize`` does it,
+    then ``encode`` (``ops/quantized.py:232-287``) in one pass."""
+    xc = x.contiguous()
+    shape = list(xc.shape)
+    sp, keep_s = _param(scale, shape, block_size, cdt, "scale", own_precision=True)
+    zpp, keep_z = _param(zero_point, shape, block_size, cdt, "zero_point")
+    cb, keep = _codebook_desc(codebook, shape, bounds, True)
+    out = torch.empty(shape, dtype=cdt, device=x.device)
+    st = load().vh_quantize_codebook(ptr(xc), dtype_code(xc.dtype), _shape_arr(shape), len(shape),
+                                     ctypes.byref(sp) if sp else None, ctypes.byref(zpp) if zpp else None,
+                                     dtype_code(cdt), ctypes.byref(cb), ptr(out), ctypes.c_void_p(stream_of(x)))
+    _lib.check(st, "vh_quantize_codebook")
+    del keep_s, keep_z, keep
+    return out
+
+
+def decode_codes(x, code, scale=None, block_size=None):
+    """``decode`` then, with a scale, ``* repeat_per_block(scale)``
+    (``ops/quantized.py:290-315, 574-591``): a 1-D codebook read by
+    bfloat16 codes goes through its 65,536-entry table; any other codebook
+    (a region grid, float16 or float32 codes) through ``vh_decode_codebook``."""
+    if code.dim() == 1 and x.dtype == torch.bfloat16:
+        fi = _fmt_of(decode_table(code)).fmt
+        if scale is None:
+            return _elementwise("quantize", x, None, None, None, x.dtype, fi, None, x.dtype)
+        probe = torch.empty([1] * max(x.dim(), 1), dtype=x.dtype, device="meta")
+        cdt = torch.result_type(probe, scale)
+        return _elementwise("dequantize", x, scale, None, block_size, cdt, fi, None, cdt)
+    if x.dtype not in _CB_DTYPES:
+        raise NotImplementedError(f"codebook indices of dtype {x.dtype} are not supported on the GPU")
+    xc = x.contiguous()
+    shape = list(xc.shape)
+    out_dtype = x.dtype
+    sp, keep_s = None, None
+    if scale is not None:
+        probe = torch.empty([1] * max(x.dim(), 1), dtype=x.dtype, device="meta")
+        out_dtype = torch.result_type(probe, scale)
+        sp, keep_s = _param(scale, shape, block_size, out_dtype, "scale", own_precision=True)
+    cb, keep = _codebook_desc(code, shape, None, False)
+    out = torch.empty(shape, dtype=out_dtype, device=x.device)
+    st = load().vh_decode_codebook(ptr(xc), dtype_code(xc.dtype), _shape_arr(shape), len(shape), ctypes.byref(cb),
+                                   1 if code.dim() == 1 else 0, ctypes.byref(sp) if sp else None, ptr(out),
+                                   dtype_code(out_dtype), ctypes.c_void_p(stream_of(x)))
+    _lib.check(st, "vh_decode_codebook")
+    del keep_s, keep
+    return out
+
+
 # ----------------------------------------------------------------- quantize
 def _quantize_dtype(input, scale, zero_point):
     d = torch.result_type(input, scale)
@@ -200,7 +340,7 @@ def _quantize_cuda(input, scale, zero_point=None, axes=None, block_size=None, qm
     if seed is not None and qmap is not None:
         return _quantize_sr(input, scale, zero_point, block_size, qmap, seed, cdt)
     if qmap is not None and not _is_table(qmap):
-        raise NotImplementedError("quantized_ops.quantize: codebook (searchsorted) maps are not supported yet")
+        return _encode_cuda(input, scale, zero_point, block_size, cdt, qmap, output_code)
     fmt = _fmt_of(qmap).fmt if qmap is not None else None
     return _elementwise("quantize", input, scale, zero_point, block_size, cdt, fmt, None, cdt)
 
@@ -242,14 +382,27 @@ def _dequantize_fake(input, scale, zero_point=None, axes=None, block_size=None, 
 
 
 # ----------------------------------------------------------------- block views
+def _axes_list(x: torch.Tensor, axes) -> List[int]:
+    """The blocked axes, non-negative and ascending (``_reshape_to_blocks``,
+    ``quantization/mx_utils.py:66-80``)."""
+    axes = [axes] if isinstance(axes, int) else list(axes)
+    out = []
+    for a in axes:
+        ax = a + x.dim() if a < 0 else a
+        if not 0 <= ax < max(x.dim(), 1):
+            raise IndexError(f"axis {a} out of range for a {x.dim()}-d tensor")
+        out.append(ax)
+    if len(set(out)) != len(out):
+        raise ValueError(f"repeated block axes {axes}")
+    return sorted(out)
+
+
 def _block_view(x: torch.Tensor, axes):
     """``x`` as contiguous ``[outer, L, inner]`` around its one blocked axis."""
-    axes = [axes] if isinstance(axes, int) else list(axes)
+    axes = _axes_list(x, axes)
     if len(axes) != 1:
-        raise NotImplementedError("block scaling along more than one axis is not supported on the GPU")
-    ax = axes[0] + x.dim() if axes[0] < 0 else axes[0]
-    if not 0 <= ax < x.dim():
-        raise IndexError(f"axis {axes[0]} out of range for a {x.dim()}-d tensor")
+        raise ValueError("one block axis expected")
+    ax = axes[0]
     xc = x.contiguous()
     outer = 1
     for n in xc.shape[:ax]:
@@ -290,12 +443,37 @@ def _mx_launch(x, axes, block_size, quant_max, pot, scale_qmap, global_scale, qm
     return scale, codes
 
 
+def _mx_scale(x, axes, block_size, quant_max, pot, scale_qmap, global_scale):
+    """``calculate_mx_qparam`` (``ops/quantized.py:958-1031``).  One axis:
+    the block-scale kernel.  Several: a block's scale depends on nothing but
+    its max |x|, so ``vh_block_amax`` reduces the blocked axes one at a time
+    and the block-scale kernel turns each max into its scale (blocks of
+    one)."""
+    if block_size <= 0:
+        raise AssertionError("block_size must be > 0")
+    axes = _axes_list(x, axes)
+    if len(axes) == 1:
+        scale, _ = _mx_launch(x, axes, block_size, quant_max, pot, scale_qmap, global_scale, None, False)
+        return scale
+    a = x.contiguous()
+    lib_ = load()
+    for ax in axes:
+        outer = math.prod(a.shape[:ax])
+        inner = math.prod(a.shape[ax + 1:])
+        shape = list(a.shape)
+        shape[ax] = -(-shape[ax] // block_size)
+        out = torch.empty(shape, dtype=a.dtype, device=a.device)
+        _lib.check(lib_.vh_block_amax(ptr(a), dtype_code(a.dtype), outer, a.shape[ax], inner, block_size, ptr(out),
+                                      ctypes.c_void_p(stream_of(x))), "vh_block_amax")
+        a = out
+    scale, _ = _mx_launch(a, [a.dim() - 1], 1, quant_max, pot, scale_qmap, global_scale, None, False)
+    return scale
+
+
 def _calculate_mx_qparam_cuda(input, axes, block_size, quant_max, force_scale_power_of_two=False,
                               scale_qmap=None, global_scale=None):
     _require_gpu(input, scale_qmap, global_scale)
-    scale, _ = _mx_launch(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, global_scale,
-                          None, False)
-    return scale
+    return _mx_scale(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, global_scale)
 
 
 cuda_kernel("calculate_mx_qparam")(_calculate_mx_qparam_cuda)
@@ -304,27 +482,35 @@ cuda_kernel("calculate_mx_qparam")(_calculate_mx_qparam_cuda)
 @fake_kernel("calculate_mx_qparam")
 def _calculate_mx_qparam_fake(input, axes, block_size, quant_max, force_scale_power_of_two=False,
                               scale_qmap=None, global_scale=None):
-    axes = [axes] if isinstance(axes, int) else list(axes)
-    ax = axes[0] % input.dim()
-    return input.new_empty(_scale_shape(input, ax, block_size))
+    return input.new_empty(_scale_shape_axes(input, axes, block_size))
+
+
+def _scale_shape_axes(x, axes, block_size):
+    shape = list(x.shape)
+    for ax in _axes_list(x, axes):
+        shape[ax] = -(-shape[ax] // block_size)
+    return shape
 
 
 def _quantize_mx_cuda(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
                       scale_qmap=None, output_code=None, seed=None, global_scale=None):
-    _require_gpu(input, qmap, scale_qmap, global_scale, seed)
+    _require_gpu(input, qmap, scale_qmap, global_scale, seed, output_code)
+    if seed is None and _is_table(qmap) and len(_axes_list(input, axes)) == 1:
+        # one pass: block scales and codes
+        return _mx_launch(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, global_scale,
+                          qmap, True)
+    # ops/quantized.py:1097-1115: the block scales, then quantize (with the
+    # seed, against the codebook, or per block over several axes)
+    if global_scale is not None:
+        raise NotImplementedError("quantized_ops.quantize_mx: a global scale with stochastic rounding, a codebook "
+                                  "or several block axes is not supported on the GPU")
+    scale = _mx_scale(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, None)
+    cdt = _quantize_dtype(input, scale, None)
     if seed is not None:
-        # ops/quantized.py:1097-1115: the block scales, then quantize with the seed
-        if global_scale is not None:
-            raise NotImplementedError("quantized_ops.quantize_mx: stochastic rounding with a global scale is not "
-                                      "supported on the GPU")
-        scale, _ = _mx_launch(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, None, None,
-                              False)
-        cdt = _quantize_dtype(input, scale, None)
         return scale, _quantize_sr(input, scale, None, block_size, qmap, seed, cdt)
-    if not _is_table(qmap):
-        raise NotImplementedError("quantized_ops.quantize_mx: codebook (searchsorted) maps are not supported yet")
-    return _mx_launch(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, global_scale, qmap,
-                      True)
+    if _is_table(qmap):
+        return scale, _elementwise("quantize", input, scale, None, block_size, cdt, _fmt_of(qmap).fmt, None, cdt)
+    return scale, _encode_cuda(input, scale, None, block_size, cdt, qmap, output_code)
 
 
 cuda_kernel("quantize_mx")(_quantize_mx_cuda)
@@ -333,9 +519,7 @@ cuda_kernel("quantize_mx")(_quantize_mx_cuda)
 @fake_kernel("quantize_mx")
 def _quantize_mx_fake(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
                       scale_qmap=None, output_code=None, seed=None, global_scale=None):
-    axes = [axes] if isinstance(axes, int) else list(axes)
-    ax = axes[0] % input.dim()
-    return input.new_empty(_scale_shape(input, ax, block_size)), torch.empty_like(input)
+    return input.new_empty(_scale_shape_axes(input, axes, block_size)), torch.empty_like(input)
 
 
 def _quantize_affine_cuda(input, qmap, axes, block_size, quant_min, quant_max, scale_qmap=None):
@@ -344,20 +528,23 @@ def _quantize_affine_cuda(input, qmap, axes, block_size, quant_min, quant_max, s
         raise AssertionError("block_size must be > 0")
     if len(axes) != 1:
         raise ValueError("quantize_affine takes exactly one axis")
-    if not _is_table(qmap):
-        raise NotImplementedError("quantized_ops.quantize_affine: codebook maps are not supported yet")
     xc, ax, outer, L, inner = _block_view(input, axes)
     cdt = xc.dtype
     sshape = _scale_shape(xc, ax, block_size)
     scale = torch.empty(sshape, dtype=cdt, device=input.device)
     zp = torch.empty(sshape, dtype=cdt, device=input.device)
-    codes = torch.empty_like(xc)
+    table = _is_table(qmap)
+    codes = torch.empty_like(xc) if table else None
     sc = _fmt_of(scale_qmap) if scale_qmap is not None else None
-    ec = _fmt_of(qmap)
+    ec = _fmt_of(qmap) if table else None
     st = load().vh_quantize_affine(ptr(xc), dtype_code(cdt), outer, L, inner, block_size, float(quant_min),
                                    float(quant_max), _fmt_ref(sc), _fmt_ref(ec), ptr(scale), ptr(zp), ptr(codes),
                                    dtype_code(cdt), ctypes.c_void_p(stream_of(input)))
     _lib.check(st, "vh_quantize_affine")
+    if not table:
+        # a codebook: quantize (ops/quantized.py:1282) searches it with the
+        # block's scale and zero point
+        codes = _encode_cuda(xc, scale, zp, block_size, _quantize_dtype(xc, scale, zp), qmap, None)
     return scale, zp, codes
 
 
@@ -400,13 +587,12 @@ def decode_table(code: torch.Tensor) -> torch.Tensor:
 
 def _dequantize_mx_cuda(input, scale, block_size, code=None, global_scale=None):
     _require_gpu(input, scale, code, global_scale)
-    if code is not None and code.dim() != 1:
-        raise NotImplementedError("dequantize_mx: region (per-head) codebooks are not supported yet")
-    fi = _fmt_of(decode_table(code)).fmt if code is not None else None
-    dec_dtype = input.dtype if code is None else input.dtype
-    probe = torch.empty([1] * max(input.dim(), 1), dtype=dec_dtype, device="meta")
-    cdt = torch.result_type(probe, scale)
-    out = _elementwise("dequantize", input, scale, None, block_size, cdt, fi, None, cdt)
+    if code is not None:
+        out = decode_codes(input, code, scale, block_size)
+    else:
+        probe = torch.empty([1] * max(input.dim(), 1), dtype=input.dtype, device="meta")
+        cdt = torch.result_type(probe, scale)
+        out = _elementwise("dequantize", input, scale, None, block_size, cdt, None, None, cdt)
     if global_scale is not None:
         out = out * global_scale
     return out
