@@ -85,10 +85,16 @@ def capture(fn):
     return g
 
 
-def time_graph(g, reps):
-    """Average ms of one replay, from HIP events on the current stream."""
+def time_graph(g, reps, warm_s=0.5):
+    """Average ms of one replay, from HIP events on the current stream, after
+    replaying for ``warm_s`` seconds: the clock settles under a sustained
+    load, and a short window would time its transient instead."""
+    t_end = time.perf_counter() + warm_s
     g.replay()
     torch.cuda.synchronize()
+    while time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(reps):
@@ -131,19 +137,12 @@ def gpu_bench(args):
             gemm.linear_fp8(L["xq"], L["wq"], L["s"], out=L["y"])
 
     g_step = capture(step)
-    for _ in range(args.warmup):
-        g_step.replay()
-    torch.cuda.synchronize()
-    # Timed region: K whole steps, bracketed by synchronisation.
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        g_step.replay()
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
     # Per-kernel average launch durations (HIP events around graph replays of
-    # back-to-back launches).  Quantize inputs rotate over more than the
-    # 256 MB Infinity Cache so HBM, not the cache, serves them.
+    # back-to-back launches), measured first: they also bring the GPU to the
+    # clock it holds under sustained load before the steps are timed.
+    # Quantize inputs rotate over more than the 256 MB Infinity Cache so HBM,
+    # not the cache, serves them.
     R = 10
     g_ms, q_ms = [], []
     for L in layers:
@@ -156,6 +155,16 @@ def gpu_bench(args):
         q_ms.append(time_graph(gq, 5) / nbuf)
         del xs, gq, gg
     torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        g_step.replay()
+    torch.cuda.synchronize()
+    # Timed region: K whole steps, bracketed by synchronisation.
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        g_step.replay()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
     flops = [2.0 * M * L["N"] * L["K"] for L in layers]
     qbytes = [M * L["K"] * 3.0 for L in layers]  # bf16 in + 1-byte codes out
@@ -223,7 +232,7 @@ def bench_config1(args):
         mm()
 
     gs = capture(step)
-    ms = time_graph(gs, max(args.steps, 20))
+    ms = time_graph(gs, max(args.steps, 20), warm_s=0.0)
     gq = capture(lambda: [quant() for _ in range(20)])
     q_ms = time_graph(gq, 5) / 20
     gm = capture(lambda: [mm() for _ in range(20)])

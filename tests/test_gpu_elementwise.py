@@ -145,6 +145,24 @@ def test_quantize_packed_e4m3_every_bf16_pattern(scale):
     assert torch.equal(got[fin], ref[fin])
 
 
+def test_quantize_packed_e4m3_large_ragged():
+    """The per-tensor E4M3 fast path on a tensor large enough for its
+    8-groups-per-thread variant (over 2^24 elements), with a last workgroup
+    that is partly past the end: every bf16 pattern 257 times, then 40 more."""
+    from voyager_amd import packed
+
+    pat = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    s = torch.tensor(0.0173, dtype=torch.bfloat16)
+    tab = T.quantization_map("fp8_e4m3")
+    exp = packed.quantize_packed(pat.cuda(), s.cuda(), tab.cuda()).cpu()
+    back = packed.unpack_codes(exp.cuda(), tab.cuda()).cpu()
+    assert_same_bits(back, O.quantize(pat, s, qmap=tab), "patterns")
+    x = torch.cat([pat.cuda().repeat(257), pat[:40].cuda()])
+    got = packed.quantize_packed(x, s.cuda(), tab.cuda())
+    assert torch.equal(got[: 257 * 65536].view(257, 65536), exp.cuda().expand(257, 65536))
+    assert torch.equal(got[257 * 65536:].cpu(), exp[:40])
+
+
 @pytest.mark.parametrize("dtype", ["posit8_1", "posit8_0", "posit8_2", "posit16_1"])
 @pytest.mark.parametrize("scale", [1.0, 0.0173, 3.5, 2.0**-130, 1.5e38])
 def test_quantize_posit_every_bf16_pattern(dtype, scale):

@@ -268,20 +268,38 @@ VH_DEV uint32_t pk_max_u16(uint32_t a, uint32_t b) {
 // packed 16-bit extremes flag the rare cases this shortcut cannot decide --
 // a product within 4 fp32 ulps of a bf16 rounding midpoint, a NaN -- and the
 // thread then redoes its elements with the correctly rounded division.
+// Workgroup b converts the U * 256 consecutive 16-byte groups from
+// b * U * 256 (one contiguous run of memory per workgroup, every load issued
+// before the first use): on MI355X this streams 2048 x 4096 bf16 at 4.8 TB/s
+// with no arithmetic, against 4.1 TB/s for a grid-stride loop.
+template <int U>
 __global__ void __launch_bounds__(256)
 k_quantize_e4m3_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp, int sdt, uint8_t* __restrict__ out) {
-  const float s = load_any(sp, sdt, 0);
-  const float as = fabsf(s);
-  const bool fast_scale = as >= 0x1p-126f && as <= 0x1p126f;
-  const float r = __builtin_amdgcn_rcpf(s);
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t v0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v0 < nvec; v0 += stride * UNROLL) {
+  constexpr int64_t stride = 256;
+  {
+    const int64_t v0 = (int64_t)blockIdx.x * (U * 256) + threadIdx.x;
+    constexpr int UNROLL = U;
+    // the element loads go out first and unconditionally (a group past the
+    // end reloads the last one and is not stored); the scale is read after
+    // them through the scalar cache (a bfloat16 scale as the aligned 4-byte
+    // word that holds it, which lies in the same mapped allocation), so its
+    // latency overlaps theirs and no wait for it holds them back
     uint4 raw[UNROLL];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int64_t v = v0 + u * stride;
-      raw[u] = v < nvec ? ld_stream16(x + v * 8) : make_uint4(0, 0, 0, 0);
+      raw[u] = ld_stream16(x + (v < nvec ? v : nvec - 1) * 8);
     }
+    asm volatile("" ::: "memory");
+    typedef const __attribute__((address_space(4))) uint32_t cword;  // constant space: a scalar load
+    const uintptr_t a = (uintptr_t)sp;
+    const uint32_t w = *(cword*)(a & ~(uintptr_t)3);
+    const uint32_t h = (a & 2) ? (w >> 16) : (w & 0xffffu);
+    const float s = sdt == VH_F32 ? __uint_as_float(w) : sdt == VH_F16 ? __half2float(__ushort_as_half((unsigned short)h))
+                                                                     : bf2f(h);
+    const float as = fabsf(s);
+    const bool fast_scale = as >= 0x1p-126f && as <= 0x1p126f;
+    const float r = __builtin_amdgcn_rcpf(s);
     uint2 res[UNROLL];
     uint32_t mn = 0xffffffffu, mx = 0u;
 #pragma unroll
@@ -727,6 +745,7 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
   if (x_dtype == VH_BF16 && compute_dtype == VH_BF16 && sp.ptr && sp.scalar && !zp.ptr && n % 8 == 0 && aligned &&
       (out_dtype == VH_U8 || out_dtype == VH_BF16)) {
     const int64_t nvec = n / 8;
+    VH_REQUIRE(nvec / 1024 < (1ll << 31), "vh_quantize: tensor too large");
     int64_t blocks = (nvec + 256 * UNROLL - 1) / (256 * UNROLL);
     if (blocks > 8192) blocks = 8192;
     int lo = 0, hi = 0;
@@ -741,8 +760,15 @@ extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape,
         if constexpr (K == K_NONE || K == K_IDENTITY || K == K_LUT) {
           return (int)VH_EINVAL;  // unreachable: checked by packable()
         } else if constexpr (K == K_E4M3) {
-          hipLaunchKernelGGL(k_quantize_e4m3_pt, dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)x, nvec,
-                             sp.ptr, sp.dtype, (uint8_t*)out);
+          // 4 groups per thread up to 2^21 groups, 8 beyond (measured best for
+          // the 16.8 MB and 58.7 MB inputs)
+          if (nvec <= (1ll << 21)) {
+            hipLaunchKernelGGL(k_quantize_e4m3_pt<4>, dim3((unsigned)((nvec + 1023) / 1024)), dim3(256), 0, st,
+                               (const uint16_t*)x, nvec, sp.ptr, sp.dtype, (uint8_t*)out);
+          } else {
+            hipLaunchKernelGGL(k_quantize_e4m3_pt<8>, dim3((unsigned)((nvec + 2047) / 2048)), dim3(256), 0, st,
+                               (const uint16_t*)x, nvec, sp.ptr, sp.dtype, (uint8_t*)out);
+          }
         } else if (K == K_POSIT && posit_table_range(f, true, &lo, &hi, &tab_bytes)) {
           hipLaunchKernelGGL(k_quantize_posit_tab<true>, dim3((unsigned)tab_blocks), dim3(TAB_THREADS), tab_bytes, st,
                              (const uint16_t*)x, nvec, sp.ptr, sp.dtype, f, lo, hi, out);
