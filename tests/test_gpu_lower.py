@@ -1,11 +1,15 @@
 """voyager_amd.lower on graphs laid out as convert_pt2e leaves them: each
 site kind is checked with check_sites, lowered, and its output compared with
-the converted graph's (1e-2 max-abs-normalized, the GEMM tolerance)."""
+the same converted graph run by the oracle on the CPU (1e-2
+max-abs-normalized, the GEMM tolerance)."""
+
+import copy
 
 import pytest
 import torch
 
 import voyager_amd.library  # noqa: F401  (defines quantized_ops)
+from convert_helpers import OracleRun
 from helpers import max_rel_err
 from oracle import ops as O
 from oracle import tables as T
@@ -62,9 +66,14 @@ def _kinds(gm):
 
 
 def _check_and_lower(gm, x, kind):
+    """Checks the site, lowers it, and compares both the converted graph on
+    the GPU and the lowered one with the same graph run by the oracle on the
+    CPU."""
     from voyager_amd import lower
 
+    exp = OracleRun(copy.deepcopy(gm).cpu()).run(x.cpu())
     ref = gm(x)
+    assert max_rel_err(ref, exp) < TOL
     results, out = lower.check_sites(gm, (x,))
     assert torch.equal(out, ref)
     (res,) = results.values()
@@ -75,6 +84,7 @@ def _check_and_lower(gm, x, kind):
     assert torch.ops.aten.linear.default not in targets and Q.linear_mx.default not in targets
     got = gm(x)
     assert got.shape == ref.shape and got.dtype == ref.dtype
+    assert max_rel_err(got, exp) < TOL
     assert max_rel_err(got, ref) < TOL
     return report
 
