@@ -151,3 +151,27 @@ def test_matmul_mx_with_region_codebook_operand():
     exp = O.matmul_mx(xi, w, input_code=code).float()
     got = Q.matmul_mx(xi.cuda(), w.cuda(), input_code=code.cuda()).float().cpu()
     assert torch.allclose(got, exp, rtol=1e-2, atol=1e-2 * exp.abs().max().item())
+
+
+@pytest.mark.parametrize("case", ["seed", "codebook", "two_axes"])
+def test_quantize_mx_global_scale_unfused(case):
+    """quantize_mx with a 0-d global scale on the paths that quantize after
+    the block scales (stochastic rounding, a codebook, blocks over two axes):
+    scales and codes bit-exact, the elements divided by scale * global_scale
+    as eager torch forms it."""
+    g = torch.Generator().manual_seed(29)
+    x = (torch.randn(24, 256, generator=g) * 300).bfloat16()
+    e4m3 = T.quantization_map("fp8_e4m3")
+    gs = (x.float().abs().amax() / (6.0 * 448.0)).to(torch.float32)
+    axes, qmap, seed, oc = [-1], T.quantization_map("fp4_e2m1"), None, None
+    if case == "seed":
+        seed = torch.tensor(1234, dtype=torch.int64)
+    elif case == "codebook":
+        qmap = torch.tensor([-6.0, -3.0, -1.0, 0.0, 1.0, 3.0, 6.0])
+    else:
+        axes = [0, 1]
+    es, ec = O.quantize_mx(x, qmap, axes, 16, 6.0, False, e4m3, oc, seed, gs)
+    gs_, gc = Q.quantize_mx(x.cuda(), qmap.cuda(), axes, 16, 6.0, False, e4m3.cuda(), oc,
+                            seed.cuda() if seed is not None else None, gs.cuda())
+    assert_same_bits(gs_, es, f"{case} scales")
+    assert_same_bits(gc, ec, f"{case} codes")

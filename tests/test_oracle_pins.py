@@ -446,3 +446,38 @@ def test_kivi_round_trip_float64():
         deq = D.kivi_dequantize(c, s, z, axis).double().numpy()
         ref = bf(bf(codes - rep(zp)) * rep(sc))
         assert np.allclose(deq, ref, rtol=0, atol=0)
+
+
+def test_nvfp4_global_scale_round_trip():
+    """The NVFP4 branch of quantize_mx / dequantize_mx (a 0-d global scale
+    divided out of the block scale before its E4M3 map and multiplied back
+    into the elements' divisor and into the dequantized values), pinned by
+    what the two-level scheme guarantees rather than by its formula: with a
+    global scale far from 1, the returned block scales lie on the E4M3 grid
+    and near amax / 6 / gs, every code lies on the E2M1 grid, and the round
+    trip recovers each element to within half an E2M1 step at that block's
+    scale (or saturates at 6 steps) -- dropping gs from the divisor, from the
+    scale or from the dequantize misses all of these by the factor gs."""
+    g = torch.Generator().manual_seed(41)
+    x = (torch.randn(32, 128, generator=g) * torch.exp(torch.randn(32, 1, generator=g) * 2) * 5e4).bfloat16()
+    fp4, e4m3 = T.quantization_map("fp4_e2m1"), T.quantization_map("fp8_e4m3")
+    gs = (x.float().abs().amax() / (6.0 * 448.0)).to(torch.float32)
+    assert gs > 10.0  # far from 1
+    scale, codes = O.quantize_mx(x, fp4, [-1], 16, 6.0, False, e4m3, None, None, gs)
+    grid4 = {v * s for v in (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0) for s in (1.0, -1.0)}
+    assert set(codes.float().unique().tolist()) <= grid4
+    e4 = set(e4m3.float().unique().tolist())
+    assert set(scale.float().unique().tolist()) <= e4
+    xb = x.float().view(32, 8, 16)
+    amax = xb.abs().amax(-1)
+    s = scale.float()
+    # the E4M3 rounding of amax / 6 / gs (relative step 2**-3; subnormal scales excluded)
+    ref = amax / 6.0 / gs
+    big = ref > 2.0**-6
+    assert torch.all((s[big] - ref[big]).abs() <= ref[big] * 2.0**-3)
+    back = O.dequantize_mx(codes, scale, 16, None, gs).float().view(32, 8, 16)
+    step = s.unsqueeze(-1) * gs  # one unit of E2M1 at this block's scale
+    err = (back - xb).abs()
+    # nearest E2M1 value: within a half of the local gap (gap 2 between 4 and 6), or saturation at 6
+    tol = torch.where(xb.abs() > 6 * step, xb.abs() - 6 * step, step) + step * 2.0**-6
+    assert torch.all(err[big.unsqueeze(-1).expand_as(err)] <= tol[big.unsqueeze(-1).expand_as(tol)])

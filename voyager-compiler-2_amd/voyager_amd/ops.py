@@ -500,17 +500,20 @@ def _quantize_mx_cuda(input, qmap, axes, block_size, quant_max, force_scale_powe
         return _mx_launch(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, global_scale,
                           qmap, True)
     # ops/quantized.py:1097-1115: the block scales, then quantize (with the
-    # seed, against the codebook, or per block over several axes)
+    # seed, against the codebook, or per block over several axes) by
+    # scale * global_scale, which the dequantize kernel forms as eager torch
+    # does (the 0-d global scale at its own precision, one rounding)
+    scale = _mx_scale(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, global_scale)
+    el = scale
     if global_scale is not None:
-        raise NotImplementedError("quantized_ops.quantize_mx: a global scale with stochastic rounding, a codebook "
-                                  "or several block axes is not supported on the GPU")
-    scale = _mx_scale(input, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap, None)
-    cdt = _quantize_dtype(input, scale, None)
+        el = _elementwise("dequantize", scale, global_scale.reshape(()), None, None, scale.dtype, None, None,
+                          scale.dtype)
+    cdt = _quantize_dtype(input, el, None)
     if seed is not None:
-        return scale, _quantize_sr(input, scale, None, block_size, qmap, seed, cdt)
+        return scale, _quantize_sr(input, el, None, block_size, qmap, seed, cdt)
     if _is_table(qmap):
-        return scale, _elementwise("quantize", input, scale, None, block_size, cdt, _fmt_of(qmap).fmt, None, cdt)
-    return scale, _encode_cuda(input, scale, None, block_size, cdt, qmap, output_code)
+        return scale, _elementwise("quantize", input, el, None, block_size, cdt, _fmt_of(qmap).fmt, None, cdt)
+    return scale, _encode_cuda(input, el, None, block_size, cdt, qmap, output_code)
 
 
 cuda_kernel("quantize_mx")(_quantize_mx_cuda)
