@@ -302,6 +302,28 @@ int vh_gemm_plan(const vh_gemm_desc* desc, int32_t* family, int32_t* tile, int32
  * in the low nibble of byte j, column j + 8 in its high nibble).  Needs
  * N % 16 == 0 and K % 64 == 0.  Replaces the weight baking of
  * quantization/quantize_pt2e.py:819-828 for this format. */
+/* MX-int8 linear at small M on exact fp16 operands.  vh_quantize_mx8_f16:
+ * quantize_mx(x, int8, [-1], 16, 127, force_scale_power_of_two=True) of each
+ * bf16 row of x [M, K] (ops/quantized.py:1070-1115), written decoded as
+ * code * 2**(e - E_row) in fp16 (exact) with E_row, the row's largest finite
+ * block exponent, in ex [M]; blocks more than 24 binades under E_row are
+ * flushed to zero, blocks with a non-finite scale hold code * scale.
+ * vh_mx8_bake_f16: packed weights (int8 codes [N, K], scale bytes
+ * 2**(byte - scale_bias) per 16, 255 = inf) the same way, E per row in ew
+ * [N] (weight baking, quantization/quantize_pt2e.py:819-828).
+ * vh_gemm_mx8_f16: y = epilogue(sum_k x[m,k] w[n,k] * 2**(ex[m] + ew[n])),
+ * the linear_mx GEMM (ops/quantized.py:651-723), as an fp16 GEMM over
+ * `splits` K ranges into float32 partials `part` (splits * M * N floats)
+ * and one reduction; tile 0: 128x128, 1: 64x128, 2: 128x64, 3: 256x128.  No
+ * reference counterpart for the operand form: it is this library's
+ * small-M layout of the same values. */
+int vh_quantize_mx8_f16(const uint16_t* x, int64_t M, int64_t K, uint16_t* out, int32_t* ex, vh_stream_t stream);
+int vh_mx8_bake_f16(const int8_t* codes, const uint8_t* scale, int32_t scale_bias, int64_t N, int64_t K,
+                    uint16_t* out, int32_t* ew, vh_stream_t stream);
+int vh_gemm_mx8_f16(const uint16_t* x, const int32_t* ex, const uint16_t* w, const int32_t* ew, int64_t M,
+                    int64_t N, int64_t K, const vh_epilogue* epi, void* y, int64_t ldy, float* part,
+                    int64_t part_bytes, int32_t splits, int32_t tile, vh_stream_t stream);
+
 int vh_pack_nf4(const uint8_t* codes, int64_t N, int64_t K, uint8_t* out, vh_stream_t stream);
 
 /* y[M, N] = sum over blocks b of s_x[m, b] * s_w[n, b] * sum_k Lx[m, k] Lw[n, k]

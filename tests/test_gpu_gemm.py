@@ -394,3 +394,82 @@ def test_gemm_float32_results(M, N, K, batch):
     ref = (a.double() @ b.double().mT) * 0.75 + bias.double()
     assert got.dtype == torch.float32 and got.shape == ref.shape
     assert max_rel_err(got, ref) < 1e-5
+
+
+def _mx8_f16_decoded(x16, ex):
+    return x16.cpu().double() * torch.pow(2.0, ex.cpu().double()).unsqueeze(1)
+
+
+@pytest.mark.parametrize("M,K", [(256, 4096), (7, 1024), (300, 640)])
+def test_quantize_mx8_f16_exact(M, K):
+    """The activation quantize of the small-M MX-int8 path: each row's fp16
+    values times 2**E_row are exactly the reference's decoded quantize_mx
+    (codes times block scales), NaN and infinities included."""
+    from voyager_amd import gemm
+
+    g = torch.Generator().manual_seed(M + K)
+    x = (torch.randn(M, K, generator=g) * torch.exp(torch.randn(M, 1, generator=g) * 3)).bfloat16()
+    # a NaN block takes scale 1 (exponent 0) and sets its row's E; keep the
+    # row's other blocks within 24 binades of it, where nothing is flushed
+    x[0] = torch.randn(K, generator=g).bfloat16()
+    x[0, :3] = torch.tensor([float("nan"), float("inf"), -1.0])
+    x[1, 16:32] = 0.0
+    tab = T.quantization_map("int8")
+    s, c = O.quantize_mx(x, tab, [-1], 16, 127.0, True)
+    exp = O.dequantize_mx(c, s, 16).double()
+    x16, ex = gemm.quantize_mx8_f16(x.cuda())
+    got = _mx8_f16_decoded(x16, ex)
+    same = (got == exp) | (torch.isnan(got) & torch.isnan(exp))
+    assert bool(same.all()), (~same).nonzero()[:5]
+
+
+def test_mx8_f16_bake_flushes_only_far_blocks():
+    """Weight baking: exact where a block is within 24 binades of its row's
+    largest, zero below."""
+    from voyager_amd import gemm, packed
+
+    N, K = 64, 512
+    g = torch.Generator().manual_seed(5)
+    ew = torch.randint(-40, 1, (N, K // 16), generator=g)
+    ew[:, 0] = 0
+    w = (torch.randn(N, K, generator=g) * torch.pow(2.0, ew.float()).repeat_interleave(16, dim=1)).bfloat16()
+    tab = T.quantization_map("int8")
+    pw = packed.quantize_mx_packed(w.cuda(), tab.cuda(), [-1], 16, 127.0, True)
+    s, c = O.quantize_mx(w, tab, [-1], 16, 127.0, True)
+    exp = O.dequantize_mx(c, s, 16).double()
+    bw = gemm.bake_mx8_f16(pw.codes.view(torch.int8), pw.scale, pw.bias)
+    got = _mx8_f16_decoded(bw.w, bw.e)
+    e_blk = torch.floor(torch.log2(exp.abs().view(N, K // 16, 16).amax(-1).clamp_min(1e-300))).repeat_interleave(16, 1)
+    far = e_blk < (e_blk.amax(1, keepdim=True) - 24 + 1)  # within the flush margin of a block's code range
+    assert torch.equal(got[~far], exp[~far])
+    assert bool((got[far].abs() <= exp[far].abs()).all())
+
+
+@pytest.mark.parametrize("M,N,K,tile,splits", [(256, 4096, 4096, -1, 0), (256, 4096, 4096, 1, 2),
+                                               (256, 4096, 4096, 2, 2), (256, 4096, 4096, 3, 8),
+                                               (33, 520, 1024, -1, 0), (130, 264, 768, 0, 3)])
+def test_linear_mx8_f16(M, N, K, tile, splits):
+    """The small-M MX-int8 linear on exact fp16 operands against the exact
+    float64 product of the reference's decoded operands, bf16 and fp32
+    results (alpha and bias in the reduction's epilogue)."""
+    from voyager_amd import gemm, packed
+
+    tab = T.quantization_map("int8").cuda()
+    x = _rand((M, K), 40).cuda()
+    w = _rand((N, K), 41, 0.02).cuda()
+    px = packed.quantize_mx_packed(x, tab, [-1], 16, 127.0, True)
+    pw = packed.quantize_mx_packed(w, tab, [-1], 16, 127.0, True)
+    ref = _deq_mxint8(px) @ _deq_mxint8(pw).T
+    bw = gemm.bake_mx8_f16(pw.codes.view(torch.int8), pw.scale, pw.bias)
+    x16, ex = gemm.quantize_mx8_f16(x)
+    got = gemm.linear_mx8_f16(x16, ex, bw, tile=tile, splits=splits)
+    assert got.dtype == torch.bfloat16
+    assert max_rel_err(got, ref) < TOL
+    alpha = torch.tensor(0.75, device="cuda")
+    bias = _rand((N,), 42).cuda()
+    got32 = gemm.linear_mx8_f16(x16, ex, bw, out_dtype=torch.float32, bias=bias, alpha=alpha, tile=tile,
+                                splits=splits)
+    assert max_rel_err(got32, ref * 0.75 + bias.cpu().double()) < 1e-5
+    # the packed path's result agrees
+    old = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias)
+    assert max_rel_err(got, old) < TOL

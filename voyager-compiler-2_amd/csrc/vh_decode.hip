@@ -165,6 +165,117 @@ k_rmsnorm_mx8(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, in
   }
 }
 
+// ------------------------------------------------ MX-int8 as exact fp16 rows
+// The operands of vh_gemm_mx8_f16: an MX-int8 row (int8 codes, a power-of-
+// two scale 2**e per 16 elements) as code * 2**(e - E) in fp16, E the row's
+// largest finite block exponent -- exact, since an 8-bit code at a power of
+// two down to 2**-24 is an fp16 value.  Blocks more than 24 binades under E
+// are flushed: their products lie below the float32 resolution of the row's
+// largest ones.  A block whose scale is not finite writes code * scale, as
+// the reference's decode does (infinities and NaN).
+constexpr int F16_FLUSH = -24;
+
+VH_DEV _Float16 rebased_f16(float code, int e, bool finite, float s, int E) {
+  if (!finite) return (_Float16)(code * s);
+  const int d = e - E;
+  return (_Float16)(d >= F16_FLUSH ? ldexpf(code, d) : code * 0.0f);
+}
+
+VH_DEV int block_max_int(int v, int* s_red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int r = max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3]));
+  __syncthreads();
+  return r;
+}
+
+// quantize_mx(x, int8, [-1], 16, 127, force_scale_power_of_two=True) of each
+// bf16 row (ops/quantized.py:1070-1115; codes and scales as mx8_scale /
+// mx8_fq form them), written as the exact fp16 row above with E in ex.  One
+// workgroup per row: the blocks' exponents, their maximum, then the codes.
+__global__ void __launch_bounds__(256) k_quantize_mx8_f16(const uint16_t* __restrict__ x, int64_t K,
+                                                          _Float16* __restrict__ out, int32_t* __restrict__ ex) {
+  __shared__ int s_red[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * K;
+  const int64_t nb = K / 16;
+  int emax = INT_MIN;
+  for (int64_t b = threadIdx.x; b < nb; b += 256) {
+    const uint4* p = (const uint4*)(xr + b * 16);
+    const uint4 v0 = p[0], v1 = p[1];
+    const uint32_t wv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = nmax(amax, nmax(fabsf(bf2f(wv[j] & 0xffffu)), fabsf(bf2f(wv[j] >> 16))));
+    const Mx8Scale sc = mx8_scale(amax);
+    if (sc.pow2) emax = max(emax, sc.e);
+  }
+  int E = block_max_int(emax, s_red);
+  if (E == INT_MIN) E = 0;
+  for (int64_t b = threadIdx.x; b < nb; b += 256) {
+    const uint4* p = (const uint4*)(xr + b * 16);
+    const uint4 v0 = p[0], v1 = p[1];
+    const uint32_t wv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float xv[16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      xv[2 * j] = bf2f(wv[j] & 0xffffu);
+      xv[2 * j + 1] = bf2f(wv[j] >> 16);
+      amax = nmax(amax, nmax(fabsf(xv[2 * j]), fabsf(xv[2 * j + 1])));
+    }
+    const Mx8Scale sc = mx8_scale(amax);
+    f16x8 o[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float q = rbf(sc.pow2 ? ldexpf(xv[j], -sc.e) : xv[j] / sc.s);
+      if (!isnan_f(q)) q = fminf(fmaxf(rintf(q), -128.0f), 127.0f);
+      o[j >> 3][j & 7] = rebased_f16(q, sc.e, sc.pow2, sc.s, E);
+    }
+    f16x8* dst = (f16x8*)(out + row * K + b * 16);
+    dst[0] = o[0];
+    dst[1] = o[1];
+  }
+  if (threadIdx.x == 0) ex[row] = E;
+}
+
+// Packed MX-int8 weights (int8 codes [N, K], scale bytes 2**(byte - bias)
+// [N, K / 16], 255 = inf) as exact fp16 rows with their E.  One workgroup
+// per row.
+__global__ void __launch_bounds__(256) k_mx8_bake_f16(const int8_t* __restrict__ codes, const uint8_t* __restrict__ sb,
+                                                      int bias, int64_t K, _Float16* __restrict__ out,
+                                                      int32_t* __restrict__ ew) {
+  __shared__ int s_red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t nb = K / 16;
+  int emax = INT_MIN;
+  for (int64_t b = threadIdx.x; b < nb; b += 256) {
+    const int byte = sb[row * nb + b];
+    if (byte != 255) emax = max(emax, byte - bias);
+  }
+  int E = block_max_int(emax, s_red);
+  if (E == INT_MIN) E = 0;
+  for (int64_t b = threadIdx.x; b < nb; b += 256) {
+    const int byte = sb[row * nb + b];
+    const bool finite = byte != 255;
+    const int4* p = (const int4*)(codes + row * K + b * 16);
+    const int4 c = p[0];
+    const uint32_t cw[4] = {(uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w};
+    f16x8 o[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float code = (float)(int8_t)(cw[j >> 2] >> (8 * (j & 3)));
+      o[j >> 3][j & 7] = rebased_f16(code, byte - bias, finite, __builtin_inff(), E);
+    }
+    f16x8* dst = (f16x8*)(out + row * K + b * 16);
+    dst[0] = o[0];
+    dst[1] = o[1];
+  }
+  if (threadIdx.x == 0) ew[row] = E;
+}
+
 // ------------------------------------------------------------ MX-int8 GEMV
 // Baked weight layout, per 16-column tile T (K = 256 G):
 //   codes [T][K/64 step pairs][64 lanes][16 B]: bytes 0-7 step 2p, 8-15 step
@@ -1179,3 +1290,23 @@ extern "C" int vh_kivi_attention(const vh_kivi_desc* d, vh_stream_t stream) {
 }
 
 
+
+extern "C" int vh_quantize_mx8_f16(const uint16_t* x, int64_t M, int64_t K, uint16_t* out, int32_t* ex,
+                                   vh_stream_t stream) {
+  VH_REQUIRE(x && out && ex, "vh_quantize_mx8_f16: null argument");
+  VH_REQUIRE(M > 0 && K > 0 && K % 16 == 0, "vh_quantize_mx8_f16: needs K a multiple of 16");
+  VH_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0, "vh_quantize_mx8_f16: misaligned tensor");
+  hipLaunchKernelGGL(k_quantize_mx8_f16, dim3((unsigned)M), dim3(256), 0, vh::as_stream(stream), x, K,
+                     (_Float16*)out, ex);
+  return vh::check_launch("vh_quantize_mx8_f16");
+}
+
+extern "C" int vh_mx8_bake_f16(const int8_t* codes, const uint8_t* scale, int32_t scale_bias, int64_t N, int64_t K,
+                               uint16_t* out, int32_t* ew, vh_stream_t stream) {
+  VH_REQUIRE(codes && scale && out && ew, "vh_mx8_bake_f16: null argument");
+  VH_REQUIRE(N > 0 && K > 0 && K % 16 == 0, "vh_mx8_bake_f16: needs K a multiple of 16");
+  VH_REQUIRE((uintptr_t)codes % 16 == 0 && (uintptr_t)out % 16 == 0, "vh_mx8_bake_f16: misaligned tensor");
+  hipLaunchKernelGGL(k_mx8_bake_f16, dim3((unsigned)N), dim3(256), 0, vh::as_stream(stream), codes, scale, scale_bias,
+                     K, (_Float16*)out, ew);
+  return vh::check_launch("vh_mx8_bake_f16");
+}

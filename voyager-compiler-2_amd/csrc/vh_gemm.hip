@@ -30,6 +30,11 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Exact fp16 operands (vh_gemm_mx8_f16); internal to this file, not a
+// descriptor format.
+constexpr int OP_F16X = 16;
 
 constexpr int ROWB = 128;   // bytes of K per row per stage
 constexpr int ROWP = 144;   // padded LDS row pitch
@@ -962,8 +967,12 @@ __global__ void __launch_bounds__(512) k_gemm_mxi8_ws(GemmArgs g, int64_t kc, fl
 // C = epilogue(sum over z of part[z]) for split-K partials [S][M][N] (fp32),
 // summed in split order; four consecutive elements of a row per thread
 // (N % 4 == 0).
+// ea / eb (or null): per row of A and column of B, a power of two the sum
+// is multiplied by before the epilogue (the exact fp16 operands' rebasing).
 __global__ void __launch_bounds__(256) k_split_reduce(const float* __restrict__ part, int S, int64_t M, int64_t N,
-                                                      vh_epilogue e, void* __restrict__ C, int64_t ldc) {
+                                                      vh_epilogue e, void* __restrict__ C, int64_t ldc,
+                                                      const int32_t* __restrict__ ea = nullptr,
+                                                      const int32_t* __restrict__ eb = nullptr) {
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   const int64_t MN = M * N;
   if (i >= MN) return;
@@ -976,6 +985,13 @@ __global__ void __launch_bounds__(256) k_split_reduce(const float* __restrict__ 
     v.w += t.w;
   }
   const int64_t row = i / N, col = i % N;
+  if (ea) {
+    const int r = ea[row];
+    v.x = ldexpf(v.x, r + eb[col]);
+    v.y = ldexpf(v.y, r + eb[col + 1]);
+    v.z = ldexpf(v.z, r + eb[col + 2]);
+    v.w = ldexpf(v.w, r + eb[col + 3]);
+  }
   const float sc = epi_scale(e);
   const float r0 = epi_value(e, v.x, sc, epi_bias(e, col));
   const float r1 = epi_value(e, v.y, sc, epi_bias(e, col + 1));
@@ -1078,8 +1094,9 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   constexpr int L = LA + LB;
   static_assert((KS == 64 || KS == 128) && BM % 64 == 0 && BN % 32 == 0 && NS >= 2 && (NS * P) % 2 == 0,
                 "bad fp8 tile");
-  static_assert(OP == OP_FP8 || OP == OP_BF16, "fp8 or bf16 operands");
-  constexpr bool BF = OP == OP_BF16;  // a 64-byte step is 32 bf16: two 32x32x16 MFMAs
+  static_assert(OP == OP_FP8 || OP == OP_BF16 || OP == OP_F16X, "fp8, bf16 or fp16 operands");
+  // a 64-byte step is 32 two-byte elements: two 32x32x16 MFMAs
+  constexpr bool BF = OP == OP_BF16 || OP == OP_F16X;
   static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0 && TM >= 2 && TM % 2 == 0 && TN >= 1,
                 "DMA blocks must divide among the waves");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1157,8 +1174,12 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
     if constexpr (BF) {
       const int p = q % (TM * TN), i = p / TN, j = p % TN;
       const i32x4 a = q < TM * TN ? fa[i].lo : fa[i].hi, b = q < TM * TN ? fb[j].lo : fb[j].hi;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b), __builtin_bit_cast(bf16x8, a),
-                                                         acc[i][j], 0, 0, 0);
+      if constexpr (OP == OP_F16X)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a),
+                                                          acc[i][j], 0, 0, 0);
+      else
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b),
+                                                           __builtin_bit_cast(bf16x8, a), acc[i][j], 0, 0, 0);
     } else {
       const int i = q / TN, j = q % TN;
       acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
@@ -1276,7 +1297,6 @@ constexpr int MH_NS = 4;                         // raw stages in LDS
 constexpr int MH_KQ = 4 * MH_KE;                 // K granule: splits and K are multiples of it
 constexpr int MH_KC_MAX = 2048;                  // K elements per split at most (128 scale bytes per row)
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
@@ -1939,4 +1959,63 @@ extern "C" int64_t vh_gemm_workspace_bytes(const vh_gemm_desc* d) {
   int cfg, splits;
   mxi8_plan(d, cfg, splits);
   return cfg ? mxi8_workspace(d, splits) : 0;
+}
+
+// ------------------------------------------------------------ MX-int8 on exact fp16
+// linear_mx of MX-int8 operands (ops/quantized.py:651-723) at small M, with
+// both operands already decoded to exact fp16 against a power of two per row
+// of x and per column of w (vh_quantize_mx8_f16, vh_mx8_bake_f16): a plain
+// fp16 direct-to-LDS GEMM over K splits into float32 partials, then the
+// split reduction multiplies each sum by 2**(E_row + E_col) and applies the
+// epilogue.  The decode is gone from the GEMM's inner loop, which bounds the
+// kernels that decode MX-int8 codes in staging at these sizes.
+extern "C" int vh_gemm_mx8_f16(const uint16_t* x, const int32_t* ex, const uint16_t* w, const int32_t* ew, int64_t M,
+                               int64_t N, int64_t K, const vh_epilogue* epi, void* y, int64_t ldy, float* part,
+                               int64_t part_bytes, int32_t splits, int32_t tile, vh_stream_t stream) {
+  VH_REQUIRE(x && ex && w && ew && epi && y && part, "vh_gemm_mx8_f16: null argument");
+  VH_REQUIRE(M > 0 && N > 0 && K > 0, "vh_gemm_mx8_f16: empty GEMM");
+  VH_REQUIRE(splits >= 1 && K % (8 * (int64_t)splits) == 0,
+             "vh_gemm_mx8_f16: K (%lld) must split into %d multiples of 8", (long long)K, splits);
+  VH_REQUIRE(N % 4 == 0 && ldy >= N, "vh_gemm_mx8_f16: N must be a multiple of 4 and ldy >= N");
+  VH_REQUIRE(part_bytes >= (int64_t)splits * M * N * 4, "vh_gemm_mx8_f16: workspace of %lld bytes, %lld needed",
+             (long long)part_bytes, (long long)((int64_t)splits * M * N * 4));
+  VH_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)part % 16 == 0,
+             "vh_gemm_mx8_f16: operands and workspace must be 16-byte aligned");
+  VH_REQUIRE(K * 2 < (1ll << 31) && M * K * 2 < (1ll << 31) && N * K * 2 < (1ll << 31),
+             "vh_gemm_mx8_f16: operands over 2 GiB");
+  VH_REQUIRE(epi->mode == EPI_PLAIN && (epi->out_dtype == VH_BF16 || epi->out_dtype == VH_F32),
+             "vh_gemm_mx8_f16: unsupported epilogue");
+  VH_REQUIRE(!epi->scale || epi->scale_dtype == VH_BF16 || epi->scale_dtype == VH_F32,
+             "vh_gemm_mx8_f16: scale must be bf16 or float32");
+  VH_REQUIRE(!epi->bias || epi->bias_dtype == VH_BF16 || epi->bias_dtype == VH_F32,
+             "vh_gemm_mx8_f16: bias must be bf16 or float32");
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.A = (const uint8_t*)x;
+  g.B = (const uint8_t*)w;
+  g.C = part;
+  g.M = M;
+  g.N = N;
+  g.K = K / splits;
+  g.lda = K * 2;
+  g.ldb = K * 2;
+  g.ldc = N;
+  g.sa = (K / splits) * 2;  // split z reads columns [z K / S, (z + 1) K / S)
+  g.sb = (K / splits) * 2;
+  g.sc = M * N;             // and writes partial z
+  g.epi.mode = EPI_PLAIN;
+  g.epi.out_dtype = VH_F32;
+  hipStream_t st = vh::as_stream(stream);
+  int rc;
+  switch (tile) {
+    case 1: rc = launch_f8dl<64, 128, 4, 128, 1, 4, OP_F16X>(g, splits, st); break;
+    case 2: rc = launch_f8dl<128, 64, 4, 128, 2, 2, OP_F16X>(g, splits, st); break;
+    case 3: rc = launch_f8dl<256, 128, 3, 128, 2, 2, OP_F16X>(g, splits, st); break;
+    default: rc = launch_f8dl<128, 128, 4, 128, 2, 2, OP_F16X>(g, splits, st); break;
+  }
+  if (rc) return rc;
+  const int64_t quads = M * N / 4;
+  hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, (const float*)part,
+                     (int)splits, M, N, *epi, y, ldy, ex, ew);
+  return vh::check_launch("vh_gemm_mx8_f16");
 }

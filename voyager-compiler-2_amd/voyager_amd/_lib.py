@@ -114,6 +114,9 @@ _SIGNATURES = {
         _I32,
     ),
     "vh_block_amax": ([_P, _I32, _I64, _I64, _I64, _I64, _P, _P], _I32),
+    "vh_quantize_mx8_f16": ([_P, _I64, _I64, _P, _P, _P], _I32),
+    "vh_mx8_bake_f16": ([_P, _P, _I32, _I64, _I64, _P, _P, _P], _I32),
+    "vh_gemm_mx8_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I32, _I32, _P], _I32),
     "vh_dequantize": (
         [_P, _I32, ctypes.POINTER(_I64), _I32, ctypes.POINTER(Param), ctypes.POINTER(Param), _I32,
          ctypes.POINTER(Format), ctypes.POINTER(Format), _P, _I32, _P],

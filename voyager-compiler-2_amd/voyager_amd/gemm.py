@@ -11,7 +11,7 @@ order (the parity bar is 1e-2 max-abs-normalized error).
 """
 
 import ctypes
-from typing import NamedTuple, Optional
+from typing import NamedTuple, Optional, Tuple
 
 import torch
 
@@ -325,6 +325,90 @@ def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: i
         ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x_codes.device)
         d.workspace, d.workspace_bytes = ws.data_ptr(), nbytes
     run(d, x_codes.device)
+    return out
+
+
+# ----------------------------------------------------------------- MX-int8, small M
+class MX8F16Weight(NamedTuple):
+    """An MX-int8 weight (block 16, power-of-two scales) baked for
+    ``linear_mx8_f16``: each row as exact fp16 ``code * 2**(e - E)`` with the
+    row's largest block exponent ``E``."""
+
+    w: torch.Tensor  # float16 [N, K]
+    e: torch.Tensor  # int32 [N]
+    N: int
+    K: int
+
+
+def bake_mx8_f16(codes: torch.Tensor, scale_bytes: torch.Tensor, scale_bias: int) -> MX8F16Weight:
+    """Bake packed MX-int8 weights (int8 codes [N, K], scale bytes [N, K / 16]
+    as ``packed.quantize_mx_packed`` writes them)."""
+    N, K = codes.shape
+    if K % 16 or scale_bytes.shape != (N, K // 16):
+        raise ValueError("bake_mx8_f16 needs [N, K] codes with one scale byte per 16 along K")
+    c = codes.contiguous()
+    sb = scale_bytes.contiguous()
+    w = torch.empty(N, K, dtype=torch.float16, device=codes.device)
+    e = torch.empty(N, dtype=torch.int32, device=codes.device)
+    _lib.check(load().vh_mx8_bake_f16(ptr(c), ptr(sb), int(scale_bias), N, K, ptr(w), ptr(e),
+                                      ctypes.c_void_p(stream_of(codes))), "vh_mx8_bake_f16")
+    return MX8F16Weight(w, e, N, K)
+
+
+def quantize_mx8_f16(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``quantize_mx(x, int8, [-1], 16, 127, force_scale_power_of_two=True)``
+    of the rows of a bf16 ``x`` [M, K], as the exact fp16 rows ``linear_mx8_f16``
+    reads, and their exponents."""
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise NotImplementedError("quantize_mx8_f16 takes a 2-D bfloat16 tensor")
+    M, K = x.shape
+    xc = x.contiguous()
+    out = torch.empty(M, K, dtype=torch.float16, device=x.device)
+    ex = torch.empty(M, dtype=torch.int32, device=x.device)
+    _lib.check(load().vh_quantize_mx8_f16(ptr(xc), M, K, ptr(out), ptr(ex), ctypes.c_void_p(stream_of(x))),
+               "vh_quantize_mx8_f16")
+    return out, ex
+
+
+def mx8_f16_plan(M: int, N: int, K: int) -> Tuple[int, int]:
+    """(tile, splits) of ``linear_mx8_f16``.  Measured on MI355X at K = N =
+    4096: M = 256 takes 64x128 tiles with K split in two (19.2 us; 128x128 in
+    four 23.7, unsplit 24.6), M = 2048 256x128 unsplit (77.2 us; 128x128
+    82.7).  Below 1024 rows: 64x128, K split until the grid reaches 256
+    workgroups (each split at least 512 elements); from 1024: 256x128."""
+    if M >= 1024:
+        return 3, 1
+    tiles = -(-M // 64) * -(-N // 128)
+    splits = 1
+    while tiles * splits < 256 and K % (splits * 2 * 512) == 0 and splits < 8:
+        splits *= 2
+    return 1, splits
+
+
+def linear_mx8_f16(x16: torch.Tensor, ex: torch.Tensor, weight: MX8F16Weight, out_dtype=torch.bfloat16, bias=None,
+                   alpha=None, tile: int = -1, splits: int = 0) -> torch.Tensor:
+    """MX-int8 ``linear_mx`` (``ops/quantized.py:651-723``) on the exact fp16
+    operands of ``quantize_mx8_f16`` and ``bake_mx8_f16``: an fp16 GEMM over
+    K splits and one reduction that applies ``2**(E_row + E_col)``, alpha,
+    bias and the output rounding."""
+    M, K = x16.shape
+    if K != weight.K:
+        raise RuntimeError("linear_mx8_f16: contraction mismatch")
+    N = weight.N
+    t, sp = mx8_f16_plan(M, N, K)
+    tile = t if tile < 0 else tile
+    splits = sp if splits <= 0 else splits
+    out = torch.empty(M, N, dtype=out_dtype, device=x16.device)
+    if alpha is not None:
+        alpha = alpha.reshape(()).to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+    epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
+    part = torch.empty(splits * M * N, dtype=torch.float32, device=x16.device)
+    _lib.check(load().vh_gemm_mx8_f16(ptr(x16), ptr(ex), ptr(weight.w), ptr(weight.e), M, N, K,
+                                      ctypes.c_void_p(ctypes.addressof(epi)), ptr(out), N, ptr(part),
+                                      part.numel() * 4, splits, tile, ctypes.c_void_p(stream_of(x16))),
+               "vh_gemm_mx8_f16")
     return out
 
 
