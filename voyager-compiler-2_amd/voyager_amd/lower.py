@@ -11,8 +11,10 @@ library runs packed:
   dequantize: a direct cast, unit scale).  One cast to E4M3 bytes
   (``vh_quantize``) and the FP8 GEMM with the round-scale epilogue.
 * ``posit8`` -- ``quantize(x, s_x, qmap=posit8)`` -> ``aten.linear`` with
-  posit-grid weights, no dequantize (``quantize_pt2e.py:557-561``): posit8
-  bytes and the posit8 GEMM.
+  posit-grid weights, no dequantize (``quantize_pt2e.py:557-561``): the
+  quantize as written (posit values in bf16) and the bf16 GEMM on the
+  graph's own weight.  At the shapes a posit8 site has (compute-bound), a
+  decode of packed posit bytes per call costs more than it saves.
 * ``mxint8`` -- ``quantize_mx(x, int8, [-1], bs, 127, pot)`` ->
   ``linear_mx``: int8 codes plus scale bytes and the MX-int8 GEMM.
 * ``mxnf4``  -- ``quantize_mx(x, lut4_to_int6 index, [-1], 64, 31,
@@ -288,11 +290,12 @@ def lowered_fp8_linear(x, x_scale, qmap, w_bytes, out_scale):
     return y.reshape(*x.shape[:-1], w_bytes.shape[0])
 
 
-def lowered_posit8_linear(x, x_scale, qmap, w_codes, lut):
-    """quantize(x, x_scale, qmap=posit8) -> linear on posit8 bytes."""
-    xq = packed.quantize_packed(_rows(x), x_scale, qmap)
-    y = gemm.linear_posit8(xq, w_codes, lut)
-    return y.reshape(*x.shape[:-1], w_codes.shape[0])
+def lowered_posit8_linear(x, x_scale, qmap, w):
+    """quantize(x, x_scale, qmap=posit8) -> linear: the quantize's posit
+    values in bf16 and the bf16 GEMM against the posit-grid weight."""
+    xq = torch.ops.quantized_ops.quantize(_rows(x), x_scale, qmap=qmap)
+    y = gemm.gemm_bf16(xq, w, torch.bfloat16)
+    return y.reshape(*x.shape[:-1], w.shape[0])
 
 
 def lowered_mxint8_linear(x, qmap, w_codes, w_scale, w_bias, block_size: int, bias=None):
@@ -330,14 +333,6 @@ def _bake_fp8(w: torch.Tensor) -> torch.Tensor:
     if not torch.equal(b.to(w.dtype), w):
         raise ValueError("weight values off the fp8_e4m3 grid")
     return b.view(torch.uint8).contiguous()
-
-
-def _bake_posit8(w: torch.Tensor, qmap: torch.Tensor) -> torch.Tensor:
-    one = torch.ones((), dtype=torch.bfloat16, device=w.device)
-    codes = packed.quantize_packed(w.contiguous(), one, qmap)
-    if not torch.equal(packed.unpack_codes(codes, qmap), w):
-        raise ValueError("weight values off the posit8 grid")
-    return codes
 
 
 def _bake_mxint8(w: torch.Tensor, ws: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, int]:
@@ -403,10 +398,7 @@ def _insert(model: GraphModule, site: Site) -> Node:
                 s = site.out_scale
             return graph.call_function(lowered_fp8_linear, (x, k["scale"], k["qmap"], wb, s))
         if site.kind == "posit8":
-            qmap = _attr(model, k["qmap"])
-            wc = _const(model, graph, f"{name}_posit8_weight", _bake_posit8(w, qmap))
-            lut = _const(model, graph, f"{name}_posit8_lut", gemm.posit8_lut(qmap))
-            return graph.call_function(lowered_posit8_linear, (x, k["scale"], k["qmap"], wc, lut))
+            return graph.call_function(lowered_posit8_linear, (x, k["scale"], k["qmap"], site.weight))
         ws = _attr(model, site.weight_scale)
         if site.kind == "mxint8":
             codes, sbytes, bias_w = _bake_mxint8(w, ws)
@@ -499,7 +491,7 @@ class _SiteCheck(Interpreter):
             return lowered_fp8_linear(x, env[k["scale"]], env[k["qmap"]], _bake_fp8(w), s)
         if site.kind == "posit8":
             qmap = env[k["qmap"]]
-            return lowered_posit8_linear(x, env[k["scale"]], qmap, _bake_posit8(w, qmap), gemm.posit8_lut(qmap))
+            return lowered_posit8_linear(x, env[k["scale"]], qmap, w)
         ws = _attr(m, site.weight_scale)
         if site.kind == "mxint8":
             codes, sbytes, bias_w = _bake_mxint8(w, ws)
