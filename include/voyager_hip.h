@@ -337,6 +337,20 @@ int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t M, const u
                 const uint8_t* w_scale, const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N,
                 int64_t K, const vh_epilogue* epi, void* y, vh_stream_t stream);
 
+/* vh_quantize_mx_rows16 + vh_gemv_nf4 for one bfloat16 row x[K], in one
+ * launch: each 64-element block of x is quantized inside the GEMV
+ * (quantize_mx(x, fmt, [-1], 64, quant_max, scale map x_scale_fmt),
+ * ops/quantized.py:1070-1115, by the same block-scale and element-code
+ * functions, so levels and scales are those of the two launches bit for
+ * bit), its codes taken to levels through levels16.  Replaces, like
+ * vh_gemv_nf4, quantized_ops.linear_mx at M = 1 (ops/quantized.py:651-723).
+ * x_scale_fmt: a minifloat (not the E4M3 hardware form); x_fmt: an index
+ * table (STEPS) of at most 16 levels. */
+int vh_gemv_nf4_m1(const void* x, int32_t x_dtype, float quant_max, const vh_format* x_scale_fmt,
+                   const vh_format* x_fmt, const uint8_t* w_packed, const uint8_t* w_scale,
+                   const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N, int64_t K,
+                   const vh_epilogue* epi, void* y, vh_stream_t stream);
+
 /* ------------------------------------------------- decoder-layer decode step
  * One decode step (a batch of single tokens, M <= 16) of a Llama-style layer
  * whose linears are MX-int8 (int8 codes, block 16 along K, power-of-two

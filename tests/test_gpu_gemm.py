@@ -283,8 +283,13 @@ def test_decode_bytes(n):
     assert_same_bits(got, O.quantize(x, one, qmap=tab), f"n={n}")
 
 
-@pytest.mark.parametrize("M", [1, 16])
-@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("M,K,N", [
+    (1, 4096, 4096), (16, 4096, 4096), (1, 4096, 1024), (16, 4096, 1024), (1, 4096, 14336),
+    (16, 4096, 14336), (1, 14336, 4096), (16, 14336, 4096),
+    # ragged: K ranges of 0-2 blocks (empty waves), chunks padded past the
+    # range end, one row per lane (M == 1) and four (M > 1), four tiles per
+    # workgroup (N / 16 >= 512 with K <= 2048)
+    (5, 320, 48), (1, 1088, 2048), (3, 2048, 8192), (1, 2048, 8192), (2, 960, 8192)])
 def test_linear_nf4_gemv_cfg3(M, K, N):
     """Config 3's decode GEMV on baked 4-bit weights against the oracle's
     linear_mx of the same quantized operands."""
@@ -305,6 +310,51 @@ def test_linear_nf4_gemv_cfg3(M, K, N):
     got = gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d))
     assert got.dtype == torch.bfloat16 and list(got.shape) == [M, N]
     assert max_rel_err(got, exp) < TOL
+    if M == 1:
+        # the one-launch path (the row quantized inside the GEMV) is the
+        # two-launch path bit for bit: same levels, scales and sums
+        two = gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d), fused=False)
+        one = gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d), fused=True)
+        assert_same_bits(one, two, "one launch vs two")
+        assert torch.equal(got, one)
+
+
+@pytest.mark.parametrize("K,N", [(1024, 64), (4096, 8192)])
+def test_linear_nf4_one_launch_special_blocks(K, N):
+    """The one-launch M = 1 path on blocks of zeros, NaN, +-inf, tiny and
+    large values, with alpha and bias and a float32 output: bit for bit the
+    two-launch path, and the finite outputs within tolerance of the
+    oracle."""
+    from voyager_amd import gemm
+
+    vt = T.quantization_map("lut4_to_int6")
+    index, entries, mid = T.codebook_index_table(vt)
+    stab = T.quantization_map("fp8_e5m3")
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(1, K, generator=g)
+    x[0, 0:64] = 0.0
+    x[0, 70] = float("nan")
+    x[0, 130] = float("inf")
+    x[0, 200] = -float("inf")
+    x[0, 256:320] *= 1e-30
+    x[0, 320:384] *= 3e4
+    x = x.bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    d = "cuda"
+    wb = gemm.bake_nf4_weight(w.to(d), index.to(d), stab.to(d), entries.to(d))
+    alpha = torch.tensor(0.75)
+    bias = torch.randn(N, generator=g)
+    args = (x.to(d), wb, index.to(d), stab.to(d), torch.float32, bias.to(d), alpha.to(d))
+    two = gemm.linear_nf4(*args, fused=False)
+    one = gemm.linear_nf4(*args, fused=True)
+    assert_same_bits(one, two, "one launch vs two")
+    sx, cx = O.quantize_mx(x, index, [-1], 64, 31.0, False, stab, mid)
+    sw, cw = O.quantize_mx(w, index, [-1], 64, 31.0, False, stab)
+    exp = O.linear_mx(cx, cw, input_scale=sx, weight_scale=sw, block_size=64, input_code=entries,
+                      weight_code=entries).float() * 0.75 + bias
+    fin = torch.isfinite(exp)
+    assert torch.equal(torch.isfinite(one.cpu()), fin)
+    assert max_rel_err(one.cpu()[fin], exp[fin]) < TOL
 
 
 @pytest.mark.parametrize("M,K", [(1, 4096), (16, 14336), (5, 320)])

@@ -215,13 +215,16 @@ VH_DEV float fmt_posit(float x, const vh_format& f) {
 // level is the number of thresholds whose key is <= the input's key (keys are
 // staged in LDS by the kernel: `keys` holds f.thr_key).  NaN inputs are
 // handled by the caller (they take nan_out / nan_level).
+// TOP: the first halving's step (32 covers up to 63 thresholds; a table
+// known to hold at most 2 * TOP - 1 may start lower).
+template <int TOP = 32>
 VH_DEV uint32_t steps_level(uint32_t b, int nsteps, const uint16_t* keys) {
   // Branch-free search: six halvings cover up to 63 thresholds, so the
   // lookups of a thread's elements can overlap.
   const uint32_t k = bf_key(b);
   int pos = 0;
 #pragma unroll
-  for (int step = 32; step >= 1; step >>= 1) {
+  for (int step = TOP; step >= 1; step >>= 1) {
     const int nxt = pos + step;
     const bool ok = nxt <= nsteps && (uint32_t)keys[nxt <= nsteps ? nxt - 1 : 0] <= k;
     pos = ok ? nxt : pos;

@@ -17,12 +17,15 @@
 // the tile's 16 scale bytes of a block contiguous, the activations' scales
 // block-major [K/64][16] -- two rounds of UNROLL blocks in flight, with no
 // staging prologue; nibbles become int8 levels with three v_perm_b32 per 4
-// values.  The K ranges meet through LDS at the end.
+// values, and a weight scale byte becomes its value through a 256-entry
+// table in LDS, decoded once per workgroup.  The K ranges meet through LDS
+// at the end.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
 #include <type_traits>
 
+#include "vh_blockscale.h"
 #include "vh_device.h"
 #include "vh_host.h"
 
@@ -53,119 +56,53 @@ __global__ void __launch_bounds__(256) k_pack_nf4(const uint8_t* __restrict__ co
   *(uint2*)(out + t * 8) = make_uint2(lo, hi);
 }
 
-// Four byte indices (0..15) -> four int8 levels from a 16-entry table held in
-// four dwords (t0 = levels 0..3, ... t3 = levels 12..15).
-// The third v_perm picks, per byte i, byte i of the low-half lookup (selector
-// i) or of the high-half one (i + 4) by bit 3 of the index: six full-rate
-// ops, no per-byte multiply.
-__device__ __forceinline__ uint32_t lut16(uint32_t idx, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
-  const uint32_t sel = idx & 0x07070707u;
+// Four 4-bit indices -> four int8 levels from a 16-entry table held in four
+// dwords (t0 = levels 0..3, ... t3 = levels 12..15).  `sel` holds the low
+// three bits of each index (one per byte), `hib` its bit 3 at bit 2 of the
+// byte; the third v_perm picks, per byte i, byte i of the low-half lookup
+// (selector i) or of the high-half one (i + 4).  `base` is 0x03020100 in a
+// VGPR: with a register operand the merge selector is one v_and_or_b32 (a
+// VOP3 encoding takes no second literal here).
+__device__ __forceinline__ uint32_t lut16(uint32_t sel, uint32_t hib, uint32_t base, uint32_t t0, uint32_t t1,
+                                          uint32_t t2, uint32_t t3) {
   const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
   const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-  const uint32_t pick = ((idx >> 1) & 0x04040404u) | 0x03020100u;
-  return __builtin_amdgcn_perm(hi, lo, pick);
+  return __builtin_amdgcn_perm(hi, lo, (hib & 0x04040404u) | base);
 }
 
-// SK: the weight scale map's kind (fmt_decode_k), fixed at compile time so
-// the block loop stays free of branches (a runtime switch there makes the
-// compiler drain every outstanding load at each merge).
-// NBW: blocks per chunk of a wave's K range (padded with empty blocks); a
-// chunk's two rounds are unrolled into straight-line code, where the
-// compiler's count of outstanding loads is exact (around a loop, or over
-// more rounds, it drains them all or spills).
-template <int T, int SK, int NBW, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64)
-k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, const uint8_t* __restrict__ wp,
-           const uint8_t* __restrict__ ws, vh_format sfmt, uint4 lv, int64_t N, int64_t K, vh_epilogue epi,
-           void* __restrict__ y) {
-  constexpr int KR = WAVES / T;  // K ranges per tile
-  constexpr int UNROLL = NBW < 8 ? NBW : 8;  // blocks per round; two rounds in flight (256 VGPRs)
-  constexpr int ROUNDS = NBW / UNROLL;
-  __shared__ float s_red[WAVES][4][64];
-  const int tid = threadIdx.x;
-  const int nb = (int)(K / 64);
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tl = wave % T, kr = wave / T;
-  const int64_t tile = (int64_t)blockIdx.x * T + tl;
-  const int b0 = kr * nb / KR, b1 = (kr + 1) * nb / KR;
-  const int64_t n = tile * 16 + (lane & 15);
-  const int ma = lane & 15;          // activation row this lane feeds to the MFMA
-  const int mrow = (lane >> 4) * 4;  // output rows this lane accumulates
+// The low / high nibbles of a dword of packed indices.
+__device__ __forceinline__ uint32_t lut_lo(uint32_t w, uint32_t base, const uint4& lv) {
+  return lut16(w & 0x07070707u, w >> 1, base, lv.x, lv.y, lv.z, lv.w);
+}
+__device__ __forceinline__ uint32_t lut_hi(uint32_t w, uint32_t base, const uint4& lv) {
+  return lut16((w >> 4) & 0x07070707u, w >> 5, base, lv.x, lv.y, lv.z, lv.w);
+}
 
-  // Buffer loads: a lane whose row is past M, or a block past this wave's
-  // range, reads out of range and gets zeros without a memory access.
-  constexpr uint32_t OOB = 0x80000000u;
-  const __amdgpu_buffer_rsrc_t wr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(wp + tile * nb * 512), (short)0, nb * 512, 0x00020000);
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xl, (short)0, M * (int)K, 0x00020000);
-  const __amdgpu_buffer_rsrc_t wsr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(ws + tile * nb * 16), (short)0, nb * 16, 0x00020000);
-  const __amdgpu_buffer_rsrc_t xsr = __builtin_amdgcn_make_buffer_rsrc((void*)xs, (short)0, nb * 64, 0x00020000);
-  const uint32_t woff = (uint32_t)lane * 8u;
-  const uint32_t xoff = ma < M ? (uint32_t)(ma * K + (lane >> 4) * 16) : OOB;
-  const uint32_t wsoff = (uint32_t)(lane & 15), xsoff = (uint32_t)mrow * 4u;
-  struct Set {
-    vh_u32x2 w[UNROLL];
-    vh_u32x4 x[UNROLL];
-    vh_u32x4 sx[UNROLL];
-    uint32_t sw[UNROLL];
-  };
-  auto load = [&](int b, Set& st) {
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const bool ok = b + u < b1;
-      const uint32_t bb = (uint32_t)(b + u);
-      st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, ok ? woff + bb * 512u : OOB, 0, 0);
-      st.x[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff + bb * 64u : OOB, 0, 0);
-      st.sw[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, ok ? wsoff + bb * 16u : OOB, 0, 0);
-      st.sx[u] = __builtin_amdgcn_raw_buffer_load_b128(xsr, ok ? xsoff + bb * 64u : OOB, 0, 0);
-    }
-  };
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto round = [&](const Set& st) {
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      i32x4 wl;
-      wl[0] = (int)lut16(st.w[u].x & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      wl[1] = (int)lut16(st.w[u].y & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      wl[2] = (int)lut16((st.w[u].x >> 4) & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      wl[3] = (int)lut16((st.w[u].y >> 4) & 0x0f0f0f0fu, lv.x, lv.y, lv.z, lv.w);
-      const i32x4 xa = {(int)st.x[u].x, (int)st.x[u].y, (int)st.x[u].z, (int)st.x[u].w};
-      i32x4 d = {0, 0, 0, 0};
-      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
-      // past the range: zero dot products (zero activations); the decoded
-      // scale of a zero byte is finite
-      const float swv = fmt_decode_k<SK>(st.sw[u], sfmt, nullptr);
-      acc[0] = fmaf((float)d[0], __uint_as_float(st.sx[u].x) * swv, acc[0]);
-      acc[1] = fmaf((float)d[1], __uint_as_float(st.sx[u].y) * swv, acc[1]);
-      acc[2] = fmaf((float)d[2], __uint_as_float(st.sx[u].z) * swv, acc[2]);
-      acc[3] = fmaf((float)d[3], __uint_as_float(st.sx[u].w) * swv, acc[3]);
-    }
-  };
-  // blocks past the range load zeros without a memory access; a range
-  // longer than NBW blocks runs in chunks of NBW
-  for (int c0 = b0; c0 < b1; c0 += NBW) {
-    Set s[2];
-    load(c0, s[0]);
-#pragma unroll
-    for (int r = 0; r < ROUNDS; ++r) {
-      if (r + 1 < ROUNDS) load(c0 + (r + 1) * UNROLL, s[(r + 1) & 1]);
-      round(s[r & 1]);
-      // keep later rounds' loads in place (two register sets, not ROUNDS):
-      // no memory access moves across this point
-      asm volatile("" ::: "memory");
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) s_red[wave][r][lane] = acc[r];
-  __syncthreads();
-  if (kr != 0) return;
+// A weight scale byte's value, for the kinds the launcher accepts (the ones
+// with a closed form: integer, minifloat, posit).
+__device__ float scale_value(uint32_t c, const vh_format& f) {
+  if (f.kind == VH_FMT_INT) return fmt_decode_k<K_INT>(c, f, nullptr);
+  if (f.kind == VH_FMT_MINIFLOAT)
+    return (f.flags & VH_FMT_HW_E4M3) ? fmt_decode_k<K_E4M3>(c, f, nullptr) : fmt_decode_k<K_MINI>(c, f, nullptr);
+  return fmt_decode_k<K_POSIT>(c, f, nullptr);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)(bytes > 0 ? bytes : 0), 0x00020000);
+}
+
+// The tile's K-range partial sums (added in range order), alpha, bias and
+// the output rounding; run by the waves of range 0.
+template <int T, int MR, int WAVES>
+__device__ __forceinline__ void finish(float (*s_red)[MR][64], int tl, int lane, int mrow, int M, int64_t n,
+                                       int64_t N, const vh_epilogue& epi, void* y) {
+  constexpr int KR = WAVES / T;
   float alpha = 1.0f;
   if (epi.scale) alpha = epi.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)epi.scale) : *(const float*)epi.scale;
   float bias = 0.0f;
   if (epi.bias) bias = epi.bias_dtype == VH_BF16 ? bf2f(((const uint16_t*)epi.bias)[n]) : ((const float*)epi.bias)[n];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < MR; ++r) {
     const int m = mrow + r;
     if (m >= M) continue;
     float v = 0.0f;
@@ -176,6 +113,323 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
     if (epi.out_dtype == VH_BF16) ((uint16_t*)y)[m * N + n] = (uint16_t)f2bf(v);
     else ((float*)y)[m * N + n] = v;
   }
+}
+
+// MR: output rows a lane accumulates -- 4 (rows 4*(lane/16) .. +3 of the
+// MFMA's 16x16 result) or 1 when M == 1 (only row 0 is stored, so one
+// scale product and one accumulation per block).
+// NBW: blocks per chunk of a wave's K range; a chunk's rounds are unrolled
+// into straight-line code, where the compiler's count of outstanding loads
+// is exact (around a loop, or over more than two register sets, it drains
+// them all or spills).
+template <int T, int MR, int NBW, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64)
+k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, const uint8_t* __restrict__ wp,
+           const uint8_t* __restrict__ ws, vh_format sfmt, uint4 lv, int64_t N, int64_t K, vh_epilogue epi,
+           void* __restrict__ y) {
+  static_assert(MR == 1 || MR == 4, "rows per lane");
+  constexpr int KR = WAVES / T;  // K ranges per tile
+  constexpr int UNROLL = NBW < 8 ? NBW : 8;  // blocks per round; two rounds in flight
+  constexpr int ROUNDS = NBW / UNROLL;
+  __shared__ float s_red[WAVES][MR][64];
+  __shared__ float s_scale[256];  // the weight scale map, decoded once per workgroup
+  const int tid = threadIdx.x;
+  const int nb = (int)(K / 64);
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tl = wave % T, kr = wave / T;
+  const int64_t tile = (int64_t)blockIdx.x * T + tl;
+  const int b0 = kr * nb / KR, b1 = (kr + 1) * nb / KR;
+  const int64_t n = tile * 16 + (lane & 15);
+  const int ma = lane & 15;          // activation row this lane feeds to the MFMA
+  const int mrow = (lane >> 4) * 4;  // output rows this lane accumulates
+  uint32_t base;
+  asm volatile("v_mov_b32 %0, 0x3020100" : "=v"(base));
+
+  // Every buffer starts at the round's first block and ends at the wave's
+  // range end (the activations: at the end of X), so the per-block offsets
+  // are instruction immediates and a block past the range, or a lane whose
+  // row is past M, reads zeros without a memory access: its weights and
+  // activation scale are zero, so it adds nothing.
+  constexpr uint32_t OOB = 0x80000000u;
+  const uint32_t woff = (uint32_t)lane * 8u;
+  const uint32_t xoff = ma < M ? (uint32_t)(ma * K + (lane >> 4) * 16) : OOB;
+  const uint32_t wsoff = (uint32_t)(lane & 15), xsoff = (uint32_t)mrow * 4u;
+  // With one row the activation scale is the same for the whole wave: it
+  // is read through the scalar cache at the start of its round, and holds
+  // no vector registers while the round's loads are in flight.
+  struct Set {
+    vh_u32x2 w[UNROLL];
+    vh_u32x4 x[UNROLL];
+    vh_u32x4 sx[MR == 1 ? 1 : UNROLL];
+    uint32_t sw[UNROLL];
+  };
+  auto load = [&](int b, Set& st) {
+    // opaque copies of the lane offsets: the per-block constants are then
+    // added here, where they become instruction immediates, instead of
+    // being hoisted out of the loop into a register each
+    uint32_t wo = woff, xo = xoff, wso = wsoff, xso = xsoff;
+    asm volatile("" : "+v"(wo), "+v"(xo), "+v"(wso), "+v"(xso));
+    const int64_t rem = b1 - b;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(wp + (tile * nb + b) * 512, rem * 512);
+    const __amdgpu_buffer_rsrc_t wsr = rsrc(ws + (tile * nb + b) * 16, rem * 16);
+    const __amdgpu_buffer_rsrc_t xsr = rsrc(xs + (int64_t)b * 16, rem * 64);
+    const __amdgpu_buffer_rsrc_t xr = rsrc(xl + (int64_t)b * 64, (int64_t)M * K - (int64_t)b * 64);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + u * 512u, 0, 0);
+      st.x[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo + u * 64u, 0, 0);
+      st.sw[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, wso + u * 16u, 0, 0);
+      if constexpr (MR == 4) st.sx[u] = __builtin_amdgcn_raw_buffer_load_b128(xsr, xso + u * 64u, 0, 0);
+    }
+  };
+  float acc[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
+  // b: the round's first block
+  auto round = [&](Set& st, int b) {
+    float sx1[UNROLL];
+    if constexpr (MR == 1) {
+      typedef const __attribute__((address_space(4))) float cfloat;
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        // row 0's scale of block b + u; zero past the range (block 0 is read
+        // there, which always exists)
+        sx1[u] = *(const cfloat*)(uintptr_t)(xs + (int64_t)(b + u < b1 ? b + u : 0) * 16);
+      }
+      // all of them arrive before the round's first LDS read (scalar loads
+      // return out of order and share the LDS counter: interleaved, every
+      // table read would wait for all outstanding scalar loads)
+      static_assert(UNROLL == 4 || UNROLL == 8, "one statement holds the round's scales");
+      if constexpr (UNROLL == 8)
+        asm volatile("" : "+s"(sx1[0]), "+s"(sx1[1]), "+s"(sx1[2]), "+s"(sx1[3]), "+s"(sx1[4]), "+s"(sx1[5]),
+                     "+s"(sx1[6]), "+s"(sx1[7]));
+      else
+        asm volatile("" : "+s"(sx1[0]), "+s"(sx1[1]), "+s"(sx1[2]), "+s"(sx1[3]));
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+        if (b + u >= b1) sx1[u] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      // the block's registers pass through here, after every load issued
+      // before this round: its arithmetic cannot rise above them (left
+      // alone, the scheduler interleaves loads with arithmetic and a round
+      // waits on several memory latencies in turn)
+      if constexpr (MR == 1) asm volatile("" : "+v"(st.w[u]), "+v"(st.x[u]), "+v"(st.sw[u])::"memory");
+      else asm volatile("" : "+v"(st.w[u]), "+v"(st.x[u]), "+v"(st.sx[u]), "+v"(st.sw[u])::"memory");
+      i32x4 wl;
+      wl[0] = (int)lut_lo(st.w[u].x, base, lv);
+      wl[1] = (int)lut_lo(st.w[u].y, base, lv);
+      wl[2] = (int)lut_hi(st.w[u].x, base, lv);
+      wl[3] = (int)lut_hi(st.w[u].y, base, lv);
+      const i32x4 xa = {(int)st.x[u].x, (int)st.x[u].y, (int)st.x[u].z, (int)st.x[u].w};
+      i32x4 d = {0, 0, 0, 0};
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
+      // past the range: zero dot products and a zero activation scale; the
+      // decoded scale of a zero byte is finite
+      const float swv = s_scale[st.sw[u]];
+      if constexpr (MR == 1) {
+        acc[0] = fmaf((float)d[0], sx1[u] * swv, acc[0]);
+      } else {
+        acc[0] = fmaf((float)d[0], __uint_as_float(st.sx[u].x) * swv, acc[0]);
+        acc[1] = fmaf((float)d[1], __uint_as_float(st.sx[u].y) * swv, acc[1]);
+        acc[2] = fmaf((float)d[2], __uint_as_float(st.sx[u].z) * swv, acc[2]);
+        acc[3] = fmaf((float)d[3], __uint_as_float(st.sx[u].w) * swv, acc[3]);
+      }
+    }
+  };
+  static_assert(ROUNDS <= 2, "two register sets");
+  Set s[2];
+  // PRE: the chunk's rounds were all loaded before it starts
+  auto chunk = [&](int c0, auto pre) {
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+      if constexpr (!decltype(pre)::value)
+        if (r + 1 < ROUNDS) load(c0 + (r + 1) * UNROLL, s[(r + 1) & 1]);
+      round(s[r & 1], c0 + r * UNROLL);
+      // keep later rounds' loads in place (two register sets, not ROUNDS):
+      // no memory access moves across this point
+      asm volatile("" ::: "memory");
+    }
+  };
+  // The first chunk's loads go out before the scale table is built (an
+  // empty range loads nothing: every access is past its buffer's end), and
+  // the barrier waits for LDS only, so they stay in flight across it.
+  load(b0, s[0]);
+  if constexpr (ROUNDS == 2) load(b0 + UNROLL, s[1]);
+  if (tid < 256) s_scale[tid] = scale_value((uint32_t)tid, sfmt);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // a range longer than NBW blocks runs in chunks of NBW
+  if (b0 < b1) chunk(b0, std::true_type{});
+  for (int c0 = b0 + NBW; c0 < b1; c0 += NBW) {
+    load(c0, s[0]);
+    chunk(c0, std::false_type{});
+  }
+#pragma unroll
+  for (int r = 0; r < MR; ++r) s_red[wave][r][lane] = acc[r];
+  __syncthreads();
+  if (kr != 0) return;
+  finish<T, MR, WAVES>(s_red, tl, lane, mrow, M, n, N, epi, y);
+}
+
+// M == 1 with the activation row quantized here: quantize_mx(x, index, [-1],
+// 64, quant_max, scale map) (ops/quantized.py:1070-1115) of the blocks this
+// wave multiplies, by the block-scale and element-code functions of the
+// quantize kernels, so its levels and scales are those of the two-launch
+// path bit for bit.  A round's UNROLL blocks are one contiguous load of
+// UNROLL * 64 bfloat16 values, UNROLL consecutive elements per lane (a
+// block's amax is a butterfly over its 64 / UNROLL lanes); the int6 levels
+// pass through LDS into the MFMA's A operand, whose every row then holds
+// row 0 (only row 0 of the product is stored).  The activation is read by
+// every tile (it is 2K bytes against the tile's K / 2 of weights).
+template <int T, int NBW, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64)
+k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, vh_format xfmt,
+              const uint8_t* __restrict__ wp,
+              const uint8_t* __restrict__ ws, vh_format sfmt, uint4 lv, int64_t N, int64_t K, vh_epilogue epi,
+              void* __restrict__ y) {
+  constexpr int KR = WAVES / T;
+  constexpr int UNROLL = NBW < 8 ? NBW : 8;
+  constexpr int ROUNDS = NBW / UNROLL;
+  constexpr int EPL = UNROLL;    // activation elements per lane in a round
+  constexpr int LPB = 64 / EPL;  // lanes per block
+  static_assert(ROUNDS <= 2 && (UNROLL == 4 || UNROLL == 8), "round shape");
+  __shared__ float s_red[WAVES][1][64];
+  __shared__ float s_scale[256];
+  __shared__ __attribute__((aligned(4))) uint16_t s_keys[16];  // the element map's thresholds
+  __shared__ __attribute__((aligned(16))) uint8_t s_xq[WAVES][UNROLL * 64];
+  const int tid = threadIdx.x;
+  const int nb = (int)(K / 64);
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tl = wave % T, kr = wave / T;
+  const int64_t tile = (int64_t)blockIdx.x * T + tl;
+  const int b0 = kr * nb / KR, b1 = (kr + 1) * nb / KR;
+  const int64_t n = tile * 16 + (lane & 15);
+  uint32_t base;
+  asm volatile("v_mov_b32 %0, 0x3020100" : "=v"(base));
+  // quantize_mx's parameters, the mode and dtype fixed here so that the
+  // block scale's other branches fold away
+  Params P;
+  P.mode = MX_SCALED;
+  P.cdt = VH_BF16;
+  P.quant_max = quant_max;
+  P.gs = nullptr;
+  P.gs_dtype = VH_F32;
+  P.has_sfmt = 1;
+  P.sfmt = xsfmt;
+
+  // buffers from the round's first block to the range end (past it: zeros)
+  const uint32_t woff = (uint32_t)lane * 8u, wsoff = (uint32_t)(lane & 15), xoff = (uint32_t)lane * (2u * EPL);
+  typedef typename std::conditional<EPL == 8, vh_u32x4, vh_u32x2>::type XT;
+  struct Set {
+    vh_u32x2 w[UNROLL];
+    uint32_t sw[UNROLL];
+    XT x;
+  };
+  auto load = [&](int b, Set& st) __attribute__((always_inline)) {
+    uint32_t wo = woff, wso = wsoff, xo = xoff;
+    asm volatile("" : "+v"(wo), "+v"(wso), "+v"(xo));
+    const int64_t rem = b1 - b;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(wp + (tile * nb + b) * 512, rem * 512);
+    const __amdgpu_buffer_rsrc_t wsr = rsrc(ws + (tile * nb + b) * 16, rem * 16);
+    const __amdgpu_buffer_rsrc_t xr = rsrc(x + (int64_t)b * 64, rem * 128);
+    // the activation first: waiting for it leaves the weights in flight
+    if constexpr (EPL == 8) st.x = __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0);
+    else st.x = __builtin_amdgcn_raw_buffer_load_b64(xr, xo, 0, 0);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + u * 512u, 0, 0);
+      st.sw[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, wso + u * 16u, 0, 0);
+    }
+  };
+  float acc = 0.0f;
+  auto round = [&](Set& st, int b) __attribute__((always_inline)) {
+    asm volatile("" : "+v"(st.x)::"memory");
+    float xv[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL / 2; ++j) {
+      xv[2 * j] = bf2f(st.x[j] & 0xffffu);
+      xv[2 * j + 1] = bf2f(st.x[j] >> 16);
+    }
+    float hi = fabsf(xv[0]);
+#pragma unroll
+    for (int j = 1; j < EPL; ++j) hi = nmax(hi, fabsf(xv[j]));
+#pragma unroll
+    for (int off = 1; off < LPB; off <<= 1) hi = nmax(hi, __shfl_xor(hi, off));
+    const BlockScale bs = block_scale<K_MINI>(hi, 0.0f, P, nullptr);
+    // element codes as element_code<K_STEPS> forms them (levels <= 15)
+    uint32_t lvw[EPL / 4];
+#pragma unroll
+    for (int q = 0; q < EPL / 4; ++q) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float qv = div_round(xv[4 * q + j], bs.el_scale, VH_BF16);
+        const uint32_t bq = isnan_f(qv) ? f2bf(qv) : (__float_as_uint(qv) >> 16);
+        const uint32_t lvl =
+            bf_isnan_bits(bq) ? (uint32_t)xfmt.nan_level : steps_level<8>(bq, xfmt.nsteps, s_keys);
+        c |= lvl << (8 * j);
+      }
+      lvw[q] = lut_lo(c, base, lv);
+    }
+    if constexpr (EPL == 8) *(vh_u32x2*)&s_xq[wave][8 * lane] = vh_u32x2{lvw[0], lvw[1]};
+    else *(uint32_t*)&s_xq[wave][4 * lane] = lvw[0];
+    // each block's scale from the first lane of its group; zero past the range
+    float sxb[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs.scale), u * LPB));
+      sxb[u] = b + u < b1 ? v : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      asm volatile("" : "+v"(st.w[u]), "+v"(st.sw[u])::"memory");
+      i32x4 wl;
+      wl[0] = (int)lut_lo(st.w[u].x, base, lv);
+      wl[1] = (int)lut_lo(st.w[u].y, base, lv);
+      wl[2] = (int)lut_hi(st.w[u].x, base, lv);
+      wl[3] = (int)lut_hi(st.w[u].y, base, lv);
+      const vh_u32x4 xq = *(const vh_u32x4*)&s_xq[wave][u * 64 + 16 * (lane >> 4)];
+      const i32x4 xa = {(int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w};
+      i32x4 d = {0, 0, 0, 0};
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
+      acc = fmaf((float)d[0], sxb[u] * s_scale[st.sw[u]], acc);
+    }
+  };
+  Set s[2];
+  auto chunk = [&](int c0, auto pre) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+      if constexpr (!decltype(pre)::value)
+        if (r + 1 < ROUNDS) load(c0 + (r + 1) * UNROLL, s[(r + 1) & 1]);
+      round(s[r & 1], c0 + r * UNROLL);
+      asm volatile("" ::: "memory");
+    }
+  };
+  load(b0, s[0]);
+  if constexpr (ROUNDS == 2) load(b0 + UNROLL, s[1]);
+  if (tid < 256) s_scale[tid] = scale_value((uint32_t)tid, sfmt);
+  {
+    // the first 16 thresholds (all a table of at most 16 levels uses), read
+    // through the scalar cache and spread over lanes 0..7 of wave 0 (a
+    // per-lane read of the argument would be a vector load, and storing it
+    // would wait for every load in flight)
+    const uint32_t* kw = (const uint32_t*)xfmt.thr_key;
+    uint32_t kv = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kv = lane == i ? kw[i] : kv;
+    if (wave == 0 && lane < 8) *(uint32_t*)&s_keys[2 * lane] = kv;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (b0 < b1) chunk(b0, std::true_type{});
+  for (int c0 = b0 + NBW; c0 < b1; c0 += NBW) {
+    load(c0, s[0]);
+    chunk(c0, std::false_type{});
+  }
+  s_red[wave][0][lane] = acc;
+  __syncthreads();
+  if (kr != 0) return;
+  finish<T, 1, WAVES>(s_red, tl, lane, (lane >> 4) * 4, 1, n, N, epi, y);
 }
 
 }  // namespace
@@ -216,25 +470,64 @@ extern "C" int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t
   // 8 or 16 (longer ranges in chunks of 16)
   const int64_t nb = K / 64;
   const int64_t kr = four ? 2 : 8, bpw = (nb + kr - 1) / kr;
-  auto go = [&](auto sk) {
-    constexpr int SK = decltype(sk)::value;
+  auto go = [&](auto mr) {
+    constexpr int MR = decltype(mr)::value;
     auto launch = [&](auto nbw) {
       constexpr int NBW = decltype(nbw)::value;
       if (four)
-        hipLaunchKernelGGL((k_gemv_nf4<4, SK, NBW, 8>), dim3((unsigned)(tiles / 4)), dim3(512), 0, st, x_levels,
+        hipLaunchKernelGGL((k_gemv_nf4<4, MR, NBW, 8>), dim3((unsigned)(tiles / 4)), dim3(512), 0, st, x_levels,
                            x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
       else
-        hipLaunchKernelGGL((k_gemv_nf4<1, SK, NBW, 8>), dim3((unsigned)tiles), dim3(512), 0, st, x_levels, x_scale,
+        hipLaunchKernelGGL((k_gemv_nf4<1, MR, NBW, 8>), dim3((unsigned)tiles), dim3(512), 0, st, x_levels, x_scale,
                            (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
     };
     if (bpw <= 4) launch(std::integral_constant<int, 4>{});
     else if (bpw <= 8) launch(std::integral_constant<int, 8>{});
     else launch(std::integral_constant<int, 16>{});
   };
-  const vh_format& f = *w_scale_fmt;
-  if (f.kind == VH_FMT_INT) go(std::integral_constant<int, K_INT>{});
-  else if (f.kind == VH_FMT_MINIFLOAT && (f.flags & VH_FMT_HW_E4M3)) go(std::integral_constant<int, K_E4M3>{});
-  else if (f.kind == VH_FMT_MINIFLOAT) go(std::integral_constant<int, K_MINI>{});
-  else go(std::integral_constant<int, K_POSIT>{});
+  if (M == 1) go(std::integral_constant<int, 1>{});
+  else go(std::integral_constant<int, 4>{});
   return vh::check_launch("vh_gemv_nf4");
+}
+
+extern "C" int vh_gemv_nf4_m1(const void* x, int32_t x_dtype, float quant_max, const vh_format* x_scale_fmt,
+                              const vh_format* x_fmt, const uint8_t* w_packed, const uint8_t* w_scale,
+                              const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N, int64_t K,
+                              const vh_epilogue* epi, void* y, vh_stream_t stream) {
+  VH_REQUIRE(x && x_scale_fmt && x_fmt && w_packed && w_scale && w_scale_fmt && levels16 && epi && y,
+             "vh_gemv_nf4_m1: null argument");
+  VH_REQUIRE(x_dtype == VH_BF16, "vh_gemv_nf4_m1: the activation must be bfloat16");
+  VH_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 64 == 0, "vh_gemv_nf4_m1: needs N %% 16 == 0 and K %% 64 == 0");
+  VH_REQUIRE(K / 64 <= 8 * 32, "vh_gemv_nf4_m1: K must be <= %d", 8 * 32 * 64);
+  VH_REQUIRE(((uintptr_t)x % 16 == 0) && ((uintptr_t)w_packed % 8 == 0), "vh_gemv_nf4_m1: misaligned operand");
+  VH_REQUIRE(kernel_kind(x_scale_fmt) == K_MINI, "vh_gemv_nf4_m1: the activation scale map must be a minifloat");
+  VH_REQUIRE(x_fmt->kind == VH_FMT_STEPS && x_fmt->nsteps >= 0 && x_fmt->nsteps <= 15 && x_fmt->nan_level <= 15,
+             "vh_gemv_nf4_m1: the activation map must be an index table of at most 16 levels");
+  VH_REQUIRE(epi->mode == EPI_PLAIN && (epi->out_dtype == VH_BF16 || epi->out_dtype == VH_F32),
+             "vh_gemv_nf4_m1: unsupported epilogue");
+  VH_REQUIRE(w_scale_fmt->kind != VH_FMT_LUT && w_scale_fmt->kind != VH_FMT_IDENTITY &&
+                 w_scale_fmt->kind != VH_FMT_STEPS,
+             "vh_gemv_nf4_m1: the weight scale map needs a closed form with packed codes");
+  uint32_t t[4];
+  memcpy(t, levels16, 16);
+  const uint4 lv = make_uint4(t[0], t[1], t[2], t[3]);
+  // the same workgroup shapes as vh_gemv_nf4
+  const int64_t tiles = N / 16, nb = K / 64;
+  const bool four = tiles >= 512 && tiles % 4 == 0 && nb <= 2 * 16;
+  const int64_t kr = four ? 2 : 8, bpw = (nb + kr - 1) / kr;
+  hipStream_t st = vh::as_stream(stream);
+  auto launch = [&](auto nbw) {
+    constexpr int NBW = decltype(nbw)::value;
+    if (four)
+      hipLaunchKernelGGL((k_gemv_nf4_q1<4, NBW, 8>), dim3((unsigned)(tiles / 4)), dim3(512), 0, st,
+                         (const uint16_t*)x, quant_max, *x_scale_fmt, *x_fmt, w_packed, w_scale, *w_scale_fmt, lv, N,
+                         K, *epi, y);
+    else
+      hipLaunchKernelGGL((k_gemv_nf4_q1<1, NBW, 8>), dim3((unsigned)tiles), dim3(512), 0, st, (const uint16_t*)x,
+                         quant_max, *x_scale_fmt, *x_fmt, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
+  };
+  if (bpw <= 4) launch(std::integral_constant<int, 4>{});
+  else if (bpw <= 8) launch(std::integral_constant<int, 8>{});
+  else launch(std::integral_constant<int, 16>{});
+  return vh::check_launch("vh_gemv_nf4_m1");
 }

@@ -16,7 +16,7 @@ from typing import NamedTuple, Optional, Tuple
 import torch
 
 from . import _lib, formats
-from ._lib import VH_BF16, VH_F32, dtype_code, load, ptr, stream_of
+from ._lib import FMT_HW_E4M3, FMT_MINIFLOAT, FMT_STEPS, VH_BF16, VH_F32, dtype_code, load, ptr, stream_of
 from .ops import _dequantize_mx_cuda, _require_gpu, decode_codes
 from .registry import cuda_kernel, fake_kernel
 from .schemas import LINEAR_LAYOUT, MATMUL_LAYOUT
@@ -511,18 +511,61 @@ def _level_lut(levels: bytes, device) -> torch.Tensor:
     return t
 
 
+def _nf4_fusable(x: torch.Tensor, ec, sc) -> bool:
+    """Whether ``vh_gemv_nf4_m1`` can take this call: one bfloat16 row, a
+    minifloat activation scale map and an index table of at most 16 levels."""
+    f, s = ec.fmt, sc.fmt
+    return (x.shape[0] == 1 and x.dtype == torch.bfloat16 and s.kind == FMT_MINIFLOAT
+            and not (s.flags & FMT_HW_E4M3) and f.kind == FMT_STEPS and f.nsteps <= 15 and f.nan_level <= 15)
+
+
+def _nf4_one_launch_pays(N: int, K: int) -> bool:
+    """Every 16-column tile quantizes the row again (about 1.7x the GEMV's
+    own vector work), which costs less than a second launch while the grid
+    is at most 512 tiles and each wave's K range one round of 8 blocks
+    (MI355X: 8.1-8.7 us against 10.4-10.8 at K = 4096, N <= 4096; 16.9
+    against 16.2 at N = 14336; 24.7 against 17.9 at K = 14336)."""
+    return N <= 8192 and K <= 4096
+
+
 def linear_nf4(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, scale_qmap: torch.Tensor,
-               out_dtype=torch.bfloat16, bias=None, alpha=None) -> torch.Tensor:
+               out_dtype=torch.bfloat16, bias=None, alpha=None, fused=None) -> torch.Tensor:
     """MXNF4 ``linear_mx`` at decode shapes (M <= 16): the activations are
     quantized like the reference's in-graph ``quantize_mx`` (one launch that
     emits their int8 levels and float32 block scales), then the weight-
-    streaming GEMV."""
+    streaming GEMV.  One bfloat16 row is quantized inside the GEMV instead
+    (``vh_gemv_nf4_m1``: the same levels and scales, one launch) when the
+    formats allow and the shape is small enough for that to pay
+    (``_nf4_one_launch_pays``); ``fused`` = False keeps the two launches,
+    True requires the one."""
     M, K = x.shape
     if K != weight.K:
         raise RuntimeError("linear_nf4: contraction mismatch")
     xc = x.contiguous()
     ec = formats.classify(index_table)
     sc = formats.classify(scale_qmap)
+    one = _nf4_fusable(xc, ec, sc)
+    if fused and not one:
+        raise RuntimeError("linear_nf4: the one-launch path needs one bfloat16 row, a minifloat scale map and "
+                           "an index table of at most 16 levels")
+    if fused is None:
+        fused = one and _nf4_one_launch_pays(weight.N, K)
+    if fused:
+        y = torch.empty(M, weight.N, dtype=out_dtype, device=x.device)
+        if alpha is not None:
+            alpha = alpha.reshape(()).to(torch.float32).contiguous()
+        if bias is not None:
+            bias = bias.to(torch.float32).contiguous()
+        epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
+        lv = ctypes.create_string_buffer(weight.levels, 16)
+        st = load().vh_gemv_nf4_m1(ctypes.c_void_p(xc.data_ptr()), dtype_code(xc.dtype), 31.0,
+                                   ctypes.byref(sc.fmt), ctypes.byref(ec.fmt),
+                                   ctypes.c_void_p(weight.packed.data_ptr()), ctypes.c_void_p(weight.scale.data_ptr()),
+                                   ctypes.byref(weight.scale_fmt.fmt), lv, weight.N, weight.K,
+                                   ctypes.c_void_p(ctypes.addressof(epi)), ctypes.c_void_p(y.data_ptr()),
+                                   ctypes.c_void_p(stream_of(x)))
+        _lib.check(st, "vh_gemv_nf4_m1")
+        return y
     xl = torch.empty(M, K, dtype=torch.uint8, device=x.device)
     xs = torch.empty(K // 64, 16, dtype=torch.float32, device=x.device)  # block-major, rows past M unused
     lut = _level_lut(weight.levels, x.device)
