@@ -20,7 +20,8 @@ Options: --gpus N (1 only), --steps K, --warmup W, --no-cpu (skip the CPU
 baseline), --copy-calibration BYTES (run only a plain device copy, for
 rocprofv3 counter calibration), --profile-shapes R (run only, shape by shape
 in SHAPES order, R quantize launches then R GEMM launches, eagerly: dispatch
-order names the shape in a rocprofv3 counter run), --calibrate (run only
+order names the shape in a rocprofv3 counter run; with --config 3, R
+linear_nf4 calls at M = 1 then M = 16 per shape), --calibrate (run only
 the reference points: plain device copies and the vendor GEMMs at the
 config-2 shapes), --outliers (the outlier (CSR) path: the filter's
 bandwidth and the config-1 linear with its outlier stream).
@@ -701,13 +702,31 @@ def calibrate():
     print(json.dumps(out), flush=True)
 
 
-def profile_shapes(reps: int):
-    """The config-2 kernels shape by shape, for rocprofv3 counter runs."""
+def profile_shapes(reps: int, config: int = 2):
+    """The config-2 kernels shape by shape, for rocprofv3 counter runs (with
+    --config 3: config 3's linear_nf4 calls, M = 1 then M = 16 per shape)."""
     import voyager_amd.library  # noqa: F401  (defines quantized_ops)
     from voyager_amd import formats, gemm, packed
     from voyager_amd.ops import _elementwise
 
     dev = torch.device("cuda:0")
+    if config == 3:
+        sp = formats.parse_spec(CFG3_SPEC)
+        index, entries, _ = formats.codebook_tables(sp["dtype"], dev)
+        stab = formats.quantization_map(sp["scale_dtype"], dev)
+        for i, (K, N) in enumerate(SHAPES):
+            g = torch.Generator().manual_seed(1)
+            wb = gemm.bake_nf4_weight((torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev), index, stab,
+                                      entries)
+            for M in (1, 16):
+                x = torch.randn(M, K, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
+                torch.cuda.synchronize()
+                for _ in range(reps):
+                    gemm.linear_nf4(x, wb, index, stab)
+                torch.cuda.synchronize()
+            log(f"profile-shapes: shape {i} (K, N) = {SHAPES[i]} done")
+        print(json.dumps({"profile_shapes": SHAPES, "M": [1, 16], "reps": reps}))
+        return
     tab = formats.quantization_map("fp8_e4m3", dev)
     fmt = formats.classify(tab).fmt
     for i, (x, w) in enumerate(make_inputs(dev)):
@@ -747,7 +766,7 @@ def main():
         copy_calibration(args.copy_calibration)
         return
     if args.profile_shapes:
-        profile_shapes(args.profile_shapes)
+        profile_shapes(args.profile_shapes, args.config)
         return
     if args.calibrate:
         calibrate()
