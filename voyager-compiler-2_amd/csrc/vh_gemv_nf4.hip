@@ -122,24 +122,27 @@ __device__ __forceinline__ void finish(float (*s_red)[MR][64], int tl, int lane,
 // into straight-line code, where the compiler's count of outstanding loads
 // is exact (around a loop, or over more than two register sets, it drains
 // them all or spills).
-template <int T, int MR, int NBW, int WAVES>
+template <int T, int MR, int NBW, int WAVES, int TPW>
 __global__ void __launch_bounds__(WAVES * 64)
 k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, const uint8_t* __restrict__ wp,
            const uint8_t* __restrict__ ws, vh_format sfmt, uint4 lv, int64_t N, int64_t K, vh_epilogue epi,
            void* __restrict__ y) {
   static_assert(MR == 1 || MR == 4, "rows per lane");
+  static_assert(TPW == 1 || TPW == 2, "tiles per wave");
   constexpr int KR = WAVES / T;  // K ranges per tile
   constexpr int UNROLL = NBW < 8 ? NBW : 8;  // blocks per round; two rounds in flight
   constexpr int ROUNDS = NBW / UNROLL;
-  __shared__ float s_red[WAVES][MR][64];
+  __shared__ float s_red[TPW][WAVES][MR][64];
   __shared__ float s_scale[256];  // the weight scale map, decoded once per workgroup
+  // M > 1: a round's activation scales, one 16-byte load per lane, read
+  // back per block (rows 4 (lane / 16) .. + 3)
+  __shared__ __attribute__((aligned(16))) uint8_t s_sx[MR == 4 ? WAVES : 1][MR == 4 ? 64 * 16 : 16];
   const int tid = threadIdx.x;
   const int nb = (int)(K / 64);
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tl = wave % T, kr = wave / T;
-  const int64_t tile = (int64_t)blockIdx.x * T + tl;
+  const int64_t tile0 = ((int64_t)blockIdx.x * T + tl) * TPW;  // this wave's first tile
   const int b0 = kr * nb / KR, b1 = (kr + 1) * nb / KR;
-  const int64_t n = tile * 16 + (lane & 15);
   const int ma = lane & 15;          // activation row this lane feeds to the MFMA
   const int mrow = (lane >> 4) * 4;  // output rows this lane accumulates
   uint32_t base;
@@ -153,40 +156,46 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
   constexpr uint32_t OOB = 0x80000000u;
   const uint32_t woff = (uint32_t)lane * 8u;
   const uint32_t xoff = ma < M ? (uint32_t)(ma * K + (lane >> 4) * 16) : OOB;
-  const uint32_t wsoff = (uint32_t)(lane & 15), xsoff = (uint32_t)mrow * 4u;
+  const uint32_t wsoff = (uint32_t)(lane & 15);
+  const uint32_t xsoff = lane < UNROLL * 4 ? (uint32_t)lane * 16u : OOB;  // M > 1: the round's scales
   // With one row the activation scale is the same for the whole wave: it
   // is read through the scalar cache at the start of its round, and holds
   // no vector registers while the round's loads are in flight.
   struct Set {
-    vh_u32x2 w[UNROLL];
+    vh_u32x2 w[TPW][UNROLL];
     vh_u32x4 x[UNROLL];
-    vh_u32x4 sx[MR == 1 ? 1 : UNROLL];
-    uint32_t sw[UNROLL];
+    vh_u32x4 sx;
+    uint32_t sw[TPW][UNROLL];
   };
-  auto load = [&](int b, Set& st) {
+  auto load = [&](int b, Set& st) __attribute__((always_inline)) {
     // opaque copies of the lane offsets: the per-block constants are then
     // added here, where they become instruction immediates, instead of
     // being hoisted out of the loop into a register each
     uint32_t wo = woff, xo = xoff, wso = wsoff, xso = xsoff;
     asm volatile("" : "+v"(wo), "+v"(xo), "+v"(wso), "+v"(xso));
     const int64_t rem = b1 - b;
-    const __amdgpu_buffer_rsrc_t wr = rsrc(wp + (tile * nb + b) * 512, rem * 512);
-    const __amdgpu_buffer_rsrc_t wsr = rsrc(ws + (tile * nb + b) * 16, rem * 16);
-    const __amdgpu_buffer_rsrc_t xsr = rsrc(xs + (int64_t)b * 16, rem * 64);
     const __amdgpu_buffer_rsrc_t xr = rsrc(xl + (int64_t)b * 64, (int64_t)M * K - (int64_t)b * 64);
+    if constexpr (MR == 4) st.sx = __builtin_amdgcn_raw_buffer_load_b128(rsrc(xs + (int64_t)b * 16, rem * 64), xso, 0, 0);
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + u * 512u, 0, 0);
-      st.x[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo + u * 64u, 0, 0);
-      st.sw[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, wso + u * 16u, 0, 0);
-      if constexpr (MR == 4) st.sx[u] = __builtin_amdgcn_raw_buffer_load_b128(xsr, xso + u * 64u, 0, 0);
+    for (int t = 0; t < TPW; ++t) {
+      const __amdgpu_buffer_rsrc_t wr = rsrc(wp + ((tile0 + t) * nb + b) * 512, rem * 512);
+      const __amdgpu_buffer_rsrc_t wsr = rsrc(ws + ((tile0 + t) * nb + b) * 16, rem * 16);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        st.w[t][u] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + u * 512u, 0, 0);
+        st.sw[t][u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, wso + u * 16u, 0, 0);
+      }
     }
-  };
-  float acc[MR];
 #pragma unroll
-  for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
+    for (int u = 0; u < UNROLL; ++u) st.x[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo + u * 64u, 0, 0);
+  };
+  float acc[TPW][MR];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[t][r] = 0.0f;
   // b: the round's first block
-  auto round = [&](Set& st, int b) {
+  auto round = [&](Set& st, int b) __attribute__((always_inline)) {
     float sx1[UNROLL];
     if constexpr (MR == 1) {
       typedef const __attribute__((address_space(4))) float cfloat;
@@ -208,6 +217,12 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u)
         if (b + u >= b1) sx1[u] = 0.0f;
+    } else {
+      // the round's activation scales (zero past the range) into this
+      // wave's LDS slot; read back by other lanes of the same wave (LDS
+      // keeps a wave's accesses in order)
+      asm volatile("" : "+v"(st.sx)::"memory");
+      *(vh_u32x4*)&s_sx[wave][lane * 16] = st.sx;
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -215,33 +230,41 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
       // before this round: its arithmetic cannot rise above them (left
       // alone, the scheduler interleaves loads with arithmetic and a round
       // waits on several memory latencies in turn)
-      if constexpr (MR == 1) asm volatile("" : "+v"(st.w[u]), "+v"(st.x[u]), "+v"(st.sw[u])::"memory");
-      else asm volatile("" : "+v"(st.w[u]), "+v"(st.x[u]), "+v"(st.sx[u]), "+v"(st.sw[u])::"memory");
-      i32x4 wl;
-      wl[0] = (int)lut_lo(st.w[u].x, base, lv);
-      wl[1] = (int)lut_lo(st.w[u].y, base, lv);
-      wl[2] = (int)lut_hi(st.w[u].x, base, lv);
-      wl[3] = (int)lut_hi(st.w[u].y, base, lv);
+      if constexpr (TPW == 1)
+        asm volatile("" : "+v"(st.w[0][u]), "+v"(st.x[u]), "+v"(st.sw[0][u])::"memory");
+      else
+        asm volatile("" : "+v"(st.w[0][u]), "+v"(st.w[1][u]), "+v"(st.x[u]), "+v"(st.sw[0][u]),
+                     "+v"(st.sw[1][u])::"memory");
       const i32x4 xa = {(int)st.x[u].x, (int)st.x[u].y, (int)st.x[u].z, (int)st.x[u].w};
-      i32x4 d = {0, 0, 0, 0};
-      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
-      // past the range: zero dot products and a zero activation scale; the
-      // decoded scale of a zero byte is finite
-      const float swv = s_scale[st.sw[u]];
-      if constexpr (MR == 1) {
-        acc[0] = fmaf((float)d[0], sx1[u] * swv, acc[0]);
-      } else {
-        acc[0] = fmaf((float)d[0], __uint_as_float(st.sx[u].x) * swv, acc[0]);
-        acc[1] = fmaf((float)d[1], __uint_as_float(st.sx[u].y) * swv, acc[1]);
-        acc[2] = fmaf((float)d[2], __uint_as_float(st.sx[u].z) * swv, acc[2]);
-        acc[3] = fmaf((float)d[3], __uint_as_float(st.sx[u].w) * swv, acc[3]);
+      vh_u32x4 sxq;
+      if constexpr (MR == 4) sxq = *(const vh_u32x4*)&s_sx[wave][u * 64 + mrow * 4];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        i32x4 wl;
+        wl[0] = (int)lut_lo(st.w[t][u].x, base, lv);
+        wl[1] = (int)lut_lo(st.w[t][u].y, base, lv);
+        wl[2] = (int)lut_hi(st.w[t][u].x, base, lv);
+        wl[3] = (int)lut_hi(st.w[t][u].y, base, lv);
+        i32x4 d = {0, 0, 0, 0};
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
+        // past the range: zero dot products and a zero activation scale; the
+        // decoded scale of a zero byte is finite
+        const float swv = s_scale[st.sw[t][u]];
+        if constexpr (MR == 1) {
+          acc[t][0] = fmaf((float)d[0], sx1[u] * swv, acc[t][0]);
+        } else {
+          acc[t][0] = fmaf((float)d[0], __uint_as_float(sxq.x) * swv, acc[t][0]);
+          acc[t][1] = fmaf((float)d[1], __uint_as_float(sxq.y) * swv, acc[t][1]);
+          acc[t][2] = fmaf((float)d[2], __uint_as_float(sxq.z) * swv, acc[t][2]);
+          acc[t][3] = fmaf((float)d[3], __uint_as_float(sxq.w) * swv, acc[t][3]);
+        }
       }
     }
   };
   static_assert(ROUNDS <= 2, "two register sets");
   Set s[2];
   // PRE: the chunk's rounds were all loaded before it starts
-  auto chunk = [&](int c0, auto pre) {
+  auto chunk = [&](int c0, auto pre) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
       if constexpr (!decltype(pre)::value)
@@ -266,10 +289,14 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
     chunk(c0, std::false_type{});
   }
 #pragma unroll
-  for (int r = 0; r < MR; ++r) s_red[wave][r][lane] = acc[r];
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int r = 0; r < MR; ++r) s_red[t][wave][r][lane] = acc[t][r];
   __syncthreads();
   if (kr != 0) return;
-  finish<T, MR, WAVES>(s_red, tl, lane, mrow, M, n, N, epi, y);
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+    finish<T, MR, WAVES>(s_red[t], tl, lane, mrow, M, (tile0 + t) * 16 + (lane & 15), N, epi, y);
 }
 
 // M == 1 with the activation row quantized here: quantize_mx(x, index, [-1],
@@ -470,15 +497,21 @@ extern "C" int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t
   // 8 or 16 (longer ranges in chunks of 16)
   const int64_t nb = K / 64;
   const int64_t kr = four ? 2 : 8, bpw = (nb + kr - 1) / kr;
+  // two tiles per wave (the activation loads shared) while that leaves at
+  // least 256 workgroups: 896 tiles then run in one round of the CUs
+  const bool pair = !four && tiles >= 512 && tiles % 2 == 0;
   auto go = [&](auto mr) {
     constexpr int MR = decltype(mr)::value;
     auto launch = [&](auto nbw) {
       constexpr int NBW = decltype(nbw)::value;
       if (four)
-        hipLaunchKernelGGL((k_gemv_nf4<4, MR, NBW, 8>), dim3((unsigned)(tiles / 4)), dim3(512), 0, st, x_levels,
+        hipLaunchKernelGGL((k_gemv_nf4<4, MR, NBW, 8, 1>), dim3((unsigned)(tiles / 4)), dim3(512), 0, st, x_levels,
+                           x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
+      else if (pair)
+        hipLaunchKernelGGL((k_gemv_nf4<1, MR, NBW, 8, 2>), dim3((unsigned)(tiles / 2)), dim3(512), 0, st, x_levels,
                            x_scale, (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
       else
-        hipLaunchKernelGGL((k_gemv_nf4<1, MR, NBW, 8>), dim3((unsigned)tiles), dim3(512), 0, st, x_levels, x_scale,
+        hipLaunchKernelGGL((k_gemv_nf4<1, MR, NBW, 8, 1>), dim3((unsigned)tiles), dim3(512), 0, st, x_levels, x_scale,
                            (int)M, w_packed, w_scale, *w_scale_fmt, lv, N, K, *epi, y);
     };
     if (bpw <= 4) launch(std::integral_constant<int, 4>{});
