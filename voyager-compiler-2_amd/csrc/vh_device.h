@@ -246,6 +246,28 @@ VH_DEV void stage_steps(const vh_format& f, uint16_t* lds) {
 
 VH_DEV bool bf_isnan_bits(uint32_t b) { return (b & 0x7fffu) > 0x7f80u; }
 
+// Four 4-bit indices -> four int8 levels from a 16-entry table held in four
+// dwords (t0 = levels 0..3, ... t3 = levels 12..15).  `sel` holds the low
+// three bits of each index (one per byte), `hib` its bit 3 at bit 2 of the
+// byte; the third v_perm picks, per byte i, byte i of the low-half lookup
+// (selector i) or of the high-half one (i + 4).  `base` is 0x03020100 in a
+// VGPR: with a register operand the merge selector is one v_and_or_b32 (a
+// VOP3 encoding takes no second literal here).
+VH_DEV uint32_t lut16(uint32_t sel, uint32_t hib, uint32_t base, uint32_t t0, uint32_t t1,
+                        uint32_t t2, uint32_t t3) {
+  const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
+  return __builtin_amdgcn_perm(hi, lo, (hib & 0x04040404u) | base);
+}
+
+// The low / high nibbles of a dword of packed indices.
+VH_DEV uint32_t lut_lo(uint32_t w, uint32_t base, const uint4& lv) {
+  return lut16(w & 0x07070707u, w >> 1, base, lv.x, lv.y, lv.z, lv.w);
+}
+VH_DEV uint32_t lut_hi(uint32_t w, uint32_t base, const uint4& lv) {
+  return lut16((w >> 4) & 0x07070707u, w >> 5, base, lv.x, lv.y, lv.z, lv.w);
+}
+
 // Kernels are specialised on the format kind (K_* below) so each instance
 // holds only its own closed form; the runtime-dispatch versions serve the
 // per-block scale maps.
