@@ -239,17 +239,21 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
       }
     }
   };
-  static_assert(ROUNDS <= 2, "two register sets");
   Set s[2];
-  // PRE: the chunk's rounds were all loaded before it starts
+  // Two register sets, double-buffered: round r + 2 is loaded into the set
+  // round r has just finished with, so a wave always has one round in
+  // flight while it computes another.  PRE: the chunk's first two rounds
+  // were loaded before it starts.
   auto chunk = [&](int c0, auto pre) __attribute__((always_inline)) {
+    if constexpr (!decltype(pre)::value) {
+      load(c0, s[0]);
+      if constexpr (ROUNDS > 1) load(c0 + UNROLL, s[1]);
+    }
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
-      if constexpr (!decltype(pre)::value)
-        if (r + 1 < ROUNDS) load(c0 + (r + 1) * UNROLL, s[(r + 1) & 1]);
       round(s[r & 1], c0 + r * UNROLL);
-      // keep later rounds' loads in place (two register sets, not ROUNDS):
-      // no memory access moves across this point
+      if (r + 2 < ROUNDS) load(c0 + (r + 2) * UNROLL, s[r & 1]);
+      // keep the loads in place: no memory access moves across this point
       asm volatile("" ::: "memory");
     }
   };
@@ -257,15 +261,12 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
   // empty range loads nothing: every access is past its buffer's end), and
   // the barrier waits for LDS only, so they stay in flight across it.
   load(b0, s[0]);
-  if constexpr (ROUNDS == 2) load(b0 + UNROLL, s[1]);
+  if constexpr (ROUNDS > 1) load(b0 + UNROLL, s[1]);
   if (tid < 256) s_scale[tid] = scale_value((uint32_t)tid, sfmt);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   // a range longer than NBW blocks runs in chunks of NBW
   if (b0 < b1) chunk(b0, std::true_type{});
-  for (int c0 = b0 + NBW; c0 < b1; c0 += NBW) {
-    load(c0, s[0]);
-    chunk(c0, std::false_type{});
-  }
+  for (int c0 = b0 + NBW; c0 < b1; c0 += NBW) chunk(c0, std::false_type{});
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
@@ -472,7 +473,7 @@ extern "C" int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t
   hipStream_t st = vh::as_stream(stream);
   const bool four = tiles >= 512 && tiles % 4 == 0 && K / 64 <= 2 * 16;
   // blocks per wave: the tile's K blocks over its K ranges, rounded up to 4,
-  // 8 or 16 (longer ranges in chunks of 16)
+  // 8, 16 or 32 (longer ranges in chunks of 32)
   const int64_t nb = K / 64;
   const int64_t kr = four ? 2 : 8, bpw = (nb + kr - 1) / kr;
   // two tiles per wave (the activation loads shared) while that leaves at
@@ -494,7 +495,8 @@ extern "C" int vh_gemv_nf4(const int8_t* x_levels, const float* x_scale, int64_t
     };
     if (bpw <= 4) launch(std::integral_constant<int, 4>{});
     else if (bpw <= 8) launch(std::integral_constant<int, 8>{});
-    else launch(std::integral_constant<int, 16>{});
+    else if (bpw <= 16) launch(std::integral_constant<int, 16>{});
+    else launch(std::integral_constant<int, 32>{});
   };
   if (M == 1) go(std::integral_constant<int, 1>{});
   else go(std::integral_constant<int, 4>{});
