@@ -8,14 +8,16 @@
 // the reference only by its bf16 rounding of each decoded operand (at most
 // 2**-9 relative per element), well inside the 1e-2 GEMM tolerance.
 //
-// Layout: a workgroup of 8 waves covers T 16-column tiles; the tile's K
-// blocks are split into 8 / T contiguous ranges, one per wave, so the T
-// waves of a range read the same activation bytes at the same time (they
-// hit in L1: the activations are re-read once per T tiles, not per tile).
+// Layout: a workgroup of 8 waves covers T 16-column tiles (TPW per wave);
+// the tile's K blocks are split into 8 / T contiguous ranges, one per wave,
+// so the T waves of a range read the same activation bytes at the same time
+// (they hit in L1: the activations are re-read once per T tiles, not per
+// tile), and a wave with two tiles loads the activation once for both.
 // Every load is issued per block straight from the baked layouts -- weight
 // nibbles in MFMA lane order (one coalesced 512-byte wave access per block),
 // the tile's 16 scale bytes of a block contiguous, the activations' scales
-// block-major [K/64][16] -- two rounds of UNROLL blocks in flight, with no
+// block-major [K/64][16] (at M > 1 one 16-byte load per lane per round,
+// staged through LDS) -- two rounds of UNROLL blocks in flight, with no
 // staging prologue; nibbles become int8 levels with three v_perm_b32 per 4
 // values, and a weight scale byte becomes its value through a 256-entry
 // table in LDS, decoded once per workgroup.  The K ranges meet through LDS
