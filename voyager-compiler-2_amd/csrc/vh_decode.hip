@@ -607,7 +607,16 @@ VH_DEV float rbf_hw(float x) { return __uint_as_float(f2bf2_hw(x, 0.0f) << 16); 
 // (max, sum, output) partial per query head.  Splits past the cache's groups
 // return at once (the combine merges only the live ones), so one launch
 // shape serves every cache length up to the capacity.
+// MFMA column n = 4 cg + h: the score MFMA repeats query head h in the four
+// columns n % 4 == h, so every lane holds its own head's scores, and the
+// value MFMA's column n carries p * s for value channel group cg of head h.
+// Of a 16-channel output tile only the columns of its own channel group are
+// kept, so each lane builds one column of value operands (one scale per
+// token) instead of four.  Only the query waits for memory before the
+// workgroup barrier: a wave's second group is still loading while its first
+// is computed.
 __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
+  static_assert(GQA * HEAD_DIM == SPLIT_WAVES * 64, "one rotated query element per thread");
   __shared__ __attribute__((aligned(64))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
   __shared__ __attribute__((aligned(16))) uint4 s_vprm[SPLIT_WAVES][GROUPS_PER_WAVE][32];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
@@ -619,10 +628,17 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
   if (!state_ok(a, n_main, n_res) || g_begin >= G) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, kq = lane >> 4;
+  const int cg = n >> 2, hq = n & 3;  // this lane's column: value channel group cg of query head hq
   const int b = P / a.nkv, kvh = P % a.nkv;
   const int pos = n_main + n_res;
 
-  // this wave's blocks go out first (an absent group re-reads a live one; it is skipped)
+  // the query element this thread rotates (head tid / 128, channel tid % 128) goes out first
+  const int qh = tid / HEAD_DIM, qc = tid % HEAD_DIM;
+  const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld + (kvh * GQA + qh) * HEAD_DIM;
+  uint32_t qv = qrow[qc], qp = qrow[qc < HEAD_DIM / 2 ? qc + HEAD_DIM / 2 : qc - HEAD_DIM / 2];
+  uint32_t qcs = a.rope[(int64_t)pos * HEAD_DIM + qc], qsn = a.rope[(a.max_pos + pos) * HEAD_DIM + qc];
+  asm volatile("" ::: "memory");
+  // then this wave's blocks, group by group (an absent group re-reads a live one; it is skipped)
   uint4 kc[GROUPS_PER_WAVE], vc[GROUPS_PER_WAVE], pr[GROUPS_PER_WAVE];
   int ng = 0;
   const uint8_t* seq = a.main + (int64_t)P * a.group_cap * GROUP_BYTES;
@@ -631,64 +647,52 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
     const int g = g_begin + i * SPLIT_WAVES + wave;
     ng += g < G ? 1 : 0;
     const uint8_t* blk = seq + (int64_t)(g < G ? g : G - 1) * GROUP_BYTES;
+    pr[i] = *(const uint4*)(blk + 2048 + lane * 16);
     kc[i] = *(const uint4*)(blk + lane * 16);
     vc[i] = *(const uint4*)(blk + 1024 + lane * 16);
-    pr[i] = *(const uint4*)(blk + 2048 + lane * 16);
   }
-  const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
-  const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
-  const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
-  for (int i = tid; i < GQA * HEAD_DIM; i += SPLIT_WAVES * 64) {
-    const int h = i / HEAD_DIM, c = i % HEAD_DIM;
-    s_q[h][c] = rope1(qrow + (kvh * GQA + h) * HEAD_DIM, cs_, sn_, c);
+  // waits for the query alone; the blocks stay in flight across the barrier
+  asm volatile("" : "+v"(qv), "+v"(qp), "+v"(qcs), "+v"(qsn)::"memory");
+  {
+    const float x = bf2f(qv), xr = qc < HEAD_DIM / 2 ? -bf2f(qp) : bf2f(qp);
+    s_q[qh][qc] = (uint16_t)f2bf(rbf(x * bf2f(qcs)) + rbf(xr * bf2f(qsn)));
   }
-  // value parameters (lanes 32-63) to LDS; the largest value scale of the wave's groups
-  float vmax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
-    if (lane >= 32) {
-      s_vprm[wave][i][lane - 32] = pr[i];
-      if (i < ng) {
-        const f16x8 e = __builtin_bit_cast(f16x8, pr[i]);
-        vmax = fmaxf(vmax, fmaxf(fmaxf((float)e[0], (float)e[2]), fmaxf((float)e[4], (float)e[6])));
-      }
-    }
-  }
-  vmax = max_x32(max_x16(vmax));
-  vmax = fmaxf(vmax, __shfl_xor(vmax, 8));
-  vmax = fmaxf(vmax, __shfl_xor(vmax, 4));
-  vmax = fmaxf(vmax, __shfl_xor(vmax, 2));
-  vmax = fmaxf(vmax, __shfl_xor(vmax, 1));
-  const int ve = (vmax > 0.0f && vmax < __builtin_inff()) ? floor_log2(vmax) : 0;
-  const float bscale = ldexpf(1.0f, V_EXP - ve), oscale = ldexpf(1.0f, ve - V_EXP);
-  __syncthreads();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  const bool head_lane = n < GQA;
-  // key B operands: q[head n][32 kq + 8 cs + j] (zero past the heads)
+  // key B operands: q[head hq][32 kq + 8 cs + j], the same in the four columns of a head
   bf16x8 Bq[4];
 #pragma unroll
-  for (int cs = 0; cs < 4; ++cs) {
-    const uint4 v = head_lane ? *(const uint4*)&s_q[n][32 * kq + 8 * cs] : make_uint4(0u, 0u, 0u, 0u);
-    Bq[cs] = __builtin_bit_cast(bf16x8, v);
-  }
+  for (int cs = 0; cs < 4; ++cs) Bq[cs] = __builtin_bit_cast(bf16x8, *(const uint4*)&s_q[hq][32 * kq + 8 * cs]);
   const CodeMasks cm = code_masks();
   const f16x8 NEG = __builtin_bit_cast(f16x8, make_uint4(0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u));
-  float m = -__builtin_inff(), lsum = 0.0f;
-  float zt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -__builtin_inff(), lsum = 0.0f, zt = 0.0f, vmax = 0.0f;
+  int ve = 0;
   f32x4 acc[8];
 #pragma unroll
   for (int r8 = 0; r8 < 8; ++r8) acc[r8] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll
-  for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
-    if (i >= ng) break;
+  // one group (i constant at each call: the block registers stay unindexed)
+  auto group = [&](const int i) __attribute__((always_inline)) {
+    // value parameters (lanes 32-63) to LDS; the largest value scale of the
+    // wave's groups so far sets the value operands' exponent
+    if (lane >= 32) {
+      s_vprm[wave][i][lane - 32] = pr[i];
+      const f16x8 e = __builtin_bit_cast(f16x8, pr[i]);
+      vmax = fmaxf(vmax, fmaxf(fmaxf((float)e[0], (float)e[2]), fmaxf((float)e[4], (float)e[6])));
+    }
+    vmax = max_x32(max_x16(vmax));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 8));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 4));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 2));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 1));
+    const int ve_new = (vmax > 0.0f && vmax < __builtin_inff()) ? floor_log2(vmax) : 0;
     // this group's key table (lanes 0-31 build it; the wave's LDS accesses
     // stay in order, and the previous group's reads precede these writes)
     if (lane < 32) build_key_table(pr[i], lane, s_tab[wave]);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // scores: S[tile][r] = q[head n] . k[token 16 tile + 4 kq + r]; operand
+    // scores: S[tile][r] = q[head hq] . k[token 16 tile + 4 kq + r]; operand
     // dword p of channel chunk cs is the table entry of its code nibble
     const uint8_t* tab = s_tab[wave] + kq * KEY_TAB_BLOCK;
     f32x4 S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
@@ -728,55 +732,55 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
       ps += p[j];
     }
     lsum = lsum * alpha + ps;
-    if (i > 0) {  // the first group starts from zero
+    if (i > 0) {  // the first group starts from zero; a new exponent rescales by a power of two (exact)
+      const float f = alpha * ldexpf(1.0f, ve - ve_new);
+      zt *= f;
 #pragma unroll
-      for (int cg = 0; cg < 4; ++cg) zt[cg] *= alpha;
-#pragma unroll
-      for (int r8 = 0; r8 < 8; ++r8) acc[r8] *= alpha;
+      for (int r8 = 0; r8 < 8; ++r8) acc[r8] *= f;
     }
-    // value B operands per channel group: p * s * 2**(V_EXP - ve) * 4**-(j / 2)
-    // (zero past the heads); the zero-point terms accumulate p * s * zp in the
+    ve = ve_new;
+    // value B operands of column (cg, hq): p * s * 2**(V_EXP - ve) * 4**-(j / 2)
+    // at the lane's tokens; the zero-point term accumulates p * s * zp in the
     // same 2**(V_EXP - ve) units
-    const float vf = head_lane ? bscale : 0.0f;
-    const uint8_t* vprm = (const uint8_t*)s_vprm[wave][i];
-    uint32_t bv[4][4];
+    const float bscale = ldexpf(1.0f, V_EXP - ve);
+    const uint8_t* vprm = (const uint8_t*)s_vprm[wave][i] + cg * 4;
+    uint32_t bv[4];
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
-      const f16x8 e0 = *(const f16x8*)(vprm + (kq * 8 + 2 * pp) * 16);
-      const f16x8 e1 = *(const f16x8*)(vprm + (kq * 8 + 2 * pp + 1) * 16);
-      const float f = vf * (1.0f / (float)(1 << (2 * pp)));
+      const f16x2 e0 = *(const f16x2*)(vprm + (kq * 8 + 2 * pp) * 16);
+      const f16x2 e1 = *(const f16x2*)(vprm + (kq * 8 + 2 * pp + 1) * 16);
+      const float f = bscale * (1.0f / (float)(1 << (2 * pp)));
       const float p0 = p[2 * pp] * f, p1 = p[2 * pp + 1] * f;
-#pragma unroll
-      for (int cg = 0; cg < 4; ++cg) {
-        const float b0 = fmaf(p0, (float)e0[2 * cg], 0.0f), b1 = fmaf(p1, (float)e1[2 * cg], 0.0f);
-        const float z = fmaf(b1, (float)e1[2 * cg + 1], b0 * (float)e0[2 * cg + 1]);
-        zt[cg] = fmaf(z, (float)(1 << (2 * pp)), zt[cg]);
-        bv[cg][pp] = pack_h2(b0, b1);
-      }
+      const float b0 = fmaf(p0, (float)e0[0], 0.0f), b1 = fmaf(p1, (float)e1[0], 0.0f);
+      const float z = fmaf(b1, (float)e1[1], b0 * (float)e0[1]);
+      zt = fmaf(z, (float)(1 << (2 * pp)), zt);
+      bv[pp] = pack_h2(b0, b1);
     }
+    const f16x8 B = __builtin_bit_cast(f16x8, make_uint4(bv[0], bv[1], bv[2], bv[3]));
     const uint32_t vw[4] = {vc[i].x, vc[i].y, vc[i].z, vc[i].w};
 #pragma unroll
     for (int r8 = 0; r8 < 8; ++r8) {
-      const f16x8 B = __builtin_bit_cast(f16x8, make_uint4(bv[r8 >> 1][0], bv[r8 >> 1][1], bv[r8 >> 1][2],
-                                                           bv[r8 >> 1][3]));
       acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(vw[r8 >> 1], r8 & 1, cm), B, acc[r8], 0, 0, 0);
       acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(NEG, B, acc[r8], 0, 0, 0);
     }
-  }
-  // wave totals: sums over the lane quarters; output o[head n][16 r8 + 4 kq + r]
+  };
+  static_assert(GROUPS_PER_WAVE == 2, "two group calls");
+  if (ng > 0) group(0);
+  if (ng > 1) group(1);
+  // wave totals: sums over the lane quarters; column (cg, hq) keeps the
+  // channel tiles of its group, o[head hq][16 r8 + 4 kq + r] for r8 / 2 == cg
   lsum = sum_x32(sum_x16(lsum));
+  zt = sum_x32(sum_x16(zt));
+  const float oscale = ldexpf(1.0f, ve - V_EXP);
 #pragma unroll
-  for (int cg = 0; cg < 4; ++cg) zt[cg] = sum_x32(sum_x16(zt[cg]));
-  if (head_lane) {
+  for (int r8 = 0; r8 < 8; ++r8)
+    if ((r8 >> 1) == cg) {
 #pragma unroll
-    for (int r8 = 0; r8 < 8; ++r8)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        s_part[wave][n][2 + 16 * r8 + 4 * kq + r] = (acc[r8][r] - zt[r8 >> 1]) * oscale;
-    if (kq == 0) {
-      s_part[wave][n][0] = m;
-      s_part[wave][n][1] = lsum;
+      for (int r = 0; r < 4; ++r) s_part[wave][hq][2 + 16 * r8 + 4 * kq + r] = (acc[r8][r] - zt) * oscale;
     }
+  if (n < GQA && kq == 0) {
+    s_part[wave][hq][0] = m;
+    s_part[wave][hq][1] = lsum;
   }
   __syncthreads();
   // merge the waves: thread (head, channel)
@@ -1118,14 +1122,19 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   // sequence's chunk into the main cache (no other workgroup writes it, and
   // this step reads no main group at or past g0); then the last workgroup to
   // finish -- every one has read the state by then -- writes the new state.
+  // The counter needs no fence: what it orders is every workgroup's state
+  // read (consumed, and past the workgroup barriers above, before its
+  // increment is issued) before the last one's state write; everything else
+  // this kernel writes is read by later launches only, which the kernel
+  // boundary orders.  (An agent-scope fence here writes back the XCD's L2 in
+  // every workgroup: it cost 2.3 us per step.)
   const bool fold = n_res + 1 == RES_CAP;
   const int g0 = n_main / KV_GROUP;
   const bool room = g0 + GROUPS_PER_CHUNK <= a.group_cap;
   if (fold && room && h == 0) fold_chunk(a, P, g0, s_newk, s_newv, s_fold, flag);
   if (tid == 0) {
     if (fold && !room && bh == 0) atomicOr(flag, VH_DECODE_ERR_KV_FULL);
-    __threadfence();
-    const int done = atomicAdd(&a.state[2], 1);
+    const int done = __hip_atomic_fetch_add(&a.state[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (done == (int)gridDim.x - 1) {
       if (fold && room) {
         a.state[0] = n_main + RES_CAP;
@@ -1134,7 +1143,6 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
         a.state[1] = n_res + 1;
       }
       a.state[2] = 0;
-      __threadfence();
     }
   }
 }
