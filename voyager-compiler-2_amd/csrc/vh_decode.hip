@@ -568,34 +568,30 @@ constexpr int PAIR_TAB = 16 * 4;
 constexpr int KEY_TAB_BLOCK = 16 * PAIR_TAB + 64;
 constexpr int KEY_TAB_BYTES = 4 * KEY_TAB_BLOCK;
 
-// Lanes 0-31: the pairs of channels 4 l .. 4 l + 3 from the lane's parameter
-// piece (fp16 scale / zero point pairs).
-VH_DEV void build_key_table(const uint4& piece, int lane, uint8_t* tab) {
-  const f16x8 e = __builtin_bit_cast(f16x8, piece);
-  uint32_t v01[4], v23[4];  // per channel: keys of codes 0, 1 and 2, 3 (bf16 pairs)
+// One pair of channels from its fp16 (scale, zero point) pairs [s0, z0, s1,
+// z1]: the 16 entries (every code pair) at dst.
+VH_DEV void build_key_pair(const uint2& prm, uint8_t* dst) {
+  const f16x2 e0 = __builtin_bit_cast(f16x2, prm.x), e1 = __builtin_bit_cast(f16x2, prm.y);
+  uint32_t v01[2], v23[2];  // per channel: keys of codes 0, 1 and 2, 3 (bf16 pairs)
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float sc = (float)e[2 * q], zp = (float)e[2 * q + 1];
+  for (int q = 0; q < 2; ++q) {
+    const float sc = (float)(q ? e1[0] : e0[0]), zp = (float)(q ? e1[1] : e0[1]);
     const uint32_t t01 = f2bf2_hw(0.0f - zp, 1.0f - zp), t23 = f2bf2_hw(2.0f - zp, 3.0f - zp);
     v01[q] = f2bf2_hw(__uint_as_float(t01 << 16) * sc, __uint_as_float(t01 & 0xffff0000u) * sc);
     v23[q] = f2bf2_hw(__uint_as_float(t23 << 16) * sc, __uint_as_float(t23 & 0xffff0000u) * sc);
   }
-  uint8_t* dst = tab + (lane >> 3) * KEY_TAB_BLOCK + (lane & 7) * 2 * PAIR_TAB;
+  uint32_t ent[16];
 #pragma unroll
-  for (int pr = 0; pr < 2; ++pr) {
-    uint32_t ent[16];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int c0 = v & 3, c1 = v >> 2;
-      // bytes 0-3 of the selection: channel 2 pr's key of c0 (low), channel 2 pr + 1's of c1 (high)
-      const uint32_t lo = c0 < 2 ? v01[2 * pr] : v23[2 * pr], hi = c1 < 2 ? v01[2 * pr + 1] : v23[2 * pr + 1];
-      const uint32_t sl = (uint32_t)(2 * (c0 & 1)), sh = (uint32_t)(4 + 2 * (c1 & 1));
-      ent[v] = __builtin_amdgcn_perm(hi, lo, sl | (sl + 1) << 8 | sh << 16 | (sh + 1) << 24);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      *(uint4*)(dst + pr * PAIR_TAB + 16 * k) = make_uint4(ent[4 * k], ent[4 * k + 1], ent[4 * k + 2], ent[4 * k + 3]);
+  for (int v = 0; v < 16; ++v) {
+    const int c0 = v & 3, c1 = v >> 2;
+    // bytes 0-3 of the selection: channel 0's key of c0 (low), channel 1's of c1 (high)
+    const uint32_t lo = c0 < 2 ? v01[0] : v23[0], hi = c1 < 2 ? v01[1] : v23[1];
+    const uint32_t sl = (uint32_t)(2 * (c0 & 1)), sh = (uint32_t)(4 + 2 * (c1 & 1));
+    ent[v] = __builtin_amdgcn_perm(hi, lo, sl | (sl + 1) << 8 | sh << 16 | (sh + 1) << 24);
   }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    *(uint4*)(dst + 16 * k) = make_uint4(ent[4 * k], ent[4 * k + 1], ent[4 * k + 2], ent[4 * k + 3]);
 }
 
 // bf16 rounding on the hardware converter (round half to even).
@@ -618,7 +614,7 @@ VH_DEV float rbf_hw(float x) { return __uint_as_float(f2bf2_hw(x, 0.0f) << 16); 
 __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
   static_assert(GQA * HEAD_DIM == SPLIT_WAVES * 64, "one rotated query element per thread");
   __shared__ __attribute__((aligned(64))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
-  __shared__ __attribute__((aligned(16))) uint4 s_vprm[SPLIT_WAVES][GROUPS_PER_WAVE][32];
+  __shared__ __attribute__((aligned(16))) uint4 s_prm[SPLIT_WAVES][GROUPS_PER_WAVE][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
   __shared__ float s_part[SPLIT_WAVES][GQA][PART];
   const int n_main = a.state[0], n_res = a.state[1];
@@ -673,10 +669,11 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
 
   // one group (i constant at each call: the block registers stay unindexed)
   auto group = [&](const int i) __attribute__((always_inline)) {
-    // value parameters (lanes 32-63) to LDS; the largest value scale of the
-    // wave's groups so far sets the value operands' exponent
+    // the group's parameters (keys: lanes 0-31, values: lanes 32-63) to LDS;
+    // the largest value scale of the wave's groups so far sets the value
+    // operands' exponent
+    s_prm[wave][i][lane] = pr[i];
     if (lane >= 32) {
-      s_vprm[wave][i][lane - 32] = pr[i];
       const f16x8 e = __builtin_bit_cast(f16x8, pr[i]);
       vmax = fmaxf(vmax, fmaxf(fmaxf((float)e[0], (float)e[2]), fmaxf((float)e[4], (float)e[6])));
     }
@@ -686,9 +683,11 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
     vmax = fmaxf(vmax, __shfl_xor(vmax, 2));
     vmax = fmaxf(vmax, __shfl_xor(vmax, 1));
     const int ve_new = (vmax > 0.0f && vmax < __builtin_inff()) ? floor_log2(vmax) : 0;
-    // this group's key table (lanes 0-31 build it; the wave's LDS accesses
-    // stay in order, and the previous group's reads precede these writes)
-    if (lane < 32) build_key_table(pr[i], lane, s_tab[wave]);
+    // this group's key table, lane l the pair of channels 2 l, 2 l + 1 (the
+    // wave's LDS accesses stay in order: the parameters above land first, and
+    // the previous group's reads precede these writes)
+    build_key_pair(*(const uint2*)((const uint8_t*)s_prm[wave][i] + 8 * lane),
+                   s_tab[wave] + (lane >> 4) * KEY_TAB_BLOCK + (lane & 15) * PAIR_TAB);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -743,7 +742,7 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
     // at the lane's tokens; the zero-point term accumulates p * s * zp in the
     // same 2**(V_EXP - ve) units
     const float bscale = ldexpf(1.0f, V_EXP - ve);
-    const uint8_t* vprm = (const uint8_t*)s_vprm[wave][i] + cg * 4;
+    const uint8_t* vprm = (const uint8_t*)&s_prm[wave][i][32] + cg * 4;
     uint32_t bv[4];
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
