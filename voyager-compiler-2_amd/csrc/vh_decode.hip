@@ -516,6 +516,14 @@ VH_DEV float eager_score_log2(float qk, float scale) {
   return __uint_as_float(f2bf2_hw(__uint_as_float(f2bf2_hw(qk, 0.0f) << 16) * scale, 0.0f) << 16) * LOG2E;
 }
 
+// Two scores through the same chain, each bf16 rounding done for both by
+// one packed conversion (the same rounding as one at a time).
+VH_DEV float2 eager_score_log2_x2(float qk0, float qk1, float scale) {
+  const uint32_t t = f2bf2_hw(qk0, qk1);
+  const uint32_t u = f2bf2_hw(__uint_as_float(t << 16) * scale, __uint_as_float(t & 0xffff0000u) * scale);
+  return make_float2(__uint_as_float(u << 16) * LOG2E, __uint_as_float(u & 0xffff0000u) * LOG2E);
+}
+
 VH_DEV uint16_t rope1(const uint16_t* base, const uint16_t* cs, const uint16_t* sn, int c) {
   const float x = bf2f(base[c]);
   const float xr = c < HEAD_DIM / 2 ? -bf2f(base[c + HEAD_DIM / 2]) : bf2f(base[c - HEAD_DIM / 2]);
@@ -562,11 +570,35 @@ VH_DEV f16x8 code_operand(uint32_t W, int half, const CodeMasks& m) {
 // zero_point) * scale, each bfloat16 op rounding its result as the
 // reference's dequantize does (ops/quantized.py:518-571).  An MFMA operand
 // dword is then one 32-bit LDS read at its pair's table + 4 * nibble.
-// Blocks kq are KEY_TAB_BLOCK bytes apart (a 64-byte pad spreads the four
-// blocks a wave reads at once over the LDS banks).
+// Pair 4 cs + p of block kq sits at byte 272 (4 cs + p) + 64 kq of the
+// wave's 256-byte-aligned table.  The low address byte before the row
+// offset, 64 kq + 4 * nibble, is one byte of a precomputed word
+// (KeyNibbles), so an address is one v_perm_b32 of that word and the table's
+// base, and the row offset is the read's immediate.  The four blocks a read
+// touches fall in distinct LDS banks, and so do the 16 rows a quarter-wave
+// writes (the 16-byte skew of the 272-byte rows).
 constexpr int PAIR_TAB = 16 * 4;
-constexpr int KEY_TAB_BLOCK = 16 * PAIR_TAB + 64;
-constexpr int KEY_TAB_BYTES = 4 * KEY_TAB_BLOCK;
+constexpr int KEY_TAB_ROW = 4 * PAIR_TAB + 16;
+constexpr int KEY_TAB_BYTES = 16 * KEY_TAB_ROW;
+static_assert(KEY_TAB_BYTES % 256 == 0, "every wave's table 256-byte aligned");
+
+// The two words whose bytes are 64 kq + 4 * nibble for the even (lo) and
+// odd (hi) nibbles of a code dword D: nibble 2 b in byte b of lo, 2 b + 1
+// in byte b of hi.
+struct KeyNibbles {
+  uint32_t lo, hi;
+};
+
+VH_DEV KeyNibbles key_nibbles(uint32_t D, uint32_t kq_bytes) {
+  return {((D << 2) & 0x3c3c3c3cu) | kq_bytes, ((D >> 2) & 0x3c3c3c3cu) | kq_bytes};
+}
+
+// LDS address of nibble `nib` (0-7) of D in the table at `base` (256-byte
+// aligned); the pair's row offset goes into the read's immediate.
+VH_DEV uint32_t key_entry_addr(const KeyNibbles& kn, int nib, uint32_t base) {
+  const uint32_t sel = (uint32_t)(nib >> 1) | 0x07060500u;
+  return __builtin_amdgcn_perm(base, (nib & 1) ? kn.hi : kn.lo, sel);
+}
 
 // One pair of channels from its fp16 (scale, zero point) pairs [s0, z0, s1,
 // z1]: the 16 entries (every code pair) at dst.
@@ -613,7 +645,7 @@ VH_DEV float rbf_hw(float x) { return __uint_as_float(f2bf2_hw(x, 0.0f) << 16); 
 // is computed.
 __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
   static_assert(GQA * HEAD_DIM == SPLIT_WAVES * 64, "one rotated query element per thread");
-  __shared__ __attribute__((aligned(64))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
+  __shared__ __attribute__((aligned(256))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
   __shared__ __attribute__((aligned(16))) uint4 s_prm[SPLIT_WAVES][GROUPS_PER_WAVE][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
   __shared__ float s_part[SPLIT_WAVES][GQA][PART];
@@ -625,6 +657,7 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, kq = lane >> 4;
   const int cg = n >> 2, hq = n & 3;  // this lane's column: value channel group cg of query head hq
+  const uint32_t kq_bytes = (uint32_t)kq * 0x40404040u;  // 64 kq in every byte: the key table block
   const int b = P / a.nkv, kvh = P % a.nkv;
   const int pos = n_main + n_res;
 
@@ -687,37 +720,42 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
     // wave's LDS accesses stay in order: the parameters above land first, and
     // the previous group's reads precede these writes)
     build_key_pair(*(const uint2*)((const uint8_t*)s_prm[wave][i] + 8 * lane),
-                   s_tab[wave] + (lane >> 4) * KEY_TAB_BLOCK + (lane & 15) * PAIR_TAB);
+                   s_tab[wave] + (lane & 15) * KEY_TAB_ROW + (lane >> 4) * PAIR_TAB);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // scores: S[tile][r] = q[head hq] . k[token 16 tile + 4 kq + r]; operand
     // dword p of channel chunk cs is the table entry of its code nibble
-    const uint8_t* tab = s_tab[wave] + kq * KEY_TAB_BLOCK;
+    const uint32_t tab = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)s_tab[wave];
     f32x4 S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
     const uint32_t kd[4] = {kc[i].x, kc[i].y, kc[i].z, kc[i].w};
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int cs = 0; cs < 4; ++cs) {
-        const uint32_t D = kd[2 * t + (cs >> 1)];
-        uint32_t w[4];
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const KeyNibbles kn = key_nibbles(kd[2 * t + h2], kq_bytes);
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const int nib = 4 * (cs & 1) + p;
-          const uint32_t off = (nib ? (D >> (4 * nib - 2)) : (D << 2)) & 0x3cu;
-          w[p] = *(const uint32_t*)(tab + off + (4 * cs + p) * PAIR_TAB);
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const int cs = 2 * h2 + c2;
+          uint32_t w[4];
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint32_t addr = key_entry_addr(kn, 4 * c2 + p, tab);
+            w[p] = *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)(addr + (4 * cs + p) * KEY_TAB_ROW);
+          }
+          S[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3])), Bq[cs], S[t], 0, 0, 0);
         }
-        S[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3])),
-                                                       Bq[cs], S[t], 0, 0, 0);
       }
     // online softmax (every lane of a head holds its running max)
     float sc[8];
     float mg = -__builtin_inff();
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sc[j] = eager_score_log2(S[j >> 2][j & 3], a.scale);
-      mg = fmaxf(mg, sc[j]);
+    for (int j = 0; j < 8; j += 2) {
+      const float2 s2 = eager_score_log2_x2(S[j >> 2][j & 3], S[j >> 2][(j & 3) + 1], a.scale);
+      sc[j] = s2.x;
+      sc[j + 1] = s2.y;
+      mg = fmaxf(mg, fmaxf(s2.x, s2.y));
     }
     mg = max_x32(max_x16(mg));
     const float m_new = fmaxf(m, mg);
