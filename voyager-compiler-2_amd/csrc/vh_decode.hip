@@ -1030,7 +1030,14 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   const int n_main = a.state[0], n_res = a.state[1];
   const int pos = n_main + n_res;
   const int splits = (n_main / KV_GROUP + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
-  const int bh = blockIdx.x, b = bh / a.nq, H = bh % a.nq, kvh = H / GQA, h = H % GQA;
+  // Workgroups go to the 8 XCDs round-robin: XCD x takes the contiguous
+  // range x * G / 8 + [0, G / 8) of (batch, head) rows when that keeps the
+  // GQA heads of a kv head together (G % 32 == 0), so a residual window is
+  // read into one XCD's L2 rather than four.
+  const int G = (int)gridDim.x;
+  const int bid = (int)blockIdx.x;
+  const int bh = G % (8 * GQA) == 0 ? (bid & 7) * (G >> 3) + (bid >> 3) : bid;
+  const int b = bh / a.nq, H = bh % a.nq, kvh = H / GQA, h = H % GQA;
   const int P = b * a.nkv + kvh, tid = threadIdx.x;
   if (!state_ok(a, n_main, n_res)) {
     if (tid < HEAD_DIM) {
