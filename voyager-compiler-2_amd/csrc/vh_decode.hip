@@ -626,9 +626,6 @@ VH_DEV void build_key_pair(const uint2& prm, uint8_t* dst) {
     *(uint4*)(dst + 16 * k) = make_uint4(ent[4 * k], ent[4 * k + 1], ent[4 * k + 2], ent[4 * k + 3]);
 }
 
-// bf16 rounding on the hardware converter (round half to even).
-VH_DEV float rbf_hw(float x) { return __uint_as_float(f2bf2_hw(x, 0.0f) << 16); }
-
 // Workgroups (split, P) stream the main cache: wave w takes groups
 // GROUPS_PER_SPLIT split + SPLIT_WAVES i + w (i < GROUPS_PER_WAVE) with one
 // online softmax, the waves merge through LDS and the workgroup leaves one
