@@ -433,8 +433,9 @@ typedef struct vh_kivi_desc {
   int64_t max_pos;
   uint8_t* main;           /* main cache [P][group_cap][3072] (vh_kivi_bake) */
   int64_t group_cap;       /* groups of 32 tokens the main cache holds per sequence */
-  uint16_t* kr;            /* residual window (this step's key and value are written to slot n_res) */
-  uint16_t* vr;
+  uint16_t* kr;            /* residual window, bf16 [P][VH_KIVI_RES_CAP][128]: every slot is read (those past
+                              the state's n_res are masked), this step's key and value land in slot n_res */
+  uint16_t* vr;            /* the same for values */
   int32_t* state;          /* device int32[4], see above */
   int64_t batch, nkv, nq, head_dim; /* nq == 4 nkv, head_dim == 128 */
   float softmax_scale;     /* 1 / sqrt(head_dim) */

@@ -1024,9 +1024,6 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   __shared__ float s_red[4];
   __shared__ uint16_t s_newk[HEAD_DIM], s_newv[HEAD_DIM];
   __shared__ FoldLds s_fold;
-  const int n_main = a.state[0], n_res = a.state[1];
-  const int pos = n_main + n_res;
-  const int splits = (n_main / KV_GROUP + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
   // Workgroups go to the 8 XCDs round-robin: XCD x takes the contiguous
   // range x * G / 8 + [0, G / 8) of (batch, head) rows when that keeps the
   // GQA heads of a kv head together (G % 32 == 0), so a residual window is
@@ -1036,6 +1033,38 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   const int bh = G % (8 * GQA) == 0 ? (bid & 7) * (G >> 3) + (bid >> 3) : bid;
   const int b = bh / a.nq, H = bh % a.nq, kvh = H / GQA, h = H % GQA;
   const int P = b * a.nkv + kvh, tid = threadIdx.x;
+  // the state is read first, its value used only after the loads below are out
+  const int2 st = *(const int2*)a.state;
+  const int c = tid & (HEAD_DIM - 1);              // channel (first half of the block: merge / output)
+  const int tk = tid >> 1, kh = tid & 1;           // key row tk, channel half kh
+  const int co = tid & 15, ts = tid >> 4;          // value octet co, token subset ts (slots ts + 16u)
+  const bool merger = tid < HEAD_DIM;
+  // The residual window and the split partials go out before the state is
+  // read: their addresses do not depend on it (every slot of the window and
+  // every split of the partials is allocated), and what the state leaves
+  // unused is masked once it arrives.
+  uint4 kw[HEAD_DIM / 16], vw[RES_CAP / 16];
+  const uint4* kp = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + tk) * HEAD_DIM + kh * (HEAD_DIM / 2));
+  const uint4* vp = (const uint4*)(a.vr + (int64_t)P * RES_CAP * HEAD_DIM) + co;
+#pragma unroll
+  for (int i = 0; i < HEAD_DIM / 16; ++i) kw[i] = kp[i];
+#pragma unroll
+  for (int u = 0; u < RES_CAP / 16; ++u) vw[u] = vp[(int64_t)(ts + 16 * u) * (HEAD_DIM / 8)];
+  const float* base = a.part + ((int64_t)P * a.splits_cap * GQA + h) * PART;
+  float pm[COMBINE_PRELOAD], pl[COMBINE_PRELOAD], po[COMBINE_PRELOAD];
+#pragma unroll
+  for (int s = 0; s < COMBINE_PRELOAD; ++s) {
+    // no predicate: a split past the capacity re-reads the last one
+    const int se = s < a.splits_cap ? s : a.splits_cap - 1;
+    const float* ps = base + (int64_t)se * GQA * PART;
+    pm[s] = ps[0];
+    pl[s] = ps[1];
+    po[s] = ps[2 + c];
+  }
+  asm volatile("" ::: "memory");  // the loads above are issued before the state is used
+  const int n_main = st.x, n_res = st.y;
+  const int pos = n_main + n_res;
+  const int splits = (n_main / KV_GROUP + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
   if (!state_ok(a, n_main, n_res)) {
     if (tid < HEAD_DIM) {
       const int64_t idx = (int64_t)b * a.nq * HEAD_DIM + H * HEAD_DIM + tid;
@@ -1045,32 +1074,21 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
     if (bh == 0 && tid == 0) atomicOr(flag, VH_DECODE_ERR_KV_STATE);
     return;
   }
-  const int c = tid & (HEAD_DIM - 1);              // channel (first half of the block: merge / output)
-  const int tk = tid >> 1, kh = tid & 1;           // key row tk, channel half kh
-  const int co = tid & 15, ts = tid >> 4;          // value octet co, token subset ts (slots ts + 16u)
+  // slots past the window and splits past the cache hold stale bytes (a
+  // zero weight times a stale infinity would be NaN): cleared
+#pragma unroll
+  for (int u = 0; u < RES_CAP / 16; ++u)
+    if (ts + 16 * u >= n_res) vw[u] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int s = 0; s < COMBINE_PRELOAD; ++s)
+    if (s >= splits) {
+      pm[s] = -__builtin_inff();
+      pl[s] = 0.0f;
+      po[s] = 0.0f;
+    }
   const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
   const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
   const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
-  // every independent load goes out first (one round trip)
-  uint4 kw[HEAD_DIM / 16], vw[RES_CAP / 16];
-  const uint4* kp = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + tk) * HEAD_DIM + kh * (HEAD_DIM / 2));
-  const uint4* vp = (const uint4*)(a.vr + (int64_t)P * RES_CAP * HEAD_DIM) + co;
-#pragma unroll
-  for (int i = 0; i < HEAD_DIM / 16; ++i) kw[i] = tk < n_res ? kp[i] : make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-  for (int u = 0; u < RES_CAP / 16; ++u)
-    vw[u] = ts + 16 * u < n_res ? vp[(int64_t)(ts + 16 * u) * (HEAD_DIM / 8)] : make_uint4(0u, 0u, 0u, 0u);
-  const float* base = a.part + ((int64_t)P * a.splits_cap * GQA + h) * PART;
-  float pm[COMBINE_PRELOAD], pl[COMBINE_PRELOAD], po[COMBINE_PRELOAD];
-  const bool merger = tid < HEAD_DIM;
-#pragma unroll
-  for (int s = 0; s < COMBINE_PRELOAD; ++s) {
-    const bool ok = merger && s < splits;
-    const float* ps = base + (int64_t)s * GQA * PART;
-    pm[s] = ok ? ps[0] : -__builtin_inff();
-    pl[s] = ok ? ps[1] : 0.0f;
-    po[s] = ok ? ps[2 + c] : 0.0f;
-  }
   // RoPE of this step's query / key (channel c; the second half of the block duplicates)
   const float qc = bf2f(rope1(qrow + H * HEAD_DIM, cs_, sn_, c));
   const uint16_t kn = rope1(qrow + (a.nq + kvh) * HEAD_DIM, cs_, sn_, c);
