@@ -194,6 +194,46 @@ def test_bf16_tile_sweep(tile):
     assert max_rel_err(out, ref) < 1e-5
 
 
+@pytest.mark.parametrize("fam,tile", [("bf16", t) for t in BF16_DIRECT_TILES] +
+                         [("fp8", t) for t in (20, 24, 31, 35, 41, 44, 48)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_direct_tile_bias_epilogue(fam, tile, out_dtype):
+    """The direct-to-LDS tiles' bias instantiation (plain epilogue with alpha
+    and a bias, bf16 or float32 bias alternating with the tile, bf16 or
+    float32 output) at one ragged size against float64.  Alpha brings the
+    products to the bias's magnitude (E4M3 grid values are up to 448), so a
+    wrong or missing bias moves the result far past the tolerance."""
+    M, N, K = SWEEP
+    if fam == "bf16":
+        a, b = _rand((M, K), 70), _rand((N, K), 71, 0.05)
+        ac, bc = a.cuda(), b.cuda()
+        av, bv = a.double(), b.double()
+        fmt, lda, family, al, tol32 = gemm.OP_BF16, K * 2, gemm.FAMILY_DIRECT_BF16, 0.75, 1e-5
+    else:
+        ac, bc, _, _, xq, wq = _fp8_operands(M, N, K, 72)
+        av, bv = xq.double(), wq.double()
+        # fp32 sums of ~1e5-sized products: 1e-4 of the largest output
+        fmt, lda, family, al, tol32 = gemm.OP_FP8, K, gemm.FAMILY_DIRECT_FP8, 2.0 ** -16, 1e-4
+    bias = _rand((N,), 73)
+    bias_dev = bias.cuda() if tile % 2 else bias.float().cuda()
+    alpha = torch.tensor(al, device="cuda")
+    out = torch.empty(M, N, dtype=out_dtype, device="cuda")
+    d = gemm.GemmDesc()
+    d.A, d.B, d.C = ac.data_ptr(), bc.data_ptr(), out.data_ptr()
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb, d.ldc = lda, lda, N
+    d.a_fmt = d.b_fmt = fmt
+    d.tile_hint = tile
+    d.epi = gemm._epilogue(gemm.EPI_PLAIN, out_dtype, alpha, bias_dev)
+    with _Plans() as log:
+        gemm.run(d, ac.device)
+    assert log == [(family, tile, 1, M, N, K)]
+    ref = (av @ bv.T) * al + bias.double()
+    assert max_rel_err(out, ref) < (TOL if out_dtype == torch.bfloat16 else tol32)
+    # the bias is a visible part of the result
+    assert max_rel_err(ref - bias.double(), ref) > 10 * (TOL if out_dtype == torch.bfloat16 else tol32)
+
+
 def test_posit8_in_staging_tiles():
     """The posit8 operands decoded in the register-staged kernel's staging
     (a tile hint), every staged tile, against the oracle."""

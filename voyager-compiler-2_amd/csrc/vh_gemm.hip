@@ -179,6 +179,36 @@ __device__ __forceinline__ float epi_scale(const vh_epilogue& e) {
   return e.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)e.scale) : *(const float*)e.scale;
 }
 
+// The biases of NB columns col_of(k), 0 past N.  Each load is clamped into
+// the row, so none needs a branch, and all are issued before any is
+// converted.  The bias instantiations of k_gemm_f8dl load a column tile's
+// biases this way, once, ahead of the rows they add to (read beside each
+// element under its bounds and dtype branches, the loads waited one at a
+// time); the bias-free instantiations carry none of it, so their register
+// demand is the main loop's.
+template <int NB, typename ColOf>
+__device__ __forceinline__ void load_biases(const vh_epilogue& e, int64_t N, ColOf col_of, float (&out)[NB]) {
+  if (e.bias_dtype == VH_BF16) {
+    uint32_t raw[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int64_t c = col_of(k);
+      raw[k] = ((const uint16_t*)e.bias)[c < N ? c : N - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k) out[k] = col_of(k) < N ? bf2f(raw[k]) : 0.0f;
+  } else {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int64_t c = col_of(k);
+      out[k] = ((const float*)e.bias)[c < N ? c : N - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k)
+      if (col_of(k) >= N) out[k] = 0.0f;
+  }
+}
+
 // bf16 output through LDS: each wave rounds its sub-tile (hardware
 // converter, round half to even), writes it row-major to LDS (padded rows,
 // WM * WN * 32 TM * (32 TN + 8) bf16 in all), and stores whole 16-byte row
@@ -250,6 +280,36 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& g, f32x16 (&acc)[
 // columns n = 8 q + 4 (lane / 32) + {0..3}: one 8-byte LDS write each.
 // MODE: 0 round-scale (dequantize(linear(xq, wq), s): round to bf16, times
 // s, round again), 1 scale only, 2 scale and bias.
+// MODE 2 (scale and bias), column tile by column tile: the tile's biases
+// loaded once for all its rows.
+template <int TM, int TN>
+__device__ __forceinline__ void stage_tile_t_bias(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint16_t* ct, int64_t n0,
+                                                  int wn, int lane) {
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  const vh_epilogue& e = g.epi;
+  const float sc = epi_scale(e);
+  constexpr int SUBN = TN * 32, PITCH = SUBN + 8;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    float bias[16];  // columns j * 32 + q * 8 + lhalf * 4 + u of this lane
+    load_biases(e, g.N, [&](int k) { return n0 + wn * SUBN + j * 32 + (k >> 2) * 8 + lhalf * 4 + (k & 3); }, bias);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = j * 32 + q * 8 + lhalf * 4;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = acc[i][j][4 * q + u] * sc + bias[4 * q + u];
+        *(uint2*)(ct + (i * 32 + lrow) * PITCH + nl) = make_uint2(f2bf2_hw(v[0], v[1]), f2bf2_hw(v[2], v[3]));
+      }
+      // one accumulator tile at a time keeps the register demand at 16
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 template <int TM, int TN, int MODE>
 __device__ __forceinline__ void stage_tile_t(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint16_t* ct, int64_t n0,
                                              int wn, int lane) {
@@ -288,14 +348,14 @@ __device__ __forceinline__ void stage_tile_t(const GemmArgs& g, f32x16 (&acc)[TM
   }
 }
 
-template <int TM, int TN>
+template <int TM, int TN, bool BIAS>
 __device__ __forceinline__ void store_tile_lds_t(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint8_t* smem, int64_t m0,
                                                  int64_t n0, int wave, int wm, int wn, int lane) {
   constexpr int SUBM = TM * 32, SUBN = TN * 32, PITCH = SUBN + 8;  // bf16 elements
   uint16_t* ct = (uint16_t*)smem + wave * SUBM * PITCH;
   if (g.epi.mode == EPI_ROUND_SCALE) stage_tile_t<TM, TN, 0>(g, acc, ct, n0, wn, lane);
-  else if (!g.epi.bias) stage_tile_t<TM, TN, 1>(g, acc, ct, n0, wn, lane);
-  else stage_tile_t<TM, TN, 2>(g, acc, ct, n0, wn, lane);
+  else if constexpr (!BIAS) stage_tile_t<TM, TN, 1>(g, acc, ct, n0, wn, lane);
+  else stage_tile_t_bias<TM, TN>(g, acc, ct, n0, wn, lane);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -360,7 +420,7 @@ __device__ __forceinline__ void store_tile_direct(const GemmArgs& g, f32x16 (&ac
 // Float32 result of transposed accumulators (B was the row operand: lane l
 // holds row m = l % 32 of each 32 x 32 tile, columns (r / 4) * 8 +
 // (l / 32) * 4 + r % 4): four consecutive columns per 16-byte store.
-template <int TM, int TN>
+template <int TM, int TN, bool BIAS>
 __device__ __forceinline__ void store_tile_t_f32(const GemmArgs& g, f32x16 (&acc)[TM][TN], int64_t m0, int64_t n0,
                                                  int wm, int wn, int lane) {
   const int lrow = lane & 31, lhalf = lane >> 5;
@@ -368,18 +428,28 @@ __device__ __forceinline__ void store_tile_t_f32(const GemmArgs& g, f32x16 (&acc
   const float sc = epi_scale(e);
   constexpr int SUBM = TM * 32, SUBN = TN * 32;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int64_t row = m0 + wm * SUBM + i * 32 + lrow;
-    if (row >= g.M) continue;
-    float* crow = (float*)g.C + row * g.ldc;
+  for (int j = 0; j < TN; ++j) {
+    float bias[16];  // columns j * 32 + q * 8 + lhalf * 4 + u of this lane (BIAS only)
+    if constexpr (BIAS)
+      load_biases(e, g.N, [&](int k) { return n0 + wn * SUBN + j * 32 + (k >> 2) * 8 + lhalf * 4 + (k & 3); }, bias);
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+    for (int i = 0; i < TM; ++i) {
+      const int64_t row = m0 + wm * SUBM + i * 32 + lrow;
+      if (row >= g.M) continue;
+      float* crow = (float*)g.C + row * g.ldc;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t col = n0 + wn * SUBN + j * 32 + q * 8 + lhalf * 4;
         float v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = epi_value(e, acc[i][j][4 * q + u], sc, col + u < g.N ? epi_bias(e, col + u) : 0.0f);
+        for (int u = 0; u < 4; ++u) {
+          if constexpr (BIAS) {  // the plain epilogue (launch_f8dl routes a bias here only then)
+            const float x = e.scale ? acc[i][j][4 * q + u] * sc : acc[i][j][4 * q + u];
+            v[u] = x + bias[4 * q + u];
+          } else {
+            v[u] = epi_value(e, acc[i][j][4 * q + u], sc, 0.0f);
+          }
+        }
         if (col + 3 < g.N) {
           *(float4*)(crow + col) = make_float4(v[0], v[1], v[2], v[3]);
         } else {
@@ -388,6 +458,7 @@ __device__ __forceinline__ void store_tile_t_f32(const GemmArgs& g, f32x16 (&acc
             if (col + u < g.N) crow[col + u] = v[u];
         }
       }
+    }
   }
 }
 
@@ -1081,7 +1152,7 @@ __device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t lds, int voff)
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 
-template <int BM, int BN, int NS, int KS, int WM, int WN, int OP>
+template <int BM, int BN, int NS, int KS, int WM, int WN, int OP, bool BIAS>
 __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
     __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) k_gemm_f8dl(GemmArgs g) {
   constexpr int P = KS / 64;                 // MFMA steps per stage
@@ -1253,8 +1324,8 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   // every DMA has landed and every wave is done with the stage buffers
   wait_vmcnt<0>();
   __syncthreads();
-  if (g.epi.out_dtype == VH_F32) store_tile_t_f32<TM, TN>(g, acc, m0, n0, wm, wn, lane);
-  else store_tile_lds_t<TM, TN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+  if (g.epi.out_dtype == VH_F32) store_tile_t_f32<TM, TN, BIAS>(g, acc, m0, n0, wm, wn, lane);
+  else store_tile_lds_t<TM, TN, BIAS>(g, acc, smem, m0, n0, wave, wm, wn, lane);
 }
 
 // ------------------------------------------------------------ MX-int8, fp16
@@ -1537,8 +1608,8 @@ int group_rows(int64_t M, int64_t N, int BM, int BN) {
   return best;
 }
 
-template <int BM, int BN, int NS, int KS, int WM = 2, int WN = 2, int OP = OP_FP8>
-int launch_f8dl(GemmArgs g, int64_t batch, hipStream_t stream) {
+template <int BM, int BN, int NS, int KS, int WM, int WN, int OP, bool BIAS>
+int launch_f8dl_as(GemmArgs g, int64_t batch, hipStream_t stream) {
   g.group_m = group_rows(g.M, g.N, BM, BN);
   constexpr size_t stages = (size_t)NS * (BM + BN) * KS;
   constexpr size_t epi = (size_t)WM * WN * (BM / WM) * (BN / WN + 8) * 2;  // store_tile_lds_t: bf16, padded rows
@@ -1547,7 +1618,7 @@ int launch_f8dl(GemmArgs g, int64_t batch, hipStream_t stream) {
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)k_gemm_f8dl<BM, BN, NS, KS, WM, WN, OP>,
+    if (hipFuncSetAttribute((const void*)k_gemm_f8dl<BM, BN, NS, KS, WM, WN, OP, BIAS>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)smem) != hipSuccess) {
       vh::set_error("vh_gemm: cannot reserve %zu bytes of LDS", smem);
@@ -1555,9 +1626,17 @@ int launch_f8dl(GemmArgs g, int64_t batch, hipStream_t stream) {
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_gemm_f8dl<BM, BN, NS, KS, WM, WN, OP>), dim3((unsigned)tiles, (unsigned)batch), dim3(WM * WN * 64),
-                     smem, stream, g);
+  hipLaunchKernelGGL((k_gemm_f8dl<BM, BN, NS, KS, WM, WN, OP, BIAS>), dim3((unsigned)tiles, (unsigned)batch),
+                     dim3(WM * WN * 64), smem, stream, g);
   return vh::check_launch("vh_gemm");
+}
+
+// A bias (only the plain epilogue adds one) takes the instantiation that
+// loads it; every other epilogue, the one without.
+template <int BM, int BN, int NS, int KS, int WM = 2, int WN = 2, int OP = OP_FP8>
+int launch_f8dl(GemmArgs g, int64_t batch, hipStream_t stream) {
+  if (g.epi.bias && g.epi.mode != EPI_ROUND_SCALE) return launch_f8dl_as<BM, BN, NS, KS, WM, WN, OP, true>(g, batch, stream);
+  return launch_f8dl_as<BM, BN, NS, KS, WM, WN, OP, false>(g, batch, stream);
 }
 
 template <int BM, int BN, int WM, int WN, int MINB, int PF, int AF, int BF>

@@ -96,6 +96,16 @@ def _epilogue(mode, out_dtype, scale=None, bias=None) -> Epilogue:
     return e
 
 
+def _bias_operand(bias: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """A bias as the epilogues read it: bf16 and float32 as they are (every
+    epilogue widens bf16 exactly), other dtypes converted to float32."""
+    if bias is None:
+        return None
+    if bias.dtype not in (torch.bfloat16, torch.float32):
+        bias = bias.to(torch.float32)
+    return bias.contiguous()
+
+
 def gemm_bf16(a: torch.Tensor, b: torch.Tensor, out_dtype, bias=None, alpha=None) -> torch.Tensor:
     """``a[..., M, K] . b[..., N, K]^T`` (bf16 operands, fp32 accumulation),
     ``* alpha + bias`` in fp32, one rounding to ``out_dtype``."""
@@ -118,8 +128,7 @@ def gemm_bf16(a: torch.Tensor, b: torch.Tensor, out_dtype, bias=None, alpha=None
     out = torch.empty(*batch_shape, M, N, dtype=out_dtype, device=a.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
-    if bias is not None:
-        bias = bias.to(torch.float32).contiguous()
+    bias = _bias_operand(bias)
     d = GemmDesc()
     d.A, d.B, d.C = a3.data_ptr(), b3.data_ptr(), out.data_ptr()
     d.M, d.N, d.K = M, N, K
@@ -305,8 +314,7 @@ def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: i
     out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
-    if bias is not None:
-        bias = bias.to(torch.float32).contiguous()
+    bias = _bias_operand(bias)
     d = GemmDesc()
     d.A, d.B, d.C = x_codes.data_ptr(), w_codes.data_ptr(), out.data_ptr()
     d.M, d.N, d.K = M, N, K
@@ -401,8 +409,7 @@ def linear_mx8_f16(x16: torch.Tensor, ex: torch.Tensor, weight: MX8F16Weight, ou
     out = torch.empty(M, N, dtype=out_dtype, device=x16.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
-    if bias is not None:
-        bias = bias.to(torch.float32).contiguous()
+    bias = _bias_operand(bias)
     epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
     part = torch.empty(splits * M * N, dtype=torch.float32, device=x16.device)
     _lib.check(load().vh_gemm_mx8_f16(ptr(x16), ptr(ex), ptr(weight.w), ptr(weight.e), M, N, K,
@@ -554,8 +561,7 @@ def linear_nf4(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, sc
         y = torch.empty(M, weight.N, dtype=out_dtype, device=x.device)
         if alpha is not None:
             alpha = alpha.reshape(()).to(torch.float32).contiguous()
-        if bias is not None:
-            bias = bias.to(torch.float32).contiguous()
+        bias = _bias_operand(bias)
         epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
         lv = ctypes.create_string_buffer(weight.levels, 16)
         st = load().vh_gemv_nf4_m1(ctypes.c_void_p(xc.data_ptr()), dtype_code(xc.dtype), 31.0,
@@ -578,8 +584,7 @@ def linear_nf4(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, sc
     y = torch.empty(M, weight.N, dtype=out_dtype, device=x.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
-    if bias is not None:
-        bias = bias.to(torch.float32).contiguous()
+    bias = _bias_operand(bias)
     epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
     lv = ctypes.create_string_buffer(weight.levels, 16)
     st = lib_.vh_gemv_nf4(ctypes.c_void_p(xl.data_ptr()), ctypes.c_void_p(xs.data_ptr()), M,
