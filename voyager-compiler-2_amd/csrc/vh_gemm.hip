@@ -179,34 +179,11 @@ __device__ __forceinline__ float epi_scale(const vh_epilogue& e) {
   return e.scale_dtype == VH_BF16 ? bf2f(*(const uint16_t*)e.scale) : *(const float*)e.scale;
 }
 
-// The biases of NB columns col_of(k), 0 past N.  Each load is clamped into
-// the row, so none needs a branch, and all are issued before any is
-// converted.  The bias instantiations of k_gemm_f8dl load a column tile's
-// biases this way, once, ahead of the rows they add to (read beside each
-// element under its bounds and dtype branches, the loads waited one at a
-// time); the bias-free instantiations carry none of it, so their register
-// demand is the main loop's.
-template <int NB, typename ColOf>
-__device__ __forceinline__ void load_biases(const vh_epilogue& e, int64_t N, ColOf col_of, float (&out)[NB]) {
-  if (e.bias_dtype == VH_BF16) {
-    uint32_t raw[NB];
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-      const int64_t c = col_of(k);
-      raw[k] = ((const uint16_t*)e.bias)[c < N ? c : N - 1];
-    }
-#pragma unroll
-    for (int k = 0; k < NB; ++k) out[k] = col_of(k) < N ? bf2f(raw[k]) : 0.0f;
-  } else {
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-      const int64_t c = col_of(k);
-      out[k] = ((const float*)e.bias)[c < N ? c : N - 1];
-    }
-#pragma unroll
-    for (int k = 0; k < NB; ++k)
-      if (col_of(k) >= N) out[k] = 0.0f;
-  }
+// Bytes of the direct-to-LDS kernel's bf16 epilogue staging (padded rows);
+// its bias instantiations keep the tile's BN biases (float32) right after.
+template <int BM, int BN, int WM, int WN>
+constexpr int f8dl_epi_bytes() {
+  return WM * WN * (BM / WM) * (BN / WN + 8) * 2;
 }
 
 // bf16 output through LDS: each wave rounds its sub-tile (hardware
@@ -280,29 +257,26 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& g, f32x16 (&acc)[
 // columns n = 8 q + 4 (lane / 32) + {0..3}: one 8-byte LDS write each.
 // MODE: 0 round-scale (dequantize(linear(xq, wq), s): round to bf16, times
 // s, round again), 1 scale only, 2 scale and bias.
-// MODE 2 (scale and bias), column tile by column tile: the tile's biases
-// loaded once for all its rows.
+// MODE 2 (scale and bias): the tile's biases sb (float32, in LDS, one per
+// column of the block tile, 0 past N) added before the rounding.
 template <int TM, int TN>
-__device__ __forceinline__ void stage_tile_t_bias(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint16_t* ct, int64_t n0,
-                                                  int wn, int lane) {
+__device__ __forceinline__ void stage_tile_t_bias(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint16_t* ct,
+                                                  const float* sb, int wn, int lane) {
   const int lrow = lane & 31;
   const int lhalf = lane >> 5;
-  const vh_epilogue& e = g.epi;
-  const float sc = epi_scale(e);
+  const float sc = epi_scale(g.epi);
   constexpr int SUBN = TN * 32, PITCH = SUBN + 8;
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    float bias[16];  // columns j * 32 + q * 8 + lhalf * 4 + u of this lane
-    load_biases(e, g.N, [&](int k) { return n0 + wn * SUBN + j * 32 + (k >> 2) * 8 + lhalf * 4 + (k & 3); }, bias);
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int j = 0; j < TN; ++j) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int nl = j * 32 + q * 8 + lhalf * 4;
-        float v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = acc[i][j][4 * q + u] * sc + bias[4 * q + u];
-        *(uint2*)(ct + (i * 32 + lrow) * PITCH + nl) = make_uint2(f2bf2_hw(v[0], v[1]), f2bf2_hw(v[2], v[3]));
+        const float4 bq = *(const float4*)(sb + wn * SUBN + nl);
+        const float v0 = acc[i][j][4 * q] * sc + bq.x, v1 = acc[i][j][4 * q + 1] * sc + bq.y;
+        const float v2 = acc[i][j][4 * q + 2] * sc + bq.z, v3 = acc[i][j][4 * q + 3] * sc + bq.w;
+        *(uint2*)(ct + (i * 32 + lrow) * PITCH + nl) = make_uint2(f2bf2_hw(v0, v1), f2bf2_hw(v2, v3));
       }
       // one accumulator tile at a time keeps the register demand at 16
       __builtin_amdgcn_sched_barrier(0);
@@ -350,12 +324,12 @@ __device__ __forceinline__ void stage_tile_t(const GemmArgs& g, f32x16 (&acc)[TM
 
 template <int TM, int TN, bool BIAS>
 __device__ __forceinline__ void store_tile_lds_t(const GemmArgs& g, f32x16 (&acc)[TM][TN], uint8_t* smem, int64_t m0,
-                                                 int64_t n0, int wave, int wm, int wn, int lane) {
+                                                 int64_t n0, int wave, int wm, int wn, int lane, const float* sb) {
   constexpr int SUBM = TM * 32, SUBN = TN * 32, PITCH = SUBN + 8;  // bf16 elements
   uint16_t* ct = (uint16_t*)smem + wave * SUBM * PITCH;
   if (g.epi.mode == EPI_ROUND_SCALE) stage_tile_t<TM, TN, 0>(g, acc, ct, n0, wn, lane);
   else if constexpr (!BIAS) stage_tile_t<TM, TN, 1>(g, acc, ct, n0, wn, lane);
-  else stage_tile_t_bias<TM, TN>(g, acc, ct, n0, wn, lane);
+  else stage_tile_t_bias<TM, TN>(g, acc, ct, sb, wn, lane);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -422,16 +396,13 @@ __device__ __forceinline__ void store_tile_direct(const GemmArgs& g, f32x16 (&ac
 // (l / 32) * 4 + r % 4): four consecutive columns per 16-byte store.
 template <int TM, int TN, bool BIAS>
 __device__ __forceinline__ void store_tile_t_f32(const GemmArgs& g, f32x16 (&acc)[TM][TN], int64_t m0, int64_t n0,
-                                                 int wm, int wn, int lane) {
+                                                 int wm, int wn, int lane, const float* sb) {
   const int lrow = lane & 31, lhalf = lane >> 5;
   const vh_epilogue& e = g.epi;
   const float sc = epi_scale(e);
   constexpr int SUBM = TM * 32, SUBN = TN * 32;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    float bias[16];  // columns j * 32 + q * 8 + lhalf * 4 + u of this lane (BIAS only)
-    if constexpr (BIAS)
-      load_biases(e, g.N, [&](int k) { return n0 + wn * SUBN + j * 32 + (k >> 2) * 8 + lhalf * 4 + (k & 3); }, bias);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int64_t row = m0 + wm * SUBM + i * 32 + lrow;
@@ -439,16 +410,17 @@ __device__ __forceinline__ void store_tile_t_f32(const GemmArgs& g, f32x16 (&acc
       float* crow = (float*)g.C + row * g.ldc;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t col = n0 + wn * SUBN + j * 32 + q * 8 + lhalf * 4;
+        const int nl = j * 32 + q * 8 + lhalf * 4;
+        const int64_t col = n0 + wn * SUBN + nl;
         float v[4];
+        if constexpr (BIAS) {  // the plain epilogue (launch_f8dl routes a bias here only then)
+          const float4 bq = *(const float4*)(sb + wn * SUBN + nl);
+          const float b4[4] = {bq.x, bq.y, bq.z, bq.w};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if constexpr (BIAS) {  // the plain epilogue (launch_f8dl routes a bias here only then)
-            const float x = e.scale ? acc[i][j][4 * q + u] * sc : acc[i][j][4 * q + u];
-            v[u] = x + bias[4 * q + u];
-          } else {
-            v[u] = epi_value(e, acc[i][j][4 * q + u], sc, 0.0f);
-          }
+          for (int u = 0; u < 4; ++u) v[u] = (e.scale ? acc[i][j][4 * q + u] * sc : acc[i][j][4 * q + u]) + b4[u];
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] = epi_value(e, acc[i][j][4 * q + u], sc, 0.0f);
         }
         if (col + 3 < g.N) {
           *(float4*)(crow + col) = make_float4(v[0], v[1], v[2], v[3]);
@@ -1188,6 +1160,20 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   const i32x4 rb = raw_desc(g.B + n0 * g.ldb, rows_b * g.ldb);
   const int K = (int)g.K * (BF ? 2 : 1);  // bytes of a row
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+  // BIAS: the tile's BN biases (at most two per thread, clamped into the
+  // row) are read now, ahead of the main loop's DMA; they are older than
+  // every stage's loads, so the loop's vmcnt waits only retire them earlier
+  constexpr int NBT = BIAS ? (BN + NW * 64 - 1) / (NW * 64) : 1;
+  uint32_t braw[NBT];
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int k = 0; k < NBT; ++k) {
+      const int64_t c = n0 + threadIdx.x + k * NW * 64;
+      const int64_t cc = c < g.N ? c : g.N - 1;
+      braw[k] = g.epi.bias_dtype == VH_BF16 ? (uint32_t)((const uint16_t*)g.epi.bias)[cc] << 16
+                                            : ((const uint32_t*)g.epi.bias)[cc];
+    }
+  }
 
   // DMA: block q of RPI rows (A blocks, then B blocks) is fetched by wave
   // q % NW; lane l takes row q RPI + l / CPR, LDS chunk l % CPR.  Row % 16
@@ -1324,8 +1310,18 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   // every DMA has landed and every wave is done with the stage buffers
   wait_vmcnt<0>();
   __syncthreads();
-  if (g.epi.out_dtype == VH_F32) store_tile_t_f32<TM, TN, BIAS>(g, acc, m0, n0, wm, wn, lane);
-  else store_tile_lds_t<TM, TN, BIAS>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+  float* sb = nullptr;
+  if constexpr (BIAS) {
+    sb = (float*)(smem + f8dl_epi_bytes<BM, BN, WM, WN>());
+#pragma unroll
+    for (int k = 0; k < NBT; ++k) {
+      const int c = threadIdx.x + k * NW * 64;
+      if (c < BN) sb[c] = n0 + c < g.N ? __uint_as_float(braw[k]) : 0.0f;
+    }
+    __syncthreads();
+  }
+  if (g.epi.out_dtype == VH_F32) store_tile_t_f32<TM, TN, BIAS>(g, acc, m0, n0, wm, wn, lane, sb);
+  else store_tile_lds_t<TM, TN, BIAS>(g, acc, smem, m0, n0, wave, wm, wn, lane, sb);
 }
 
 // ------------------------------------------------------------ MX-int8, fp16
@@ -1612,7 +1608,8 @@ template <int BM, int BN, int NS, int KS, int WM, int WN, int OP, bool BIAS>
 int launch_f8dl_as(GemmArgs g, int64_t batch, hipStream_t stream) {
   g.group_m = group_rows(g.M, g.N, BM, BN);
   constexpr size_t stages = (size_t)NS * (BM + BN) * KS;
-  constexpr size_t epi = (size_t)WM * WN * (BM / WM) * (BN / WN + 8) * 2;  // store_tile_lds_t: bf16, padded rows
+  // store_tile_lds_t's bf16 staging, then (BIAS) the tile's float32 biases
+  constexpr size_t epi = (size_t)f8dl_epi_bytes<BM, BN, WM, WN>() + (BIAS ? (size_t)BN * 4 : 0);
   constexpr size_t smem = stages > epi ? stages : epi;
   static_assert(smem <= 160 * 1024, "LDS");
   const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
