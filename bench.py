@@ -718,8 +718,8 @@ def profile_shapes(reps: int, config: int = 2):
             g = torch.Generator().manual_seed(1)
             wb = gemm.bake_nf4_weight((torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev), index, stab,
                                       entries)
-            for M in (1, 16):
-                x = torch.randn(M, K, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
+            for rows in (1, 16):
+                x = torch.randn(rows, K, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
                 torch.cuda.synchronize()
                 for _ in range(reps):
                     gemm.linear_nf4(x, wb, index, stab)
