@@ -315,7 +315,16 @@ __global__ void __launch_bounds__(ROW_WAVES * 64) k_outlier_fill(const raw_t<DT>
   // is kept) plus the row's earlier segments' counts
   const int64_t r = w / S;
   int64_t start = (int64_t)ip[r] - offset;
-  for (int64_t sg = r * S; sg < w && start < cap; ++sg) start += fw.seg[sg];
+  // the earlier segments' counts, eight loads in flight at a time (clamped
+  // into the row and masked, so no load waits on the one before; a start
+  // past cap returns below whatever the sum)
+  for (int64_t s0 = r * S; s0 < w; s0 += 8) {
+    int64_t cnt[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cnt[k] = fw.seg[s0 + k < w ? s0 + k : s0];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) start += s0 + k < w ? cnt[k] : 0;
+  }
   const int64_t n = fw.seg[w];
   if (start >= cap || n == 0) return;
   if (n <= SEG_STAGE) {
