@@ -37,3 +37,22 @@ def test_unsupported_device_reasons():
     cpu = torch.device("cpu")
     assert lower.fp8_unsupported(cpu) == "cpu is not a GPU"
     assert lower.nvfp4_unsupported(cpu) == "cpu is not a GPU"
+
+
+def test_bias_operand_keeps_bf16_and_float32():
+    """The GEMM epilogues widen a bf16 bias exactly, so the host passes bf16
+    and float32 biases through as they are (no conversion launch) and
+    converts any other dtype to float32."""
+    from voyager_amd import gemm
+
+    assert gemm._bias_operand(None) is None
+    for dt in (torch.bfloat16, torch.float32):
+        b = torch.randn(12).to(dt)
+        assert gemm._bias_operand(b) is b
+    strided = torch.randn(12, 2).bfloat16()[:, 0]
+    out = gemm._bias_operand(strided)
+    assert out.dtype == torch.bfloat16 and out.is_contiguous() and torch.equal(out, strided)
+    for dt in (torch.float16, torch.float64):
+        b = torch.randn(12).to(dt)
+        out = gemm._bias_operand(b)
+        assert out.dtype == torch.float32 and torch.equal(out, b.float())
