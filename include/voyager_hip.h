@@ -439,8 +439,10 @@ typedef struct vh_kivi_desc {
   int32_t* state;          /* device int32[4], see above */
   int64_t batch, nkv, nq, head_dim; /* nq == 4 nkv, head_dim == 128 */
   float softmax_scale;     /* 1 / sqrt(head_dim) */
-  float* part;             /* workspace of part_floats floats */
-  int64_t part_floats;     /* >= batch * nkv * ceil(group_cap / 16) * 4 * 130 */
+  float* part;             /* workspace of part_floats floats, 16-byte aligned */
+  int64_t part_floats;     /* >= w(P, S, T) = r4(P (S + 1) 8) + r4(P S 512) + r4(P 4 T / 2), P = batch * nkv,
+                              S = ceil(group_cap / 16), T = 32 group_cap + 128, r4 = round up to a multiple
+                              of 4 */
   uint16_t* attn;          /* [batch, nq * 128] bf16 attention output (optional) */
   uint16_t* attn_fq;       /* [batch, nq * 128] fp16 bits: its MX-int8 fake quantization */
   int32_t* flag;

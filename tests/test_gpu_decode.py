@@ -170,6 +170,20 @@ def _expected_attention(nq, nkv, qkv, k_deq, v_deq, k_res, v_res, cos, sin):
 ROPE = {}
 
 
+def _ulp_stats(got, exp):
+    """The fraction of bf16 outputs that differ from ``exp`` and the largest
+    difference in ulps among those not near zero (|exp| above 1/64 of its
+    largest magnitude, where a difference in summation order cannot cancel
+    to a few ulps of a tiny value)."""
+    g, e = got.detach().cpu(), exp.detach().cpu()
+    gi, ei = g.view(torch.int16).int(), e.view(torch.int16).int()
+    differ = gi != ei
+    big = e.float().abs() > e.float().abs().max() / 64
+    same_sign = (g.float() * e.float()) > 0
+    d = (gi - ei).abs()[big & same_sign]
+    return float(differ.float().mean()), int(d.max()) if d.numel() else 0
+
+
 def _rope(max_pos=8192, theta=5e5):
     key = (max_pos, theta)
     if key not in ROPE:
@@ -199,14 +213,17 @@ def test_kivi_attention(B, nkv, n_main, n_res):
     flag = decode.ErrorFlag(DEV)
     attn = torch.empty(B, nq * 128, dtype=torch.bfloat16, device=DEV)
     fq = decode.kivi_attention(qkv.to(DEV), cache, rope, nq, flag, attn=attn)
-    # Keys are dequantized with the reference's bf16 roundings and every
-    # score is rounded where its eager chain rounds it, so the kernel follows
-    # that chain -- which is itself up to ~1.5% (max-abs-normalized) from
-    # float64 at these lengths -- to its summation order
+    # Keys and values are dequantized with the reference's bf16 roundings,
+    # and every score and probability is rounded where its eager chain rounds
+    # it, so the kernels follow that chain -- itself up to ~1.5%
+    # (max-abs-normalized) from float64 at these lengths -- to summation
+    # order: almost every output is the chain's bf16 value bit for bit
     err = max_rel_err(attn, exp)
-    print(f"attention B={B} nkv={nkv} n_main={n_main} n_res={n_res}: {err:.5f} vs the eager chain, "
-          f"{max_rel_err(exp, exp64):.5f} eager chain vs float64", flush=True)
-    assert err < 1e-2
+    frac, ulps = _ulp_stats(attn, exp)
+    print(f"attention B={B} nkv={nkv} n_main={n_main} n_res={n_res}: {err:.5f} vs the eager chain "
+          f"({frac:.4%} of outputs differ, by at most {ulps} ulp), {max_rel_err(exp, exp64):.5f} eager chain "
+          f"vs float64", flush=True)
+    assert err < 5e-3 and frac < 0.01
     assert torch.equal(fq.cpu(), D.mx8_fake_quant(attn.cpu()).half())
     # the step's key (after RoPE) and value landed in the residual window; the state is not advanced
     kr, vr = cache.residual_tokens(n_res + 1)
@@ -338,15 +355,17 @@ def test_decode_layer_cfg5():
     act_ref = torch.nn.functional.silu(D.mx8_linear(h2, *mx["wg"])) * D.mx8_linear(h2, *mx["wu"])
     assert max_rel_err(g_act, act_ref) < 1e-2  # the RMSNorm's row sum is accumulated in another order
     assert torch.equal(g_out, g_x1 + D.mx8_linear(g_act, *mx["wd"]))
-    # End to end, the attention's bf16-ulp differences (summation order) pass
-    # through the MX re-quantization of x1 and act: in the reference's own
-    # pipeline, moving 0.05% of the attention outputs by one ulp already moves
-    # the layer output 0.6-0.8% (tests/test_oracle_decode.py)
+    # End to end, the attention's remaining ulp differences (summation
+    # order) pass through the MX re-quantization of x1 and act: in the
+    # reference's own pipeline, moving 0.05% of the attention outputs by one
+    # ulp already moves the layer output 0.6-0.8% (tests/test_oracle_decode.py)
     errs = {k: max_rel_err(b[k], exp[k]) for k in ("attn", "x1", "act")}
     errs["out"] = max_rel_err(out, exp["out"])
-    print("cfg5 max-abs-normalized errors vs the oracle:", errs, flush=True)
-    assert errs["attn"] < 1e-2 and errs["x1"] < 1e-2
-    assert errs["act"] < 2e-2 and errs["out"] < 2e-2
+    frac, ulps = _ulp_stats(b["attn"], exp["attn"])
+    print("cfg5 max-abs-normalized errors vs the oracle:", errs,
+          f"attention outputs differing: {frac:.4%} (at most {ulps} ulp)", flush=True)
+    assert frac < 0.01
+    assert all(v < 1e-2 for v in errs.values()), errs
 
 
 def test_decode_replay_crosses_folds():

@@ -44,7 +44,6 @@ constexpr int HEAD_DIM = 128;
 constexpr int GQA = 4;        // query heads per kv head
 constexpr int KV_GROUP = 32;  // KIVI group: tokens per key group, channels per value group
 constexpr int RES_CAP = VH_KIVI_RES_CAP;
-constexpr int PART = HEAD_DIM + 2;  // m, l, o[128]
 
 // ------------------------------------------------------- MX-int8 fake quant
 // quantize_mx(x, int8, block 16, force_scale_power_of_two=True) followed by
@@ -450,38 +449,52 @@ __global__ void __launch_bounds__(256) k_bake_mx8_scales(const uint8_t* __restri
   *(uint2*)(out + t * 8) = make_uint2(lo, hi);
 }
 
-// ------------------------------------------------------------ KIVI attention
 // ------------------------------------------------------------ KIVI cache
 // Main-cache layout: P = batch x kv heads sequences, each with room for
-// group_cap groups of 32 tokens; one 3072-byte block per (P, group), read by
-// one wave with three 16-byte loads per lane:
+// group_cap groups of 32 tokens; one 3072-byte block per (P, group).  The
+// score kernel reads the key half and the PV kernel the value half, each
+// with one 16-byte and one 8-byte load per lane:
 //   [0, 1024)     key codes, lane l (kq = l / 16, r = l % 16): dwords
 //                 D[2 tile + cs / 2] hold token 16 tile + r, channels
 //                 32 kq + 8 cs + j (j < 8): code (cs, j) at bit
 //                 16 (cs % 2) + 2 j, so the codes of channels j = 2p, 2p + 1
 //                 (one MFMA operand dword) form nibble 4 (cs % 2) + p.
-//   [1024, 2048)  value codes, lane l: dword w holds row tiles r8 = 2 w and
-//                 2 w + 1 (channel 16 r8 + r) at tokens tok(kq, j): code at
-//                 bit 8 (r8 % 2) + 16 (j % 2) + 2 (j / 2).
-//   [2048, 2560)  key scale / zero point, fp16 [128 channels][2].
-//   [2560, 3072)  value scale / zero point, fp16 [4 kq][8 j][4 channel
-//                 groups][2] of token tok(kq, j).
-// tok(kq, j) = 16 (j / 4) + 4 kq + j % 4: the token the score MFMA leaves in
-// lane quarter kq, register j % 4 of tile j / 4.
+//   [1024, 2048)  value codes, lane l: nibble nb (bits 4 nb .. 4 nb + 3) of
+//                 dword w holds channel 16 r8 + r, r8 = 2 w + nb / 4, of
+//                 tokens 8 kq + 2 (nb % 4) (bits 4 nb, 4 nb + 1) and the one
+//                 after it (bits 4 nb + 2, 4 nb + 3).
+//   [2048, 2560)  key scale / zero point, fp16 [128 channels][2]: lane l's
+//                 8 bytes are channels 2 l and 2 l + 1.
+//   [2560, 3072)  value scale / zero point, fp16: lane l's 8 bytes are the
+//                 (scale, zero point) of tokens 2 tp and 2 tp + 1,
+//                 tp = 4 (l / 16) + l % 4, in channel group (l / 4) % 4.
 // Residual window: keys and values bf16 [P][RES_CAP][128]; slot s holds the
 // token at position n_main + s.
 // Cache state (device int32[4]): {tokens in the main cache, residual slots
 // filled, completion counter of the advance kernel, unused}.
+//
+// Attention follows the reference's eager chain (transformers'
+// eager_attention_forward over the dequantized cache) rounding for rounding:
+// scores bf16(bf16(q . k) * scale), probabilities bf16(exp(s - M) * (1 / L))
+// from the float32 softmax over every position, values as dequantize rounds
+// them (bf16(bf16(code - zero_point) * scale)), and the PV product of those
+// bf16 operands accumulated in float32 and rounded once.  Only summation
+// orders differ.  That takes two passes over the cache: the score kernel
+// (key halves) writes every score and a (max, sum) per split; the PV kernel
+// (value halves) reduces those to the softmax's M and L, forms each
+// probability and multiplies it into the values; the combine adds the
+// splits and the residual window.
+// Workspace (float words, in this order): ml [P][splits_cap + 1][GQA][2]
+// (max and sum of exp(s - max) over a split's scores; index splits_cap is the
+// residual window), po [P][splits_cap][GQA][128] (a split's share of the
+// output, already divided by L), sc bf16 [P][GQA][t_stride] (scores: main
+// token t at t, residual slot s at group_cap * 32 + s).
 constexpr int GROUP_BYTES = 3072;
 constexpr int SPLIT_WAVES = 8;
 constexpr int GROUPS_PER_WAVE = 2;
 constexpr int GROUPS_PER_SPLIT = SPLIT_WAVES * GROUPS_PER_WAVE;
 constexpr int GROUPS_PER_CHUNK = RES_CAP / KV_GROUP;  // groups a fold appends
-constexpr float LOG2E = 1.4426950408889634f;
-// value operands are p * s * 2**(V_EXP - e), e = floor(log2) of the largest
-// value scale the wave reads: at most 2**(V_EXP + 1), far above fp16
-// subnormals for any term that matters
-constexpr int V_EXP = 14;
+static_assert(RES_CAP == SPLIT_WAVES * 16, "one 16-slot tile of the residual window per wave");
 
 struct KiviArgs {
   const uint16_t* qkv;
@@ -495,7 +508,10 @@ struct KiviArgs {
   int32_t* state;  // written by the combine's last workgroup when advancing
   int32_t nkv, nq, splits_cap;
   float scale;  // softmax scale (1 / sqrt(head_dim))
-  float* part;  // [P][splits_cap][GQA][PART]
+  float* ml;
+  float* po;
+  uint16_t* sc;
+  int64_t t_stride;
   int32_t advance;
   vh_format sf;  // fold: scale / zero-point map
   vh_format cf;  // fold: code map
@@ -509,19 +525,60 @@ VH_DEV bool state_ok(const KiviArgs& a, int n_main, int n_res) {
          n_res < RES_CAP && (int64_t)n_main + n_res < a.max_pos;
 }
 
-// A score as eager attention forms it, in log2 units for exp2: q . k rounded
-// to bf16 (the bf16 matmul), times the scale rounded to bf16 again
-// (transformers' eager_attention_forward: matmul(q, k^T) * scaling).
-VH_DEV float eager_score_log2(float qk, float scale) {
-  return __uint_as_float(f2bf2_hw(__uint_as_float(f2bf2_hw(qk, 0.0f) << 16) * scale, 0.0f) << 16) * LOG2E;
+// Two scores as eager attention forms them: q . k rounded to bf16 (the bf16
+// matmul), times the float32 scale, rounded to bf16 again
+// (eager_attention_forward: matmul(q, k^T) * scaling); each rounding done
+// for both by one packed conversion.  Returns the bf16 pair (qk0 low).
+VH_DEV uint32_t eager_scores_x2(float qk0, float qk1, float scale) {
+  const uint32_t t = f2bf2_hw(qk0, qk1);
+  return f2bf2_hw(__uint_as_float(t << 16) * scale, __uint_as_float(t & 0xffff0000u) * scale);
 }
 
-// Two scores through the same chain, each bf16 rounding done for both by
-// one packed conversion (the same rounding as one at a time).
-VH_DEV float2 eager_score_log2_x2(float qk0, float qk1, float scale) {
-  const uint32_t t = f2bf2_hw(qk0, qk1);
-  const uint32_t u = f2bf2_hw(__uint_as_float(t << 16) * scale, __uint_as_float(t & 0xffff0000u) * scale);
-  return make_float2(__uint_as_float(u << 16) * LOG2E, __uint_as_float(u & 0xffff0000u) * LOG2E);
+VH_DEV float lo_bf(uint32_t u) { return __uint_as_float(u << 16); }
+VH_DEV float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// e**x in float32 to about an ulp, as the softmax's float32 exp: x log2(e)
+// is carried as y + ylo (an fma recovers the product's rounding error), then
+// 2**y (v_exp_f32) times 1 + ylo ln 2.  With the product rounded to float32
+// alone the exponent would be off by up to |x| 2**-24, which moves one
+// bf16-rounded probability in a few thousand.
+VH_DEV float exp_acc(float x) {
+  constexpr float L2E = 1.44269502162933349609375f;   // float32(log2 e)
+  constexpr float L2E_LO = 1.925963033500011079e-8f;  // log2 e - L2E
+  constexpr float LN2 = 0.693147180559945309f;
+  if (x < -104.0f) return 0.0f;  // below the smallest float32 subnormal, and -inf
+  const float y = x * L2E;
+  const float ylo = fmaf(x, L2E_LO, fmaf(x, L2E, -y));
+  const float e = __builtin_amdgcn_exp2f(y);
+  return fmaf(e, ylo * LN2, e);
+}
+
+VH_DEV float pick4(float v0, float v1, float v2, float v3, int r) {
+  return r == 0 ? v0 : (r == 1 ? v1 : (r == 2 ? v2 : v3));
+}
+
+// The softmax's maximum M and 1 / L, L = sum of exp(s - M) over every
+// position, for head h of sequence P, from the per-split (max, sum) partials
+// of the live splits and the residual window.  The PV kernel and the combine
+// both reduce them in this one order, so their probabilities agree bit for
+// bit.  1 / L is the correctly rounded reciprocal; the probability is then
+// e * (1 / L), as the float32 softmax scales its exponentials.
+struct SoftmaxTotals {
+  float M, rcpL;
+};
+
+VH_DEV SoftmaxTotals softmax_totals(const KiviArgs& a, int P, int splits, int h) {
+  const float* ml = a.ml + (int64_t)P * (a.splits_cap + 1) * GQA * 2 + h * 2;
+  const float2 r = *(const float2*)(ml + (int64_t)a.splits_cap * GQA * 2);
+  float M = r.x;
+  for (int s = 0; s < splits; ++s) M = fmaxf(M, ml[(int64_t)s * GQA * 2]);
+  float L = 0.0f;
+  for (int s = 0; s < splits; ++s) {
+    const float2 p = *(const float2*)(ml + (int64_t)s * GQA * 2);
+    L = fmaf(p.y, exp_acc(p.x - M), L);
+  }
+  L = fmaf(r.y, exp_acc(r.x - M), L);
+  return {M, 1.0f / L};
 }
 
 VH_DEV uint16_t rope1(const uint16_t* base, const uint16_t* cs, const uint16_t* sn, int c) {
@@ -530,53 +587,30 @@ VH_DEV uint16_t rope1(const uint16_t* base, const uint16_t* cs, const uint16_t* 
   return (uint16_t)f2bf(rbf(x * bf2f(cs[c])) + rbf(xr * bf2f(sn[c])));
 }
 
-VH_DEV uint32_t pack_h2(float a, float b) {
-  const f16x2 h = {(_Float16)a, (_Float16)b};
-  return __builtin_bit_cast(uint32_t, h);
-}
-
 // lane l and lane l ^ 16 (l ^ 32)
 VH_DEV float sum_x16(float v) { return v + __shfl_xor(v, 16); }
 VH_DEV float sum_x32(float v) { return v + __shfl_xor(v, 32); }
 VH_DEV float max_x16(float v) { return fmaxf(v, __shfl_xor(v, 16)); }
 VH_DEV float max_x32(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
 
-// Value code operands: the pair of 2-bit fields at bits 2p and 16 + 2p of W
-// becomes the fp16 pair (1024 + c * 4**p), one v_and_or_b32 with a mask
-// held in a VGPR; the 4**-p goes into the other operand and the 1024 offset
-// is removed by one MFMA against -1024.  mk[p] = 0x00030003 << 2p.
-struct CodeMasks {
-  uint32_t mk[4];
-};
-
-VH_DEV CodeMasks code_masks() {
-  CodeMasks m;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) asm volatile("v_mov_b32 %0, %1" : "=v"(m.mk[p]) : "i"(0x00030003u << (2 * p)));
-  return m;
-}
-
-// The four operand dwords of the codes at bits 8 half + [0, 8) and
-// 16 + 8 half + [0, 8) of W.
-VH_DEV f16x8 code_operand(uint32_t W, int half, const CodeMasks& m) {
-  const uint32_t w = half ? (W >> 8) : W;
-  return __builtin_bit_cast(f16x8, make_uint4((w & m.mk[0]) | 0x64006400u, (w & m.mk[1]) | 0x64006400u,
-                                              (w & m.mk[2]) | 0x64006400u, (w & m.mk[3]) | 0x64006400u));
-}
-
-// Per wave and group, a table of every key operand the group can hold: for
-// each pair of channels (2p, 2p + 1 of 8 cs + [0, 8) in block kq) and each of
-// the 16 pairs of codes, the bf16 pair of dequantized keys -- (code -
-// zero_point) * scale, each bfloat16 op rounding its result as the
-// reference's dequantize does (ops/quantized.py:518-571).  An MFMA operand
-// dword is then one 32-bit LDS read at its pair's table + 4 * nibble.
-// Pair 4 cs + p of block kq sits at byte 272 (4 cs + p) + 64 kq of the
-// wave's 256-byte-aligned table.  The low address byte before the row
+// Pair tables.  Keys and values are both dequantized through LDS tables of
+// every MFMA operand dword a group can hold: for a pair of elements that
+// share an operand dword (two channels of a token for keys, two tokens of a
+// channel for values) and each of the 16 pairs of codes, the bf16 pair of
+// dequantized elements -- (code - zero_point) * scale, each bfloat16 op
+// rounding its result as the reference's dequantize does
+// (ops/quantized.py:518-571).  An operand dword is then one 32-bit LDS read
+// at its pair's table + 4 * nibble.  Table (row q, block kq) sits at byte
+// 272 q + 64 kq of the wave's 256-byte-aligned tables (16 rows); lane l
+// builds table (l % 16, l / 16).  The low address byte before the row
 // offset, 64 kq + 4 * nibble, is one byte of a precomputed word
-// (KeyNibbles), so an address is one v_perm_b32 of that word and the table's
-// base, and the row offset is the read's immediate.  The four blocks a read
-// touches fall in distinct LDS banks, and so do the 16 rows a quarter-wave
-// writes (the 16-byte skew of the 272-byte rows).
+// (KeyNibbles), so an address is one v_perm_b32 of that word and the
+// table's base, and the row offset is the read's immediate.  The four blocks
+// a read touches fall in distinct LDS banks, and so do the 16 rows a
+// quarter-wave writes (the 16-byte skew of the 272-byte rows).
+// Keys: row 4 cs + p, block kq holds channels 32 kq + 8 cs + 2p, +1.
+// Values: row 4 cg + p, block kq holds tokens 2 tp, 2 tp + 1 (tp = 4 kq + p)
+// in channel group cg.
 constexpr int PAIR_TAB = 16 * 4;
 constexpr int KEY_TAB_ROW = 4 * PAIR_TAB + 16;
 constexpr int KEY_TAB_BYTES = 16 * KEY_TAB_ROW;
@@ -600,11 +634,16 @@ VH_DEV uint32_t key_entry_addr(const KeyNibbles& kn, int nib, uint32_t base) {
   return __builtin_amdgcn_perm(base, (nib & 1) ? kn.hi : kn.lo, sel);
 }
 
-// One pair of channels from its fp16 (scale, zero point) pairs [s0, z0, s1,
-// z1]: the 16 entries (every code pair) at dst.
-VH_DEV void build_key_pair(const uint2& prm, uint8_t* dst) {
+VH_DEV uint32_t lds_u32(uint32_t addr) {
+  return *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr;
+}
+
+// One pair of elements from their fp16 (scale, zero point) pairs [s0, z0,
+// s1, z1]: the 16 entries (every code pair c0 + 4 c1) at dst, element 0's
+// value of c0 in the low half, element 1's of c1 in the high half.
+VH_DEV void build_pair_table(const uint2& prm, uint8_t* dst) {
   const f16x2 e0 = __builtin_bit_cast(f16x2, prm.x), e1 = __builtin_bit_cast(f16x2, prm.y);
-  uint32_t v01[2], v23[2];  // per channel: keys of codes 0, 1 and 2, 3 (bf16 pairs)
+  uint32_t v01[2], v23[2];  // per element: values of codes 0, 1 and 2, 3 (bf16 pairs)
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const float sc = (float)(q ? e1[0] : e0[0]), zp = (float)(q ? e1[1] : e0[1]);
@@ -616,7 +655,7 @@ VH_DEV void build_key_pair(const uint2& prm, uint8_t* dst) {
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int c0 = v & 3, c1 = v >> 2;
-    // bytes 0-3 of the selection: channel 0's key of c0 (low), channel 1's of c1 (high)
+    // bytes 0-3 of the selection: element 0's value of c0 (low), element 1's of c1 (high)
     const uint32_t lo = c0 < 2 ? v01[0] : v23[0], hi = c1 < 2 ? v01[1] : v23[1];
     const uint32_t sl = (uint32_t)(2 * (c0 & 1)), sh = (uint32_t)(4 + 2 * (c1 & 1));
     ent[v] = __builtin_amdgcn_perm(hi, lo, sl | (sl + 1) << 8 | sh << 16 | (sh + 1) << 24);
@@ -626,56 +665,117 @@ VH_DEV void build_key_pair(const uint2& prm, uint8_t* dst) {
     *(uint4*)(dst + 16 * k) = make_uint4(ent[4 * k], ent[4 * k + 1], ent[4 * k + 2], ent[4 * k + 3]);
 }
 
-// Workgroups (split, P) stream the main cache: wave w takes groups
-// GROUPS_PER_SPLIT split + SPLIT_WAVES i + w (i < GROUPS_PER_WAVE) with one
-// online softmax, the waves merge through LDS and the workgroup leaves one
-// (max, sum, output) partial per query head.  Splits past the cache's groups
-// return at once (the combine merges only the live ones), so one launch
-// shape serves every cache length up to the capacity.
-// MFMA column n = 4 cg + h: the score MFMA repeats query head h in the four
-// columns n % 4 == h, so every lane holds its own head's scores, and the
-// value MFMA's column n carries p * s for value channel group cg of head h.
-// Of a 16-channel output tile only the columns of its own channel group are
-// kept, so each lane builds one column of value operands (one scale per
-// token) instead of four.  Only the query waits for memory before the
-// workgroup barrier: a wave's second group is still loading while its first
-// is computed.
-__global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
+VH_DEV uint8_t* pair_table_slot(uint8_t* tab, int lane) {
+  return tab + (lane & 15) * KEY_TAB_ROW + (lane >> 4) * PAIR_TAB;
+}
+
+// Orders a wave's LDS table writes before its reads of them by other lanes.
+VH_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The wave's (max, sum of exp(s - max)) over its scores for the head of its
+// lane's column, merged by the workgroup and written as split `slot` of the
+// partials.  Lane (kq, n) holds sc[i][j] for token j of its quarter in its
+// i-th of ng groups; the four column replicas of a head (n / 4) hold the same
+// scores, so replica cg sums only the tokens j % 4 == cg.
+template <int NG>
+VH_DEV void split_totals(const KiviArgs& a, int P, int slot, const float (&sc)[NG][8], const bool (&live)[NG][8],
+                         float (*s_ml)[GQA][2]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, cg = n >> 2;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NG; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (live[i][j]) m = fmaxf(m, sc[i][j]);
+  m = max_x32(max_x16(m));
+  float l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NG; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float s = pick4(sc[i][4 * t], sc[i][4 * t + 1], sc[i][4 * t + 2], sc[i][4 * t + 3], cg);
+      const bool ok = cg == 0 ? live[i][4 * t] : cg == 1 ? live[i][4 * t + 1] : cg == 2 ? live[i][4 * t + 2]
+                                                                                        : live[i][4 * t + 3];
+      if (ok) l += exp_acc(s - m);
+    }
+  l += __shfl_xor(l, 4);
+  l += __shfl_xor(l, 8);
+  l = sum_x32(sum_x16(l));
+  if (lane < GQA) {
+    s_ml[wave][lane][0] = m;
+    s_ml[wave][lane][1] = l;
+  }
+  __syncthreads();
+  if (tid < GQA) {
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < SPLIT_WAVES; ++w) M = fmaxf(M, s_ml[w][tid][0]);
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < SPLIT_WAVES; ++w)
+      if (s_ml[w][tid][0] != -__builtin_inff()) L = fmaf(s_ml[w][tid][1], exp_acc(s_ml[w][tid][0] - M), L);
+    float* out = a.ml + (((int64_t)P * (a.splits_cap + 1) + slot) * GQA + tid) * 2;
+    out[0] = M;
+    out[1] = L;
+  }
+}
+
+// Score pass.  Workgroups (split, P) with split < splits_cap stream the
+// main cache's key halves: wave w takes groups GROUPS_PER_SPLIT split +
+// SPLIT_WAVES i + w (i < GROUPS_PER_WAVE); splits past the cache's groups
+// return at once, so one launch shape serves every cache length up to the
+// capacity.  Workgroup split == splits_cap takes the residual window: its
+// n_res cached keys and this step's key (RoPE'd from the qkv row), which it
+// appends, with this step's value, at residual slot n_res.
+// MFMA column n = 4 cg + h repeats query head h in the four columns
+// n % 4 == h, so every lane holds its own head's scores: S[tile][r] is the
+// score of token 16 tile + 4 kq + r.
+__global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_scores(KiviArgs a) {
   static_assert(GQA * HEAD_DIM == SPLIT_WAVES * 64, "one rotated query element per thread");
   __shared__ __attribute__((aligned(256))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
-  __shared__ __attribute__((aligned(16))) uint4 s_prm[SPLIT_WAVES][GROUPS_PER_WAVE][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
-  __shared__ float s_part[SPLIT_WAVES][GQA][PART];
+  __shared__ __attribute__((aligned(16))) uint16_t s_newk[HEAD_DIM];
+  __shared__ float s_ml[SPLIT_WAVES][GQA][2];
   const int n_main = a.state[0], n_res = a.state[1];
   const int G = n_main / KV_GROUP;
   const int split = blockIdx.x, P = blockIdx.y;
+  const bool residual = split == a.splits_cap;
   const int g_begin = split * GROUPS_PER_SPLIT;
-  if (!state_ok(a, n_main, n_res) || g_begin >= G) return;
+  if (!state_ok(a, n_main, n_res) || (!residual && g_begin >= G)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = lane & 15, kq = lane >> 4;
-  const int cg = n >> 2, hq = n & 3;  // this lane's column: value channel group cg of query head hq
-  const uint32_t kq_bytes = (uint32_t)kq * 0x40404040u;  // 64 kq in every byte: the key table block
+  const int n = lane & 15, kq = lane >> 4, hq = n & 3;
+  const uint32_t kq_bytes = (uint32_t)kq * 0x40404040u;  // 64 kq in every byte: the table block
   const int b = P / a.nkv, kvh = P % a.nkv;
   const int pos = n_main + n_res;
+  const uint16_t* row = a.qkv + (int64_t)b * a.qkv_ld;
+  const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
+  const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
 
   // the query element this thread rotates (head tid / 128, channel tid % 128) goes out first
   const int qh = tid / HEAD_DIM, qc = tid % HEAD_DIM;
-  const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld + (kvh * GQA + qh) * HEAD_DIM;
+  const uint16_t* qrow = row + (kvh * GQA + qh) * HEAD_DIM;
   uint32_t qv = qrow[qc], qp = qrow[qc < HEAD_DIM / 2 ? qc + HEAD_DIM / 2 : qc - HEAD_DIM / 2];
-  uint32_t qcs = a.rope[(int64_t)pos * HEAD_DIM + qc], qsn = a.rope[(a.max_pos + pos) * HEAD_DIM + qc];
+  uint32_t qcs = cs_[qc], qsn = sn_[qc];
   asm volatile("" ::: "memory");
-  // then this wave's blocks, group by group (an absent group re-reads a live one; it is skipped)
-  uint4 kc[GROUPS_PER_WAVE], vc[GROUPS_PER_WAVE], pr[GROUPS_PER_WAVE];
+  // then this wave's key blocks (an absent group re-reads a live one and is skipped)
+  uint4 kc[GROUPS_PER_WAVE];
+  uint2 kp[GROUPS_PER_WAVE];
   int ng = 0;
-  const uint8_t* seq = a.main + (int64_t)P * a.group_cap * GROUP_BYTES;
+  if (!residual) {
+    const uint8_t* seq = a.main + (int64_t)P * a.group_cap * GROUP_BYTES;
 #pragma unroll
-  for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
-    const int g = g_begin + i * SPLIT_WAVES + wave;
-    ng += g < G ? 1 : 0;
-    const uint8_t* blk = seq + (int64_t)(g < G ? g : G - 1) * GROUP_BYTES;
-    pr[i] = *(const uint4*)(blk + 2048 + lane * 16);
-    kc[i] = *(const uint4*)(blk + lane * 16);
-    vc[i] = *(const uint4*)(blk + 1024 + lane * 16);
+    for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
+      const int g = g_begin + i * SPLIT_WAVES + wave;
+      ng += g < G ? 1 : 0;
+      const uint8_t* blk = seq + (int64_t)(g < G ? g : G - 1) * GROUP_BYTES;
+      kp[i] = *(const uint2*)(blk + 2048 + lane * 8);
+      kc[i] = *(const uint4*)(blk + lane * 16);
+    }
   }
   // waits for the query alone; the blocks stay in flight across the barrier
   asm volatile("" : "+v"(qv), "+v"(qp), "+v"(qcs), "+v"(qsn)::"memory");
@@ -683,44 +783,60 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
     const float x = bf2f(qv), xr = qc < HEAD_DIM / 2 ? -bf2f(qp) : bf2f(qp);
     s_q[qh][qc] = (uint16_t)f2bf(rbf(x * bf2f(qcs)) + rbf(xr * bf2f(qsn)));
   }
+  if (residual && tid < HEAD_DIM) {
+    // this step's key (after RoPE) and value enter residual slot n_res
+    const uint16_t kn = rope1(row + (a.nq + kvh) * HEAD_DIM, cs_, sn_, tid);
+    const uint16_t vn = row[(a.nq + a.nkv + kvh) * HEAD_DIM + tid];
+    s_newk[tid] = kn;
+    a.kr[((int64_t)P * RES_CAP + n_res) * HEAD_DIM + tid] = kn;
+    a.vr[((int64_t)P * RES_CAP + n_res) * HEAD_DIM + tid] = vn;
+  }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // key B operands: q[head hq][32 kq + 8 cs + j], the same in the four columns of a head
   bf16x8 Bq[4];
 #pragma unroll
   for (int cs = 0; cs < 4; ++cs) Bq[cs] = __builtin_bit_cast(bf16x8, *(const uint4*)&s_q[hq][32 * kq + 8 * cs]);
-  const CodeMasks cm = code_masks();
-  const f16x8 NEG = __builtin_bit_cast(f16x8, make_uint4(0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u));
-  float m = -__builtin_inff(), lsum = 0.0f, zt = 0.0f, vmax = 0.0f;
-  int ve = 0;
-  f32x4 acc[8];
-#pragma unroll
-  for (int r8 = 0; r8 < 8; ++r8) acc[r8] = {0.0f, 0.0f, 0.0f, 0.0f};
+  uint16_t* sc_head = a.sc + ((int64_t)P * GQA + hq) * a.t_stride;
 
+  if (residual) {
+    // wave w: residual slots 16 w + r; slot n_res is this step's key from LDS
+    const int slot = 16 * wave + n;
+    const uint4* src = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + slot) * HEAD_DIM + 32 * kq);
+    uint4 k4[4];
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs) k4[cs] = src[cs];
+    if (slot == n_res) {
+#pragma unroll
+      for (int cs = 0; cs < 4; ++cs) k4[cs] = *(const uint4*)&s_newk[32 * kq + 8 * cs];
+    }
+    f32x4 S = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs) S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k4[cs]),
+                                                                              Bq[cs], S, 0, 0, 0);
+    const uint32_t u0 = eager_scores_x2(S[0], S[1], a.scale), u1 = eager_scores_x2(S[2], S[3], a.scale);
+    const int s0 = 16 * wave + 4 * kq;  // slots s0 .. s0 + 3
+    if (n < GQA) *(uint2*)(sc_head + a.group_cap * KV_GROUP + s0) = make_uint2(u0, u1);
+    float sc[1][8];
+    bool live[1][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sc[0][j] = j < 4 ? (j & 1 ? hi_bf(j < 2 ? u0 : u1) : lo_bf(j < 2 ? u0 : u1)) : 0.0f;
+      live[0][j] = j < 4 && s0 + j <= n_res;
+    }
+    split_totals<1>(a, P, a.splits_cap, sc, live, s_ml);
+    return;
+  }
+
+  float sc[GROUPS_PER_WAVE][8];
+  bool live[GROUPS_PER_WAVE][8];
   // one group (i constant at each call: the block registers stay unindexed)
   auto group = [&](const int i) __attribute__((always_inline)) {
-    // the group's parameters (keys: lanes 0-31, values: lanes 32-63) to LDS;
-    // the largest value scale of the wave's groups so far sets the value
-    // operands' exponent
-    s_prm[wave][i][lane] = pr[i];
-    if (lane >= 32) {
-      const f16x8 e = __builtin_bit_cast(f16x8, pr[i]);
-      vmax = fmaxf(vmax, fmaxf(fmaxf((float)e[0], (float)e[2]), fmaxf((float)e[4], (float)e[6])));
-    }
-    vmax = max_x32(max_x16(vmax));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 8));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 4));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 2));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 1));
-    const int ve_new = (vmax > 0.0f && vmax < __builtin_inff()) ? floor_log2(vmax) : 0;
+    const int g = g_begin + i * SPLIT_WAVES + wave;
     // this group's key table, lane l the pair of channels 2 l, 2 l + 1 (the
-    // wave's LDS accesses stay in order: the parameters above land first, and
-    // the previous group's reads precede these writes)
-    build_key_pair(*(const uint2*)((const uint8_t*)s_prm[wave][i] + 8 * lane),
-                   s_tab[wave] + (lane & 15) * KEY_TAB_ROW + (lane >> 4) * PAIR_TAB);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // previous group's reads precede these writes in the wave's LDS order)
+    build_pair_table(kp[i], pair_table_slot(s_tab[wave], lane));
+    wave_lds_sync();
     // scores: S[tile][r] = q[head hq] . k[token 16 tile + 4 kq + r]; operand
     // dword p of channel chunk cs is the table entry of its code nibble
     const uint32_t tab = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)s_tab[wave];
@@ -736,106 +852,113 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_split(KiviArgs a) {
           const int cs = 2 * h2 + c2;
           uint32_t w[4];
 #pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            const uint32_t addr = key_entry_addr(kn, 4 * c2 + p, tab);
-            w[p] = *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)(addr + (4 * cs + p) * KEY_TAB_ROW);
-          }
+          for (int p = 0; p < 4; ++p) w[p] = lds_u32(key_entry_addr(kn, 4 * c2 + p, tab) + (4 * cs + p) * KEY_TAB_ROW);
           S[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
               __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3])), Bq[cs], S[t], 0, 0, 0);
         }
       }
-    // online softmax (every lane of a head holds its running max)
-    float sc[8];
-    float mg = -__builtin_inff();
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      const float2 s2 = eager_score_log2_x2(S[j >> 2][j & 3], S[j >> 2][(j & 3) + 1], a.scale);
-      sc[j] = s2.x;
-      sc[j + 1] = s2.y;
-      mg = fmaxf(mg, fmaxf(s2.x, s2.y));
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t u0 = eager_scores_x2(S[t][0], S[t][1], a.scale), u1 = eager_scores_x2(S[t][2], S[t][3], a.scale);
+      if (n < GQA) *(uint2*)(sc_head + (int64_t)g * KV_GROUP + 16 * t + 4 * kq) = make_uint2(u0, u1);
+      sc[i][4 * t] = lo_bf(u0);
+      sc[i][4 * t + 1] = hi_bf(u0);
+      sc[i][4 * t + 2] = lo_bf(u1);
+      sc[i][4 * t + 3] = hi_bf(u1);
     }
-    mg = max_x32(max_x16(mg));
-    const float m_new = fmaxf(m, mg);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-    m = m_new;
-    float p[8];
-    float ps = 0.0f;
+  };
+  static_assert(GROUPS_PER_WAVE == 2, "two group calls");
+#pragma unroll
+  for (int i = 0; i < GROUPS_PER_WAVE; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      p[j] = __builtin_amdgcn_exp2f(sc[j] - m_new);
-      ps += p[j];
+      sc[i][j] = 0.0f;
+      live[i][j] = i < ng;
     }
-    lsum = lsum * alpha + ps;
-    if (i > 0) {  // the first group starts from zero; a new exponent rescales by a power of two (exact)
-      const float f = alpha * ldexpf(1.0f, ve - ve_new);
-      zt *= f;
+  if (ng > 0) group(0);
+  if (ng > 1) group(1);
+  split_totals<GROUPS_PER_WAVE>(a, P, split, sc, live, s_ml);
+}
+
+// PV pass.  Workgroups (split, P) as the score pass's main splits, over the
+// value halves: each wave's groups, probabilities bf16(exp(s - M) * (1 / L))
+// from the scores and the softmax totals, times the values (pair tables),
+// on v_mfma_f32_16x16x32_bf16: A = values (row = channel of a 16-channel
+// tile, k = token), B = probabilities (column n = head n % 4; the
+// replicas are ignored).  The waves add their outputs through LDS and the
+// workgroup writes its split's share of the output.
+__global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_pv(KiviArgs a) {
+  __shared__ __attribute__((aligned(256))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t s_p[SPLIT_WAVES][GQA][KV_GROUP];
+  static_assert(sizeof(float) * SPLIT_WAVES * GQA * HEAD_DIM <= sizeof(s_tab), "outputs reuse the tables");
+  const int n_main = a.state[0], n_res = a.state[1];
+  const int G = n_main / KV_GROUP;
+  const int split = blockIdx.x, P = blockIdx.y;
+  const int g_begin = split * GROUPS_PER_SPLIT;
+  if (!state_ok(a, n_main, n_res) || g_begin >= G) return;
+  const int splits = (G + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, kq = lane >> 4;
+  const uint32_t kq_bytes = (uint32_t)kq * 0x40404040u;
+  const int hp = lane >> 4, tp = lane & 15;  // this lane's probabilities: head hp, tokens 2 tp, 2 tp + 1
+  uint4 vc[GROUPS_PER_WAVE];
+  uint2 vp[GROUPS_PER_WAVE];
+  uint32_t sp[GROUPS_PER_WAVE];
+  int ng = 0;
+  const uint8_t* seq = a.main + (int64_t)P * a.group_cap * GROUP_BYTES;
+  const uint16_t* sc_head = a.sc + ((int64_t)P * GQA + hp) * a.t_stride;
 #pragma unroll
-      for (int r8 = 0; r8 < 8; ++r8) acc[r8] *= f;
-    }
-    ve = ve_new;
-    // value B operands of column (cg, hq): p * s * 2**(V_EXP - ve) * 4**-(j / 2)
-    // at the lane's tokens; the zero-point term accumulates p * s * zp in the
-    // same 2**(V_EXP - ve) units
-    const float bscale = ldexpf(1.0f, V_EXP - ve);
-    const uint8_t* vprm = (const uint8_t*)&s_prm[wave][i][32] + cg * 4;
-    uint32_t bv[4];
+  for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
+    const int g = g_begin + i * SPLIT_WAVES + wave;
+    ng += g < G ? 1 : 0;
+    const int gl = g < G ? g : G - 1;
+    const uint8_t* blk = seq + (int64_t)gl * GROUP_BYTES;
+    vp[i] = *(const uint2*)(blk + 2560 + lane * 8);
+    vc[i] = *(const uint4*)(blk + 1024 + lane * 16);
+    sp[i] = *(const uint32_t*)(sc_head + (int64_t)gl * KV_GROUP + 2 * tp);
+  }
+  const SoftmaxTotals tot = softmax_totals(a, P, splits, hp);
+  f32x4 acc[8];
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      const f16x2 e0 = *(const f16x2*)(vprm + (kq * 8 + 2 * pp) * 16);
-      const f16x2 e1 = *(const f16x2*)(vprm + (kq * 8 + 2 * pp + 1) * 16);
-      const float f = bscale * (1.0f / (float)(1 << (2 * pp)));
-      const float p0 = p[2 * pp] * f, p1 = p[2 * pp + 1] * f;
-      const float b0 = fmaf(p0, (float)e0[0], 0.0f), b1 = fmaf(p1, (float)e1[0], 0.0f);
-      const float z = fmaf(b1, (float)e1[1], b0 * (float)e0[1]);
-      zt = fmaf(z, (float)(1 << (2 * pp)), zt);
-      bv[pp] = pack_h2(b0, b1);
-    }
-    const f16x8 B = __builtin_bit_cast(f16x8, make_uint4(bv[0], bv[1], bv[2], bv[3]));
+  for (int r8 = 0; r8 < 8; ++r8) acc[r8] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto group = [&](const int i) __attribute__((always_inline)) {
+    build_pair_table(vp[i], pair_table_slot(s_tab[wave], lane));
+    const float p0 = exp_acc(lo_bf(sp[i]) - tot.M) * tot.rcpL, p1 = exp_acc(hi_bf(sp[i]) - tot.M) * tot.rcpL;
+    *(uint32_t*)&s_p[wave][hp][2 * tp] = f2bf2_hw(p0, p1);
+    wave_lds_sync();
+    const bf16x8 B = __builtin_bit_cast(bf16x8, *(const uint4*)&s_p[wave][n & 3][8 * kq]);
+    const uint32_t tab = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)s_tab[wave];
     const uint32_t vw[4] = {vc[i].x, vc[i].y, vc[i].z, vc[i].w};
 #pragma unroll
-    for (int r8 = 0; r8 < 8; ++r8) {
-      acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(code_operand(vw[r8 >> 1], r8 & 1, cm), B, acc[r8], 0, 0, 0);
-      acc[r8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(NEG, B, acc[r8], 0, 0, 0);
+    for (int w = 0; w < 4; ++w) {
+      const KeyNibbles kn = key_nibbles(vw[w], kq_bytes);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint32_t A[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) A[p] = lds_u32(key_entry_addr(kn, 4 * half + p, tab) + (4 * w + p) * KEY_TAB_ROW);
+        acc[2 * w + half] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, make_uint4(A[0], A[1], A[2], A[3])), B, acc[2 * w + half], 0, 0, 0);
+      }
     }
   };
   static_assert(GROUPS_PER_WAVE == 2, "two group calls");
   if (ng > 0) group(0);
   if (ng > 1) group(1);
-  // wave totals: sums over the lane quarters; column (cg, hq) keeps the
-  // channel tiles of its group, o[head hq][16 r8 + 4 kq + r] for r8 / 2 == cg
-  lsum = sum_x32(sum_x16(lsum));
-  zt = sum_x32(sum_x16(zt));
-  const float oscale = ldexpf(1.0f, ve - V_EXP);
+  __syncthreads();  // every wave is done with its tables
+  float(*s_o)[GQA][HEAD_DIM] = reinterpret_cast<float(*)[GQA][HEAD_DIM]>(&s_tab[0][0]);
+  // lane (kq, n < 4): head n, channels 16 r8 + 4 kq + r
+  if (n < GQA) {
 #pragma unroll
-  for (int r8 = 0; r8 < 8; ++r8)
-    if ((r8 >> 1) == cg) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_part[wave][hq][2 + 16 * r8 + 4 * kq + r] = (acc[r8][r] - zt) * oscale;
-    }
-  if (n < GQA && kq == 0) {
-    s_part[wave][hq][0] = m;
-    s_part[wave][hq][1] = lsum;
+    for (int r8 = 0; r8 < 8; ++r8)
+      *(f32x4*)&s_o[wave][n][16 * r8 + 4 * kq] = acc[r8];
   }
   __syncthreads();
-  // merge the waves: thread (head, channel)
   const int h = tid >> 7, c = tid & (HEAD_DIM - 1);
-  float M = -__builtin_inff();
+  float O = 0.0f;
 #pragma unroll
-  for (int w = 0; w < SPLIT_WAVES; ++w) M = fmaxf(M, s_part[w][h][0]);
-  float L = 0.0f, O = 0.0f;
-#pragma unroll
-  for (int w = 0; w < SPLIT_WAVES; ++w) {
-    const float mw = s_part[w][h][0];
-    const float f = mw == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-    L = fmaf(f, s_part[w][h][1], L);
-    O = fmaf(f, s_part[w][h][2 + c], O);
-  }
-  float* out = a.part + (((int64_t)P * a.splits_cap + split) * GQA + h) * PART;
-  if (c == 0) {
-    out[0] = M;
-    out[1] = L;
-  }
-  out[2 + c] = O;
+  for (int w = 0; w < SPLIT_WAVES; ++w) O += s_o[w][h][c];
+  a.po[(((int64_t)P * a.splits_cap + split) * GQA + h) * HEAD_DIM + c] = O;
 }
 
 // Writes one group block from codes (bytes 0..3) and bf16 scale / zero
@@ -859,15 +982,18 @@ VH_DEV void write_group(const uint8_t* kcode, int64_t kstride, const uint16_t* k
   *(uint4*)(blk + lane * 16) = make_uint4(D[0], D[1], D[2], D[3]);
   uint32_t V[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int r8 = 0; r8 < 8; ++r8)
+  for (int w = 0; w < 4; ++w)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int tok = 16 * (j >> 2) + 4 * kq + (j & 3);
-      const uint32_t code = vcode[(int64_t)tok * vstride + 16 * r8 + r] & 3u;
-      V[r8 >> 1] |= code << (8 * (r8 & 1) + 16 * (j & 1) + 2 * (j >> 1));
-    }
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int ch = 16 * (2 * w + (nb >> 2)) + r, tok = 8 * kq + 2 * (nb & 3) + u;
+        const uint32_t code = vcode[(int64_t)tok * vstride + ch] & 3u;
+        V[w] |= code << (4 * nb + 2 * u);
+      }
   *(uint4*)(blk + 1024 + lane * 16) = make_uint4(V[0], V[1], V[2], V[3]);
-  // parameters: lanes 0-31 four key channels each, lanes 32-63 one value token each
+  // parameters: lanes 0-31 four key channels each, lanes 32-63 the value
+  // records of reader lanes 2 i and 2 i + 1
   _Float16 piece[8];
   if (lane < 32) {
 #pragma unroll
@@ -876,12 +1002,16 @@ VH_DEV void write_group(const uint8_t* kcode, int64_t kstride, const uint16_t* k
       piece[2 * k + 1] = (_Float16)bf2f(kz[4 * lane + k]);
     }
   } else {
-    const int i = lane - 32, qq = i >> 3, j = i & 7;
-    const int tok = 16 * (j >> 2) + 4 * qq + (j & 3);
+    const int i = lane - 32;
 #pragma unroll
-    for (int cg = 0; cg < 4; ++cg) {
-      piece[2 * cg] = (_Float16)bf2f(vs[tok * 4 + cg]);
-      piece[2 * cg + 1] = (_Float16)bf2f(vz[tok * 4 + cg]);
+    for (int e = 0; e < 2; ++e) {
+      const int l = 2 * i + e, tp = 4 * (l >> 4) + (l & 3), cg = (l >> 2) & 3;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int tok = 2 * tp + u;
+        piece[4 * e + 2 * u] = (_Float16)bf2f(vs[tok * 4 + cg]);
+        piece[4 * e + 2 * u + 1] = (_Float16)bf2f(vz[tok * 4 + cg]);
+      }
     }
   }
   *(f16x8*)(blk + 2048 + lane * 16) = *(const f16x8*)piece;
@@ -922,8 +1052,8 @@ VH_DEV uint8_t kivi_code(float x, const Affine& af, const vh_format& cf, int* ba
 // values along channels, group 32) into groups [g0, g0 + GROUPS_PER_CHUNK)
 // of the main cache -- what a lowered decode graph stores for a completed
 // chunk (codegen/transform/quant_folding.py:1994-2065, 2634-2700).  The
-// last token (slot RES_CAP - 1, written by this step) comes from LDS.  All
-// threads of the workgroup; returns with them synchronised.
+// residual's last slot was written by this step's score pass.  All threads
+// of the workgroup; returns with them synchronised.
 struct FoldLds {
   uint8_t kc[RES_CAP][HEAD_DIM];
   uint8_t vc[RES_CAP][HEAD_DIM];
@@ -932,12 +1062,7 @@ struct FoldLds {
   int bad;
 };
 
-VH_DEV float res_at(const uint16_t* R, const uint16_t* last, int t, int ch) {
-  return bf2f(t == RES_CAP - 1 ? last[ch] : R[t * HEAD_DIM + ch]);
-}
-
-VH_DEV void fold_chunk(const KiviArgs& a, int P, int g0, const uint16_t* newk, const uint16_t* newv, FoldLds& L,
-                       int* flag) {
+VH_DEV void fold_chunk(const KiviArgs& a, int P, int g0, FoldLds& L, int* flag) {
   const int tid = threadIdx.x, nthreads = blockDim.x;
   if (tid == 0) L.bad = 0;
   __syncthreads();
@@ -947,9 +1072,9 @@ VH_DEV void fold_chunk(const KiviArgs& a, int P, int g0, const uint16_t* newk, c
   // keys: one column (group, channel) of 32 tokens per pass
   for (int col = tid; col < GROUPS_PER_CHUNK * HEAD_DIM; col += nthreads) {
     const int g = col / HEAD_DIM, ch = col % HEAD_DIM;
-    float lo = res_at(K, newk, g * KV_GROUP, ch), hi = lo;
+    float lo = bf2f(K[g * KV_GROUP * HEAD_DIM + ch]), hi = lo;
     for (int t = 1; t < KV_GROUP; ++t) {
-      const float x = res_at(K, newk, g * KV_GROUP + t, ch);
+      const float x = bf2f(K[(g * KV_GROUP + t) * HEAD_DIM + ch]);
       lo = nmin(lo, x);
       hi = nmax(hi, x);
     }
@@ -957,22 +1082,22 @@ VH_DEV void fold_chunk(const KiviArgs& a, int P, int g0, const uint16_t* newk, c
     L.ks[g][ch] = (uint16_t)f2bf(af.s);
     L.kz[g][ch] = (uint16_t)f2bf(af.zp);
     for (int t = 0; t < KV_GROUP; ++t)
-      L.kc[g * KV_GROUP + t][ch] = kivi_code(res_at(K, newk, g * KV_GROUP + t, ch), af, a.cf, &bad);
+      L.kc[g * KV_GROUP + t][ch] = kivi_code(bf2f(K[(g * KV_GROUP + t) * HEAD_DIM + ch]), af, a.cf, &bad);
   }
   // values: one row (token, channel group) of 32 channels per pass
   for (int row = tid; row < RES_CAP * 4; row += nthreads) {
     const int t = row / 4, cg = row % 4;
-    float lo = res_at(V, newv, t, cg * KV_GROUP), hi = lo;
+    const uint16_t* vt = V + t * HEAD_DIM + cg * KV_GROUP;
+    float lo = bf2f(vt[0]), hi = lo;
     for (int c = 1; c < KV_GROUP; ++c) {
-      const float x = res_at(V, newv, t, cg * KV_GROUP + c);
+      const float x = bf2f(vt[c]);
       lo = nmin(lo, x);
       hi = nmax(hi, x);
     }
     const Affine af = kivi_affine(lo, hi, a.sf);
     L.vs[t][cg] = (uint16_t)f2bf(af.s);
     L.vz[t][cg] = (uint16_t)f2bf(af.zp);
-    for (int c = 0; c < KV_GROUP; ++c)
-      L.vc[t][cg * KV_GROUP + c] = kivi_code(res_at(V, newv, t, cg * KV_GROUP + c), af, a.cf, &bad);
+    for (int c = 0; c < KV_GROUP; ++c) L.vc[t][cg * KV_GROUP + c] = kivi_code(bf2f(vt[c]), af, a.cf, &bad);
   }
   if (bad) L.bad = 1;
   __syncthreads();
@@ -987,42 +1112,20 @@ VH_DEV void fold_chunk(const KiviArgs& a, int P, int g0, const uint16_t* newk, c
   __syncthreads();
 }
 
-// Per (batch, query head): attention over the residual window (its n_res
-// cached tokens and this step's key / value, taken from the qkv row), merged
-// with the main-cache splits; writes the attention output (bf16) and its
-// MX-int8 fake quantization.  The workgroup of head 0 of each kv head
-// appends this step's key (after RoPE) and value at residual slot n_res.
-// 256 threads: two per residual key row, 16 token subsets for the values;
-// the first 128 (one per channel) merge and write.
-constexpr int COMBINE_PRELOAD = 16;  // splits whose partials are loaded up front
+// Per (batch, query head): the residual window's share of the output (its
+// n_res cached tokens and this step's, appended by the score pass, with the
+// probabilities formed as the PV pass forms them), plus the main splits'
+// shares; writes the attention output (bf16, the one rounding) and its
+// MX-int8 fake quantization.  256 threads: one probability per residual
+// slot, then 16 token subsets x 16 channel octets for the products; the
+// first 128 (one per channel) add the splits and write.
+constexpr int COMBINE_PRELOAD = 16;  // splits whose shares are loaded up front
 constexpr int COMBINE_THREADS = 2 * HEAD_DIM;
-
-VH_DEV float block_max256(float v, float* s_red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  const float r = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  __syncthreads();
-  return r;
-}
-
-VH_DEV float block_sum256(float v, float* s_red) {
-  v = wave_sum(v);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  const float r = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-  __syncthreads();
-  return r;
-}
 
 __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, uint16_t* __restrict__ attn,
                                                                   _Float16* __restrict__ fq, int* __restrict__ flag) {
-  __shared__ __attribute__((aligned(16))) float s_q[HEAD_DIM];
   __shared__ float s_p[RES_CAP];
   __shared__ float s_o[16][HEAD_DIM];
-  __shared__ float s_red[4];
-  __shared__ uint16_t s_newk[HEAD_DIM], s_newv[HEAD_DIM];
   __shared__ FoldLds s_fold;
   // Workgroups go to the 8 XCDs round-robin: XCD x takes the contiguous
   // range x * G / 8 + [0, G / 8) of (batch, head) rows when that keeps the
@@ -1035,35 +1138,27 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   const int P = b * a.nkv + kvh, tid = threadIdx.x;
   // the state is read first, its value used only after the loads below are out
   const int2 st = *(const int2*)a.state;
-  const int c = tid & (HEAD_DIM - 1);              // channel (first half of the block: merge / output)
-  const int tk = tid >> 1, kh = tid & 1;           // key row tk, channel half kh
-  const int co = tid & 15, ts = tid >> 4;          // value octet co, token subset ts (slots ts + 16u)
-  const bool merger = tid < HEAD_DIM;
-  // The residual window and the split partials go out before the state is
-  // read: their addresses do not depend on it (every slot of the window and
-  // every split of the partials is allocated), and what the state leaves
-  // unused is masked once it arrives.
-  uint4 kw[HEAD_DIM / 16], vw[RES_CAP / 16];
-  const uint4* kp = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + tk) * HEAD_DIM + kh * (HEAD_DIM / 2));
+  const int c = tid & (HEAD_DIM - 1);
+  const int co = tid & 15, ts = tid >> 4;  // value octet co, token subset ts (slots ts + 16 u)
+  // The residual values, the slot's score and the splits' shares go out
+  // before the state is read: their addresses do not depend on it (every
+  // slot and split is allocated), and what the state leaves unused is
+  // masked once it arrives.
+  uint4 vw[RES_CAP / 16];
   const uint4* vp = (const uint4*)(a.vr + (int64_t)P * RES_CAP * HEAD_DIM) + co;
 #pragma unroll
-  for (int i = 0; i < HEAD_DIM / 16; ++i) kw[i] = kp[i];
-#pragma unroll
   for (int u = 0; u < RES_CAP / 16; ++u) vw[u] = vp[(int64_t)(ts + 16 * u) * (HEAD_DIM / 8)];
-  const float* base = a.part + ((int64_t)P * a.splits_cap * GQA + h) * PART;
-  float pm[COMBINE_PRELOAD], pl[COMBINE_PRELOAD], po[COMBINE_PRELOAD];
+  const uint16_t sraw = a.sc[((int64_t)P * GQA + h) * a.t_stride + a.group_cap * KV_GROUP + (tid & (RES_CAP - 1))];
+  const float* base = a.po + ((int64_t)P * a.splits_cap * GQA + h) * HEAD_DIM + c;
+  float po[COMBINE_PRELOAD];
 #pragma unroll
   for (int s = 0; s < COMBINE_PRELOAD; ++s) {
     // no predicate: a split past the capacity re-reads the last one
     const int se = s < a.splits_cap ? s : a.splits_cap - 1;
-    const float* ps = base + (int64_t)se * GQA * PART;
-    pm[s] = ps[0];
-    pl[s] = ps[1];
-    po[s] = ps[2 + c];
+    po[s] = base[(int64_t)se * GQA * HEAD_DIM];
   }
   asm volatile("" ::: "memory");  // the loads above are issued before the state is used
   const int n_main = st.x, n_res = st.y;
-  const int pos = n_main + n_res;
   const int splits = (n_main / KV_GROUP + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
   if (!state_ok(a, n_main, n_res)) {
     if (tid < HEAD_DIM) {
@@ -1074,62 +1169,14 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
     if (bh == 0 && tid == 0) atomicOr(flag, VH_DECODE_ERR_KV_STATE);
     return;
   }
-  // slots past the window and splits past the cache hold stale bytes (a
-  // zero weight times a stale infinity would be NaN): cleared
+  const SoftmaxTotals tot = softmax_totals(a, P, splits, h);
+  if (tid < RES_CAP) s_p[tid] = tid <= n_res ? rbf(exp_acc(bf2f(sraw) - tot.M) * tot.rcpL) : 0.0f;
+  // slots past the window hold stale bytes (a zero weight times a stale
+  // infinity would be NaN): cleared
 #pragma unroll
   for (int u = 0; u < RES_CAP / 16; ++u)
-    if (ts + 16 * u >= n_res) vw[u] = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-  for (int s = 0; s < COMBINE_PRELOAD; ++s)
-    if (s >= splits) {
-      pm[s] = -__builtin_inff();
-      pl[s] = 0.0f;
-      po[s] = 0.0f;
-    }
-  const uint16_t* qrow = a.qkv + (int64_t)b * a.qkv_ld;
-  const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
-  const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
-  // RoPE of this step's query / key (channel c; the second half of the block duplicates)
-  const float qc = bf2f(rope1(qrow + H * HEAD_DIM, cs_, sn_, c));
-  const uint16_t kn = rope1(qrow + (a.nq + kvh) * HEAD_DIM, cs_, sn_, c);
-  const uint16_t vn = qrow[(a.nq + a.nkv + kvh) * HEAD_DIM + c];
-  if (merger) s_q[c] = qc;
-  // this step's own score, q . k_new
-  const float s_new = eager_score_log2(block_sum256(merger ? qc * bf2f(kn) : 0.0f, s_red), a.scale);
-  if (h == 0 && merger) {
-    // this step's key (after RoPE) and value enter residual slot n_res (read
-    // by later steps only: this step takes them from the qkv row)
-    a.kr[((int64_t)P * RES_CAP + n_res) * HEAD_DIM + c] = kn;
-    a.vr[((int64_t)P * RES_CAP + n_res) * HEAD_DIM + c] = vn;
-    s_newk[c] = kn;
-    s_newv[c] = vn;
-  }
-  // score of residual slot tk: two threads, 64 channels each
-  float acc = 0.0f;
-  {
-    const float4* q4 = (const float4*)(s_q + kh * (HEAD_DIM / 2));
-#pragma unroll
-    for (int i = 0; i < HEAD_DIM / 16; ++i) {
-      const float4 qa = q4[2 * i], qb = q4[2 * i + 1];
-      const uint32_t ww[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
-      acc = fmaf(qa.x, bf2f(ww[0] & 0xffffu), acc);
-      acc = fmaf(qa.y, bf2f(ww[0] >> 16), acc);
-      acc = fmaf(qa.z, bf2f(ww[1] & 0xffffu), acc);
-      acc = fmaf(qa.w, bf2f(ww[1] >> 16), acc);
-      acc = fmaf(qb.x, bf2f(ww[2] & 0xffffu), acc);
-      acc = fmaf(qb.y, bf2f(ww[2] >> 16), acc);
-      acc = fmaf(qb.z, bf2f(ww[3] & 0xffffu), acc);
-      acc = fmaf(qb.w, bf2f(ww[3] >> 16), acc);
-    }
-  }
-  acc += __shfl_xor(acc, 1);
-  float sc = -__builtin_inff();
-  if (tk < n_res) sc = eager_score_log2(acc, a.scale);
-  else if (tk == n_res) sc = s_new;
-  const float mr = block_max256(kh == 0 ? sc : -__builtin_inff(), s_red);
-  const float p = tk <= n_res ? exp2f(sc - mr) : 0.0f;
-  if (kh == 0) s_p[tk] = p;
-  const float lr = block_sum256(kh == 0 ? p : 0.0f, s_red);
+    if (ts + 16 * u > n_res) vw[u] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
   {
     float o8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1146,30 +1193,15 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
     for (int j = 0; j < 8; ++j) s_o[ts][co * 8 + j] = o8[j];
   }
   __syncthreads();
-  if (merger) {
-    float orr = s_p[n_res] * bf2f(vn);
+  if (tid < HEAD_DIM) {
+    float O = 0.0f;
 #pragma unroll
-    for (int t16 = 0; t16 < 16; ++t16) orr += s_o[t16][c];
-    // merge with the main-cache splits
-    float M = mr;
+    for (int s = 0; s < COMBINE_PRELOAD; ++s)
+      if (s < splits) O += po[s];
+    for (int s = COMBINE_PRELOAD; s < splits; ++s) O += base[(int64_t)s * GQA * HEAD_DIM];
 #pragma unroll
-    for (int s = 0; s < COMBINE_PRELOAD; ++s) M = fmaxf(M, pm[s]);
-    for (int s = COMBINE_PRELOAD; s < splits; ++s) M = fmaxf(M, base[(int64_t)s * GQA * PART]);
-    const float fr = exp2f(mr - M);
-    float L = lr * fr, O = orr * fr;
-#pragma unroll
-    for (int s = 0; s < COMBINE_PRELOAD; ++s) {
-      const float f = pm[s] == -__builtin_inff() ? 0.0f : exp2f(pm[s] - M);
-      L = fmaf(f, pl[s], L);
-      O = fmaf(f, po[s], O);
-    }
-    for (int s = COMBINE_PRELOAD; s < splits; ++s) {
-      const float* ps = base + (int64_t)s * GQA * PART;
-      const float f = ps[0] == -__builtin_inff() ? 0.0f : exp2f(ps[0] - M);
-      L = fmaf(f, ps[1], L);
-      O = fmaf(f, ps[2 + c], O);
-    }
-    const float o = rbf(O / L);
+    for (int t16 = 0; t16 < 16; ++t16) O += s_o[t16][c];
+    const float o = rbf(O);
     const int64_t idx = (int64_t)b * a.nq * HEAD_DIM + H * HEAD_DIM + c;
     if (attn) attn[idx] = (uint16_t)f2bf(o);
     const Mx8Scale scl = mx8_scale(max16(fabsf(o)));
@@ -1190,7 +1222,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
   const bool fold = n_res + 1 == RES_CAP;
   const int g0 = n_main / KV_GROUP;
   const bool room = g0 + GROUPS_PER_CHUNK <= a.group_cap;
-  if (fold && room && h == 0) fold_chunk(a, P, g0, s_newk, s_newv, s_fold, flag);
+  if (fold && room && h == 0) fold_chunk(a, P, g0, s_fold, flag);
   if (tid == 0) {
     if (fold && !room && bh == 0) atomicOr(flag, VH_DECODE_ERR_KV_FULL);
     const int done = __hip_atomic_fetch_add(&a.state[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1317,21 +1349,36 @@ extern "C" int vh_kivi_bake_residual(const uint16_t* k, const uint16_t* v, int64
 
 namespace {
 
+// The attention workspace: the (max, sum) partials, the splits' output
+// shares and the bf16 scores, each region a multiple of 4 floats.
+int64_t kivi_workspace_floats(int64_t P, int64_t group_cap, int64_t* ml_floats, int64_t* po_floats) {
+  const int64_t splits_cap = (group_cap + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
+  const int64_t t_stride = group_cap * KV_GROUP + RES_CAP;
+  auto up4 = [](int64_t v) { return (v + 3) / 4 * 4; };
+  *ml_floats = up4(P * (splits_cap + 1) * GQA * 2);
+  *po_floats = up4(P * splits_cap * GQA * HEAD_DIM);
+  return *ml_floats + *po_floats + up4(P * GQA * t_stride / 2);
+}
+
 int kivi_common(const vh_kivi_desc* d, KiviArgs& a) {
   VH_REQUIRE(d && d->main && d->kr && d->vr && d->state && d->flag, "vh_kivi: null argument");
   VH_REQUIRE(d->batch >= 1 && d->nkv >= 1 && d->nq == GQA * d->nkv, "vh_kivi: needs nq == 4 nkv");
   VH_REQUIRE(d->head_dim == HEAD_DIM, "vh_kivi: head_dim must be %d", HEAD_DIM);
   VH_REQUIRE(d->group_cap >= GROUPS_PER_CHUNK, "vh_kivi: the main cache must hold at least one chunk");
   const int64_t splits_cap = (d->group_cap + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
-  VH_REQUIRE(splits_cap <= 65535 && d->batch * d->nkv <= 65535, "vh_kivi: cache too large");
+  VH_REQUIRE(splits_cap < 65535 && d->batch * d->nkv <= 65535, "vh_kivi: cache too large");
   VH_REQUIRE(d->qkv && d->rope && d->attn_fq && d->part, "vh_kivi_attention: null argument");
   VH_REQUIRE(d->max_pos >= 1, "vh_kivi_attention: empty RoPE table");
   VH_REQUIRE(d->qkv_ld >= (int64_t)(d->nq + 2 * d->nkv) * HEAD_DIM, "vh_kivi_attention: qkv_ld too small");
-  VH_REQUIRE(d->part_floats >= d->batch * d->nkv * splits_cap * GQA * PART,
-             "vh_kivi_attention: workspace too small (needs %lld floats)",
-             (long long)(d->batch * d->nkv * splits_cap * GQA * PART));
+  const int64_t P = d->batch * d->nkv;
+  const int64_t t_stride = d->group_cap * KV_GROUP + RES_CAP;
+  int64_t ml_floats = 0, po_floats = 0;
+  const int64_t need = kivi_workspace_floats(P, d->group_cap, &ml_floats, &po_floats);
+  VH_REQUIRE(d->part_floats >= need, "vh_kivi_attention: workspace too small (needs %lld floats)", (long long)need);
+  VH_REQUIRE((uintptr_t)d->part % 16 == 0, "vh_kivi_attention: misaligned workspace");
   a = KiviArgs{d->qkv, d->qkv_ld, d->rope, d->max_pos, d->main, d->group_cap, d->kr, d->vr, d->state,
                (int32_t)d->nkv, (int32_t)d->nq, (int32_t)splits_cap, d->softmax_scale, d->part,
+               d->part + ml_floats, (uint16_t*)(d->part + ml_floats + po_floats), t_stride,
                d->advance ? 1 : 0, d->scale_fmt, d->code_fmt};
   return VH_OK;
 }
@@ -1350,7 +1397,8 @@ extern "C" int vh_kivi_attention(const vh_kivi_desc* d, vh_stream_t stream) {
   }
   hipStream_t s = vh::as_stream(stream);
   const unsigned P = (unsigned)(d->batch * d->nkv);
-  hipLaunchKernelGGL(k_kivi_split, dim3((unsigned)a.splits_cap, P), dim3(SPLIT_WAVES * 64), 0, s, a);
+  hipLaunchKernelGGL(k_kivi_scores, dim3((unsigned)a.splits_cap + 1, P), dim3(SPLIT_WAVES * 64), 0, s, a);
+  hipLaunchKernelGGL(k_kivi_pv, dim3((unsigned)a.splits_cap, P), dim3(SPLIT_WAVES * 64), 0, s, a);
   hipLaunchKernelGGL(k_kivi_combine, dim3((unsigned)(d->batch * d->nq)), dim3(COMBINE_THREADS), 0, s, a, d->attn,
                      (_Float16*)d->attn_fq, (int*)d->flag);
   return vh::check_launch("vh_kivi_attention");

@@ -276,7 +276,13 @@ class KiviCache:
         return -(-self.group_cap // GROUPS_PER_SPLIT)
 
     def part_floats(self) -> int:
-        return self.P * self.splits_cap() * GQA * (HEAD_DIM + 2)
+        """The attention workspace in floats: per split and the residual
+        window a (max, sum) per head, per split a share of the output, and
+        the bf16 scores of every position."""
+        def up4(v):
+            return -(-v // 4) * 4
+        S, T = self.splits_cap(), self.group_cap * KIVI_GROUP + RES_CAP
+        return up4(self.P * (S + 1) * GQA * 2) + up4(self.P * S * GQA * HEAD_DIM) + up4(self.P * GQA * T // 2)
 
 
 def kivi_attention(qkv: torch.Tensor, cache: KiviCache, rope: torch.Tensor, nq: int, flag: ErrorFlag,
