@@ -13,12 +13,18 @@ N(0,1) activations, N(0,0.02) weights) and resident in HBM.
 Prints ONE JSON line.  `value` = GEMM TFLOP/s over the whole step (the four
 GEMMs' 2*M*N*K, divided by the step time, which includes the quantize
 kernels).  `roofline` is for the dominant kernel (the fp8 GEMM), timed with
-HIP events on the launch stream; `cpu_baseline` times the CPU oracle (the
-reference's op sequence in eager PyTorch) on a bounded sample.
+HIP events on the launch stream, with its operands replayed (Infinity-Cache
+warm) and, under `rotated`, rotated over more than 512 MB as the step meets
+them; `cpu_baseline` times the CPU oracle (the reference's op sequence in
+eager PyTorch) on a bounded sample.  `configs` carries configs 1, 3, 4 and 5
+as `--config N` measures them (value, roofline, CPU baseline on a shorter
+sample); `--headline-only` leaves them out.
 
 Options: --gpus N (1 only), --steps K, --warmup W, --no-cpu (skip the CPU
 baseline), --copy-calibration BYTES (run only a plain device copy, for
-rocprofv3 counter calibration), --profile-shapes R (run only, shape by shape
+rocprofv3 counter calibration), --profile-steps K (config 2's setup, then
+only W warm-up and K timed step replays: a kernel trace of the timed steps
+themselves), --profile-shapes R (run only, shape by shape
 in SHAPES order, R quantize launches then R GEMM launches, eagerly: dispatch
 order names the shape in a rocprofv3 counter run; with --config 3, R
 linear_nf4 calls at M = 1 then M = 16 per shape), --calibrate (run only
@@ -138,6 +144,17 @@ def gpu_bench(args):
             gemm.linear_fp8(L["xq"], L["wq"], L["s"], out=L["y"])
 
     g_step = capture(step)
+    if args.profile_steps:
+        # only the timed region's replays, for a kernel trace of the steps themselves
+        for _ in range(args.warmup):
+            g_step.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.profile_steps):
+            g_step.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.profile_steps
+        return {"profile_steps": args.profile_steps, "warmup": args.warmup, "ms_per_step": round(ms, 4)}, None
 
     # Per-kernel average launch durations (HIP events around graph replays of
     # back-to-back launches), measured first: they also bring the GPU to the
@@ -157,6 +174,18 @@ def gpu_bench(args):
         del xs, gq, gg
     torch.cuda.synchronize()
 
+    # The same GEMMs with their operands rotated over more than twice the
+    # Infinity Cache, as a step meets them: a step moves ~400 MB, so every
+    # operand was last touched a whole step earlier and comes from HBM.
+    gc_ms = []
+    for L in layers:
+        nbuf = max(2, -(-2 * MALL_BYTES // (L["xq"].numel() + L["wq"].numel())))
+        ops = [(L["xq"].clone(), L["wq"].clone()) for _ in range(nbuf)]
+        gg = capture(lambda ops=ops, L=L: [gemm.linear_fp8(a, b, L["s"], out=L["y"]) for a, b in ops])
+        gc_ms.append(time_graph(gg, 3) / nbuf)
+        del ops, gg
+    torch.cuda.synchronize()
+
     for _ in range(args.warmup):
         g_step.replay()
     torch.cuda.synchronize()
@@ -167,17 +196,50 @@ def gpu_bench(args):
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    # In-step kernel durations, right after the timed region and in the same
+    # thermal state: S more steps launched eagerly behind three graph replays
+    # (so the launches queue ahead of the GPU and no kernel waits for its
+    # launch), with a HIP event between consecutive kernels on the launch
+    # stream.  The GEMMs meet their operands as in the timed steps (the
+    # activation codes just written, the weight last read a step earlier).
+    S = 20
+    nk = 2 * len(layers)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nk + 1)] for _ in range(S)]
+    for _ in range(3):
+        g_step.replay()
+    for e in ev:
+        e[0].record()
+        for i, L in enumerate(layers):
+            L["xq"] = quantize(L["x"], L["sx"])
+            e[2 * i + 1].record()
+            gemm.linear_fp8(L["xq"], L["wq"], L["s"], out=L["y"])
+            e[2 * i + 2].record()
+    torch.cuda.synchronize()
+
+    def med(v):
+        v = sorted(v)
+        return v[len(v) // 2]
+
+    in_q = [med([e[2 * i].elapsed_time(e[2 * i + 1]) for e in ev]) for i in range(len(layers))]
+    in_g = [med([e[2 * i + 1].elapsed_time(e[2 * i + 2]) for e in ev]) for i in range(len(layers))]
+
     flops = [2.0 * M * L["N"] * L["K"] for L in layers]
     qbytes = [M * L["K"] * 3.0 for L in layers]  # bf16 in + 1-byte codes out
     total_flops = sum(flops)
     value = total_flops / (ms_per_step * 1e-3) / 1e12
     gemm_tflops = total_flops / (sum(g_ms) * 1e-3) / 1e12
+    cold_tflops = total_flops / (sum(gc_ms) * 1e-3) / 1e12
+    step_tflops = total_flops / (sum(in_g) * 1e-3) / 1e12
     q_gbs = sum(qbytes) / (sum(q_ms) * 1e-3) / 1e9
+    step_q_gbs = sum(qbytes) / (sum(in_q) * 1e-3) / 1e9
     per_shape = []
     for i, L in enumerate(layers):
         per_shape.append({
             "K": L["K"], "N": L["N"],
             "gemm_us": round(g_ms[i] * 1e3, 2), "gemm_tflops": round(flops[i] / (g_ms[i] * 1e-3) / 1e12, 1),
+            "gemm_rotated_us": round(gc_ms[i] * 1e3, 2),
+            "gemm_rotated_tflops": round(flops[i] / (gc_ms[i] * 1e-3) / 1e12, 1),
+            "gemm_in_step_us": round(in_g[i] * 1e3, 2), "quantize_in_step_us": round(in_q[i] * 1e3, 2),
             "quantize_us": round(q_ms[i] * 1e3, 2),
             "quantize_gbs": round(qbytes[i] / (q_ms[i] * 1e-3) / 1e9, 1),
         })
@@ -187,10 +249,18 @@ def gpu_bench(args):
             traffic = json.load(f).get("hbm_bytes_per_launch")
     res = {
         "value": value, "ms_per_step": ms_per_step,
-        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": FP8_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4), "traffic": traffic},
-        "quantize": {"achieved": round(q_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(q_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(step_tflops, 1), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(step_tflops / FP8_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "durations": f"in the step: median over {S} steps of the HIP-event time around each GEMM "
+                                  "launch, right after the timed region",
+                     "rotated": {"achieved": round(cold_tflops, 1), "frac": round(cold_tflops / FP8_PEAK_TFLOPS, 4),
+                                 "operands": "GEMMs alone, operands rotated over > 2 x 256 MB (HBM)"},
+                     "warm": {"achieved": round(gemm_tflops, 1), "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
+                              "operands": "GEMMs alone, the same operands replayed 10 times (Infinity-Cache warm)"}},
+        "quantize": {"achieved": round(step_q_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(step_q_gbs / HBM_PEAK_GBS, 4), "durations": "in the step, as the GEMMs",
+                     "rotated": {"achieved": round(q_gbs, 1), "frac": round(q_gbs / HBM_PEAK_GBS, 4),
+                                 "operands": "quantizes alone, inputs rotated over > 2 x 256 MB"}},
         "per_shape": per_shape,
     }
     return res, cpu_data
@@ -202,7 +272,7 @@ CFG1_SPEC = "int8,qs=microscaling,bs=16,pot=1"
 CFG3_SPEC = "lut4_to_int6,qs=microscaling,bs=64,scale=fp8_e5m3"
 
 
-def bench_config1(args):
+def bench_config1(args, cpu_budget_s=0.0):
     """Config 1: MXINT8 linear, X [256,4096] (0.1% outliers x20, seed 0), W
     [4096,4096] N(0,0.02); int8 bs=16 pot scales.  Step = quantize_mx(X) to
     packed codes + scale bytes, then the packed MX-int8 GEMM."""
@@ -276,8 +346,17 @@ def bench_config1(args):
     gp16 = capture(lambda: [gemm.linear_mx8_f16(*xp16, bw) for _ in range(10)])
     p16_ms = time_graph(gp16, 5) / 10
     p_tf = max(p_tf, p_flops / (p16_ms * 1e-3) / 1e12)
+    cpu = None
+    if cpu_budget_s > 0:
+        cpu = cpu_config1(x, w, cpu_budget_s)
+    g_gbs = gbytes / (g_ms * 1e-3) / 1e9
     return {"metric": "MXINT8 linear TFLOP/s (config 1)", "value": round(flops / (ms * 1e-3) / 1e12, 2),
             "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "roofline": {"bound": "hbm", "achieved": round(g_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(g_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "note": "the GEMM at M = 256 (arithmetic intensity 408 FLOP/B, under the ridge): "
+                                 "algorithmic bytes (int8 codes, scale bytes, bf16 out) / its duration"},
+            "cpu_baseline": cpu,
             "gemm": {"us": round(g_ms * 1e3, 2), "TFLOP/s": round(flops / (g_ms * 1e-3) / 1e12, 1),
                      "GB/s": round(gbytes / (g_ms * 1e-3) / 1e9, 1),
                      "roofline_us": round(max(flops / 2.5e15, gbytes / 8e12) * 1e6, 2),
@@ -383,7 +462,7 @@ def bench_outliers(args):
     return res
 
 
-def bench_config3(args):
+def bench_config3(args, cpu_budget_s=0.0):
     """Config 3: MXNF4 decode linear at M in {1, 16} over the four Llama-3.1-8B
     projections; weights baked once, rotated over > 256 MB."""
     import voyager_amd.library  # noqa: F401  (defines quantized_ops)
@@ -414,12 +493,19 @@ def bench_config3(args):
             tot_b += b
             tot_t += ms
         del ws
-    return {"metric": "MXNF4 decode linear GB/s (config 3)", "value": round(tot_b / (tot_t * 1e-3) / 1e9, 1),
-            "unit": "GB/s", "frac_of_hbm": round(tot_b / (tot_t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "per_shape": res, "config": {"workload": "cfg3: lut4_to_int6 bs=64 fp8_e5m3 scales, M in {1,16}"}}
+    gbs = tot_b / (tot_t * 1e-3) / 1e9
+    cpu = cpu_config3(cpu_budget_s) if cpu_budget_s > 0 else None
+    return {"metric": "MXNF4 decode linear GB/s (config 3)", "value": round(gbs, 1),
+            "unit": "GB/s", "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "note": "the eight decode linears (weights rotated over > 512 MB): algorithmic bytes "
+                                 "(4-bit codes, scale bytes, bf16 activations and outputs) / their durations"},
+            "per_shape": res, "cpu_baseline": cpu,
+            "config": {"workload": "cfg3: lut4_to_int6 bs=64 fp8_e5m3 scales, M in {1,16}"}}
 
 
-def bench_config4(args):
+def bench_config4(args, cpu_budget_s=0.0):
     """Config 4: posit8 (es=1) quantize / dequantize of a 64M-element bf16
     tensor N(0,4), and the posit8 GEMM 2048x4096x4096."""
     import voyager_amd.library  # noqa: F401  (defines quantized_ops)
@@ -457,7 +543,14 @@ def bench_config4(args):
     gl = capture(lambda: [gemm.gemm_bf16(xq, wq, torch.bfloat16) for _ in range(10)])
     l_ms = time_graph(gl, 5) / 10
     flops = 2.0 * 2048 * 4096 * 4096
+    q_gbs = n * 3 / (q_ms * 1e-3) / 1e9
+    cpu = cpu_config4(cpu_budget_s) if cpu_budget_s > 0 else None
     return {"metric": "posit8 quantize GB/s + posit8 GEMM TFLOP/s (config 4)",
+            "value": round(q_gbs, 1), "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": round(q_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(q_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "note": "the packed posit8 quantize of the 64M-element tensor (bf16 in, one byte out)"},
+            "cpu_baseline": cpu,
             "quantize_packed": {"us": round(q_ms * 1e3, 2), "GB/s": round(n * 3 / (q_ms * 1e-3) / 1e9, 1)},
             "quantize_ref_form": {"us": round(r_ms * 1e3, 2), "GB/s": round(n * 4 / (r_ms * 1e-3) / 1e9, 1)},
             "dequantize_packed": {"us": round(d_ms * 1e3, 2), "GB/s": round(n * 3 / (d_ms * 1e-3) / 1e9, 1)},
@@ -472,123 +565,241 @@ def bench_config4(args):
                                    "GEMM M=2048 K=N=4096"}}
 
 
-def bench_config5(args):
+# Config 5's layer: Llama-3.1-8B's architecture (hidden 4096, 32 query / 8 kv
+# heads of 128, MLP 14336, RMSNorm eps 1e-5, RoPE theta 5e5).
+CFG5 = dict(hidden=4096, n_heads=32, n_kv_heads=8, intermediate=14336, eps=1e-5, rope_theta=5e5)
+
+
+def cfg5_weights(seed):
+    """A random-init layer in bf16, drawn from one generator in this order:
+    ln1 = 1 + 0.1 N(0,1) (so the RMSNorm gain is exercised), wq, wk, wv, wo
+    ~ N(0, 0.02), ln2, wg, wu, wd ([out, in], nn.Linear layout)."""
+    g = torch.Generator().manual_seed(seed)
+    H, F = CFG5["hidden"], CFG5["intermediate"]
+    q, kv = CFG5["n_heads"] * 128, CFG5["n_kv_heads"] * 128
+
+    def w(n, k):
+        return (torch.randn(n, k, generator=g) * 0.02).bfloat16()
+
+    return {
+        "ln1": (1 + 0.1 * torch.randn(H, generator=g)).bfloat16(),
+        "wq": w(q, H), "wk": w(kv, H), "wv": w(kv, H), "wo": w(H, q),
+        "ln2": (1 + 0.1 * torch.randn(H, generator=g)).bfloat16(),
+        "wg": w(F, H), "wu": w(F, H), "wd": w(H, F),
+    }
+
+
+def bench_config5(args, cpu_budget_s=10.0):
     """Config 5: one random-init Llama-3.1-8B-architecture decoder layer, decode
-    step at batch 8 over a 4096-token context (3968 KIVI 2-bit tokens, 127
-    residual, this step's).  Two such layers (and caches) alternate in the
-    graph, as consecutive layers of a model do, so neither fits the 256 MB
-    Infinity Cache; the time of one layer step is half a replay."""
+    at batch 8 over a 4096-token context.  Two such layers (weights and KIVI
+    caches) run in turn, layer 0's output feeding layer 1, as consecutive
+    layers of a model do, so neither fits the 256 MB Infinity Cache.
+
+    The step is timed as it runs in a decode loop: one HIP graph of 128
+    consecutive steps of both layers, each step advancing its cache on the
+    device, from position 4032 (3968 tokens in the 2-bit main cache, 64 in
+    the residual window) to 4159, so every step attends to 4033-4160 tokens
+    (4096 on average) and each cache folds one completed 128-token chunk into
+    its main cache on the way; the graph restores both states first, so it
+    replays the same 128 steps.  ``us_per_step`` is one replay over 256.
+    ``per_stage`` times each stage alone at position 4095 without the
+    advance (a breakdown, not the step)."""
     import voyager_amd.library  # noqa: F401  (defines quantized_ops)
-    from oracle import decode as D
     from voyager_amd import decode
 
     dev = torch.device("cuda:0")
-    cfg = D.Config()
-    B, n_main, n_res = 8, 3968, 127
-    pos = n_main + n_res
-    layers, caches, xs, cpu_data = [], [], [], None
+    B, n_main, n_res0, steps = 8, 3968, 64, 128
+    cap = 4096 + decode.RES_CAP
+    nkv = CFG5["n_kv_heads"]
+    layers, caches, kvq, ws = [], [], [], []
     for li in range(2):
-        w = D.random_layer(cfg, seed=li)
+        w = cfg5_weights(li)
         g = torch.Generator().manual_seed(100 + li)
-        kv = [torch.randn(B, cfg.n_kv_heads, n, 128, generator=g).bfloat16() for n in (n_main, n_main, n_res, n_res)]
-        x = torch.randn(B, cfg.hidden, generator=g).bfloat16()
+        k_main, v_main = (torch.randn(B, nkv, n_main, 128, generator=g).bfloat16() for _ in range(2))
+        k_res, v_res = (torch.randn(B, nkv, 127, 128, generator=g).bfloat16() for _ in range(2))
         wd = {k: v.to(dev) for k, v in w.items()}
-        layer = decode.DecoderLayer(wd, cfg.n_heads, cfg.n_kv_heads, cfg.eps, cfg.rope_theta, max_batch=B,
-                                    max_pos=pos + 1)
-        cache, kq, vq = decode.KiviCache.from_bf16(*[t.to(dev) for t in kv], capacity=n_main + 128)
-        if li == 0 and not args.no_cpu:
-            tab = voyager_amd.formats.quantization_map("int8", dev)
-            mx = {}
-            for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
-                sc, cd = torch.ops.quantized_ops.quantize_mx(wd[k], tab, [-1], 16, 127.0, True)
-                mx[k] = (cd.cpu(), sc.cpu())
-            k_past = torch.cat((D.kivi_dequantize(kq[2].cpu(), kq[0].cpu(), kq[1].cpu(), -2), kv[2]), dim=2)
-            v_past = torch.cat((D.kivi_dequantize(vq[2].cpu(), vq[0].cpu(), vq[1].cpu(), -1), kv[3]), dim=2)
-            cpu_data = (x, w, k_past, v_past, mx)
-        del wd, kq, vq
+        layer = decode.DecoderLayer(wd, CFG5["n_heads"], nkv, CFG5["eps"], CFG5["rope_theta"], max_batch=B,
+                                    max_pos=cap)
+        cache, kq, vq = decode.KiviCache.from_bf16(k_main.to(dev), v_main.to(dev), k_res.to(dev), v_res.to(dev),
+                                                   capacity=cap)
         layers.append(layer)
         caches.append(cache)
-        xs.append(x.to(dev))
+        kvq.append((kq, vq, k_res, v_res))
+        ws.append((w, wd))
+    x0 = torch.randn(B, CFG5["hidden"], generator=torch.Generator().manual_seed(7)).bfloat16().to(dev)
+    xs = [x0, layers[0].buf["out"][:B]]
+    sbytes = layers[0].stage_bytes(B, caches[0])  # at position 4095: 3968 main tokens, 127 residual
+    total_b = sum(sbytes.values())
     torch.cuda.synchronize()
-    # The compute stages with the cache state held at position 4095 (every
-    # replay is the same context-4096 step); the state advance that follows
-    # each step in a real decode, and the fold of a completed chunk (one step
-    # in 128), are timed on their own below and added.
+
+    # per-stage breakdown at position 4095, no advance
     stage_lists = [l.stages(x, c, advance=False) for l, c, x in zip(layers, caches, xs)]
     names = [n for n, _ in stage_lists[0]]
     reps = 10
-    step_g = capture(lambda: [fn() for _ in range(reps) for st in stage_lists for _, fn in st])
-    for _ in range(max(1, args.warmup // 10)):
-        step_g.replay()
-    torch.cuda.synchronize()
-    compute_ms = time_graph(step_g, max(1, args.steps // 10)) / (2 * reps)
-    layers[0].flag.check()
     per = {}
-    sbytes = layers[0].stage_bytes(B, caches[0])
     for i, name in enumerate(names):
         gi = capture(lambda: [st[i][1]() for _ in range(reps) for st in stage_lists])
         ms = time_graph(gi, 5) / (2 * reps)
         per[name] = {"us": round(ms * 1e3, 2), "GB/s": round(sbytes[name] / (ms * 1e-3) / 1e9, 1)}
-    # the attention with the state advance a real decode step does: from
-    # residual slot 0 (nothing completes), then one step that folds a chunk
-    for c in caches:
-        c.state.copy_(torch.tensor([n_main, 0, 0, 0], dtype=torch.int32))
-    att_i = names.index("attention")
-    adv_lists = [l.stages(x, c, advance=True) for l, c, x in zip(layers, caches, xs)]
-    adv_g = capture(lambda: [st[att_i][1]() for _ in range(reps) for st in adv_lists])
-    # each replay advances the cache by `reps` positions: no timed warm-up,
-    # 6 replays stay inside the residual window
-    adv_ms = time_graph(adv_g, 5, warm_s=0.0) / (2 * reps)
-    for c in caches:
-        c.state.copy_(torch.tensor([n_main, n_res, 0, 0], dtype=torch.int32))
+    del gi
+
+    # the decode loop: 128 advancing steps of both layers per replay
+    state0 = torch.tensor([n_main, n_res0, 0, 0], dtype=torch.int32, device=dev)
+
+    def window():
+        for c in caches:
+            c.state.copy_(state0)
+        for _ in range(steps):
+            for l, c, x in zip(layers, caches, xs):
+                l.step(x, c, advance=True)
+
+    gw = capture(window)
+    for _ in range(max(1, args.warmup // 10)):
+        gw.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    fold_g = capture(lambda: adv_lists[0][att_i][1]())
-    for c in caches:
-        c.state.copy_(torch.tensor([n_main, n_res, 0, 0], dtype=torch.int32))
-    torch.cuda.synchronize()
-    e0.record()
-    fold_g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    fold_ms = e0.elapsed_time(e1)
+    step_ms = time_graph(gw, 3) / (2 * steps)
     for l, c in zip(layers, caches):
-        c.state.copy_(torch.tensor([n_main, n_res, 0, 0], dtype=torch.int32))
-        c.n_main, c.n_res = n_main, n_res
         l.flag.check()
-    per["attention_advancing"] = {"us": round(adv_ms * 1e3, 2), "fold_step_us": round(fold_ms * 1e3, 2),
-                                  "note": "the attention stage with the cache advance (from residual slot 0), "
-                                          "and one step that folds a completed 128-token chunk (one step in 128)"}
-    att_ms = per["attention"]["us"] * 1e-3
-    step_ms = compute_ms + (adv_ms - att_ms) + (fold_ms - adv_ms) / 128
-    total_b = sum(sbytes.values())
+        if c.device_state() != (4096, 64):
+            raise RuntimeError(f"config 5: the decode loop ended at {c.device_state()}, not (4096, 64)")
     gbs = total_b / (step_ms * 1e-3) / 1e9
     dom = max(("gate_up_proj", "down_proj", "qkv_proj", "o_proj", "attention"), key=lambda n: sbytes[n])
     d_gbs = per[dom]["GB/s"]
     cpu = None
-    if cpu_data is not None:
-        x, w, k_past, v_past, mx = cpu_data
-        cos, sin = D.rope_cos_sin(torch.tensor([pos]), 128, cfg.rope_theta)
-        D.decode_layer(x, w, k_past, v_past, cos, sin, cfg, mx=mx)
-        t0 = time.perf_counter()
-        n = 0
-        while n < 2 or time.perf_counter() - t0 < 10.0:
-            D.decode_layer(x, w, k_past, v_past, cos, sin, cfg, mx=mx)
-            n += 1
-        cs = (time.perf_counter() - t0) / n
-        cpu = {"value": round(total_b / cs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-               "kind": "port", "ms_per_step": round(cs * 1e3, 1),
-               "sample": f"{n} full decode steps of the oracle layer (eager torch, reference op sequence)"}
+    if cpu_budget_s > 0:
+        cpu = cpu_config5(ws[0], kvq[0], layers[0], n_main, cpu_budget_s)
+        cpu["value"] = round(total_b / (cpu["ms_per_step"] * 1e-3) / 1e9, 3)
     return {"metric": "MX-int8 / KIVI decoder-layer decode step, HBM GB/s (config 5)",
             "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
             "us_per_step": round(step_ms * 1e3, 2), "roofline_us": round(total_b / 8e12 * 1e6, 2),
             "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": total_b,
-            "dtype": "int8 codes / 2-bit KIVI, fp32 accumulate", "data": "synthetic",
-            "roofline": {"bound": "hbm", "kernel": dom, "achieved": d_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(d_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+            "dtype": "int8 codes / 2-bit KIVI, fp32 accumulate", "data": "synthetic (random-init layers, seeded)",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "note": "the whole step (algorithmic bytes at context 4096 / step time)",
+                         "dominant_kernel": {"stage": dom, "achieved": d_gbs, "frac": round(d_gbs / HBM_PEAK_GBS, 4)}},
             "per_stage": per, "stage_bytes": sbytes, "cpu_baseline": cpu,
+            "timing": f"{steps} consecutive advancing steps of 2 layers per graph replay (one fold each), "
+                      "positions 4032-4159",
             "config": {"workload": "cfg5: Llama-3.1-8B-arch decoder layer, decode, batch 8, ctx 4096, MXINT8 bs=16 "
                                    "linears, KIVI 2-bit K/V (group 32, fp16 scale/zero), 128-token residual"}}
+
+
+def cpu_config5(w, kvq, layer, n_main, budget_s):
+    """The oracle layer (eager torch, the reference's op sequence) on the
+    host, at position 4095 over the same layer's weights and cache: the
+    MX-int8 weight codes and the KIVI codes are the GPU's reference-form
+    outputs of the same quantize ops, moved to the host."""
+    from oracle import decode as D  # the CPU baseline only
+    from voyager_amd import formats
+
+    kq, vq, k_res, v_res = kvq
+    tab = formats.quantization_map("int8", "cuda:0")
+    mx = {}
+    for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
+        sc, cd = torch.ops.quantized_ops.quantize_mx(w[1][k], tab, [-1], 16, 127.0, True)
+        mx[k] = (cd.cpu(), sc.cpu())
+    k_past = torch.cat((D.kivi_dequantize(kq[2].cpu(), kq[0].cpu(), kq[1].cpu(), -2), k_res), dim=2)
+    v_past = torch.cat((D.kivi_dequantize(vq[2].cpu(), vq[0].cpu(), vq[1].cpu(), -1), v_res), dim=2)
+    cfg = D.Config()
+    x = torch.randn(k_past.shape[0], cfg.hidden, generator=torch.Generator().manual_seed(7)).bfloat16()
+    cos, sin = D.rope_cos_sin(torch.tensor([n_main + 127]), 128, cfg.rope_theta)
+    med, n, el = _time_cpu(lambda: D.decode_layer(x, w[0], k_past, v_past, cos, sin, cfg, mx=mx),
+                           torch.get_num_threads(), budget_s, min_runs=3)
+    return {"unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port", "ms_per_step": round(med * 1e3, 1),
+            "cpu_model": cpu_model(),
+            "sample": f"{n} decode steps of the oracle layer at position 4095 (eager torch, the reference's op "
+                      f"sequence), median, {el:.1f} s"}
+
+
+def cpu_config1(x, w, budget_s):
+    """The oracle's config-1 step on the host: quantize_mx of X, then
+    linear_mx against the weight quantized once (as baked)."""
+    from oracle import ops as O  # the CPU baseline only
+    from oracle import tables as T
+
+    tab = T.quantization_map("int8")
+    ws, wc = O.quantize_mx(w, tab, [-1], 16, 127.0, True)
+
+    def step():
+        sx, cx = O.quantize_mx(x, tab, [-1], 16, 127.0, True)
+        O.linear_mx(cx, wc, input_scale=sx, weight_scale=ws, block_size=16)
+
+    med, n, el = _time_cpu(step, torch.get_num_threads(), budget_s, min_runs=3)
+    flops = 2.0 * 256 * 4096 * 4096
+    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{n} whole config-1 steps (quantize_mx + linear_mx, 256x4096x4096) of the oracle, "
+                      f"median {med * 1e3:.1f} ms, {el:.1f} s"}
+
+
+def cpu_config3(budget_s):
+    """The oracle's config-3 linears on the host (quantize_mx of x, then
+    linear_mx against the weight quantized once) for the two K = 4096, N <=
+    4096 shapes at M = 1 and 16: a bounded sample of the eight (the two
+    larger weights take the oracle several seconds each just to quantize)."""
+    from oracle import ops as O  # the CPU baseline only
+    from oracle import tables as T
+
+    index, entries, mid = T.codebook_index_table(T.quantization_map("lut4_to_int6"))
+    stab = T.quantization_map("fp8_e5m3")
+    work, nbytes = [], 0
+    for K, N in [(4096, 4096), (4096, 1024)]:
+        w = (torch.randn(N, K, generator=torch.Generator().manual_seed(1)) * 0.02).bfloat16()
+        sw, cw = O.quantize_mx(w, index, [-1], 64, 31.0, False, stab)
+        for M in (1, 16):
+            x = torch.randn(M, K, generator=torch.Generator().manual_seed(0)).bfloat16()
+            work.append((x, cw, sw))
+            nbytes += N * K // 2 + N * K // 64 + M * K * 2 + M * N * 2
+
+    def step():
+        for x, cw, sw in work:
+            sx, cx = O.quantize_mx(x, index, [-1], 64, 31.0, False, stab, mid)
+            O.linear_mx(cx, cw, input_scale=sx, weight_scale=sw, block_size=64, input_code=entries,
+                        weight_code=entries)
+
+    med, n, el = _time_cpu(step, torch.get_num_threads(), budget_s, min_runs=3)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{n} passes over the (K, N) = (4096, 4096), (4096, 1024) linears at M = 1 and 16 "
+                      f"(quantize_mx + linear_mx, the GPU's algorithmic bytes), median {med * 1e3:.1f} ms, "
+                      f"{el:.1f} s"}
+
+
+def cpu_config4(budget_s):
+    """The oracle's posit8 quantize on the host over an 8M-element sample of
+    config 4's N(0, 4) tensor (the reference form it computes: bf16 in, bf16
+    out, 4 bytes an element)."""
+    from oracle import ops as O  # the CPU baseline only
+    from oracle import tables as T
+
+    tab = T.quantization_map("posit8_1")
+    one = torch.ones((), dtype=torch.bfloat16)
+    n = 1 << 23
+    t = (torch.randn(n, generator=torch.Generator().manual_seed(0)) * 2).bfloat16()
+    med, runs, el = _time_cpu(lambda: O.quantize(t, one, qmap=tab), torch.get_num_threads(), budget_s,
+                              min_runs=3)
+    return {"value": round(n * 4 / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{runs} quantize calls of the oracle (posit8_1, reference form) over the first 8M elements "
+                      f"of the tensor, median {med * 1e3:.1f} ms, {el:.1f} s"}
+
+
+def summary(res):
+    """The fields of a config's measurement the headline line carries."""
+    rl = res.get("roofline") or {}
+    out = {"metric": res.get("metric"), "value": res.get("value"), "unit": res.get("unit"),
+           "roofline": {k: rl.get(k) for k in ("bound", "achieved", "peak", "unit", "frac")},
+           "cpu_baseline": res.get("cpu_baseline")}
+    for k in ("us_per_step", "ms_per_step"):
+        if k in res:
+            out[k] = res[k]
+    if "gemm" in res and "frac" in res["gemm"]:
+        out["gemm"] = {k: res["gemm"].get(k) for k in ("us", "TFLOP/s", "frac")}
+    if "prefill_gemm" in res:
+        out["prefill_gemm"] = {k: res["prefill_gemm"].get(k) for k in ("us", "TFLOP/s", "frac_of_mfma")}
+    out["workload"] = (res.get("config") or {}).get("workload")
+    return out
 
 
 def cpu_model() -> str:
@@ -753,8 +964,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0)
     ap.add_argument("--profile-shapes", type=int, default=0)
+    ap.add_argument("--profile-steps", type=int, default=0)
     ap.add_argument("--calibrate", action="store_true")
     ap.add_argument("--outliers", action="store_true")
+    ap.add_argument("--headline-only", action="store_true", help="config 2 alone, without the other configs")
     ap.add_argument("--config", type=int, default=2,
                     help="2 (default): the headline line; 1, 3, 4, 5: that config's measurements")
     args = ap.parse_args()
@@ -774,12 +987,26 @@ def main():
     if args.outliers:
         print(json.dumps(bench_outliers(args)), flush=True)
         return
-    if args.config in (1, 3, 4, 5):
-        fn = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config]
-        print(json.dumps(fn(args)), flush=True)
+    fns = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}
+    if args.config in fns:
+        print(json.dumps(fns[args.config](args, 0.0 if args.no_cpu else 10.0)), flush=True)
         return
     res, cpu_data = gpu_bench(args)
+    if args.profile_steps:
+        print(json.dumps(res), flush=True)
+        return
     cpu = None if args.no_cpu else cpu_baseline(cpu_data)
+    # the other configs, each as `--config N` measures it, with a shorter CPU sample
+    configs = {}
+    if not args.headline_only:
+        for n, fn in fns.items():
+            t0 = time.perf_counter()
+            try:
+                configs[str(n)] = summary(fn(args, 0.0 if args.no_cpu else 4.0))
+            except Exception as e:  # one config's failure must not lose the line
+                configs[str(n)] = {"error": f"{type(e).__name__}: {e}"}
+            log(f"bench: config {n} done in {time.perf_counter() - t0:.1f} s")
+            torch.cuda.empty_cache()
     line = {
         "metric": METRIC,
         "value": round(res["value"], 2),
@@ -800,6 +1027,7 @@ def main():
         "quantize": res["quantize"],
         "per_shape": res["per_shape"],
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

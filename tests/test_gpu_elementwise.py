@@ -163,6 +163,56 @@ def test_quantize_packed_e4m3_large_ragged():
     assert torch.equal(got[257 * 65536:].cpu(), exp[:40])
 
 
+@pytest.mark.parametrize("scale", [1.0, 0.0173])
+def test_posit8_elementwise_at_config4_size(scale):
+    """Config 4's elementwise leg at its size: every bf16 pattern 1030 times
+    plus a 48-element tail (67,502,128 elements, more than the config's
+    64M) through the posit table quantize, packed and reference form, and the
+    packed dequantize, with and without a scale.  At this size the quantize's
+    grid-stride loop (256 workgroups x 1024 threads x 4 vectors a pass) runs
+    nine passes, alternating its two load buffers, and the dequantize's
+    gather loop (4096 workgroups, 65,536 units of 1024 codes a pass) a second,
+    partial pass; the tail's last workgroup ends past the end.  Every
+    65,536-pattern block is bit-exact against the oracle."""
+    from voyager_amd import formats, packed
+    from voyager_amd.ops import _elementwise
+
+    R, tail = 1030, 48
+    n = R * 65536 + tail
+    # vectors of 8 past eight quantize passes; units of 1024 codes past one gather pass
+    assert n % 16 == 0 and n // 8 > 8 * 256 * 1024 * 4 and n // 1024 > 4096 * 4 * 4
+    pat = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    s = torch.tensor(scale, dtype=torch.bfloat16)
+    s2 = torch.tensor(0.375, dtype=torch.bfloat16)
+    tab = T.quantization_map("posit8_1")
+    exp_ref = O.quantize(pat, s, qmap=tab)
+    exp_deq = O.dequantize(exp_ref, s2)
+    tab_d, s_d, s2_d = tab.cuda(), s.cuda(), s2.cuda()
+    x = torch.cat([pat.cuda().repeat(R), pat[:tail].cuda()])
+
+    def blocks(t):
+        return t[: R * 65536].view(R, 65536)
+
+    def check(got, exp, what):
+        # the pattern block once against the oracle, then every repeat and the tail against it on the GPU
+        assert_same_bits(got[:65536].cpu(), exp, what)
+        g16 = got.view(torch.int16)
+        assert torch.equal(blocks(g16), g16[:65536].expand(R, 65536)), what
+        assert torch.equal(g16[R * 65536:], g16[:tail]), what
+
+    ref = torch.ops.quantized_ops.quantize(x, s_d, qmap=tab_d)
+    check(ref, exp_ref, "reference form")
+    del ref
+    codes = packed.quantize_packed(x, s_d, tab_d)
+    assert torch.equal(blocks(codes), codes[:65536].expand(R, 65536)) and torch.equal(codes[R * 65536:],
+                                                                                     codes[:tail])
+    del x
+    check(packed.unpack_codes(codes, tab_d), exp_ref, "packed, read back")
+    deq = _elementwise("dequantize", codes, s2_d, None, None, torch.bfloat16, formats.classify(tab_d).fmt, None,
+                       torch.bfloat16)
+    check(deq, exp_deq, "packed dequantize with a scale")
+
+
 @pytest.mark.parametrize("dtype", ["posit8_1", "posit8_0", "posit8_2", "posit16_1"])
 @pytest.mark.parametrize("scale", [1.0, 0.0173, 3.5, 2.0**-130, 1.5e38])
 def test_quantize_posit_every_bf16_pattern(dtype, scale):
