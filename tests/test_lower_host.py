@@ -56,3 +56,37 @@ def test_bias_operand_keeps_bf16_and_float32():
         b = torch.randn(12).to(dt)
         out = gemm._bias_operand(b)
         assert out.dtype == torch.float32 and torch.equal(out, b.float())
+
+
+def test_lower_imports_alone_and_names_what_it_needs():
+    """``import voyager_amd.lower`` works in a fresh interpreter where no
+    quantized_ops namespace is defined; matching a graph then says which
+    import defines it, and works once ``voyager_amd.library`` is loaded."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = """
+import torch
+from voyager_amd import lower
+
+class M(torch.nn.Module):
+    def forward(self, x):
+        return torch.ops.aten.linear.default(x, x)
+
+gm = torch.fx.symbolic_trace(M())
+try:
+    lower.find_sites(gm)
+except RuntimeError as e:
+    assert "import voyager_amd.library" in str(e), e
+else:
+    raise AssertionError("no error without the namespace")
+import voyager_amd.library  # noqa: F401
+sites, skipped = lower.find_sites(gm)
+assert sites == [] and list(skipped.values()) == ["cpu is not a GPU"], skipped
+print("ok")
+"""
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([root, os.path.join(root, "voyager-compiler-2_amd")]))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr[-2000:]

@@ -22,7 +22,6 @@
 #include <cstring>
 
 #include "vh_device.h"
-#include "vh_gemm.h"
 #include "vh_host.h"
 
 namespace {

@@ -27,8 +27,10 @@ copies dropped where no other node reads them.  NVFP4 needs CUDA (as the
 reference reports on ROCm).
 """
 
+import functools
 import operator
 from dataclasses import dataclass, field
+from types import SimpleNamespace
 from typing import Callable, Dict, List, Optional, Tuple
 
 import torch
@@ -39,13 +41,26 @@ from ._lib import FMT_HW_E4M3, FMT_INT, FMT_MINIFLOAT, FMT_POSIT
 
 __all__ = ["check_sites", "find_sites", "fp8_unsupported", "lower", "nvfp4_unsupported"]
 
-QUANTIZE = torch.ops.quantized_ops.quantize.default
-DEQUANTIZE = torch.ops.quantized_ops.dequantize.default
-QUANTIZE_MX = torch.ops.quantized_ops.quantize_mx.default
-LINEAR_MX = torch.ops.quantized_ops.linear_mx.default
 LINEAR = torch.ops.aten.linear.default
 MATMUL = torch.ops.aten.matmul.default
-GEMM_TARGETS = (LINEAR, MATMUL, LINEAR_MX, torch.ops.quantized_ops.matmul_mx.default)
+
+
+@functools.lru_cache(maxsize=None)
+def _q():
+    """The ``quantized_ops`` overloads a converted graph calls, looked up on
+    first use: the namespace is defined by ``voyager_amd.library`` or by the
+    reference (``ops/quantized.py:97``), whichever the caller loaded, and
+    importing this module needs neither."""
+    try:
+        q = torch.ops.quantized_ops
+        t = SimpleNamespace(quantize=q.quantize.default, dequantize=q.dequantize.default,
+                            quantize_mx=q.quantize_mx.default, linear_mx=q.linear_mx.default,
+                            matmul_mx=q.matmul_mx.default)
+    except (AttributeError, RuntimeError) as e:
+        raise RuntimeError("voyager_amd.lower needs the quantized_ops namespace: import voyager_amd.library "
+                           "(or load the reference's voyager_compiler.ops) first") from e
+    t.gemm_targets = (LINEAR, MATMUL, t.linear_mx, t.matmul_mx)
+    return t
 
 # K in multiples of 16 for the FP8 and posit8 GEMMs (16-byte operand rows).
 GEMM_ALIGNMENT = 16
@@ -128,7 +143,7 @@ def _classify(model: GraphModule, node) -> Optional[formats.Classified]:
 def _plain_quantize(node: Node) -> Optional[str]:
     """Why ``node`` is not ``quantize(x, scale, qmap=...)`` against one
     scale, or None."""
-    if node.op != "call_function" or node.target is not QUANTIZE:
+    if node.op != "call_function" or node.target is not _q().quantize:
         return "input is not quantized"
     for i, name in ((2, "zero_point"), (3, "axes"), (4, "block_size"), (6, "output_code"), (7, "seed")):
         if _arg(node, i, name) is not None:
@@ -162,7 +177,7 @@ def _match_linear(model: GraphModule, linear: Node) -> "Site | str":
     users = list(linear.users)
     if c.fmt.kind == FMT_MINIFLOAT and c.fmt.flags & FMT_HW_E4M3:
         output, out_scale = linear, None
-        if any(u.target is DEQUANTIZE for u in users):
+        if any(u.target is _q().dequantize for u in users):
             if len(users) != 1:
                 return "output dequantize is not its only user"
             output = users[0]
@@ -179,7 +194,7 @@ def _match_linear(model: GraphModule, linear: Node) -> "Site | str":
         return Site("fp8", linear, output, x, weight, out_scale=out_scale,
                     consts={"scale": x.args[1], "qmap": _arg(x, 5, "qmap")})
     if c.fmt.kind == FMT_POSIT and c.fmt.p0 == 8:
-        if any(u.target is DEQUANTIZE for u in users):
+        if any(u.target is _q().dequantize for u in users):
             return "a posit8 linear with a dequantize is not lowered"
         return Site("posit8", linear, linear, x, weight, consts={"scale": x.args[1], "qmap": _arg(x, 5, "qmap")})
     return "input format has no packed GEMM"
@@ -190,7 +205,7 @@ def _match_linear_mx(model: GraphModule, linear: Node) -> "Site | str":
     if not (isinstance(codes, Node) and codes.target is operator.getitem and codes.args[1] == 1):
         return "input is not quantized"
     quantize = codes.args[0]
-    if quantize.target is not QUANTIZE_MX:
+    if quantize.target is not _q().quantize_mx:
         return "input is not quantized"
     scale = linear.kwargs.get("input_scale")
     if not (isinstance(scale, Node) and scale.target is operator.getitem and scale.args == (quantize, 0)):
@@ -244,7 +259,7 @@ def match_site(model: GraphModule, node: Node) -> "Site | str":
     """The site ``node`` (a GEMM) heads, or why it is not one."""
     if node.target is LINEAR:
         return _match_linear(model, node)
-    if node.target is LINEAR_MX:
+    if node.target is _q().linear_mx:
         return _match_linear_mx(model, node)
     return f"{node.target} is not lowered"
 
@@ -262,7 +277,7 @@ def find_sites(model: GraphModule) -> Tuple[List[Site], Dict[str, str]]:
     device = buffers[0].device if buffers else torch.device("cpu")
     reason = fp8_unsupported(device)
     for node in model.graph.nodes:
-        if node.op != "call_function" or node.target not in GEMM_TARGETS:
+        if node.op != "call_function" or node.target not in _q().gemm_targets:
             continue
         if reason is not None:
             skipped[node.name] = reason
