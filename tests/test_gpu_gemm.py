@@ -497,11 +497,17 @@ def test_mx8_f16_bake_flushes_only_far_blocks():
 
 @pytest.mark.parametrize("M,N,K,tile,splits", [(256, 4096, 4096, -1, 0), (256, 4096, 4096, 1, 2),
                                                (256, 4096, 4096, 2, 2), (256, 4096, 4096, 3, 8),
-                                               (33, 520, 1024, -1, 0), (130, 264, 768, 0, 3)])
+                                               (33, 520, 1024, -1, 0), (130, 264, 768, 0, 3),
+                                               # one split: the GEMM's own epilogue (ragged rows and
+                                               # tiles), and N % 8 != 0 through the reduction
+                                               (2048, 4096, 1024, -1, 0), (256, 4096, 4096, 1, 1),
+                                               (130, 264, 768, 0, 1), (33, 520, 1024, 2, 1),
+                                               (1100, 136, 512, 3, 1), (50, 260, 512, 0, 1)])
 def test_linear_mx8_f16(M, N, K, tile, splits):
     """The small-M MX-int8 linear on exact fp16 operands against the exact
     float64 product of the reference's decoded operands, bf16 and fp32
-    results (alpha and bias in the reduction's epilogue)."""
+    results (alpha and bias in the reduction's epilogue, or the GEMM's own
+    with one split)."""
     from voyager_amd import gemm, packed
 
     tab = T.quantization_map("int8").cuda()

@@ -56,6 +56,8 @@ struct GemmArgs {
   int64_t ssa, ssb;          // batch strides of the scale bytes
   int group_m;               // tile-rows per column walk (tile_origin)
   vh_epilogue epi;
+  const int32_t* ea;         // OP_F16X, or null: per row of A and column of B, a power of two
+  const int32_t* eb;         // the accumulator is multiplied by before the epilogue
 };
 
 // ------------------------------------------------------------ staging
@@ -1308,6 +1310,31 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   }
   // every DMA has landed and every wave is done with the stage buffers
   wait_vmcnt<0>();
+  if constexpr (OP == OP_F16X) {
+    // exact fp16 operands: each sum times 2**(E_row + E_col) (exact in
+    // float32), as k_split_reduce applies it to split partials.  Transposed
+    // accumulators: lane row m = lane % 32 of tile i, columns
+    // 8 q + 4 (lane / 32) + u of tile j for element 4 q + u.
+    if (g.ea) {
+      const int lrow = lane & 31, lhalf = lane >> 5;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int64_t row = m0 + wm * (BM / WM) + i * 32 + lrow;
+        const int er = g.ea[row < g.M ? row : g.M - 1];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t col = n0 + wn * (BN / WN) + j * 32 + q * 8 + lhalf * 4;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int ec = g.eb[col + u < g.N ? col + u : g.N - 1];
+              acc[i][j][4 * q + u] = ldexpf(acc[i][j][4 * q + u], er + ec);
+            }
+          }
+      }
+    }
+  }
   __syncthreads();
   float* sb = nullptr;
   if constexpr (BIAS) {
@@ -2047,14 +2074,17 @@ extern "C" int64_t vh_gemm_workspace_bytes(const vh_gemm_desc* d) {
 extern "C" int vh_gemm_mx8_f16(const uint16_t* x, const int32_t* ex, const uint16_t* w, const int32_t* ew, int64_t M,
                                int64_t N, int64_t K, const vh_epilogue* epi, void* y, int64_t ldy, float* part,
                                int64_t part_bytes, int32_t splits, int32_t tile, vh_stream_t stream) {
-  VH_REQUIRE(x && ex && w && ew && epi && y && part, "vh_gemm_mx8_f16: null argument");
+  VH_REQUIRE(x && ex && w && ew && epi && y && (part || splits == 1), "vh_gemm_mx8_f16: null argument");
   VH_REQUIRE(M > 0 && N > 0 && K > 0, "vh_gemm_mx8_f16: empty GEMM");
   VH_REQUIRE(splits >= 1 && K % (8 * (int64_t)splits) == 0,
              "vh_gemm_mx8_f16: K (%lld) must split into %d multiples of 8", (long long)K, splits);
   VH_REQUIRE(N % 4 == 0 && ldy >= N, "vh_gemm_mx8_f16: N must be a multiple of 4 and ldy >= N");
-  VH_REQUIRE(part_bytes >= (int64_t)splits * M * N * 4, "vh_gemm_mx8_f16: workspace of %lld bytes, %lld needed",
-             (long long)part_bytes, (long long)((int64_t)splits * M * N * 4));
-  VH_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)part % 16 == 0,
+  // one split whose output the kernel's own epilogue can store needs no workspace
+  const bool direct = splits == 1 && f8dl_epilogue_ok(y, epi->out_dtype, ldy, N);
+  VH_REQUIRE(direct || part_bytes >= (int64_t)splits * M * N * 4,
+             "vh_gemm_mx8_f16: workspace of %lld bytes, %lld needed", (long long)part_bytes,
+             (long long)((int64_t)splits * M * N * 4));
+  VH_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (direct || (uintptr_t)part % 16 == 0),
              "vh_gemm_mx8_f16: operands and workspace must be 16-byte aligned");
   VH_REQUIRE(K * 2 < (1ll << 31) && M * K * 2 < (1ll << 31) && N * K * 2 < (1ll << 31),
              "vh_gemm_mx8_f16: operands over 2 GiB");
@@ -2080,6 +2110,13 @@ extern "C" int vh_gemm_mx8_f16(const uint16_t* x, const int32_t* ex, const uint1
   g.sc = M * N;             // and writes partial z
   g.epi.mode = EPI_PLAIN;
   g.epi.out_dtype = VH_F32;
+  if (direct) {  // the exponents, alpha, bias and the rounding in the GEMM's own epilogue
+    g.C = y;
+    g.ldc = ldy;
+    g.epi = *epi;
+    g.ea = ex;
+    g.eb = ew;
+  }
   hipStream_t st = vh::as_stream(stream);
   int rc;
   switch (tile) {
@@ -2088,7 +2125,7 @@ extern "C" int vh_gemm_mx8_f16(const uint16_t* x, const int32_t* ex, const uint1
     case 3: rc = launch_f8dl<256, 128, 3, 128, 2, 2, OP_F16X>(g, splits, st); break;
     default: rc = launch_f8dl<128, 128, 4, 128, 2, 2, OP_F16X>(g, splits, st); break;
   }
-  if (rc) return rc;
+  if (rc || direct) return rc;
   const int64_t quads = M * N / 4;
   hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, (const float*)part,
                      (int)splits, M, N, *epi, y, ldy, ex, ew);

@@ -380,15 +380,17 @@ def quantize_mx8_f16(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
 
 def mx8_f16_plan(M: int, N: int, K: int) -> Tuple[int, int]:
     """(tile, splits) of ``linear_mx8_f16``.  Measured on MI355X at K = N =
-    4096: M = 256 takes 64x128 tiles with K split in two (19.2 us; 128x128 in
-    four 23.7, unsplit 24.6), M = 2048 256x128 unsplit (77.2 us; 128x128
-    82.7).  Below 1024 rows: 64x128, K split until the grid reaches 256
-    workgroups (each split at least 512 elements); from 1024: 256x128."""
+    4096, one split storing through the GEMM's own epilogue: M = 2048 on
+    256x128 tiles 56.0 us (1226 TFLOP/s; 128x128 65.0; 256x128 in two
+    splits plus the reduction 92.5); M = 256 on 64x128 tiles 18.9 us (in two
+    splits 19.0, 128x64 19.0, 128x128 25.0).  Below 1024 rows: 64x128, K
+    split until the grid reaches 128 workgroups (each split at least 512
+    elements); from 1024: 256x128."""
     if M >= 1024:
         return 3, 1
     tiles = -(-M // 64) * -(-N // 128)
     splits = 1
-    while tiles * splits < 256 and K % (splits * 2 * 512) == 0 and splits < 8:
+    while tiles * splits < 128 and K % (splits * 2 * 512) == 0 and splits < 8:
         splits *= 2
     return 1, splits
 
@@ -398,7 +400,8 @@ def linear_mx8_f16(x16: torch.Tensor, ex: torch.Tensor, weight: MX8F16Weight, ou
     """MX-int8 ``linear_mx`` (``ops/quantized.py:651-723``) on the exact fp16
     operands of ``quantize_mx8_f16`` and ``bake_mx8_f16``: an fp16 GEMM over
     K splits and one reduction that applies ``2**(E_row + E_col)``, alpha,
-    bias and the output rounding."""
+    bias and the output rounding; unsplit, the GEMM's epilogue applies them
+    itself."""
     M, K = x16.shape
     if K != weight.K:
         raise RuntimeError("linear_mx8_f16: contraction mismatch")
@@ -411,10 +414,14 @@ def linear_mx8_f16(x16: torch.Tensor, ex: torch.Tensor, weight: MX8F16Weight, ou
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
     bias = _bias_operand(bias)
     epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
-    part = torch.empty(splits * M * N, dtype=torch.float32, device=x16.device)
+    # one split stores through the GEMM's own epilogue (rows of N outputs,
+    # N a multiple of 8): no float32 partials
+    direct = splits == 1 and N % 8 == 0
+    part = None if direct else torch.empty(splits * M * N, dtype=torch.float32, device=x16.device)
     _lib.check(load().vh_gemm_mx8_f16(ptr(x16), ptr(ex), ptr(weight.w), ptr(weight.e), M, N, K,
                                       ctypes.c_void_p(ctypes.addressof(epi)), ptr(out), N, ptr(part),
-                                      part.numel() * 4, splits, tile, ctypes.c_void_p(stream_of(x16))),
+                                      0 if part is None else part.numel() * 4, splits, tile,
+                                      ctypes.c_void_p(stream_of(x16))),
                "vh_gemm_mx8_f16")
     return out
 
