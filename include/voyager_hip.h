@@ -354,6 +354,26 @@ int vh_gemv_nf4_m1(const void* x, int32_t x_dtype, float quant_max, const vh_for
                    const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N, int64_t K,
                    const vh_epilogue* epi, void* y, vh_stream_t stream);
 
+/* MXNF4 linear_mx at any M (prefill; ops/quantized.py:651-723 with the
+ * operand decode of :574-591): x_idx [M, K] codebook indices (0..15, one
+ * byte each, as quantize_mx packs them) with x_scale [M, K / 64] codes of
+ * x_scale_fmt; the weight as vh_pack_nf4 bakes it (w_packed) with w_scale
+ * tile-major [N / 16][K / 64][16] codes of w_scale_fmt (the decode GEMV's
+ * operands).  y = epilogue(sum_k xd[m,k] wd[n,k]), xd = bf16(level[x_idx] *
+ * x_scale) and wd likewise -- the reference's decoded operands exactly --
+ * accumulated in float32.  Needs N % 16 == 0, K % 64 == 0.  tile 0 and
+ * splits 0 choose (vh_gemm_nf4_plan); tile 1: 128 x 128, 2: 256 x 128;
+ * with more than one K split the float32 partials go to `part` (splits * M
+ * * N floats, ldy == N) and one reduction applies the epilogue. */
+int vh_gemm_nf4(const uint8_t* x_idx, const uint8_t* x_scale, const vh_format* x_scale_fmt, int64_t M,
+                const uint8_t* w_packed, const uint8_t* w_scale, const vh_format* w_scale_fmt,
+                const int8_t* levels16, int64_t N, int64_t K, const vh_epilogue* epi, void* y, int64_t ldy,
+                int32_t tile, int32_t splits, float* part, int64_t part_bytes, vh_stream_t stream);
+/* The tile, split count and block rows vh_gemm_nf4 takes for a shape (the
+ * caller's nonzero *tile / *splits are kept, the splits rounded to whole
+ * ranges of 64-element blocks), so the caller can size its workspace. */
+int vh_gemm_nf4_plan(int64_t M, int64_t N, int64_t K, int32_t* tile, int32_t* splits, int64_t* bm);
+
 /* ------------------------------------------------- decoder-layer decode step
  * One decode step (a batch of single tokens, M <= 16) of a Llama-style layer
  * whose linears are MX-int8 (int8 codes, block 16 along K, power-of-two

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import voyager_amd.library  # noqa: F401  (defines quantized_ops)
-from helpers import assert_same_bits, max_rel_err
+from helpers import assert_same_bits, assert_within_bf16_ulps, max_rel_err
 from oracle import ops as O
 from oracle import tables as T
 
@@ -317,6 +317,49 @@ def test_linear_nf4_gemv_cfg3(M, K, N):
         one = gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d), fused=True)
         assert_same_bits(one, two, "one launch vs two")
         assert torch.equal(got, one)
+
+
+@pytest.mark.parametrize("M,K,N,tile,splits", [(17, 1024, 256, 0, 0), (64, 4096, 1024, 0, 0), (300, 576, 1040, 1, 1),
+                                               (300, 576, 1040, 2, 3), (2048, 4096, 4096, 0, 0), (33, 64, 16, 0, 0),
+                                               (40, 4160, 48, 1, 7)])
+def test_linear_nf4_prefill(M, K, N, tile, splits):
+    """MXNF4 linear_mx above the GEMV's 16 rows, on the GEMV's baked weight:
+    against the oracle's linear_mx (1e-2), and -- both operands decoded
+    exactly as the reference decodes them -- within one bf16 ulp of the
+    float64 product of the oracle's decoded operands (plus the float32
+    accumulation allowance); ragged rows, columns and block counts, bf16
+    and float32 results with alpha and bias."""
+    from voyager_amd import gemm
+
+    vt = T.quantization_map("lut4_to_int6")
+    index, entries, mid = T.codebook_index_table(vt)
+    stab = T.quantization_map("fp8_e5m3")
+    g = torch.Generator().manual_seed(M + K + N)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    x[0, :64] = 0  # an all-zero block
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    sx, cx = O.quantize_mx(x, index, [-1], 64, 31.0, False, stab, mid)
+    sw, cw = O.quantize_mx(w, index, [-1], 64, 31.0, False, stab)
+    exp = O.linear_mx(cx, cw, input_scale=sx, weight_scale=sw, block_size=64, input_code=entries,
+                      weight_code=entries)
+    xd = O.dequantize_mx_parts(cx, sx, entries, 64).double()
+    wd = O.dequantize_mx_parts(cw, sw, entries, 64).double()
+    d = "cuda"
+    wb = gemm.bake_nf4_weight(w.to(d), index.to(d), stab.to(d), entries.to(d))
+    t, sp = gemm.nf4_prefill_plan(M, N, K, tile, splits)
+    print(f"nf4 prefill M={M} K={K} N={N}: tile {t}, {sp} K splits", flush=True)
+    got = gemm.linear_nf4_prefill(x.to(d), wb, index.to(d), stab.to(d), tile=tile, splits=splits)
+    assert got.dtype == torch.bfloat16 and list(got.shape) == [M, N]
+    assert max_rel_err(got, exp) < TOL
+    assert_within_bf16_ulps(got, xd @ wd.T, 1.0, 2.0**-14 * (xd.abs() @ wd.abs().T), "prefill")
+    if M > 16:
+        assert torch.equal(got, gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d)))
+    alpha = torch.tensor(0.75, device=d)
+    bias = (torch.randn(N, generator=g)).bfloat16()
+    got32 = gemm.linear_nf4_prefill(x.to(d), wb, index.to(d), stab.to(d), out_dtype=torch.float32, bias=bias.to(d),
+                                    alpha=alpha, tile=tile, splits=splits)
+    ref = (xd @ wd.T) * 0.75 + bias.double()
+    assert max_rel_err(got32, ref) < 1e-5
 
 
 @pytest.mark.parametrize("K,N", [(1024, 64), (4096, 8192)])

@@ -124,8 +124,8 @@ def test_lower_mxint8_linear(with_bias):
 
 @pytest.mark.parametrize("M", [1, 32])
 def test_lower_mxnf4_linear(M):
-    """M = 1 runs the GEMV on nibble-packed weights, M = 32 the
-    reference-form ops on the weights kept beside them."""
+    """M = 1 runs the GEMV on nibble-packed weights, M = 32 the prefill GEMM
+    on the same baked bytes."""
     vt = T.quantization_map("lut4_to_int6")
     index, entries, mid = T.codebook_index_table(vt)
     stab = T.quantization_map("fp8_e5m3")

@@ -1814,6 +1814,255 @@ struct Fmts {
   static constexpr int a = A, b = B;
 };
 
+// ------------------------------------------------------------ MXNF4 prefill
+// linear_mx of codebook operands at any M (ops/quantized.py:651-723 with
+// the decode of :574-591): A = the activation's codebook indices, one byte
+// each [M, K], with its block scales as codes of their map [M, K / 64]; B =
+// the weight as the decode GEMV bakes it (vh_pack_nf4: nibbles in MFMA lane
+// order, scale bytes tile-major [N / 16][K / 64][16]), so one baked copy
+// serves both.  Every element is decoded while staging to exactly the
+// operand the reference multiplies, bf16(level * scale): the index through
+// a 16-entry table of level + 128 (lut16: three v_perm per four), an
+// unsigned-byte convert, one fma by the block scale that also removes the
+// 128 bias ((level + 128) s and 128 s are exact in float32), and the
+// hardware round to bf16.  Then v_mfma_f32_32x32x16_bf16 with float32
+// accumulation, as the reference's float32 GEMM of the decoded operands:
+// the results differ by summation order only.  A stage is one 64-element
+// block: per row four 16-element chunks, each one load of 16 index bytes (A)
+// or one 8-byte GEMV record (B, lane (r % 16) + 16 c of the row's tile) and
+// the row's scale byte; loads run P - 1 stages ahead in registers.
+struct Nf4Args {
+  uint4 lvb;        // level + 128 of each index, one byte each
+  vh_format a_sf;   // the activation's scale map
+  vh_format b_sf;   // the weight's scale map
+};
+
+// four indices (one per byte, 0..15) -> four bf16 pairs' worth of floats
+__device__ __forceinline__ void nf4_levels4(uint32_t biased, float s, float nb, float (&f)[4]) {
+  f[0] = fmaf((float)(biased & 0xffu), s, nb);
+  f[1] = fmaf((float)((biased >> 8) & 0xffu), s, nb);
+  f[2] = fmaf((float)((biased >> 16) & 0xffu), s, nb);
+  f[3] = fmaf((float)(biased >> 24), s, nb);
+}
+
+// Sixteen biased levels (four dwords, element order) times s -> 16 bf16.
+__device__ __forceinline__ void nf4_pack16(const uint32_t (&l)[4], float s, uint4& lo, uint4& hi) {
+  const float nb = -128.0f * s;
+  uint32_t o[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float f[4];
+    nf4_levels4(l[j], s, nb, f);
+    o[2 * j] = f2bf2_hw(f[0], f[1]);
+    o[2 * j + 1] = f2bf2_hw(f[2], f[3]);
+  }
+  lo = make_uint4(o[0], o[1], o[2], o[3]);
+  hi = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+template <int BM, int BN, int WM, int WN, int P>
+__global__ void __launch_bounds__(WM * WN * 64) k_gemm_nf4(GemmArgs g, Nf4Args q, int kcs, float* __restrict__ part) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int CA = BM * 4 / NT, CB = BN * 4 / NT;  // 16-element chunks per thread and stage
+  static_assert(CA >= 1 && CB >= 1 && (BM * 4) % NT == 0 && (BN * 4) % NT == 0, "stage chunks must divide");
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1 && BM % (WM * 32) == 0 && BN % (WN * 32) == 0 && BN % 16 == 0,
+                "bad wave layout");
+  static_assert(WN * BM * (BN / WN + 8) * 2 <= 2 * (BM + BN) * ROWP, "epilogue tile does not fit the stage LDS");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* As = smem;                  // [2][BM][ROWP]: 64 bf16 per row
+  uint8_t* Bs = smem + 2 * BM * ROWP;  // [2][BN][ROWP]
+  float* s_sa = (float*)(smem + 2 * (BM + BN) * ROWP);  // [256] decoded activation scale codes
+  float* s_sb = s_sa + 256;                             // [256] decoded weight scale codes
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int64_t m0, n0;
+  tile_origin(g.M, g.N, BM, BN, g.group_m, m0, n0);
+  const int nbk = (int)(g.K / 64);  // blocks of a row
+  // split blockIdx.y takes blocks [kb0, kb0 + nk)
+  const int kb0 = (int)blockIdx.y * kcs;
+  const int nk = (nbk - kb0) < kcs ? (nbk - kb0) : kcs;
+  const int64_t rows_a = (g.M - m0) < BM ? (g.M - m0) : BM;
+  const int64_t rows_b = (g.N - n0) < BN ? (g.N - n0) : BN;  // a multiple of 16
+  const rsrc_t ad = make_rsrc(g.A + m0 * g.lda, rows_a * g.lda);
+  const rsrc_t as = make_rsrc(g.a_scale + m0 * g.lds_a, rows_a * g.lds_a);
+  const rsrc_t bd = make_rsrc(g.B + (n0 / 16) * nbk * 512, rows_b / 16 * nbk * 512);
+  const rsrc_t bs = make_rsrc(g.b_scale + (n0 / 16) * nbk * 16, rows_b / 16 * nbk * 16);
+  uint32_t base;
+  asm volatile("v_mov_b32 %0, 0x3020100" : "=v"(base));
+
+  // chunk i of this thread: row ch / 4, elements 16 (ch % 4) .. + 15 of the stage
+  int aoff[CA], asrow[CA], boff[CB], bsoff[CB];
+#pragma unroll
+  for (int i = 0; i < CA; ++i) {
+    const int ch = tid + i * NT, r = ch >> 2;
+    aoff[i] = r * (int)g.lda + (ch & 3) * 16;
+    asrow[i] = r * (int)g.lds_a;
+  }
+#pragma unroll
+  for (int i = 0; i < CB; ++i) {
+    const int ch = tid + i * NT, r = ch >> 2;
+    boff[i] = ((r >> 4) * nbk * 64 + (r & 15) + 16 * (ch & 3)) * 8;
+    bsoff[i] = (r >> 4) * nbk * 16 + (r & 15);
+  }
+
+  static_assert(P >= 2 && P % 2 == 0, "an even number of register sets");
+  uint4 ra[P][CA];
+  uint2 rb[P][CB];
+  uint32_t sa[P][CA], sb[P][CB];
+  // Stage s into set j (clamped to the last stage: a prefetch past the end
+  // re-reads it and is never stored).
+  auto fetch = [&](int j, int s) {
+    const int kb = kb0 + (s < nk ? s : nk - 1);
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      ra[j][i] = bload16(ad, aoff[i] + kb * 64);
+      sa[j][i] = bload1(as, asrow[i] + kb);
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      rb[j][i] = bload8(bd, boff[i] + kb * 512);
+      sb[j][i] = bload1(bs, bsoff[i] + kb * 16);
+    }
+  };
+  auto stash = [&](int j, int st) {
+    uint8_t* a = As + st * BM * ROWP;
+    uint8_t* b = Bs + st * BN * ROWP;
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      const int ch = tid + i * NT;
+      const uint32_t w[4] = {ra[j][i].x, ra[j][i].y, ra[j][i].z, ra[j][i].w};
+      uint32_t l[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) l[t] = lut_lo(w[t], base, q.lvb);
+      uint4 lo, hi;
+      nf4_pack16(l, s_sa[sa[j][i] & 0xffu], lo, hi);
+      uint8_t* d = a + (ch >> 2) * ROWP + (ch & 3) * 32;
+      *(uint4*)d = lo;
+      *(uint4*)(d + 16) = hi;
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int ch = tid + i * NT;
+      // byte t of the record: element t in its low nibble, t + 8 in its high one
+      const uint32_t l[4] = {lut_lo(rb[j][i].x, base, q.lvb), lut_lo(rb[j][i].y, base, q.lvb),
+                             lut_hi(rb[j][i].x, base, q.lvb), lut_hi(rb[j][i].y, base, q.lvb)};
+      uint4 lo, hi;
+      nf4_pack16(l, s_sb[sb[j][i] & 0xffu], lo, hi);
+      uint8_t* d = b + (ch >> 2) * ROWP + (ch & 3) * 32;
+      *(uint4*)d = lo;
+      *(uint4*)(d + 16) = hi;
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  auto compute = [&](int st) {
+    const uint8_t* a = As + st * BM * ROWP + (wm * (BM / WM) + lrow) * ROWP;
+    const uint8_t* b = Bs + st * BN * ROWP + (wn * (BN / WN) + lrow) * ROWP;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int off = kk * 32 + lhalf * 16;
+      bf16x8 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = *(const bf16x8*)(a + i * 32 * ROWP + off);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = *(const bf16x8*)(b + j * 32 * ROWP + off);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int j = 0; j < P; ++j) fetch(j, j);
+  // the scale maps' values, while the first stages load
+  for (int c = tid; c < 256; c += NT) {
+    s_sa[c] = fmt_decode((uint32_t)c, q.a_sf, nullptr);
+    s_sb[c] = fmt_decode((uint32_t)c, q.b_sf, nullptr);
+  }
+  __syncthreads();
+  stash(0, 0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ks += P) {
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      // stage ks + j is in LDS buffer j % 2; set j is free
+      fetch(j, ks + j + P);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(j & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + j + 1 >= nk) goto done;
+      stash((j + 1) % P, (j + 1) & 1);
+      __syncthreads();
+    }
+  }
+done:
+  __syncthreads();  // the LDS epilogue reuses the stage buffers
+  if (gridDim.y == 1) {
+    store_tile<TM, TN, WM, WN>(g, acc, smem, m0, n0, wave, wm, wn, lane);
+  } else {
+    GemmArgs p = g;
+    p.C = part + (int64_t)blockIdx.y * g.M * g.N;
+    p.ldc = g.N;
+    p.epi.mode = EPI_PLAIN;
+    p.epi.out_dtype = VH_F32;
+    p.epi.scale = nullptr;
+    p.epi.bias = nullptr;
+    store_tile_direct<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane);
+  }
+}
+
+// Splits of K (in 64-element blocks) that fill the CUs when the tile grid
+// alone does not; each split keeps at least two blocks.
+inline int nf4_splits(int64_t tiles, int64_t nbk) {
+  if (tiles >= 192) return 1;
+  int64_t sp = (256 + tiles - 1) / tiles;
+  if (sp > nbk / 2) sp = nbk / 2;
+  return sp < 1 ? 1 : (int)sp;
+}
+
+template <int BM, int BN, int WM, int WN>
+int launch_nf4(GemmArgs g, const Nf4Args& q, int splits, float* part, hipStream_t stream) {
+  g.group_m = 8;
+  constexpr int NT = WM * WN * 64;
+  const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+  const int nbk = (int)(g.K / 64);
+  const int kcs = (nbk + splits - 1) / splits;
+  const int sp = (nbk + kcs - 1) / kcs;  // every split has at least one block
+  const size_t smem = 2 * (BM + BN) * ROWP + 2 * 256 * 4;
+  static_assert(2 * (BM + BN) * ROWP + 2 * 256 * 4 <= 160 * 1024, "LDS");
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)k_gemm_nf4<BM, BN, WM, WN, 2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)smem) != hipSuccess) {
+      vh::set_error("vh_gemm_nf4: cannot reserve %zu bytes of LDS", smem);
+      return VH_ELAUNCH;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_gemm_nf4<BM, BN, WM, WN, 2>), dim3((unsigned)tiles, (unsigned)sp), dim3(NT), smem, stream, g,
+                     q, kcs, sp > 1 ? part : nullptr);
+  if (sp > 1) {
+    const int64_t quads = g.M * g.N / 4;
+    hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, part, sp, g.M,
+                       g.N, g.epi, g.C, g.ldc);
+  }
+  return vh::check_launch("vh_gemm_nf4");
+}
+
 }  // namespace
 
 namespace {
@@ -2130,4 +2379,70 @@ extern "C" int vh_gemm_mx8_f16(const uint16_t* x, const int32_t* ex, const uint1
   hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, (const float*)part,
                      (int)splits, M, N, *epi, y, ldy, ex, ew);
   return vh::check_launch("vh_gemm_mx8_f16");
+}
+
+extern "C" int vh_gemm_nf4(const uint8_t* x_idx, const uint8_t* x_scale, const vh_format* x_scale_fmt, int64_t M,
+                           const uint8_t* w_packed, const uint8_t* w_scale, const vh_format* w_scale_fmt,
+                           const int8_t* levels16, int64_t N, int64_t K, const vh_epilogue* epi, void* y,
+                           int64_t ldy, int32_t tile, int32_t splits, float* part, int64_t part_bytes,
+                           vh_stream_t stream) {
+  VH_REQUIRE(x_idx && x_scale && x_scale_fmt && w_packed && w_scale && w_scale_fmt && levels16 && epi && y,
+             "vh_gemm_nf4: null argument");
+  VH_REQUIRE(M >= 1 && N > 0 && K > 0 && N % 16 == 0 && K % 64 == 0,
+             "vh_gemm_nf4: needs N %% 16 == 0 and K %% 64 == 0");
+  VH_REQUIRE(M * K < (1ll << 31) && (N / 16) * (K / 64) * 512 < (1ll << 31), "vh_gemm_nf4: operands over 2 GiB");
+  VH_REQUIRE((uintptr_t)x_idx % 16 == 0 && K % 16 == 0 && (uintptr_t)w_packed % 8 == 0,
+             "vh_gemm_nf4: misaligned operand");
+  VH_REQUIRE(epi->mode == EPI_PLAIN && (epi->out_dtype == VH_BF16 || epi->out_dtype == VH_F32) && ldy >= N,
+             "vh_gemm_nf4: unsupported epilogue");
+  VH_REQUIRE(!epi->scale || epi->scale_dtype == VH_BF16 || epi->scale_dtype == VH_F32,
+             "vh_gemm_nf4: scale must be bf16 or float32");
+  VH_REQUIRE(!epi->bias || epi->bias_dtype == VH_BF16 || epi->bias_dtype == VH_F32,
+             "vh_gemm_nf4: bias must be bf16 or float32");
+  for (const vh_format* f : {x_scale_fmt, w_scale_fmt})
+    VH_REQUIRE(f->kind == VH_FMT_INT || f->kind == VH_FMT_MINIFLOAT || f->kind == VH_FMT_POSIT,
+               "vh_gemm_nf4: the scale maps need a closed form with packed codes");
+  uint8_t lvb[16];
+  for (int v = 0; v < 16; ++v) lvb[v] = (uint8_t)(levels16[v] + 128);
+  uint32_t t[4];
+  memcpy(t, lvb, 16);
+  Nf4Args q;
+  q.lvb = make_uint4(t[0], t[1], t[2], t[3]);
+  q.a_sf = *x_scale_fmt;
+  q.b_sf = *w_scale_fmt;
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.A = x_idx;
+  g.B = w_packed;
+  g.C = y;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = K;
+  g.ldc = ldy;
+  g.a_scale = x_scale;
+  g.b_scale = w_scale;
+  g.lds_a = K / 64;
+  g.epi = *epi;
+  hipStream_t st = vh::as_stream(stream);
+  int64_t bm = 0;
+  VH_REQUIRE(vh_gemm_nf4_plan(M, N, K, &tile, &splits, &bm) == VH_OK, "vh_gemm_nf4: tile must be 0, 1 or 2");
+  VH_REQUIRE(splits == 1 || (part && part_bytes >= (int64_t)splits * M * N * 4 && (ldy == N) && N % 4 == 0),
+             "vh_gemm_nf4: %d K splits need a workspace of %lld bytes (and ldy == N)", splits,
+             (long long)((int64_t)splits * M * N * 4));
+  if (tile == 2) return launch_nf4<256, 128, 4, 2>(g, q, splits, part, st);
+  return launch_nf4<128, 128, 2, 2>(g, q, splits, part, st);
+}
+
+extern "C" int vh_gemm_nf4_plan(int64_t M, int64_t N, int64_t K, int32_t* tile, int32_t* splits, int64_t* bm) {
+  VH_REQUIRE(tile && splits && bm && M >= 1 && N > 0 && K >= 64, "vh_gemm_nf4_plan: bad arguments");
+  // 256 x 128 tiles (8 waves) while they fill the 256 CUs, else 128 x 128
+  // (4 waves) with K split to fill them
+  if (*tile == 0) *tile = ((M + 255) / 256) * ((N + 127) / 128) >= 192 ? 2 : 1;
+  VH_REQUIRE(*tile == 1 || *tile == 2, "vh_gemm_nf4_plan: tile must be 0, 1 or 2");
+  *bm = *tile == 2 ? 256 : 128;
+  if (*splits <= 0) *splits = nf4_splits(((M + *bm - 1) / *bm) * ((N + 127) / 128), K / 64);
+  const int64_t nbk = K / 64, kcs = (nbk + *splits - 1) / *splits;
+  *splits = (int32_t)((nbk + kcs - 1) / kcs);
+  return VH_OK;
 }

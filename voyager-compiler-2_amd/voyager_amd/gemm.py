@@ -542,19 +542,64 @@ def _nf4_one_launch_pays(N: int, K: int) -> bool:
     return N <= 8192 and K <= 4096
 
 
+def nf4_prefill_plan(M: int, N: int, K: int, tile: int = 0, splits: int = 0) -> Tuple[int, int]:
+    """(tile, splits) ``vh_gemm_nf4`` takes for a shape."""
+    t, sp, bm = ctypes.c_int32(tile), ctypes.c_int32(splits), ctypes.c_int64(0)
+    _lib.check(load().vh_gemm_nf4_plan(M, N, K, ctypes.byref(t), ctypes.byref(sp), ctypes.byref(bm)),
+               "vh_gemm_nf4_plan")
+    return t.value, sp.value
+
+
+def linear_nf4_prefill(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, scale_qmap: torch.Tensor,
+                       out_dtype=torch.bfloat16, bias=None, alpha=None, tile: int = 0,
+                       splits: int = 0) -> torch.Tensor:
+    """MXNF4 ``linear_mx`` at any M on the GEMV's baked weight: the
+    activation's ``quantize_mx`` to index and scale bytes, then
+    ``vh_gemm_nf4``, which decodes both operands while staging to the
+    reference's ``bf16(level * scale)`` and multiplies them on the bf16 MFMA
+    with float32 accumulation."""
+    from . import packed as _packed
+
+    M, K = x.shape
+    if K != weight.K:
+        raise RuntimeError("linear_nf4_prefill: contraction mismatch")
+    px = _packed.quantize_mx_packed(x.contiguous(), index_table, [-1], 64, 31.0, False, scale_qmap)
+    y = torch.empty(M, weight.N, dtype=out_dtype, device=x.device)
+    if alpha is not None:
+        alpha = alpha.reshape(()).to(torch.float32).contiguous()
+    bias = _bias_operand(bias)
+    epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
+    lv = ctypes.create_string_buffer(weight.levels, 16)
+    tile, splits = nf4_prefill_plan(M, weight.N, K, tile, splits)
+    part = torch.empty(splits * M * weight.N, dtype=torch.float32, device=x.device) if splits > 1 else None
+    st = load().vh_gemm_nf4(ctypes.c_void_p(px.codes.data_ptr()), ctypes.c_void_p(px.scale.data_ptr()),
+                            ctypes.byref(px.scale_fmt.fmt), M, ctypes.c_void_p(weight.packed.data_ptr()),
+                            ctypes.c_void_p(weight.scale.data_ptr()), ctypes.byref(weight.scale_fmt.fmt), lv,
+                            weight.N, weight.K, ctypes.c_void_p(ctypes.addressof(epi)),
+                            ctypes.c_void_p(y.data_ptr()), weight.N, tile, splits, ptr(part),
+                            0 if part is None else part.numel() * 4, ctypes.c_void_p(stream_of(x)))
+    _lib.check(st, "vh_gemm_nf4")
+    return y
+
+
 def linear_nf4(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, scale_qmap: torch.Tensor,
                out_dtype=torch.bfloat16, bias=None, alpha=None, fused=None) -> torch.Tensor:
-    """MXNF4 ``linear_mx`` at decode shapes (M <= 16): the activations are
-    quantized like the reference's in-graph ``quantize_mx`` (one launch that
-    emits their int8 levels and float32 block scales), then the weight-
-    streaming GEMV.  One bfloat16 row is quantized inside the GEMV instead
-    (``vh_gemv_nf4_m1``: the same levels and scales, one launch) when the
-    formats allow and the shape is small enough for that to pay
-    (``_nf4_one_launch_pays``); ``fused`` = False keeps the two launches,
-    True requires the one."""
+    """MXNF4 ``linear_mx`` on the baked weight.  At decode shapes (M <= 16)
+    the activations are quantized like the reference's in-graph
+    ``quantize_mx`` (one launch that emits their int8 levels and float32
+    block scales), then the weight-streaming GEMV.  One bfloat16 row is
+    quantized inside the GEMV instead (``vh_gemv_nf4_m1``: the same levels
+    and scales, one launch) when the formats allow and the shape is small
+    enough for that to pay (``_nf4_one_launch_pays``); ``fused`` = False
+    keeps the two launches, True requires the one.  More rows take the
+    prefill GEMM (``linear_nf4_prefill``)."""
     M, K = x.shape
     if K != weight.K:
         raise RuntimeError("linear_nf4: contraction mismatch")
+    if M > 16:
+        if fused:
+            raise RuntimeError("linear_nf4: the one-launch path takes one row")
+        return linear_nf4_prefill(x, weight, index_table, scale_qmap, out_dtype, bias, alpha)
     xc = x.contiguous()
     ec = formats.classify(index_table)
     sc = formats.classify(scale_qmap)

@@ -19,8 +19,8 @@ library runs packed:
   ``linear_mx``: int8 codes plus scale bytes and the MX-int8 GEMM.
 * ``mxnf4``  -- ``quantize_mx(x, lut4_to_int6 index, [-1], 64, 31,
   scale_qmap=fp8_e5m3)`` -> ``linear_mx`` with codebook entries: at most 16
-  activation rows run the weight-streaming GEMV on nibble-packed weights;
-  more rows take the reference-form ops.
+  activation rows run the weight-streaming GEMV on nibble-packed weights,
+  more the prefill GEMM on the same baked bytes.
 
 Each site's weights are packed once at ``lower`` time and their reference-form
 copies dropped where no other node reads them.  NVFP4 needs CUDA (as the
@@ -321,23 +321,19 @@ def lowered_mxint8_linear(x, qmap, w_codes, w_scale, w_bias, block_size: int, bi
     return y.reshape(*x.shape[:-1], w_codes.shape[0])
 
 
-def lowered_mxnf4_linear(x, index, scale_qmap, output_code, input_code, weight_code, w_packed, w_scale_bytes,
-                         levels: Tuple[int, ...], w_codes, w_scale):
-    """quantize_mx(x, lut4_to_int6, [-1], 64, 31, fp8_e5m3) -> linear_mx: the
-    GEMV on nibble-packed weights for up to 16 rows, the reference-form ops
-    otherwise. ``levels`` are the codebook's 16 int8 levels, read from
-    ``weight_code`` once when the graph is lowered, so no call copies device
-    memory to the host (a lowered graph can be captured in a HIP graph)."""
+def lowered_mxnf4_linear(x, index, scale_qmap, w_packed, w_scale_bytes, levels: Tuple[int, ...], N: int):
+    """quantize_mx(x, lut4_to_int6, [-1], 64, 31, fp8_e5m3) -> linear_mx on
+    the weight baked once for the GEMV: the GEMV for up to 16 rows, the
+    prefill GEMM on the same baked bytes for more (both decode each operand
+    to the reference's bf16(level * scale)).  ``levels`` are the codebook's
+    16 int8 levels, read from ``weight_code`` once when the graph is lowered,
+    so no call copies device memory to the host (a lowered graph can be
+    captured in a HIP graph)."""
     xr = _rows(x)
-    N, K = w_codes.shape
-    if xr.shape[0] <= 16:
-        sc = formats.classify(scale_qmap)
-        wt = gemm.NF4Weight(w_packed, w_scale_bytes, sc, bytes(levels), N, K)
-        y = gemm.linear_nf4(xr, wt, index, scale_qmap)
-    else:
-        s, c = torch.ops.quantized_ops.quantize_mx(xr, index, [-1], 64, 31.0, False, scale_qmap, output_code)
-        y = torch.ops.quantized_ops.linear_mx(c, w_codes, input_scale=s, weight_scale=w_scale, block_size=64,
-                                              input_code=input_code, weight_code=weight_code)
+    K = xr.shape[1]
+    sc = formats.classify(scale_qmap)
+    wt = gemm.NF4Weight(w_packed, w_scale_bytes, sc, bytes(levels), N, K)
+    y = gemm.linear_nf4(xr, wt, index, scale_qmap)
     return y.reshape(*x.shape[:-1], N)
 
 
@@ -426,8 +422,7 @@ def _insert(model: GraphModule, site: Site) -> Node:
         sbn = _const(model, graph, f"{name}_nf4_scale", sb)
         levels = tuple(gemm._levels_of(_attr(model, k["weight_code"])))
         return graph.call_function(lowered_mxnf4_linear,
-                                   (x, k["qmap"], k["scale_qmap"], k["output_code"], k["input_code"],
-                                    k["weight_code"], wpn, sbn, levels, site.weight, site.weight_scale))
+                                   (x, k["qmap"], k["scale_qmap"], wpn, sbn, levels, int(w.shape[0])))
 
 
 def _erase_unused(model: GraphModule, nodes: List[Node]) -> None:
@@ -514,9 +509,8 @@ class _SiteCheck(Interpreter):
             return lowered_mxint8_linear(x, env[k["qmap"]], codes, sbytes, bias_w,
                                          _arg(site.quantize, 3, "block_size"), bias)
         wp, sb = _bake_mxnf4(w, ws, env[k["scale_qmap"]])
-        return lowered_mxnf4_linear(x, env[k["qmap"]], env[k["scale_qmap"]], env[k["output_code"]],
-                                    env[k["input_code"]], env[k["weight_code"]], wp, sb,
-                                    tuple(gemm._levels_of(env[k["weight_code"]])), w, ws)
+        return lowered_mxnf4_linear(x, env[k["qmap"]], env[k["scale_qmap"]], wp, sb,
+                                    tuple(gemm._levels_of(env[k["weight_code"]])), int(w.shape[0]))
 
 
 def check_sites(model: GraphModule, args, kwargs=None):
