@@ -408,22 +408,33 @@ int vh_rmsnorm_mx8(const uint16_t* x, const uint16_t* w, int64_t M, int64_t H, f
  * biased exponent bytes 2**(byte - scale_bias), as vh_quantize_mx packs
  * them -- into the GEMV layout: w_codes N*K bytes, w_hb N*K/16 bytes.
  * paired != 0 interleaves rows [0, N/2) and [N/2, N) tile by tile (gate / up
- * projections for VH_GEMV_SWIGLU).  Blocks whose exponent is outside
- * [-24, 5] (and not all-zero) set VH_DECODE_ERR_WEIGHT_RANGE.  Needs
- * N % 16 == 0 (32 when paired) and K % 256 == 0.  Replaces the weight baking
- * of quantization/quantize_pt2e.py:819-828 for this format. */
+ * projections for VH_GEMV_SWIGLU).  The operand holds a block's exponent
+ * in the fp16 exponent field, so it must lie in [-24, 5]: with w_shift
+ * (int32 [N], rows in the input order) each row whose nonzero blocks leave
+ * that range is rebased to its largest exponent E (baked as e - (E - 5),
+ * w_shift[n] = E - 5, the GEMV multiplying the row's sums back; blocks more
+ * than 29 binades under E are flushed) and the others get 0; without it
+ * such blocks set VH_DECODE_ERR_WEIGHT_RANGE.  An infinite block scale
+ * always does.  Needs N % 16 == 0 (32 when paired) and K % 256 == 0.
+ * Replaces the weight baking of quantization/quantize_pt2e.py:819-828 for
+ * this format. */
 int vh_mx8_bake(const uint8_t* codes, const uint8_t* scale, int32_t scale_bias, int64_t N, int64_t K,
-                int32_t paired, uint8_t* w_codes, uint8_t* w_hb, int32_t* flag, vh_stream_t stream);
+                int32_t paired, uint8_t* w_codes, uint8_t* w_hb, int32_t* w_shift, int32_t* flag,
+                vh_stream_t stream);
 
 /* linear_mx of fake-quantized activations x_fq [M, K] (fp16 bits) and baked
  * MX-int8 weights with N output columns (2N baked rows for VH_GEMV_SWIGLU);
  * exact products, fp32 accumulation, bf16 output y [M, N] (optional for
  * SWIGLU), residual [M, N] for VH_GEMV_RESIDUAL, fq_out [M, N] (fp16 bits)
  * for SWIGLU.  tiles_per_block 1 or 2 (16 or 32 columns per workgroup,
- * STORE / RESIDUAL).  M <= 16, K % 256 == 0, N % 16 == 0. */
+ * STORE / RESIDUAL).  M <= 16, K % 256 == 0, N % 16 == 0.  Rebased
+ * operands (optional, else null): row_exp [M] -- each row of x_fq holds
+ * its values times 2**-row_exp[m] (vh_quantize_mx8_f16's exact fp16 rows),
+ * w_shift -- the bake's row shifts; the sums are multiplied by
+ * 2**(row_exp + w_shift) before the epilogue. */
 int vh_gemv_mx8(const uint16_t* x_fq, int64_t M, int64_t K, const uint8_t* w_codes, const uint8_t* w_hb, int64_t N,
                 int32_t mode, int32_t tiles_per_block, const uint16_t* residual, uint16_t* y, uint16_t* fq_out,
-                int32_t* flag, vh_stream_t stream);
+                const int32_t* row_exp, const int32_t* w_shift, int32_t* flag, vh_stream_t stream);
 
 /* Bake a KIVI main cache: T tokens (T % 32 == 0, head_dim 128) of each of
  * P = batch x kv-heads sequences -- codes (0..3, one per byte) [P, T, 128]

@@ -87,8 +87,85 @@ def test_gemv_mx8_residual_and_zero_blocks():
 def test_gemv_mx8_weight_range_error():
     w = torch.zeros(16, 256, dtype=torch.bfloat16, device=DEV)
     w[0, 0] = 2.0**-40  # block exponent -46: not representable in the fp16 operand
+    tab = decode.formats.quantization_map("int8", DEV)
+    p = decode.packed.quantize_mx_packed(w, tab, [-1], 16, 127.0, True)
     with pytest.raises(RuntimeError, match="weight block exponent"):
-        decode.quantize_mx8_weight(w)
+        decode.bake_mx8(p.codes, p.scale, p.bias, rebase=False)
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_gemv_mx8_rebased_weight_rows(M):
+    """Rows whose block exponents leave the fp16 operand's [-24, 5] bake
+    rebased to their largest (any magnitude), the others as before: tiny,
+    huge and mixed rows against the reference's linear_mx, and within one
+    bf16 ulp of the float64 product (blocks within 29 binades of their row's
+    largest, so nothing is flushed)."""
+    g = _gen(21 + M)
+    K, N = 512, 64
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    w[0] *= 2.0**-40                     # every block near 2**-52
+    w[1] *= 2.0**20                      # every block near 2**14
+    w[2, :256] *= 2.0**-25               # a row spanning 25 binades
+    w[3, 96:112] = 2.0**-100             # one tiny block in a normal row: the row is rebased, the block flushed
+    wg = w.to(DEV)
+    cw, sw = _mx_ref(wg)
+    exp = D.mx8_linear(x, cw, sw)
+    flag = decode.ErrorFlag(DEV)
+    wt = decode.quantize_mx8_weight(wg)
+    assert wt.shift is not None
+    shift = wt.shift.cpu()
+    assert int(shift[4:].abs().sum()) == 0 and all(int(shift[i]) != 0 for i in range(4))
+    xq = D.mx8_fake_quant(x)
+    got = decode.gemv_mx8(xq.half().to(DEV), wt, flag)
+    flag.check()
+    assert max_rel_err(got[:, 4:], exp[:, 4:]) < 1e-2
+    ref64, abs64 = _ref64(xq, cw, sw)
+    # the rebased rows: exact products, float32 sums, one rounding (row 3's
+    # flushed block is 2**-88 of its others, far under one ulp)
+    for n in range(4):
+        assert_within_bf16_ulps(got[:, n], ref64[:, n], 1.0, 2.0**-14 * abs64[:, n], f"row {n}")
+    assert_within_bf16_ulps(got[:, 4:], ref64[:, 4:], 1.0, 2.0**-14 * abs64[:, 4:], "rows in range")
+
+
+def test_step_checked_reruns_activation_overflow():
+    """A layer whose RMSNorm gain pushes its normed activations past the fp16
+    range of the GEMV operand: the fast step flags it, step_checked puts the
+    cache back and reruns the step on rebased rows, and the result matches
+    the oracle layer (which has no such range) within 1e-2; the cache ends
+    one position on, as after any step."""
+    cfg = D.Config(hidden=512, n_heads=4, n_kv_heads=1, head_dim=128, intermediate=1024)
+    w = D.random_layer(cfg, seed=5)
+    w["ln1"] = (w["ln1"].float() * 3.0e4).bfloat16()  # |h1| up to ~1e5
+    wd = {k: v.to(DEV) for k, v in w.items()}
+    mx = {k: _mx_ref(wd[k]) for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")}
+    layer = decode.DecoderLayer(wd, cfg.n_heads, cfg.n_kv_heads, cfg.eps, cfg.rope_theta, max_batch=2, max_pos=1024)
+    g = _gen(6)
+    B, n_main, n_res = 2, 256, 40
+    k_main, v_main = (torch.randn(B, 1, n_main, 128, generator=g).bfloat16() for _ in range(2))
+    k_res, v_res = (torch.randn(B, 1, n_res, 128, generator=g).bfloat16() for _ in range(2))
+    x = torch.randn(B, cfg.hidden, generator=g).bfloat16()
+    cache, kq, vq = decode.KiviCache.from_bf16(k_main.to(DEV), v_main.to(DEV), k_res.to(DEV), v_res.to(DEV),
+                                               capacity=512)
+    k_past = torch.cat((D.kivi_dequantize(kq[2].cpu(), kq[0].cpu(), kq[1].cpu(), -2), k_res), dim=2)
+    v_past = torch.cat((D.kivi_dequantize(vq[2].cpu(), vq[0].cpu(), vq[1].cpu(), -1), v_res), dim=2)
+    cos, sin = D.rope_cos_sin(torch.tensor([n_main + n_res]), 128, cfg.rope_theta)
+    exp = D.decode_layer(x, w, k_past, v_past, cos, sin, cfg, mx=mx)
+    assert float(exp["h1"].float().abs().max()) > 65504  # the fast path's operand cannot hold it
+    # the fast step alone flags it
+    state0 = cache.state.clone()
+    layer.step(x.to(DEV), cache, advance=False)
+    with pytest.raises(RuntimeError, match="fp16 range"):
+        layer.flag.check()
+    cache.state.copy_(state0)
+    out = layer.step_checked(x.to(DEV), cache)
+    torch.cuda.synchronize()
+    err = max_rel_err(out, exp["out"])
+    print(f"step_checked after an fp16-range overflow: {err:.5f} vs the oracle", flush=True)
+    assert err < 1e-2
+    assert cache.device_state() == (n_main, n_res + 1) == (cache.n_main, cache.n_res)
+    kr, vr = cache.residual_tokens(n_res + 1)
+    assert torch.equal(kr[:, :, n_res:].cpu(), exp["k"]) or max_rel_err(kr[:, :, n_res:], exp["k"]) < 1e-2
 
 
 @pytest.mark.parametrize("M", [1, 8])

@@ -297,6 +297,8 @@ struct GemvArgs {
   uint16_t* y;            // [M, n_out] bf16 (may be null for VH_GEMV_SWIGLU)
   _Float16* fq;           // [M, n_out] fp16 (VH_GEMV_SWIGLU)
   int* flag;
+  const int32_t* row_exp;  // or null: per row of x, 2**e its sums are multiplied by (rebased activations)
+  const int32_t* w_shift;  // or null: per weight row (original order), likewise (rebased weights)
 };
 
 template <int NT>
@@ -373,6 +375,17 @@ __global__ void __launch_bounds__(GEMV_WAVES * 64, 2) k_gemv_mx8(GemvArgs a) {
     for (int w = 0; w < GEMV_WAVES; ++w) sum += s_red[w][t][r][l2];
     v[t] = sum;
   }
+  if (a.row_exp || a.w_shift) {
+    // rebased operands: the sum times 2**(row exponent + column shift), exact
+    const int re = a.row_exp && row_ok ? a.row_exp[row] : 0;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      // the weight row of tile t's column: gate / up rows n and n_out + n when paired
+      const int64_t n = a.mode == VH_GEMV_SWIGLU ? (t == 0 ? 0 : a.n_out) + (int64_t)blockIdx.x * 16 + col
+                                                 : (tile0 + t) * 16 + col;
+      v[t] = ldexpf(v[t], re + (a.w_shift ? a.w_shift[n] : 0));
+    }
+  }
   if (a.mode == VH_GEMV_SWIGLU) {
     // LlamaMLP: act(gate) * up in bfloat16, then the MX-int8 fake
     // quantization of that product for the down projection (tiles 2i / 2i+1
@@ -402,8 +415,41 @@ __global__ void __launch_bounds__(GEMV_WAVES * 64, 2) k_gemv_mx8(GemvArgs a) {
 // Bake MX-int8 weights (one code byte per weight, one biased exponent byte per
 // 16-weight block, as vh_quantize_mx packs them) into the GEMV layout.
 // paired: rows [0, N/2) and [N/2, N) are interleaved tile by tile (gate / up).
+// Rebased rows (shift != null): a row whose nonzero blocks' exponents leave
+// [-24, 5] (the fp16 exponent field of the operand) is baked against its
+// largest, e - (E_row - 5), and its sums multiplied back by 2**(E_row - 5)
+// in the GEMV's epilogue (exact); its blocks more than 29 binades under
+// E_row are flushed (codes 0).  A row within range keeps shift 0 and bakes
+// as without rebasing.  One thread per row.
+__global__ void __launch_bounds__(256) k_mx8_row_shift(const uint8_t* __restrict__ codes,
+                                                       const uint8_t* __restrict__ scale, int bias, int64_t N,
+                                                       int64_t K, int32_t* __restrict__ shift) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t nb = K / 16;
+  int hi = -1000, lo = 1000;
+  for (int64_t b = 0; b < nb; ++b) {
+    const uint4 cv = *(const uint4*)(codes + n * K + b * 16);
+    const int byte = scale[n * nb + b];
+    if ((cv.x | cv.y | cv.z | cv.w) == 0u || byte == 255) continue;
+    const int e = byte - bias;
+    hi = e > hi ? e : hi;
+    lo = e < lo ? e : lo;
+  }
+  shift[n] = (hi == -1000 || (lo >= -24 && hi <= 5)) ? 0 : hi - 5;
+}
+
+__device__ __forceinline__ bool mx8_flushed(const uint8_t* scale, int64_t n, int64_t nb, int64_t blk, int bias,
+                                            const int32_t* shift) {
+  if (!shift) return false;
+  const int byte = scale[n * nb + blk];
+  return byte != 255 && byte - bias - shift[n] < -24;
+}
+
 __global__ void __launch_bounds__(256) k_bake_mx8_codes(const uint8_t* __restrict__ codes, int64_t N, int64_t K,
-                                                        int paired, uint8_t* __restrict__ out) {
+                                                        int paired, const uint8_t* __restrict__ scale, int bias,
+                                                        const int32_t* __restrict__ shift,
+                                                        uint8_t* __restrict__ out) {
   const int64_t nsp = K / 64;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (N / 16) * nsp * 64) return;
@@ -412,15 +458,18 @@ __global__ void __launch_bounds__(256) k_bake_mx8_codes(const uint8_t* __restric
   const int64_t src_tile = paired ? ((tile & 1) * (N / 32) + (tile >> 1)) : tile;
   const int64_t n = src_tile * 16 + (lane & 15);
   const int64_t k0 = sp * 64 + (lane >> 4) * 8;
-  const uint2 a = *(const uint2*)(codes + n * K + k0);
-  const uint2 b = *(const uint2*)(codes + n * K + k0 + 32);
+  uint2 a = *(const uint2*)(codes + n * K + k0);
+  uint2 b = *(const uint2*)(codes + n * K + k0 + 32);
+  // a flushed block's codes bake as 0 (the 8 codes of a lane lie in one block)
+  if (mx8_flushed(scale, n, K / 16, k0 / 16, bias, shift)) a = make_uint2(0u, 0u);
+  if (mx8_flushed(scale, n, K / 16, (k0 + 32) / 16, bias, shift)) b = make_uint2(0u, 0u);
   *(uint4*)(out + t * 16) = make_uint4(a.x ^ 0x80808080u, a.y ^ 0x80808080u, b.x ^ 0x80808080u, b.y ^ 0x80808080u);
 }
 
 __global__ void __launch_bounds__(256) k_bake_mx8_scales(const uint8_t* __restrict__ codes,
                                                          const uint8_t* __restrict__ scale, int bias, int64_t N,
-                                                         int64_t K, int paired, uint8_t* __restrict__ out,
-                                                         int* __restrict__ flag) {
+                                                         int64_t K, int paired, const int32_t* __restrict__ shift,
+                                                         uint8_t* __restrict__ out, int* __restrict__ flag) {
   const int64_t ngr = K / 256, nb = K / 16;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (N / 16) * ngr * 32) return;
@@ -436,8 +485,9 @@ __global__ void __launch_bounds__(256) k_bake_mx8_scales(const uint8_t* __restri
     const uint4* cp = (const uint4*)(codes + n * K + blk * 16);
     const uint4 cv = *cp;
     const bool zero = (cv.x | cv.y | cv.z | cv.w) == 0u;
-    int e = byte - bias;
-    if (zero) e = 0;  // an all-zero block contributes nothing at any scale
+    int e = byte - bias - (shift ? shift[n] : 0);
+    // an all-zero block contributes nothing at any scale, nor does a flushed one
+    if (zero || (shift && byte != 255 && e < -24)) e = 0;
     if (!zero && (byte == 255 || e < -24 || e > 5)) {
       atomicOr(flag, VH_DECODE_ERR_WEIGHT_RANGE);
       e = 0;
@@ -1283,27 +1333,34 @@ extern "C" int vh_rmsnorm_mx8(const uint16_t* x, const uint16_t* w, int64_t M, i
 }
 
 extern "C" int vh_mx8_bake(const uint8_t* codes, const uint8_t* scale, int32_t scale_bias, int64_t N, int64_t K,
-                           int32_t paired, uint8_t* w_codes, uint8_t* w_hb, int32_t* flag, vh_stream_t stream) {
+                           int32_t paired, uint8_t* w_codes, uint8_t* w_hb, int32_t* w_shift, int32_t* flag,
+                           vh_stream_t stream) {
   VH_REQUIRE(codes && scale && w_codes && w_hb && flag, "vh_mx8_bake: null argument");
   VH_REQUIRE(N > 0 && K > 0 && N % (paired ? 32 : 16) == 0 && K % 256 == 0,
              "vh_mx8_bake: needs N %% 16 == 0 (32 when paired) and K %% 256 == 0");
   hipStream_t s = vh::as_stream(stream);
+  if (w_shift)
+    hipLaunchKernelGGL(k_mx8_row_shift, dim3(blocks_for(N, 256)), dim3(256), 0, s, codes, scale, (int)scale_bias, N,
+                       K, w_shift);
   const int64_t nc = (N / 16) * (K / 64) * 64, ns = (N / 16) * (K / 256) * 32;
-  hipLaunchKernelGGL(k_bake_mx8_codes, dim3(blocks_for(nc, 256)), dim3(256), 0, s, codes, N, K, (int)paired, w_codes);
+  hipLaunchKernelGGL(k_bake_mx8_codes, dim3(blocks_for(nc, 256)), dim3(256), 0, s, codes, N, K, (int)paired, scale,
+                     (int)scale_bias, (const int32_t*)w_shift, w_codes);
   hipLaunchKernelGGL(k_bake_mx8_scales, dim3(blocks_for(ns, 256)), dim3(256), 0, s, codes, scale, (int)scale_bias, N,
-                     K, (int)paired, w_hb, (int*)flag);
+                     K, (int)paired, (const int32_t*)w_shift, w_hb, (int*)flag);
   return vh::check_launch("vh_mx8_bake");
 }
 
 extern "C" int vh_gemv_mx8(const uint16_t* x_fq, int64_t M, int64_t K, const uint8_t* w_codes, const uint8_t* w_hb,
                            int64_t N, int32_t mode, int32_t tiles_per_block, const uint16_t* residual, uint16_t* y,
-                           uint16_t* fq_out, int32_t* flag, vh_stream_t stream) {
+                           uint16_t* fq_out, const int32_t* row_exp, const int32_t* w_shift, int32_t* flag,
+                           vh_stream_t stream) {
   VH_REQUIRE(x_fq && w_codes && w_hb && flag, "vh_gemv_mx8: null argument");
   VH_REQUIRE(M >= 1 && M <= 16, "vh_gemv_mx8: M must be in [1, 16] (got %lld)", (long long)M);
   VH_REQUIRE(K > 0 && K % 256 == 0 && N > 0 && N % 16 == 0, "vh_gemv_mx8: needs K %% 256 == 0 and N %% 16 == 0");
   VH_REQUIRE(((uintptr_t)x_fq % 16) == 0 && ((uintptr_t)w_codes % 16) == 0 && ((uintptr_t)w_hb % 8) == 0,
              "vh_gemv_mx8: misaligned operand");
-  GemvArgs a{(const _Float16*)x_fq, (int32_t)M, K, w_codes, w_hb, N, mode, residual, y, (_Float16*)fq_out, (int*)flag};
+  GemvArgs a{(const _Float16*)x_fq, (int32_t)M, K, w_codes, w_hb, N, mode, residual, y, (_Float16*)fq_out, (int*)flag,
+             row_exp, w_shift};
   hipStream_t s = vh::as_stream(stream);
   const int64_t tiles = N / 16;
   if (mode == VH_GEMV_SWIGLU) {

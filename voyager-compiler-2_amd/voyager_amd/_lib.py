@@ -149,8 +149,8 @@ _SIGNATURES = {
                         ctypes.POINTER(Format), _P, _I64, _I64, _P, _P, _P], _I32),
     # decoder-layer decode step
     "vh_rmsnorm_mx8": ([_P, _P, _I64, _I64, _F32, _P, _P, _P, _P], _I32),
-    "vh_mx8_bake": ([_P, _P, _I32, _I64, _I64, _I32, _P, _P, _P, _P], _I32),
-    "vh_gemv_mx8": ([_P, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P], _I32),
+    "vh_mx8_bake": ([_P, _P, _I32, _I64, _I64, _I32, _P, _P, _P, _P, _P], _I32),
+    "vh_gemv_mx8": ([_P, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P], _I32),
     "vh_kivi_bake": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "vh_kivi_bake_residual": ([_P, _P, _I64, _I64, _P, _P, _P], _I32),
     # vh_kivi_attention takes a vh_kivi_desc*; voyager_amd.decode.KiviDesc mirrors it.

@@ -65,22 +65,31 @@ class MX8Weight(NamedTuple):
     n_out: int           # output columns (gate/up pairs count once when paired)
     K: int
     paired: bool
+    shift: Optional[torch.Tensor] = None  # int32 per weight row: the rebased rows' 2**shift, None when all 0
 
 
-def bake_mx8(codes: torch.Tensor, scale: torch.Tensor, bias: int, paired: bool = False) -> MX8Weight:
+def bake_mx8(codes: torch.Tensor, scale: torch.Tensor, bias: int, paired: bool = False,
+             rebase: bool = True) -> MX8Weight:
     """Bake packed MX-int8 weights ``[N, K]`` (codes one int8 per byte, scales
-    as biased exponent bytes, as ``packed.quantize_mx_packed`` returns them)."""
+    as biased exponent bytes, as ``packed.quantize_mx_packed`` returns them).
+    A row whose block exponents leave the GEMV operand's [-24, 5] is rebased
+    to its largest (``rebase``; the row's blocks more than 29 binades under
+    it are flushed), otherwise flagged; the bake reads back whether any row
+    was (one synchronisation, at bake time)."""
     N, K = codes.shape
     if codes.dtype != torch.uint8 or scale.dtype != torch.uint8:
         raise TypeError("bake_mx8: codes and scales must be uint8")
     wc = torch.empty(N * K, dtype=torch.uint8, device=codes.device)
     wh = torch.empty(N * K // MX_BLOCK, dtype=torch.uint8, device=codes.device)
+    shift = torch.empty(N, dtype=torch.int32, device=codes.device) if rebase else None
     flag = ErrorFlag(codes.device)
     st = load().vh_mx8_bake(ptr(codes.contiguous()), ptr(scale.contiguous()), int(bias), N, K, 1 if paired else 0,
-                            ptr(wc), ptr(wh), ptr(flag.t), _stream(codes))
+                            ptr(wc), ptr(wh), ptr(shift), ptr(flag.t), _stream(codes))
     check(st, "vh_mx8_bake")
     flag.check()
-    return MX8Weight(wc, wh, N // 2 if paired else N, K, paired)
+    if shift is not None and not bool(shift.any()):
+        shift = None
+    return MX8Weight(wc, wh, N // 2 if paired else N, K, paired, shift)
 
 
 def quantize_mx8_weight(w: torch.Tensor, paired: bool = False) -> MX8Weight:
@@ -105,10 +114,13 @@ def rmsnorm_mx8(x: torch.Tensor, weight: torch.Tensor, eps: float, flag: ErrorFl
 
 def gemv_mx8(x_fq: torch.Tensor, w: MX8Weight, flag: ErrorFlag, mode: int = _lib.GEMV_STORE,
              residual: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
-             fq_out: Optional[torch.Tensor] = None, tiles_per_block: int = 0):
+             fq_out: Optional[torch.Tensor] = None, tiles_per_block: int = 0,
+             row_exp: Optional[torch.Tensor] = None):
     """``linear_mx`` of fake-quantized activations and baked weights.  STORE /
     RESIDUAL return ``y`` (bf16); SWIGLU returns the fp16 fake quantization
-    of ``silu(gate) * up`` (and fills ``y`` with the bf16 product if given)."""
+    of ``silu(gate) * up`` (and fills ``y`` with the bf16 product if given).
+    ``row_exp`` (int32 [M]): ``x_fq`` holds rows rebased as
+    ``gemm.quantize_mx8_f16`` writes them (row m times 2**-row_exp[m])."""
     M, K = x_fq.shape
     if K != w.K:
         raise ValueError(f"gemv_mx8: K mismatch ({K} vs {w.K})")
@@ -122,7 +134,7 @@ def gemv_mx8(x_fq: torch.Tensor, w: MX8Weight, flag: ErrorFlag, mode: int = _lib
     if tiles_per_block == 0:
         tiles_per_block = 2 if (w.n_out // 16) >= 1024 and (w.n_out // 16) % 2 == 0 else 1
     st = load().vh_gemv_mx8(ptr(x_fq), M, K, ptr(w.codes), ptr(w.hb), w.n_out, mode, tiles_per_block, ptr(residual),
-                            ptr(y), ptr(fq_out), ptr(flag.t), _stream(x_fq))
+                            ptr(y), ptr(fq_out), ptr(row_exp), ptr(w.shift), ptr(flag.t), _stream(x_fq))
     check(st, "vh_gemv_mx8")
     return fq_out if mode == _lib.GEMV_SWIGLU else y
 
@@ -382,6 +394,64 @@ class DecoderLayer:
             ("down_proj", lambda: gemv_mx8(b["act_fq"], self.down, f, _lib.GEMV_RESIDUAL, residual=b["x1"],
                                            y=b["out"])),
         ]
+        return out
+
+    def safe_stages(self, x: torch.Tensor, cache: KiviCache, advance: bool, flag: ErrorFlag):
+        """The step with each linear's input taken from its bf16 form as exact
+        fp16 rows rebased to the row's largest block exponent
+        (``gemm.quantize_mx8_f16``; the GEMV multiplies each row's sums back),
+        in place of the fake-quantized fp16 operand, whose blocks must stay in
+        the fp16 range: any activation magnitude, at the cost of a quantize
+        launch per linear (and allocations, so not for graph capture).  The
+        kernels whose fp16 operands it does not use report into ``flag``."""
+        from . import gemm
+
+        B = x.shape[0]
+        b = {k: v[:B] for k, v in self.buf.items()}
+        if "h1" not in self.buf:
+            H = self.hidden
+            self.buf["h1"] = torch.empty(self.buf["out"].shape[0], H, dtype=torch.bfloat16, device=x.device)
+            self.buf["h2"] = torch.empty_like(self.buf["h1"])
+        h1, h2 = self.buf["h1"][:B], self.buf["h2"][:B]
+        f = self.flag
+
+        def lin(inp, w, mode, **kw):
+            x16, ex = gemm.quantize_mx8_f16(inp)
+            return gemv_mx8(x16, w, flag if mode == _lib.GEMV_SWIGLU else f, mode, row_exp=ex, **kw)
+
+        return [
+            ("rmsnorm_1", lambda: rmsnorm_mx8(x, self.ln1, self.eps, flag, fq=b["fq1"], h_out=h1)),
+            ("qkv_proj", lambda: lin(h1, self.qkv, _lib.GEMV_STORE, y=b["qkv"])),
+            ("attention", lambda: kivi_attention(b["qkv"], cache, self.rope, self.nq, flag, part=self.part,
+                                                 attn=b["attn"], attn_fq=b["attn_fq"], advance=advance)),
+            ("o_proj", lambda: lin(b["attn"], self.o, _lib.GEMV_RESIDUAL, residual=x, y=b["x1"])),
+            ("rmsnorm_2", lambda: rmsnorm_mx8(b["x1"], self.ln2, self.eps, flag, fq=b["fq3"], h_out=h2)),
+            ("gate_up_proj", lambda: lin(h2, self.gate_up, _lib.GEMV_SWIGLU, y=b["act"], fq_out=b["act_fq"])),
+            ("down_proj", lambda: lin(b["act"], self.down, _lib.GEMV_RESIDUAL, residual=b["x1"], y=b["out"])),
+        ]
+
+    def step_checked(self, x: torch.Tensor, cache: KiviCache, advance: bool = True) -> torch.Tensor:
+        """``step``, then a synchronising look at the flag: when an activation
+        block left the fp16 range of the GEMV operand, the cache state is put
+        back and the step runs again through ``safe_stages`` (the cache bytes
+        the first run wrote past the state -- the new token's residual slot, a
+        folded chunk -- are written again); every other error raises, as
+        ``ErrorFlag.check`` does."""
+        state0, host0 = cache.state.clone(), (cache.n_main, cache.n_res)
+        out = self.step(x, cache, advance)
+        v = int(self.flag.t.item())
+        if v & _lib.DECODE_ERR_FP16_RANGE:
+            self.flag.t.fill_(v & ~_lib.DECODE_ERR_FP16_RANGE)
+            cache.state.copy_(state0)
+            cache.n_main, cache.n_res = host0
+            side = ErrorFlag(x.device)
+            self.stages(x, cache)  # sizes the attention workspace
+            for _, fn in self.safe_stages(x, cache, advance, side):
+                fn()
+            sv = int(side.t.item()) & ~_lib.DECODE_ERR_FP16_RANGE
+            if sv:
+                self.flag.t.bitwise_or_(sv)
+        self.flag.check()
         return out
 
     def step(self, x: torch.Tensor, cache: KiviCache, advance: bool = True) -> torch.Tensor:
