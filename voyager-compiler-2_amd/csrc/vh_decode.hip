@@ -617,17 +617,46 @@ struct SoftmaxTotals {
   float M, rcpL;
 };
 
-VH_DEV SoftmaxTotals softmax_totals(const KiviArgs& a, int P, int splits, int h) {
-  const float* ml = a.ml + (int64_t)P * (a.splits_cap + 1) * GQA * 2 + h * 2;
-  const float2 r = *(const float2*)(ml + (int64_t)a.splits_cap * GQA * 2);
-  float M = r.x;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, ml[(int64_t)s * GQA * 2]);
+// The partials of head h: the first ML_PRE splits' and the residual
+// window's, loaded (with no predicate: every slot is allocated, a split past
+// the capacity re-reads the last) before the kernel reads the state.
+constexpr int ML_PRE = 16;
+struct MlPre {
+  float2 v[ML_PRE];
+  float2 r;
+};
+
+VH_DEV const float* ml_head(const KiviArgs& a, int P, int h) {
+  return a.ml + (int64_t)P * (a.splits_cap + 1) * GQA * 2 + h * 2;
+}
+
+VH_DEV MlPre ml_preload(const KiviArgs& a, int P, int h) {
+  const float* ml = ml_head(a, P, h);
+  MlPre m;
+#pragma unroll
+  for (int s = 0; s < ML_PRE; ++s)
+    m.v[s] = *(const float2*)(ml + (int64_t)(s < a.splits_cap ? s : a.splits_cap - 1) * GQA * 2);
+  m.r = *(const float2*)(ml + (int64_t)a.splits_cap * GQA * 2);
+  return m;
+}
+
+VH_DEV SoftmaxTotals softmax_totals(const KiviArgs& a, const MlPre& pre, int P, int splits, int h) {
+  const float* ml = ml_head(a, P, h);
+  auto part = [&](int s) { return s < ML_PRE ? pre.v[s] : *(const float2*)(ml + (int64_t)s * GQA * 2); };
+  float M = pre.r.x;
+#pragma unroll
+  for (int s = 0; s < ML_PRE; ++s)
+    if (s < splits) M = fmaxf(M, pre.v[s].x);
+  for (int s = ML_PRE; s < splits; ++s) M = fmaxf(M, part(s).x);
   float L = 0.0f;
-  for (int s = 0; s < splits; ++s) {
-    const float2 p = *(const float2*)(ml + (int64_t)s * GQA * 2);
+#pragma unroll
+  for (int s = 0; s < ML_PRE; ++s)
+    if (s < splits) L = fmaf(pre.v[s].y, exp_acc(pre.v[s].x - M), L);
+  for (int s = ML_PRE; s < splits; ++s) {
+    const float2 p = part(s);
     L = fmaf(p.y, exp_acc(p.x - M), L);
   }
-  L = fmaf(r.y, exp_acc(r.x - M), L);
+  L = fmaf(pre.r.y, exp_acc(pre.r.x - M), L);
   return {M, 1.0f / L};
 }
 
@@ -791,42 +820,50 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_scores(KiviArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t s_q[GQA][HEAD_DIM];
   __shared__ __attribute__((aligned(16))) uint16_t s_newk[HEAD_DIM];
   __shared__ float s_ml[SPLIT_WAVES][GQA][2];
-  const int n_main = a.state[0], n_res = a.state[1];
-  const int G = n_main / KV_GROUP;
   const int split = blockIdx.x, P = blockIdx.y;
   const bool residual = split == a.splits_cap;
   const int g_begin = split * GROUPS_PER_SPLIT;
-  if (!state_ok(a, n_main, n_res) || (!residual && g_begin >= G)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, kq = lane >> 4, hq = n & 3;
   const uint32_t kq_bytes = (uint32_t)kq * 0x40404040u;  // 64 kq in every byte: the table block
   const int b = P / a.nkv, kvh = P % a.nkv;
-  const int pos = n_main + n_res;
   const uint16_t* row = a.qkv + (int64_t)b * a.qkv_ld;
-  const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
-  const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
-
-  // the query element this thread rotates (head tid / 128, channel tid % 128) goes out first
-  const int qh = tid / HEAD_DIM, qc = tid % HEAD_DIM;
+  // The state is read first and used only after every load whose address
+  // does not depend on it is out: the query's elements and this wave's key
+  // blocks (groups clamped into the capacity: a group past the cache's is
+  // read from allocated memory and skipped), or the residual window's rows.
+  const int2 st = *(const int2*)a.state;
+  const int qh = tid / HEAD_DIM, qc = tid % HEAD_DIM;  // the query element this thread rotates
   const uint16_t* qrow = row + (kvh * GQA + qh) * HEAD_DIM;
   uint32_t qv = qrow[qc], qp = qrow[qc < HEAD_DIM / 2 ? qc + HEAD_DIM / 2 : qc - HEAD_DIM / 2];
-  uint32_t qcs = cs_[qc], qsn = sn_[qc];
-  asm volatile("" ::: "memory");
-  // then this wave's key blocks (an absent group re-reads a live one and is skipped)
   uint4 kc[GROUPS_PER_WAVE];
   uint2 kp[GROUPS_PER_WAVE];
-  int ng = 0;
+  uint4 k4[4];  // the residual window: slot 16 wave + n, channels 32 kq + 8 cs + [0, 8)
   if (!residual) {
     const uint8_t* seq = a.main + (int64_t)P * a.group_cap * GROUP_BYTES;
 #pragma unroll
     for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
       const int g = g_begin + i * SPLIT_WAVES + wave;
-      ng += g < G ? 1 : 0;
-      const uint8_t* blk = seq + (int64_t)(g < G ? g : G - 1) * GROUP_BYTES;
+      const uint8_t* blk = seq + (int64_t)(g < a.group_cap ? g : a.group_cap - 1) * GROUP_BYTES;
       kp[i] = *(const uint2*)(blk + 2048 + lane * 8);
       kc[i] = *(const uint4*)(blk + lane * 16);
     }
+  } else {
+    const uint4* src = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + 16 * wave + n) * HEAD_DIM + 32 * kq);
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs) k4[cs] = src[cs];
   }
+  asm volatile("" ::: "memory");
+  const int n_main = st.x, n_res = st.y;
+  const int G = n_main / KV_GROUP;
+  if (!state_ok(a, n_main, n_res) || (!residual && g_begin >= G)) return;
+  int ng = 0;
+#pragma unroll
+  for (int i = 0; i < GROUPS_PER_WAVE; ++i) ng += g_begin + i * SPLIT_WAVES + wave < G ? 1 : 0;
+  const int pos = n_main + n_res;
+  const uint16_t* cs_ = a.rope + (int64_t)pos * HEAD_DIM;
+  const uint16_t* sn_ = a.rope + (a.max_pos + pos) * HEAD_DIM;
+  uint32_t qcs = cs_[qc], qsn = sn_[qc];
   // waits for the query alone; the blocks stay in flight across the barrier
   asm volatile("" : "+v"(qv), "+v"(qp), "+v"(qcs), "+v"(qsn)::"memory");
   {
@@ -850,12 +887,8 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_scores(KiviArgs a) {
   uint16_t* sc_head = a.sc + ((int64_t)P * GQA + hq) * a.t_stride;
 
   if (residual) {
-    // wave w: residual slots 16 w + r; slot n_res is this step's key from LDS
+    // wave w: residual slots 16 w + r (loaded above); slot n_res is this step's key, from LDS
     const int slot = 16 * wave + n;
-    const uint4* src = (const uint4*)(a.kr + ((int64_t)P * RES_CAP + slot) * HEAD_DIM + 32 * kq);
-    uint4 k4[4];
-#pragma unroll
-    for (int cs = 0; cs < 4; ++cs) k4[cs] = src[cs];
     if (slot == n_res) {
 #pragma unroll
       for (int cs = 0; cs < 4; ++cs) k4[cs] = *(const uint4*)&s_newk[32 * kq + 8 * cs];
@@ -941,33 +974,39 @@ __global__ void __launch_bounds__(SPLIT_WAVES * 64) k_kivi_pv(KiviArgs a) {
   __shared__ __attribute__((aligned(256))) uint8_t s_tab[SPLIT_WAVES][KEY_TAB_BYTES];
   __shared__ __attribute__((aligned(16))) uint16_t s_p[SPLIT_WAVES][GQA][KV_GROUP];
   static_assert(sizeof(float) * SPLIT_WAVES * GQA * HEAD_DIM <= sizeof(s_tab), "outputs reuse the tables");
-  const int n_main = a.state[0], n_res = a.state[1];
-  const int G = n_main / KV_GROUP;
   const int split = blockIdx.x, P = blockIdx.y;
   const int g_begin = split * GROUPS_PER_SPLIT;
-  if (!state_ok(a, n_main, n_res) || g_begin >= G) return;
-  const int splits = (G + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, kq = lane >> 4;
   const uint32_t kq_bytes = (uint32_t)kq * 0x40404040u;
   const int hp = lane >> 4, tp = lane & 15;  // this lane's probabilities: head hp, tokens 2 tp, 2 tp + 1
+  // the state is used only after the value blocks, the scores and the
+  // partials are out (groups clamped into the capacity, as the score pass)
+  const int2 st = *(const int2*)a.state;
   uint4 vc[GROUPS_PER_WAVE];
   uint2 vp[GROUPS_PER_WAVE];
   uint32_t sp[GROUPS_PER_WAVE];
-  int ng = 0;
   const uint8_t* seq = a.main + (int64_t)P * a.group_cap * GROUP_BYTES;
   const uint16_t* sc_head = a.sc + ((int64_t)P * GQA + hp) * a.t_stride;
 #pragma unroll
   for (int i = 0; i < GROUPS_PER_WAVE; ++i) {
     const int g = g_begin + i * SPLIT_WAVES + wave;
-    ng += g < G ? 1 : 0;
-    const int gl = g < G ? g : G - 1;
+    const int gl = g < a.group_cap ? g : a.group_cap - 1;
     const uint8_t* blk = seq + (int64_t)gl * GROUP_BYTES;
     vp[i] = *(const uint2*)(blk + 2560 + lane * 8);
     vc[i] = *(const uint4*)(blk + 1024 + lane * 16);
     sp[i] = *(const uint32_t*)(sc_head + (int64_t)gl * KV_GROUP + 2 * tp);
   }
-  const SoftmaxTotals tot = softmax_totals(a, P, splits, hp);
+  const MlPre pre = ml_preload(a, P, hp);
+  asm volatile("" ::: "memory");
+  const int n_main = st.x, n_res = st.y;
+  const int G = n_main / KV_GROUP;
+  if (!state_ok(a, n_main, n_res) || g_begin >= G) return;
+  const int splits = (G + GROUPS_PER_SPLIT - 1) / GROUPS_PER_SPLIT;
+  int ng = 0;
+#pragma unroll
+  for (int i = 0; i < GROUPS_PER_WAVE; ++i) ng += g_begin + i * SPLIT_WAVES + wave < G ? 1 : 0;
+  const SoftmaxTotals tot = softmax_totals(a, pre, P, splits, hp);
   f32x4 acc[8];
 #pragma unroll
   for (int r8 = 0; r8 < 8; ++r8) acc[r8] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1199,6 +1238,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
 #pragma unroll
   for (int u = 0; u < RES_CAP / 16; ++u) vw[u] = vp[(int64_t)(ts + 16 * u) * (HEAD_DIM / 8)];
   const uint16_t sraw = a.sc[((int64_t)P * GQA + h) * a.t_stride + a.group_cap * KV_GROUP + (tid & (RES_CAP - 1))];
+  const MlPre pre = ml_preload(a, P, h);
   const float* base = a.po + ((int64_t)P * a.splits_cap * GQA + h) * HEAD_DIM + c;
   float po[COMBINE_PRELOAD];
 #pragma unroll
@@ -1219,7 +1259,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) k_kivi_combine(KiviArgs a, ui
     if (bh == 0 && tid == 0) atomicOr(flag, VH_DECODE_ERR_KV_STATE);
     return;
   }
-  const SoftmaxTotals tot = softmax_totals(a, P, splits, h);
+  const SoftmaxTotals tot = softmax_totals(a, pre, P, splits, h);
   if (tid < RES_CAP) s_p[tid] = tid <= n_res ? rbf(exp_acc(bf2f(sraw) - tot.M) * tot.rcpL) : 0.0f;
   // slots past the window hold stale bytes (a zero weight times a stale
   // infinity would be NaN): cleared
