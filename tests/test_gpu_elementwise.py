@@ -163,12 +163,12 @@ def test_quantize_packed_e4m3_large_ragged():
     assert torch.equal(got[257 * 65536:].cpu(), exp[:40])
 
 
-@pytest.mark.parametrize("scale", [1.0, 0.0173])
+@pytest.mark.parametrize("scale", [1.0, 0.0173, 0.25])
 def test_posit8_elementwise_at_config4_size(scale):
     """Config 4's elementwise leg at its size: every bf16 pattern 1030 times
     plus a 48-element tail (67,502,128 elements, more than the config's
     64M) through the posit table quantize, packed and reference form, and the
-    packed dequantize, with and without a scale.  At this size the quantize's
+    packed dequantize, with a unit, a general and a power-of-two scale.  At this size the quantize's
     grid-stride loop (256 workgroups x 1024 threads x 4 vectors a pass) runs
     nine passes, alternating its two load buffers, and the dequantize's
     gather loop (4096 workgroups, 65,536 units of 1024 codes a pass) a second,
@@ -214,14 +214,17 @@ def test_posit8_elementwise_at_config4_size(scale):
 
 
 @pytest.mark.parametrize("dtype", ["posit8_1", "posit8_0", "posit8_2", "posit16_1"])
-@pytest.mark.parametrize("scale", [1.0, 0.0173, 3.5, 2.0**-130, 1.5e38])
+@pytest.mark.parametrize("scale", [1.0, 0.0173, 3.5, 2.0**-130, 1.5e38, 0.25, 2.0**-20, 2.0**100, 2.0**-120])
 def test_quantize_posit_every_bf16_pattern(dtype, scale):
     """The posit table path (per-tensor scale, whole 16-byte rows): all
     65,536 bf16 patterns, reference form and (8-bit posits) packed codes read
     back through the code table, against the oracle's closed-form posit
     rounding.  The patterns cover zero, the flush region below the threshold,
     the saturating region above maxpos and the non-finite inputs; the
-    subnormal and huge scales force the exact-division fallback."""
+    subnormal and huge scales force the exact-division fallback; a unit scale
+    takes q = x, and the other powers of two skip the rounding-midpoint test
+    (their quotients, subnormal and overflowing ones included, are the
+    products by the exact reciprocal)."""
     from voyager_amd import packed
 
     x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
