@@ -494,6 +494,23 @@ def bench_config3(args, cpu_budget_s=0.0):
             tot_t += ms
         del ws
     gbs = tot_b / (tot_t * 1e-3) / 1e9
+    # prefill: the same format at M = 2048 (the lowered site's quantize_mx of
+    # the activations, then vh_gemm_nf4 on the GEMV's baked weight bytes)
+    from voyager_amd import packed
+    prefill = {}
+    for K, N in ((4096, 4096), (4096, 14336)):
+        w = (torch.randn(N, K, generator=torch.Generator().manual_seed(1)) * 0.02).bfloat16().to(dev)
+        wb = gemm.bake_nf4_weight(w, index, stab, entries)
+        x = torch.randn(2048, K, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
+        px = packed.quantize_mx_packed(x, index, [-1], 64, 31.0, False, stab)
+        gq = capture(lambda: [packed.quantize_mx_packed(x, index, [-1], 64, 31.0, False, stab) for _ in range(10)])
+        q_ms = time_graph(gq, 5) / 10
+        gg = capture(lambda: [gemm.gemm_nf4_packed(px, wb) for _ in range(10)])
+        g_ms = time_graph(gg, 5) / 10
+        tf = 2 * 2048 * N * K / (g_ms * 1e-3) / 1e12
+        prefill[f"M2048_K{K}_N{N}"] = {"gemm_us": round(g_ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                                       "frac_of_mfma": round(tf / 2500.0, 4), "quantize_us": round(q_ms * 1e3, 2)}
+        del w, wb, x, px, gq, gg
     cpu = cpu_config3(cpu_budget_s) if cpu_budget_s > 0 else None
     return {"metric": "MXNF4 decode linear GB/s (config 3)", "value": round(gbs, 1),
             "unit": "GB/s", "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
@@ -502,6 +519,9 @@ def bench_config3(args, cpu_budget_s=0.0):
                          "note": "the eight decode linears (weights rotated over > 512 MB): algorithmic bytes "
                                  "(4-bit codes, scale bytes, bf16 activations and outputs) / their durations"},
             "per_shape": res, "cpu_baseline": cpu,
+            "prefill_gemm": {"shapes": prefill, "mfma": "v_mfma_f32_32x32x16_bf16 (2.5 PF dense)",
+                             "note": "vh_gemm_nf4: both operands decoded while staging to bf16(level * scale), "
+                                     "bf16 MFMA, float32 accumulation; quantize_us = the activation's quantize_mx"},
             "config": {"workload": "cfg3: lut4_to_int6 bs=64 fp8_e5m3 scales, M in {1,16}"}}
 
 
@@ -797,7 +817,8 @@ def summary(res):
     if "gemm" in res and "frac" in res["gemm"]:
         out["gemm"] = {k: res["gemm"].get(k) for k in ("us", "TFLOP/s", "frac")}
     if "prefill_gemm" in res:
-        out["prefill_gemm"] = {k: res["prefill_gemm"].get(k) for k in ("us", "TFLOP/s", "frac_of_mfma")}
+        pg = res["prefill_gemm"]
+        out["prefill_gemm"] = pg["shapes"] if "shapes" in pg else {k: pg.get(k) for k in ("us", "TFLOP/s", "frac_of_mfma")}
     out["workload"] = (res.get("config") or {}).get("workload")
     return out
 

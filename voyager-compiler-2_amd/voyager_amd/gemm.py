@@ -564,20 +564,30 @@ def linear_nf4_prefill(x: torch.Tensor, weight: NF4Weight, index_table: torch.Te
     if K != weight.K:
         raise RuntimeError("linear_nf4_prefill: contraction mismatch")
     px = _packed.quantize_mx_packed(x.contiguous(), index_table, [-1], 64, 31.0, False, scale_qmap)
-    y = torch.empty(M, weight.N, dtype=out_dtype, device=x.device)
+    return gemm_nf4_packed(px, weight, out_dtype, bias, alpha, tile, splits)
+
+
+def gemm_nf4_packed(px, weight: NF4Weight, out_dtype=torch.bfloat16, bias=None, alpha=None, tile: int = 0,
+                    splits: int = 0) -> torch.Tensor:
+    """``vh_gemm_nf4`` on an activation already packed by ``quantize_mx_packed``
+    (index bytes [M, K] and scale codes [M, K / 64])."""
+    M, K = px.codes.shape
+    if K != weight.K:
+        raise RuntimeError("gemm_nf4_packed: contraction mismatch")
+    y = torch.empty(M, weight.N, dtype=out_dtype, device=px.codes.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
     bias = _bias_operand(bias)
     epi = _epilogue(EPI_PLAIN, out_dtype, alpha, bias)
     lv = ctypes.create_string_buffer(weight.levels, 16)
     tile, splits = nf4_prefill_plan(M, weight.N, K, tile, splits)
-    part = torch.empty(splits * M * weight.N, dtype=torch.float32, device=x.device) if splits > 1 else None
+    part = torch.empty(splits * M * weight.N, dtype=torch.float32, device=y.device) if splits > 1 else None
     st = load().vh_gemm_nf4(ctypes.c_void_p(px.codes.data_ptr()), ctypes.c_void_p(px.scale.data_ptr()),
                             ctypes.byref(px.scale_fmt.fmt), M, ctypes.c_void_p(weight.packed.data_ptr()),
                             ctypes.c_void_p(weight.scale.data_ptr()), ctypes.byref(weight.scale_fmt.fmt), lv,
                             weight.N, weight.K, ctypes.c_void_p(ctypes.addressof(epi)),
                             ctypes.c_void_p(y.data_ptr()), weight.N, tile, splits, ptr(part),
-                            0 if part is None else part.numel() * 4, ctypes.c_void_p(stream_of(x)))
+                            0 if part is None else part.numel() * 4, ctypes.c_void_p(stream_of(y)))
     _lib.check(st, "vh_gemm_nf4")
     return y
 
