@@ -34,6 +34,7 @@ bandwidth and the config-1 linear with its outlier stream).
 """
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -90,6 +91,15 @@ def capture(fn):
         fn()
     torch.cuda.synchronize()
     return g
+
+
+def stream_2to1(x, out):
+    """vh_stream_2to1 of a bf16 tensor's bytes into ``out`` (half of them)."""
+    from voyager_amd import _lib
+
+    st = _lib.load().vh_stream_2to1(ctypes.c_void_p(x.data_ptr()), x.numel() // 8, ctypes.c_void_p(out.data_ptr()),
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(st, "vh_stream_2to1")
 
 
 def time_graph(g, reps, warm_s=0.5):
@@ -162,7 +172,7 @@ def gpu_bench(args):
     # Quantize inputs rotate over more than the 256 MB Infinity Cache so HBM,
     # not the cache, serves them.
     R = 10
-    g_ms, q_ms = [], []
+    g_ms, q_ms, c_ms = [], [], []
     for L in layers:
         gg = capture(lambda L=L: [gemm.linear_fp8(L["xq"], L["wq"], L["s"], out=L["y"]) for _ in range(R)])
         g_ms.append(time_graph(gg, 5) / R)
@@ -171,7 +181,12 @@ def gpu_bench(args):
         outs = {}
         gq = capture(lambda xs=xs: [outs.__setitem__(i, quantize(xb, L["sx"])) for i, xb in enumerate(xs)])
         q_ms.append(time_graph(gq, 5) / nbuf)
-        del xs, gq, gg
+        # the same inputs through the quantize's access pattern with no
+        # arithmetic (vh_stream_2to1): the ceiling that pattern reaches here
+        oc = [torch.empty(M * L["K"], dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+        gs = capture(lambda xs=xs, oc=oc: [stream_2to1(xb, ob) for xb, ob in zip(xs, oc)])
+        c_ms.append(time_graph(gs, 5) / nbuf)
+        del xs, gq, gg, oc, gs
     torch.cuda.synchronize()
 
     # The same GEMMs with their operands rotated over more than twice the
@@ -231,6 +246,7 @@ def gpu_bench(args):
     cold_tflops = total_flops / (sum(gc_ms) * 1e-3) / 1e12
     step_tflops = total_flops / (sum(in_g) * 1e-3) / 1e12
     q_gbs = sum(qbytes) / (sum(q_ms) * 1e-3) / 1e9
+    c_gbs = sum(qbytes) / (sum(c_ms) * 1e-3) / 1e9
     step_q_gbs = sum(qbytes) / (sum(in_q) * 1e-3) / 1e9
     per_shape = []
     for i, L in enumerate(layers):
@@ -240,7 +256,7 @@ def gpu_bench(args):
             "gemm_rotated_us": round(gc_ms[i] * 1e3, 2),
             "gemm_rotated_tflops": round(flops[i] / (gc_ms[i] * 1e-3) / 1e12, 1),
             "gemm_in_step_us": round(in_g[i] * 1e3, 2), "quantize_in_step_us": round(in_q[i] * 1e3, 2),
-            "quantize_us": round(q_ms[i] * 1e3, 2),
+            "quantize_us": round(q_ms[i] * 1e3, 2), "stream_2to1_us": round(c_ms[i] * 1e3, 2),
             "quantize_gbs": round(qbytes[i] / (q_ms[i] * 1e-3) / 1e9, 1),
         })
     traffic = None
@@ -260,7 +276,11 @@ def gpu_bench(args):
         "quantize": {"achieved": round(step_q_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(step_q_gbs / HBM_PEAK_GBS, 4), "durations": "in the step, as the GEMMs",
                      "rotated": {"achieved": round(q_gbs, 1), "frac": round(q_gbs / HBM_PEAK_GBS, 4),
-                                 "operands": "quantizes alone, inputs rotated over > 2 x 256 MB"}},
+                                 "operands": "quantizes alone, inputs rotated over > 2 x 256 MB"},
+                     "ceiling": {"achieved": round(c_gbs, 1), "frac": round(c_gbs / HBM_PEAK_GBS, 4),
+                                 "quantize_frac_of_ceiling": round(q_gbs / c_gbs, 4),
+                                 "kernel": "vh_stream_2to1: the quantize's loads and stores (same workgroup "
+                                           "shape, runs and cache hints) with no arithmetic, same rotated inputs"}},
         "per_shape": per_shape,
     }
     return res, cpu_data

@@ -101,6 +101,14 @@ int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t nd
                 const vh_param* scale, const vh_param* zero_point, int32_t compute_dtype,
                 const vh_format* fmt, void* out, int32_t out_dtype, vh_stream_t stream);
 
+/* Measurement aid, no counterpart in the reference: the memory access of
+ * vh_quantize's per-tensor bf16 -> one-byte path without its arithmetic --
+ * reads nvec 16-byte groups of x, writes 8 bytes per group to out (each
+ * group's high bytes) with the same workgroup shape, run length and cache
+ * hints -- so a quantize's bandwidth can be read against what its access
+ * pattern reaches on the part (bench.py reports both). */
+int vh_stream_2to1(const void* x, int64_t nvec, void* out, vh_stream_t stream);
+
 /* quantize with stochastic rounding (a `seed`): out = x / scale (+ zp) as
  * vh_quantize computes it, rounded to one of the two of `levels` around it
  * (levels ascending, device memory, bf16/fp16/fp32; a table's distinct

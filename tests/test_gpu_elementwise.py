@@ -289,3 +289,21 @@ def test_zero_dim_scale_of_another_dtype(op, sdtype):
         got = torch.ops.quantized_ops.dequantize(x.cuda(), s.cuda(), zp.cuda())
     assert got.dtype == exp.dtype == torch.bfloat16
     assert_same_bits(got, exp, f"{op} {sdtype}")
+
+
+@pytest.mark.parametrize("n", [8 * 1000 + 8 * 7, 8 * ((1 << 21) + 333)])
+def test_stream_2to1_writes_each_high_byte(n):
+    """The bench's streaming ceiling kernel (vh_stream_2to1) reads every
+    16-byte group and writes its elements' high bytes: a ragged size on the
+    4-group path and one past 2^21 groups on the 8-group path."""
+    import ctypes
+
+    from voyager_amd import _lib
+
+    x = torch.randint(-32768, 32768, (n,), dtype=torch.int32).to(torch.int16).cuda()
+    out = torch.full((n,), 7, dtype=torch.uint8, device="cuda")
+    st = _lib.load().vh_stream_2to1(ctypes.c_void_p(x.data_ptr()), n // 8, ctypes.c_void_p(out.data_ptr()),
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(st, "vh_stream_2to1")
+    exp = ((x.int() >> 8) & 0xFF).to(torch.uint8)
+    assert torch.equal(out, exp)

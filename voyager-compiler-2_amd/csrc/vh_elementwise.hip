@@ -347,6 +347,30 @@ k_quantize_e4m3_pt(const uint16_t* __restrict__ x, int64_t nvec, const void* sp,
   }
 }
 
+// Measurement aid: the per-tensor quantize's memory access with no
+// arithmetic -- workgroup b reads the U * 256 consecutive 16-byte groups
+// from b * U * 256 (non-temporal), every load before the first store, and
+// writes 8 bytes per group (half of each one's bytes) -- so a quantize's
+// bandwidth can be read against what its own access pattern reaches.
+template <int U>
+__global__ void __launch_bounds__(256) k_stream_2to1(const uint16_t* __restrict__ x, int64_t nvec,
+                                                     uint8_t* __restrict__ out) {
+  const int64_t v0 = (int64_t)blockIdx.x * (U * 256) + threadIdx.x;
+  uint4 raw[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t v = v0 + u * 256;
+    raw[u] = ld_stream16(x + (v < nvec ? v : nvec - 1) * 8);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t v = v0 + u * 256;
+    if (v < nvec)
+      st_stream8(out + v * 8, make_uint2(__builtin_amdgcn_perm(raw[u].y, raw[u].x, 0x07050301u),
+                                         __builtin_amdgcn_perm(raw[u].w, raw[u].z, 0x07050301u)));
+  }
+}
+
 // ------------------------------------------------------------ posit tables
 // A posit's code (or reference-form value) as a function of the bfloat16
 // pattern q = bf16(x / s) only changes for magnitudes between the flush
@@ -717,6 +741,21 @@ static bool packable(const vh_format* f) {
     case VH_FMT_STEPS: return true;
     default: return false;
   }
+}
+
+extern "C" int vh_stream_2to1(const void* x, int64_t nvec, void* out, vh_stream_t stream) {
+  VH_REQUIRE(x && out && nvec > 0, "vh_stream_2to1: null argument or empty");
+  VH_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 8) == 0, "vh_stream_2to1: misaligned operand");
+  VH_REQUIRE(nvec / 1024 < (1ll << 31), "vh_stream_2to1: too large");
+  hipStream_t st = vh::as_stream(stream);
+  // the E4M3 quantize's choice: 4 groups per thread up to 2^21 groups, 8 beyond
+  if (nvec <= (1ll << 21))
+    hipLaunchKernelGGL(k_stream_2to1<4>, dim3((unsigned)((nvec + 1023) / 1024)), dim3(256), 0, st,
+                       (const uint16_t*)x, nvec, (uint8_t*)out);
+  else
+    hipLaunchKernelGGL(k_stream_2to1<8>, dim3((unsigned)((nvec + 2047) / 2048)), dim3(256), 0, st,
+                       (const uint16_t*)x, nvec, (uint8_t*)out);
+  return vh::check_launch("vh_stream_2to1");
 }
 
 extern "C" int vh_quantize(const void* x, int32_t x_dtype, const int64_t* shape, int32_t ndim,

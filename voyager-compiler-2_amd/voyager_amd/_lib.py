@@ -104,6 +104,7 @@ _SIGNATURES = {
         _I32,
     ),
     "vh_quantize_sr": ([_P, _I32, _P, _I32, _P, _P, _I32, _P, _I32, _I32, _P, _P, _I32, _P], _I32),
+    "vh_stream_2to1": ([_P, _I64, _P, _P], _I32),
     "vh_quantize_codebook": (
         [_P, _I32, ctypes.POINTER(_I64), _I32, ctypes.POINTER(Param), ctypes.POINTER(Param), _I32,
          ctypes.POINTER(Codebook), _P, _P],
