@@ -383,7 +383,8 @@ def mx8_f16_plan(M: int, N: int, K: int) -> Tuple[int, int]:
     4096, one split storing through the GEMM's own epilogue: M = 2048 on
     256x128 tiles 56.0 us (1226 TFLOP/s; 128x128 65.0; 256x128 in two
     splits plus the reduction 92.5); M = 256 on 64x128 tiles 18.9 us (in two
-    splits 19.0, 128x64 19.0, 128x128 25.0).  Below 1024 rows: 64x128, K
+    splits plus the reduction 18.1, in four 26.2; 128x64 18.9; 128x128 25.1,
+    in four splits 21.8; 256x128 in eight 30.0).  Below 1024 rows: 64x128, K
     split until the grid reaches 128 workgroups (each split at least 512
     elements); from 1024: 256x128."""
     if M >= 1024:
