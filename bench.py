@@ -13,10 +13,14 @@ N(0,1) activations, N(0,0.02) weights) and resident in HBM.
 Prints ONE JSON line.  `value` = GEMM TFLOP/s over the whole step (the four
 GEMMs' 2*M*N*K, divided by the step time, which includes the quantize
 kernels).  `roofline` is for the dominant kernel (the fp8 GEMM), timed with
-HIP events on the launch stream, with its operands replayed (Infinity-Cache
-warm) and, under `rotated`, rotated over more than 512 MB as the step meets
-them; `cpu_baseline` times the CPU oracle (the reference's op sequence in
-eager PyTorch) on a bounded sample.  `configs` carries configs 1, 3, 4 and 5
+HIP events on the launch stream around each GEMM of 20 more steps right after
+the timed region (in the step's own thermal and cache state); beside it,
+`rotated` (the GEMMs alone, operands rotated over more than 512 MB) and
+`warm` (the same operands replayed, Infinity-Cache resident).  `quantize`
+is reported the same ways plus `ceiling`, the quantize's access pattern
+without its arithmetic.  `cpu_baseline` times the CPU oracle (the
+reference's op sequence in eager PyTorch) on a bounded sample.  `configs`
+carries configs 1, 3, 4 and 5
 as `--config N` measures them (value, roofline, CPU baseline on a shorter
 sample); `--headline-only` leaves them out.
 
