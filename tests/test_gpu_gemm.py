@@ -493,11 +493,13 @@ def _mx8_f16_decoded(x16, ex):
     return x16.cpu().double() * torch.pow(2.0, ex.cpu().double()).unsqueeze(1)
 
 
-@pytest.mark.parametrize("M,K", [(256, 4096), (7, 1024), (300, 640)])
+@pytest.mark.parametrize("M,K", [(256, 4096), (7, 1024), (300, 640), (5, 6144), (3, 14336)])
 def test_quantize_mx8_f16_exact(M, K):
     """The activation quantize of the small-M MX-int8 path: each row's fp16
     values times 2**E_row are exactly the reference's decoded quantize_mx
-    (codes times block scales), NaN and infinities included."""
+    (codes times block scales), NaN and infinities included.  Rows of up to
+    256 blocks, up to 512 (two per thread kept in registers) and longer (the
+    two-pass kernel)."""
     from voyager_amd import gemm
 
     g = torch.Generator().manual_seed(M + K)

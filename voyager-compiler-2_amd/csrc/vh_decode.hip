@@ -240,6 +240,63 @@ __global__ void __launch_bounds__(256) k_quantize_mx8_f16(const uint16_t* __rest
   if (threadIdx.x == 0) ex[row] = E;
 }
 
+// The same for rows of at most 256 NBT blocks: each thread loads its NBT
+// blocks once and keeps them in registers across the row maximum (no second
+// read of the row); identical arithmetic, so identical output.
+template <int NBT>
+__global__ void __launch_bounds__(256) k_quantize_mx8_f16_r(const uint16_t* __restrict__ x, int64_t K,
+                                                            _Float16* __restrict__ out, int32_t* __restrict__ ex) {
+  __shared__ int s_red[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * K;
+  const int nb = (int)(K / 16);
+  uint4 raw[NBT][2];
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) {
+    const int b = threadIdx.x + 256 * j;
+    if (b < nb) {
+      const uint4* p = (const uint4*)(xr + (int64_t)b * 16);
+      raw[j][0] = p[0];
+      raw[j][1] = p[1];
+    } else {
+      raw[j][0] = raw[j][1] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  Mx8Scale sc[NBT];
+  int emax = INT_MIN;
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) {
+    const uint32_t wv[8] = {raw[j][0].x, raw[j][0].y, raw[j][0].z, raw[j][0].w,
+                            raw[j][1].x, raw[j][1].y, raw[j][1].z, raw[j][1].w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = nmax(amax, nmax(fabsf(bf2f(wv[i] & 0xffffu)), fabsf(bf2f(wv[i] >> 16))));
+    sc[j] = mx8_scale(amax);
+    if (threadIdx.x + 256 * j < nb && sc[j].pow2) emax = max(emax, sc[j].e);
+  }
+  int E = block_max_int(emax, s_red);
+  if (E == INT_MIN) E = 0;
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) {
+    const int b = threadIdx.x + 256 * j;
+    if (b >= nb) continue;
+    const uint32_t wv[8] = {raw[j][0].x, raw[j][0].y, raw[j][0].z, raw[j][0].w,
+                            raw[j][1].x, raw[j][1].y, raw[j][1].z, raw[j][1].w};
+    f16x8 o[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float xv = bf2f((i & 1) ? wv[i >> 1] >> 16 : wv[i >> 1] & 0xffffu);
+      float q = rbf(sc[j].pow2 ? ldexpf(xv, -sc[j].e) : xv / sc[j].s);
+      if (!isnan_f(q)) q = fminf(fmaxf(rintf(q), -128.0f), 127.0f);
+      o[i >> 3][i & 7] = rebased_f16(q, sc[j].e, sc[j].pow2, sc[j].s, E);
+    }
+    f16x8* dst = (f16x8*)(out + row * K + (int64_t)b * 16);
+    dst[0] = o[0];
+    dst[1] = o[1];
+  }
+  if (threadIdx.x == 0) ex[row] = E;
+}
+
 // Packed MX-int8 weights (int8 codes [N, K], scale bytes 2**(byte - bias)
 // [N, K / 16], 255 = inf) as exact fp16 rows with their E.  One workgroup
 // per row.
@@ -1508,8 +1565,14 @@ extern "C" int vh_quantize_mx8_f16(const uint16_t* x, int64_t M, int64_t K, uint
   VH_REQUIRE(x && out && ex, "vh_quantize_mx8_f16: null argument");
   VH_REQUIRE(M > 0 && K > 0 && K % 16 == 0, "vh_quantize_mx8_f16: needs K a multiple of 16");
   VH_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0, "vh_quantize_mx8_f16: misaligned tensor");
-  hipLaunchKernelGGL(k_quantize_mx8_f16, dim3((unsigned)M), dim3(256), 0, vh::as_stream(stream), x, K,
-                     (_Float16*)out, ex);
+  const int64_t nb = K / 16;
+  hipStream_t s = vh::as_stream(stream);
+  if (nb <= 256)
+    hipLaunchKernelGGL(k_quantize_mx8_f16_r<1>, dim3((unsigned)M), dim3(256), 0, s, x, K, (_Float16*)out, ex);
+  else if (nb <= 512)
+    hipLaunchKernelGGL(k_quantize_mx8_f16_r<2>, dim3((unsigned)M), dim3(256), 0, s, x, K, (_Float16*)out, ex);
+  else
+    hipLaunchKernelGGL(k_quantize_mx8_f16, dim3((unsigned)M), dim3(256), 0, s, x, K, (_Float16*)out, ex);
   return vh::check_launch("vh_quantize_mx8_f16");
 }
 
