@@ -249,6 +249,37 @@ def test_linear_fp8_per_tensor(M, K, N):
     assert max_rel_err(got2, exp) < TOL
 
 
+def test_packed_gemms_take_strided_views():
+    """The packed-operand linears address rows as base + row * ld: column-
+    strided views are copied first (same result as the contiguous operands),
+    row-strided ones are read in place, and a misshapen ``out`` is refused."""
+    from voyager_amd import gemm, packed
+
+    d = "cuda"
+    x, w = _rand((192, 512), 22).to(d), _rand((256, 512), 23, 0.02).to(d)
+    tab = T.quantization_map("fp8_e4m3").to(d)
+    sx, sw = O.per_tensor_scale(x.cpu(), 448.0).to(d), O.per_tensor_scale(w.cpu(), 448.0).to(d)
+    s = sx * sw
+    cx, cw = packed.quantize_packed(x, sx, tab), packed.quantize_packed(w, sw, tab)
+    ref = gemm.linear_fp8(cx, cw, s)
+    cxt = cx.t().contiguous().t()          # column-strided view of the same codes
+    wide = torch.zeros(256, 640, dtype=torch.uint8, device=d)
+    wide[:, :512] = cw
+    assert torch.equal(gemm.linear_fp8(cxt, wide[:, :512], s), ref)  # rows 640 bytes apart
+    with pytest.raises(RuntimeError, match="out must be"):
+        gemm.linear_fp8(cx, cw, s, out=torch.empty(192, 256, dtype=torch.float32, device=d))
+    with pytest.raises(RuntimeError, match="one-byte"):
+        gemm.linear_fp8(x, cw, s)
+    # MX-int8 codes and scale bytes likewise
+    t8 = T.quantization_map("int8").to(d)
+    px = packed.quantize_mx_packed(x, t8, [-1], 16, 127.0, True)
+    pw = packed.quantize_mx_packed(w, t8, [-1], 16, 127.0, True)
+    r8 = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias)
+    got8 = gemm.linear_mxint8(px.codes.t().contiguous().t(), px.scale.t().contiguous().t(), pw.codes, pw.scale, 16,
+                              px.bias, pw.bias)
+    assert torch.equal(got8, r8)
+
+
 def test_linear_posit8():
     """Config 4's GEMM at a reduced M: posit8-cast operands, bf16 GEMM."""
     x, w = _rand((256, 4096), 30), _rand((512, 4096), 31, 0.02)

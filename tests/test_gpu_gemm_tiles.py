@@ -263,3 +263,32 @@ def test_plan_follows_output_alignment():
         got = torch.ops.quantized_ops.linear(a, b)
     assert log[0][0] == gemm.FAMILY_STAGED
     assert max_rel_err(got, O.linear(a.cpu(), b.cpu())) < TOL
+
+
+@pytest.mark.parametrize("ld", [1032, 1040])
+def test_fp8_rows_in_wider_buffers(ld):
+    """E4M3 operands of K = 1024 inside rows of ``ld`` bytes whose padding
+    holds NaN codes: rows 16-byte aligned (1040) take the direct-to-LDS
+    kernel, rows at 8 bytes past alignment (1032) the register-staged one
+    (the direct kernel moves whole aligned 16-byte chunks); both match the
+    oracle, so no padding byte enters a product."""
+    M, N, K = 256, 384, 1024
+    cx, cw, s, exp, _, _ = _fp8_operands(M, N, K, 90)
+    bx = torch.full((M, ld), 0x7F, dtype=torch.uint8, device="cuda")
+    bw = torch.full((N, ld), 0x7F, dtype=torch.uint8, device="cuda")
+    bx[:, :K], bw[:, :K] = cx, cw
+    with _Plans() as log:
+        got = gemm.linear_fp8(bx[:, :K], bw[:, :K], s)
+    assert log[0][0] == (gemm.FAMILY_DIRECT_FP8 if ld % 16 == 0 else gemm.FAMILY_STAGED)
+    assert max_rel_err(got, exp) < TOL
+
+
+def test_bf16_linear_odd_contraction():
+    """quantized_ops.linear with K = 27 (a first convolution's C * kh * kw):
+    K is zero-padded to whole 16-byte chunks, which adds nothing."""
+    a, b = _rand((64, 27), 91).cuda(), _rand((40, 27), 92).cuda()
+    got = torch.ops.quantized_ops.linear(a, b)
+    assert max_rel_err(got, O.linear(a.cpu(), b.cpu())) < TOL
+    a3 = _rand((3, 16, 27), 93).cuda()
+    got3 = torch.ops.quantized_ops.linear(a3, b)
+    assert max_rel_err(got3, O.linear(a3.cpu(), b.cpu())) < TOL

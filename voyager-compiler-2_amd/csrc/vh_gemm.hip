@@ -2118,7 +2118,12 @@ Plan plan_gemm(const vh_gemm_desc* d) {
     else staged = 4;
   }
   staged = staged_tile(staged);
-  if (fp8 && dl_ok) {
+  // The direct-to-LDS kernels move whole aligned 16-byte chunks of each
+  // row: rows 16-byte aligned and K a whole number of chunks (a chunk that
+  // straddled K would bring the row's padding into the products; fp8 K is
+  // validated a multiple of 16 below, where the descriptor is checked).
+  const bool chunks_ok = d->lda % 16 == 0 && d->ldb % 16 == 0 && d->K % (fp8 ? 16 : 8) == 0;
+  if (fp8 && dl_ok && chunks_ok) {
     // Direct-to-LDS kernels with 128-byte stages.  Measured on MI355X at
     // M = 2048 (K in {4096, 14336}, N in {1024, 4096, 14336}): the largest
     // tile that still gives every CU a block wins, since each CU's operand
@@ -2137,7 +2142,7 @@ Plan plan_gemm(const vh_gemm_desc* d) {
     if (is_direct_fp8_tile(c)) return {FAM_DIRECT_FP8, c, 1};
   }
   if (fp8) return {FAM_STAGED, staged, 1};
-  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16 && dl_ok && (d->tile_hint == 0 || d->tile_hint >= 20)) {
+  if (d->a_fmt == OP_BF16 && d->b_fmt == OP_BF16 && dl_ok && chunks_ok && (d->tile_hint == 0 || d->tile_hint >= 20)) {
     // As for fp8; a grid under 224 tiles of 128 x 128 takes 128 x 64
     // (M = 256, K = 4096 on MI355X: N = 4096 in 18.5 us against 24.6 us,
     // 21.4 against 30.1 with a float32 result; N = 14336, 224 tiles, stays

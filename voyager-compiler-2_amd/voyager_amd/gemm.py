@@ -96,6 +96,17 @@ def _epilogue(mode, out_dtype, scale=None, bias=None) -> Epilogue:
     return e
 
 
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """``t`` [R, C] with unit column stride and rows at least C elements
+    apart (the layout the kernels address as ``base + row * ld + col``);
+    a copy when the view is laid out otherwise."""
+    if t.dim() != 2:
+        raise RuntimeError(f"expected a 2-D operand, got shape {list(t.shape)}")
+    if t.stride(1) == 1 and t.stride(0) >= t.shape[1]:
+        return t
+    return t.contiguous()
+
+
 def _bias_operand(bias: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     """A bias as the epilogues read it: bf16 and float32 as they are (every
     epilogue widens bf16 exactly), other dtypes converted to float32."""
@@ -114,6 +125,10 @@ def gemm_bf16(a: torch.Tensor, b: torch.Tensor, out_dtype, bias=None, alpha=None
     K = a.shape[-1]
     if b.shape[-1] != K:
         raise RuntimeError(f"GEMM contraction mismatch: {list(a.shape)} vs {list(b.shape)}")
+    if K % 8:  # the kernels move 16-byte chunks of each row: zero-pad K
+        a = torch.nn.functional.pad(a, (0, -K % 8))
+        b = torch.nn.functional.pad(b, (0, -K % 8))
+        K = a.shape[-1]
     if b.dim() == 2 and a.dim() > 2:  # one GEMM over all leading dims
         lead = a.shape[:-1]
         return gemm_bf16(a.reshape(-1, K), b, out_dtype, bias, alpha).view(*lead, b.shape[0])
@@ -285,12 +300,18 @@ def linear_fp8(xq: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor, out: Opt
     xq, wq), s)`` (``quantization/quantize_pt2e.py:538-600``) with E4M3 bytes
     ``xq`` [M, K] and ``wq`` [N, K] and the bf16 scale product ``s``: the fp32
     accumulator is rounded to bf16, multiplied by ``s`` and rounded again."""
+    if xq.element_size() != 1 or wq.element_size() != 1:
+        raise RuntimeError("linear_fp8: operands must hold one-byte E4M3 codes")
+    xq, wq = _rows(xq), _rows(wq)
     M, K = xq.shape
     N = wq.shape[0]
     if wq.shape[1] != K:
         raise RuntimeError("linear_fp8: contraction mismatch")
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=xq.device)
+    elif (out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1
+          or out.stride(0) < N):
+        raise RuntimeError("linear_fp8: out must be a bfloat16 [M, N] tensor with unit column stride")
     d = GemmDesc()
     d.A, d.B, d.C = xq.data_ptr(), wq.data_ptr(), out.data_ptr()
     d.M, d.N, d.K = M, N, K
@@ -309,8 +330,11 @@ def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: i
     power-of-two scale bytes, decoded exactly to bf16 in the GEMM's staging.
     Grids too small for the GPU split K (``split_k`` 0: automatic); the
     partials live in a workspace from torch's allocator."""
+    x_codes, w_codes, x_scale, w_scale = _rows(x_codes), _rows(w_codes), _rows(x_scale), _rows(w_scale)
     M, K = x_codes.shape
     N = w_codes.shape[0]
+    if w_codes.shape[1] != K:
+        raise RuntimeError("linear_mxint8: contraction mismatch")
     out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
@@ -403,6 +427,7 @@ def linear_mx8_f16(x16: torch.Tensor, ex: torch.Tensor, weight: MX8F16Weight, ou
     K splits and one reduction that applies ``2**(E_row + E_col)``, alpha,
     bias and the output rounding; unsplit, the GEMM's epilogue applies them
     itself."""
+    x16 = x16.contiguous()
     M, K = x16.shape
     if K != weight.K:
         raise RuntimeError("linear_mx8_f16: contraction mismatch")
@@ -453,8 +478,11 @@ def linear_posit8(x_codes, w_codes, lut: torch.Tensor, out_dtype=torch.bfloat16,
     end.  Both operands are decoded through ``lut`` to bf16 (exact) and run
     through the bf16 GEMM; with a ``tile_hint`` the codes are decoded while
     the GEMM stages them instead."""
+    x_codes, w_codes = _rows(x_codes), _rows(w_codes)
     M, K = x_codes.shape
     N = w_codes.shape[0]
+    if w_codes.shape[1] != K:
+        raise RuntimeError("linear_posit8: contraction mismatch")
     if tile_hint == 0 and K % 8 == 0:
         return gemm_bf16(decode_bytes(x_codes, lut), decode_bytes(w_codes, lut), out_dtype)
     out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
