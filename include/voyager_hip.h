@@ -70,6 +70,10 @@ typedef struct vh_format {
   const void* lut;  /* LUT: 65,536 bfloat16 entries in device memory */
 } vh_format;
 
+/* Raised whenever an entry point's arguments or meaning change; a loader
+ * compares vh_abi_version() with the VH_ABI_VERSION it was written against. */
+#define VH_ABI_VERSION 2
+
 const char* vh_last_error(void);
 int vh_abi_version(void);
 

@@ -48,7 +48,10 @@ def test_ctypes_table_matches_the_header():
 def test_host_side_entry_points():
     lib = _library()
     lib.vh_abi_version.restype = ctypes.c_int32
-    assert lib.vh_abi_version() >= 1
+    from voyager_amd import _lib
+
+    macro = re.search(r"#define VH_ABI_VERSION (\d+)", open(HEADER).read())
+    assert macro and int(macro.group(1)) == _lib.ABI_VERSION == lib.vh_abi_version()
     lib.vh_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.vh_last_error(), bytes)
     lib.vh_filter_outlier_workspace_bytes.restype = ctypes.c_int64

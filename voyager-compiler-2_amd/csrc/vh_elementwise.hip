@@ -43,7 +43,7 @@ int check_launch(const char* what) {
 }  // namespace vh
 
 extern "C" const char* vh_last_error(void) { return vh::g_error.c_str(); }
-extern "C" int vh_abi_version(void) { return 1; }
+extern "C" int vh_abi_version(void) { return VH_ABI_VERSION; }
 
 // ------------------------------------------------------------ table rebuild
 // Rebuilds a table with the same specialised closed form the quantize

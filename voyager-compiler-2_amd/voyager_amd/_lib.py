@@ -176,6 +176,9 @@ KIVI_RES_CAP = 128
 FILTER_NOALLOC_SCRATCH_BYTES = 8 << 20
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
 
+#: ``VH_ABI_VERSION`` of the header these bindings follow.
+ABI_VERSION = 2
+
 #: Every symbol ``include/voyager_hip.h`` declares.
 EXPORTED = tuple(_SIGNATURES)
 
@@ -191,6 +194,10 @@ def load() -> ctypes.CDLL:
             "run __graft_entry__.build() first"
         )
     lib = ctypes.CDLL(LIB_PATH)
+    lib.vh_abi_version.restype = _I32
+    if lib.vh_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"voyager_amd: {LIB_PATH} has ABI version {lib.vh_abi_version()}, this package binds "
+                           f"version {ABI_VERSION}; rebuild it with __graft_entry__.build()")
     for name, (args, res) in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = args
