@@ -536,10 +536,15 @@ def bench_config3(args, cpu_budget_s=0.0):
         q_ms = time_graph(gq, 5) / 10
         gg = capture(lambda: [gemm.gemm_nf4_packed(px, wb) for _ in range(10)])
         g_ms = time_graph(gg, 5) / 10
+        gf = capture(lambda: [gemm.gemm_nf4_packed(px, wb, two_pass=False) for _ in range(10)])
+        f_ms = time_graph(gf, 5) / 10
+        gd = capture(lambda: [gemm.nf4_decode_bf16(px, wb) for _ in range(10)])
+        d_ms = time_graph(gd, 5) / 10
         tf = 2 * 2048 * N * K / (g_ms * 1e-3) / 1e12
         prefill[f"M2048_K{K}_N{N}"] = {"gemm_us": round(g_ms * 1e3, 2), "TFLOP/s": round(tf, 1),
-                                       "frac_of_mfma": round(tf / 2500.0, 4), "quantize_us": round(q_ms * 1e3, 2)}
-        del w, wb, x, px, gq, gg
+                                       "frac_of_mfma": round(tf / 2500.0, 4), "decode_us": round(d_ms * 1e3, 2),
+                                       "fused_us": round(f_ms * 1e3, 2), "quantize_us": round(q_ms * 1e3, 2)}
+        del w, wb, x, px, gq, gg, gf, gd
     cpu = cpu_config3(cpu_budget_s) if cpu_budget_s > 0 else None
     return {"metric": "MXNF4 decode linear GB/s (config 3)", "value": round(gbs, 1),
             "unit": "GB/s", "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
@@ -549,8 +554,10 @@ def bench_config3(args, cpu_budget_s=0.0):
                                  "(4-bit codes, scale bytes, bf16 activations and outputs) / their durations"},
             "per_shape": res, "cpu_baseline": cpu,
             "prefill_gemm": {"shapes": prefill, "mfma": "v_mfma_f32_32x32x16_bf16 (2.5 PF dense)",
-                             "note": "vh_gemm_nf4: both operands decoded while staging to bf16(level * scale), "
-                                     "bf16 MFMA, float32 accumulation; quantize_us = the activation's quantize_mx"},
+                             "note": "at M = 2048 both operands decoded once to bf16(level * scale) "
+                                     "(vh_nf4_decode_bf16, decode_us) and multiplied by the bf16 GEMM, float32 "
+                                     "accumulation (gemm_us, both); fused_us = vh_gemm_nf4, which decodes them "
+                                     "while staging; quantize_us = the activation's quantize_mx"},
             "config": {"workload": "cfg3: lut4_to_int6 bs=64 fp8_e5m3 scales, M in {1,16}"}}
 
 

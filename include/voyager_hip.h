@@ -385,6 +385,16 @@ int vh_gemm_nf4(const uint8_t* x_idx, const uint8_t* x_scale, const vh_format* x
  * caller's nonzero *tile / *splits are kept, the splits rounded to whole
  * ranges of 64-element blocks), so the caller can size its workspace. */
 int vh_gemm_nf4_plan(int64_t M, int64_t N, int64_t K, int32_t* tile, int32_t* splits, int64_t* bm);
+/* The operands of vh_gemm_nf4 decoded once to bfloat16, for the two-pass
+ * prefill (decode, then the bf16 GEMM of vh_gemm): x_out [M, K] =
+ * bf16(level[x_idx] * x_scale) and w_out [N, K] the weight's rows likewise,
+ * bit for bit the operands vh_gemm_nf4 multiplies -- the reference's
+ * decoded operands (_dequantize_mx, ops/quantized.py:574-591).  Either
+ * output may be NULL to skip that operand.  Arguments as vh_gemm_nf4. */
+int vh_nf4_decode_bf16(const uint8_t* x_idx, const uint8_t* x_scale, const vh_format* x_scale_fmt, int64_t M,
+                       const uint8_t* w_packed, const uint8_t* w_scale, const vh_format* w_scale_fmt,
+                       const int8_t* levels16, int64_t N, int64_t K, uint16_t* x_out, uint16_t* w_out,
+                       vh_stream_t stream);
 
 /* ------------------------------------------------- decoder-layer decode step
  * One decode step (a batch of single tokens, M <= 16) of a Llama-style layer

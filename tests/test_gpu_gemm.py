@@ -350,17 +350,20 @@ def test_linear_nf4_gemv_cfg3(M, K, N):
         assert torch.equal(got, one)
 
 
+@pytest.mark.parametrize("two_pass", [False, True])
 @pytest.mark.parametrize("M,K,N,tile,splits", [(17, 1024, 256, 0, 0), (64, 4096, 1024, 0, 0), (300, 576, 1040, 1, 1),
                                                (300, 576, 1040, 2, 3), (2048, 4096, 4096, 0, 0), (33, 64, 16, 0, 0),
                                                (40, 4160, 48, 1, 7)])
-def test_linear_nf4_prefill(M, K, N, tile, splits):
-    """MXNF4 linear_mx above the GEMV's 16 rows, on the GEMV's baked weight:
-    against the oracle's linear_mx (1e-2), and -- both operands decoded
-    exactly as the reference decodes them -- within one bf16 ulp of the
-    float64 product of the oracle's decoded operands (plus the float32
-    accumulation allowance); ragged rows, columns and block counts, bf16
-    and float32 results with alpha and bias."""
-    from voyager_amd import gemm
+def test_linear_nf4_prefill(M, K, N, tile, splits, two_pass):
+    """MXNF4 linear_mx above the GEMV's 16 rows, on the GEMV's baked weight,
+    fused (both operands decoded while the GEMM stages them) and in two
+    passes (both decoded once, then the bf16 GEMM): against the oracle's
+    linear_mx (1e-2), and -- both operands decoded exactly as the reference
+    decodes them, which the two-pass decode shows bit for bit -- within one
+    bf16 ulp of the float64 product of the oracle's decoded operands (plus
+    the float32 accumulation allowance); ragged rows, columns and block
+    counts, bf16 and float32 results with alpha and bias."""
+    from voyager_amd import gemm, packed
 
     vt = T.quantization_map("lut4_to_int6")
     index, entries, mid = T.codebook_index_table(vt)
@@ -379,16 +382,20 @@ def test_linear_nf4_prefill(M, K, N, tile, splits):
     wb = gemm.bake_nf4_weight(w.to(d), index.to(d), stab.to(d), entries.to(d))
     t, sp = gemm.nf4_prefill_plan(M, N, K, tile, splits)
     print(f"nf4 prefill M={M} K={K} N={N}: tile {t}, {sp} K splits", flush=True)
-    got = gemm.linear_nf4_prefill(x.to(d), wb, index.to(d), stab.to(d), tile=tile, splits=splits)
+    if two_pass:
+        px = packed.quantize_mx_packed(x.to(d), index.to(d), [-1], 64, 31.0, False, stab.to(d))
+        xo, wo = gemm.nf4_decode_bf16(px, wb)
+        assert torch.equal(xo.cpu().double(), xd) and torch.equal(wo.cpu().double(), wd)
+    got = gemm.linear_nf4_prefill(x.to(d), wb, index.to(d), stab.to(d), tile=tile, splits=splits, two_pass=two_pass)
     assert got.dtype == torch.bfloat16 and list(got.shape) == [M, N]
     assert max_rel_err(got, exp) < TOL
     assert_within_bf16_ulps(got, xd @ wd.T, 1.0, 2.0**-14 * (xd.abs() @ wd.abs().T), "prefill")
-    if M > 16:
+    if M > 16 and two_pass == gemm.nf4_two_pass_pays(M, N, K):
         assert torch.equal(got, gemm.linear_nf4(x.to(d), wb, index.to(d), stab.to(d)))
     alpha = torch.tensor(0.75, device=d)
     bias = (torch.randn(N, generator=g)).bfloat16()
     got32 = gemm.linear_nf4_prefill(x.to(d), wb, index.to(d), stab.to(d), out_dtype=torch.float32, bias=bias.to(d),
-                                    alpha=alpha, tile=tile, splits=splits)
+                                    alpha=alpha, tile=tile, splits=splits, two_pass=two_pass)
     ref = (xd @ wd.T) * 0.75 + bias.double()
     assert max_rel_err(got32, ref) < 1e-5
 

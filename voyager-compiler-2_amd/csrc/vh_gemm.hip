@@ -2063,6 +2063,91 @@ int launch_nf4(GemmArgs g, const Nf4Args& q, int splits, float* part, hipStream_
   return vh::check_launch("vh_gemm_nf4");
 }
 
+// ------------------------------------------------------------ MXNF4 operands to bf16
+// The two-pass form of the prefill: each operand decoded once to exactly
+// the bf16(level * scale) k_gemm_nf4 stages (the same lut16 and nf4_pack16
+// steps), for the bf16 GEMM.  k_gemm_nf4 decodes a weight block once per
+// row tile and an activation block once per column tile; at large M one
+// decode plus a write and a read of the bf16 operands costs less.
+
+// Weight as vh_pack_nf4 bakes it, in groups of one 16-row tile and four
+// 64-element blocks (256 columns); a workgroup takes NF4_DEC groups.  In a
+// group, thread t takes row r = t / 16 and the 16 elements 16 (t % 16) .. +
+// 15 of its 256 columns: GEMV record r + 16 c of block t % 16 / 4 (c = t %
+// 4; element e in the low nibble of byte e, e + 8 in its high nibble) and
+// the row's scale byte.  The 16 threads of a row write its 512 bytes
+// contiguously.  Every group's loads go out before the scale table is built.
+constexpr int NF4_DEC = 4;
+
+__global__ void __launch_bounds__(256) k_nf4_weight_bf16(const uint8_t* __restrict__ w, const uint8_t* __restrict__ ws,
+                                                         Nf4Args q, int64_t N, int64_t K, uint16_t* __restrict__ out) {
+  __shared__ float s_sc[256];
+  const int64_t nbk = K / 64, nq = (nbk + 3) / 4, groups = (N / 16) * nq;
+  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
+  uint2 rec[NF4_DEC];
+  uint32_t sb[NF4_DEC];
+  int64_t dst[NF4_DEC];
+#pragma unroll
+  for (int i = 0; i < NF4_DEC; ++i) {
+    const int64_t gi = (int64_t)blockIdx.x * NF4_DEC + i;
+    const int64_t tile = gi / nq, kb = (gi % nq) * 4 + (j >> 2);
+    const bool ok = gi < groups && kb < nbk;
+    const int64_t u = ok ? tile * nbk + kb : 0;  // (tile, block) record group
+    rec[i] = *(const uint2*)(w + (u * 64 + r + 16 * (j & 3)) * 8);
+    sb[i] = ws[u * 16 + r];
+    dst[i] = ok ? (tile * 16 + r) * K + kb * 64 + (j & 3) * 16 : -1;
+  }
+  s_sc[threadIdx.x] = fmt_decode(threadIdx.x, q.b_sf, nullptr);
+  __syncthreads();
+  uint32_t base;
+  asm volatile("v_mov_b32 %0, 0x3020100" : "=v"(base));
+#pragma unroll
+  for (int i = 0; i < NF4_DEC; ++i) {
+    if (dst[i] < 0) continue;
+    const uint32_t l[4] = {lut_lo(rec[i].x, base, q.lvb), lut_lo(rec[i].y, base, q.lvb),
+                           lut_hi(rec[i].x, base, q.lvb), lut_hi(rec[i].y, base, q.lvb)};
+    uint4 lo, hi;
+    nf4_pack16(l, s_sc[sb[i]], lo, hi);
+    *(uint4*)(out + dst[i]) = lo;
+    *(uint4*)(out + dst[i] + 8) = hi;
+  }
+}
+
+// Activation as quantize_mx packs it (index bytes [M, K], scale codes
+// [M, K / 64]): each thread takes NF4_DEC runs of 16 indices, 4096
+// elements apart, loaded before the scale table is built.
+__global__ void __launch_bounds__(256) k_nf4_act_bf16(const uint8_t* __restrict__ x, const uint8_t* __restrict__ xs,
+                                                      Nf4Args q, int64_t M, int64_t K, uint16_t* __restrict__ out) {
+  __shared__ float s_sc[256];
+  const int64_t chunks = M * K / 16;
+  uint4 v[NF4_DEC];
+  uint32_t sc[NF4_DEC];
+  int64_t e[NF4_DEC];
+#pragma unroll
+  for (int i = 0; i < NF4_DEC; ++i) {
+    const int64_t c = ((int64_t)blockIdx.x * NF4_DEC + i) * 256 + threadIdx.x;
+    const bool ok = c < chunks;
+    const int64_t ei = ok ? c * 16 : 0, row = ei / K;
+    v[i] = *(const uint4*)(x + ei);
+    sc[i] = xs[row * (K / 64) + (ei - row * K) / 64];
+    e[i] = ok ? ei : -1;
+  }
+  s_sc[threadIdx.x] = fmt_decode(threadIdx.x, q.a_sf, nullptr);
+  __syncthreads();
+  uint32_t base;
+  asm volatile("v_mov_b32 %0, 0x3020100" : "=v"(base));
+#pragma unroll
+  for (int i = 0; i < NF4_DEC; ++i) {
+    if (e[i] < 0) continue;
+    const uint32_t l[4] = {lut_lo(v[i].x, base, q.lvb), lut_lo(v[i].y, base, q.lvb), lut_lo(v[i].z, base, q.lvb),
+                           lut_lo(v[i].w, base, q.lvb)};
+    uint4 lo, hi;
+    nf4_pack16(l, s_sc[sc[i]], lo, hi);
+    *(uint4*)(out + e[i]) = lo;
+    *(uint4*)(out + e[i] + 8) = hi;
+  }
+}
+
 }  // namespace
 
 namespace {
@@ -2450,4 +2535,41 @@ extern "C" int vh_gemm_nf4_plan(int64_t M, int64_t N, int64_t K, int32_t* tile, 
   const int64_t nbk = K / 64, kcs = (nbk + *splits - 1) / *splits;
   *splits = (int32_t)((nbk + kcs - 1) / kcs);
   return VH_OK;
+}
+
+extern "C" int vh_nf4_decode_bf16(const uint8_t* x_idx, const uint8_t* x_scale, const vh_format* x_scale_fmt,
+                                  int64_t M, const uint8_t* w_packed, const uint8_t* w_scale,
+                                  const vh_format* w_scale_fmt, const int8_t* levels16, int64_t N, int64_t K,
+                                  uint16_t* x_out, uint16_t* w_out, vh_stream_t stream) {
+  VH_REQUIRE(levels16 && K > 0 && K % 64 == 0, "vh_nf4_decode_bf16: needs the levels and K %% 64 == 0");
+  VH_REQUIRE(!x_out || (x_idx && x_scale && x_scale_fmt && M >= 1), "vh_nf4_decode_bf16: activation arguments");
+  VH_REQUIRE(!w_out || (w_packed && w_scale && w_scale_fmt && N > 0 && N % 16 == 0),
+             "vh_nf4_decode_bf16: weight arguments (N %% 16 == 0)");
+  VH_REQUIRE((!x_out || ((uintptr_t)x_idx % 16 == 0 && (uintptr_t)x_out % 16 == 0)) &&
+                 (!w_out || ((uintptr_t)w_packed % 8 == 0 && (uintptr_t)w_out % 16 == 0)),
+             "vh_nf4_decode_bf16: misaligned operand");
+  for (const vh_format* f : {x_out ? x_scale_fmt : nullptr, w_out ? w_scale_fmt : nullptr})
+    VH_REQUIRE(!f || f->kind == VH_FMT_INT || f->kind == VH_FMT_MINIFLOAT || f->kind == VH_FMT_POSIT,
+               "vh_nf4_decode_bf16: the scale maps need a closed form with packed codes");
+  uint8_t lvb[16];
+  for (int v = 0; v < 16; ++v) lvb[v] = (uint8_t)(levels16[v] + 128);
+  uint32_t t[4];
+  memcpy(t, lvb, 16);
+  Nf4Args q;
+  memset(&q, 0, sizeof(q));
+  q.lvb = make_uint4(t[0], t[1], t[2], t[3]);
+  if (x_out) q.a_sf = *x_scale_fmt;
+  if (w_out) q.b_sf = *w_scale_fmt;
+  hipStream_t st = vh::as_stream(stream);
+  if (x_out) {
+    const int64_t per = 256 * NF4_DEC, chunks = M * K / 16;
+    hipLaunchKernelGGL(k_nf4_act_bf16, dim3((unsigned)((chunks + per - 1) / per)), dim3(256), 0, st, x_idx, x_scale,
+                       q, M, K, x_out);
+  }
+  if (w_out) {
+    const int64_t groups = (N / 16) * ((K / 64 + 3) / 4);  // (tile, four blocks)
+    hipLaunchKernelGGL(k_nf4_weight_bf16, dim3((unsigned)((groups + NF4_DEC - 1) / NF4_DEC)), dim3(256), 0, st,
+                       w_packed, w_scale, q, N, K, w_out);
+  }
+  return vh::check_launch("vh_nf4_decode_bf16");
 }

@@ -146,6 +146,8 @@ _SIGNATURES = {
     "vh_gemm_nf4": ([_P, _P, ctypes.POINTER(Format), _I64, _P, _P, ctypes.POINTER(Format), _P, _I64, _I64, _P,
                      _P, _I64, _I32, _I32, _P, _I64, _P], _I32),
     "vh_gemm_nf4_plan": ([_I64, _I64, _I64, _P, _P, _P], _I32),
+    "vh_nf4_decode_bf16": ([_P, _P, ctypes.POINTER(Format), _I64, _P, _P, ctypes.POINTER(Format), _P, _I64, _I64,
+                            _P, _P, _P], _I32),
     "vh_gemv_nf4_m1": ([_P, _I32, ctypes.c_float, ctypes.POINTER(Format), ctypes.POINTER(Format), _P, _P,
                         ctypes.POINTER(Format), _P, _I64, _I64, _P, _P, _P], _I32),
     # decoder-layer decode step

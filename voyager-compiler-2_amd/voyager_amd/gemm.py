@@ -581,7 +581,7 @@ def nf4_prefill_plan(M: int, N: int, K: int, tile: int = 0, splits: int = 0) -> 
 
 def linear_nf4_prefill(x: torch.Tensor, weight: NF4Weight, index_table: torch.Tensor, scale_qmap: torch.Tensor,
                        out_dtype=torch.bfloat16, bias=None, alpha=None, tile: int = 0,
-                       splits: int = 0) -> torch.Tensor:
+                       splits: int = 0, two_pass: Optional[bool] = None) -> torch.Tensor:
     """MXNF4 ``linear_mx`` at any M on the GEMV's baked weight: the
     activation's ``quantize_mx`` to index and scale bytes, then
     ``vh_gemm_nf4``, which decodes both operands while staging to the
@@ -593,16 +593,61 @@ def linear_nf4_prefill(x: torch.Tensor, weight: NF4Weight, index_table: torch.Te
     if K != weight.K:
         raise RuntimeError("linear_nf4_prefill: contraction mismatch")
     px = _packed.quantize_mx_packed(x.contiguous(), index_table, [-1], 64, 31.0, False, scale_qmap)
-    return gemm_nf4_packed(px, weight, out_dtype, bias, alpha, tile, splits)
+    return gemm_nf4_packed(px, weight, out_dtype, bias, alpha, tile, splits, two_pass)
+
+
+def nf4_decode_bf16(px, weight: NF4Weight, decode_x: bool = True, decode_w: bool = True):
+    """``(x, w)``: the operands ``vh_gemm_nf4`` multiplies, decoded once to
+    bf16 (``vh_nf4_decode_bf16``): the activation packed by
+    ``quantize_mx_packed`` [M, K] and the baked weight's rows [N, K], each
+    ``bf16(level * scale)`` as the reference decodes them; None where not
+    asked for."""
+    M, K = px.codes.shape
+    if K != weight.K:
+        raise RuntimeError("nf4_decode_bf16: contraction mismatch")
+    dev = weight.packed.device
+    xo = torch.empty(M, K, dtype=torch.bfloat16, device=dev) if decode_x else None
+    wo = torch.empty(weight.N, K, dtype=torch.bfloat16, device=dev) if decode_w else None
+    codes, scale = px.codes.contiguous(), px.scale.contiguous()
+    lv = ctypes.create_string_buffer(weight.levels, 16)
+    st = load().vh_nf4_decode_bf16(ptr(codes), ptr(scale), ctypes.byref(px.scale_fmt.fmt), M,
+                                   ptr(weight.packed), ptr(weight.scale), ctypes.byref(weight.scale_fmt.fmt), lv,
+                                   weight.N, K, ptr(xo), ptr(wo), ctypes.c_void_p(stream_of(weight.packed)))
+    _lib.check(st, "vh_nf4_decode_bf16")
+    return xo, wo
+
+
+def nf4_two_pass_pays(M: int, N: int, K: int) -> bool:
+    """Whether the prefill runs as two passes (both operands decoded once,
+    then the bf16 GEMM) rather than ``vh_gemm_nf4``, which decodes each
+    weight block once per row tile of the output.  Measured on MI355X
+    (fused / two-pass, us): (K, N) = (4096, 4096) at M = 256: 35.1 / 37.5,
+    M = 512: 49.8 / 37.4, M = 2048: 96.3 / 74.4; (4096, 14336): 78.0 / 57.8,
+    95.4 / 79.5, 368.7 / 227.9; (14336, 4096): 77.1 / 90.1, 140.8 / 98.7,
+    321.1 / 219.1.  The two-pass form holds the decoded weight (2 bytes per
+    element) for the call."""
+    return M >= NF4_TWO_PASS_MIN_M
+
+
+#: Rows from which the two-pass MXNF4 prefill is taken.
+NF4_TWO_PASS_MIN_M = 512
 
 
 def gemm_nf4_packed(px, weight: NF4Weight, out_dtype=torch.bfloat16, bias=None, alpha=None, tile: int = 0,
-                    splits: int = 0) -> torch.Tensor:
+                    splits: int = 0, two_pass: Optional[bool] = None) -> torch.Tensor:
     """``vh_gemm_nf4`` on an activation already packed by ``quantize_mx_packed``
-    (index bytes [M, K] and scale codes [M, K / 64])."""
+    (index bytes [M, K] and scale codes [M, K / 64]); with ``two_pass`` (by
+    default where ``nf4_two_pass_pays``) the operands decoded once by
+    ``nf4_decode_bf16`` and multiplied by the bf16 GEMM instead, which gives
+    the same products summed in another order."""
     M, K = px.codes.shape
     if K != weight.K:
         raise RuntimeError("gemm_nf4_packed: contraction mismatch")
+    if two_pass is None:
+        two_pass = nf4_two_pass_pays(M, weight.N, K)
+    if two_pass:
+        xo, wo = nf4_decode_bf16(px, weight)
+        return gemm_bf16(xo, wo, out_dtype, bias, alpha)
     y = torch.empty(M, weight.N, dtype=out_dtype, device=px.codes.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
