@@ -145,7 +145,11 @@ VH_DEV void element_code(float x, const BlockScale& bs, const Params& P, const u
   const uint32_t b = (P.cdt == VH_BF16 && !isnan_f(q)) ? (__float_as_uint(q) >> 16) : f2bf(q);
   if constexpr (KIND == K_STEPS) {
     const bool nan = bf_isnan_bits(b);
-    const uint32_t lvl = nan ? (uint32_t)P.fmt.nan_level : steps_level(b, P.fmt.nsteps, lds);
+    // (a wave-uniform branch: a table of at most 15 thresholds, as the
+    // 16-entry codebooks, needs four halvings rather than six)
+    const uint32_t lvl = nan ? (uint32_t)P.fmt.nan_level
+                             : P.fmt.nsteps <= 15 ? steps_level<8>(b, P.fmt.nsteps, lds)
+                                                  : steps_level(b, P.fmt.nsteps, lds);
     *v = round_to(nan ? bf2f(P.fmt.nan_out) : bf2f(lds[VH_MAX_STEPS + lvl]), P.cdt);
     *code = lvl;
   } else {
