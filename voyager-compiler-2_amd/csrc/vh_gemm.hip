@@ -2079,9 +2079,9 @@ int launch_nf4(GemmArgs g, const Nf4Args& q, int splits, float* part, hipStream_
 // contiguously.  Every group's loads go out before the scale table is built.
 constexpr int NF4_DEC = 4;
 
-__global__ void __launch_bounds__(256) k_nf4_weight_bf16(const uint8_t* __restrict__ w, const uint8_t* __restrict__ ws,
-                                                         Nf4Args q, int64_t N, int64_t K, uint16_t* __restrict__ out) {
-  __shared__ float s_sc[256];
+__device__ __forceinline__ void nf4_weight_bf16(int64_t wg, const uint8_t* __restrict__ w, const uint8_t* __restrict__ ws,
+                                                const Nf4Args& q, int64_t N, int64_t K, uint16_t* __restrict__ out,
+                                                float* s_sc) {
   const int64_t nbk = K / 64, nq = (nbk + 3) / 4, groups = (N / 16) * nq;
   const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
   uint2 rec[NF4_DEC];
@@ -2089,7 +2089,7 @@ __global__ void __launch_bounds__(256) k_nf4_weight_bf16(const uint8_t* __restri
   int64_t dst[NF4_DEC];
 #pragma unroll
   for (int i = 0; i < NF4_DEC; ++i) {
-    const int64_t gi = (int64_t)blockIdx.x * NF4_DEC + i;
+    const int64_t gi = wg * NF4_DEC + i;
     const int64_t tile = gi / nq, kb = (gi % nq) * 4 + (j >> 2);
     const bool ok = gi < groups && kb < nbk;
     const int64_t u = ok ? tile * nbk + kb : 0;  // (tile, block) record group
@@ -2116,16 +2116,16 @@ __global__ void __launch_bounds__(256) k_nf4_weight_bf16(const uint8_t* __restri
 // Activation as quantize_mx packs it (index bytes [M, K], scale codes
 // [M, K / 64]): each thread takes NF4_DEC runs of 16 indices, 4096
 // elements apart, loaded before the scale table is built.
-__global__ void __launch_bounds__(256) k_nf4_act_bf16(const uint8_t* __restrict__ x, const uint8_t* __restrict__ xs,
-                                                      Nf4Args q, int64_t M, int64_t K, uint16_t* __restrict__ out) {
-  __shared__ float s_sc[256];
+__device__ __forceinline__ void nf4_act_bf16(int64_t wg, const uint8_t* __restrict__ x, const uint8_t* __restrict__ xs,
+                                             const Nf4Args& q, int64_t M, int64_t K, uint16_t* __restrict__ out,
+                                             float* s_sc) {
   const int64_t chunks = M * K / 16;
   uint4 v[NF4_DEC];
   uint32_t sc[NF4_DEC];
   int64_t e[NF4_DEC];
 #pragma unroll
   for (int i = 0; i < NF4_DEC; ++i) {
-    const int64_t c = ((int64_t)blockIdx.x * NF4_DEC + i) * 256 + threadIdx.x;
+    const int64_t c = (wg * NF4_DEC + i) * 256 + threadIdx.x;
     const bool ok = c < chunks;
     const int64_t ei = ok ? c * 16 : 0, row = ei / K;
     v[i] = *(const uint4*)(x + ei);
@@ -2146,6 +2146,18 @@ __global__ void __launch_bounds__(256) k_nf4_act_bf16(const uint8_t* __restrict_
     *(uint4*)(out + e[i]) = lo;
     *(uint4*)(out + e[i] + 8) = hi;
   }
+}
+
+// One launch for both operands: workgroups [0, xw) take the activation,
+// the rest the weight.
+__global__ void __launch_bounds__(256) k_nf4_decode_bf16(const uint8_t* __restrict__ x, const uint8_t* __restrict__ xs,
+                                                         int64_t M, const uint8_t* __restrict__ w,
+                                                         const uint8_t* __restrict__ ws, int64_t N, int64_t K, Nf4Args q,
+                                                         int64_t xw, uint16_t* __restrict__ x_out,
+                                                         uint16_t* __restrict__ w_out) {
+  __shared__ float s_sc[256];
+  if ((int64_t)blockIdx.x < xw) nf4_act_bf16(blockIdx.x, x, xs, q, M, K, x_out, s_sc);
+  else nf4_weight_bf16((int64_t)blockIdx.x - xw, w, ws, q, N, K, w_out, s_sc);
 }
 
 }  // namespace
@@ -2560,16 +2572,13 @@ extern "C" int vh_nf4_decode_bf16(const uint8_t* x_idx, const uint8_t* x_scale, 
   q.lvb = make_uint4(t[0], t[1], t[2], t[3]);
   if (x_out) q.a_sf = *x_scale_fmt;
   if (w_out) q.b_sf = *w_scale_fmt;
-  hipStream_t st = vh::as_stream(stream);
-  if (x_out) {
-    const int64_t per = 256 * NF4_DEC, chunks = M * K / 16;
-    hipLaunchKernelGGL(k_nf4_act_bf16, dim3((unsigned)((chunks + per - 1) / per)), dim3(256), 0, st, x_idx, x_scale,
-                       q, M, K, x_out);
-  }
-  if (w_out) {
-    const int64_t groups = (N / 16) * ((K / 64 + 3) / 4);  // (tile, four blocks)
-    hipLaunchKernelGGL(k_nf4_weight_bf16, dim3((unsigned)((groups + NF4_DEC - 1) / NF4_DEC)), dim3(256), 0, st,
-                       w_packed, w_scale, q, N, K, w_out);
-  }
+  const int64_t per = 256 * NF4_DEC;
+  const int64_t xw = x_out ? (M * K / 16 + per - 1) / per : 0;
+  const int64_t groups = w_out ? (N / 16) * ((K / 64 + 3) / 4) : 0;  // (tile, four blocks)
+  const int64_t ww = (groups + NF4_DEC - 1) / NF4_DEC;
+  VH_REQUIRE(xw + ww < (1ll << 31), "vh_nf4_decode_bf16: operands too large");
+  if (xw + ww == 0) return VH_OK;
+  hipLaunchKernelGGL(k_nf4_decode_bf16, dim3((unsigned)(xw + ww)), dim3(256), 0, vh::as_stream(stream), x_idx, x_scale,
+                     x_out ? M : 0, w_packed, w_scale, w_out ? N : 0, K, q, xw, x_out, w_out);
   return vh::check_launch("vh_nf4_decode_bf16");
 }
