@@ -148,6 +148,39 @@ def test_linear_mxint8_split_k(M, N, K, block, hint, split, tile):
     assert max_rel_err(got32, ref32) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(1030, 520, 1024), (2048, 4096, 4096)])
+def test_linear_mxint8_two_pass(M, N, K, monkeypatch):
+    """Grids past ``mxint8_two_pass_pays`` rebase both packed operands to
+    exact fp16 rows (``bake_mx8_f16``) and run the fp16 GEMM
+    (``linear_mx8_f16``), with no ``vh_gemm`` launch: against the exact
+    float64 product of the decoded operands and the in-staging decode
+    kernel, bf16 and float32 results with alpha and bias."""
+    from voyager_amd import gemm, packed
+
+    monkeypatch.setattr(gemm, "MXI8_TWO_PASS_MIN_WORK", 0)
+    assert gemm.mxint8_two_pass_pays(M, N, K)
+    tab = T.quantization_map("int8").cuda()
+    x = _rand((M, K), 34).cuda()
+    w = _rand((N, K), 35, 0.02).cuda()
+    px = packed.quantize_mx_packed(x, tab, [-1], 16, 127.0, True)
+    pw = packed.quantize_mx_packed(w, tab, [-1], 16, 127.0, True)
+    ref = _deq_mxint8(px) @ _deq_mxint8(pw).T
+    gemm.plan_log = log = []
+    try:
+        got = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias)
+    finally:
+        gemm.plan_log = None
+    assert log == [] and got.dtype == torch.bfloat16 and list(got.shape) == [M, N]
+    assert max_rel_err(got, ref) < TOL
+    staged = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias, tile_hint=4)
+    assert max_rel_err(got, staged) < 1e-2
+    alpha = torch.tensor(0.75, device="cuda")
+    bias = _rand((N,), 36).cuda()
+    got32 = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias, out_dtype=torch.float32,
+                               bias=bias, alpha=alpha)
+    assert max_rel_err(got32, ref * 0.75 + bias.cpu().double()) < 1e-5
+
+
 def test_linear_mxint8_fp16_operands_exponent_range():
     """k_gemm_mx8h rebases each row to its largest block exponent: rows whose
     blocks span 2**-40 .. 2**20 (blocks more than 24 binades below the row's
@@ -556,12 +589,13 @@ def test_quantize_mx8_f16_exact(M, K):
     assert bool(same.all()), (~same).nonzero()[:5]
 
 
-def test_mx8_f16_bake_flushes_only_far_blocks():
+@pytest.mark.parametrize("N,K", [(64, 512), (48, 6144), (16, 20480)])
+def test_mx8_f16_bake_flushes_only_far_blocks(N, K):
     """Weight baking: exact where a block is within 24 binades of its row's
-    largest, zero below."""
+    largest, zero below; rows of up to 256 blocks, up to 1024 (kept in
+    registers) and longer (the two-pass kernel)."""
     from voyager_amd import gemm, packed
 
-    N, K = 64, 512
     g = torch.Generator().manual_seed(5)
     ew = torch.randint(-40, 1, (N, K // 16), generator=g)
     ew[:, 0] = 0

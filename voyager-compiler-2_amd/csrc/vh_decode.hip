@@ -332,6 +332,50 @@ __global__ void __launch_bounds__(256) k_mx8_bake_f16(const int8_t* __restrict__
   if (threadIdx.x == 0) ew[row] = E;
 }
 
+// The same for rows of at most 256 NBT blocks: each thread loads its NBT
+// blocks' codes and scale bytes once, before the row maximum, and keeps
+// them in registers; identical arithmetic, so identical output.
+template <int NBT>
+__global__ void __launch_bounds__(256) k_mx8_bake_f16_r(const int8_t* __restrict__ codes,
+                                                        const uint8_t* __restrict__ sb, int bias, int64_t K,
+                                                        _Float16* __restrict__ out, int32_t* __restrict__ ew) {
+  __shared__ int s_red[4];
+  const int64_t row = blockIdx.x;
+  const int nb = (int)(K / 16);
+  int4 c[NBT];
+  int byte[NBT];
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) {
+    const int b = threadIdx.x + 256 * j;
+    const bool ok = b < nb;
+    c[j] = ok ? *(const int4*)(codes + row * K + (int64_t)b * 16) : make_int4(0, 0, 0, 0);
+    byte[j] = ok ? sb[row * nb + b] : 255;
+  }
+  int emax = INT_MIN;
+#pragma unroll
+  for (int j = 0; j < NBT; ++j)
+    if (byte[j] != 255) emax = max(emax, byte[j] - bias);
+  int E = block_max_int(emax, s_red);
+  if (E == INT_MIN) E = 0;
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) {
+    const int b = threadIdx.x + 256 * j;
+    if (b >= nb) continue;
+    const bool finite = byte[j] != 255;
+    const uint32_t cw[4] = {(uint32_t)c[j].x, (uint32_t)c[j].y, (uint32_t)c[j].z, (uint32_t)c[j].w};
+    f16x8 o[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float code = (float)(int8_t)(cw[i >> 2] >> (8 * (i & 3)));
+      o[i >> 3][i & 7] = rebased_f16(code, byte[j] - bias, finite, __builtin_inff(), E);
+    }
+    f16x8* dst = (f16x8*)(out + row * K + (int64_t)b * 16);
+    dst[0] = o[0];
+    dst[1] = o[1];
+  }
+  if (threadIdx.x == 0) ew[row] = E;
+}
+
 // ------------------------------------------------------------ MX-int8 GEMV
 // Baked weight layout, per 16-column tile T (K = 256 G):
 //   codes [T][K/64 step pairs][64 lanes][16 B]: bytes 0-7 step 2p, 8-15 step
@@ -1581,7 +1625,16 @@ extern "C" int vh_mx8_bake_f16(const int8_t* codes, const uint8_t* scale, int32_
   VH_REQUIRE(codes && scale && out && ew, "vh_mx8_bake_f16: null argument");
   VH_REQUIRE(N > 0 && K > 0 && K % 16 == 0, "vh_mx8_bake_f16: needs K a multiple of 16");
   VH_REQUIRE((uintptr_t)codes % 16 == 0 && (uintptr_t)out % 16 == 0, "vh_mx8_bake_f16: misaligned tensor");
-  hipLaunchKernelGGL(k_mx8_bake_f16, dim3((unsigned)N), dim3(256), 0, vh::as_stream(stream), codes, scale, scale_bias,
-                     K, (_Float16*)out, ew);
+  const int64_t nb = K / 16;
+  hipStream_t s = vh::as_stream(stream);
+  if (nb <= 256)
+    hipLaunchKernelGGL(k_mx8_bake_f16_r<1>, dim3((unsigned)N), dim3(256), 0, s, codes, scale, scale_bias, K,
+                       (_Float16*)out, ew);
+  else if (nb <= 1024)
+    hipLaunchKernelGGL(k_mx8_bake_f16_r<4>, dim3((unsigned)N), dim3(256), 0, s, codes, scale, scale_bias, K,
+                       (_Float16*)out, ew);
+  else
+    hipLaunchKernelGGL(k_mx8_bake_f16, dim3((unsigned)N), dim3(256), 0, s, codes, scale, scale_bias, K,
+                       (_Float16*)out, ew);
   return vh::check_launch("vh_mx8_bake_f16");
 }

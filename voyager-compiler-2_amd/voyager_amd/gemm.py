@@ -329,12 +329,20 @@ def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: i
     """MX-int8 ``linear_mx`` on packed operands: int8 codes with biased
     power-of-two scale bytes, decoded exactly to bf16 in the GEMM's staging.
     Grids too small for the GPU split K (``split_k`` 0: automatic); the
-    partials live in a workspace from torch's allocator."""
+    partials live in a workspace from torch's allocator.  With 16-element
+    blocks, no tile or split asked for and ``mxint8_two_pass_pays``, both
+    operands are rebased to exact fp16 rows (``bake_mx8_f16``) and
+    multiplied by ``linear_mx8_f16`` instead."""
     x_codes, w_codes, x_scale, w_scale = _rows(x_codes), _rows(w_codes), _rows(x_scale), _rows(w_scale)
     M, K = x_codes.shape
     N = w_codes.shape[0]
     if w_codes.shape[1] != K:
         raise RuntimeError("linear_mxint8: contraction mismatch")
+    if (block_size == 16 and tile_hint == 0 and split_k == 0 and K % 16 == 0
+            and x_scale.shape == (M, K // 16) and w_scale.shape == (N, K // 16) and mxint8_two_pass_pays(M, N, K)):
+        bx = bake_mx8_f16(x_codes.view(torch.int8), x_scale, bias_x)
+        bw = bake_mx8_f16(w_codes.view(torch.int8), w_scale, bias_w)
+        return linear_mx8_f16(bx.w, bx.e, bw, out_dtype, bias, alpha)
     out = torch.empty(M, N, dtype=out_dtype, device=x_codes.device)
     if alpha is not None:
         alpha = alpha.reshape(()).to(torch.float32).contiguous()
@@ -358,6 +366,21 @@ def linear_mxint8(x_codes, x_scale, w_codes, w_scale, block_size: int, bias_x: i
         d.workspace, d.workspace_bytes = ws.data_ptr(), nbytes
     run(d, x_codes.device)
     return out
+
+
+def mxint8_two_pass_pays(M: int, N: int, K: int) -> bool:
+    """Whether ``linear_mxint8`` rebases both operands to fp16 rows and runs
+    the fp16 GEMM rather than decoding the codes in the GEMM's staging.
+    Measured on MI355X (packed / two-pass, us): (K, N) = (4096, 4096) at
+    M = 1024: 53.8 / 60.4, M = 2048: 87.0 / 76.7; (4096, 14336): 161.4 /
+    134.9, 326.1 / 241.6; (14336, 4096): 181.4 / 164.8, 288.8 / 240.3."""
+    return M >= MXI8_TWO_PASS_MIN_M and M * N * K >= MXI8_TWO_PASS_MIN_WORK
+
+
+#: The two-pass MX-int8 linear needs at least these rows and this much work
+#: (M * N * K).
+MXI8_TWO_PASS_MIN_M = 1024
+MXI8_TWO_PASS_MIN_WORK = 1 << 35
 
 
 # ----------------------------------------------------------------- MX-int8, small M
