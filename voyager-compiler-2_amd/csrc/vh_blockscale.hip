@@ -96,6 +96,41 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
   }
   if constexpr (KIND == K_NONE) return;
   if (!live || !codes_out) return;
+  if constexpr (VEC == 8 && KIND == K_STEPS) {
+    // Packed indices of a codebook of at most 16 levels (element_code's
+    // steps for this case, no reference-form values): the eight searches
+    // step together, so their LDS reads overlap.
+    if (P.mode != AFFINE && P.cdt == VH_BF16 && P.codes_dtype == VH_U8 && !P.code_lut && P.fmt.nsteps <= 15) {
+      const int ns = P.fmt.nsteps;
+      uint32_t key[8], pos[8];
+      bool nanv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float q = div_bf16(xv[j], bs.el_scale);
+        const uint32_t b = !isnan_f(q) ? (__float_as_uint(q) >> 16) : f2bf(q);
+        nanv[j] = bf_isnan_bits(b);
+        key[j] = bf_key(b);
+        pos[j] = 0;
+      }
+#pragma unroll
+      for (int step = 8; step >= 1; step >>= 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int nxt = (int)pos[j] + step;
+          const bool ok = nxt <= ns && (uint32_t)lds[nxt <= ns ? nxt - 1 : 0] <= key[j];
+          pos[j] = ok ? (uint32_t)nxt : pos[j];
+        }
+      }
+      uint32_t c8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c8[j] = nanv[j] ? (uint32_t)P.fmt.nan_level : pos[j];
+      uint2 pk;
+      pk.x = c8[0] | (c8[1] << 8) | (c8[2] << 16) | (c8[3] << 24);
+      pk.y = c8[4] | (c8[5] << 8) | (c8[6] << 16) | (c8[7] << 24);
+      *(uint2*)((uint8_t*)codes_out + base) = pk;
+      return;
+    }
+  }
   float cv[VEC];
   uint32_t cc[VEC];
 #pragma unroll
