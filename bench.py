@@ -361,8 +361,9 @@ def bench_config1(args, cpu_budget_s=0.0):
     flops = 2.0 * 256 * 4096 * 4096
     qbytes = 256 * 4096 * 3 + 256 * 256  # bf16 in, int8 codes + scale bytes out
     gbytes = 256 * 4096 + 256 * 256 + 4096 * 4096 + 4096 * 256 + 256 * 4096 * 2
-    # prefill: the same weight against X [2048, 4096] (the GEMM alone; its
-    # plan at this size runs 4 decoding + 4 multiplying waves on bf16 MFMA)
+    # prefill: the same weight against X [2048, 4096] (the GEMM alone): the
+    # packed linear (at this size both operands rebased to exact fp16 rows
+    # per call, then the fp16 GEMM) and the fp16 GEMM on the weight baked once
     xp = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(1)).bfloat16().to(dev)
     pxp = packed.quantize_mx_packed(xp, tab, [-1], bs, qmax, pot)
     gp = capture(lambda: [gemm.linear_mxint8(pxp.codes, pxp.scale, pw.codes, pw.scale, bs, pxp.bias, pw.bias)
@@ -397,6 +398,9 @@ def bench_config1(args, cpu_budget_s=0.0):
                        "note": "k_gemm_mxi8 on int8 codes + scale bytes (codes decoded to bf16 in staging, K split 4)"},
             "prefill_gemm": {"M": 2048, "us": round(min(p_ms, p16_ms) * 1e3, 2), "TFLOP/s": round(p_tf, 1),
                              "packed_us": round(p_ms * 1e3, 2), "f16_us": round(p16_ms * 1e3, 2),
+                             "note": "packed_us: gemm.linear_mxint8 on the packed codes, which at this size rebases "
+                                     "both operands to exact fp16 rows per call; f16_us: the fp16 GEMM on the "
+                                     "weight baked once",
                              "mfma": "v_mfma_f32_32x32x16_f16 / _bf16 (2.5 PF dense)", "frac_of_mfma": round(p_tf / 2500.0, 4),
                              "frac_of_int8_peak": round(p_tf / 5000.0, 4)},
             "config": {"workload": "cfg1: MXINT8 bs=16 pot, X[256,4096] . W[4096,4096]^T"}}
