@@ -50,6 +50,7 @@ VH_DEV float vmap1(float v, const vh_format& f, const uint16_t* lds, int cdt) {
 struct BlockScale {
   float scale;      // the returned scale (cdt value)
   float el_scale;   // what the elements are divided by
+  float inv;        // MX_POT: 1 / el_scale when that is exact and normal, else 0
   float zp;         // AFFINE zero point
   uint32_t packed;  // packed scale byte
 };
@@ -76,6 +77,7 @@ template <int SKIND>
 VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_t* slds) {
   BlockScale r;
   r.zp = 0.0f;
+  r.inv = 0.0f;
   r.packed = 0;
   const int cdt = P.cdt;
   if (P.mode == MX_POT) {
@@ -98,6 +100,11 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
     }
     r.scale = s;
     r.el_scale = s;
+    // a power of two in [2**-126, 2**126]: x / s and x * (1 / s) are the
+    // same exact quotient, rounded alike
+    const uint32_t sb = __float_as_uint(s);
+    if (s >= 0x1p-126f && s <= 0x1p126f && (sb & 0x7fffffu) == 0u)
+      r.inv = __uint_as_float((uint32_t)(254 - (int)(sb >> 23)) << 23);
     int byte = inf ? 255 : e + P.pot_bias;
     r.packed = (uint32_t)(byte < 0 ? 0 : (byte > 254 && !inf ? 254 : byte));
     return r;
@@ -140,7 +147,7 @@ VH_DEV BlockScale block_scale(float hi, float lo, const Params& P, const uint16_
 template <int KIND>
 VH_DEV void element_code(float x, const BlockScale& bs, const Params& P, const uint16_t* lds, const uint8_t* clut,
                          float* v, uint32_t* code) {
-  float q = div_round(x, bs.el_scale, P.cdt);
+  float q = (P.mode == MX_POT && bs.inv != 0.0f) ? round_to(x * bs.inv, P.cdt) : div_round(x, bs.el_scale, P.cdt);
   if (P.mode == AFFINE) q = round_to(q + bs.zp, P.cdt);
   const uint32_t b = (P.cdt == VH_BF16 && !isnan_f(q)) ? (__float_as_uint(q) >> 16) : f2bf(q);
   if constexpr (KIND == K_STEPS) {

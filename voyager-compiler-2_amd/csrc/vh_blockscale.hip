@@ -31,10 +31,25 @@ VH_DEV void stage_code_lut(const Params& P, uint8_t* clut) {
   }
 }
 
-template <int VEC, int KIND, int SKIND>
+// LEAN >= 0: the instance for bf16 input, packed codes and scale bytes, no
+// code remap, global scale or block-major scales, in mode LEAN -- the
+// runtime fields are replaced by those constants in a local copy of the
+// parameters, so the compiler drops every branch they decide (the same
+// arithmetic: the same output).
+template <int VEC, int KIND, int SKIND, int LEAN = -1>
 __global__ void __launch_bounds__(256)
-k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, Params P,
+k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, Params Pin,
        void* __restrict__ scale_out, void* __restrict__ zp_out, void* __restrict__ codes_out) {
+  Params P = Pin;
+  if constexpr (LEAN >= 0) {
+    P.mode = LEAN;
+    P.cdt = VH_BF16;
+    P.codes_dtype = VH_U8;
+    P.scale_dtype = VH_U8;
+    P.code_lut = nullptr;
+    P.gs = nullptr;
+    P.scale_t16 = 0;
+  }
   __shared__ uint16_t lds[2 * VH_MAX_STEPS];
   __shared__ uint16_t slds[2 * VH_MAX_STEPS];
   __shared__ uint8_t clut[256];
@@ -63,8 +78,10 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
 #pragma unroll
     for (int j = 0; j < VEC; ++j) xv[j] = 0.0f;  // zero padding of a partial block
   }
-  if constexpr (KIND == K_STEPS) stage_steps(P.fmt, lds);
-  if constexpr (SKIND == K_STEPS || SKIND == K_RUNTIME) stage_steps(P.sfmt, slds);
+  // (the tables are read from the kernel argument: indexing the local copy
+  // by thread would keep it in memory)
+  if constexpr (KIND == K_STEPS) stage_steps(Pin.fmt, lds);
+  if constexpr (SKIND == K_STEPS || SKIND == K_RUNTIME) stage_steps(Pin.sfmt, slds);
   stage_code_lut(P, clut);
   float hi, lo;
   if (P.mode == AFFINE) {
@@ -156,6 +173,94 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
 #pragma unroll
     for (int j = 0; j < VEC; ++j) store_f(codes_out, P.cdt, base + j, cv[j]);
   }
+}
+
+// quantize_mx with power-of-two scales to packed integer codes and scale
+// bytes, bf16 rows (the MX-int8 form of configs 1 and 5 and the lowered
+// graphs): block_scale (MX_POT) and element_code (K_INT) for that case
+// restated without their runtime switches, NaN-propagating maxima as a
+// plain max and a NaN flag -- the same values, codes and bytes.  Thread
+// layout as k_rows<8>: eight consecutive elements, g = block / 8 lanes per
+// block.
+// IDX: the index type (32-bit when every thread index fits).
+template <typename IDX>
+__global__ void __launch_bounds__(256)
+k_mx_pot_int_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, int shift,
+                   int pot_bias, float lo, float hi, uint8_t* __restrict__ scale_out, uint8_t* __restrict__ codes_out) {
+  const IDX tpr = (IDX)(nblk * g);
+  const IDX t = (IDX)blockIdx.x * (IDX)blockDim.x + (IDX)threadIdx.x;
+  const int64_t row = (int64_t)(t / tpr);
+  const int64_t v = (int64_t)(t - (IDX)row * tpr);
+  const bool live = row < rows && v * 8 < L;
+  const int64_t base = row * L + v * 8;
+  uint4 raw = make_uint4(0u, 0u, 0u, 0u);  // zero padding of a partial block
+  if (live) raw = *(const uint4*)(x + base);
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float xv[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    xv[2 * j] = __uint_as_float(w[j] << 16);
+    xv[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+  }
+  float m = 0.0f;
+  uint32_t nan = 0u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float a = fabsf(xv[j]);
+    nan |= (uint32_t)(a != a);
+    m = fmaxf(m, a);
+  }
+  for (int off = 1; off < g; off <<= 1) {
+    m = fmaxf(m, __shfl_xor(m, off));
+    nan |= (uint32_t)__shfl_xor((int)nan, off);
+  }
+  if (row >= rows) return;
+  // the block's scale (block_scale, MX_POT, bf16)
+  float s;
+  int e = 0;
+  bool inf = false;
+  if (nan) {
+    s = 1.0f;
+  } else if (m == __builtin_inff()) {
+    s = __builtin_inff();
+    inf = true;
+  } else {
+    e = (m == 0.0f ? -126 : floor_log2(m)) - shift;
+    s = rbf(ldexpf(1.0f, e));
+    if (s == __builtin_inff()) inf = true;
+    if (!(s > 0.0f)) {
+      s = 1.0f;
+      e = 0;
+    }
+  }
+  const int64_t blk = v / g;
+  if (v - blk * g == 0 && blk < nblk) {
+    const int byte = inf ? 255 : e + pot_bias;
+    scale_out[row * nblk + blk] = (uint8_t)(byte < 0 ? 0 : (byte > 254 && !inf ? 254 : byte));
+  }
+  if (!live) return;
+  // 1 / s exactly when s is a normal power of two: x * (1 / s) is x / s
+  const uint32_t sb = __float_as_uint(s);
+  const bool exact = s >= 0x1p-126f && s <= 0x1p126f && (sb & 0x7fffffu) == 0u;
+  const float inv = __uint_as_float((uint32_t)(254 - (int)(sb >> 23)) << 23);
+  float q[8];
+  if (exact) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = rbf(xv[j] * inv);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = div_bf16(xv[j], s);
+  }
+  uint32_t c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float r = fminf(fmaxf(rintf(q[j]), lo), hi);
+    c[j] = q[j] != q[j] ? 0u : ((uint32_t)(int32_t)r & 0xffu);
+  }
+  uint2 pk;
+  pk.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+  pk.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+  *(uint2*)(codes_out + base) = pk;
 }
 
 // One thread per (outer, block, inner) column.
@@ -254,15 +359,33 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
     const int64_t threads = outer * nblk * g;
     const int64_t blocks = (threads + 255) / 256;
     VH_REQUIRE(blocks < (1ll << 31), "%s: tensor too large", what);
-    dispatch_kind(P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE, [&](auto kind) {
-      constexpr int K = decltype(kind)::value;
-      return dispatch_scale(P, [&](auto skind) {
-        constexpr int S = decltype(skind)::value;
-        hipLaunchKernelGGL((k_rows<8, K, S>), dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P,
-                           scale_out, zp_out, codes_out);
-        return 0;
+    // the packed forms the configs and lowered graphs run take a lean instance
+    const bool lean = P.mode != AFFINE && P.cdt == VH_BF16 && P.codes_dtype == VH_U8 && P.scale_dtype == VH_U8 &&
+                      !P.code_lut && !P.gs && !P.scale_t16 && codes_out && P.has_fmt;
+    const int k0 = P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE;
+    if (lean && P.mode == MX_POT && k0 == K_INT && !P.has_sfmt) {
+      if (blocks * 256 < (1ll << 31))
+        hipLaunchKernelGGL(k_mx_pot_int_rows8<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                           (const uint16_t*)x, outer, L, nblk, g, P.shift, P.pot_bias, (float)P.fmt.p0,
+                           (float)P.fmt.p1, (uint8_t*)scale_out, (uint8_t*)codes_out);
+      else
+        hipLaunchKernelGGL(k_mx_pot_int_rows8<int64_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                           (const uint16_t*)x, outer, L, nblk, g, P.shift, P.pot_bias, (float)P.fmt.p0,
+                           (float)P.fmt.p1, (uint8_t*)scale_out, (uint8_t*)codes_out);
+    } else if (lean && P.mode == MX_SCALED && k0 == K_STEPS && P.has_sfmt && kernel_kind(&P.sfmt) == K_MINI) {
+      hipLaunchKernelGGL((k_rows<8, K_STEPS, K_MINI, MX_SCALED>), dim3((unsigned)blocks), dim3(256), 0, stream, x,
+                         outer, L, nblk, g, P, scale_out, zp_out, codes_out);
+    } else {
+      dispatch_kind(k0, [&](auto kind) {
+        constexpr int K = decltype(kind)::value;
+        return dispatch_scale(P, [&](auto skind) {
+          constexpr int S = decltype(skind)::value;
+          hipLaunchKernelGGL((k_rows<8, K, S>), dim3((unsigned)blocks), dim3(256), 0, stream, x, outer, L, nblk, g, P,
+                             scale_out, zp_out, codes_out);
+          return 0;
+        });
       });
-    });
+    }
   } else {
     const int64_t threads = outer * nblk * inner;
     const int64_t blocks = (threads + 255) / 256;
