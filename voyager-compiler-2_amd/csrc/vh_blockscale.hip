@@ -182,11 +182,14 @@ k_rows(const void* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g,
 // plain max and a NaN flag -- the same values, codes and bytes.  Thread
 // layout as k_rows<8>: eight consecutive elements, g = block / 8 lanes per
 // block.
-// IDX: the index type (32-bit when every thread index fits).
-template <typename IDX>
+// IDX: the index type (32-bit when every thread index fits).  REF: the
+// reference form instead of packed bytes -- codes as bf16 values (NaN kept,
+// -0 kept) and the scales as bf16 values, as quantized_ops.quantize_mx
+// returns them.
+template <typename IDX, bool REF>
 __global__ void __launch_bounds__(256)
 k_mx_pot_int_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, int shift,
-                   int pot_bias, float lo, float hi, uint8_t* __restrict__ scale_out, uint8_t* __restrict__ codes_out) {
+                   int pot_bias, float lo, float hi, void* __restrict__ scale_out, void* __restrict__ codes_out) {
   const IDX tpr = (IDX)(nblk * g);
   const IDX t = (IDX)blockIdx.x * (IDX)blockDim.x + (IDX)threadIdx.x;
   const int64_t row = (int64_t)(t / tpr);
@@ -236,7 +239,8 @@ k_mx_pot_int_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int6
   const int64_t blk = v / g;
   if (v - blk * g == 0 && blk < nblk) {
     const int byte = inf ? 255 : e + pot_bias;
-    scale_out[row * nblk + blk] = (uint8_t)(byte < 0 ? 0 : (byte > 254 && !inf ? 254 : byte));
+    if constexpr (REF) ((uint16_t*)scale_out)[row * nblk + blk] = (uint16_t)f2bf(s);
+    else ((uint8_t*)scale_out)[row * nblk + blk] = (uint8_t)(byte < 0 ? 0 : (byte > 254 && !inf ? 254 : byte));
   }
   if (!live) return;
   // 1 / s exactly when s is a normal power of two: x * (1 / s) is x / s
@@ -255,12 +259,18 @@ k_mx_pot_int_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int6
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float r = fminf(fmaxf(rintf(q[j]), lo), hi);
-    c[j] = q[j] != q[j] ? 0u : ((uint32_t)(int32_t)r & 0xffu);
+    if constexpr (REF) c[j] = q[j] != q[j] ? 0x7FC0u : f2bf(r);  // an integer: exact in bf16
+    else c[j] = q[j] != q[j] ? 0u : ((uint32_t)(int32_t)r & 0xffu);
   }
-  uint2 pk;
-  pk.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-  pk.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-  *(uint2*)(codes_out + base) = pk;
+  if constexpr (REF) {
+    *(uint4*)((uint16_t*)codes_out + base) =
+        make_uint4(c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16));
+  } else {
+    uint2 pk;
+    pk.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    pk.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+    *(uint2*)((uint8_t*)codes_out + base) = pk;
+  }
 }
 
 // One thread per (outer, block, inner) column.
@@ -363,15 +373,23 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
     const bool lean = P.mode != AFFINE && P.cdt == VH_BF16 && P.codes_dtype == VH_U8 && P.scale_dtype == VH_U8 &&
                       !P.code_lut && !P.gs && !P.scale_t16 && codes_out && P.has_fmt;
     const int k0 = P.has_fmt ? kernel_kind(&P.fmt) : (int)K_NONE;
-    if (lean && P.mode == MX_POT && k0 == K_INT && !P.has_sfmt) {
-      if (blocks * 256 < (1ll << 31))
-        hipLaunchKernelGGL(k_mx_pot_int_rows8<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                           (const uint16_t*)x, outer, L, nblk, g, P.shift, P.pot_bias, (float)P.fmt.p0,
-                           (float)P.fmt.p1, (uint8_t*)scale_out, (uint8_t*)codes_out);
-      else
-        hipLaunchKernelGGL(k_mx_pot_int_rows8<int64_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                           (const uint16_t*)x, outer, L, nblk, g, P.shift, P.pot_bias, (float)P.fmt.p0,
-                           (float)P.fmt.p1, (uint8_t*)scale_out, (uint8_t*)codes_out);
+    // the same with reference-form outputs (bf16 codes and scales)
+    const bool lean_ref = P.mode == MX_POT && P.cdt == VH_BF16 && P.codes_dtype == VH_BF16 &&
+                          P.scale_dtype == VH_BF16 && !P.code_lut && !P.gs && !P.scale_t16 && codes_out &&
+                          P.has_fmt && !P.has_sfmt && k0 == K_INT;
+    if ((lean && P.mode == MX_POT && k0 == K_INT && !P.has_sfmt) || lean_ref) {
+      const bool i32 = blocks * 256 < (1ll << 31);
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x, outer, L, nblk, g,
+                           P.shift, P.pot_bias, (float)P.fmt.p0, (float)P.fmt.p1, scale_out, codes_out);
+      };
+      if (lean_ref) {
+        if (i32) go(k_mx_pot_int_rows8<uint32_t, true>);
+        else go(k_mx_pot_int_rows8<int64_t, true>);
+      } else {
+        if (i32) go(k_mx_pot_int_rows8<uint32_t, false>);
+        else go(k_mx_pot_int_rows8<int64_t, false>);
+      }
     } else if (lean && P.mode == MX_SCALED && k0 == K_STEPS && P.has_sfmt && kernel_kind(&P.sfmt) == K_MINI) {
       hipLaunchKernelGGL((k_rows<8, K_STEPS, K_MINI, MX_SCALED>), dim3((unsigned)blocks), dim3(256), 0, stream, x,
                          outer, L, nblk, g, P, scale_out, zp_out, codes_out);
