@@ -273,6 +273,85 @@ k_mx_pot_int_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int6
   }
 }
 
+// quantize_mx with a minifloat scale map to packed codebook indices (a
+// table of at most 15 thresholds: the 16-level codebooks), bf16 rows:
+// block_scale (MX_SCALED, no global scale) and element_code (K_STEPS) for
+// that case restated without their runtime switches -- the same scale
+// codes and indices.  Thread layout as k_rows<8>.
+template <typename IDX>
+__global__ void __launch_bounds__(256)
+k_mx_steps_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, float quant_max,
+                 vh_format sfmt, vh_format fmt, uint8_t* __restrict__ scale_out, uint8_t* __restrict__ codes_out) {
+  __shared__ uint16_t keys[16];
+  const IDX tpr = (IDX)(nblk * g);
+  const IDX t = (IDX)blockIdx.x * (IDX)blockDim.x + (IDX)threadIdx.x;
+  const int64_t row = (int64_t)(t / tpr);
+  const int64_t v = (int64_t)(t - (IDX)row * tpr);
+  const bool live = row < rows && v * 8 < L;
+  const int64_t base = row * L + v * 8;
+  uint4 raw = make_uint4(0u, 0u, 0u, 0u);  // zero padding of a partial block
+  if (live) raw = *(const uint4*)(x + base);
+  if (threadIdx.x < 16) keys[threadIdx.x] = fmt.thr_key[threadIdx.x < fmt.nsteps ? threadIdx.x : 0];
+  __syncthreads();
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float xv[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    xv[2 * j] = __uint_as_float(w[j] << 16);
+    xv[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+  }
+  float m = 0.0f;
+  uint32_t nan = 0u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float a = fabsf(xv[j]);
+    nan |= (uint32_t)(a != a);
+    m = fmaxf(m, a);
+  }
+  for (int off = 1; off < g; off <<= 1) {
+    m = fmaxf(m, __shfl_xor(m, off));
+    nan |= (uint32_t)__shfl_xor((int)nan, off);
+  }
+  if (row >= rows) return;
+  const float hi = nan ? __uint_as_float(0x7fc00000u) : m;
+  float s = div_bf16(hi, quant_max);
+  s = rbf(fmt_value_k<K_MINI>(f2bf(s), sfmt, nullptr));
+  if (!(s > 0.0f)) s = 1.0f;
+  const int64_t blk = v / g;
+  if (v - blk * g == 0 && blk < nblk) {
+    const uint32_t b = f2bf(s);
+    scale_out[row * nblk + blk] = (uint8_t)fmt_code_k<K_MINI>(b, bf2f(b), sfmt, nullptr);
+  }
+  if (!live) return;
+  const int ns = fmt.nsteps;
+  uint32_t key[8], pos[8];
+  bool nanv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float q = div_bf16(xv[j], s);
+    const uint32_t b = !isnan_f(q) ? (__float_as_uint(q) >> 16) : f2bf(q);
+    nanv[j] = bf_isnan_bits(b);
+    key[j] = bf_key(b);
+    pos[j] = 0;
+  }
+#pragma unroll
+  for (int step = 8; step >= 1; step >>= 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int nxt = (int)pos[j] + step;
+      const bool ok = nxt <= ns && (uint32_t)keys[nxt <= ns ? nxt - 1 : 0] <= key[j];
+      pos[j] = ok ? (uint32_t)nxt : pos[j];
+    }
+  }
+  uint32_t c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c[j] = nanv[j] ? (uint32_t)fmt.nan_level : pos[j];
+  uint2 pk;
+  pk.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+  pk.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+  *(uint2*)(codes_out + base) = pk;
+}
+
 // One thread per (outer, block, inner) column.
 template <int KIND, int SKIND>
 __global__ void __launch_bounds__(256)
@@ -391,8 +470,19 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
         else go(k_mx_pot_int_rows8<int64_t, false>);
       }
     } else if (lean && P.mode == MX_SCALED && k0 == K_STEPS && P.has_sfmt && kernel_kind(&P.sfmt) == K_MINI) {
-      hipLaunchKernelGGL((k_rows<8, K_STEPS, K_MINI, MX_SCALED>), dim3((unsigned)blocks), dim3(256), 0, stream, x,
-                         outer, L, nblk, g, P, scale_out, zp_out, codes_out);
+      if (P.fmt.nsteps <= 15) {
+        if (blocks * 256 < (1ll << 31))
+          hipLaunchKernelGGL(k_mx_steps_rows8<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                             (const uint16_t*)x, outer, L, nblk, g, P.quant_max, P.sfmt, P.fmt, (uint8_t*)scale_out,
+                             (uint8_t*)codes_out);
+        else
+          hipLaunchKernelGGL(k_mx_steps_rows8<int64_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                             (const uint16_t*)x, outer, L, nblk, g, P.quant_max, P.sfmt, P.fmt, (uint8_t*)scale_out,
+                             (uint8_t*)codes_out);
+      } else {
+        hipLaunchKernelGGL((k_rows<8, K_STEPS, K_MINI, MX_SCALED>), dim3((unsigned)blocks), dim3(256), 0, stream, x,
+                           outer, L, nblk, g, P, scale_out, zp_out, codes_out);
+      }
     } else {
       dispatch_kind(k0, [&](auto kind) {
         constexpr int K = decltype(kind)::value;
