@@ -352,6 +352,54 @@ k_mx_steps_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_
   *(uint2*)(codes_out + base) = pk;
 }
 
+// The same at decode sizes, one element per lane (a block's g lanes reduce
+// it): the activation quantize ahead of the MXNF4 GEMV -- indices remapped
+// through `clut` to the GEMV's levels when given, scales as float32 values
+// (block-major [nblk][16] with t16) or packed codes.
+__global__ void __launch_bounds__(256)
+k_mx_steps_lanes(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, float quant_max,
+                 vh_format sfmt, vh_format fmt, int t16, int scale_f32, void* __restrict__ scale_out,
+                 uint8_t* __restrict__ codes_out, const uint8_t* __restrict__ code_lut) {
+  __shared__ uint16_t keys[16];
+  __shared__ uint8_t clut[256];
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = t / L;
+  const int64_t v = t - row * L;
+  const bool live = row < rows;
+  const float xv = live ? __uint_as_float((uint32_t)x[row * L + v] << 16) : 0.0f;
+  if (threadIdx.x < 16) keys[threadIdx.x] = fmt.thr_key[threadIdx.x < fmt.nsteps ? threadIdx.x : 0];
+  if (code_lut) clut[threadIdx.x] = code_lut[threadIdx.x];
+  __syncthreads();
+  float m = fabsf(xv);
+  uint32_t nan = (uint32_t)(m != m);
+  for (int off = 1; off < g; off <<= 1) {
+    m = fmaxf(m, __shfl_xor(m, off));
+    nan |= (uint32_t)__shfl_xor((int)nan, off);
+  }
+  if (!live) return;
+  const float hi = nan ? __uint_as_float(0x7fc00000u) : m;
+  float s = div_bf16(hi, quant_max);
+  s = rbf(fmt_value_k<K_MINI>(f2bf(s), sfmt, nullptr));
+  if (!(s > 0.0f)) s = 1.0f;
+  const int64_t blk = v / g;
+  if (v - blk * g == 0) {
+    const int64_t si = t16 ? blk * 16 + row : row * nblk + blk;
+    if (scale_f32) {
+      ((float*)scale_out)[si] = s;
+    } else {
+      const uint32_t b = f2bf(s);
+      ((uint8_t*)scale_out)[si] = (uint8_t)fmt_code_k<K_MINI>(b, bf2f(b), sfmt, nullptr);
+    }
+  }
+  const float q = div_bf16(xv, s);
+  const uint32_t b = !isnan_f(q) ? (__float_as_uint(q) >> 16) : f2bf(q);
+  uint32_t c;
+  if (bf_isnan_bits(b)) c = (uint32_t)fmt.nan_level;
+  else c = steps_level<8>(b, fmt.nsteps, keys);
+  if (code_lut) c = clut[c & 0xffu];
+  codes_out[row * L + v] = (uint8_t)c;
+}
+
 // One thread per (outer, block, inner) column.
 template <int KIND, int SKIND>
 __global__ void __launch_bounds__(256)
@@ -430,7 +478,18 @@ int launch(const void* x, int64_t outer, int64_t L, int64_t inner, int64_t block
   // there are eight times as many waves.
   const bool lanes_ok = inner == 1 && block <= 64 && (block & (block - 1)) == 0 && L % block == 0 &&
                         outer * L <= (1 << 18);
-  if (lanes_ok) {
+  // the decode-size activation quantize of the MXNF4 GEMV (and any small
+  // tensor of that form) takes its own kernel
+  const bool steps_lanes = lanes_ok && P.mode == MX_SCALED && P.cdt == VH_BF16 && P.codes_dtype == VH_U8 &&
+                           (P.scale_dtype == VH_F32 || P.scale_dtype == VH_U8) && !P.gs && codes_out &&
+                           P.has_fmt && kernel_kind(&P.fmt) == K_STEPS && P.fmt.nsteps <= 15 && P.has_sfmt &&
+                           kernel_kind(&P.sfmt) == K_MINI;
+  if (steps_lanes) {
+    const int64_t threads = outer * L;
+    hipLaunchKernelGGL(k_mx_steps_lanes, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                       (const uint16_t*)x, outer, L, nblk, (int)block, P.quant_max, P.sfmt, P.fmt, P.scale_t16,
+                       P.scale_dtype == VH_F32 ? 1 : 0, scale_out, (uint8_t*)codes_out, P.code_lut);
+  } else if (lanes_ok) {
     const int g = (int)block;
     const int64_t threads = outer * nblk * g;
     const int64_t blocks = (threads + 255) / 256;
