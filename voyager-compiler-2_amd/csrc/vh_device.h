@@ -74,8 +74,19 @@ VH_DEV float round_to(float f, int dtype) {
 VH_DEV bool isnan_f(float f) { return f != f; }
 
 // NaN-propagating max/min, as torch.amax / torch.amin.
-VH_DEV float nmax(float a, float b) { return isnan_f(a) ? a : (isnan_f(b) ? b : fmaxf(a, b)); }
-VH_DEV float nmin(float a, float b) { return isnan_f(a) ? a : (isnan_f(b) ? b : fminf(a, b)); }
+// (written as selects: the nested conditional compiled to branches)
+VH_DEV float nmax(float a, float b) {
+  const bool na = isnan_f(a), nb = isnan_f(b);
+  const float m = fmaxf(a, b);
+  const float n = na ? a : b;
+  return (na | nb) ? n : m;
+}
+VH_DEV float nmin(float a, float b) {
+  const bool na = isnan_f(a), nb = isnan_f(b);
+  const float m = fminf(a, b);
+  const float n = na ? a : b;
+  return (na | nb) ? n : m;
+}
 
 // RNE_bf16(RN_f32(x / s)), the result of an eager bfloat16 division.
 // x * rcp(s) is within 3 float32 ulps of RN_f32(x / s) when s and 1/s are
