@@ -84,6 +84,13 @@ VH_DEV float mx8_fq(float x, const Mx8Scale& sc) {
 
 // The fp16 operand of a fake-quantized activation; flags values that do not
 // fit fp16 (|x| > 65504).
+// The same with the overflow noted in `ovf` (one flag update per thread).
+VH_DEV _Float16 fq_half_ovf(float v, bool& ovf) {
+  const _Float16 h = (_Float16)v;
+  ovf |= __builtin_isinf((float)h) && !__builtin_isinf(v);
+  return h;
+}
+
 VH_DEV _Float16 fq_half(float v, int* flag) {
   const _Float16 h = (_Float16)v;
   if (__builtin_isinf((float)h) && !__builtin_isinf(v)) atomicOr(flag, VH_DECODE_ERR_FP16_RANGE);
@@ -153,11 +160,13 @@ k_rmsnorm_mx8(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, in
     }
     const Mx8Scale sc = mx8_scale(amax);
     f16x8 o0, o1;
+    bool ovf = false;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      o0[j] = fq_half(mx8_fq(h[j], sc), flag);
-      o1[j] = fq_half(mx8_fq(h[8 + j], sc), flag);
+      o0[j] = fq_half_ovf(mx8_fq(h[j], sc), ovf);
+      o1[j] = fq_half_ovf(mx8_fq(h[8 + j], sc), ovf);
     }
+    if (ovf) atomicOr(flag, VH_DECODE_ERR_FP16_RANGE);
     f16x8* fo = (f16x8*)(fq + row * H + b * 16);
     fo[0] = o0;
     fo[1] = o1;
