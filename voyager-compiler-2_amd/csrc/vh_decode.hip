@@ -291,13 +291,18 @@ __global__ void __launch_bounds__(256) k_quantize_mx8_f16_r(const uint16_t* __re
     if (b >= nb) continue;
     const uint32_t wv[8] = {raw[j][0].x, raw[j][0].y, raw[j][0].z, raw[j][0].w,
                             raw[j][1].x, raw[j][1].y, raw[j][1].z, raw[j][1].w};
+    // mx8_fq's division and rebased_f16 with the block's choices made once
+    // (a scale that is not a power of two is infinite: x / inf is x * 0)
+    const bool p2 = sc[j].pow2;
+    const int d = sc[j].e - E;
+    const bool keep = d >= F16_FLUSH;
     f16x8 o[2];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const float xv = bf2f((i & 1) ? wv[i >> 1] >> 16 : wv[i >> 1] & 0xffffu);
-      float q = rbf(sc[j].pow2 ? ldexpf(xv, -sc[j].e) : xv / sc[j].s);
-      if (!isnan_f(q)) q = fminf(fmaxf(rintf(q), -128.0f), 127.0f);
-      o[i >> 3][i & 7] = rebased_f16(q, sc[j].e, sc[j].pow2, sc[j].s, E);
+      float q = rbf(p2 ? ldexpf(xv, -sc[j].e) : xv * 0.0f);
+      q = isnan_f(q) ? q : fminf(fmaxf(rintf(q), -128.0f), 127.0f);
+      o[i >> 3][i & 7] = (_Float16)(p2 ? (keep ? ldexpf(q, d) : q * 0.0f) : q * sc[j].s);
     }
     f16x8* dst = (f16x8*)(out + row * K + (int64_t)b * 16);
     dst[0] = o[0];
