@@ -70,6 +70,34 @@ def test_mx_edge_blocks(block):
         assert_same_bits(gc, ec, f"{dtype} codes")
 
 
+@pytest.mark.parametrize("dtype", ["lut4_to_int6", "lut3_to_int4", "lut2_to_int3"])
+@pytest.mark.parametrize("rows,L", [(1, 4096), (16, 1024), (10, 640), (512, 1024)])
+def test_mx_index_packed_edge_blocks(dtype, rows, L):
+    """Packed codebook indices and E5M3 scale bytes -- the decode-size lane
+    kernel up to 2**18 elements, the eight-per-thread row kernel beyond --
+    for codebooks of 16, 8 and 4 levels (15, 7 and 3 thresholds: the key
+    table is padded past them), on blocks of zeros, NaN, +-inf, subnormals
+    and huge values among random ones of a wide range: the oracle's indices
+    and scales bit for bit."""
+    from voyager_amd import packed
+
+    vt = T.quantization_map(dtype)
+    index, entries, mid = T.codebook_index_table(vt)
+    qmax = float(entries.abs().max())
+    stab = T.quantization_map("fp8_e5m3")
+    g = torch.Generator().manual_seed(rows * L)
+    x = torch.randn(rows, L, generator=g) * torch.exp(torch.randn(rows, L, generator=g) * 2)
+    e = _edge_blocks(64).float()
+    nb = min(e.shape[0], L // 64)
+    x[0, :nb * 64] = e[:nb].reshape(-1)
+    x[-1, L - nb * 64:] = e[:nb].flip(0).reshape(-1)
+    x = x.bfloat16()
+    es, ec = O.quantize_mx(x, index, [-1], 64, qmax, False, stab)
+    p = packed.quantize_mx_packed(x.cuda(), index.cuda(), [-1], 64, qmax, False, stab.cuda())
+    assert torch.equal(p.codes.cpu().to(torch.int64), ec.to(torch.int64)), f"{dtype} indices"
+    assert_same_bits(packed.unpack_mx_scale(p), es, f"{dtype} scales")
+
+
 def test_mxnf4_cfg3_shapes():
     vt = T.quantization_map("lut4_to_int6")
     index, entries, mid = T.codebook_index_table(vt)

@@ -205,18 +205,13 @@ k_mx_pot_int_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int6
     xv[2 * j] = __uint_as_float(w[j] << 16);
     xv[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
   }
-  float m = 0.0f;
-  uint32_t nan = 0u;
+  // the block's amax over its g lanes (NaN-propagating, as one key)
+  uint32_t mk = 0u;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float a = fabsf(xv[j]);
-    nan |= (uint32_t)(a != a);
-    m = fmaxf(m, a);
-  }
-  for (int off = 1; off < g; off <<= 1) {
-    m = fmaxf(m, __shfl_xor(m, off));
-    nan |= (uint32_t)__shfl_xor((int)nan, off);
-  }
+  for (int j = 0; j < 8; ++j) mk = umax32(mk, amax_key(xv[j]));
+  mk = group_umax_rt(mk, g);
+  const uint32_t nan = mk == 0xFFFFFFFFu;
+  const float m = __uint_as_float(mk);
   if (row >= rows) return;
   // the block's scale (block_scale, MX_POT, bf16)
   float s;
@@ -291,7 +286,8 @@ k_mx_steps_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_
   const int64_t base = row * L + v * 8;
   uint4 raw = make_uint4(0u, 0u, 0u, 0u);  // zero padding of a partial block
   if (live) raw = *(const uint4*)(x + base);
-  if (threadIdx.x < 16) keys[threadIdx.x] = fmt.thr_key[threadIdx.x < fmt.nsteps ? threadIdx.x : 0];
+  // the thresholds, padded with 0xFFFF (steps_level_padded)
+  if (threadIdx.x < 16) keys[threadIdx.x] = threadIdx.x < fmt.nsteps ? fmt.thr_key[threadIdx.x] : 0xFFFFu;
   __syncthreads();
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
   float xv[8];
@@ -300,18 +296,13 @@ k_mx_steps_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_
     xv[2 * j] = __uint_as_float(w[j] << 16);
     xv[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
   }
-  float m = 0.0f;
-  uint32_t nan = 0u;
+  // the block's amax over its g lanes (NaN-propagating, as one key)
+  uint32_t mk = 0u;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float a = fabsf(xv[j]);
-    nan |= (uint32_t)(a != a);
-    m = fmaxf(m, a);
-  }
-  for (int off = 1; off < g; off <<= 1) {
-    m = fmaxf(m, __shfl_xor(m, off));
-    nan |= (uint32_t)__shfl_xor((int)nan, off);
-  }
+  for (int j = 0; j < 8; ++j) mk = umax32(mk, amax_key(xv[j]));
+  mk = group_umax_rt(mk, g);
+  const uint32_t nan = mk == 0xFFFFFFFFu;
+  const float m = __uint_as_float(mk);
   if (row >= rows) return;
   const float hi = nan ? __uint_as_float(0x7fc00000u) : m;
   float s = div_bf16(hi, quant_max);
@@ -323,25 +314,21 @@ k_mx_steps_rows8(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_
     scale_out[row * nblk + blk] = (uint8_t)fmt_code_k<K_MINI>(b, bf2f(b), sfmt, nullptr);
   }
   if (!live) return;
-  const int ns = fmt.nsteps;
   uint32_t key[8], pos[8];
   bool nanv[8];
+  uint32_t bq[8];
+  div_bf16_bits_n(xv, s, bq);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float q = div_bf16(xv[j], s);
-    const uint32_t b = !isnan_f(q) ? (__float_as_uint(q) >> 16) : f2bf(q);
-    nanv[j] = bf_isnan_bits(b);
-    key[j] = bf_key(b);
+    nanv[j] = bf_isnan_bits(bq[j]);
+    key[j] = bf_key(bq[j]);
     pos[j] = 0;
   }
+  // steps_level_padded for the eight elements, stepping together
 #pragma unroll
   for (int step = 8; step >= 1; step >>= 1) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int nxt = (int)pos[j] + step;
-      const bool ok = nxt <= ns && (uint32_t)keys[nxt <= ns ? nxt - 1 : 0] <= key[j];
-      pos[j] = ok ? (uint32_t)nxt : pos[j];
-    }
+    for (int j = 0; j < 8; ++j) pos[j] = (uint32_t)keys[pos[j] + step - 1] <= key[j] ? pos[j] + step : pos[j];
   }
   uint32_t c[8];
 #pragma unroll
@@ -360,30 +347,41 @@ __global__ void __launch_bounds__(256)
 k_mx_steps_lanes(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_t nblk, int g, float quant_max,
                  vh_format sfmt, vh_format fmt, int t16, int scale_f32, void* __restrict__ scale_out,
                  uint8_t* __restrict__ codes_out, const uint8_t* __restrict__ code_lut) {
-  __shared__ uint16_t keys[16];
+  __shared__ __attribute__((aligned(4))) uint16_t keys[16];
   __shared__ uint8_t clut[256];
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = t / L;
-  const int64_t v = t - row * L;
-  const bool live = row < rows;
-  const float xv = live ? __uint_as_float((uint32_t)x[row * L + v] << 16) : 0.0f;
-  if (threadIdx.x < 16) keys[threadIdx.x] = fmt.thr_key[threadIdx.x < fmt.nsteps ? threadIdx.x : 0];
-  if (code_lut) clut[threadIdx.x] = code_lut[threadIdx.x];
+  // rows * L <= 2**18 (the launcher's bound): 32-bit indices; g divides L
+  // and is a power of two, so the blocks are aligned groups of g lanes
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t Lu = (uint32_t)L;
+  const bool live = t < (uint32_t)(rows * L);
+  const uint32_t row = t / Lu, v = t - row * Lu;
+  // The loads go out together, before any wait: the element (index 0 past
+  // the end), the thresholds through the scalar cache (spread over lanes
+  // 0..7, padded with 0xFFFF for steps_level_padded) and the code map.
+  const uint32_t xb = x[live ? t : 0u];
+  const uint32_t* kw = (const uint32_t*)fmt.thr_key;
+  const int lane = (int)(threadIdx.x & 63u);
+  uint32_t kv = 0u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kv = lane == i ? kw[i] : kv;
+  const int ns = fmt.nsteps;
+  kv = (2 * lane < ns ? kv & 0xffffu : 0xffffu) | (2 * lane + 1 < ns ? kv & 0xffff0000u : 0xffff0000u);
+  uint32_t cl = 0u;
+  if (code_lut) cl = code_lut[threadIdx.x];
+  if (threadIdx.x < 8) *(uint32_t*)&keys[2 * threadIdx.x] = kv;
+  if (code_lut) clut[threadIdx.x] = (uint8_t)cl;
+  const float xv = live ? __uint_as_float(xb << 16) : 0.0f;
+  // the block's amax (NaN-propagating) across its g lanes
+  const uint32_t mk = group_umax_rt(amax_key(xv), g);
   __syncthreads();
-  float m = fabsf(xv);
-  uint32_t nan = (uint32_t)(m != m);
-  for (int off = 1; off < g; off <<= 1) {
-    m = fmaxf(m, __shfl_xor(m, off));
-    nan |= (uint32_t)__shfl_xor((int)nan, off);
-  }
   if (!live) return;
-  const float hi = nan ? __uint_as_float(0x7fc00000u) : m;
+  const float hi = mk == 0xFFFFFFFFu ? __uint_as_float(0x7fc00000u) : __uint_as_float(mk);
   float s = div_bf16(hi, quant_max);
   s = rbf(fmt_value_k<K_MINI>(f2bf(s), sfmt, nullptr));
   if (!(s > 0.0f)) s = 1.0f;
-  const int64_t blk = v / g;
-  if (v - blk * g == 0) {
-    const int64_t si = t16 ? blk * 16 + row : row * nblk + blk;
+  const uint32_t blk = v >> __builtin_ctz((unsigned)g);
+  if ((v & ((uint32_t)g - 1u)) == 0u) {
+    const uint32_t si = t16 ? blk * 16u + row : row * (uint32_t)nblk + blk;
     if (scale_f32) {
       ((float*)scale_out)[si] = s;
     } else {
@@ -395,9 +393,9 @@ k_mx_steps_lanes(const uint16_t* __restrict__ x, int64_t rows, int64_t L, int64_
   const uint32_t b = !isnan_f(q) ? (__float_as_uint(q) >> 16) : f2bf(q);
   uint32_t c;
   if (bf_isnan_bits(b)) c = (uint32_t)fmt.nan_level;
-  else c = steps_level<8>(b, fmt.nsteps, keys);
+  else c = steps_level_padded<8>(bf_key(b), keys);
   if (code_lut) c = clut[c & 0xffu];
-  codes_out[row * L + v] = (uint8_t)c;
+  codes_out[t] = (uint8_t)c;
 }
 
 // One thread per (outer, block, inner) column.

@@ -104,6 +104,77 @@ VH_DEV float div_bf16(float x, float s) {
   return bf2f(f2bf(x / s));
 }
 
+// The bfloat16 bits of div_bf16(x[j], s) for N (even) values, rounded by the
+// hardware converter (v_cvt_pk_bf16_f32: half to even, denormals kept):
+// f2bf(div_bf16(x[j], s)) for every non-NaN result; a NaN result is some NaN
+// pattern, which callers test with bf_isnan_bits.
+template <int N>
+VH_DEV void div_bf16_bits_n(const float (&x)[N], float s, uint32_t (&b)[N]) {
+  static_assert(N % 2 == 0, "pairs");
+  const float as = fabsf(s);
+  const bool normal = as >= 0x1p-126f && as <= 0x1p126f;
+  const float r = __builtin_amdgcn_rcpf(s);
+  uint32_t slow = 0u;
+#pragma unroll
+  for (int j = 0; j < N; j += 2) {
+    const float p0 = x[j] * r, p1 = x[j + 1] * r;
+    const uint32_t pk = f2bf2_hw(p0, p1);
+    b[j] = pk & 0xffffu;
+    b[j + 1] = pk >> 16;
+    slow |= (uint32_t)(!normal || ((__float_as_uint(p0) - 0x7FFCu) & 0xFFFFu) <= 8u) << j;
+    slow |= (uint32_t)(!normal || ((__float_as_uint(p1) - 0x7FFCu) & 0xFFFFu) <= 8u) << (j + 1);
+  }
+  if (slow) {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if ((slow >> j) & 1u) b[j] = f2bf(x[j] / s);
+  }
+}
+
+// The unsigned maximum over aligned groups of G consecutive lanes (G a power
+// of two up to 64), delivered to every lane of the group: DPP moves inside
+// rows of 16 lanes (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror,
+// row_mirror: each step pairs every lane with one of the other half of its
+// 2^k group), then across rows a lane exchange (G = 32) or the four row
+// maxima through scalar registers (G = 64).  Register moves only, with no
+// LDS round trip; every lane of the wave must be active.
+VH_DEV uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+template <int G>
+VH_DEV uint32_t group_umax(uint32_t v) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "group size");
+  if constexpr (G >= 2) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  if constexpr (G >= 4) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  if constexpr (G >= 8) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  if constexpr (G >= 16) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  if constexpr (G == 32) v = umax32(v, (uint32_t)__shfl_xor((int)v, 16));
+  if constexpr (G == 64) {
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    v = umax32(umax32(r0, r1), umax32(r2, r3));
+  }
+  return v;
+}
+
+// group_umax for a group size known only at run time (a power of two <= 64).
+VH_DEV uint32_t group_umax_rt(uint32_t v, int g) {
+  switch (g) {
+    case 64: return group_umax<64>(v);
+    case 32: return group_umax<32>(v);
+    case 16: return group_umax<16>(v);
+    case 8: return group_umax<8>(v);
+    case 4: return group_umax<4>(v);
+    case 2: return group_umax<2>(v);
+    default: return v;
+  }
+}
+
+// A block maximum of |x| with torch.amax's NaN propagation, as one unsigned
+// key: the bits of |x| (ordered as the values, +inf included), NaN above
+// them all.
+VH_DEV uint32_t amax_key(float a) { return a != a ? 0xFFFFFFFFu : __float_as_uint(fabsf(a)); }
+
 // The eager result dtype's rounding of x / s.
 VH_DEV float div_round(float x, float s, int dtype) {
   if (dtype == VH_BF16) return div_bf16(x, s);
@@ -227,20 +298,34 @@ VH_DEV float fmt_posit(float x, const vh_format& f) {
 // staged in LDS by the kernel: `keys` holds f.thr_key).  NaN inputs are
 // handled by the caller (they take nan_out / nan_level).
 // TOP: the first halving's step (32 covers up to 63 thresholds; a table
-// known to hold at most 2 * TOP - 1 may start lower).
+// known to hold at most 2 * TOP - 1 may start lower).  `keys` must hold
+// 2 * TOP - 1 readable entries (those past nsteps are read and ignored).
 template <int TOP = 32>
 VH_DEV uint32_t steps_level(uint32_t b, int nsteps, const uint16_t* keys) {
   // Branch-free search: six halvings cover up to 63 thresholds, so the
-  // lookups of a thread's elements can overlap.
+  // lookups of a thread's elements can overlap.  The key is read before the
+  // bound is tested (nxt - 1 <= 2 * TOP - 2): with the test first, each read
+  // became a branch of its own, waited on alone.
   const uint32_t k = bf_key(b);
   int pos = 0;
 #pragma unroll
   for (int step = TOP; step >= 1; step >>= 1) {
     const int nxt = pos + step;
-    const bool ok = nxt <= nsteps && (uint32_t)keys[nxt <= nsteps ? nxt - 1 : 0] <= k;
+    const bool ok = (nxt <= nsteps) & ((uint32_t)keys[nxt - 1] <= k);
     pos = ok ? nxt : pos;
   }
   return (uint32_t)pos;
+}
+
+// steps_level over a key table padded with 0xFFFF from nsteps on (at least
+// 2 * TOP - 1 entries): the same level for every non-NaN input, whose key is
+// below 0xFF81 (only a NaN's key reaches a padded entry), with no bound test.
+template <int TOP>
+VH_DEV uint32_t steps_level_padded(uint32_t k, const uint16_t* keys) {
+  uint32_t pos = 0;
+#pragma unroll
+  for (int step = TOP; step >= 1; step >>= 1) pos = (uint32_t)keys[pos + step - 1] <= k ? pos + step : pos;
+  return pos;
 }
 
 // Stage a STEPS format's keys and entries in LDS (2 * VH_MAX_STEPS halves).

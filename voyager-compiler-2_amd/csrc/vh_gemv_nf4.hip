@@ -204,20 +204,30 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
       asm volatile("" : "+v"(st.sx)::"memory");
       *(vh_u32x4*)&s_sx[wave][lane * 16] = st.sx;
     }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      // the block's registers pass through here, after every load issued
-      // before this round: its arithmetic cannot rise above them (left
-      // alone, the scheduler interleaves loads with arithmetic and a round
-      // waits on several memory latencies in turn)
+    // Three stages per block, software-pipelined over the round: (a) its
+    // registers pass through an empty asm, after every load issued before
+    // this round, so its arithmetic cannot rise above them (left alone, the
+    // scheduler interleaves loads with arithmetic and a round waits on
+    // several memory latencies in turn), and its LDS reads go out; (b) the
+    // nibble lookup and the MFMA; (c) the scale products.  (a) runs one
+    // block ahead of (b) and (c) one behind, so each block's LDS and MFMA
+    // latencies pass while the neighbouring blocks compute; the
+    // accumulation order is the block order.
+    float swv[TPW][UNROLL];
+    vh_u32x4 sxq[UNROLL];
+    i32x4 dd[TPW][UNROLL];
+    auto stage_a = [&](int u) __attribute__((always_inline)) {
       if constexpr (TPW == 1)
-        asm volatile("" : "+v"(st.w[0][u]), "+v"(st.x[u]), "+v"(st.sw[0][u])::"memory");
+        asm volatile("" : "+v"(st.w[0][u]), "+v"(st.x[u]), "+v"(st.sw[0][u]));
       else
         asm volatile("" : "+v"(st.w[0][u]), "+v"(st.w[1][u]), "+v"(st.x[u]), "+v"(st.sw[0][u]),
-                     "+v"(st.sw[1][u])::"memory");
+                     "+v"(st.sw[1][u]));
+      if constexpr (MR == 4) sxq[u] = *(const vh_u32x4*)&s_sx[wave][u * 64 + mrow * 4];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) swv[t][u] = s_scale[st.sw[t][u]];
+    };
+    auto stage_b = [&](int u) __attribute__((always_inline)) {
       const i32x4 xa = {(int)st.x[u].x, (int)st.x[u].y, (int)st.x[u].z, (int)st.x[u].w};
-      vh_u32x4 sxq;
-      if constexpr (MR == 4) sxq = *(const vh_u32x4*)&s_sx[wave][u * 64 + mrow * 4];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         i32x4 wl;
@@ -225,21 +235,34 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
         wl[1] = (int)lut_lo(st.w[t][u].y, base, lv);
         wl[2] = (int)lut_hi(st.w[t][u].x, base, lv);
         wl[3] = (int)lut_hi(st.w[t][u].y, base, lv);
-        i32x4 d = {0, 0, 0, 0};
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
-        // past the range: zero dot products and a zero activation scale; the
-        // decoded scale of a zero byte is finite
-        const float swv = s_scale[st.sw[t][u]];
+        const i32x4 z = {0, 0, 0, 0};
+        dd[t][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, z, 0, 0, 0);
+      }
+    };
+    auto stage_c = [&](int u) __attribute__((always_inline)) {
+      // past the range: zero dot products and a zero activation scale; the
+      // decoded scale of a zero byte is finite
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const i32x4 d = dd[t][u];
         if constexpr (MR == 1) {
-          acc[t][0] = fmaf((float)d[0], sx1[u] * swv, acc[t][0]);
+          acc[t][0] = fmaf((float)d[0], sx1[u] * swv[t][u], acc[t][0]);
         } else {
-          acc[t][0] = fmaf((float)d[0], __uint_as_float(sxq.x) * swv, acc[t][0]);
-          acc[t][1] = fmaf((float)d[1], __uint_as_float(sxq.y) * swv, acc[t][1]);
-          acc[t][2] = fmaf((float)d[2], __uint_as_float(sxq.z) * swv, acc[t][2]);
-          acc[t][3] = fmaf((float)d[3], __uint_as_float(sxq.w) * swv, acc[t][3]);
+          acc[t][0] = fmaf((float)d[0], __uint_as_float(sxq[u].x) * swv[t][u], acc[t][0]);
+          acc[t][1] = fmaf((float)d[1], __uint_as_float(sxq[u].y) * swv[t][u], acc[t][1]);
+          acc[t][2] = fmaf((float)d[2], __uint_as_float(sxq[u].z) * swv[t][u], acc[t][2]);
+          acc[t][3] = fmaf((float)d[3], __uint_as_float(sxq[u].w) * swv[t][u], acc[t][3]);
         }
       }
+    };
+    stage_a(0);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (u + 1 < UNROLL) stage_a(u + 1);
+      stage_b(u);
+      if (u > 0) stage_c(u - 1);
     }
+    stage_c(UNROLL - 1);
   };
   Set s[2];
   // Two register sets, double-buffered: round r + 2 is loaded into the set
@@ -282,8 +305,10 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
 
 // M == 1 with the activation row quantized here: quantize_mx(x, index, [-1],
 // 64, quant_max, scale map) (ops/quantized.py:1070-1115) of the blocks this
-// wave multiplies, by the block-scale and element-code functions of the
-// quantize kernels, so its levels and scales are those of the two-launch
+// wave multiplies, by the arithmetic of the quantize kernels' restatement
+// for this case (k_mx_steps_rows8: div_bf16, fmt_value_k and the same
+// threshold search, the lane's searches stepping together, with no
+// per-element branch), so its levels and scales are those of the two-launch
 // path bit for bit.  A round's UNROLL blocks are one contiguous load of
 // UNROLL * 64 bfloat16 values, UNROLL consecutive elements per lane (a
 // block's amax is a butterfly over its 64 / UNROLL lanes); the int6 levels
@@ -315,16 +340,6 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
   const int64_t n = tile * 16 + (lane & 15);
   uint32_t base;
   asm volatile("v_mov_b32 %0, 0x3020100" : "=v"(base));
-  // quantize_mx's parameters, the mode and dtype fixed here so that the
-  // block scale's other branches fold away
-  Params P;
-  P.mode = MX_SCALED;
-  P.cdt = VH_BF16;
-  P.quant_max = quant_max;
-  P.gs = nullptr;
-  P.gs_dtype = VH_F32;
-  P.has_sfmt = 1;
-  P.sfmt = xsfmt;
 
   // buffers from the round's first block to the range end (past it: zeros)
   const uint32_t woff = (uint32_t)lane * 8u, wsoff = (uint32_t)(lane & 15), xoff = (uint32_t)lane * (2u * EPL);
@@ -359,25 +374,42 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
       xv[2 * j] = bf2f(st.x[j] & 0xffffu);
       xv[2 * j + 1] = bf2f(st.x[j] >> 16);
     }
-    float hi = fabsf(xv[0]);
+    // the block's scale (block_scale, MX_SCALED, bf16, no global scale):
+    // the NaN-propagating amax over the block's LPB lanes as one key
+    uint32_t mk = 0u;
 #pragma unroll
-    for (int j = 1; j < EPL; ++j) hi = nmax(hi, fabsf(xv[j]));
+    for (int j = 0; j < EPL; ++j) mk = umax32(mk, amax_key(xv[j]));
+    mk = group_umax<LPB>(mk);
+    float sc = div_bf16(mk == 0xFFFFFFFFu ? __uint_as_float(0x7fc00000u) : __uint_as_float(mk), quant_max);
+    sc = rbf(fmt_value_k<K_MINI>(f2bf(sc), xsfmt, nullptr));
+    if (!(sc > 0.0f)) sc = 1.0f;
+    // element codes as element_code<K_STEPS> forms them (levels <= 15):
+    // q = bf16(x / sc) as div_bf16 forms it, rounded by the hardware
+    // converter (a NaN is flagged below, so its payload does not matter)
+    uint32_t bq[EPL];
+    div_bf16_bits_n(xv, sc, bq);
+    uint32_t key[EPL], pos[EPL];
+    bool nanv[EPL];
 #pragma unroll
-    for (int off = 1; off < LPB; off <<= 1) hi = nmax(hi, __shfl_xor(hi, off));
-    const BlockScale bs = block_scale<K_MINI>(hi, 0.0f, P, nullptr);
-    // element codes as element_code<K_STEPS> forms them (levels <= 15)
+    for (int j = 0; j < EPL; ++j) {
+      nanv[j] = bf_isnan_bits(bq[j]);
+      key[j] = bf_key(bq[j]);
+      pos[j] = 0u;
+    }
+    // the level: steps_level_padded (s_keys is padded with 0xFFFF past
+    // nsteps), the lane's searches stepping together
+#pragma unroll
+    for (int step = 8; step >= 1; step >>= 1) {
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        pos[j] = (uint32_t)s_keys[pos[j] + step - 1] <= key[j] ? pos[j] + step : pos[j];
+    }
     uint32_t lvw[EPL / 4];
 #pragma unroll
     for (int q = 0; q < EPL / 4; ++q) {
       uint32_t c = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float qv = div_round(xv[4 * q + j], bs.el_scale, VH_BF16);
-        const uint32_t bq = isnan_f(qv) ? f2bf(qv) : (__float_as_uint(qv) >> 16);
-        const uint32_t lvl =
-            bf_isnan_bits(bq) ? (uint32_t)xfmt.nan_level : steps_level<8>(bq, xfmt.nsteps, s_keys);
-        c |= lvl << (8 * j);
-      }
+      for (int j = 0; j < 4; ++j) c |= (nanv[4 * q + j] ? (uint32_t)xfmt.nan_level : pos[4 * q + j]) << (8 * j);
       lvw[q] = lut_lo(c, base, lv);
     }
     if constexpr (EPL == 8) *(vh_u32x2*)&s_xq[wave][8 * lane] = vh_u32x2{lvw[0], lvw[1]};
@@ -386,23 +418,37 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
     float sxb[UNROLL];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs.scale), u * LPB));
+      const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), u * LPB));
       sxb[u] = b + u < b1 ? v : 0.0f;
     }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      asm volatile("" : "+v"(st.w[u]), "+v"(st.sw[u])::"memory");
+    // the blocks software-pipelined as in k_gemv_nf4: LDS reads one block
+    // ahead of the lookup and MFMA, the scale product one block behind
+    vh_u32x4 xq[UNROLL];
+    float swv[UNROLL];
+    int dd[UNROLL];
+    auto stage_a = [&](int u) __attribute__((always_inline)) {
+      asm volatile("" : "+v"(st.w[u]), "+v"(st.sw[u]));
+      xq[u] = *(const vh_u32x4*)&s_xq[wave][u * 64 + 16 * (lane >> 4)];
+      swv[u] = s_scale[st.sw[u]];
+    };
+    auto stage_b = [&](int u) __attribute__((always_inline)) {
       i32x4 wl;
       wl[0] = (int)lut_lo(st.w[u].x, base, lv);
       wl[1] = (int)lut_lo(st.w[u].y, base, lv);
       wl[2] = (int)lut_hi(st.w[u].x, base, lv);
       wl[3] = (int)lut_hi(st.w[u].y, base, lv);
-      const vh_u32x4 xq = *(const vh_u32x4*)&s_xq[wave][u * 64 + 16 * (lane >> 4)];
-      const i32x4 xa = {(int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w};
-      i32x4 d = {0, 0, 0, 0};
-      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, d, 0, 0, 0);
-      acc = fmaf((float)d[0], sxb[u] * s_scale[st.sw[u]], acc);
+      const i32x4 xa = {(int)xq[u].x, (int)xq[u].y, (int)xq[u].z, (int)xq[u].w};
+      const i32x4 z = {0, 0, 0, 0};
+      dd[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, z, 0, 0, 0)[0];
+    };
+    stage_a(0);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (u + 1 < UNROLL) stage_a(u + 1);
+      stage_b(u);
+      if (u > 0) acc = fmaf((float)dd[u - 1], sxb[u - 1] * swv[u - 1], acc);
     }
+    acc = fmaf((float)dd[UNROLL - 1], sxb[UNROLL - 1] * swv[UNROLL - 1], acc);
   };
   Set s[2];
   auto chunk = [&](int c0, auto pre) __attribute__((always_inline)) {
@@ -421,11 +467,13 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
     // the first 16 thresholds (all a table of at most 16 levels uses), read
     // through the scalar cache and spread over lanes 0..7 of wave 0 (a
     // per-lane read of the argument would be a vector load, and storing it
-    // would wait for every load in flight)
+    // would wait for every load in flight); 0xFFFF past nsteps
     const uint32_t* kw = (const uint32_t*)xfmt.thr_key;
     uint32_t kv = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) kv = lane == i ? kw[i] : kv;
+    const int ns = xfmt.nsteps;
+    kv = (2 * lane < ns ? kv & 0xffffu : 0xffffu) | (2 * lane + 1 < ns ? kv & 0xffff0000u : 0xffff0000u);
     if (wave == 0 && lane < 8) *(uint32_t*)&s_keys[2 * lane] = kv;
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");

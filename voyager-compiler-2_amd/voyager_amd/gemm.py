@@ -586,12 +586,11 @@ def _nf4_fusable(x: torch.Tensor, ec, sc) -> bool:
 
 
 def _nf4_one_launch_pays(N: int, K: int) -> bool:
-    """Every 16-column tile quantizes the row again (about 1.7x the GEMV's
-    own vector work), which costs less than a second launch while the grid
-    is at most 512 tiles and each wave's K range one round of 8 blocks
-    (MI355X: 8.1-8.7 us against 10.4-10.8 at K = 4096, N <= 4096; 16.9
-    against 16.2 at N = 14336; 24.7 against 17.9 at K = 14336)."""
-    return N <= 8192 and K <= 4096
+    """Every 16-column tile quantizes the row again, which costs less than
+    a second launch while each wave's K range is at most 32 blocks (MI355X,
+    weights from HBM: 6.0-6.6 us against 8.6-9.1 at K = 4096, N <= 4096;
+    13.9 against 14.5 at N = 14336; even, 16.4 us, at K = 14336)."""
+    return K <= 4096
 
 
 def nf4_prefill_plan(M: int, N: int, K: int, tile: int = 0, splits: int = 0) -> Tuple[int, int]:
