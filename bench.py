@@ -390,8 +390,8 @@ def bench_config1(args, cpu_budget_s=0.0):
                      "GB/s": round(gbytes / (g_ms * 1e-3) / 1e9, 1),
                      "roofline_us": round(max(flops / 2.5e15, gbytes / 8e12) * 1e6, 2),
                      "note": "the weight baked once as exact fp16 rows (code * 2**(e - E_row)), an fp16 direct-to-LDS "
-                             "GEMM (2.5 PF MFMA) on 64 x 128 tiles (128 workgroups, K unsplit) whose epilogue "
-                             "applies 2**(E_row + E_col)"},
+                             "GEMM (2.5 PF MFMA) on 64 x 64 tiles (256 workgroups of two waves, eight stages in flight, "
+                             "K unsplit) whose epilogue applies 2**(E_row + E_col)"},
             "quantize_mx": {"us": round(q_ms * 1e3, 2), "GB/s": round(qbytes / (q_ms * 1e-3) / 1e9, 1),
                             "note": "quantize_mx of X written as exact fp16 rows and their exponents"},
             "packed": {"gemm_us": round(gp_ms * 1e3, 2), "quantize_us": round(qp_ms * 1e3, 2),

@@ -329,7 +329,8 @@ int vh_gemm_plan(const vh_gemm_desc* desc, int32_t* family, int32_t* tile, int32
  * and one reduction; with splits == 1 and a 16-byte aligned y (ldy and N
  * multiples of 8 for bf16, ldy of 4 for float32) the GEMM applies the
  * exponents and the epilogue itself and `part` may be null; tile 0:
- * 128x128, 1: 64x128, 2: 128x64, 3: 256x128.  No
+ * 128x128, 1: 64x128, 2: 128x64, 3: 256x128, 4: 64x64 (two waves, eight
+ * stages in flight: the small-M tile).  No
  * reference counterpart for the operand form: it is this library's
  * small-M layout of the same values. */
 int vh_quantize_mx8_f16(const uint16_t* x, int64_t M, int64_t K, uint16_t* out, int32_t* ex, vh_stream_t stream);

@@ -619,7 +619,11 @@ def test_mx8_f16_bake_flushes_only_far_blocks(N, K):
                                                # tiles), and N % 8 != 0 through the reduction
                                                (2048, 4096, 1024, -1, 0), (256, 4096, 4096, 1, 1),
                                                (130, 264, 768, 0, 1), (33, 520, 1024, 2, 1),
-                                               (1100, 136, 512, 3, 1), (50, 260, 512, 0, 1)])
+                                               (1100, 136, 512, 3, 1), (50, 260, 512, 0, 1),
+                                               # the 64x64 small-M tile: automatic at M <= 256, ragged
+                                               # rows and tiles, its own epilogue and split
+                                               (16, 4096, 4096, -1, 0), (256, 4096, 4096, 4, 1),
+                                               (33, 520, 1024, 4, 1), (130, 264, 768, 4, 2)])
 def test_linear_mx8_f16(M, N, K, tile, splits):
     """The small-M MX-int8 linear on exact fp16 operands against the exact
     float64 product of the reference's decoded operands, bf16 and fp32
@@ -646,3 +650,21 @@ def test_linear_mx8_f16(M, N, K, tile, splits):
     # the packed path's result agrees
     old = gemm.linear_mxint8(px.codes, px.scale, pw.codes, pw.scale, 16, px.bias, pw.bias)
     assert max_rel_err(got, old) < TOL
+
+
+@pytest.mark.parametrize("M", [256, 100])
+def test_mx8_f16_small_tile_matches(M):
+    """One split: every tile accumulates each output over K in the same
+    order, so the 64x64 tile's result is the 64x128 tile's bit for bit."""
+    from voyager_amd import gemm, packed
+
+    tab = T.quantization_map("int8").cuda()
+    x = _rand((M, 4096), 43).cuda()
+    w = _rand((1024, 4096), 44, 0.02).cuda()
+    pw = packed.quantize_mx_packed(w, tab, [-1], 16, 127.0, True)
+    bw = gemm.bake_mx8_f16(pw.codes.view(torch.int8), pw.scale, pw.bias)
+    x16, ex = gemm.quantize_mx8_f16(x)
+    a = gemm.linear_mx8_f16(x16, ex, bw, tile=1, splits=1)
+    b = gemm.linear_mx8_f16(x16, ex, bw, tile=4, splits=1)
+    assert torch.equal(a, b)
+    assert gemm.mx8_f16_plan(M, 4096, 4096)[0] == 4

@@ -1125,9 +1125,13 @@ __device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t lds, int voff)
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 
+// Waves per SIMD the direct-to-LDS kernel asks for: one per four waves of
+// its workgroup (at least one).
+constexpr int f8dl_wpe(int nw) { return nw >= 4 ? nw / 4 : 1; }
+
 template <int BM, int BN, int NS, int KS, int WM, int WN, int OP, bool BIAS>
-__global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
-    __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) k_gemm_f8dl(GemmArgs g) {
+__global__ void __launch_bounds__(WM * WN * 64, f8dl_wpe(WM * WN))
+    __attribute__((amdgpu_waves_per_eu(f8dl_wpe(WM * WN), f8dl_wpe(WM * WN)))) k_gemm_f8dl(GemmArgs g) {
   constexpr int P = KS / 64;                 // MFMA steps per stage
   constexpr int CPR = KS / 16;               // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;              // rows per DMA instruction
@@ -1143,6 +1147,7 @@ __global__ void __launch_bounds__(WM * WN * 64, WM * WN / 4)
   constexpr bool BF = OP == OP_BF16 || OP == OP_F16X;
   static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0 && TM >= 2 && TM % 2 == 0 && TN >= 1,
                 "DMA blocks must divide among the waves");
+  static_assert((NW * RPI) % 16 == 0, "a wave's DMA blocks share row % 16 (the swizzle)");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
@@ -2474,6 +2479,7 @@ extern "C" int vh_gemm_mx8_f16(const uint16_t* x, const int32_t* ex, const uint1
     case 1: rc = launch_f8dl<64, 128, 4, 128, 1, 4, OP_F16X>(g, splits, st); break;
     case 2: rc = launch_f8dl<128, 64, 4, 128, 2, 2, OP_F16X>(g, splits, st); break;
     case 3: rc = launch_f8dl<256, 128, 3, 128, 2, 2, OP_F16X>(g, splits, st); break;
+    case 4: rc = launch_f8dl<64, 64, 8, 128, 1, 2, OP_F16X>(g, splits, st); break;
     default: rc = launch_f8dl<128, 128, 4, 128, 2, 2, OP_F16X>(g, splits, st); break;
   }
   if (rc || direct) return rc;

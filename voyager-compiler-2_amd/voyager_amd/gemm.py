@@ -427,15 +427,21 @@ def quantize_mx8_f16(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
 
 def mx8_f16_plan(M: int, N: int, K: int) -> Tuple[int, int]:
     """(tile, splits) of ``linear_mx8_f16``.  Measured on MI355X at K = N =
-    4096, one split storing through the GEMM's own epilogue: M = 2048 on
-    256x128 tiles 56.0 us (1226 TFLOP/s; 128x128 65.0; 256x128 in two
-    splits plus the reduction 92.5); M = 256 on 64x128 tiles 18.9 us (in two
-    splits plus the reduction 18.1, in four 26.2; 128x64 18.9; 128x128 25.1,
-    in four splits 21.8; 256x128 in eight 30.0).  Below 1024 rows: 64x128, K
-    split until the grid reaches 128 workgroups (each split at least 512
-    elements); from 1024: 256x128."""
+    4096, one split storing through the GEMM's own epilogue unless stated:
+    M = 2048 on 256x128 tiles 56.0 us (1226 TFLOP/s; 128x128 65.0; 256x128
+    in two splits plus the reduction 92.5); M = 256 on 64x64 tiles (two
+    waves, eight stages) 15.8 us (64x128 18.9; 64x64 in two splits plus the
+    reduction 25.9); M = 128 / 64 / 16 on 64x64 tiles in two splits 15.1 /
+    14.7 / 12.5 us (unsplit 15.7 / 15.7 / 15.5; 64x128 18.7 / 18.6 / 16.8);
+    M = 512 on 64x128 tiles 21.5 us (64x64 30.1).  So: 64x64 while its grid
+    is at most 256 workgroups, in two K splits while that grid is at most
+    128; then 64x128 below 1024 rows (K split until the grid reaches 128
+    workgroups, each split at least 512 elements); from 1024, 256x128."""
     if M >= 1024:
         return 3, 1
+    t64 = -(-M // 64) * -(-N // 64)
+    if t64 <= 256:
+        return 4, (2 if t64 <= 128 and K % (2 * 512) == 0 else 1)
     tiles = -(-M // 64) * -(-N // 128)
     splits = 1
     while tiles * splits < 128 and K % (splits * 2 * 512) == 0 and splits < 8:
