@@ -214,9 +214,11 @@ VH_DEV _Float16 rebased_f16(float code, int e, bool finite, float s, int E) {
   return (_Float16)(d >= F16_FLUSH ? ldexpf(code, d) : code * 0.0f);
 }
 
+// The maximum of v over a 256-thread workgroup (every thread calls it):
+// each wave's by DPP moves (signed order as unsigned with the sign bit
+// flipped), then the four through LDS.
 VH_DEV int block_max_int(int v, int* s_red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
+  v = (int)(group_umax<64>((uint32_t)v ^ 0x80000000u) ^ 0x80000000u);
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
   __syncthreads();
   const int r = max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3]));
