@@ -119,21 +119,10 @@ k_rmsnorm_mx8(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, in
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * H;
   const int64_t nb = H / 16;
-  // A row of at most 256 blocks (H <= 4096) is one block per thread: its x
-  // block and weight block are loaded together at the start and kept in
-  // registers, so the weight's latency passes under the row's reduction.
-  const bool one = nb <= 256;
-  uint4 x0 = make_uint4(0u, 0u, 0u, 0u), x1 = x0, w0 = x0, w1 = x0;
-  if (one && threadIdx.x < nb) {
-    const uint4* p = (const uint4*)(xr + threadIdx.x * 16);
-    const uint4* q = (const uint4*)(w + threadIdx.x * 16);
-    x0 = p[0];
-    x1 = p[1];
-    w0 = q[0];
-    w1 = q[1];
-  }
   float ss = 0.0f;
-  auto sumsq = [&](const uint4& v0, const uint4& v1) __attribute__((always_inline)) {
+  for (int64_t b = threadIdx.x; b < nb; b += 256) {
+    const uint4* p = (const uint4*)(xr + b * 16);
+    const uint4 v0 = p[0], v1 = p[1];
     const uint32_t wv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -141,24 +130,18 @@ k_rmsnorm_mx8(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, in
       ss = fmaf(a, a, ss);
       ss = fmaf(c, c, ss);
     }
-  };
-  if (one) {
-    if (threadIdx.x < nb) sumsq(x0, x1);
-  } else {
-    for (int64_t b = threadIdx.x; b < nb; b += 256) {
-      const uint4* p = (const uint4*)(xr + b * 16);
-      sumsq(p[0], p[1]);
-    }
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float total = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
   const float r = 1.0f / sqrtf(total / (float)H + eps);
-  auto block = [&](int64_t b, const uint4& v0, const uint4& v1, const uint4& u0, const uint4& u1)
-      __attribute__((always_inline)) {
+  for (int64_t b = threadIdx.x; b < nb; b += 256) {
+    const uint4* p = (const uint4*)(xr + b * 16);
+    const uint4* q = (const uint4*)(w + b * 16);
+    const uint4 v0 = p[0], v1 = p[1], w0 = q[0], w1 = q[1];
     const uint32_t xv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    const uint32_t wv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
     float h[16];
     float amax = 0.0f;
 #pragma unroll
@@ -186,15 +169,6 @@ k_rmsnorm_mx8(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, in
     f16x8* fo = (f16x8*)(fq + row * H + b * 16);
     fo[0] = o0;
     fo[1] = o1;
-  };
-  if (one) {
-    if (threadIdx.x < nb) block(threadIdx.x, x0, x1, w0, w1);
-  } else {
-    for (int64_t b = threadIdx.x; b < nb; b += 256) {
-      const uint4* p = (const uint4*)(xr + b * 16);
-      const uint4* q = (const uint4*)(w + b * 16);
-      block(b, p[0], p[1], q[0], q[1]);
-    }
   }
 }
 
