@@ -315,7 +315,9 @@ k_gemv_nf4(const int8_t* __restrict__ xl, const float* __restrict__ xs, int M, c
 // pass through LDS into the MFMA's A operand, whose every row then holds
 // row 0 (only row 0 of the product is stored).  The activation is read by
 // every tile (it is 2K bytes against the tile's K / 2 of weights).
-template <int T, int NBW, int WAVES>
+// TPW: tiles per wave (2: adjacent tiles share the wave's quantized
+// activation range, so each range is quantized once per pair of tiles).
+template <int T, int NBW, int WAVES, int TPW = 1>
 __global__ void __launch_bounds__(WAVES * 64)
 k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, vh_format xfmt,
               const uint8_t* __restrict__ wp,
@@ -327,7 +329,8 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
   constexpr int EPL = UNROLL;    // activation elements per lane in a round
   constexpr int LPB = 64 / EPL;  // lanes per block
   static_assert(ROUNDS <= 2 && (UNROLL == 4 || UNROLL == 8), "round shape");
-  __shared__ float s_red[WAVES][1][64];
+  static_assert(TPW == 1 || TPW == 2, "tiles per wave");
+  __shared__ float s_red[TPW][WAVES][1][64];
   __shared__ float s_scale[256];
   __shared__ __attribute__((aligned(4))) uint16_t s_keys[16];  // the element map's thresholds
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[WAVES][UNROLL * 64];
@@ -335,9 +338,8 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
   const int nb = (int)(K / 64);
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tl = wave % T, kr = wave / T;
-  const int64_t tile = (int64_t)blockIdx.x * T + tl;
+  const int64_t tile0 = ((int64_t)blockIdx.x * T + tl) * TPW;  // this wave's first tile
   const int b0 = kr * nb / KR, b1 = (kr + 1) * nb / KR;
-  const int64_t n = tile * 16 + (lane & 15);
   uint32_t base;
   asm volatile("v_mov_b32 %0, 0x3020100" : "=v"(base));
 
@@ -345,27 +347,32 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
   const uint32_t woff = (uint32_t)lane * 8u, wsoff = (uint32_t)(lane & 15), xoff = (uint32_t)lane * (2u * EPL);
   typedef typename std::conditional<EPL == 8, vh_u32x4, vh_u32x2>::type XT;
   struct Set {
-    vh_u32x2 w[UNROLL];
-    uint32_t sw[UNROLL];
+    vh_u32x2 w[TPW][UNROLL];
+    uint32_t sw[TPW][UNROLL];
     XT x;
   };
   auto load = [&](int b, Set& st) __attribute__((always_inline)) {
     uint32_t wo = woff, wso = wsoff, xo = xoff;
     asm volatile("" : "+v"(wo), "+v"(wso), "+v"(xo));
     const int64_t rem = b1 - b;
-    const __amdgpu_buffer_rsrc_t wr = rsrc(wp + (tile * nb + b) * 512, rem * 512);
-    const __amdgpu_buffer_rsrc_t wsr = rsrc(ws + (tile * nb + b) * 16, rem * 16);
     const __amdgpu_buffer_rsrc_t xr = rsrc(x + (int64_t)b * 64, rem * 128);
     // the activation first: waiting for it leaves the weights in flight
     if constexpr (EPL == 8) st.x = __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0);
     else st.x = __builtin_amdgcn_raw_buffer_load_b64(xr, xo, 0, 0);
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      st.w[u] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + u * 512u, 0, 0);
-      st.sw[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, wso + u * 16u, 0, 0);
+    for (int t = 0; t < TPW; ++t) {
+      const __amdgpu_buffer_rsrc_t wr = rsrc(wp + ((tile0 + t) * nb + b) * 512, rem * 512);
+      const __amdgpu_buffer_rsrc_t wsr = rsrc(ws + ((tile0 + t) * nb + b) * 16, rem * 16);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        st.w[t][u] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + u * 512u, 0, 0);
+        st.sw[t][u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(wsr, wso + u * 16u, 0, 0);
+      }
     }
   };
-  float acc = 0.0f;
+  float acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = 0.0f;
   auto round = [&](Set& st, int b) __attribute__((always_inline)) {
     asm volatile("" : "+v"(st.x)::"memory");
     float xv[EPL];
@@ -424,31 +431,42 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
     // the blocks software-pipelined as in k_gemv_nf4: LDS reads one block
     // ahead of the lookup and MFMA, the scale product one block behind
     vh_u32x4 xq[UNROLL];
-    float swv[UNROLL];
-    int dd[UNROLL];
+    float swv[TPW][UNROLL];
+    int dd[TPW][UNROLL];
     auto stage_a = [&](int u) __attribute__((always_inline)) {
-      asm volatile("" : "+v"(st.w[u]), "+v"(st.sw[u]));
+      if constexpr (TPW == 1)
+        asm volatile("" : "+v"(st.w[0][u]), "+v"(st.sw[0][u]));
+      else
+        asm volatile("" : "+v"(st.w[0][u]), "+v"(st.sw[0][u]), "+v"(st.w[1][u]), "+v"(st.sw[1][u]));
       xq[u] = *(const vh_u32x4*)&s_xq[wave][u * 64 + 16 * (lane >> 4)];
-      swv[u] = s_scale[st.sw[u]];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) swv[t][u] = s_scale[st.sw[t][u]];
     };
     auto stage_b = [&](int u) __attribute__((always_inline)) {
-      i32x4 wl;
-      wl[0] = (int)lut_lo(st.w[u].x, base, lv);
-      wl[1] = (int)lut_lo(st.w[u].y, base, lv);
-      wl[2] = (int)lut_hi(st.w[u].x, base, lv);
-      wl[3] = (int)lut_hi(st.w[u].y, base, lv);
       const i32x4 xa = {(int)xq[u].x, (int)xq[u].y, (int)xq[u].z, (int)xq[u].w};
-      const i32x4 z = {0, 0, 0, 0};
-      dd[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, z, 0, 0, 0)[0];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        i32x4 wl;
+        wl[0] = (int)lut_lo(st.w[t][u].x, base, lv);
+        wl[1] = (int)lut_lo(st.w[t][u].y, base, lv);
+        wl[2] = (int)lut_hi(st.w[t][u].x, base, lv);
+        wl[3] = (int)lut_hi(st.w[t][u].y, base, lv);
+        const i32x4 z = {0, 0, 0, 0};
+        dd[t][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wl, z, 0, 0, 0)[0];
+      }
+    };
+    auto stage_c = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) acc[t] = fmaf((float)dd[t][u], sxb[u] * swv[t][u], acc[t]);
     };
     stage_a(0);
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       if (u + 1 < UNROLL) stage_a(u + 1);
       stage_b(u);
-      if (u > 0) acc = fmaf((float)dd[u - 1], sxb[u - 1] * swv[u - 1], acc);
+      if (u > 0) stage_c(u - 1);
     }
-    acc = fmaf((float)dd[UNROLL - 1], sxb[UNROLL - 1] * swv[UNROLL - 1], acc);
+    stage_c(UNROLL - 1);
   };
   Set s[2];
   auto chunk = [&](int c0, auto pre) __attribute__((always_inline)) {
@@ -482,10 +500,13 @@ k_gemv_nf4_q1(const uint16_t* __restrict__ x, float quant_max, vh_format xsfmt, 
     load(c0, s[0]);
     chunk(c0, std::false_type{});
   }
-  s_red[wave][0][lane] = acc;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) s_red[t][wave][0][lane] = acc[t];
   __syncthreads();
   if (kr != 0) return;
-  finish<T, 1, WAVES>(s_red, tl, lane, (lane >> 4) * 4, 1, n, N, epi, y);
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+    finish<T, 1, WAVES>(s_red[t], tl, lane, (lane >> 4) * 4, 1, (tile0 + t) * 16 + (lane & 15), N, epi, y);
 }
 
 }  // namespace
@@ -574,15 +595,21 @@ extern "C" int vh_gemv_nf4_m1(const void* x, int32_t x_dtype, float quant_max, c
   uint32_t t[4];
   memcpy(t, levels16, 16);
   const uint4 lv = make_uint4(t[0], t[1], t[2], t[3]);
-  // the same workgroup shapes as vh_gemv_nf4
+  // the same workgroup shapes as vh_gemv_nf4: two tiles per wave on grids
+  // of at least 512 tiles (each K range then quantized once per pair)
   const int64_t tiles = N / 16, nb = K / 64;
   const bool four = tiles >= 512 && tiles % 4 == 0 && nb <= 2 * 16;
+  const bool pair = !four && tiles >= 512 && tiles % 2 == 0;
   const int64_t kr = four ? 2 : 8, bpw = (nb + kr - 1) / kr;
   hipStream_t st = vh::as_stream(stream);
   auto launch = [&](auto nbw) {
     constexpr int NBW = decltype(nbw)::value;
     if (four)
       hipLaunchKernelGGL((k_gemv_nf4_q1<4, NBW, 8>), dim3((unsigned)(tiles / 4)), dim3(512), 0, st,
+                         (const uint16_t*)x, quant_max, *x_scale_fmt, *x_fmt, w_packed, w_scale, *w_scale_fmt, lv, N,
+                         K, *epi, y);
+    else if (pair)
+      hipLaunchKernelGGL((k_gemv_nf4_q1<1, NBW, 8, 2>), dim3((unsigned)(tiles / 2)), dim3(512), 0, st,
                          (const uint16_t*)x, quant_max, *x_scale_fmt, *x_fmt, w_packed, w_scale, *w_scale_fmt, lv, N,
                          K, *epi, y);
     else

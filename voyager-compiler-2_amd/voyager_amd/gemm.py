@@ -592,10 +592,10 @@ def _nf4_fusable(x: torch.Tensor, ec, sc) -> bool:
 
 
 def _nf4_one_launch_pays(N: int, K: int) -> bool:
-    """Every 16-column tile quantizes the row again, which costs less than
-    a second launch while each wave's K range is at most 32 blocks (MI355X,
-    weights from HBM: 6.0-6.6 us against 8.6-9.1 at K = 4096, N <= 4096;
-    13.9 against 14.5 at N = 14336; even, 16.4 us, at K = 14336)."""
+    """Every 16-column tile (pair of tiles from 512 tiles) quantizes the
+    row again, which costs less than a second launch at K = 4096 (MI355X,
+    weights from HBM: 5.7-6.3 us against 7.8-8.4 at N <= 4096; 12.0 against
+    13.7 at N = 14336); at K = 14336 the two are even (16.0 / 15.7 us)."""
     return K <= 4096
 
 
